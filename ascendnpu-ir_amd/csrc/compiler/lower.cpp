@@ -1,0 +1,1494 @@
+// ConvertHFusionToHIP — see lower.h.
+//
+// Group classification follows the reference's fusion kinds
+// (FusibleHelper.cpp:51-70 pattern -> kind; HFusionEnums.td:210-233):
+//   * a `linalg.matmul[_transpose_b]` + elementwise epilogue -> SINGLE_CUBE
+//     (hand-written MFMA kernel, hf_mmad.h, with a generated epilogue);
+//   * `hfusion.reduce_with_index` -> split-row arg-reduction (hf_argmax.h);
+//   * last-axis `linalg.reduce` chains -> LAST_AXIS_PBR row programs (one row
+//     group of threads keeps its row resident in VGPRs, hf_row.h helpers);
+//   * everything else (elementwise + broadcast) -> PURE_ELEMWISE / ANY_PB
+//     streaming kernels with 128-bit accesses.
+// Scalar meaning of each op: hf_ops.h (region builders of
+// bishengir/lib/Dialect/HFusion/IR/HFusionOps.cpp:434-862).
+#include "lower.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <set>
+#include <sstream>
+
+namespace hfc {
+namespace {
+
+[[noreturn]] void unsupported(const Op *op, const std::string &why) {
+  throw CompileError("unsupported: " + why + (op ? " ('" + op->name + "' at line " + std::to_string(op->line) + ")" : std::string()));
+}
+
+std::string ctype(Elem e) {
+  switch (e) {
+  case Elem::F32: return "float";
+  case Elem::F64: return "double";
+  case Elem::F16: case Elem::BF16: return "uint16_t";
+  case Elem::I1: return "bool";
+  case Elem::I8: return "int8_t";
+  case Elem::I16: return "int16_t";
+  case Elem::I32: return "int32_t";
+  case Elem::I64: case Elem::Index: return "int64_t";
+  default: throw CompileError("no storage type for element type");
+  }
+}
+// in-memory element type (i1 is one byte)
+std::string mtype(Elem e) { return e == Elem::I1 ? "uint8_t" : ctype(e); }
+
+std::string floatLit(float f) {
+  if (std::isnan(f)) return "__builtin_nanf(\"\")";
+  if (std::isinf(f)) return f > 0 ? "__builtin_inff()" : "(-__builtin_inff())";
+  char buf[64];
+  std::snprintf(buf, sizeof buf, "%af", (double)f);
+  return std::string("(") + buf + ")";
+}
+std::string doubleLit(double d) {
+  if (std::isnan(d)) return "__builtin_nan(\"\")";
+  if (std::isinf(d)) return d > 0 ? "__builtin_inf()" : "(-__builtin_inf())";
+  char buf[64];
+  std::snprintf(buf, sizeof buf, "%a", d);
+  return std::string("(") + buf + ")";
+}
+
+// --------------------------------------------------------------- constants
+bool parseLiteral(const std::string &lit, Elem e, Value *v) {
+  std::string s = lit;
+  if (s.rfind("dense<", 0) == 0) s = s.substr(6, s.size() - 7);
+  if (s.empty()) return false;
+  if (s == "true" || s == "false") {
+    v->isConst = true;
+    v->iconst = s == "true";
+    v->fconst = (double)v->iconst;
+    return true;
+  }
+  bool hex = s.size() > 2 && (s.compare(0, 2, "0x") == 0 || s.compare(0, 2, "0X") == 0);
+  v->isConst = true;
+  if (isFloat(e)) {
+    if (hex) {
+      uint64_t bits = std::stoull(s, nullptr, 16);
+      v->constBits = bits;
+      v->constHasBits = true;
+      if (e == Elem::F32) { float f; uint32_t u = (uint32_t)bits; std::memcpy(&f, &u, 4); v->fconst = f; }
+      else if (e == Elem::F64) { double d; std::memcpy(&d, &bits, 8); v->fconst = d; }
+      else if (e == Elem::BF16) { float f; uint32_t u = (uint32_t)bits << 16; std::memcpy(&f, &u, 4); v->fconst = f; }
+      else throw CompileError("hex f16 constants are not supported");
+    } else if (e == Elem::F32 || e == Elem::BF16 || e == Elem::F16) {
+      v->fconst = std::strtof(s.c_str(), nullptr);
+    } else {
+      v->fconst = std::strtod(s.c_str(), nullptr);
+    }
+    v->iconst = (int64_t)v->fconst;
+  } else {
+    v->iconst = hex ? (int64_t)std::stoull(s, nullptr, 16) : std::stoll(s);
+    v->fconst = (double)v->iconst;
+  }
+  return true;
+}
+
+float roundF32(double d) { return (float)d; }
+
+void foldConstants(Func &f) {
+  for (Op *op : f.ops) {
+    if (op->results.empty()) continue;
+    Value *r = op->results[0];
+    const std::string &n = op->name;
+    auto allConst = [&]() {
+      for (auto *o : op->operands) if (!o->isConst) return false;
+      return !op->operands.empty();
+    };
+    if (n == "arith.constant") {
+      if (!parseLiteral(op->literal, r->type.elem, r))
+        unsupported(op, "constant literal '" + op->literal + "'");
+      continue;
+    }
+    if (n == "tensor.dim") {
+      r->type = Type();
+      r->type.elem = Elem::Index;
+      if (op->operands.size() == 2 && op->operands[1]->isConst) {
+        auto &sh = op->operands[0]->type.shape;
+        int64_t i = op->operands[1]->iconst;
+        if (i < 0 || i >= (int64_t)sh.size()) unsupported(op, "dimension index");
+        r->isConst = true;
+        r->iconst = sh[i];
+        r->fconst = (double)sh[i];
+      }
+      continue;
+    }
+    if (r->type.tensor || !allConst()) continue;
+    Value *a = op->operands[0];
+    Value *b = op->operands.size() > 1 ? op->operands[1] : nullptr;
+    Elem e = r->type.elem;
+    bool f32 = e == Elem::F32;
+    auto setF = [&](double d) { r->isConst = true; r->fconst = f32 ? (double)roundF32(d) : d; r->iconst = (int64_t)r->fconst; };
+    auto setI = [&](int64_t i) { r->isConst = true; r->iconst = i; r->fconst = (double)i; };
+    if (n == "arith.index_cast" || n == "arith.index_castui" || n == "arith.extsi" ||
+        n == "arith.extui" || n == "arith.trunci") setI(a->iconst);
+    else if (n == "arith.sitofp" || n == "arith.uitofp") setF((double)a->iconst);
+    else if (n == "arith.extf" || n == "arith.truncf") setF(a->fconst);
+    else if (n == "arith.fptosi" || n == "arith.fptoui") setI((int64_t)std::trunc(a->fconst));
+    else if (n == "arith.negf") setF(-a->fconst);
+    else if (b && f32 && n == "arith.addf") setF(roundF32(a->fconst) + roundF32(b->fconst));
+    else if (b && f32 && n == "arith.subf") setF(roundF32(a->fconst) - roundF32(b->fconst));
+    else if (b && f32 && n == "arith.mulf") setF(roundF32(a->fconst) * roundF32(b->fconst));
+    else if (b && f32 && n == "arith.divf") setF(roundF32(a->fconst) / roundF32(b->fconst));
+    else if (b && n == "arith.addf") setF(a->fconst + b->fconst);
+    else if (b && n == "arith.subf") setF(a->fconst - b->fconst);
+    else if (b && n == "arith.mulf") setF(a->fconst * b->fconst);
+    else if (b && n == "arith.divf") setF(a->fconst / b->fconst);
+    else if (b && n == "arith.addi") setI(a->iconst + b->iconst);
+    else if (b && n == "arith.subi") setI(a->iconst - b->iconst);
+    else if (b && n == "arith.muli") setI(a->iconst * b->iconst);
+    else if (b && n == "arith.divsi" && b->iconst) setI(a->iconst / b->iconst);
+  }
+}
+
+// A scalar literal expression for a constant value of element type e.
+std::string constExpr(const Value *v, Elem e) {
+  if (!v->isConst) throw CompileError("value " + v->name + " is not a constant");
+  switch (e) {
+  case Elem::F32:
+    if (v->constHasBits && v->type.elem == Elem::F32) {
+      char b[64];
+      std::snprintf(b, sizeof b, "__uint_as_float(0x%08xu)", (unsigned)v->constBits);
+      return b;
+    }
+    return floatLit((float)v->fconst);
+  case Elem::F64: return doubleLit(v->fconst);
+  case Elem::BF16: {
+    char b[64];
+    float f = (float)v->fconst;
+    uint32_t u; std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) u = (u >> 16) | 0x40u;
+    else u = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    std::snprintf(b, sizeof b, "((uint16_t)0x%04x)", u & 0xffffu);
+    return b;
+  }
+  case Elem::F16: return "hf::f32_to_f16<0>(" + floatLit((float)v->fconst) + ")";
+  case Elem::I1: return v->iconst ? "true" : "false";
+  case Elem::I8: return "((int8_t)" + std::to_string(v->iconst) + ")";
+  case Elem::I16: return "((int16_t)" + std::to_string(v->iconst) + ")";
+  case Elem::I32: return "((int32_t)" + std::to_string(v->iconst) + ")";
+  default: return "((int64_t)" + std::to_string(v->iconst) + "ll)";
+  }
+}
+
+// --------------------------------------------------------------- scalar ops
+// convertScalarToDtype (upstream MLIR), used by the `cast` type_fn of named ops.
+std::string castExpr(const std::string &x, Elem from, Elem to, bool unsignedCast) {
+  if (from == to) return x;
+  if (from == Elem::Index) from = Elem::I64;
+  if (to == Elem::Index) to = Elem::I64;
+  if (from == to) return x;
+  auto toF32 = [&](const std::string &s, Elem f) -> std::string {
+    if (f == Elem::F32) return s;
+    if (f == Elem::BF16) return "hf::bf16_to_f32(" + s + ")";
+    if (f == Elem::F16) return "hf::f16_to_f32(" + s + ")";
+    if (f == Elem::F64) return "((float)(" + s + "))";
+    throw CompileError("internal: toF32");
+  };
+  if (isFloat(from) && isFloat(to)) {
+    if (to == Elem::F64) return "((double)" + toF32(x, from) + ")";
+    std::string f = toF32(x, from);
+    if (to == Elem::F32) return f;
+    if (to == Elem::BF16) return "hf::f32_to_bf16<0>(" + f + ")";
+    return "hf::f32_to_f16<0>(" + f + ")";
+  }
+  if (isInt(from) && isFloat(to)) {
+    bool uns = unsignedCast || from == Elem::I1;
+    std::string iv = uns ? "(int64_t)(uint" + std::to_string(std::max(8, elemBits(from))) + "_t)(" + x + ")"
+                         : "(int64_t)(" + x + ")";
+    if (from == Elem::I1) iv = "(int64_t)(" + x + ")";
+    if (to == Elem::F64) return "((double)" + iv + ")";
+    if (to == Elem::F32) return "hf::int_to_f32<0>(" + iv + ")";
+    if (to == Elem::BF16) return "hf::f32_to_bf16<0>((float)hf::round_to_format((double)" + iv + ", 8, -126, 127, 0))";
+    return "hf::f32_to_f16<0>((float)hf::round_to_format((double)" + iv + ", 11, -14, 15, 0))";
+  }
+  if (isFloat(from) && isInt(to)) {
+    std::string f = from == Elem::F64 ? x : toF32(x, from);
+    if (to == Elem::I1) return "((" + f + ") != 0)";
+    return "hf::fptosi<" + ctype(to) + ">(" + f + ")";
+  }
+  // int -> int
+  if (to == Elem::I1) return "((" + x + ") & 1)";
+  if (from == Elem::I1 || (unsignedCast && elemBits(to) > elemBits(from)))
+    return "(" + ctype(to) + ")(uint" + std::to_string(std::max(8, elemBits(from))) + "_t)(" + x + ")";
+  return "(" + ctype(to) + ")(" + x + ")";
+}
+
+// hfusion.cast with its declared RoundMode (HFusionEnums.td:122-141) and
+// enable_saturate (HFusionNamedStructuredOps.yaml:375-432).
+std::string declaredCastExpr(const std::string &x, Elem from, Elem to, int mode, bool sat, bool uns) {
+  if (from == Elem::Index) from = Elem::I64;
+  if (to == Elem::Index) to = Elem::I64;
+  std::string M = std::to_string(mode);
+  if (isFloat(from) && isFloat(to)) {
+    std::string f = castExpr(x, from, Elem::F32, false);
+    if (from == to) {
+      if (to == Elem::F32) return "hf::round_integral<" + M + ">(" + f + ")";
+      std::string r = "hf::round_integral<" + M + ">(" + f + ")";
+      return castExpr(r, Elem::F32, to, false);
+    }
+    if (to == Elem::F32) return f;
+    if (to == Elem::F64) return "((double)" + f + ")";
+    if (from == Elem::F64) f = "((float)(" + x + "))";
+    if (to == Elem::BF16) return "hf::f32_to_bf16<" + M + ">(" + f + ")";
+    return "hf::f32_to_f16<" + M + ">(" + f + ")";
+  }
+  if (isFloat(from) && isInt(to)) {
+    std::string f = castExpr(x, from, Elem::F32, false);
+    if (to == Elem::I1) return "((" + f + ") != 0)";
+    return "hf::f32_to_int<" + ctype(to) + ", " + M + ", " + (sat ? "true" : "false") + ">(" + f + ")";
+  }
+  if (isInt(from) && isFloat(to)) {
+    std::string iv = (uns || from == Elem::I1) && from != Elem::I64
+                         ? "(int64_t)(uint" + std::to_string(std::max(8, elemBits(from))) + "_t)(" + x + ")"
+                         : "(int64_t)(" + x + ")";
+    if (to == Elem::F32) return "hf::int_to_f32<" + M + ">(" + iv + ")";
+    if (to == Elem::F64) return "((double)" + iv + ")";
+    if (to == Elem::BF16) return "hf::f32_to_bf16<0>((float)hf::round_to_format((double)" + iv + ", 8, -126, 127, " + M + "))";
+    return "hf::f32_to_f16<0>((float)hf::round_to_format((double)" + iv + ", 11, -14, 15, " + M + "))";
+  }
+  // int -> int
+  if (sat && elemBits(to) < elemBits(from) && to != Elem::I1) {
+    int b = elemBits(to);
+    std::string lo = "(-(int64_t)1 << " + std::to_string(b - 1) + ")";
+    std::string hi = "(((int64_t)1 << " + std::to_string(b - 1) + ") - 1)";
+    return "(" + ctype(to) + ")(((int64_t)(" + x + ")) < " + lo + " ? " + lo + " : (((int64_t)(" + x + ")) > " + hi + " ? " + hi + " : (int64_t)(" + x + ")))";
+  }
+  return castExpr(x, from, to, uns);
+}
+
+std::string f32UnaryFn(const std::string &fn, const std::string &x, const Op *op) {
+  if (fn == "sqrt") return "__builtin_sqrtf(" + x + ")";
+  if (fn == "rsqrt") return "hf::rsqrt(" + x + ")";
+  if (fn == "exp") return "expf(" + x + ")";
+  if (fn == "exp2") return "exp2f(" + x + ")";
+  if (fn == "log") return "logf(" + x + ")";
+  if (fn == "log2") return "log2f(" + x + ")";
+  if (fn == "log10") return "log10f(" + x + ")";
+  if (fn == "log1p") return "log1pf(" + x + ")";
+  if (fn == "expm1") return "expm1f(" + x + ")";
+  if (fn == "abs" || fn == "absf") return "__builtin_fabsf(" + x + ")";
+  if (fn == "negf" || fn == "neg") return "(-(" + x + "))";
+  if (fn == "relu") return "hf::relu(" + x + ")";
+  if (fn == "rec" || fn == "reciprocal") return "hf::rec(" + x + ")";
+  if (fn == "tanh") return "tanhf(" + x + ")";
+  if (fn == "sin") return "sinf(" + x + ")";
+  if (fn == "cos") return "cosf(" + x + ")";
+  if (fn == "erf") return "erff(" + x + ")";
+  if (fn == "nearbyint") return "__builtin_roundevenf(" + x + ")";
+  if (fn == "ceil") return "__builtin_ceilf(" + x + ")";
+  if (fn == "floor") return "__builtin_floorf(" + x + ")";
+  if (fn == "round") return "__builtin_roundf(" + x + ")";
+  if (fn == "square") return "((" + x + ") * (" + x + "))";
+  if (fn == "trunc") return "__builtin_truncf(" + x + ")";
+  unsupported(op, "unary function '" + fn + "' on f32");
+}
+
+std::string f32BinaryFn(const std::string &fn, const std::string &a, const std::string &b, const Op *op) {
+  if (fn == "add") return "(" + a + " + " + b + ")";
+  if (fn == "sub") return "(" + a + " - " + b + ")";
+  if (fn == "mul") return "(" + a + " * " + b + ")";
+  if (fn == "div" || fn == "div_unsigned") return "(" + a + " / " + b + ")";
+  if (fn == "maxf" || fn == "max_signed" || fn == "max_unsigned") return "hf::maximumf(" + a + ", " + b + ")";
+  if (fn == "minf" || fn == "min_signed" || fn == "min_unsigned") return "hf::minimumf(" + a + ", " + b + ")";
+  if (fn == "maxnumf") return "hf::maxnumf(" + a + ", " + b + ")";
+  if (fn == "minnumf") return "hf::minnumf(" + a + ", " + b + ")";
+  if (fn == "powf") return "powf(" + a + ", " + b + ")";
+  if (fn == "mod" || fn == "modui") return "fmodf(" + a + ", " + b + ")";
+  if (fn == "copysign") return "copysignf(" + a + ", " + b + ")";
+  unsupported(op, "binary function '" + fn + "' on floats");
+}
+
+std::string intBinaryFn(const std::string &fn, const std::string &a, const std::string &b, Elem t, const Op *op) {
+  std::string T = ctype(t);
+  std::string A = "(int64_t)(" + a + ")", B = "(int64_t)(" + b + ")";
+  std::string U = "uint" + std::to_string(std::max(8, elemBits(t))) + "_t";
+  if (fn == "add") return "(" + T + ")((uint64_t)" + A + " + (uint64_t)" + B + ")";
+  if (fn == "sub") return "(" + T + ")((uint64_t)" + A + " - (uint64_t)" + B + ")";
+  if (fn == "mul") return "(" + T + ")((uint64_t)" + A + " * (uint64_t)" + B + ")";
+  if (fn == "div") return "(" + T + ")(" + B + " == 0 ? 0 : " + A + " / " + B + ")";
+  if (fn == "mod") return "(" + T + ")(" + B + " == 0 ? 0 : " + A + " % " + B + ")";
+  if (fn == "max_signed" || fn == "maxsi") return "(" + A + " > " + B + " ? (" + T + ")(" + a + ") : (" + T + ")(" + b + "))";
+  if (fn == "min_signed" || fn == "minsi") return "(" + A + " < " + B + " ? (" + T + ")(" + a + ") : (" + T + ")(" + b + "))";
+  if (fn == "max_unsigned") return "((" + U + ")(" + a + ") > (" + U + ")(" + b + ") ? (" + T + ")(" + a + ") : (" + T + ")(" + b + "))";
+  if (fn == "min_unsigned") return "((" + U + ")(" + a + ") < (" + U + ")(" + b + ") ? (" + T + ")(" + a + ") : (" + T + ")(" + b + "))";
+  if (fn == "vand") return "(" + T + ")(" + A + " & " + B + ")";
+  if (fn == "vor") return "(" + T + ")(" + A + " | " + B + ")";
+  if (fn == "vxor") return "(" + T + ")(" + A + " ^ " + B + ")";
+  if (fn == "shli") return "(" + T + ")((uint64_t)" + A + " << " + B + ")";
+  if (fn == "shrsi") return "(" + T + ")(" + A + " >> " + B + ")";
+  if (fn == "shrui") return "(" + T + ")((" + U + ")(" + a + ") >> " + B + ")";
+  if (fn == "floordivsi") return "(" + T + ")hf_floordiv(" + A + ", " + B + ")";
+  if (fn == "ceildivsi") return "(" + T + ")hf_ceildiv(" + A + ", " + B + ")";
+  unsupported(op, "binary function '" + fn + "' on integers");
+}
+
+// Applies a float-domain expression builder in element type U (f16/bf16 are
+// computed in f32 and rounded back, as LLVM promotes them on the CPU).
+std::string inFloatType(Elem U, const std::vector<std::string> &xs,
+                        const std::function<std::string(const std::vector<std::string> &)> &f32fn) {
+  if (U == Elem::F32) return f32fn(xs);
+  if (U == Elem::BF16 || U == Elem::F16) {
+    std::vector<std::string> ys;
+    for (auto &x : xs) ys.push_back(castExpr(x, U, Elem::F32, false));
+    return castExpr(f32fn(ys), Elem::F32, U, false);
+  }
+  if (U == Elem::F64) {
+    // f64 math: the f32 builders with double arguments resolve to the double
+    // overloads of the arithmetic operators; named libm calls are mapped.
+    std::string s = f32fn(xs);
+    const char *pairs[][2] = {{"__builtin_sqrtf", "__builtin_sqrt"}, {"expf", "exp"}, {"logf", "log"},
+                              {"__builtin_fabsf", "__builtin_fabs"}, {"hf::maximumf", "__builtin_elementwise_maximum"},
+                              {"hf::minimumf", "__builtin_elementwise_minimum"}, {"__builtin_roundevenf", "__builtin_roundeven"},
+                              {"__builtin_floorf", "__builtin_floor"}, {"__builtin_ceilf", "__builtin_ceil"}};
+    for (auto &p : pairs) {
+      size_t pos;
+      while ((pos = s.find(p[0])) != std::string::npos) s.replace(pos, std::strlen(p[0]), p[1]);
+    }
+    return s;
+  }
+  throw CompileError("float function on non-float type");
+}
+
+int roundModeOf(const std::string &s) {
+  if (s.empty() || s == "rint") return 0;
+  if (s == "round") return 1;
+  if (s == "floor") return 2;
+  if (s == "ceil") return 3;
+  if (s == "trunc") return 4;
+  if (s == "odd") return 5;
+  if (s == "truncwithoverflow") return 6;
+  throw CompileError("unknown round_mode '" + s + "'");
+}
+
+bool isElementwiseOp(const Op *op) {
+  static const std::set<std::string> s = {
+      "hfusion.elemwise_unary", "hfusion.elemwise_binary", "hfusion.elemwise_ternary",
+      "linalg.elemwise_unary",  "linalg.elemwise_binary",  "hfusion.compare",
+      "hfusion.select",         "hfusion.cast",            "arith.addf", "arith.subf",
+      "arith.mulf",             "arith.divf",              "arith.maximumf", "arith.minimumf",
+      "arith.negf",             "arith.extf",              "arith.truncf", "arith.sitofp",
+      "arith.fptosi",           "arith.addi",              "arith.subi", "arith.muli",
+      "linalg.add", "linalg.sub", "linalg.mul", "linalg.div", "linalg.max", "linalg.min",
+      "linalg.exp", "linalg.abs", "linalg.negf", "linalg.sqrt", "linalg.rsqrt", "linalg.reciprocal"};
+  return s.count(op->name) != 0;
+}
+
+// Element expression of an elementwise op's result from operand expressions.
+std::string elementExpr(const Op *op, const std::vector<std::string> &a, const std::vector<Elem> &at, Elem U) {
+  const std::string &n = op->name;
+  bool uns = op->attr("cast") == "cast_unsigned";
+  auto named = [&](const std::string &fn, int arity) -> std::string {
+    if ((int)a.size() != arity) unsupported(op, "operand count");
+    std::vector<std::string> xs;
+    for (int i = 0; i < arity; ++i) xs.push_back(castExpr(a[i], at[i], U, uns));
+    if (isFloat(U)) {
+      if (arity == 1) return inFloatType(U, xs, [&](const std::vector<std::string> &y) { return f32UnaryFn(fn, y[0], op); });
+      if (arity == 2) return inFloatType(U, xs, [&](const std::vector<std::string> &y) { return f32BinaryFn(fn, y[0], y[1], op); });
+      if (fn == "fma")
+        return inFloatType(U, xs, [&](const std::vector<std::string> &y) { return "fmaf(" + y[0] + ", " + y[1] + ", " + y[2] + ")"; });
+      if (fn == "select") return "(" + a[0] + " ? " + xs[1] + " : " + xs[2] + ")";
+      unsupported(op, "ternary function '" + fn + "'");
+    }
+    std::string T = ctype(U);
+    if (arity == 1) {
+      if (fn == "relu") return "(" + T + ")((int64_t)(" + xs[0] + ") > 0 ? (int64_t)(" + xs[0] + ") : 0)";
+      if (fn == "vnot") return "(" + T + ")(~(int64_t)(" + xs[0] + "))";
+      if (fn == "absi" || fn == "abs") return "(" + T + ")((int64_t)(" + xs[0] + ") < 0 ? -(int64_t)(" + xs[0] + ") : (int64_t)(" + xs[0] + "))";
+      if (fn == "rec") return "(" + T + ")((int64_t)(" + xs[0] + ") == 0 ? 0 : 1 / (int64_t)(" + xs[0] + "))";
+      unsupported(op, "unary function '" + fn + "' on integers");
+    }
+    if (arity == 2) return intBinaryFn(fn, xs[0], xs[1], U, op);
+    if (fn == "select") return "(" + a[0] + " ? " + xs[1] + " : " + xs[2] + ")";
+    unsupported(op, "ternary function '" + fn + "' on integers");
+  };
+  if (n == "hfusion.elemwise_unary") return named(op->attr("fun", "sqrt"), 1);
+  if (n == "linalg.elemwise_unary") return named(op->attr("fun", "exp"), 1);
+  if (n == "hfusion.elemwise_binary") return named(op->attr("fun", "vand"), 2);
+  if (n == "linalg.elemwise_binary") return named(op->attr("fun", "add"), 2);
+  if (n == "hfusion.elemwise_ternary") {
+    std::string fn = op->attr("fun", "fma");
+    if (fn == "select") {
+      // select keeps the i1 condition uncast
+      std::vector<std::string> xs = {a[0], castExpr(a[1], at[1], U, uns), castExpr(a[2], at[2], U, uns)};
+      return "(" + xs[0] + " ? " + xs[1] + " : " + xs[2] + ")";
+    }
+    return named(fn, 3);
+  }
+  if (n == "hfusion.select") return "(" + a[0] + " ? " + a[1] + " : " + a[2] + ")";
+  if (n == "hfusion.compare") {
+    std::string fn = op->attr("compare_fn", "veq");
+    Elem T = at[0];
+    std::string x = a[0], y = a[1];
+    if (T == Elem::BF16 || T == Elem::F16) { x = castExpr(x, T, Elem::F32, false); y = castExpr(y, T, Elem::F32, false); }
+    if (fn == "veq") return "(" + x + " == " + y + ")";
+    if (fn == "vne") return "!(" + x + " == " + y + ")";
+    if (fn == "vlt") return "(" + x + " < " + y + ")";
+    if (fn == "vle") return "(" + x + " <= " + y + ")";
+    if (fn == "vgt") return "(" + x + " > " + y + ")";
+    if (fn == "vge") return "(" + x + " >= " + y + ")";
+    std::string U2 = "uint" + std::to_string(std::max(8, elemBits(T))) + "_t";
+    if (fn == "vult") return "((" + U2 + ")(" + x + ") < (" + U2 + ")(" + y + "))";
+    if (fn == "vule") return "((" + U2 + ")(" + x + ") <= (" + U2 + ")(" + y + "))";
+    if (fn == "vugt") return "((" + U2 + ")(" + x + ") > (" + U2 + ")(" + y + "))";
+    if (fn == "vuge") return "((" + U2 + ")(" + x + ") >= (" + U2 + ")(" + y + "))";
+    unsupported(op, "compare function '" + fn + "'");
+  }
+  if (n == "hfusion.cast") {
+    int mode = roundModeOf(op->attr("round_mode", "rint"));
+    bool sat = op->attr("enable_saturate") == "true";
+    bool u = uns || op->attr("unsigned_mode").find("ui2") != std::string::npos;
+    return declaredCastExpr(a[0], at[0], U, mode, sat, u);
+  }
+  // plain arith / linalg named ops on tensors
+  static const std::map<std::string, std::string> bin = {
+      {"arith.addf", "add"}, {"arith.subf", "sub"}, {"arith.mulf", "mul"}, {"arith.divf", "div"},
+      {"arith.maximumf", "maxf"}, {"arith.minimumf", "minf"}, {"arith.addi", "add"},
+      {"arith.subi", "sub"}, {"arith.muli", "mul"}, {"linalg.add", "add"}, {"linalg.sub", "sub"},
+      {"linalg.mul", "mul"}, {"linalg.div", "div"}, {"linalg.max", "maxf"}, {"linalg.min", "minf"}};
+  static const std::map<std::string, std::string> un = {
+      {"arith.negf", "negf"}, {"linalg.exp", "exp"}, {"linalg.abs", "abs"}, {"linalg.negf", "negf"},
+      {"linalg.sqrt", "sqrt"}, {"linalg.rsqrt", "rsqrt"}, {"linalg.reciprocal", "reciprocal"}};
+  if (bin.count(n)) return named(bin.at(n), 2);
+  if (un.count(n)) return named(un.at(n), 1);
+  if (n == "arith.extf" || n == "arith.truncf" || n == "arith.sitofp" || n == "arith.fptosi")
+    return castExpr(a[0], at[0], U, false);
+  unsupported(op, "elementwise op");
+}
+
+struct Combiner {
+  std::string name;     // arith op
+  std::string expr;     // with placeholders A (in) and B (acc)
+  std::string identity; // neutral element in the value type
+  bool isAddF = false;
+};
+
+Combiner combinerFor(const Op *op, const std::string &arith, Elem t) {
+  Combiner c;
+  c.name = arith;
+  std::string T = ctype(t);
+  auto lim = [&](bool mx) -> std::string {
+    int b = elemBits(t);
+    if (b >= 64) return mx ? "(int64_t)0x7fffffffffffffffll" : "(int64_t)(-0x7fffffffffffffffll - 1)";
+    return mx ? "(" + T + ")" + std::to_string((1ll << (b - 1)) - 1) : "(" + T + ")(" + std::to_string(-(1ll << (b - 1))) + ")";
+  };
+  if (t == Elem::F32) {
+    if (arith == "arith.addf") { c.expr = "(A + B)"; c.identity = "(-0.0f)"; c.isAddF = true; }
+    else if (arith == "arith.mulf") { c.expr = "(A * B)"; c.identity = "1.0f"; }
+    else if (arith == "arith.maximumf") { c.expr = "hf::maximumf(A, B)"; c.identity = "(-__builtin_inff())"; }
+    else if (arith == "arith.minimumf") { c.expr = "hf::minimumf(A, B)"; c.identity = "__builtin_inff()"; }
+    else if (arith == "arith.maxnumf") { c.expr = "hf::maxnumf(A, B)"; c.identity = "__builtin_nanf(\"\")"; }
+    else if (arith == "arith.minnumf") { c.expr = "hf::minnumf(A, B)"; c.identity = "__builtin_nanf(\"\")"; }
+    else unsupported(op, "reduction combiner '" + arith + "' on f32");
+    return c;
+  }
+  if (isInt(t) && t != Elem::I1) {
+    if (arith == "arith.addi") { c.expr = "(" + T + ")((uint64_t)(A) + (uint64_t)(B))"; c.identity = "(" + T + ")0"; }
+    else if (arith == "arith.muli") { c.expr = "(" + T + ")((uint64_t)(A) * (uint64_t)(B))"; c.identity = "(" + T + ")1"; }
+    else if (arith == "arith.maxsi") { c.expr = "((A) > (B) ? (A) : (B))"; c.identity = lim(false); }
+    else if (arith == "arith.minsi") { c.expr = "((A) < (B) ? (A) : (B))"; c.identity = lim(true); }
+    else if (arith == "arith.andi") { c.expr = "(" + T + ")((A) & (B))"; c.identity = "(" + T + ")(-1)"; }
+    else if (arith == "arith.ori") { c.expr = "(" + T + ")((A) | (B))"; c.identity = "(" + T + ")0"; }
+    else if (arith == "arith.xori") { c.expr = "(" + T + ")((A) ^ (B))"; c.identity = "(" + T + ")0"; }
+    else unsupported(op, "reduction combiner '" + arith + "' on integers");
+    return c;
+  }
+  unsupported(op, std::string("reductions over ") + elemName(t));
+}
+
+std::string subst(std::string e, const std::string &a, const std::string &b) {
+  std::string out;
+  for (char ch : e) {
+    if (ch == 'A') out += a;
+    else if (ch == 'B') out += b;
+    else out += ch;
+  }
+  return out;
+}
+
+// --------------------------------------------------------------- analysis
+struct Analysis {
+  Func *f = nullptr;
+  std::vector<int64_t> D;                     // iteration domain
+  std::map<const Value *, std::vector<int>> map; // tensor value -> D dims it spans
+  std::vector<BufferDesc> params, results;
+  std::vector<int> resultTied;                 // tied param per result (-1: own buffer)
+  std::set<int> paramsRead, paramsWritten;
+};
+
+// The func argument a destination operand finally writes into (through
+// linalg.fill / tensor.empty chains), or -1.
+int tiedArgOf(const Value *v) {
+  while (v) {
+    if (v->argIdx >= 0) return v->argIdx;
+    const Op *d = v->def;
+    if (!d || d->outs.empty()) return -1;
+    v = d->outs[std::min<size_t>(v->resultIdx, d->outs.size() - 1)];
+  }
+  return -1;
+}
+
+const Op *findOp(const Func &f, const std::function<bool(const Op *)> &p) {
+  for (const Op *op : f.ops) if (p(op)) return op;
+  return nullptr;
+}
+
+void describeBuffers(Analysis &A) {
+  Func &f = *A.f;
+  for (Value *a : f.args) {
+    BufferDesc b;
+    b.elem = a->type.elem;
+    b.shape = a->type.shape;
+    b.role = a->type.tensor ? "in" : "scalar";
+    A.params.push_back(b);
+  }
+  for (size_t i = 0; i < f.returns.size(); ++i) {
+    Value *r = f.returns[i];
+    BufferDesc b;
+    b.elem = r->type.elem;
+    b.shape = r->type.shape;
+    b.role = "out";
+    int t = r->def ? tiedArgOf(r->def->outs.empty() ? nullptr : r->def->outs[std::min<size_t>(r->resultIdx, r->def->outs.size() - 1)])
+                   : r->argIdx;
+    if (t >= 0 && f.args[t]->type.elem != r->type.elem) t = -1;
+    b.tiedParam = t;
+    if (t >= 0) {
+      A.paramsWritten.insert(t);
+      A.params[t].role = "out";
+    }
+    A.results.push_back(b);
+    A.resultTied.push_back(t);
+  }
+  // params that are read: used as `ins`/operands anywhere
+  for (const Op *op : f.ops) {
+    for (auto *v : op->ins) if (v->argIdx >= 0) A.paramsRead.insert(v->argIdx);
+    for (auto *v : op->operands) if (v->argIdx >= 0) A.paramsRead.insert(v->argIdx);
+  }
+  for (int p : A.paramsRead) if (A.params[p].role == "out") A.params[p].role = "inout";
+}
+
+bool isAlias(const Op *op) {
+  return op->name == "linalg.broadcast" || op->name == "tensor.empty" || op->name == "linalg.fill" ||
+         op->name == "arith.constant" || op->name == "tensor.dim" || op->name.rfind("arith.index", 0) == 0;
+}
+
+// Propagates D-dim maps through broadcasts, reductions and elementwise ops.
+void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
+  Func &f = *A.f;
+  int r = (int)A.D.size();
+  std::vector<int> all;
+  for (int i = 0; i < r; ++i) all.push_back(i);
+  auto setMap = [&](const Value *v, const std::vector<int> &m, const Op *op) -> bool {
+    if (!v->type.tensor || exclude.count(v)) return false;
+    if ((int)m.size() != (int)v->type.shape.size()) unsupported(op, "shape does not match its broadcast/reduce dimensions");
+    for (size_t i = 0; i < m.size(); ++i)
+      if (v->type.shape[i] != A.D[m[i]]) unsupported(op, "tensor shape inconsistent with the group's iteration domain");
+    auto it = A.map.find(v);
+    if (it != A.map.end()) {
+      if (it->second != m) unsupported(op, "value used with two different broadcast layouts");
+      return false;
+    }
+    A.map[v] = m;
+    return true;
+  };
+  // seeds: full-rank tensors
+  for (Value *a : f.args)
+    if (a->type.tensor && a->type.shape == A.D && !exclude.count(a)) A.map[a] = all;
+  for (Op *op : f.ops)
+    for (Value *v : op->results)
+      if (v->type.tensor && v->type.shape == A.D && !exclude.count(v)) A.map[v] = all;
+  bool changed = true;
+  while (changed) {
+    changed = false;
+    for (Op *op : f.ops) {
+      const std::string &n = op->name;
+      auto minus = [&](const std::vector<int64_t> &dims) {
+        std::vector<int> m;
+        for (int i = 0; i < r; ++i)
+          if (std::find(dims.begin(), dims.end(), i) == dims.end()) m.push_back(i);
+        return m;
+      };
+      if (n == "linalg.broadcast") {
+        if (!op->ins.empty()) changed |= setMap(op->ins[0], minus(op->dims), op);
+        continue;
+      }
+      if (n == "linalg.reduce" || n == "hfusion.reduce_with_index") {
+        for (auto *o : op->outs) changed |= setMap(o, minus(op->dims), op);
+        for (auto *o : op->results) changed |= setMap(o, minus(op->dims), op);
+        continue;
+      }
+      if (n == "linalg.fill") {
+        if (A.map.count(op->results[0])) changed |= setMap(op->outs[0], A.map[op->results[0]], op);
+        if (A.map.count(op->outs[0])) changed |= setMap(op->results[0], A.map[op->outs[0]], op);
+        continue;
+      }
+      if (isElementwiseOp(op)) {
+        std::vector<Value *> vs;
+        for (auto *v : op->ins) if (v->type.tensor) vs.push_back(v);
+        for (auto *v : op->operands) if (v->type.tensor) vs.push_back(v);
+        for (auto *v : op->outs) vs.push_back(v);
+        for (auto *v : op->results) vs.push_back(v);
+        const std::vector<int> *known = nullptr;
+        for (auto *v : vs) if (A.map.count(v)) { known = &A.map[v]; break; }
+        if (known) {
+          std::vector<int> m = *known;
+          for (auto *v : vs) changed |= setMap(v, m, op);
+        }
+      }
+    }
+  }
+  for (Value *a : f.args)
+    if (a->type.tensor && !exclude.count(a) && !A.map.count(a)) {
+      bool used = !a->users.empty();
+      if (used) throw CompileError("cannot place argument " + a->name + " in the group's iteration domain");
+    }
+}
+
+std::string resultKind(const Func &f, bool *hasMatmul, bool *hasRWI, bool *hasReduce) {
+  *hasMatmul = *hasRWI = *hasReduce = false;
+  for (const Op *op : f.ops) {
+    if (op->name == "linalg.matmul" || op->name == "linalg.matmul_transpose_b") *hasMatmul = true;
+    if (op->name == "hfusion.reduce_with_index") *hasRWI = true;
+    if (op->name == "linalg.reduce") *hasReduce = true;
+  }
+  if (*hasMatmul) return "SINGLE_CUBE";
+  if (*hasRWI) return "REDUCE_WITH_INDEX";
+  if (*hasReduce) return "LAST_AXIS_PBR";
+  return "PURE_ELEMWISE";
+}
+
+std::vector<int64_t> largestShape(const Func &f, const std::set<const Value *> &exclude) {
+  std::vector<int64_t> best;
+  auto consider = [&](const Value *v) {
+    if (!v->type.tensor || exclude.count(v)) return;
+    const auto &s = v->type.shape;
+    if (s.size() > best.size() || (s.size() == best.size() && v->type.numel() > 0 && best.empty())) best = s;
+  };
+  for (auto *a : f.args) consider(a);
+  for (auto *op : f.ops) for (auto *v : op->results) consider(v);
+  for (auto *op : f.ops) for (auto *v : op->results)
+    if (v->type.tensor && !exclude.count(v) && v->type.shape.size() == best.size() && v->type.shape != best)
+      throw CompileError("group mixes full-rank tensors of different shapes (" + v->type.str() + ")");
+  return best;
+}
+
+std::string kernelParamList(const Analysis &A, std::vector<std::string> &kargs, bool withWs) {
+  std::ostringstream s;
+  bool first = true;
+  for (size_t i = 0; i < A.params.size(); ++i) {
+    if (!first) s << ", ";
+    first = false;
+    if (A.params[i].role == "scalar") s << "uint64_t s" << i;
+    else s << "void* __restrict__ p" << i;
+    kargs.push_back("param:" + std::to_string(i));
+  }
+  for (size_t i = 0; i < A.results.size(); ++i) {
+    if (A.resultTied[i] >= 0) continue;
+    if (!first) s << ", ";
+    first = false;
+    s << "void* __restrict__ r" << i;
+    kargs.push_back("result:" + std::to_string(i));
+  }
+  if (withWs) {
+    if (!first) s << ", ";
+    s << "void* __restrict__ ws";
+    kargs.push_back("ws");
+  }
+  return s.str();
+}
+
+// Pointer expression of the buffer holding func result i.
+std::string resultPtr(const Analysis &A, size_t i) {
+  return A.resultTied[i] >= 0 ? "p" + std::to_string(A.resultTied[i]) : "r" + std::to_string(i);
+}
+
+std::string scalarArgExpr(const Analysis &A, int i) {
+  Elem e = A.params[i].elem;
+  std::string s = "s" + std::to_string(i);
+  if (e == Elem::F32) return "__uint_as_float((uint32_t)" + s + ")";
+  if (e == Elem::F64) return "__longlong_as_double((long long)" + s + ")";
+  if (e == Elem::BF16 || e == Elem::F16) return "((uint16_t)" + s + ")";
+  return "((" + ctype(e) + ")" + s + ")";
+}
+
+double bytesOf(const BufferDesc &b) {
+  double n = elemBytes(b.elem);
+  for (auto d : b.shape) n *= (double)d;
+  return n;
+}
+
+double algoBytes(const Analysis &A) {
+  double t = 0;
+  for (int p : A.paramsRead) if (A.params[p].role != "scalar") t += bytesOf(A.params[p]);
+  for (auto &r : A.results) t += bytesOf(r);
+  return t;
+}
+
+// ======================================================================
+// Elementwise / row-program emitter.  Values live in one of four spaces of a
+// 2-D domain [R, C] (1-D groups use R = 1): Full (per element, an array of EPL
+// lanes' elements), Row (per row, a scalar), Col (per column, an array),
+// Scalar (a constant or kernel argument).
+// ======================================================================
+enum class Sp { Full, Row, Col, Scalar };
+
+struct RowEmitter {
+  Analysis &A;
+  const LowerOptions &opt;
+  std::ostringstream pre, body;
+  std::map<const Value *, std::string> name;
+  std::map<const Value *, Sp> sp;
+  std::map<const Value *, Elem> elemOf;
+  std::set<const Value *> orderedReduce;
+  int tmp = 0;
+  int nred = 0;       // LDS slots for tree reductions
+  bool needOrdered = false;
+  int64_t R = 1, C = 1;
+  int TR = 64, RB = 1, VEC = 4, EPL = 4, CH = 0;
+  bool masked = false;
+
+  RowEmitter(Analysis &a, const LowerOptions &o) : A(a), opt(o) {}
+
+  Sp spaceOfMap(const std::vector<int> &m) const {
+    if (A.D.size() == 1) return m.empty() ? Sp::Scalar : Sp::Full;
+    if (m.size() == 2) return Sp::Full;
+    if (m.size() == 1) return m[0] == 0 ? Sp::Row : Sp::Col;
+    return Sp::Scalar;
+  }
+  std::string fresh() { return "v" + std::to_string(tmp++); }
+  bool isArr(Sp s) const { return s == Sp::Full || s == Sp::Col; }
+
+  // expression of value v at element e (inside an element loop) or as scalar
+  std::string at(const Value *v, const std::string &e) {
+    auto it = name.find(v);
+    if (it == name.end()) throw CompileError("internal: value " + v->name + " not materialised");
+    return isArr(sp.at(v)) ? it->second + "[" + e + "]" : it->second;
+  }
+
+  std::string colExpr(const std::string &e) const {
+    return "((int64_t)((" + e + ") / VEC) * (TR * VEC) + lt * VEC + (" + e + ") % VEC)";
+  }
+
+  // Values that must be computed with a serial-order fp32 sum: sums whose
+  // result reaches an integer-typed group output (bit-exact outputs depend on
+  // the summation order of the reference's serial loop).
+  void markOrdered() {
+    Func &f = *A.f;
+    std::set<const Value *> intOut;
+    for (auto *r : f.returns) if (isInt(r->type.elem)) intOut.insert(r);
+    for (Op *op : f.ops) {
+      if (op->name != "linalg.reduce") continue;
+      if (op->combiner != "arith.addf") continue;
+      bool reaches = opt.orderedFloatSums;
+      std::vector<const Value *> stack(op->results.begin(), op->results.end());
+      std::set<const Value *> seen;
+      while (!stack.empty() && !reaches) {
+        const Value *v = stack.back();
+        stack.pop_back();
+        if (!seen.insert(v).second) continue;
+        if (intOut.count(v)) reaches = true;
+        for (const Op *u : v->users)
+          for (auto *r : u->results) stack.push_back(r);
+      }
+      if (reaches) orderedReduce.insert(op->results[0]);
+    }
+    needOrdered = !orderedReduce.empty();
+  }
+
+  void chooseSchedule() {
+    if (A.D.size() == 2) { R = A.D[0]; C = A.D[1]; }
+    else if (A.D.size() == 1) { R = 1; C = A.D[0]; }
+    else throw CompileError("row programs support rank-1 and rank-2 groups");
+    int maxBytes = 1;
+    for (auto &kv : A.map)
+      if (spaceOfMap(kv.second) == Sp::Full || spaceOfMap(kv.second) == Sp::Col)
+        maxBytes = std::max(maxBytes, elemBytes(kv.first->type.elem));
+    VEC = std::max(1, 16 / maxBytes);
+    if (VEC > 8) VEC = 8;
+    while (VEC > 1 && C % VEC) VEC /= 2;
+    // threads per row: aim for 8-32 elements per lane
+    int64_t perLaneTarget = VEC * 4;
+    int tr = 64;
+    while (tr < 1024 && (int64_t)tr * perLaneTarget < C) tr *= 2;
+    if (needOrdered) {
+      TR = 64;
+      RB = 8;
+    } else {
+      TR = tr;
+      RB = std::max(1, 256 / TR);
+      if (R < RB) RB = (int)std::max<int64_t>(1, R);
+    }
+    int64_t span = (int64_t)TR * VEC;
+    int64_t nch = (C + span - 1) / span;
+    EPL = (int)(nch * VEC);
+    masked = (C % span) != 0;
+    if (EPL > 256) throw CompileError("row of " + std::to_string(C) + " elements does not fit one row group (max " + std::to_string(1024 * 256) + ")");
+    if (needOrdered) {
+      // LDS chunk for the serial chain: a whole number of vector-chunks
+      int jpc = std::max(1, (int)(1024 / span));
+      if (jpc > nch) jpc = (int)nch;
+      while (nch % jpc) --jpc;
+      CH = (int)(jpc * span);
+    }
+  }
+
+  void loadInput(const Value *a) {
+    int i = a->argIdx;
+    Sp s = spaceOfMap(A.map.at(a));
+    std::string T = ctype(a->type.elem), M = mtype(a->type.elem);
+    std::string nm = "in" + std::to_string(i);
+    name[a] = nm;
+    sp[a] = s;
+    if (s == Sp::Full || s == Sp::Col) {
+      std::string base = s == Sp::Full ? "(const " + M + "*)p" + std::to_string(i) + " + row * C" : "(const " + M + "*)p" + std::to_string(i);
+      pre << "  " << T << " " << nm << "[EPL];\n";
+      if (a->type.elem == Elem::I1) {
+        pre << "  { uint8_t t_[EPL]; hf::row_load<uint8_t, VEC, EPL / VEC, TR, MASKED>(" << base << ", lt, C, t_);\n"
+            << "    for (int e = 0; e < EPL; ++e) " << nm << "[e] = t_[e] != 0; }\n";
+      } else {
+        pre << "  hf::row_load<" << T << ", VEC, EPL / VEC, TR, MASKED>(" << base << ", lt, C, " << nm << ");\n";
+      }
+    } else if (s == Sp::Row) {
+      pre << "  const " << T << " " << nm << " = ((const " << M << "*)p" << i << ")[row];\n";
+    } else {
+      pre << "  const " << T << " " << nm << " = ((const " << M << "*)p" << i << ")[0];\n";
+    }
+  }
+
+  void bindScalar(const Value *v) {
+    if (v->isConst) { name[v] = constExpr(v, v->type.elem); sp[v] = Sp::Scalar; return; }
+    if (v->argIdx >= 0) { name[v] = scalarArgExpr(A, v->argIdx); sp[v] = Sp::Scalar; return; }
+    throw CompileError("non-constant scalar " + v->name + " in a tensor group");
+  }
+
+  void ensure(const Value *v) {
+    if (name.count(v)) return;
+    if (!v->type.tensor) { bindScalar(v); return; }
+    if (v->argIdx >= 0) { loadInput(v); return; }
+    if (v->isConst) { name[v] = constExpr(v, v->type.elem); sp[v] = Sp::Scalar; return; }
+    throw CompileError("internal: value " + v->name + " used before definition");
+  }
+
+  void emitElementwise(const Op *op) {
+    std::vector<const Value *> opsv;
+    for (auto *v : op->ins) opsv.push_back(v);
+    for (auto *v : op->operands) opsv.push_back(v);
+    Sp out = Sp::Scalar;
+    bool anyRow = false, anyCol = false;
+    for (auto *v : opsv) {
+      ensure(v);
+      Sp s = sp[v];
+      if (s == Sp::Full) out = Sp::Full;
+      if (s == Sp::Row) anyRow = true;
+      if (s == Sp::Col) anyCol = true;
+    }
+    if (out != Sp::Full) {
+      if (anyRow && anyCol) out = Sp::Full;
+      else if (anyRow) out = Sp::Row;
+      else if (anyCol) out = Sp::Col;
+    }
+    const Value *res = op->results[0];
+    if (A.map.count(res)) {
+      Sp ms = spaceOfMap(A.map.at(res));
+      if (ms == Sp::Full && out != Sp::Full) out = Sp::Full; // broadcast by destination
+    }
+    Elem U = res->type.elem;
+    std::vector<Elem> at_;
+    for (auto *v : opsv) at_.push_back(v->type.elem);
+    std::string nm = fresh();
+    name[res] = nm;
+    sp[res] = out;
+    if (isArr(out)) {
+      std::vector<std::string> args;
+      for (auto *v : opsv) args.push_back(at(v, "e"));
+      body << "  " << ctype(U) << " " << nm << "[EPL];\n"
+           << "#pragma unroll\n  for (int e = 0; e < EPL; ++e) " << nm << "[e] = "
+           << elementExpr(op, args, at_, U) << ";\n";
+    } else {
+      std::vector<std::string> args;
+      for (auto *v : opsv) args.push_back(at(v, ""));
+      body << "  const " << ctype(U) << " " << nm << " = " << elementExpr(op, args, at_, U) << ";\n";
+    }
+  }
+
+  void emitReduce(const Op *op) {
+    if (op->ins.size() != 1 || op->outs.size() != 1) unsupported(op, "multi-operand linalg.reduce");
+    int last = (int)A.D.size() - 1;
+    if (op->dims.size() != 1 || op->dims[0] != last) unsupported(op, "reduction over a non-last axis");
+    const Value *x = op->ins[0];
+    ensure(x);
+    if (sp[x] != Sp::Full) unsupported(op, "reduction of a broadcast value");
+    const Value *init = op->outs[0];
+    // init: a fill of a constant, or a row tensor argument
+    std::string initExpr;
+    Elem t = x->type.elem;
+    if (init->def && init->def->name == "linalg.fill") {
+      const Value *c = init->def->ins[0];
+      if (!c->isConst) { ensure(c); initExpr = at(c, ""); }
+      else initExpr = constExpr(c, t);
+    } else if (init->argIdx >= 0) {
+      ensure(init);
+      initExpr = at(init, "");
+    } else if (init->isConst) {
+      initExpr = constExpr(init, t);
+    } else {
+      unsupported(op, "reduction init must be a linalg.fill or an argument");
+    }
+    Combiner cb = combinerFor(op, op->combiner, t);
+    const Value *res = op->results[0];
+    std::string nm = fresh();
+    name[res] = nm;
+    sp[res] = (A.D.size() == 1) ? Sp::Scalar : Sp::Row;
+    std::string xs = name[x];
+    if (orderedReduce.count(res)) {
+      body << "  const float " << nm << " = hf::row_sum_ordered<TR, RB, VEC, EPL, CHUNK>(" << xs << ", " << initExpr
+           << ", lds_chain, lds_bcast, rloc, lt, C);\n";
+      return;
+    }
+    std::string T = ctype(t);
+    std::string p = nm + "_p";
+    body << "  " << T << " " << p << " = " << cb.identity << ";\n";
+    std::string inner = "#pragma unroll\n  for (int e = 0; e < EPL; ++e) ";
+    if (masked) inner += "if (" + colExpr("e") + " < C) ";
+    body << inner << p << " = " << subst(cb.expr, xs + "[e]", p) << ";\n";
+    int slot = nred++;
+    body << "  " << p << " = hf::row_allreduce<TR, RB>(" << p << ", [](" << T << " A, " << T << " B) { return "
+         << cb.expr << "; }, (" << T << "*)(lds_red + " << slot << " * RB * WPR), rloc, lt);\n";
+    body << "  const " << T << " " << nm << " = " << subst(cb.expr, p, initExpr) << ";\n";
+  }
+
+  void emitStore(size_t i) {
+    const Value *v = A.f->returns[i];
+    if (v->argIdx >= 0 && A.resultTied[i] == v->argIdx) return; // returned input: nothing to write
+    ensure(v);
+    Elem e = v->type.elem;
+    std::string ptr = resultPtr(A, i);
+    std::string M = mtype(e);
+    Sp s = sp[v];
+    Sp ms = A.map.count(v) ? spaceOfMap(A.map.at(v)) : s;
+    if (ms == Sp::Full) {
+      std::string src = name[v];
+      if (s != Sp::Full) {
+        src = fresh();
+        body << "  " << ctype(e) << " " << src << "[EPL];\n  for (int e = 0; e < EPL; ++e) " << src << "[e] = " << at(v, "e") << ";\n";
+      }
+      if (e == Elem::I1) {
+        std::string t = fresh();
+        body << "  uint8_t " << t << "[EPL];\n  for (int e = 0; e < EPL; ++e) " << t << "[e] = " << src << "[e];\n";
+        src = t;
+      }
+      body << "  if (row_ok) hf::row_store<" << M << ", VEC, EPL / VEC, TR, MASKED>((" << M << "*)" << ptr
+           << " + row * C, lt, C, " << src << ");\n";
+    } else if (ms == Sp::Row || (ms == Sp::Scalar && A.D.size() == 1)) {
+      body << "  if (row_ok && lt == 0) ((" << M << "*)" << ptr << ")[" << (ms == Sp::Row ? "row" : "0") << "] = " << at(v, "0") << ";\n";
+    } else if (ms == Sp::Col) {
+      body << "  if (blockIdx.x == 0 && rloc == 0) hf::row_store<" << M << ", VEC, EPL / VEC, TR, MASKED>((" << M << "*)" << ptr
+           << ", lt, C, " << name[v] << ");\n";
+    } else {
+      throw CompileError("cannot store a scalar result");
+    }
+  }
+
+  KernelPlan run(const std::string &kname, const std::string &kind) {
+    markOrdered();
+    chooseSchedule();
+    Func &f = *A.f;
+    for (Op *op : f.ops) {
+      const std::string &n = op->name;
+      if (n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" || n.rfind("arith.", 0) == 0 && !op->results.empty() && !op->results[0]->type.tensor) {
+        continue;
+      }
+      if (n == "linalg.fill") {
+        const Value *c = op->ins[0];
+        ensure(c);
+        name[op->results[0]] = name[c];
+        sp[op->results[0]] = Sp::Scalar;
+        continue;
+      }
+      if (n == "linalg.broadcast") {
+        ensure(op->ins[0]);
+        name[op->results[0]] = name[op->ins[0]];
+        sp[op->results[0]] = sp[op->ins[0]];
+        continue;
+      }
+      if (n == "linalg.reduce") { emitReduce(op); continue; }
+      if (isElementwiseOp(op)) { emitElementwise(op); continue; }
+      unsupported(op, "op in a " + kind + " group");
+    }
+    for (size_t i = 0; i < f.returns.size(); ++i) emitStore(i);
+
+    KernelPlan p;
+    p.kernelName = kname;
+    p.kind = kind;
+    p.variant = needOrdered ? "row-resident, serial-order fp32 sum" : "row-resident";
+    int block = TR * RB;
+    int64_t grid = (R + RB - 1) / RB;
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(" << block << ") void " << kname << "("
+      << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  constexpr int TR = " << TR << ", RB = " << RB << ", VEC = " << VEC << ", EPL = " << EPL
+      << ", WPR = " << std::max(1, TR / 64) << ";\n"
+      << "  constexpr bool MASKED = " << (masked ? "true" : "false") << ";\n"
+      << "  constexpr int64_t R = " << R << "ll, C = " << C << "ll;\n"
+      << "  (void)R;\n"
+      << "  const int tid = threadIdx.x, rloc = tid / TR, lt = tid % TR;\n"
+      << "  const int64_t row_raw = (int64_t)blockIdx.x * RB + rloc;\n"
+      << "  const bool row_ok = row_raw < R;\n"
+      << "  const int64_t row = row_ok ? row_raw : (R - 1);\n"
+      << "  (void)row_ok; (void)lt;\n";
+    if (nred) k << "  __shared__ uint64_t lds_red_[" << nred << " * RB * WPR];\n  uint64_t* lds_red = lds_red_;\n";
+    if (needOrdered)
+      k << "  constexpr int CHUNK = " << CH << ";\n"
+        << "  __shared__ float lds_chain[RB * (CHUNK + 4)];\n  __shared__ float lds_bcast[RB];\n";
+    k << pre.str() << body.str() << "}\n";
+    p.source = k.str();
+    p.grid[0] = (unsigned)grid;
+    p.block[0] = (unsigned)block;
+    return p;
+  }
+};
+
+// ======================================================================
+// PURE_ELEMWISE / ANY_PB: streaming kernel over the flattened domain.
+// ======================================================================
+struct EltwiseEmitter {
+  Analysis &A;
+  std::ostringstream body;
+  std::map<const Value *, std::string> name;
+  std::map<const Value *, bool> vec; // per-element array vs. uniform scalar
+  int tmp = 0;
+  int VEC = 4;
+  int64_t N = 1;
+
+  EltwiseEmitter(Analysis &a) : A(a) {}
+  std::string fresh() { return "v" + std::to_string(tmp++); }
+
+  std::string at(const Value *v) { return vec.at(v) ? name.at(v) + "[e]" : name.at(v); }
+
+  // flat index of the chunk base inside an input spanning dims `m`
+  std::string indexFor(const std::vector<int> &m) {
+    int r = (int)A.D.size();
+    if ((int)m.size() == r) return "base";
+    if (m.empty()) return "0";
+    std::string s;
+    int64_t stride = 1;
+    for (int i = (int)m.size() - 1; i >= 0; --i) {
+      std::string term = "c" + std::to_string(m[i]) + " * " + std::to_string(stride) + "ll";
+      s = s.empty() ? term : term + " + " + s;
+      stride *= A.D[m[i]];
+    }
+    return s;
+  }
+
+  void ensure(const Value *v) {
+    if (name.count(v)) return;
+    if (!v->type.tensor || v->isConst) {
+      if (v->isConst) name[v] = constExpr(v, v->type.elem);
+      else if (v->argIdx >= 0) name[v] = scalarArgExpr(A, v->argIdx);
+      else throw CompileError("non-constant scalar " + v->name);
+      vec[v] = false;
+      return;
+    }
+    if (v->argIdx < 0) throw CompileError("internal: value " + v->name + " used before definition");
+    int i = v->argIdx;
+    const auto &m = A.map.at(v);
+    int r = (int)A.D.size();
+    std::string T = ctype(v->type.elem), M = mtype(v->type.elem);
+    std::string nm = "in" + std::to_string(i);
+    name[v] = nm;
+    bool hasLast = !m.empty() && m.back() == r - 1;
+    if (hasLast) {
+      vec[v] = true;
+      if (v->type.elem == Elem::I1) {
+        body << "    " << T << " " << nm << "[VEC]; { uint8_t t_[VEC]; hf::vec_load<uint8_t, VEC>((const uint8_t*)p" << i << " + " << indexFor(m)
+             << ", t_); for (int e = 0; e < VEC; ++e) " << nm << "[e] = t_[e] != 0; }\n";
+      } else {
+        body << "    " << T << " " << nm << "[VEC]; hf::vec_load<" << M << ", VEC>((const " << M << "*)p" << i << " + " << indexFor(m) << ", " << nm << ");\n";
+      }
+    } else {
+      vec[v] = false;
+      body << "    const " << T << " " << nm << " = ((const " << M << "*)p" << i << ")[" << indexFor(m) << "];\n";
+    }
+  }
+
+  KernelPlan run(const std::string &kname, const std::string &kind) {
+    Func &f = *A.f;
+    int r = (int)A.D.size();
+    N = 1;
+    for (auto d : A.D) N *= d;
+    int maxBytes = 1;
+    for (auto &kv : A.map) maxBytes = std::max(maxBytes, elemBytes(kv.first->type.elem));
+    VEC = std::max(1, 16 / maxBytes);
+    if (VEC > 8) VEC = 8;
+    int64_t L = r ? A.D[r - 1] : 1;
+    while (VEC > 1 && L % VEC) VEC /= 2;
+    // coordinates of the chunk base
+    std::ostringstream coords;
+    if (r > 1) {
+      coords << "    int64_t t_ = base;\n";
+      for (int d = r - 1; d >= 0; --d) {
+        coords << "    const int64_t c" << d << " = t_ % " << A.D[d] << "ll; t_ /= " << A.D[d] << "ll;\n";
+      }
+      coords << "    (void)t_;\n";
+      for (int d = 0; d < r; ++d) coords << "    (void)c" << d << ";\n";
+    } else if (r == 1) {
+      coords << "    const int64_t c0 = base; (void)c0;\n";
+    }
+    body << coords.str();
+    for (Op *op : f.ops) {
+      const std::string &n = op->name;
+      if (n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" || (n.rfind("arith.", 0) == 0 && !op->results[0]->type.tensor))
+        continue;
+      if (n == "linalg.fill") {
+        ensure(op->ins[0]);
+        name[op->results[0]] = name[op->ins[0]];
+        vec[op->results[0]] = false;
+        continue;
+      }
+      if (n == "linalg.broadcast") {
+        const Value *in = op->ins[0];
+        ensure(in);
+        name[op->results[0]] = name[in];
+        vec[op->results[0]] = vec[in];
+        if (!vec[in]) {
+          // a broadcast value constant along the last dim stays uniform
+        }
+        continue;
+      }
+      if (!isElementwiseOp(op)) unsupported(op, "op in an elementwise group");
+      std::vector<const Value *> opsv;
+      for (auto *v : op->ins) opsv.push_back(v);
+      for (auto *v : op->operands) opsv.push_back(v);
+      bool anyVec = false;
+      for (auto *v : opsv) { ensure(v); anyVec |= vec[v]; }
+      const Value *res = op->results[0];
+      Elem U = res->type.elem;
+      std::vector<Elem> at_;
+      for (auto *v : opsv) at_.push_back(v->type.elem);
+      std::string nm = fresh();
+      name[res] = nm;
+      vec[res] = anyVec;
+      std::vector<std::string> args;
+      for (auto *v : opsv) args.push_back(at(v));
+      if (anyVec)
+        body << "    " << ctype(U) << " " << nm << "[VEC];\n#pragma unroll\n    for (int e = 0; e < VEC; ++e) " << nm << "[e] = "
+             << elementExpr(op, args, at_, U) << ";\n";
+      else
+        body << "    const " << ctype(U) << " " << nm << " = " << elementExpr(op, args, at_, U) << ";\n";
+    }
+    for (size_t i = 0; i < f.returns.size(); ++i) {
+      const Value *v = f.returns[i];
+      if (v->argIdx >= 0) continue;
+      if (v->type.shape != A.D) throw CompileError("elementwise group result must span the whole domain");
+      ensure(v);
+      std::string src = name[v];
+      Elem e = v->type.elem;
+      if (!vec[v] || e == Elem::I1) {
+        std::string t = fresh();
+        body << "    " << mtype(e) << " " << t << "[VEC];\n    for (int e = 0; e < VEC; ++e) " << t << "[e] = " << at(v) << ";\n";
+        src = t;
+      }
+      body << "    hf::vec_store<" << mtype(e) << ", VEC>((" << mtype(e) << "*)" << resultPtr(A, i) << " + base, " << src << ");\n";
+    }
+    KernelPlan p;
+    p.kernelName = kname;
+    p.kind = kind;
+    p.variant = "streaming";
+    int block = 256;
+    int64_t nch = N / VEC;
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(" << block << ") void " << kname << "("
+      << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  constexpr int VEC = " << VEC << ";\n"
+      << "  constexpr int64_t NCH = " << nch << "ll;\n"
+      << "  for (int64_t ch = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; ch < NCH; ch += (int64_t)gridDim.x * blockDim.x) {\n"
+      << "    const int64_t base = ch * VEC;\n"
+      << body.str() << "  }\n}\n";
+    p.source = k.str();
+    int64_t grid = (nch + block - 1) / block;
+    if (grid > (1 << 20)) grid = 1 << 20;
+    if (grid < 1) grid = 1;
+    p.grid[0] = (unsigned)grid;
+    p.block[0] = block;
+    return p;
+  }
+};
+
+// ======================================================================
+// REDUCE_WITH_INDEX
+// ======================================================================
+KernelPlan lowerReduceWithIndex(Analysis &A, const std::string &kname) {
+  Func &f = *A.f;
+  const Op *rw = findOp(f, [](const Op *o) { return o->name == "hfusion.reduce_with_index"; });
+  for (const Op *op : f.ops) {
+    const std::string &n = op->name;
+    if (op == rw || n == "tensor.empty" || n == "linalg.fill" || n == "arith.constant" || n == "tensor.dim") continue;
+    unsupported(op, "op fused with hfusion.reduce_with_index");
+  }
+  if (rw->ins.size() != 1) unsupported(rw, "reduce_with_index with an index input");
+  const Value *x = rw->ins[0];
+  if (x->argIdx < 0) unsupported(rw, "reduce_with_index input must be a group argument");
+  int rank = (int)x->type.shape.size();
+  if (rw->dims.size() != 1 || rw->dims[0] != rank - 1) unsupported(rw, "reduce_with_index over a non-last axis");
+  std::string kindS = rw->angleKind.empty() ? rw->attr("reduce_kind", "max") : rw->angleKind;
+  int kind;
+  if (kindS == "max") kind = 0;
+  else if (kindS == "min") kind = 1;
+  else unsupported(rw, "reduce_with_index kind '" + kindS + "'");
+  if (x->type.elem != Elem::F32) unsupported(rw, "reduce_with_index over non-f32 values");
+  int64_t C = x->type.shape.back(), R = 1;
+  for (int i = 0; i + 1 < rank; ++i) R *= x->type.shape[i];
+  Elem idxE = rw->outs[1]->type.elem;
+  if (idxE != Elem::I32 && idxE != Elem::I64) unsupported(rw, "index type");
+  auto initOf = [&](const Value *o, Elem e) -> std::string {
+    if (o->def && o->def->name == "linalg.fill") {
+      const Value *c = o->def->ins[0];
+      if (c->isConst) return constExpr(c, e);
+      if (c->argIdx >= 0) return scalarArgExpr(A, c->argIdx);
+    }
+    if (o->argIdx >= 0) return "INIT_FROM_ARG";
+    unsupported(rw, "reduce_with_index init must be a linalg.fill");
+  };
+  std::string iv = initOf(rw->outs[0], Elem::F32), ii = initOf(rw->outs[1], idxE);
+  std::string ivArg, iiArg;
+  if (iv == "INIT_FROM_ARG") { ivArg = "p" + std::to_string(rw->outs[0]->argIdx); iv = ""; }
+  if (ii == "INIT_FROM_ARG") { iiArg = "p" + std::to_string(rw->outs[1]->argIdx); ii = ""; }
+  // output pointers
+  std::string outV = "nullptr", outI = "nullptr";
+  for (size_t i = 0; i < f.returns.size(); ++i) {
+    const Value *v = f.returns[i];
+    if (v->def != rw) unsupported(rw, "group returns a value other than the reduction results");
+    (v->resultIdx == 0 ? outV : outI) = resultPtr(A, i);
+  }
+  // schedule: split every row into SEG segments of whole 1024-element tiles
+  const int BLOCK = 256;
+  int64_t tiles = (C + 1023) / 1024;
+  int64_t segs = 1;
+  while (R * segs < 2048 && segs * 2 <= tiles) segs *= 2;
+  int64_t segLen = ((tiles + segs - 1) / segs) * 1024;
+  segs = (C + segLen - 1) / segLen;
+  bool aligned = (C % 4) == 0;
+  KernelPlan p;
+  p.kernelName = kname;
+  p.kind = "REDUCE_WITH_INDEX";
+  p.variant = "split-row two-level, last-block combine";
+  std::ostringstream k;
+  std::string IT = ctype(idxE);
+  k << "extern \"C\" __global__ __launch_bounds__(" << BLOCK << ") void " << kname << "("
+    << kernelParamList(A, p.kargs, true) << ") {\n"
+    << "  constexpr int64_t R = " << R << "ll, C = " << C << "ll, SEG = " << segs << "ll, SEGLEN = " << segLen << "ll;\n"
+    << "  const float init_v = " << (ivArg.empty() ? iv : "((const float*)" + ivArg + ")[blockIdx.x / SEG]") << ";\n"
+    << "  const " << IT << " init_i = " << (iiArg.empty() ? ii : "((const " + IT + "*)" + iiArg + ")[blockIdx.x / SEG]") << ";\n"
+    << "  hf::argreduce_rows<" << kind << ", " << BLOCK << ", " << (aligned ? "true" : "false") << ", " << IT
+    << ">((const float*)p" << x->argIdx << ", R, C, SEG, SEGLEN, init_v, init_i, (float*)" << outV << ", (" << IT << "*)" << outI
+    << ", ws);\n}\n";
+  p.source = k.str();
+  p.grid[0] = (unsigned)(R * segs);
+  p.block[0] = BLOCK;
+  // workspace: per-segment partial records + one arrival counter per row
+  p.workspaceBytes = (uint64_t)(R * segs * 16 + R * 4 + 256);
+  p.workspaceZeroInit = true;
+  return p;
+}
+
+// ======================================================================
+// SINGLE_CUBE: matmul + elementwise epilogue
+// ======================================================================
+KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
+  Func &f = *A.f;
+  const Op *mm = findOp(f, [](const Op *o) { return o->name == "linalg.matmul" || o->name == "linalg.matmul_transpose_b"; });
+  bool bT = mm->name == "linalg.matmul_transpose_b";
+  const Value *a = mm->ins[0], *b = mm->ins[1];
+  if (a->argIdx < 0 || b->argIdx < 0) unsupported(mm, "matmul operands must be group arguments");
+  int64_t M = a->type.shape[0], K = a->type.shape[1];
+  int64_t N = bT ? b->type.shape[0] : b->type.shape[1];
+  if ((bT ? b->type.shape[1] : b->type.shape[0]) != K) unsupported(mm, "matmul shapes");
+  Elem ae = a->type.elem, be = b->type.elem, ce = mm->results[0]->type.elem;
+  bool i8 = ae == Elem::I8 && be == Elem::I8 && ce == Elem::I32;
+  bool bf = ae == Elem::BF16 && be == Elem::BF16 && ce == Elem::F32;
+  if (!i8 && !bf) unsupported(mm, "matmul element types (supported: i8 x i8 -> i32, bf16 x bf16 -> f32)");
+  const int esz = elemBytes(ae);
+  if ((K * esz) % 16 != 0) unsupported(mm, "matmul K must span a multiple of 16 bytes");
+  if (!bT && (N * esz) % 16 != 0) unsupported(mm, "matmul N must span a multiple of 16 bytes when B is [K, N]");
+  const Value *acc0 = mm->outs[0];
+  if (!(acc0->def && acc0->def->name == "linalg.fill" && acc0->def->ins[0]->isConst && acc0->def->ins[0]->fconst == 0.0))
+    unsupported(mm, "matmul accumulator must start from a zero linalg.fill");
+  // epilogue over D = [M, N] with the matmul result as the accumulator
+  std::set<const Value *> excl = {a, b};
+  A.D = {M, N};
+  inferMaps(A, excl);
+  std::ostringstream epi;
+  std::map<const Value *, std::string> name;
+  int tmp = 0;
+  auto ensure = [&](const Value *v) {
+    if (name.count(v)) return;
+    if (v == mm->results[0]) { name[v] = "acc"; return; }
+    if (v->isConst || !v->type.tensor) {
+      if (v->isConst) name[v] = constExpr(v, v->type.elem);
+      else if (v->argIdx >= 0) name[v] = scalarArgExpr(A, v->argIdx);
+      else throw CompileError("non-constant scalar in epilogue");
+      return;
+    }
+    if (v->argIdx < 0) throw CompileError("internal: epilogue value " + v->name);
+    const auto &m = A.map.at(v);
+    std::string idx = m.size() == 2 ? "m * " + std::to_string(N) + "ll + n" : (m.empty() ? "0" : (m[0] == 0 ? "m" : "n"));
+    std::string nm = "e" + std::to_string(tmp++);
+    epi << "    const " << ctype(v->type.elem) << " " << nm << " = ((const " << mtype(v->type.elem) << "*)P.p" << v->argIdx << ")[" << idx << "];\n";
+    name[v] = nm;
+  };
+  for (const Op *op : f.ops) {
+    const std::string &n = op->name;
+    if (op == mm || n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" || n == "linalg.fill") continue;
+    if (n.rfind("arith.", 0) == 0 && !op->results[0]->type.tensor) continue;
+    if (n == "linalg.broadcast") {
+      ensure(op->ins[0]);
+      name[op->results[0]] = name[op->ins[0]];
+      continue;
+    }
+    if (!isElementwiseOp(op)) unsupported(op, "op in a matmul epilogue");
+    std::vector<const Value *> opsv;
+    for (auto *v : op->ins) opsv.push_back(v);
+    for (auto *v : op->operands) opsv.push_back(v);
+    std::vector<std::string> args;
+    std::vector<Elem> at_;
+    for (auto *v : opsv) { ensure(v); args.push_back(name[v]); at_.push_back(v->type.elem); }
+    std::string nm = "t" + std::to_string(tmp++);
+    Elem U = op->results[0]->type.elem;
+    epi << "    const " << ctype(U) << " " << nm << " = " << elementExpr(op, args, at_, U) << ";\n";
+    name[op->results[0]] = nm;
+  }
+  if (f.returns.size() != 1) unsupported(mm, "matmul groups must return exactly one tensor");
+  const Value *outv = f.returns[0];
+  if (outv->type.shape != std::vector<int64_t>{M, N}) unsupported(mm, "matmul group result shape");
+  ensure(outv);
+  Elem oe = outv->type.elem;
+  KernelPlan p;
+  p.kernelName = kname;
+  p.kind = "SINGLE_CUBE";
+  std::ostringstream k;
+  std::string params = kernelParamList(A, p.kargs, false);
+  // epilogue functor receives all kernel pointer arguments
+  k << "namespace {\nstruct " << kname << "_args {";
+  for (size_t i = 0; i < A.params.size(); ++i)
+    k << (A.params[i].role == "scalar" ? " uint64_t s" : " const void* p") << i << ";";
+  k << " };\n"
+    << "struct " << kname << "_epi {\n"
+    << "  using out_t = " << mtype(oe) << ";\n"
+    << "  __device__ __forceinline__ static out_t apply(" << (i8 ? "int32_t" : "float") << " acc, int64_t m, int64_t n, const "
+    << kname << "_args& P) {\n";
+  for (size_t i = 0; i < A.params.size(); ++i)
+    if (A.params[i].role == "scalar") k << "    const uint64_t s" << i << " = P.s" << i << ";\n";
+  k << epi.str() << "    return (out_t)" << name[outv] << ";\n  }\n};\n}\n";
+  k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+    << "  " << kname << "_args P;\n";
+  for (size_t i = 0; i < A.params.size(); ++i)
+    k << "  P." << (A.params[i].role == "scalar" ? "s" : "p") << i << " = " << (A.params[i].role == "scalar" ? "s" : "p") << i << ";\n";
+  k << "  hf::" << (i8 ? "mmad_i8" : "mmad_bf16") << "<" << kname << "_epi, " << (bT ? "true" : "false") << ">((const "
+    << (i8 ? "int8_t" : "uint16_t") << "*)p" << a->argIdx << ", (const " << (i8 ? "int8_t" : "uint16_t") << "*)p" << b->argIdx
+    << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
+  p.source = k.str();
+  // 256x256 macro-tiles, one workgroup each (XCD-aware order inside the kernel)
+  const int64_t TM = 256, TN = 256;
+  p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
+  p.block[0] = 256;
+  p.variant = std::string(i8 ? "mfma_i32_32x32x32_i8" : "mfma_f32_32x32x16_bf16") + (bT ? ", B [N,K]" : ", B [K,N]");
+  p.algoOps = 2.0 * (double)M * (double)N * (double)K;
+  return p;
+}
+
+} // namespace
+
+std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
+  std::vector<KernelPlan> out;
+  bool anyEntry = false;
+  for (auto &f : m.funcs) anyEntry |= f->isEntry();
+  for (auto &fp : m.funcs) {
+    Func &f = *fp;
+    if (anyEntry && !f.isEntry()) continue;
+    foldConstants(f);
+    Analysis A;
+    A.f = &f;
+    describeBuffers(A);
+    bool hasMM, hasRWI, hasRed;
+    std::string kind = resultKind(f, &hasMM, &hasRWI, &hasRed);
+    std::string kname = "hf_" + f.name;
+    KernelPlan p;
+    if (kind == "SINGLE_CUBE") {
+      p = lowerMatmul(A, kname);
+    } else if (kind == "REDUCE_WITH_INDEX") {
+      p = lowerReduceWithIndex(A, kname);
+    } else {
+      A.D = largestShape(f, {});
+      if (A.D.empty()) throw CompileError("group @" + f.name + " has no tensor to iterate over");
+      inferMaps(A, {});
+      if (kind == "LAST_AXIS_PBR") {
+        RowEmitter e(A, opt);
+        p = e.run(kname, kind);
+      } else {
+        bool anyBrc = false;
+        for (auto &kv : A.map) anyBrc |= kv.second.size() != A.D.size();
+        EltwiseEmitter e(A);
+        p = e.run(kname, anyBrc ? "ANY_PB" : "PURE_ELEMWISE");
+      }
+    }
+    p.funcName = f.name;
+    p.params = A.params;
+    p.results = A.results;
+    p.algoBytes = algoBytes(A);
+    std::string declared = f.fusionKind();
+    if (!declared.empty() && declared != p.kind && !(declared == "PURE_ELEMWISE" && p.kind == "ANY_PB") &&
+        !(declared == "ANY_PB" && p.kind == "PURE_ELEMWISE") && !(declared == "ANY_PBR" && p.kind == "LAST_AXIS_PBR") &&
+        !(declared == "LAST_AXIS_PBR" && p.kind == "REDUCE_WITH_INDEX"))
+      p.variant += " (declared " + declared + ")";
+    out.push_back(p);
+  }
+  if (out.empty()) throw CompileError("no kernel functions in module");
+  return out;
+}
+
+std::string emitTranslationUnit(const std::vector<KernelPlan> &plans) {
+  std::ostringstream s;
+  s << "// Generated by bishengir-compile --target=mi355x (ConvertHFusionToHIP).\n"
+    << "#include \"hf_ops.h\"\n#include \"hf_row.h\"\n#include \"hf_argmax.h\"\n#include \"hf_mmad.h\"\n\n";
+  for (auto &p : plans) s << "// group @" << p.funcName << ": " << p.kind << " (" << p.variant << ")\n" << p.source << "\n";
+  return s.str();
+}
+
+std::string emitManifest(const KernelPlan &p, const std::string &hsacoName) {
+  std::ostringstream s;
+  s << "hfr-manifest 1\n"
+    << "func " << p.funcName << "\n"
+    << "kernel " << p.kernelName << "\n"
+    << "hsaco " << hsacoName << "\n"
+    << "kind " << p.kind << "\n"
+    << "grid " << p.grid[0] << " " << p.grid[1] << " " << p.grid[2] << "\n"
+    << "block " << p.block[0] << " " << p.block[1] << " " << p.block[2] << "\n"
+    << "lds " << p.ldsBytes << "\n"
+    << "workspace " << p.workspaceBytes << " " << (p.workspaceZeroInit ? 1 : 0) << "\n"
+    << "algo_bytes " << (uint64_t)p.algoBytes << "\n"
+    << "algo_ops " << (uint64_t)p.algoOps << "\n";
+  auto shp = [](const std::vector<int64_t> &v) {
+    std::string r = std::to_string(v.size());
+    for (auto d : v) r += " " + std::to_string(d);
+    return r;
+  };
+  for (size_t i = 0; i < p.params.size(); ++i)
+    s << "param " << i << " " << p.params[i].role << " " << elemName(p.params[i].elem) << " " << shp(p.params[i].shape) << "\n";
+  for (size_t i = 0; i < p.results.size(); ++i)
+    s << "result " << i << " " << p.results[i].tiedParam << " " << elemName(p.results[i].elem) << " " << shp(p.results[i].shape) << "\n";
+  for (auto &k : p.kargs) s << "karg " << k << "\n";
+  s << "variant " << p.variant << "\n";
+  return s.str();
+}
+
+} // namespace hfc

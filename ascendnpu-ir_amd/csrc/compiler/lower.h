@@ -1,0 +1,57 @@
+// ConvertHFusionToHIP: maps one outlined HFusion op group (a `func.func`) onto
+// a CDNA4 HIP kernel plus a launch manifest.
+//
+// This takes the place of the reference's HFusion->HIVM->Template path
+// (bishengir/lib/Conversion/HFusionToHIVM/HFusionToHIVM.cpp:1785-1933,
+// bishengir/lib/Dialect/HIVM/Pipelines/HIVMPipelines.cpp:516-546) and of the
+// external `hivmc` step (bishengir/lib/Tools/bishengir-compile/
+// BiShengIRCompileMain.cpp:188-262).
+#pragma once
+#include "ir.h"
+
+#include <string>
+#include <vector>
+
+namespace hfc {
+
+struct BufferDesc {
+  std::string role;  // "in", "out", "inout", "scalar"
+  Elem elem = Elem::None;
+  std::vector<int64_t> shape;
+  int tiedParam = -1; // results: the func argument they are written into
+};
+
+struct KernelPlan {
+  std::string funcName;
+  std::string kernelName;
+  std::string kind;           // PURE_ELEMWISE | LAST_AXIS_PBR | REDUCE_WITH_INDEX | SINGLE_CUBE
+  std::string variant;        // schedule detail, e.g. "ordered-sum"
+  std::string source;         // HIP translation-unit body (kernel only)
+  unsigned grid[3] = {1, 1, 1};
+  unsigned block[3] = {1, 1, 1};
+  unsigned ldsBytes = 0;      // dynamic LDS
+  uint64_t workspaceBytes = 0;
+  bool workspaceZeroInit = false; // workspace must be zero when first used
+  std::vector<BufferDesc> params;  // func arguments, in order
+  std::vector<BufferDesc> results; // func results, in order
+  // kernel argument list, each "param:<i>", "result:<i>", "ws"
+  std::vector<std::string> kargs;
+  double algoBytes = 0;       // algorithmic HBM bytes per launch
+  double algoOps = 0;         // algorithmic ops per launch (cube groups)
+};
+
+struct LowerOptions {
+  bool orderedFloatSums = false; // force serial-order fp sums everywhere
+};
+
+// Lowers every `hacc.entry` function (or every function if none is tagged).
+std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt);
+
+// The text of the HIP source file holding all `plans` (includes the kernel
+// library headers).
+std::string emitTranslationUnit(const std::vector<KernelPlan> &plans);
+
+// The launch manifest (line-oriented text, read by libhfr and the host API).
+std::string emitManifest(const KernelPlan &p, const std::string &hsacoName);
+
+} // namespace hfc

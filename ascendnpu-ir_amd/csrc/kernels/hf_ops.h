@@ -1,0 +1,158 @@
+// Scalar semantics of HFusion/linalg region bodies on CDNA4 (gfx950).
+//
+// Every function here is the device-side meaning of one op of the region
+// builders in bishengir/lib/Dialect/HFusion/IR/HFusionOps.cpp:434-862
+// (unary/binary/compare/ternary fns, cast with RoundMode) and
+// :1507-1595 (reduce_with_index).  Kernels are compiled with
+// -ffp-contract=off so that mul/add stay separately rounded as in the
+// reference's CPU lowering; fp32 division and sqrt are the correctly rounded
+// HIP defaults.
+//
+// Storage types in registers: f32 -> float, f64 -> double, bf16/f16 -> the
+// 16-bit pattern in uint16_t, iN -> intN_t, i1 -> bool.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace hf {
+
+// RoundMode numbering of HFusionEnums.td:122-141
+enum RoundMode : int { RINT = 0, ROUND = 1, FLOOR = 2, CEIL = 3, TRUNC = 4, ODD = 5, TRUNCWO = 6 };
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// ---------------------------------------------------------------- bf16/f16
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+// Round-to-nearest-even f32 -> bf16; NaN stays a quiet NaN of the same sign.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = f2u(f);
+  uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (f != f) ? (uint16_t)((u >> 16) | 0x40u) : (uint16_t)r;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Rounds the exact value `a` (given as double; every f32/int32 value is exact
+// in double) onto a binary format with `p` significand bits and exponent range
+// [emin, emax] under `mode`.  Directed modes and round-to-odd follow the
+// IEEE-754 definitions; overflow goes to inf or to the largest finite value as
+// the mode dictates.
+__device__ inline double round_to_format(double x, int p, int emin, int emax, int mode) {
+  if (x != x || x == 0.0 || __builtin_isinf(x)) return x;
+  bool neg = x < 0;
+  double a = neg ? -x : x;
+  int lead = ilogb(a);
+  if (lead < emin) lead = emin;
+  double q = ldexp(1.0, lead - (p - 1));
+  double s = a / q;
+  double fl = floor(s), fr = s - fl;
+  bool odd = fmod(fl, 2.0) != 0.0;
+  double r;
+  switch (mode) {
+  case RINT: r = (fr > 0.5 || (fr == 0.5 && odd)) ? fl + 1 : fl; break;
+  case ROUND: r = fr >= 0.5 ? fl + 1 : fl; break;
+  case FLOOR: r = (neg && fr > 0) ? fl + 1 : fl; break;
+  case CEIL: r = (!neg && fr > 0) ? fl + 1 : fl; break;
+  case ODD: r = (fr > 0 && !odd) ? fl + 1 : fl; break;
+  default: r = fl;
+  }
+  double v = r * q;
+  double maxf = ldexp(2.0 - ldexp(1.0, -(p - 1)), emax);
+  if (v > maxf) {
+    bool to_inf = (mode == RINT || mode == ROUND) || (mode == FLOOR && neg) ||
+                  (mode == CEIL && !neg);
+    v = to_inf ? __builtin_inf() : maxf;
+  }
+  return neg ? -v : v;
+}
+
+template <int MODE> __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  if constexpr (MODE == RINT) {
+    return f32_to_bf16_rne(f);
+  } else {
+    if (f != f) return f32_to_bf16_rne(f);
+    float v = (float)round_to_format((double)f, 8, -126, 127, MODE);
+    return (uint16_t)(f2u(v) >> 16);
+  }
+}
+
+template <int MODE> __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  if constexpr (MODE == RINT) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  } else {
+    if (f != f) return __builtin_bit_cast(uint16_t, (_Float16)f);
+    double v = round_to_format((double)f, 11, -14, 15, MODE);
+    // v is on the f16 grid (or +-inf), so the RNE conversion is exact
+    return __builtin_bit_cast(uint16_t, (_Float16)(float)v);
+  }
+}
+
+// ---------------------------------------------------------------- ints
+template <int MODE> __device__ __forceinline__ float round_integral(float x) {
+  if constexpr (MODE == RINT) return __builtin_roundevenf(x);
+  else if constexpr (MODE == ROUND) return __builtin_roundf(x);
+  else if constexpr (MODE == FLOOR) return __builtin_floorf(x);
+  else if constexpr (MODE == CEIL) return __builtin_ceilf(x);
+  else if constexpr (MODE == ODD) {
+    float t = __builtin_truncf(x);
+    if (t != x && __builtin_fmodf(t, 2.0f) == 0.0f) t += (x < 0 ? -1.0f : 1.0f);
+    return t;
+  } else return __builtin_truncf(x);
+}
+
+// hfusion.cast float -> signed integer of type T: round per MODE, then either
+// clamp (saturate; NaN -> 0) or keep the low bits (two's-complement wrap).
+template <typename T, int MODE, bool SAT> __device__ __forceinline__ T f32_to_int(float f) {
+  float r = round_integral<MODE>(f);
+  if constexpr (SAT) {
+    constexpr double lo = -(double)(1ull << (sizeof(T) * 8 - 1));
+    constexpr double hi = (double)(1ull << (sizeof(T) * 8 - 1)) - 1.0;
+    if (r != r) return (T)0;
+    double d = (double)r;
+    d = d < lo ? lo : (d > hi ? hi : d);
+    return (T)(int64_t)d;
+  } else {
+    if constexpr (sizeof(T) <= 4) {
+      // in-range values convert exactly; v_cvt_i32_f32 clamps otherwise
+      if (r >= -2147483648.0f && r < 2147483648.0f) return (T)(int32_t)r;
+      return (T)(int64_t)r;
+    } else {
+      return (T)(int64_t)r;
+    }
+  }
+}
+
+// arith.fptosi (the CPU lowering's f32 -> iN): truncation toward zero.
+template <typename T> __device__ __forceinline__ T fptosi(float f) { return (T)(int64_t)__builtin_truncf(f); }
+
+// integer -> f32 under MODE (sitofp is RINT)
+template <int MODE> __device__ __forceinline__ float int_to_f32(int64_t v) {
+  if constexpr (MODE == RINT) return (float)v;
+  else return (float)round_to_format((double)v, 24, -126, 127, MODE);
+}
+
+// ---------------------------------------------------------------- float fns
+__device__ __forceinline__ float maximumf(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float minimumf(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float maxnumf(float a, float b) { return __builtin_fmaxf(a, b); }
+__device__ __forceinline__ float minnumf(float a, float b) { return __builtin_fminf(a, b); }
+
+__device__ __forceinline__ float add(float a, float b) { return a + b; }
+__device__ __forceinline__ float sub(float a, float b) { return a - b; }
+__device__ __forceinline__ float mul(float a, float b) { return a * b; }
+__device__ __forceinline__ float div(float a, float b) { return a / b; }
+__device__ __forceinline__ float rec(float a) { return 1.0f / a; }
+__device__ __forceinline__ float relu(float a) { return maximumf(0.0f, a); }
+__device__ __forceinline__ float rsqrt(float a) { return 1.0f / __builtin_sqrtf(a); }
+
+// ---------------------------------------------------------------- wave64
+// Butterfly exchange across the 64 lanes of a wavefront.
+template <typename T> __device__ __forceinline__ T shfl_xor(T v, int m) { return __shfl_xor(v, m, 64); }
+
+} // namespace hf

@@ -1,0 +1,281 @@
+// hfr — C-ABI HIP runtime for HFusion group kernels.  See include/hfr.h.
+//
+// hipModuleLoad / hipModuleGetFunction / hipModuleLaunchKernel take the place
+// of the CANN rtDevBinaryRegister / rtFunctionRegister / rtKernelLaunch calls
+// of bishengir/test/Integration/HIVM/VecAdd/main.cpp.
+#include "../../../include/hfr.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <vector>
+
+struct hfr_module {
+  hipModule_t mod = nullptr;
+  std::string path;
+  int refs = 1;
+};
+
+struct hfr_kernel {
+  hipFunction_t fn = nullptr;
+  hfr_module *owner = nullptr;
+};
+
+struct Karg {
+  enum Kind { Param, Result, Workspace } kind;
+  int index;
+};
+
+struct hfr_group {
+  std::string func, kernel, hsaco;
+  hfr_module *mod = nullptr;
+  hipFunction_t fn = nullptr;
+  hfr_launch_cfg cfg{};
+  uint64_t wsBytes = 0;
+  bool wsZero = false;
+  uint64_t algoBytes = 0, algoOps = 0;
+  std::vector<std::string> paramRoles;
+  std::vector<int> resultTied;
+  std::vector<Karg> kargs;
+  void *ownWs = nullptr;
+  int ownWsDevice = -1;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+  g_err = msg;
+  return code;
+}
+
+int hipFail(hipError_t e, const char *what) {
+  return fail(HFR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+std::string dirOf(const std::string &p) {
+  auto s = p.find_last_of('/');
+  return s == std::string::npos ? "." : p.substr(0, s);
+}
+
+// Parses one manifest block (lines after "hfr-manifest 1" until the next one).
+int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
+  for (const auto &ln : lines) {
+    std::istringstream is(ln);
+    std::string key;
+    is >> key;
+    if (key == "func") is >> g.func;
+    else if (key == "kernel") is >> g.kernel;
+    else if (key == "hsaco") is >> g.hsaco;
+    else if (key == "grid") is >> g.cfg.grid[0] >> g.cfg.grid[1] >> g.cfg.grid[2];
+    else if (key == "block") is >> g.cfg.block[0] >> g.cfg.block[1] >> g.cfg.block[2];
+    else if (key == "lds") is >> g.cfg.lds_bytes;
+    else if (key == "workspace") { int z = 0; is >> g.wsBytes >> z; g.wsZero = z != 0; }
+    else if (key == "algo_bytes") is >> g.algoBytes;
+    else if (key == "algo_ops") is >> g.algoOps;
+    else if (key == "param") { int i; std::string role; is >> i >> role; g.paramRoles.push_back(role); }
+    else if (key == "result") { int i, tied; is >> i >> tied; g.resultTied.push_back(tied); }
+    else if (key == "karg") {
+      std::string k;
+      is >> k;
+      Karg a;
+      if (k == "ws") { a.kind = Karg::Workspace; a.index = 0; }
+      else if (k.rfind("param:", 0) == 0) { a.kind = Karg::Param; a.index = std::atoi(k.c_str() + 6); }
+      else if (k.rfind("result:", 0) == 0) { a.kind = Karg::Result; a.index = std::atoi(k.c_str() + 7); }
+      else return fail(HFR_ERR_MANIFEST, "bad karg '" + k + "'");
+      g.kargs.push_back(a);
+    }
+    if (is.fail()) return fail(HFR_ERR_MANIFEST, "malformed manifest line: " + ln);
+  }
+  if (g.kernel.empty() || g.hsaco.empty()) return fail(HFR_ERR_MANIFEST, "manifest block without kernel/hsaco");
+  if (!g.cfg.block[0] || !g.cfg.grid[0]) return fail(HFR_ERR_MANIFEST, "manifest block without launch shape");
+  for (auto &a : g.kargs) {
+    if (a.kind == Karg::Param && (a.index < 0 || a.index >= (int)g.paramRoles.size()))
+      return fail(HFR_ERR_MANIFEST, "karg refers to a missing param");
+    if (a.kind == Karg::Result && (a.index < 0 || a.index >= (int)g.resultTied.size()))
+      return fail(HFR_ERR_MANIFEST, "karg refers to a missing result");
+  }
+  return HFR_OK;
+}
+
+int launchRaw(hipFunction_t fn, const hfr_launch_cfg &cfg, const uint64_t *args, size_t nargs, void *stream) {
+  std::vector<uint64_t> buf(args, args + nargs);
+  size_t sz = buf.size() * sizeof(uint64_t);
+  void *extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, buf.empty() ? nullptr : buf.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                   HIP_LAUNCH_PARAM_END};
+  hipError_t e = hipModuleLaunchKernel(fn, cfg.grid[0], cfg.grid[1] ? cfg.grid[1] : 1, cfg.grid[2] ? cfg.grid[2] : 1,
+                                       cfg.block[0], cfg.block[1] ? cfg.block[1] : 1, cfg.block[2] ? cfg.block[2] : 1,
+                                       cfg.lds_bytes, (hipStream_t)stream, nullptr, extra);
+  if (e != hipSuccess) return hipFail(e, "hipModuleLaunchKernel");
+  return HFR_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *hfr_version(void) { return "hfr 0.1 (gfx950)"; }
+const char *hfr_last_error(void) { return g_err.c_str(); }
+
+int hfr_module_load(const char *hsaco_path, hfr_module_t *out) {
+  if (!hsaco_path || !out) return fail(HFR_ERR_INVALID, "null argument to hfr_module_load");
+  std::ifstream probe(hsaco_path, std::ios::binary);
+  if (!probe) return fail(HFR_ERR_IO, std::string("cannot open code object ") + hsaco_path);
+  auto m = std::make_unique<hfr_module>();
+  hipError_t e = hipModuleLoad(&m->mod, hsaco_path);
+  if (e != hipSuccess) return hipFail(e, "hipModuleLoad");
+  m->path = hsaco_path;
+  *out = m.release();
+  return HFR_OK;
+}
+
+int hfr_module_unload(hfr_module_t m) {
+  if (!m) return fail(HFR_ERR_INVALID, "null module");
+  if (--m->refs > 0) return HFR_OK;
+  hipError_t e = hipModuleUnload(m->mod);
+  delete m;
+  if (e != hipSuccess) return hipFail(e, "hipModuleUnload");
+  return HFR_OK;
+}
+
+int hfr_kernel_get(hfr_module_t m, const char *name, hfr_kernel_t *out) {
+  if (!m || !name || !out) return fail(HFR_ERR_INVALID, "null argument to hfr_kernel_get");
+  hipFunction_t fn;
+  hipError_t e = hipModuleGetFunction(&fn, m->mod, name);
+  if (e != hipSuccess) return fail(HFR_ERR_NOT_FOUND, std::string("kernel '") + name + "' not in " + m->path);
+  auto k = new hfr_kernel();
+  k->fn = fn;
+  k->owner = m;
+  *out = k;
+  return HFR_OK;
+}
+
+int hfr_launch(hfr_kernel_t k, const hfr_launch_cfg *cfg, const uint64_t *args, size_t nargs, void *stream) {
+  if (!k || !cfg || (nargs && !args)) return fail(HFR_ERR_INVALID, "null argument to hfr_launch");
+  return launchRaw(k->fn, *cfg, args, nargs, stream);
+}
+
+int hfr_group_load(const char *manifest_path, const char *func, hfr_group_t *out) {
+  if (!manifest_path || !out) return fail(HFR_ERR_INVALID, "null argument to hfr_group_load");
+  std::ifstream f(manifest_path);
+  if (!f) return fail(HFR_ERR_IO, std::string("cannot open manifest ") + manifest_path);
+  std::vector<std::vector<std::string>> blocks;
+  std::string ln;
+  while (std::getline(f, ln)) {
+    if (ln.rfind("hfr-manifest", 0) == 0) {
+      if (ln != "hfr-manifest 1") return fail(HFR_ERR_MANIFEST, "unsupported manifest version: " + ln);
+      blocks.emplace_back();
+      continue;
+    }
+    if (blocks.empty()) return fail(HFR_ERR_MANIFEST, "manifest must start with 'hfr-manifest 1'");
+    if (!ln.empty()) blocks.back().push_back(ln);
+  }
+  if (blocks.empty()) return fail(HFR_ERR_MANIFEST, "empty manifest");
+  auto g = std::make_unique<hfr_group>();
+  bool found = false;
+  for (auto &b : blocks) {
+    hfr_group cand;
+    int rc = parseBlock(b, cand);
+    if (rc) return rc;
+    if (!func || cand.func == func) {
+      if (!func && blocks.size() > 1) return fail(HFR_ERR_INVALID, "manifest holds several groups; name one");
+      *g = cand;
+      found = true;
+      break;
+    }
+  }
+  if (!found) return fail(HFR_ERR_NOT_FOUND, std::string("group '") + (func ? func : "") + "' not in manifest");
+  std::string hsaco = g->hsaco[0] == '/' ? g->hsaco : dirOf(manifest_path) + "/" + g->hsaco;
+  int rc = hfr_module_load(hsaco.c_str(), &g->mod);
+  if (rc) return rc;
+  hipError_t e = hipModuleGetFunction(&g->fn, g->mod->mod, g->kernel.c_str());
+  if (e != hipSuccess) {
+    hfr_module_unload(g->mod);
+    return fail(HFR_ERR_NOT_FOUND, "kernel '" + g->kernel + "' not in " + hsaco);
+  }
+  *out = g.release();
+  return HFR_OK;
+}
+
+int hfr_group_unload(hfr_group_t g) {
+  if (!g) return fail(HFR_ERR_INVALID, "null group");
+  int rc = HFR_OK;
+  if (g->ownWs) {
+    int cur = 0;
+    hipGetDevice(&cur);
+    if (g->ownWsDevice >= 0) hipSetDevice(g->ownWsDevice);
+    hipError_t e = hipFree(g->ownWs);
+    hipSetDevice(cur);
+    if (e != hipSuccess) rc = hipFail(e, "hipFree(workspace)");
+  }
+  if (g->mod) {
+    int r2 = hfr_module_unload(g->mod);
+    if (!rc) rc = r2;
+  }
+  delete g;
+  return rc;
+}
+
+int hfr_group_info_get(hfr_group_t g, hfr_group_info *info) {
+  if (!g || !info) return fail(HFR_ERR_INVALID, "null argument to hfr_group_info_get");
+  info->nparams = (int)g->paramRoles.size();
+  info->nresults = (int)g->resultTied.size();
+  info->nkargs = (int)g->kargs.size();
+  info->workspace_bytes = g->wsBytes;
+  info->algo_bytes = g->algoBytes;
+  info->algo_ops = g->algoOps;
+  info->cfg = g->cfg;
+  return HFR_OK;
+}
+
+int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
+                     void *workspace, void *stream) {
+  if (!g) return fail(HFR_ERR_INVALID, "null group");
+  if (nparams != g->paramRoles.size())
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " takes " + std::to_string(g->paramRoles.size()) +
+                                     " arguments, got " + std::to_string(nparams));
+  if (nresults != g->resultTied.size())
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " has " + std::to_string(g->resultTied.size()) +
+                                     " results, got " + std::to_string(nresults));
+  if (nparams && !params) return fail(HFR_ERR_INVALID, "null params array");
+  for (size_t i = 0; i < nparams; ++i)
+    if (g->paramRoles[i] != "scalar" && params[i] == 0)
+      return fail(HFR_ERR_INVALID, "null device pointer for argument " + std::to_string(i));
+  for (size_t i = 0; i < nresults; ++i)
+    if (g->resultTied[i] < 0 && (!results || !results[i]))
+      return fail(HFR_ERR_INVALID, "null device pointer for result " + std::to_string(i));
+  void *ws = workspace;
+  if (g->wsBytes && !ws) {
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (!g->ownWs || g->ownWsDevice != dev) {
+      if (g->ownWs) return fail(HFR_ERR_INVALID, "group workspace belongs to another device");
+      hipError_t e = hipMalloc(&g->ownWs, g->wsBytes);
+      if (e != hipSuccess) return hipFail(e, "hipMalloc(workspace)");
+      e = hipMemset(g->ownWs, 0, g->wsBytes);
+      if (e != hipSuccess) return hipFail(e, "hipMemset(workspace)");
+      g->ownWsDevice = dev;
+    }
+    ws = g->ownWs;
+  }
+  std::vector<uint64_t> args;
+  args.reserve(g->kargs.size());
+  for (auto &a : g->kargs) {
+    switch (a.kind) {
+    case Karg::Param: args.push_back(params[a.index]); break;
+    case Karg::Result: args.push_back((uint64_t)(uintptr_t)results[a.index]); break;
+    case Karg::Workspace: args.push_back((uint64_t)(uintptr_t)ws); break;
+    }
+  }
+  return launchRaw(g->fn, g->cfg, args.data(), args.size(), stream);
+}
+
+} // extern "C"

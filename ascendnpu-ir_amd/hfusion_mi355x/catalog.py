@@ -1,0 +1,176 @@
+"""Every HFusion group this repository compiles ahead of time.
+
+`__graft_entry__.build()` compiles each entry, so that tests, `smoke()` and
+`bench.py` on a GPU machine load prebuilt code objects.  Entries are IR texts
+built from `groups.py` (the headline workloads at full and reduced sizes) plus
+groups exercising the generic lowering (elementwise chains, broadcasts,
+compare/select, cast round modes, multi-reduction rows).
+"""
+from . import groups as g
+
+_T = g._t
+_ATTRS = g._ATTRS
+
+
+def cast_modes(n=4096):
+    """One module, one group per (target type, round mode, saturate) pair."""
+    X = _T([n], "f32")
+    funcs = []
+    modes = ["rint", "round", "floor", "ceil", "trunc", "odd"]
+    for m in modes:
+        for tgt, sat in (("i8", True), ("i8", False), ("i32", False), ("bf16", False), ("f16", False)):
+            O = _T([n], tgt)
+            name = f"cast_{tgt}_{m}" + ("_sat" if sat else "")
+            satattr = ", enable_saturate = true" if sat else ""
+            funcs.append(f"""  func.func @{name}(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>{satattr}}} ins(%x : {X}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    # integer -> float round modes and same-type float rounding
+    I = _T([n], "i32")
+    for m in modes:
+        funcs.append(f"""  func.func @cast_i32_f32_{m}(%x: {I}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>}} ins(%x : {I}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+        funcs.append(f"""  func.func @cast_f32_f32_{m}(%x: {X}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>}} ins(%x : {X}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+def eltwise_mix(rows=64, cols=1000):
+    """ANY_PB group: row and column broadcasts, compare/select, unary math,
+    maximumf, an i1 output and a bf16 output."""
+    X, C, R = _T([rows, cols], "f32"), _T([cols], "f32"), _T([rows], "f32")
+    B, O, M = _T([rows, cols], "bf16"), _T([rows, cols], "f32"), _T([rows, cols], "i1")
+    return f"""module {{
+  func.func @eltwise_mix(%x: {X}, %b: {C}, %s: {R}, %y: {B}, %mask: {M}) -> ({B}, {M})
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %half = arith.constant 5.000000e-01 : f32
+    %e0 = tensor.empty() : {O}
+    %bb = linalg.broadcast ins(%b : {C}) outs(%e0 : {O}) dimensions = [0]
+    %e1 = tensor.empty() : {O}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e1 : {O}) dimensions = [1]
+    %gt = hfusion.compare {{compare_fn = #hfusion.compare_fn<vgt>}} ins(%x, %bb : {O}, {O}) outs(%mask : {M}) -> {M}
+    %e2 = tensor.empty() : {O}
+    %ex = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%x : {O}) outs(%e2 : {O}) -> {O}
+    %e3 = tensor.empty() : {O}
+    %t = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%ex, %bs : {O}, {O}) outs(%e3 : {O}) -> {O}
+    %e4 = tensor.empty() : {O}
+    %ng = linalg.elemwise_unary {{fun = #linalg.unary_fn<negf>}} ins(%x : {O}) outs(%e4 : {O}) -> {O}
+    %e5 = tensor.empty() : {O}
+    %sel = hfusion.select ins(%gt, %t, %ng : {M}, {O}, {O}) outs(%e5 : {O}) -> {O}
+    %e6 = tensor.empty() : {O}
+    %mx = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<maxf>}} ins(%sel, %half : {O}, f32) outs(%e6 : {O}) -> {O}
+    %e7 = tensor.empty() : {O}
+    %sq = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%mx : {O}) outs(%e7 : {O}) -> {O}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%sq : {O}) outs(%y : {B}) -> {B}
+    return %r, %gt : {B}, {M}
+  }}
+}}
+"""
+
+
+def layernorm(rows=64, cols=2048, eps=1e-5):
+    """LAST_AXIS_PBR group with two dependent sum reductions (mean, variance),
+    a column broadcast of weight and bias and an f32 row output (the mean)."""
+    X, W, R = _T([rows, cols], "f32"), _T([cols], "f32"), _T([rows], "f32")
+    return f"""module {{
+  func.func @layernorm(%x: {X}, %w: {W}, %bias: {W}, %y: {X}, %mu: {R}) -> ({X}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %zero = arith.constant 0.000000e+00 : f32
+    %n = arith.constant {float(cols):.6e} : f32
+    %eps = arith.constant {eps:.9e} : f32
+    %e0 = tensor.empty() : {R}
+    %f0 = linalg.fill ins(%zero : f32) outs(%e0 : {R}) -> {R}
+    %s = linalg.reduce {{arith.addf}} ins(%x : {X}) outs(%f0 : {R}) dimensions = [1]
+    %m = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%s, %n : {R}, f32) outs(%mu : {R}) -> {R}
+    %e1 = tensor.empty() : {X}
+    %bm = linalg.broadcast ins(%m : {R}) outs(%e1 : {X}) dimensions = [1]
+    %e2 = tensor.empty() : {X}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%x, %bm : {X}, {X}) outs(%e2 : {X}) -> {X}
+    %e3 = tensor.empty() : {X}
+    %d2 = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%d, %d : {X}, {X}) outs(%e3 : {X}) -> {X}
+    %e4 = tensor.empty() : {R}
+    %f4 = linalg.fill ins(%zero : f32) outs(%e4 : {R}) -> {R}
+    %v = linalg.reduce {{arith.addf}} ins(%d2 : {X}) outs(%f4 : {R}) dimensions = [1]
+    %e5 = tensor.empty() : {R}
+    %vm = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%v, %n : {R}, f32) outs(%e5 : {R}) -> {R}
+    %e6 = tensor.empty() : {R}
+    %ve = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%vm, %eps : {R}, f32) outs(%e6 : {R}) -> {R}
+    %e7 = tensor.empty() : {R}
+    %rs = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<rsqrt>}} ins(%ve : {R}) outs(%e7 : {R}) -> {R}
+    %e8 = tensor.empty() : {X}
+    %br = linalg.broadcast ins(%rs : {R}) outs(%e8 : {X}) dimensions = [1]
+    %e9 = tensor.empty() : {X}
+    %nx = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%d, %br : {X}, {X}) outs(%e9 : {X}) -> {X}
+    %e10 = tensor.empty() : {X}
+    %bw = linalg.broadcast ins(%w : {W}) outs(%e10 : {X}) dimensions = [0]
+    %e11 = tensor.empty() : {X}
+    %wx = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%nx, %bw : {X}, {X}) outs(%e11 : {X}) -> {X}
+    %e12 = tensor.empty() : {X}
+    %bb = linalg.broadcast ins(%bias : {W}) outs(%e12 : {X}) dimensions = [0]
+    %o = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%wx, %bb : {X}, {X}) outs(%y : {X}) -> {X}
+    return %o, %m : {X}, {R}
+  }}
+}}
+"""
+
+
+def reduce_ops(rows=48, cols=3000):
+    """Row reductions with each f32 combiner and an i32 sum (exact)."""
+    X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
+    return f"""module {{
+  func.func @reduce_ops(%x: {X}, %xi: {XI}, %mx: {R}, %mn: {R}, %mxn: {R}, %si: {RI}) -> ({R}, {R}, {R}, {RI})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %pinf = arith.constant 0x7F800000 : f32
+    %c0 = arith.constant 0 : i32
+    %f0 = linalg.fill ins(%ninf : f32) outs(%mx : {R}) -> {R}
+    %a = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f0 : {R}) dimensions = [1]
+    %f1 = linalg.fill ins(%pinf : f32) outs(%mn : {R}) -> {R}
+    %b = linalg.reduce {{arith.minimumf}} ins(%x : {X}) outs(%f1 : {R}) dimensions = [1]
+    %f2 = linalg.fill ins(%ninf : f32) outs(%mxn : {R}) -> {R}
+    %c = linalg.reduce {{arith.maxnumf}} ins(%x : {X}) outs(%f2 : {R}) dimensions = [1]
+    %f3 = linalg.fill ins(%c0 : i32) outs(%si : {RI}) -> {RI}
+    %d = linalg.reduce {{arith.addi}} ins(%xi : {XI}) outs(%f3 : {RI}) dimensions = [1]
+    return %a, %b, %c, %d : {R}, {R}, {R}, {RI}
+  }}
+}}
+"""
+
+
+def entries():
+    """name -> IR text of every prebuilt group."""
+    e = {}
+    for name, c in g.CONFIGS.items():
+        e[name] = c["fn"](**c["kw"])
+    e["bf16_mmad"] = g.bf16_mmad(4096, 4096, 4096)
+    # reduced / ragged parity sizes
+    e["vec_add_1m"] = g.vec_add(1 << 20)
+    e["vec_add_ragged"] = g.vec_add(1001)
+    e["vec_add_i16"] = g.vec_add(16, dtype="i16")
+    e["rmsnorm_quant_256"] = g.rmsnorm_quant(256, 4096)
+    e["rmsnorm_quant_ragged"] = g.rmsnorm_quant(13, 1000)
+    e["safe_softmax_64"] = g.safe_softmax(64, 32768)
+    e["safe_softmax_ragged"] = g.safe_softmax(33, 1000)
+    e["argmax_16"] = g.argmax(16, 152064)
+    e["argmax_ragged"] = g.argmax(5, 1001)
+    e["argmax_i64"] = g.argmax(8, 4096, index_type="i64")
+    e["w8a8_512"] = g.w8a8_dequant(512, 512, 512)
+    e["w8a8_ragged"] = g.w8a8_dequant(300, 200, 160)
+    e["bf16_mmad_256"] = g.bf16_mmad(256, 256, 256)
+    e["cast_modes"] = cast_modes(4096)
+    e["eltwise_mix"] = eltwise_mix(64, 1000)
+    e["layernorm"] = layernorm(64, 2048)
+    e["reduce_ops"] = reduce_ops(48, 3000)
+    return e
+
+
+def get(name):
+    return entries()[name]

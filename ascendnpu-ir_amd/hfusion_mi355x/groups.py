@@ -1,0 +1,205 @@
+"""HFusion group IR for the workloads this backend is measured on.
+
+Each function returns the textual MLIR of one outlined, already-fused HFusion
+group (``func.func`` tagged ``hacc.entry`` and ``hfusion.fusion_kind``), in the
+form the reference's fusion stage hands to its device compiler
+(``bishengir/test/bishengir-compile/hfusion/compile-rms-norm-fp32-split-n.mlir:5-47``
+for a LAST_AXIS_PBR group).  The IR is the contract: the CPU oracle and the
+GPU kernel both execute exactly these ops.
+"""
+
+_ATTRS = ("attributes {{hacc.entry, hacc.function_kind = #hacc.function_kind<DEVICE>, "
+          "hfusion.fusion_kind = #hfusion.fusion_kind<{kind}>}}")
+
+
+def _t(shape, dt):
+    return "tensor<" + "".join(f"{d}x" for d in shape) + dt + ">"
+
+
+def vec_add(n=1 << 24, dtype="f32"):
+    """HIVM VecAdd (bishengir/test/Integration/HIVM/VecAdd/add.mlir) as the
+    HFusion elementwise group `out = a + b`."""
+    t = _t([n], dtype)
+    return f"""module {{
+  func.func @vec_add(%a: {t}, %b: {t}, %out: {t}) -> {t}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %0 = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%a, %b : {t}, {t}) outs(%out : {t}) -> {t}
+    return %0 : {t}
+  }}
+}}
+"""
+
+
+def rmsnorm_quant(rows=8192, cols=4096, eps=1e-6):
+    """RMSNorm (structure of compile-rms-norm-fp32-split-n.mlir:5-47) followed by
+    dynamic per-token int8 quantisation with explicit rounding
+    (nearbyint -> clamp +-127 -> cast), so the CPU lowering's truncating
+    fptosi and the declared RINT cast agree."""
+    X, G = _t([rows, cols], "bf16"), _t([cols], "bf16")
+    XF, GF, RF = _t([rows, cols], "f32"), _t([cols], "f32"), _t([rows], "f32")
+    Q = _t([rows, cols], "i8")
+    e = f"{eps:.9e}"
+    return f"""module {{
+  func.func @rmsnorm_quant(%x: {X}, %gamma: {G}, %q: {Q}, %scale: {RF}) -> ({Q}, {RF})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %zero = arith.constant 0.000000e+00 : f32
+    %cols = arith.constant {float(cols):.6e} : f32
+    %eps = arith.constant {e} : f32
+    %qmax = arith.constant 1.270000e+02 : f32
+    %qmin = arith.constant -1.270000e+02 : f32
+    %e0 = tensor.empty() : {XF}
+    %xf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {X}) outs(%e0 : {XF}) -> {XF}
+    %e1 = tensor.empty() : {XF}
+    %sq = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%xf, %xf : {XF}, {XF}) outs(%e1 : {XF}) -> {XF}
+    %e2 = tensor.empty() : {RF}
+    %i2 = linalg.fill ins(%zero : f32) outs(%e2 : {RF}) -> {RF}
+    %ss = linalg.reduce {{arith.addf}} ins(%sq : {XF}) outs(%i2 : {RF}) dimensions = [1]
+    %e3 = tensor.empty() : {RF}
+    %mean = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%ss, %cols : {RF}, f32) outs(%e3 : {RF}) -> {RF}
+    %e4 = tensor.empty() : {RF}
+    %ms = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%mean, %eps : {RF}, f32) outs(%e4 : {RF}) -> {RF}
+    %e5 = tensor.empty() : {RF}
+    %rt = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%ms : {RF}) outs(%e5 : {RF}) -> {RF}
+    %e6 = tensor.empty() : {RF}
+    %inv = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<rec>}} ins(%rt : {RF}) outs(%e6 : {RF}) -> {RF}
+    %e7 = tensor.empty() : {XF}
+    %binv = linalg.broadcast ins(%inv : {RF}) outs(%e7 : {XF}) dimensions = [1]
+    %e8 = tensor.empty() : {XF}
+    %y1 = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%xf, %binv : {XF}, {XF}) outs(%e8 : {XF}) -> {XF}
+    %e9 = tensor.empty() : {GF}
+    %gf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%gamma : {G}) outs(%e9 : {GF}) -> {GF}
+    %e10 = tensor.empty() : {XF}
+    %bg = linalg.broadcast ins(%gf : {GF}) outs(%e10 : {XF}) dimensions = [0]
+    %e11 = tensor.empty() : {XF}
+    %y = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%y1, %bg : {XF}, {XF}) outs(%e11 : {XF}) -> {XF}
+    %e12 = tensor.empty() : {XF}
+    %ay = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%y : {XF}) outs(%e12 : {XF}) -> {XF}
+    %e13 = tensor.empty() : {RF}
+    %i13 = linalg.fill ins(%zero : f32) outs(%e13 : {RF}) -> {RF}
+    %amax = linalg.reduce {{arith.maximumf}} ins(%ay : {XF}) outs(%i13 : {RF}) dimensions = [1]
+    %sc = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%amax, %qmax : {RF}, f32) outs(%scale : {RF}) -> {RF}
+    %e14 = tensor.empty() : {XF}
+    %bsc = linalg.broadcast ins(%sc : {RF}) outs(%e14 : {XF}) dimensions = [1]
+    %e15 = tensor.empty() : {XF}
+    %ys = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%y, %bsc : {XF}, {XF}) outs(%e15 : {XF}) -> {XF}
+    %e16 = tensor.empty() : {XF}
+    %r = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<nearbyint>}} ins(%ys : {XF}) outs(%e16 : {XF}) -> {XF}
+    %e17 = tensor.empty() : {XF}
+    %c1 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<minf>}} ins(%r, %qmax : {XF}, f32) outs(%e17 : {XF}) -> {XF}
+    %e18 = tensor.empty() : {XF}
+    %c2 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<maxf>}} ins(%c1, %qmin : {XF}, f32) outs(%e18 : {XF}) -> {XF}
+    %qv = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%c2 : {XF}) outs(%q : {Q}) -> {Q}
+    return %qv, %sc : {Q}, {RF}
+  }}
+}}
+"""
+
+
+def safe_softmax(rows=4096, cols=32768):
+    """Safe softmax (structure of bishengir/test/Dialect/HFusion/regbase/
+    Normalize/hfusion-normalize-reduction-ops.mlir:262-277 with a maximumf
+    reduce) and a final f32 -> bf16 cast (round to nearest even)."""
+    X, R, O = _t([rows, cols], "f32"), _t([rows], "f32"), _t([rows, cols], "bf16")
+    return f"""module {{
+  func.func @safe_softmax(%x: {X}, %out: {O}) -> {O}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %zero = arith.constant 0.000000e+00 : f32
+    %ninf = arith.constant 0xFF800000 : f32
+    %e0 = tensor.empty() : {R}
+    %i0 = linalg.fill ins(%ninf : f32) outs(%e0 : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%i0 : {R}) dimensions = [1]
+    %e1 = tensor.empty() : {X}
+    %bm = linalg.broadcast ins(%m : {R}) outs(%e1 : {X}) dimensions = [1]
+    %e2 = tensor.empty() : {X}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%x, %bm : {X}, {X}) outs(%e2 : {X}) -> {X}
+    %e3 = tensor.empty() : {X}
+    %ex = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%d : {X}) outs(%e3 : {X}) -> {X}
+    %e4 = tensor.empty() : {R}
+    %i4 = linalg.fill ins(%zero : f32) outs(%e4 : {R}) -> {R}
+    %s = linalg.reduce {{arith.addf}} ins(%ex : {X}) outs(%i4 : {R}) dimensions = [1]
+    %e5 = tensor.empty() : {X}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e5 : {X}) dimensions = [1]
+    %e6 = tensor.empty() : {X}
+    %p = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%ex, %bs : {X}, {X}) outs(%e6 : {X}) -> {X}
+    %o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%p : {X}) outs(%out : {O}) -> {O}
+    return %o : {O}
+  }}
+}}
+"""
+
+
+def argmax(rows=256, cols=152064, index_type="i32"):
+    """reduce_with_index <max> over the last axis, init (-inf, 0) as in
+    bishengir/test/Dialect/HFusion/canonicalize.mlir:231-237."""
+    X, V, I = _t([rows, cols], "f32"), _t([rows], "f32"), _t([rows], index_type)
+    return f"""module {{
+  func.func @argmax(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %c0 = arith.constant 0 : {index_type}
+    %ninf = arith.constant 0xFF800000 : f32
+    %v0 = linalg.fill ins(%ninf : f32) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : {index_type}) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index {{tie_break_left = true}} <max> ins(%x : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}
+}}
+"""
+
+
+def w8a8_dequant(m=4096, n=4096, k=4096):
+    """W8A8 contraction (hivm.hir.matmul, B in the [N, K] weight layout) with
+    the per-token x per-channel dequant epilogue in IR order:
+    bf16((sitofp(C) * s_tok[m]) * s_ch[n])."""
+    A, B = _t([m, k], "i8"), _t([n, k], "i8")
+    C, CF, O = _t([m, n], "i32"), _t([m, n], "f32"), _t([m, n], "bf16")
+    ST, SC = _t([m], "f32"), _t([n], "f32")
+    return f"""module {{
+  func.func @w8a8_dequant(%a: {A}, %b: {B}, %s_tok: {ST}, %s_ch: {SC}, %out: {O}) -> {O}
+      {_ATTRS.format(kind='SINGLE_CUBE')} {{
+    %c0 = arith.constant 0 : i32
+    %e0 = tensor.empty() : {C}
+    %acc0 = linalg.fill ins(%c0 : i32) outs(%e0 : {C}) -> {C}
+    %acc = linalg.matmul_transpose_b ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
+    %e1 = tensor.empty() : {CF}
+    %cf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%acc : {C}) outs(%e1 : {CF}) -> {CF}
+    %e2 = tensor.empty() : {CF}
+    %bt = linalg.broadcast ins(%s_tok : {ST}) outs(%e2 : {CF}) dimensions = [1]
+    %e3 = tensor.empty() : {CF}
+    %t = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%cf, %bt : {CF}, {CF}) outs(%e3 : {CF}) -> {CF}
+    %e4 = tensor.empty() : {CF}
+    %bc = linalg.broadcast ins(%s_ch : {SC}) outs(%e4 : {CF}) dimensions = [0]
+    %e5 = tensor.empty() : {CF}
+    %u = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%t, %bc : {CF}, {CF}) outs(%e5 : {CF}) -> {CF}
+    %o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%u : {CF}) outs(%out : {O}) -> {O}
+    return %o : {O}
+  }}
+}}
+"""
+
+
+def bf16_mmad(m=4096, n=4096, k=4096):
+    """bf16 contraction (hivm.hir.mmadL1 bf16 -> f32) with a bf16 output cast."""
+    A, B = _t([m, k], "bf16"), _t([n, k], "bf16")
+    C, O = _t([m, n], "f32"), _t([m, n], "bf16")
+    return f"""module {{
+  func.func @bf16_mmad(%a: {A}, %b: {B}, %out: {O}) -> {O}
+      {_ATTRS.format(kind='SINGLE_CUBE')} {{
+    %c0 = arith.constant 0.000000e+00 : f32
+    %e0 = tensor.empty() : {C}
+    %acc0 = linalg.fill ins(%c0 : f32) outs(%e0 : {C}) -> {C}
+    %acc = linalg.matmul_transpose_b ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
+    %o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%acc : {C}) outs(%out : {O}) -> {O}
+    return %o : {O}
+  }}
+}}
+"""
+
+
+# The headline configurations (BASELINE configs[0..4]).
+CONFIGS = {
+    "vec_add": dict(fn=vec_add, kw=dict(n=1 << 24)),
+    "rmsnorm_quant": dict(fn=rmsnorm_quant, kw=dict(rows=8192, cols=4096, eps=1e-6)),
+    "safe_softmax": dict(fn=safe_softmax, kw=dict(rows=4096, cols=32768)),
+    "argmax": dict(fn=argmax, kw=dict(rows=256, cols=152064)),
+    "w8a8_dequant": dict(fn=w8a8_dequant, kw=dict(m=4096, n=4096, k=4096)),
+}

@@ -1,0 +1,202 @@
+"""Host-side mirror of the reference's compile-then-launch flow for HFusion groups.
+
+Reference flow: ``bishengir-compile in.mlir -o kernel.o`` (device compile,
+``bishengir/tools/bishengir-compile/bishengir-compile.cpp:103-191``), then the
+host registers the binary and launches it with bare device pointers in the
+kernel's argument order (``bishengir/test/Integration/HIVM/VecAdd/main.cpp``).
+Here: ``compile(ir)`` runs the same lowering through libhfc (hipcc for gfx950)
+and ``Group.__call__`` launches through libhfr on the current HIP stream.
+PyTorch only supplies device memory and the stream.
+"""
+import ctypes
+import hashlib
+import os
+import struct
+
+from . import native
+
+_DTYPES = None
+
+
+def torch_dtype(elem):
+    global _DTYPES
+    import torch
+    if _DTYPES is None:
+        _DTYPES = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16, "f64": torch.float64,
+                   "i1": torch.bool, "i8": torch.int8, "i16": torch.int16, "i32": torch.int32,
+                   "i64": torch.int64, "index": torch.int64}
+    return _DTYPES[elem]
+
+
+CACHE_DIR = os.path.join(native.PKG_ROOT, "build", "kcache")
+
+
+class CompileError(RuntimeError):
+    pass
+
+
+def _key(ir_text, options):
+    h = hashlib.sha1()
+    h.update(ir_text.encode())
+    h.update(b"\0" + options.encode())
+    # the kernel library and compiler sources are part of the key
+    for d in (native.KERNEL_INCLUDE, os.path.join(native.PKG_ROOT, "csrc", "compiler")):
+        for fn in sorted(os.listdir(d)):
+            with open(os.path.join(d, fn), "rb") as f:
+                h.update(fn.encode() + f.read())
+    return h.hexdigest()[:20]
+
+
+class Artifact:
+    """Compiled group(s) of one IR module: P.hip / P.hsaco / P.manifest."""
+
+    def __init__(self, prefix):
+        self.prefix = prefix
+        self.manifest = prefix + ".manifest"
+        self.hsaco = prefix + ".hsaco"
+        self.source = prefix + ".hip"
+        self.blocks = parse_manifest(self.manifest)
+
+    def funcs(self):
+        return [b["func"] for b in self.blocks]
+
+    def load(self, func=None):
+        return Group(self, func)
+
+
+def compile(ir_text, options="", cache=True, require_cached=False):
+    """Compiles IR text (one or more `hacc.entry` groups) to a gfx950 code object."""
+    prefix = os.path.join(CACHE_DIR, _key(ir_text, options), "group")
+    if cache and os.path.exists(prefix + ".hsaco") and os.path.exists(prefix + ".manifest"):
+        return Artifact(prefix)
+    if require_cached:
+        raise CompileError(f"group not prebuilt (expected {prefix}.hsaco); run __graft_entry__.build()")
+    os.makedirs(os.path.dirname(prefix), exist_ok=True)
+    err = ctypes.create_string_buffer(16384)
+    opts = f"include={native.KERNEL_INCLUDE};" + options
+    rc = native.hfc().hfc_compile(ir_text.encode(), prefix.encode(), opts.encode(), err, len(err))
+    if rc != 0:
+        raise CompileError(err.value.decode(errors="replace"))
+    return Artifact(prefix)
+
+
+def parse_manifest(path):
+    blocks = []
+    with open(path) as f:
+        for ln in f:
+            ln = ln.rstrip("\n")
+            if not ln:
+                continue
+            if ln.startswith("hfr-manifest"):
+                blocks.append({"params": [], "results": [], "kargs": []})
+                continue
+            key, _, rest = ln.partition(" ")
+            b = blocks[-1]
+            parts = rest.split()
+            if key in ("func", "kernel", "hsaco", "kind"):
+                b[key] = rest
+            elif key == "variant":
+                b[key] = rest
+            elif key in ("grid", "block"):
+                b[key] = tuple(int(x) for x in parts)
+            elif key in ("lds", "algo_bytes", "algo_ops"):
+                b[key] = int(parts[0])
+            elif key == "workspace":
+                b["workspace"] = int(parts[0])
+                b["workspace_zero"] = bool(int(parts[1]))
+            elif key == "param":
+                n = int(parts[3])
+                b["params"].append(dict(role=parts[1], elem=parts[2], shape=tuple(int(x) for x in parts[4:4 + n])))
+            elif key == "result":
+                n = int(parts[3])
+                b["results"].append(dict(tied=int(parts[1]), elem=parts[2], shape=tuple(int(x) for x in parts[4:4 + n])))
+            elif key == "karg":
+                b["kargs"].append(parts[0])
+    return blocks
+
+
+def _scalar_bits(v, elem):
+    if elem == "f32":
+        return struct.unpack("<I", struct.pack("<f", float(v)))[0]
+    if elem == "f64":
+        return struct.unpack("<Q", struct.pack("<d", float(v)))[0]
+    return int(v) & 0xFFFFFFFFFFFFFFFF
+
+
+class Group:
+    """One loaded HFusion group kernel (hfr_group_t)."""
+
+    def __init__(self, artifact, func=None):
+        blocks = artifact.blocks
+        if func is None:
+            if len(blocks) != 1:
+                raise ValueError("artifact holds several groups; name one of " + ", ".join(artifact.funcs()))
+            self.meta = blocks[0]
+        else:
+            match = [b for b in blocks if b["func"] == func]
+            if not match:
+                raise ValueError(f"no group @{func} in {artifact.manifest}")
+            self.meta = match[0]
+        self.func = self.meta["func"]
+        self._h = ctypes.c_void_p()
+        native.check(native.hfr().hfr_group_load(artifact.manifest.encode(), self.func.encode(), ctypes.byref(self._h)))
+        info = native.GroupInfo()
+        native.check(native.hfr().hfr_group_info_get(self._h, ctypes.byref(info)))
+        self.info = info
+
+    @property
+    def algo_bytes(self):
+        return self.meta.get("algo_bytes", 0)
+
+    @property
+    def algo_ops(self):
+        return self.meta.get("algo_ops", 0)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and h.value and native._hfr is not None:
+            native.hfr().hfr_group_unload(h)
+            self._h = None
+
+    def __call__(self, *args, results=None, stream=None, workspace=None):
+        import torch
+        params = self.meta["params"]
+        if len(args) != len(params):
+            raise TypeError(f"@{self.func} takes {len(params)} arguments ({len(args)} given)")
+        device = None
+        slots = (ctypes.c_uint64 * len(params))()
+        for i, (a, p) in enumerate(zip(args, params)):
+            if p["role"] == "scalar":
+                slots[i] = _scalar_bits(a, p["elem"])
+                continue
+            if not isinstance(a, torch.Tensor) or not a.is_cuda:
+                raise TypeError(f"argument {i} of @{self.func} must be a device tensor")
+            if a.dtype != torch_dtype(p["elem"]) or tuple(a.shape) != p["shape"] or not a.is_contiguous():
+                raise ValueError(f"argument {i} of @{self.func}: expected contiguous {p['elem']}{list(p['shape'])}, "
+                                 f"got {a.dtype}{list(a.shape)}")
+            device = a.device if device is None else device
+            slots[i] = a.data_ptr()
+        res_meta = self.meta["results"]
+        outs = []
+        rptrs = (ctypes.c_void_p * max(1, len(res_meta)))()
+        for j, r in enumerate(res_meta):
+            if r["tied"] >= 0:
+                outs.append(args[r["tied"]])
+                rptrs[j] = None
+            else:
+                t = results[j] if results is not None else torch.empty(r["shape"], dtype=torch_dtype(r["elem"]),
+                                                                      device=device)
+                if tuple(t.shape) != r["shape"] or t.dtype != torch_dtype(r["elem"]) or not t.is_cuda:
+                    raise ValueError(f"result {j} of @{self.func}: expected {r['elem']}{list(r['shape'])}")
+                outs.append(t)
+                rptrs[j] = t.data_ptr()
+        if stream is None:
+            stream = torch.cuda.current_stream(device).cuda_stream
+        ws = workspace.data_ptr() if workspace is not None else None
+        native.check(native.hfr().hfr_group_launch(self._h, slots, len(params), rptrs, len(res_meta), ws, stream))
+        return outs[0] if len(outs) == 1 else tuple(outs)
+
+
+def load(ir_text, func=None, options="", require_cached=False):
+    """compile() + load(): the one-call host entry."""
+    return compile(ir_text, options=options, require_cached=require_cached).load(func)

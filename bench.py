@@ -1,0 +1,232 @@
+"""Benchmark of the MI355X HFusion backend on BASELINE.json's workloads.
+
+A step is one launch of a fused HFusion group over one batch of synthetic,
+seeded input already resident in HBM.  The headline `value` is the group of
+BASELINE configs[1] (fused RMSNorm + dynamic per-token int8 quant,
+x bf16 [8192, 4096]) in algorithmic HBM GB/s; every other configured group is
+measured the same way and reported under "groups" (GB/s, or TOPS for the W8A8
+contraction) with its roofline fraction.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "ascendnpu-ir_amd"))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X
+BF16_PEAK_TFLOPS = 2500.0
+HEADLINE = "rmsnorm_quant"
+ORDER = ["rmsnorm_quant", "vec_add", "safe_softmax", "argmax", "w8a8_dequant"]
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def device_inputs(name, dev):
+    """Inputs and destination buffers for config `name`, on the device."""
+    import numpy as np
+    import torch
+
+    import hfusion_mi355x as hf
+    cfg = hf.groups.CONFIGS[name]["kw"]
+    ins = hf.inputs.config_inputs(name, **cfg)
+
+    def dev_t(a, bf16=False):
+        t = torch.from_numpy(np.ascontiguousarray(a))
+        if bf16:
+            t = t.view(torch.bfloat16)
+        return t.to(dev)
+
+    if name == "vec_add":
+        a, b = ins
+        return [dev_t(a), dev_t(b), torch.empty_like(dev_t(a))], ins
+    if name == "rmsnorm_quant":
+        x, g = ins
+        r, c = x.shape
+        return [dev_t(x, True), dev_t(g, True), torch.empty((r, c), dtype=torch.int8, device=dev),
+                torch.empty((r,), dtype=torch.float32, device=dev)], ins
+    if name == "safe_softmax":
+        x, = ins
+        return [dev_t(x), torch.empty(x.shape, dtype=torch.bfloat16, device=dev)], ins
+    if name == "argmax":
+        x, = ins
+        r = x.shape[0]
+        return [dev_t(x), torch.empty((r,), dtype=torch.float32, device=dev),
+                torch.empty((r,), dtype=torch.int32, device=dev)], ins
+    if name == "w8a8_dequant":
+        a, b, st, sc = ins
+        return [dev_t(a), dev_t(b), dev_t(st), dev_t(sc),
+                torch.empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16, device=dev)], ins
+    raise KeyError(name)
+
+
+def time_group(grp, args, steps, warmup):
+    """Per-launch time (ms) from HIP events on the stream the kernels run on."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        grp(*args)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    per = []
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        grp(*args)
+        e.record(stream)
+        per.append((s, e))
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
+    launches = [s.elapsed_time(e) for s, e in per]
+    return total_ms, launches, wall
+
+
+def cpu_baseline(name, ins, budget_s=12.0):
+    """The oracle's op-by-op C restatement of the reference CPU lowering, on
+    one host core, over a bounded sample of the same workload."""
+    import ctypes
+
+    import numpy as np
+    sys.path.insert(0, REPO)
+    from oracle.interp import lib, ptr
+    L = lib()
+    if name == "rmsnorm_quant":
+        x, g = ins
+        rows = 1024
+        xs = np.ascontiguousarray(x[:rows])
+        q = np.empty((rows, x.shape[1]), np.int8)
+        s = np.empty(rows, np.float32)
+        fn = lambda: L.hfref_rmsnorm_quant(ptr(xs), ptr(g), ctypes.c_float(1e-6), ptr(q), ptr(s), rows, x.shape[1])
+        nbytes = xs.nbytes + g.nbytes + q.nbytes + s.nbytes
+        sample = f"{rows} of 8192 rows x 4096"
+    elif name == "vec_add":
+        a, b = ins
+        o = np.empty_like(a)
+        fn = lambda: L.hfref_vecadd_f32(ptr(a), ptr(b), ptr(o), a.size)
+        nbytes = 3 * a.nbytes
+        sample = "full 2^24 elements"
+    elif name == "safe_softmax":
+        x, = ins
+        rows = 128
+        xs = np.ascontiguousarray(x[:rows])
+        o = np.empty(xs.shape, np.uint16)
+        fn = lambda: L.hfref_softmax_bf16(ptr(xs), ptr(o), rows, x.shape[1])
+        nbytes = xs.nbytes + o.nbytes
+        sample = f"{rows} of 4096 rows x 32768"
+    elif name == "argmax":
+        x, = ins
+        rows = 64
+        xs = np.ascontiguousarray(x[:rows])
+        v = np.empty(rows, np.float32)
+        i = np.empty(rows, np.int32)
+        fn = lambda: L.hfref_argmax(ptr(xs), ptr(v), ptr(i), rows, x.shape[1])
+        nbytes = xs.nbytes + v.nbytes + i.nbytes
+        sample = f"{rows} of 256 rows x 152064"
+    elif name == "w8a8_dequant":
+        a, b, st, sc = ins
+        rows = 2
+        o = np.empty((rows, b.shape[0]), np.uint16)
+        fn = lambda: L.hfref_w8a8_dequant_rows(ptr(a), ptr(b), ptr(st), ptr(sc), ptr(o), a.shape[0], b.shape[0],
+                                               a.shape[1], 0, rows)
+        ops = 2.0 * rows * b.shape[0] * a.shape[1]
+        sample = f"{rows} of 4096 rows (N=K=4096)"
+    else:
+        raise KeyError(name)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    if name == "w8a8_dequant":
+        return {"value": ops / med / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
+                "sample": sample + f", median of {len(times)} runs"}
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": sample + f", median of {len(times)} runs"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default=None, help="measure one group (e.g. for rocprofv3)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (each group shards by rows/columns "
+              "with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import hfusion_mi355x as hf
+    dev = torch.device("cuda:0")
+    names = [args.only] if args.only else ORDER
+    groups = {}
+    headline_cpu = None
+    for name in names:
+        log(f"[bench] {name}: preparing inputs")
+        art = hf.compile(hf.catalog.get(name), require_cached=True)
+        grp = art.load()
+        dargs, host_ins = device_inputs(name, dev)
+        log(f"[bench] {name}: timing {args.steps} steps")
+        total_ms, launches, wall = time_group(grp, dargs, args.steps, args.warmup)
+        ms = total_ms / args.steps
+        kern_ms = statistics.mean(launches)
+        meta = grp.meta
+        if meta["kind"] == "SINGLE_CUBE":
+            ops = meta["algo_ops"]
+            achieved = ops / (kern_ms * 1e-3) / 1e12
+            entry = {"value": ops * args.steps / (total_ms * 1e-3) / 1e12, "unit": "TOPS", "ms_per_step": ms,
+                     "roofline": {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                                  "frac": achieved / INT8_PEAK_TOPS, "traffic": None}}
+        else:
+            nb = meta["algo_bytes"]
+            achieved = nb / (kern_ms * 1e-3) / 1e9
+            entry = {"value": nb * args.steps / (total_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms,
+                     "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": achieved / HBM_PEAK_GBS, "traffic": None}}
+        entry["kernel"] = meta["kernel"]
+        entry["algo_bytes"] = meta["algo_bytes"]
+        entry["wall_s"] = wall
+        groups[name] = entry
+        log(f"[bench] {name}: {entry['value']:.1f} {entry['unit']} ({entry['roofline']['frac'] * 100:.1f}% of peak), "
+            f"{ms * 1e3:.1f} us/step")
+        if not args.no_cpu and (name == HEADLINE or args.only):
+            log(f"[bench] {name}: CPU baseline (oracle restatement, 1 core)")
+            headline_cpu = cpu_baseline(name, host_ins)
+        del dargs
+        torch.cuda.empty_cache()
+    head = HEADLINE if HEADLINE in groups else names[0]
+    h = groups[head]
+    cfg = hf.groups.CONFIGS[head]["kw"]
+    line = {
+        "metric": "HBM GB/s (% of peak) per fused HFusion group; W8A8 mmad TOPS (% MFMA)",
+        "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": {"rmsnorm_quant": "bf16->f32->i8", "vec_add": "f32", "safe_softmax": "f32->bf16",
+                  "argmax": "f32/i32", "w8a8_dequant": "i8->i32->bf16"}[head],
+        "data": "synthetic (seeded splitmix64)",
+        "config": {"workload": head, **{k: v for k, v in cfg.items()}},
+        "roofline": h["roofline"],
+        "cpu_baseline": headline_cpu,
+        "groups": groups,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

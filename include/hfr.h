@@ -1,0 +1,86 @@
+/*
+ * hfr — C-ABI runtime that loads and launches HFusion group kernels on one
+ * MI355X (one GPU, caller-provided stream).
+ *
+ * Replaces the host launch sequence the reference's integration test drives
+ * through CANN (bishengir/test/Integration/HIVM/VecAdd/main.cpp:
+ * rtDevBinaryRegister + rtFunctionRegister -> rtKernelLaunch(stub, blockDim,
+ * args = {in0, in1, out}, stream) -> aclrtSynchronizeStream).  Kernel
+ * arguments are bare device pointers in the group function's argument order
+ * (destination-passing style, HFusionStructuredOps.td:38-44), followed by
+ * buffers for results that are not written into an argument.
+ *
+ * Ownership: the caller allocates and frees every tensor buffer.  The runtime
+ * owns module/group handles and, when the caller passes no workspace, one
+ * lazily allocated zero-initialised workspace per group handle.
+ * Threading: launches are asynchronous on the given stream; the caller
+ * synchronises.  A handle must not be used from two threads at once, and two
+ * in-flight launches of one group handle that both use its internal workspace
+ * must be on the same stream.
+ * Errors: every call returns 0 or a negative HFR_ERR_* code; hfr_last_error()
+ * gives the message for the calling thread.
+ */
+#ifndef HFR_H
+#define HFR_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HFR_OK 0
+#define HFR_ERR_INVALID -1  /* bad argument (null handle/pointer, count mismatch) */
+#define HFR_ERR_HIP -2      /* HIP runtime call failed */
+#define HFR_ERR_IO -3       /* file missing or unreadable */
+#define HFR_ERR_MANIFEST -4 /* malformed manifest */
+#define HFR_ERR_NOT_FOUND -5/* kernel or function name not present */
+
+typedef struct hfr_module *hfr_module_t;
+typedef struct hfr_kernel *hfr_kernel_t;
+typedef struct hfr_group *hfr_group_t;
+
+typedef struct hfr_launch_cfg {
+  unsigned grid[3];
+  unsigned block[3];
+  unsigned lds_bytes;
+} hfr_launch_cfg;
+
+typedef struct hfr_group_info {
+  int nparams;
+  int nresults;
+  int nkargs;
+  uint64_t workspace_bytes;
+  uint64_t algo_bytes; /* algorithmic HBM bytes per launch */
+  uint64_t algo_ops;   /* algorithmic ops per launch (contractions) */
+  hfr_launch_cfg cfg;
+} hfr_group_info;
+
+/* ---- code objects and kernels (replaces rtDevBinaryRegister / rtFunctionRegister) */
+int hfr_module_load(const char *hsaco_path, hfr_module_t *out);
+int hfr_module_unload(hfr_module_t m);
+int hfr_kernel_get(hfr_module_t m, const char *name, hfr_kernel_t *out);
+/* args: one 8-byte slot per kernel parameter (device pointer or raw scalar
+ * bits); replaces rtKernelLaunch. */
+int hfr_launch(hfr_kernel_t k, const hfr_launch_cfg *cfg, const uint64_t *args, size_t nargs, void *stream);
+
+/* ---- manifest-driven groups (what bishengir-compile --target=mi355x emits) */
+/* func may be NULL when the manifest holds one group. */
+int hfr_group_load(const char *manifest_path, const char *func, hfr_group_t *out);
+int hfr_group_unload(hfr_group_t g);
+int hfr_group_info_get(hfr_group_t g, hfr_group_info *info);
+/* params: one slot per group argument (device pointer, or the raw bits of a
+ * scalar argument); results: one pointer per group result (ignored — may be
+ * NULL — for results written into an argument); workspace: NULL to use the
+ * group's own, or a caller buffer of workspace_bytes (zeroed before its first
+ * use when the group requires it). */
+int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
+                     void *workspace, void *stream);
+
+const char *hfr_last_error(void);
+const char *hfr_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

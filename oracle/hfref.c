@@ -1,0 +1,602 @@
+/*
+ * hfref.c — CPU restatement of the reference's CPU lowering for HFusion op
+ * groups.  TEST INFRASTRUCTURE ONLY (the parity checker and the timed CPU
+ * baseline); the product never links it.  See hfref.h for the contract.
+ *
+ * Build: -O2 -ffp-contract=off -fno-fast-math (no FMA contraction, IEEE
+ * division/sqrt, libm for transcendental math), as the MLIR CPU pipeline
+ * produces (bishengir/lib/ExecutionEngine/ExecutionEnginePipelines.cpp:54-89).
+ */
+#define _GNU_SOURCE
+#include "hfref.h"
+
+#include <fenv.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------------ */
+/* bf16 / f16 conversions                                                    */
+/* ------------------------------------------------------------------------ */
+
+float hfref_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* arith.truncf f32->bf16: round to nearest even; NaN stays a (quiet) NaN. */
+uint16_t hfref_f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float hfref_f16_to_f32(uint16_t h) {
+  uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  if (e == 0x1f) return u2f(s | 0x7f800000u | (m << 13));
+  if (e == 0) {
+    float v = ldexpf((float)m, -24);
+    return s ? -v : v;
+  }
+  return u2f(s | ((e + 112) << 23) | (m << 13));
+}
+
+/* Generic rounding of an exact value `x` onto a binary floating format with
+ * `p` significand bits and exponent range [emin, emax], under round mode
+ * `mode` (HFusionEnums.td:122-141 numbering).  Returns the rounded value as a
+ * long double (exactly representable), or +-inf on overflow.  Written from the
+ * IEEE-754 definition of the directed/nearest modes and of round-to-odd
+ * ("jamming": truncate, then set the last bit when inexact). */
+static long double round_to_format(long double x, int p, int emin, int emax,
+                                   int mode) {
+  if (isnan(x) || isinf(x) || x == 0) return x;
+  int neg = signbit(x) != 0;
+  long double a = neg ? -x : x;
+  int E;
+  frexpl(a, &E); /* a = m * 2^E, m in [0.5, 1): leading bit at 2^(E-1) */
+  int lead = E - 1;
+  if (lead < emin) lead = emin;
+  long double q = ldexpl(1.0L, lead - (p - 1)); /* quantum */
+  long double s = a / q;                        /* exact (power of 2) */
+  long double fl = floorl(s), fr = s - fl;
+  long double r;
+  switch (mode) {
+  case 0: /* rint: nearest, ties to even */
+    r = (fr > 0.5L || (fr == 0.5L && fmodl(fl, 2.0L) != 0)) ? fl + 1 : fl;
+    break;
+  case 1: /* round: nearest, ties away */
+    r = fr >= 0.5L ? fl + 1 : fl;
+    break;
+  case 2: /* floor */
+    r = (neg && fr > 0) ? fl + 1 : fl;
+    break;
+  case 3: /* ceil */
+    r = (!neg && fr > 0) ? fl + 1 : fl;
+    break;
+  case 5: /* odd */
+    r = (fr > 0 && fmodl(fl, 2.0L) == 0) ? fl + 1 : fl;
+    break;
+  default: /* trunc / truncwithoverflow */
+    r = fl;
+  }
+  long double v = r * q;
+  long double maxf = ldexpl(2.0L - ldexpl(1.0L, -(p - 1)), emax);
+  if (v > maxf) {
+    int to_inf;
+    switch (mode) {
+    case 0: case 1: to_inf = 1; break;
+    case 2: to_inf = neg; break;
+    case 3: to_inf = !neg; break;
+    default: to_inf = 0;
+    }
+    v = to_inf ? (long double)INFINITY : maxf;
+  }
+  return neg ? -v : v;
+}
+
+uint16_t hfref_f32_to_bf16_mode(float f, int mode) {
+  if (isnan(f)) return hfref_f32_to_bf16(f);
+  long double v = round_to_format((long double)f, 8, -126, 127, mode);
+  return (uint16_t)(f2u((float)v) >> 16); /* exact: v is on the bf16 grid */
+}
+
+uint16_t hfref_f32_to_f16_mode(float f, int mode) {
+  uint32_t u = f2u(f);
+  uint16_t sgn = (uint16_t)((u >> 16) & 0x8000u);
+  if (isnan(f)) return (uint16_t)(sgn | 0x7e00u | ((u >> 13) & 0x3ffu));
+  long double v = round_to_format((long double)f, 11, -14, 15, mode);
+  if (isinf(v)) return (uint16_t)(sgn | 0x7c00u);
+  if (v == 0) return sgn;
+  long double a = fabsl(v);
+  int E;
+  frexpl(a, &E);
+  int lead = E - 1;
+  uint16_t bits;
+  if (lead < -14) { /* subnormal: a = m * 2^-24 */
+    bits = (uint16_t)(a / ldexpl(1.0L, -24));
+  } else {
+    long double mant = a / ldexpl(1.0L, lead) - 1.0L; /* [0,1) */
+    bits = (uint16_t)(((lead + 15) << 10) | (uint16_t)(mant * 1024.0L));
+  }
+  return (uint16_t)(sgn | bits);
+}
+
+uint16_t hfref_f32_to_f16(float f) { return hfref_f32_to_f16_mode(f, 0); }
+
+static inline int64_t wrap_bits(int64_t v, int bits) {
+  if (bits >= 64) return v;
+  uint64_t m = (1ull << bits) - 1ull;
+  uint64_t u = (uint64_t)v & m;
+  if (u >> (bits - 1)) u |= ~m;
+  return (int64_t)u;
+}
+
+static long double round_int(long double x, int mode) {
+  long double fl = floorl(x), fr = x - fl;
+  int neg = x < 0;
+  switch (mode) {
+  case 0: return (fr > 0.5L || (fr == 0.5L && fmodl(fl, 2.0L) != 0)) ? fl + 1 : fl;
+  case 1: return neg ? -floorl(-x + 0.5L) : floorl(x + 0.5L);
+  case 2: return fl;
+  case 3: return fr > 0 ? fl + 1 : fl;
+  case 5: { /* von Neumann: truncate toward zero, jam the last bit */
+    long double t = truncl(x);
+    if (t != x && fmodl(t, 2.0L) == 0) t += neg ? -1 : 1;
+    return t;
+  }
+  default: return truncl(x);
+  }
+}
+
+int64_t hfref_f32_to_int_mode(float f, int mode, int bits, int saturate) {
+  long double lo = -ldexpl(1.0L, bits - 1), hi = ldexpl(1.0L, bits - 1) - 1;
+  if (isnan(f)) return 0;
+  long double r = isinf(f) ? (long double)f : round_int((long double)f, mode);
+  if (saturate) {
+    if (r < lo) r = lo;
+    if (r > hi) r = hi;
+    return (int64_t)r;
+  }
+  if (isinf(r) || fabsl(r) >= ldexpl(1.0L, 63)) return INT64_MIN; /* poison */
+  return wrap_bits((int64_t)r, bits);
+}
+
+float hfref_int_to_f32_mode(int64_t v, int mode) {
+  return (float)round_to_format((long double)v, 24, -126, 127, mode);
+}
+
+/* HFusionOps.cpp:1926-1938 ConstantFolding::roundToOdd, evaluated in double. */
+int64_t hfref_fold_round_to_odd(double x) {
+  double rounded = round(x);
+  const double epsilon = 1e-9;
+  if (fabs(fabs(x - floor(x)) - 0.5) < epsilon) {
+    if (((int)rounded) % 2 != 0) rounded = x > 0 ? floor(x) : ceil(x);
+  }
+  return (int64_t)rounded;
+}
+
+/* ------------------------------------------------------------------------ */
+/* scalar region bodies (RegionBuilderHelper, HFusionOps.cpp:434-640)        */
+/* ------------------------------------------------------------------------ */
+
+/* arith.maximumf / minimumf: NaN-propagating, -0 < +0 */
+static inline float maximumf(float a, float b) {
+  if (isnan(a) || isnan(b)) return NAN;
+  if (a == 0 && b == 0) return (signbit(a) && signbit(b)) ? -0.0f : 0.0f;
+  return a > b ? a : b;
+}
+static inline float minimumf(float a, float b) {
+  if (isnan(a) || isnan(b)) return NAN;
+  if (a == 0 && b == 0) return (signbit(a) || signbit(b)) ? -0.0f : 0.0f;
+  return a < b ? a : b;
+}
+/* arith.maxnumf / minnumf: a NaN operand yields the other operand */
+static inline float maxnumf(float a, float b) {
+  if (isnan(a)) return b;
+  if (isnan(b)) return a;
+  return maximumf(a, b);
+}
+static inline float minnumf(float a, float b) {
+  if (isnan(a)) return b;
+  if (isnan(b)) return a;
+  return minimumf(a, b);
+}
+
+static inline float unary_f32(int fn, float x) {
+  switch (fn) {
+  case HFU_SQRT: return sqrtf(x);
+  case HFU_RSQRT: { volatile float s = sqrtf(x); return 1.0f / s; }
+  case HFU_EXP: return expf(x);
+  case HFU_EXP2: return exp2f(x);
+  case HFU_LOG: return logf(x);
+  case HFU_LOG2: return log2f(x);
+  case HFU_LOG10: return log10f(x);
+  case HFU_LOG1P: return log1pf(x);
+  case HFU_EXPM1: return expm1f(x);
+  case HFU_ABS: return fabsf(x);
+  case HFU_NEG: return -x;
+  case HFU_RELU: return maximumf(0.0f, x);
+  case HFU_REC: return 1.0f / x;
+  case HFU_TANH: return tanhf(x);
+  case HFU_SIN: return sinf(x);
+  case HFU_COS: return cosf(x);
+  case HFU_ERF: return erff(x);
+  case HFU_NEARBYINT: return roundevenf(x);
+  case HFU_CEIL: return ceilf(x);
+  case HFU_FLOOR: return floorf(x);
+  case HFU_ROUND: return roundf(x);
+  case HFU_SQUARE: return x * x;
+  case HFU_TRUNC: return truncf(x);
+  }
+  abort();
+}
+
+static inline float binary_f32(int fn, float a, float b) {
+  switch (fn) {
+  case HFB_ADD: return a + b;
+  case HFB_SUB: return a - b;
+  case HFB_MUL: return a * b;
+  case HFB_DIV: return a / b;
+  case HFB_MAXF: return maximumf(a, b);
+  case HFB_MINF: return minimumf(a, b);
+  case HFB_MAXNUMF: return maxnumf(a, b);
+  case HFB_MINNUMF: return minnumf(a, b);
+  case HFB_POWF: return powf(a, b);
+  case HFB_MODF: return fmodf(a, b);
+  case HFB_COPYSIGN: return copysignf(a, b);
+  }
+  abort();
+}
+
+static inline uint64_t ubits(int64_t v, int bits) {
+  return bits >= 64 ? (uint64_t)v : ((uint64_t)v & ((1ull << bits) - 1ull));
+}
+
+static inline int64_t binary_i64(int fn, int64_t a, int64_t b, int bits) {
+  int64_t r;
+  switch (fn) {
+  case HFB_IADD: r = (int64_t)((uint64_t)a + (uint64_t)b); break;
+  case HFB_ISUB: r = (int64_t)((uint64_t)a - (uint64_t)b); break;
+  case HFB_IMUL: r = (int64_t)((uint64_t)a * (uint64_t)b); break;
+  case HFB_IDIV: r = b == 0 ? 0 : a / b; break;
+  case HFB_IREM: r = b == 0 ? 0 : a % b; break;
+  case HFB_IMAX: r = a > b ? a : b; break;
+  case HFB_IMIN: r = a < b ? a : b; break;
+  case HFB_IMAXU: r = ubits(a, bits) > ubits(b, bits) ? a : b; break;
+  case HFB_IMINU: r = ubits(a, bits) < ubits(b, bits) ? a : b; break;
+  case HFB_IAND: r = a & b; break;
+  case HFB_IOR: r = a | b; break;
+  case HFB_IXOR: r = a ^ b; break;
+  case HFB_ISHL: r = (b < 0 || b >= bits) ? 0 : (int64_t)((uint64_t)a << b); break;
+  case HFB_ISHRS: r = (b < 0 || b >= bits) ? 0 : (a >> b); break;
+  case HFB_ISHRU: r = (b < 0 || b >= bits) ? 0 : (int64_t)(ubits(a, bits) >> b); break;
+  case HFB_IFLOORDIV:
+    if (b == 0) { r = 0; break; }
+    r = a / b;
+    if ((a % b != 0) && ((a < 0) != (b < 0))) r -= 1;
+    break;
+  case HFB_ICEILDIV:
+    if (b == 0) { r = 0; break; }
+    r = a / b;
+    if ((a % b != 0) && ((a < 0) == (b < 0))) r += 1;
+    break;
+  default: abort();
+  }
+  return wrap_bits(r, bits);
+}
+
+/* ------------------------------------------------------------------------ */
+/* array primitives                                                          */
+/* ------------------------------------------------------------------------ */
+
+void hfref_unary_f32(int fn, const float *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = unary_f32(fn, in[i]);
+}
+void hfref_binary_f32(int fn, const float *a, const float *b, float *out,
+                      int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = binary_f32(fn, a[i], b[i]);
+}
+void hfref_fma_f32(const float *a, const float *b, const float *c, float *out,
+                   int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = fmaf(a[i], b[i], c[i]);
+}
+void hfref_binary_i64(int fn, const int64_t *a, const int64_t *b,
+                      int64_t *out, int64_t n, int bits) {
+  for (int64_t i = 0; i < n; ++i) out[i] = binary_i64(fn, a[i], b[i], bits);
+}
+void hfref_compare_f32(int fn, const float *a, const float *b, uint8_t *out,
+                       int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    float x = a[i], y = b[i];
+    int r;
+    switch (fn) {
+    case HFC_EQ: r = x == y; break;          /* OEQ */
+    case HFC_NE: r = !(x == y); break;       /* UNE */
+    case HFC_LT: r = x < y; break;           /* OLT */
+    case HFC_LE: r = x <= y; break;          /* OLE */
+    case HFC_GT: r = x > y; break;           /* OGT */
+    default: r = x >= y;                     /* OGE */
+    }
+    out[i] = (uint8_t)r;
+  }
+}
+void hfref_compare_i64(int fn, const int64_t *a, const int64_t *b,
+                       uint8_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t x = a[i], y = b[i];
+    int r;
+    switch (fn) {
+    case HFC_EQ: r = x == y; break;
+    case HFC_NE: r = x != y; break;
+    case HFC_LT: r = x < y; break;
+    case HFC_LE: r = x <= y; break;
+    case HFC_GT: r = x > y; break;
+    default: r = x >= y;
+    }
+    out[i] = (uint8_t)r;
+  }
+}
+
+void hfref_bf16_to_f32_n(const uint16_t *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = hfref_bf16_to_f32(in[i]);
+}
+void hfref_f32_to_bf16_n(const float *in, uint16_t *out, int64_t n, int mode) {
+  if (mode == 0)
+    for (int64_t i = 0; i < n; ++i) out[i] = hfref_f32_to_bf16(in[i]);
+  else
+    for (int64_t i = 0; i < n; ++i) out[i] = hfref_f32_to_bf16_mode(in[i], mode);
+}
+void hfref_f16_to_f32_n(const uint16_t *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = hfref_f16_to_f32(in[i]);
+}
+void hfref_f32_to_f16_n(const float *in, uint16_t *out, int64_t n, int mode) {
+  for (int64_t i = 0; i < n; ++i) out[i] = hfref_f32_to_f16_mode(in[i], mode);
+}
+/* arith.fptosi: rounds toward zero; a result outside the target range (or a
+ * NaN/inf input) is poison in LLVM — flagged here, value unspecified. */
+void hfref_fptosi_n(const float *in, int64_t *out, int64_t n, int bits,
+                    int *poison) {
+  long double lo = -ldexpl(1.0L, bits - 1), hi = ldexpl(1.0L, bits - 1) - 1;
+  int p = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float f = in[i];
+    if (isnan(f) || isinf(f)) { p = 1; out[i] = 0; continue; }
+    long double t = truncl((long double)f);
+    if (t < lo || t > hi) { p = 1; out[i] = 0; continue; }
+    out[i] = (int64_t)t;
+  }
+  if (poison) *poison = p;
+}
+void hfref_f32_to_int_mode_n(const float *in, int64_t *out, int64_t n,
+                             int mode, int bits, int saturate) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = hfref_f32_to_int_mode(in[i], mode, bits, saturate);
+}
+void hfref_int_to_f32_n(const int64_t *in, float *out, int64_t n, int mode) {
+  for (int64_t i = 0; i < n; ++i) out[i] = hfref_int_to_f32_mode(in[i], mode);
+}
+void hfref_roundeven_n(const float *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = roundevenf(in[i]);
+}
+void hfref_round_n(const float *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = roundf(in[i]);
+}
+
+/* linalg.reduce region `op(%in, %init)` folded serially along the reduced
+ * index (ConvertHIVMToUpstream.cpp:573-752; convert-linalg-to-loops). */
+void hfref_reduce_f32(int op, const float *x, float *acc, int64_t K,
+                      int64_t N) {
+  for (int64_t k = 0; k < K; ++k) {
+    const float *row = x + k * N;
+    for (int64_t j = 0; j < N; ++j) {
+      float in = row[j], a = acc[j];
+      switch (op) {
+      case 0: a = in + a; break;
+      case 1: a = in * a; break;
+      case 2: a = maximumf(in, a); break;
+      case 3: a = minimumf(in, a); break;
+      case 4: a = maxnumf(in, a); break;
+      default: a = minnumf(in, a);
+      }
+      acc[j] = a;
+    }
+  }
+}
+
+void hfref_reduce_i64(int op, const int64_t *x, int64_t *acc, int64_t K,
+                      int64_t N, int bits) {
+  static const int map[] = {HFB_IADD, HFB_IMUL, HFB_IMAX, HFB_IMIN, HFB_IAND,
+                            HFB_IOR,  HFB_IXOR, HFB_IMAXU, HFB_IMINU};
+  for (int64_t k = 0; k < K; ++k)
+    for (int64_t j = 0; j < N; ++j)
+      acc[j] = binary_i64(map[op], x[k * N + j], acc[j], bits);
+}
+
+/* hfusion.reduce_with_index region (HFusionOps.cpp:1507-1595):
+ *   res = maximumf(in, outV); pred = res OGT outV;
+ *   outI = pred ? index : outI; outV = res                                  */
+void hfref_reduce_with_index_f32(int kind, const float *x, const int64_t *in_idx,
+                                 float *val, int64_t *idx, int64_t K,
+                                 int64_t N) {
+  for (int64_t k = 0; k < K; ++k)
+    for (int64_t j = 0; j < N; ++j) {
+      float in = x[k * N + j], ov = val[j];
+      float res = kind == 0 ? maximumf(in, ov) : minimumf(in, ov);
+      int pred = kind == 0 ? (res > ov) : (res < ov);
+      if (pred) idx[j] = in_idx ? in_idx[k * N + j] : k;
+      val[j] = res;
+    }
+}
+
+void hfref_reduce_with_index_i64(int kind, const int64_t *x,
+                                 const int64_t *in_idx, int64_t *val,
+                                 int64_t *idx, int64_t K, int64_t N, int bits) {
+  for (int64_t k = 0; k < K; ++k)
+    for (int64_t j = 0; j < N; ++j) {
+      int64_t in = x[k * N + j], ov = val[j], res;
+      int pred;
+      switch (kind) {
+      case 0: res = in > ov ? in : ov; pred = res > ov; break;
+      case 1: res = in < ov ? in : ov; pred = res < ov; break;
+      case 2: res = ubits(in, bits) > ubits(ov, bits) ? in : ov;
+        pred = ubits(res, bits) > ubits(ov, bits); break;
+      default: res = ubits(in, bits) < ubits(ov, bits) ? in : ov;
+        pred = ubits(res, bits) < ubits(ov, bits);
+      }
+      if (pred) idx[j] = in_idx ? in_idx[k * N + j] : k;
+      val[j] = res;
+    }
+}
+
+/* upstream linalg.matmul region: out = out + cast(a) * cast(b), k innermost */
+void hfref_matmul_i8_i32(const int8_t *A, const int8_t *B, int32_t *C,
+                         int64_t M, int64_t N, int64_t K, int b_transposed) {
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      int32_t acc = C[m * N + n];
+      const int8_t *a = A + m * K;
+      if (b_transposed) {
+        const int8_t *b = B + n * K;
+        for (int64_t k = 0; k < K; ++k) acc += (int32_t)a[k] * (int32_t)b[k];
+      } else {
+        for (int64_t k = 0; k < K; ++k)
+          acc += (int32_t)a[k] * (int32_t)B[k * N + n];
+      }
+      C[m * N + n] = acc;
+    }
+}
+
+void hfref_matmul_f32(const float *A, const float *B, float *C, int64_t M,
+                      int64_t N, int64_t K, int b_transposed) {
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = C[m * N + n];
+      for (int64_t k = 0; k < K; ++k) {
+        float b = b_transposed ? B[n * K + k] : B[k * N + n];
+        float p = A[m * K + k] * b;
+        acc = acc + p;
+      }
+      C[m * N + n] = acc;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* composed groups (op-by-op loop nests, temporaries materialised)           */
+/* ------------------------------------------------------------------------ */
+
+void hfref_vecadd_f32(const float *a, const float *b, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
+/* The RMSNorm + dynamic per-token int8 quant group, op by op as authored in
+ * the group IR (rms_norm structure of
+ * bishengir/test/bishengir-compile/hfusion/compile-rms-norm-fp32-split-n.mlir:5-47,
+ * followed by absmax / scale / nearbyint / clamp / cast). */
+void hfref_rmsnorm_quant(const uint16_t *x_bf16, const uint16_t *gamma_bf16,
+                         float eps, int8_t *q, float *scale, int64_t R,
+                         int64_t C) {
+  size_t n = (size_t)R * (size_t)C;
+  float *xf = malloc(n * 4), *t = malloc(n * 4), *g = malloc((size_t)C * 4);
+  float *ss = malloc((size_t)R * 4), *inv = malloc((size_t)R * 4);
+  float *amax = malloc((size_t)R * 4);
+  for (size_t i = 0; i < n; ++i) xf[i] = hfref_bf16_to_f32(x_bf16[i]);
+  for (size_t i = 0; i < n; ++i) t[i] = xf[i] * xf[i];
+  for (int64_t r = 0; r < R; ++r) {
+    float acc = 0.0f;
+    for (int64_t c = 0; c < C; ++c) acc = t[r * C + c] + acc;
+    ss[r] = acc;
+  }
+  float cf = (float)C;
+  for (int64_t r = 0; r < R; ++r) {
+    float mean = ss[r] / cf;
+    float ms = mean + eps;
+    float rt = sqrtf(ms);
+    inv[r] = 1.0f / rt;
+  }
+  for (int64_t c = 0; c < C; ++c) g[c] = hfref_bf16_to_f32(gamma_bf16[c]);
+  for (int64_t r = 0; r < R; ++r)
+    for (int64_t c = 0; c < C; ++c) {
+      float y1 = xf[r * C + c] * inv[r];
+      t[r * C + c] = y1 * g[c];
+    }
+  for (int64_t r = 0; r < R; ++r) {
+    float acc = 0.0f;
+    for (int64_t c = 0; c < C; ++c) acc = maximumf(fabsf(t[r * C + c]), acc);
+    amax[r] = acc;
+  }
+  for (int64_t r = 0; r < R; ++r) scale[r] = amax[r] / 127.0f;
+  for (int64_t r = 0; r < R; ++r)
+    for (int64_t c = 0; c < C; ++c) {
+      float v = t[r * C + c] / scale[r];
+      v = roundevenf(v);
+      v = minimumf(v, 127.0f);
+      v = maximumf(v, -127.0f);
+      q[r * C + c] = (int8_t)(int32_t)v; /* fptosi: value is integral, in range */
+    }
+  free(xf); free(t); free(g); free(ss); free(inv); free(amax);
+}
+
+/* Safe softmax group (bishengir/test/Dialect/HFusion/regbase/Normalize/
+ * hfusion-normalize-reduction-ops.mlir:262-277 structure, maximumf reduce),
+ * then truncf to bf16. */
+void hfref_softmax_bf16(const float *x, uint16_t *out, int64_t R, int64_t C) {
+  size_t n = (size_t)R * (size_t)C;
+  float *e = malloc(n * 4), *m = malloc((size_t)R * 4), *s = malloc((size_t)R * 4);
+  for (int64_t r = 0; r < R; ++r) {
+    float acc = -INFINITY;
+    for (int64_t c = 0; c < C; ++c) acc = maximumf(x[r * C + c], acc);
+    m[r] = acc;
+  }
+  for (int64_t r = 0; r < R; ++r)
+    for (int64_t c = 0; c < C; ++c) e[r * C + c] = x[r * C + c] - m[r];
+  for (size_t i = 0; i < n; ++i) e[i] = expf(e[i]);
+  for (int64_t r = 0; r < R; ++r) {
+    float acc = 0.0f;
+    for (int64_t c = 0; c < C; ++c) acc = e[r * C + c] + acc;
+    s[r] = acc;
+  }
+  for (int64_t r = 0; r < R; ++r)
+    for (int64_t c = 0; c < C; ++c)
+      out[r * C + c] = hfref_f32_to_bf16(e[r * C + c] / s[r]);
+  free(e); free(m); free(s);
+}
+
+/* reduce_with_index <max> over the last axis, init (-inf, 0), i32 indices. */
+void hfref_argmax(const float *x, float *val, int32_t *idx, int64_t R,
+                  int64_t C) {
+  for (int64_t r = 0; r < R; ++r) {
+    float ov = -INFINITY;
+    int32_t oi = 0;
+    const float *row = x + r * C;
+    for (int64_t c = 0; c < C; ++c) {
+      float res = maximumf(row[c], ov);
+      if (res > ov) oi = (int32_t)c;
+      ov = res;
+    }
+    val[r] = ov;
+    idx[r] = oi;
+  }
+}
+
+/* W8A8: C = matmul_transpose_b(A, B) in i32 (init 0), then
+ * bf16( (sitofp(C) * s_tok[m]) * s_ch[n] ). */
+void hfref_w8a8_dequant_rows(const int8_t *A, const int8_t *Bt,
+                             const float *s_tok, const float *s_ch,
+                             uint16_t *out, int64_t M, int64_t N, int64_t K,
+                             int64_t m0, int64_t m1) {
+  (void)M;
+  int32_t *acc = malloc((size_t)N * 4);
+  for (int64_t m = m0; m < m1; ++m) {
+    memset(acc, 0, (size_t)N * 4);
+    hfref_matmul_i8_i32(A + m * K, Bt, acc, 1, N, K, 1);
+    for (int64_t n = 0; n < N; ++n) {
+      float c = (float)acc[n];
+      float t = c * s_tok[m];
+      float u = t * s_ch[n];
+      out[m * N + n] = hfref_f32_to_bf16(u);
+    }
+  }
+  free(acc);
+}

@@ -1,0 +1,637 @@
+"""hfref interpreter — executes an HFusion group IR on the CPU the way the
+reference's CPU lowering does.  TEST INFRASTRUCTURE ONLY: imported by tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg, never by the product.
+
+Restates `lower-for-cpu-runner-pipeline`
+(bishengir/lib/ExecutionEngine/ExecutionEnginePipelines.cpp:39-90): every op
+becomes its own loop nest over materialised buffers; scalar bodies come from
+RegionBuilderHelper (bishengir/lib/Dialect/HFusion/IR/HFusionOps.cpp:434-862),
+reductions fold serially from the `outs` init (convert-linalg-to-loops),
+reduce_with_index uses the region of HFusionOps.cpp:1507-1595 and
+linalg.matmul the upstream mul/add region with k innermost.
+
+The IR reader here is independent of the product's C++ reader (a different
+implementation of the same textual subset), so a parse mistake on one side
+shows up as a parity failure.
+
+`cast_semantics`:
+  "declared" — hfusion.cast honours its round_mode / enable_saturate
+               (HFusionEnums.td:122-141); this is what the MI355X kernels do.
+  "cpu"      — what the CPU lowering executes: convertScalarToDtype ignores
+               the round mode (f32->iN is fptosi = truncation, same-type float
+               casts are math.round; HFusionOps.cpp:762-862).
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        path = os.path.join(HERE, "libhfref.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} not built (make -C {HERE})")
+        L = ctypes.CDLL(path)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        INT = ctypes.c_int
+        sig = {
+            "hfref_unary_f32": [INT, P, P, I64],
+            "hfref_binary_f32": [INT, P, P, P, I64],
+            "hfref_fma_f32": [P, P, P, P, I64],
+            "hfref_binary_i64": [INT, P, P, P, I64, INT],
+            "hfref_compare_f32": [INT, P, P, P, I64],
+            "hfref_compare_i64": [INT, P, P, P, I64],
+            "hfref_bf16_to_f32_n": [P, P, I64],
+            "hfref_f32_to_bf16_n": [P, P, I64, INT],
+            "hfref_f16_to_f32_n": [P, P, I64],
+            "hfref_f32_to_f16_n": [P, P, I64, INT],
+            "hfref_fptosi_n": [P, P, I64, INT, P],
+            "hfref_f32_to_int_mode_n": [P, P, I64, INT, INT, INT],
+            "hfref_int_to_f32_n": [P, P, I64, INT],
+            "hfref_roundeven_n": [P, P, I64],
+            "hfref_round_n": [P, P, I64],
+            "hfref_reduce_f32": [INT, P, P, I64, I64],
+            "hfref_reduce_i64": [INT, P, P, I64, I64, INT],
+            "hfref_reduce_with_index_f32": [INT, P, P, P, P, I64, I64],
+            "hfref_reduce_with_index_i64": [INT, P, P, P, P, I64, I64, INT],
+            "hfref_matmul_i8_i32": [P, P, P, I64, I64, I64, INT],
+            "hfref_matmul_f32": [P, P, P, I64, I64, I64, INT],
+            "hfref_vecadd_f32": [P, P, P, I64],
+            "hfref_rmsnorm_quant": [P, P, ctypes.c_float, P, P, I64, I64],
+            "hfref_softmax_bf16": [P, P, I64, I64],
+            "hfref_argmax": [P, P, P, I64, I64],
+            "hfref_w8a8_dequant_rows": [P, P, P, P, P, I64, I64, I64, I64, I64],
+        }
+        for name, args in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = None
+        for name in ("hfref_f32_to_bf16", "hfref_f32_to_f16", "hfref_f32_to_bf16_mode", "hfref_f32_to_f16_mode"):
+            getattr(L, name).restype = ctypes.c_uint16
+        L.hfref_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.hfref_f32_to_f16.argtypes = [ctypes.c_float]
+        L.hfref_f32_to_bf16_mode.argtypes = [ctypes.c_float, INT]
+        L.hfref_f32_to_f16_mode.argtypes = [ctypes.c_float, INT]
+        L.hfref_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.hfref_bf16_to_f32.restype = ctypes.c_float
+        L.hfref_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.hfref_f16_to_f32.restype = ctypes.c_float
+        L.hfref_f32_to_int_mode.argtypes = [ctypes.c_float, INT, INT, INT]
+        L.hfref_f32_to_int_mode.restype = ctypes.c_int64
+        L.hfref_int_to_f32_mode.argtypes = [ctypes.c_int64, INT]
+        L.hfref_int_to_f32_mode.restype = ctypes.c_float
+        L.hfref_fold_round_to_odd.argtypes = [ctypes.c_double]
+        L.hfref_fold_round_to_odd.restype = ctypes.c_int64
+        _lib = L
+    return _lib
+
+
+def ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- types
+NP = {"f32": np.float32, "f64": np.float64, "bf16": np.uint16, "f16": np.uint16, "i1": np.bool_,
+      "i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64, "index": np.int64}
+BITS = {"i1": 1, "i8": 8, "i16": 16, "i32": 32, "i64": 64, "index": 64}
+FLOATS = ("f32", "f64", "bf16", "f16")
+ROUND = {"rint": 0, "round": 1, "floor": 2, "ceil": 3, "trunc": 4, "odd": 5, "truncwithoverflow": 6}
+
+
+class T:
+    """A tensor or scalar value: numpy data + element type name."""
+
+    def __init__(self, a, elem):
+        self.a = a
+        self.elem = elem
+
+
+def parse_type(s):
+    s = s.strip()
+    m = re.fullmatch(r"tensor<(.*)>", s)
+    if m:
+        parts = m.group(1).replace(" ", "").split("x")
+        return tuple(int(p) for p in parts[:-1]), parts[-1]
+    return None, s
+
+
+def to_f32(v):
+    a = np.ascontiguousarray(v.a)
+    if v.elem == "f32":
+        return a.astype(np.float32, copy=False)
+    if v.elem == "bf16":
+        out = np.empty(a.shape, np.float32)
+        lib().hfref_bf16_to_f32_n(ptr(a), ptr(out), a.size)
+        return out
+    if v.elem == "f16":
+        out = np.empty(a.shape, np.float32)
+        lib().hfref_f16_to_f32_n(ptr(a), ptr(out), a.size)
+        return out
+    if v.elem == "f64":
+        return a.astype(np.float32)
+    raise TypeError(v.elem)
+
+
+def from_f32(f, elem, mode=0):
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    if elem == "f32":
+        return f
+    if elem in ("bf16", "f16"):
+        out = np.empty(f.shape, np.uint16)
+        getattr(lib(), "hfref_f32_to_bf16_n" if elem == "bf16" else "hfref_f32_to_f16_n")(ptr(f), ptr(out), f.size, mode)
+        return out
+    if elem == "f64":
+        return f.astype(np.float64)
+    raise TypeError(elem)
+
+
+def wrap_int(a64, elem):
+    if elem == "i1":
+        return (a64 & 1).astype(np.bool_)
+    return a64.astype(NP[elem])  # numpy astype wraps two's-complement
+
+
+def convert(v, elem, unsigned=False):
+    """convertScalarToDtype (upstream MLIR) — the `cast` type_fn of named ops."""
+    if v.elem == elem or {v.elem, elem} <= {"i64", "index"}:
+        return T(v.a, elem)
+    if v.elem in FLOATS and elem in FLOATS:
+        if elem == "f64":
+            return T(to_f32(v).astype(np.float64) if v.elem != "f64" else v.a, elem)
+        return T(from_f32(to_f32(v), elem), elem)
+    if v.elem not in FLOATS and elem in FLOATS:
+        a = np.ascontiguousarray(v.a)
+        if unsigned or v.elem == "i1":
+            bits = BITS[v.elem]
+            a64 = a.astype(np.int64) & ((1 << bits) - 1) if bits < 64 else a.astype(np.int64)
+        else:
+            a64 = a.astype(np.int64)
+        a64 = np.ascontiguousarray(a64)
+        if elem == "f64":
+            return T(a64.astype(np.float64), elem)
+        f = np.empty(a64.shape, np.float32)
+        lib().hfref_int_to_f32_n(ptr(a64), ptr(f), a64.size, 0)
+        return T(from_f32(f, elem), elem)
+    if v.elem in FLOATS and elem not in FLOATS:
+        f = np.ascontiguousarray(to_f32(v))
+        if elem == "i1":
+            return T(f != 0, elem)
+        out = np.empty(f.shape, np.int64)
+        poison = ctypes.c_int(0)
+        lib().hfref_fptosi_n(ptr(f), ptr(out), f.size, BITS[elem], ctypes.byref(poison))
+        return T(wrap_int(out, elem), elem)
+    # int -> int
+    a64 = np.asarray(v.a).astype(np.int64)
+    if (unsigned or v.elem == "i1") and BITS[elem] > BITS[v.elem]:
+        a64 = a64 & ((1 << BITS[v.elem]) - 1)
+    return T(wrap_int(a64, elem), elem)
+
+
+def declared_cast(v, elem, mode, sat, unsigned=False):
+    """hfusion.cast with its declared round mode and saturation."""
+    if v.elem in FLOATS and elem in FLOATS:
+        f = to_f32(v)
+        if v.elem == elem:
+            if mode == 0:
+                r = np.empty_like(f)
+                lib().hfref_roundeven_n(ptr(f), ptr(r), f.size)
+            else:
+                out = np.empty(f.shape, np.int64)
+                # round to an integral value in float: via the int rounding on exact values
+                r = f.copy()
+                fin = np.isfinite(f) & (np.abs(f) < 2.0 ** 23)
+                tmp = np.ascontiguousarray(f[fin])
+                o = np.empty(tmp.shape, np.int64)
+                lib().hfref_f32_to_int_mode_n(ptr(tmp), ptr(o), tmp.size, mode, 64, 0)
+                r[fin] = o.astype(np.float32)
+                r[fin & (r == 0)] = np.copysign(0.0, f[fin & (r == 0)])
+            return T(from_f32(r, elem), elem)
+        if elem == "f32":
+            return T(f, elem)
+        return T(from_f32(f, elem, mode), elem)
+    if v.elem in FLOATS and elem not in FLOATS:
+        f = np.ascontiguousarray(to_f32(v))
+        out = np.empty(f.shape, np.int64)
+        lib().hfref_f32_to_int_mode_n(ptr(f), ptr(out), f.size, mode, BITS[elem], int(sat))
+        return T(wrap_int(out, elem), elem)
+    if v.elem not in FLOATS and elem in FLOATS:
+        a64 = np.ascontiguousarray(np.asarray(v.a).astype(np.int64))
+        if unsigned or v.elem == "i1":
+            a64 = a64 & ((1 << BITS[v.elem]) - 1) if BITS[v.elem] < 64 else a64
+        f = np.empty(a64.shape, np.float32)
+        lib().hfref_int_to_f32_n(ptr(a64), ptr(f), a64.size, mode)
+        return T(from_f32(f, elem), elem)
+    a64 = np.asarray(v.a).astype(np.int64)
+    if sat and BITS[elem] < BITS[v.elem]:
+        lo, hi = -(1 << (BITS[elem] - 1)), (1 << (BITS[elem] - 1)) - 1
+        a64 = np.clip(a64, lo, hi)
+    return convert(T(a64, "i64"), elem, unsigned)
+
+
+UNARY = {"sqrt": 0, "rsqrt": 1, "exp": 2, "exp2": 3, "log": 4, "log2": 5, "log10": 6, "log1p": 7, "expm1": 8,
+         "abs": 9, "absf": 9, "negf": 10, "neg": 10, "relu": 11, "rec": 12, "reciprocal": 12, "tanh": 13,
+         "sin": 14, "cos": 15, "erf": 16, "nearbyint": 17, "ceil": 18, "floor": 19, "round": 20, "square": 21}
+BINARY_F = {"add": 0, "sub": 1, "mul": 2, "div": 3, "maxf": 4, "max_signed": 4, "minf": 5, "min_signed": 5,
+            "maxnumf": 6, "minnumf": 7, "powf": 8, "mod": 9, "copysign": 10}
+BINARY_I = {"add": 32, "sub": 33, "mul": 34, "div": 35, "max_signed": 36, "maxsi": 36, "min_signed": 37,
+            "vand": 38, "vor": 39, "vxor": 40, "shli": 41, "shrsi": 42, "shrui": 43, "mod": 44,
+            "floordivsi": 45, "ceildivsi": 46, "max_unsigned": 47, "min_unsigned": 48}
+COMPARE = {"veq": 0, "vne": 1, "vlt": 2, "vle": 3, "vgt": 4, "vge": 5}
+REDUCE_F = {"arith.addf": 0, "arith.mulf": 1, "arith.maximumf": 2, "arith.minimumf": 3, "arith.maxnumf": 4,
+            "arith.minnumf": 5}
+REDUCE_I = {"arith.addi": 0, "arith.muli": 1, "arith.maxsi": 2, "arith.minsi": 3, "arith.andi": 4,
+            "arith.ori": 5, "arith.xori": 6, "arith.maxui": 7, "arith.minui": 8}
+
+
+def _full(v, shape):
+    return np.ascontiguousarray(np.broadcast_to(v.a, shape))
+
+
+def apply_unary(fn, x, U):
+    if U in FLOATS:
+        f = np.ascontiguousarray(np.broadcast_to(to_f32(x), np.shape(x.a)))
+        out = np.empty(f.shape, np.float32)
+        lib().hfref_unary_f32(UNARY[fn], ptr(f), ptr(out), f.size)
+        return T(from_f32(out, U), U)
+    a = np.asarray(x.a).astype(np.int64)
+    if fn == "relu":
+        r = np.maximum(a, 0)
+    elif fn == "vnot":
+        r = ~a
+    elif fn in ("absi", "abs"):
+        r = np.abs(a)
+    else:
+        raise NotImplementedError(f"integer unary {fn}")
+    return T(wrap_int(r, U), U)
+
+
+def apply_binary(fn, x, y, U, shape):
+    if U in FLOATS:
+        a = np.ascontiguousarray(np.broadcast_to(to_f32(x), shape))
+        b = np.ascontiguousarray(np.broadcast_to(to_f32(y), shape))
+        out = np.empty(shape, np.float32)
+        lib().hfref_binary_f32(BINARY_F[fn], ptr(a), ptr(b), ptr(out), out.size)
+        return T(from_f32(out, U), U)
+    a = np.ascontiguousarray(np.broadcast_to(np.asarray(x.a).astype(np.int64), shape))
+    b = np.ascontiguousarray(np.broadcast_to(np.asarray(y.a).astype(np.int64), shape))
+    out = np.empty(shape, np.int64)
+    lib().hfref_binary_i64(BINARY_I[fn], ptr(a), ptr(b), ptr(out), out.size, BITS[U])
+    return T(wrap_int(out, U), U)
+
+
+# ---------------------------------------------------------------- parsing
+_RES = re.compile(r"^\s*(%[\w.$-]+)(?::(\d+))?(?:\s*,\s*(%[\w.$-]+))*\s*=\s*([\w.]+)(.*)$")
+
+
+def _statements(body):
+    """Splits a function body into statements, joining multi-line regions."""
+    out, cur, depth = [], "", 0
+    for line in body.split("\n"):
+        line = line.split("//")[0].rstrip()
+        if not line.strip():
+            continue
+        cur = (cur + " " + line) if cur else line
+        depth += line.count("{") - line.count("}") + line.count("(") - line.count(")")
+        if depth <= 0:
+            # a region opener on the following line belongs to this statement
+            out.append(cur)
+            cur, depth = "", 0
+    merged = []
+    for s in out:
+        if merged and s.strip().startswith("("):
+            merged[-1] += " " + s
+        else:
+            merged.append(s)
+    return merged
+
+
+def _split_top(s, sep=","):
+    parts, depth, cur = [], 0, ""
+    for ch in s:
+        if ch in "<([{":
+            depth += 1
+        elif ch in ">)]}":
+            depth -= 1
+        if ch == sep and depth == 0:
+            parts.append(cur)
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip():
+        parts.append(cur)
+    return [p.strip() for p in parts]
+
+
+def _group(s, key):
+    """Contents of `key(...)` with balanced parentheses."""
+    i = s.find(key + "(")
+    if i < 0:
+        return None
+    i += len(key) + 1
+    depth, j = 1, i
+    while depth:
+        if s[j] == "(":
+            depth += 1
+        elif s[j] == ")":
+            depth -= 1
+        j += 1
+    return s[i:j - 1]
+
+
+def _operands(group):
+    if group is None:
+        return [], []
+    if ":" in group:
+        names, types = group.split(":", 1)
+        return [n.strip() for n in names.split(",") if n.strip()], [parse_type(t) for t in _split_top(types)]
+    return [n.strip() for n in group.split(",") if n.strip()], []
+
+
+def _attr(s, key):
+    m = re.search(key + r"\s*=\s*#[\w.]+<(\w+)>", s)
+    if m:
+        return m.group(1)
+    m = re.search(key + r"\s*=\s*(\w+)", s)
+    return m.group(1) if m else None
+
+
+def parse_funcs(text):
+    funcs = {}
+    for m in re.finditer(r"func\.func\s+(?:private\s+)?@(\w+)\s*\(", text):
+        name = m.group(1)
+        i = m.end()
+        depth, j = 1, i
+        while depth:
+            depth += {"(": 1, ")": -1}.get(text[j], 0)
+            j += 1
+        args = []
+        for a in _split_top(text[i:j - 1]):
+            nm, ty = a.split(":", 1)
+            args.append((nm.strip(), parse_type(ty.split("{")[0])))
+        # body: first '{' after `attributes {...}` (or after the signature)
+        k = j
+        sig_end = text.index("{", k)
+        rest = text[k:sig_end]
+        if "attributes" in rest:
+            d, q = 1, sig_end + 1
+            while d:
+                d += {"{": 1, "}": -1}.get(text[q], 0)
+                q += 1
+            sig_end = text.index("{", q)
+        d, q = 1, sig_end + 1
+        while d:
+            d += {"{": 1, "}": -1}.get(text[q], 0)
+            q += 1
+        funcs[name] = (args, text[sig_end + 1:q - 1])
+    return funcs
+
+
+class Interp:
+    def __init__(self, text, cast_semantics="declared"):
+        self.funcs = parse_funcs(text)
+        self.cast_semantics = cast_semantics
+
+    def run(self, func=None, *inputs):
+        """Runs group `func` with numpy inputs (one per argument; bf16/f16
+        given as uint16 bit patterns).  Returns the list of results."""
+        if func is None:
+            if len(self.funcs) != 1:
+                raise ValueError("several functions; name one")
+            func = next(iter(self.funcs))
+        args, body = self.funcs[func]
+        if len(inputs) != len(args):
+            raise ValueError(f"@{func} takes {len(args)} arguments")
+        env = {}
+        for (nm, (shape, elem)), x in zip(args, inputs):
+            if shape is None:
+                env[nm] = T(np.asarray(x, dtype=NP[elem]), elem)
+            else:
+                a = np.ascontiguousarray(x, dtype=NP[elem])
+                if a.shape != shape:
+                    raise ValueError(f"{nm}: expected shape {shape}, got {a.shape}")
+                env[nm] = T(a.copy(), elem)
+        for st in _statements(body):
+            s = st.strip()
+            if s.startswith("return") or s.startswith("func.return"):
+                names = re.findall(r"%[\w.$#-]+", s.split(":")[0])
+                return [env[n].a for n in names]
+            self._exec(s, env)
+        raise ValueError("function without return")
+
+    def _exec(self, s, env):
+        m = re.match(r"^\s*(%[\w.$-]+)(?::(\d+))?\s*=\s*([\w.]+)(.*)$", s)
+        if not m:
+            raise ValueError(f"cannot parse statement: {s}")
+        res, nres, op, rest = m.group(1), m.group(2), m.group(3), m.group(4)
+
+        def get(n):
+            return env[n]
+
+        if op == "arith.constant":
+            lit, ty = rest.rsplit(":", 1)
+            shape, elem = parse_type(ty)
+            lit = lit.strip()
+            dm = re.match(r"dense<(.*)>", lit)
+            if dm:
+                lit = dm.group(1)
+            if lit in ("true", "false"):
+                val = lit == "true"
+            elif lit.lower().startswith("0x") and elem in FLOATS:
+                bits = int(lit, 16)
+                val = {"f32": lambda b: np.array([b], np.uint32).view(np.float32)[0],
+                       "f64": lambda b: np.array([b], np.uint64).view(np.float64)[0]}[elem](bits)
+            elif elem in FLOATS:
+                val = float(lit)
+            else:
+                val = int(lit, 0)
+            if elem in ("bf16", "f16"):
+                arr = from_f32(np.array(val, np.float32), elem)
+            else:
+                arr = np.array(val, dtype=NP[elem])
+            env[res] = T(arr if shape is None else np.broadcast_to(arr, shape).copy(), elem)
+            return
+        if op == "tensor.empty":
+            shape, elem = parse_type(rest.split(":", 1)[1])
+            env[res] = T(np.zeros(shape, NP[elem]), elem)
+            return
+        if op == "tensor.dim":
+            names = re.findall(r"%[\w.$-]+", rest)
+            env[res] = T(np.int64(env[names[0]].a.shape[int(env[names[1]].a)]), "index")
+            return
+        if op.startswith("arith.") and "ins(" not in rest:
+            self._scalar_arith(res, op, rest, env)
+            return
+        ins, ins_t = _operands(_group(rest, "ins"))
+        outs, outs_t = _operands(_group(rest, "outs"))
+        if op == "linalg.fill":
+            o = get(outs[0])
+            v = convert(get(ins[0]), o.elem)
+            env[res] = T(np.broadcast_to(v.a, o.a.shape).copy(), o.elem)
+            return
+        if op == "linalg.broadcast":
+            dims = [int(d) for d in re.search(r"dimensions\s*=\s*\[([^\]]*)\]", rest).group(1).split(",") if d.strip()]
+            x, o = get(ins[0]), get(outs[0])
+            a = x.a
+            for d in sorted(dims):
+                a = np.expand_dims(a, d)
+            env[res] = T(np.broadcast_to(a, o.a.shape).copy(), o.elem)
+            return
+        if op == "linalg.reduce":
+            self._reduce(res, rest, ins, outs, env)
+            return
+        if op == "hfusion.reduce_with_index":
+            self._reduce_with_index(res, rest, ins, outs, env)
+            return
+        if op in ("linalg.matmul", "linalg.matmul_transpose_b"):
+            A, B, Cinit = get(ins[0]), get(ins[1]), get(outs[0])
+            bt = int(op.endswith("transpose_b"))
+            M, K = A.a.shape
+            N = Cinit.a.shape[1]
+            if A.elem == "i8" and Cinit.elem == "i32":
+                C = np.ascontiguousarray(Cinit.a.copy())
+                lib().hfref_matmul_i8_i32(ptr(np.ascontiguousarray(A.a)), ptr(np.ascontiguousarray(B.a)), ptr(C), M, N, K, bt)
+            elif Cinit.elem == "f32":
+                C = np.ascontiguousarray(Cinit.a.copy())
+                lib().hfref_matmul_f32(ptr(np.ascontiguousarray(to_f32(A))), ptr(np.ascontiguousarray(to_f32(B))), ptr(C),
+                                       M, N, K, bt)
+            else:
+                raise NotImplementedError("matmul types")
+            env[res] = T(C, Cinit.elem)
+            return
+        # elementwise ops
+        o = get(outs[0])
+        U, shape = o.elem, o.a.shape
+        xs = [get(n) for n in ins]
+        uns = _attr(rest, "cast") == "cast_unsigned"
+        if op in ("hfusion.elemwise_unary", "linalg.elemwise_unary"):
+            fn = _attr(rest, "fun") or ("sqrt" if op.startswith("hfusion") else "exp")
+            r = apply_unary(fn, convert(T(np.broadcast_to(xs[0].a, shape), xs[0].elem), U, uns), U)
+        elif op in ("hfusion.elemwise_binary", "linalg.elemwise_binary"):
+            fn = _attr(rest, "fun") or ("vand" if op.startswith("hfusion") else "add")
+            r = apply_binary(fn, convert(xs[0], U, uns), convert(xs[1], U, uns), U, shape)
+        elif op == "hfusion.compare":
+            fn = _attr(rest, "compare_fn") or "veq"
+            a, b = xs
+            if a.elem in FLOATS:
+                fa = np.ascontiguousarray(np.broadcast_to(to_f32(a), shape))
+                fb = np.ascontiguousarray(np.broadcast_to(to_f32(b), shape))
+                out = np.empty(shape, np.uint8)
+                lib().hfref_compare_f32(COMPARE[fn], ptr(fa), ptr(fb), ptr(out), out.size)
+            else:
+                ia = np.ascontiguousarray(np.broadcast_to(a.a.astype(np.int64), shape))
+                ib = np.ascontiguousarray(np.broadcast_to(b.a.astype(np.int64), shape))
+                out = np.empty(shape, np.uint8)
+                lib().hfref_compare_i64(COMPARE[fn], ptr(ia), ptr(ib), ptr(out), out.size)
+            r = T(out.astype(np.bool_), "i1")
+        elif op == "hfusion.select":
+            c, a, b = xs
+            r = T(np.where(np.broadcast_to(c.a, shape), np.broadcast_to(a.a, shape), np.broadcast_to(b.a, shape)).astype(NP[U]), U)
+        elif op == "hfusion.cast":
+            mode = ROUND[_attr(rest, "round_mode") or "rint"]
+            sat = (_attr(rest, "enable_saturate") == "true")
+            x = T(np.broadcast_to(xs[0].a, shape), xs[0].elem)
+            if self.cast_semantics == "cpu":
+                if x.elem == U and U in FLOATS:
+                    f = np.ascontiguousarray(to_f32(x))
+                    rr = np.empty_like(f)
+                    lib().hfref_round_n(ptr(f), ptr(rr), f.size)
+                    r = T(from_f32(rr, U), U)
+                else:
+                    r = convert(x, U, uns)
+            else:
+                r = declared_cast(x, U, mode, sat, uns or "ui2" in (_attr(rest, "unsigned_mode") or ""))
+        else:
+            raise NotImplementedError(f"op {op}")
+        env[res] = T(np.ascontiguousarray(np.broadcast_to(r.a, shape)).astype(NP[U], copy=False), U)
+
+    def _scalar_arith(self, res, op, rest, env):
+        names = re.findall(r"%[\w.$-]+", rest)
+        ty = rest.rsplit(":", 1)[1]
+        to = None
+        if " to " in ty:
+            ty, to = ty.split(" to ")
+        _, elem = parse_type(to or ty)
+        vals = [env[n].a for n in names]
+        f32 = elem == "f32"
+        if op in ("arith.index_cast", "arith.index_castui", "arith.extsi", "arith.extui", "arith.trunci"):
+            v = np.array(int(vals[0]), NP[elem])
+        elif op in ("arith.sitofp", "arith.uitofp"):
+            v = np.array(float(vals[0]), NP[elem])
+        elif op in ("arith.extf", "arith.truncf"):
+            v = np.array(vals[0], NP[elem])
+        else:
+            a = [np.float32(x) if f32 else x for x in vals]
+            v = {"arith.addf": lambda: a[0] + a[1], "arith.subf": lambda: a[0] - a[1],
+                 "arith.mulf": lambda: a[0] * a[1], "arith.divf": lambda: a[0] / a[1],
+                 "arith.negf": lambda: -a[0], "arith.addi": lambda: a[0] + a[1],
+                 "arith.subi": lambda: a[0] - a[1], "arith.muli": lambda: a[0] * a[1]}[op]()
+            v = np.array(v, NP[elem])
+        env[res] = T(v, elem)
+
+    def _reduce(self, res, rest, ins, outs, env):
+        dims = [int(d) for d in re.search(r"dimensions\s*=\s*\[([^\]]*)\]", rest).group(1).split(",") if d.strip()]
+        comb = re.search(r"\{\s*(arith\.\w+)\s*\}", rest)
+        if comb is None:
+            comb = re.search(r"(arith\.\w+)\s+%", rest)
+        comb = comb.group(1)
+        x, init = env[ins[0]], env[outs[0]]
+        rank = x.a.ndim
+        keep = [d for d in range(rank) if d not in dims]
+        # loop nest d0..d{r-1}: for each output element the reduced indices
+        # are visited in ascending lexicographic order
+        xt = np.ascontiguousarray(np.transpose(x.a, dims + keep))
+        K = int(np.prod([x.a.shape[d] for d in dims]))
+        N = int(np.prod([x.a.shape[d] for d in keep])) if keep else 1
+        if x.elem == "f32":
+            acc = np.ascontiguousarray(init.a.astype(np.float32).reshape(N)).copy()
+            lib().hfref_reduce_f32(REDUCE_F[comb], ptr(xt.reshape(K, N)), ptr(acc), K, N)
+            env[res] = T(acc.reshape(init.a.shape), "f32")
+        elif x.elem in ("bf16", "f16"):
+            raise NotImplementedError("16-bit float reductions")
+        else:
+            acc = np.ascontiguousarray(init.a.astype(np.int64).reshape(N)).copy()
+            xi = np.ascontiguousarray(xt.reshape(K, N).astype(np.int64))
+            lib().hfref_reduce_i64(REDUCE_I[comb], ptr(xi), ptr(acc), K, N, BITS[x.elem])
+            env[res] = T(wrap_int(acc, x.elem).reshape(init.a.shape), x.elem)
+
+    def _reduce_with_index(self, res, rest, ins, outs, env):
+        dims = [int(d) for d in re.search(r"dimensions\s*=\s*\[([^\]]*)\]", rest).group(1).split(",") if d.strip()]
+        kind = re.search(r"<(\w+)>", rest.split("ins(")[0]).group(1)
+        x = env[ins[0]]
+        idx_in = env[ins[1]] if len(ins) > 1 else None
+        v0, i0 = env[outs[0]], env[outs[1]]
+        d = dims[0]
+        rank = x.a.ndim
+        keep = [k for k in range(rank) if k != d]
+        xt = np.ascontiguousarray(np.transpose(x.a, [d] + keep))
+        K = x.a.shape[d]
+        N = int(np.prod([x.a.shape[k] for k in keep])) if keep else 1
+        val = np.ascontiguousarray(v0.a.reshape(N)).copy()
+        idx = np.ascontiguousarray(i0.a.astype(np.int64).reshape(N)).copy()
+        ii = None
+        if idx_in is not None:
+            ii = np.ascontiguousarray(np.transpose(idx_in.a, [d] + keep).astype(np.int64).reshape(K, N))
+        if x.elem == "f32":
+            lib().hfref_reduce_with_index_f32({"max": 0, "min": 1}[kind], ptr(xt.reshape(K, N)),
+                                              ptr(ii) if ii is not None else None, ptr(val), ptr(idx), K, N)
+        else:
+            xi = np.ascontiguousarray(xt.reshape(K, N).astype(np.int64))
+            v64 = np.ascontiguousarray(val.astype(np.int64))
+            lib().hfref_reduce_with_index_i64({"max": 0, "min": 1, "maxui": 2, "minui": 3}[kind], ptr(xi),
+                                              ptr(ii) if ii is not None else None, ptr(v64), ptr(idx), K, N, BITS[x.elem])
+            val = wrap_int(v64, x.elem)
+        base = res
+        env[base + "#0"] = T(val.reshape(v0.a.shape), v0.elem)
+        env[base + "#1"] = T(wrap_int(idx, i0.elem).reshape(i0.a.shape), i0.elem)
+        env[base] = env[base + "#0"]
+
+
+def run(ir_text, *inputs, func=None, cast_semantics="declared"):
+    return Interp(ir_text, cast_semantics).run(func, *inputs)

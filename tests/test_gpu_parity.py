@@ -1,0 +1,224 @@
+"""GPU parity: each group runs through the HIP kernel (libhfr) and through the
+CPU oracle (oracle/interp.py) on the same seeded inputs.
+
+Bars: bit-exact for integer, index, quantised and exactly-rounded outputs;
+<= 1 bf16 ulp where the result passes through exp or a reordered fp32 sum
+before the final bf16 rounding; fp32 outputs within 1e-5 relative (plus a
+row-scaled absolute term for outputs produced by cancellation).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import hfusion_mi355x as hf
+from helpers import bf16_ulp_diff, run_gpu, run_oracle
+
+pytestmark = pytest.mark.gpu
+I = hf.inputs
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def zeros(shape, dt):
+    return np.zeros(shape, dt)
+
+
+# ------------------------------------------------------------------ vec_add
+def test_vec_add_golden_i16(gpu):
+    note("vec_add_i16 golden (VecAdd/main.cpp)")
+    g = json.load(open(os.path.join(GOLDEN, "vecadd_i16.json")))
+    a, b = np.array(g["a"], np.int16), np.array(g["b"], np.int16)
+    out, = run_gpu("vec_add_i16", [a, b, zeros(16, np.int16)], gpu)
+    assert out.tolist() == g["expect"]
+
+
+@pytest.mark.parametrize("name,n", [("vec_add_1m", 1 << 20), ("vec_add_ragged", 1001)])
+def test_vec_add(gpu, name, n):
+    note(name)
+    a, b = I.config_inputs("vec_add", n=n)
+    out, = run_gpu(name, [a, b, zeros(n, np.float32)], gpu)
+    ref, = run_oracle(name, [a, b, zeros(n, np.float32)])
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ rmsnorm + quant
+@pytest.mark.parametrize("name,rows,cols", [("rmsnorm_quant_256", 256, 4096), ("rmsnorm_quant_ragged", 13, 1000)])
+def test_rmsnorm_quant(gpu, name, rows, cols):
+    note(name)
+    x, gamma = I.config_inputs("rmsnorm_quant", rows=rows, cols=cols)
+    args = [x, gamma, zeros((rows, cols), np.int8), zeros(rows, np.float32)]
+    q, s = run_gpu(name, args, gpu)
+    rq, rs = run_oracle(name, args)
+    assert np.array_equal(s.view(np.uint32), rs.view(np.uint32)), "per-row scale must be bit-exact"
+    assert np.array_equal(q, rq), f"{int((q != rq).sum())} int8 codes differ"
+
+
+# ------------------------------------------------------------------ softmax
+@pytest.mark.parametrize("name,rows,cols", [("safe_softmax_64", 64, 32768), ("safe_softmax_ragged", 33, 1000)])
+def test_safe_softmax(gpu, name, rows, cols):
+    note(name)
+    x, = I.config_inputs("safe_softmax", rows=rows, cols=cols)
+    args = [x, zeros((rows, cols), np.uint16)]
+    out, = run_gpu(name, args, gpu)
+    ref, = run_oracle(name, args)
+    d = bf16_ulp_diff(out, ref)
+    assert d.max() <= 1, f"max {d.max()} bf16 ulp"
+
+
+# ------------------------------------------------------------------ argmax
+def argmax_special(rows, cols, seed):
+    x = I.argmax_logits(seed, rows, cols, dup_every=1)
+    if rows >= 8:
+        x[1, :] = -np.inf                       # no element beats the init -> index 0
+        x[2, :] = 0.0
+        x[2, 5] = -0.0                          # +0/-0 are one class: first of them wins
+        x[3, cols // 3] = np.nan                # NaN: value NaN, index from the prefix
+        x[4, 0] = np.nan                        # NaN first: index stays at init
+        x[5, :] = 7.0                           # all equal -> 0
+        x[6, cols - 1] = 1e30                   # maximum in the last element
+        x[7, cols // 2] = np.inf
+        x[7, cols // 2 + 3] = np.inf
+    return x
+
+
+@pytest.mark.parametrize("name,rows,cols,it", [("argmax_16", 16, 152064, np.int32), ("argmax_ragged", 5, 1001, np.int32),
+                                               ("argmax_i64", 8, 4096, np.int64)])
+def test_argmax(gpu, name, rows, cols, it):
+    note(name)
+    x = argmax_special(rows, cols, I.SEED_BASE + 30)
+    args = [x, zeros(rows, np.float32), zeros(rows, it)]
+    v, i = run_gpu(name, args, gpu)
+    rv, ri = run_oracle(name, args)
+    assert np.array_equal(i, ri)
+    assert np.array_equal(np.isnan(v), np.isnan(rv))
+    ok = ~np.isnan(rv)
+    assert np.array_equal(v[ok].view(np.uint32), rv[ok].view(np.uint32))
+
+
+def test_argmax_repeat_launch(gpu):
+    """The per-row arrival counters reset themselves: two launches agree."""
+    note("argmax_16 repeated")
+    x = argmax_special(16, 152064, I.SEED_BASE + 31)
+    args = [x, zeros(16, np.float32), zeros(16, np.int32)]
+    a = run_gpu("argmax_16", args, gpu)
+    b = run_gpu("argmax_16", args, gpu)
+    assert all(np.array_equal(p, q, equal_nan=True) for p, q in zip(a, b))
+
+
+# ------------------------------------------------------------------ W8A8
+@pytest.mark.parametrize("name,m,n,k", [("w8a8_512", 512, 512, 512), ("w8a8_ragged", 300, 200, 160)])
+def test_w8a8(gpu, name, m, n, k):
+    note(name)
+    a, b, st, sc = I.config_inputs("w8a8_dequant", m=m, n=n, k=k)
+    args = [a, b, st, sc, zeros((m, n), np.uint16)]
+    out, = run_gpu(name, args, gpu)
+    ref, = run_oracle(name, args)
+    assert np.array_equal(out, ref), f"max {bf16_ulp_diff(out, ref).max()} ulp"
+
+
+def test_bf16_mmad(gpu):
+    note("bf16_mmad_256")
+    s = I.SEED_BASE + 40
+    a, b = I.normal_bf16(s, (256, 256)), I.normal_bf16(s + 1, (256, 256))
+    args = [a, b, zeros((256, 256), np.uint16)]
+    out, = run_gpu("bf16_mmad_256", args, gpu)
+    ref, = run_oracle("bf16_mmad_256", args)
+    # fp32 accumulation order differs from the serial k loop
+    assert bf16_ulp_diff(out, ref).max() <= 1
+
+
+# ------------------------------------------------------------------ casts
+def cast_inputs(n):
+    v = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 0.49999997, 126.5, 127.5, -127.5, -128.5, 128.7, 127.5, 100.3, -129.2,
+         -128.4, 300.7, -300.2, 1e-40, -1e-40, -0.0, 0.0, 3.0000002, 1.00390625, 1.0048828, 65504.0, 65520.0, 1e5,
+         -1e5, 5.9604645e-08, 2.9802322e-08, 8.940697e-08]
+    rnd = I.normal_f32(I.SEED_BASE + 50, (n,), std=200.0)
+    x = np.concatenate([np.array(v, np.float32), rnd])[:n]
+    return np.ascontiguousarray(x.astype(np.float32))
+
+
+CAST_FUNCS = [f"cast_{t}_{m}{s}" for m in ["rint", "round", "floor", "ceil", "trunc", "odd"]
+              for t, s in (("i8", "_sat"), ("i8", ""), ("i32", ""), ("bf16", ""), ("f16", ""))]
+
+
+@pytest.mark.parametrize("func", CAST_FUNCS)
+def test_cast_round_modes(gpu, func):
+    note(func)
+    n = 4096
+    x = cast_inputs(n)
+    tgt = func.split("_")[1]
+    dt = {"i8": np.int8, "i32": np.int32, "bf16": np.uint16, "f16": np.uint16}[tgt]
+    out, = run_gpu("cast_modes", [x, zeros(n, dt)], gpu, func=func)
+    ref, = run_oracle("cast_modes", [x, zeros(n, dt)], func=func)
+    assert np.array_equal(out, ref), f"{int((out != ref).sum())} differ, e.g. x={x[out != ref][:4]}"
+
+
+@pytest.mark.parametrize("mode", ["rint", "round", "floor", "ceil", "trunc", "odd"])
+def test_cast_int_and_same_type(gpu, mode):
+    note(f"cast i32->f32 / f32->f32 {mode}")
+    n = 4096
+    xi = np.concatenate([np.array([16777217, -16777217, 16777219, 2147483647, -2147483648, 33554435, 7, -7], np.int32),
+                         (I.splitmix64(I.SEED_BASE + 51, n - 8) >> np.uint64(32)).astype(np.uint32).view(np.int32)])
+    out, = run_gpu("cast_modes", [xi, zeros(n, np.float32)], gpu, func=f"cast_i32_f32_{mode}")
+    ref, = run_oracle("cast_modes", [xi, zeros(n, np.float32)], func=f"cast_i32_f32_{mode}")
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    x = cast_inputs(n)
+    out, = run_gpu("cast_modes", [x, zeros(n, np.float32)], gpu, func=f"cast_f32_f32_{mode}")
+    ref, = run_oracle("cast_modes", [x, zeros(n, np.float32)], func=f"cast_f32_f32_{mode}")
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ generic lowering
+def test_eltwise_mix(gpu):
+    note("eltwise_mix")
+    s = I.SEED_BASE + 60
+    x = I.normal_f32(s, (64, 1000))
+    b = I.normal_f32(s + 1, (1000,))
+    sc = I.uniform_f32(s + 2, (64,), 0.5, 2.0)
+    args = [x, b, sc, zeros((64, 1000), np.uint16), zeros((64, 1000), np.bool_)]
+    y, mask = run_gpu("eltwise_mix", args, gpu)
+    ry, rmask = run_oracle("eltwise_mix", args)
+    assert np.array_equal(mask, rmask)
+    assert bf16_ulp_diff(y, ry).max() <= 1  # exp: GPU vs glibc expf
+
+
+def test_layernorm(gpu):
+    note("layernorm")
+    s = I.SEED_BASE + 70
+    x = I.normal_f32(s, (64, 2048), std=3.0) + np.float32(1.5)
+    w, bias = I.uniform_f32(s + 1, (2048,), 0.5, 1.5), I.uniform_f32(s + 2, (2048,), -0.5, 0.5)
+    args = [x, w, bias, zeros((64, 2048), np.float32), zeros(64, np.float32)]
+    y, mu = run_gpu("layernorm", args, gpu)
+    ry, rmu = run_oracle("layernorm", args)
+    np.testing.assert_allclose(mu, rmu, rtol=1e-5, atol=1e-6)
+    # tree vs serial sums: 1e-5 relative, absolute term scaled by the row's magnitude
+    np.testing.assert_allclose(y, ry, rtol=1e-5, atol=1e-5 * np.abs(ry).max())
+
+
+def test_reduce_ops(gpu):
+    note("reduce_ops")
+    s = I.SEED_BASE + 80
+    x = I.normal_f32(s, (48, 3000))
+    x[3, 17] = np.nan
+    x[4, :] = -0.0
+    x[4, 9] = 0.0
+    xi = (I.splitmix64(s + 1, 48 * 3000) % np.uint64(2000001)).astype(np.int64).astype(np.int32).reshape(48, 3000) - 1000000
+    args = [x, xi, zeros(48, np.float32), zeros(48, np.float32), zeros(48, np.float32), zeros(48, np.int32)]
+    got = run_gpu("reduce_ops", args, gpu)
+    ref = run_oracle("reduce_ops", args)
+    for k, (g_, r_) in enumerate(zip(got, ref)):
+        g_, r_ = np.asarray(g_), np.asarray(r_)
+        if k < 3:
+            assert np.array_equal(np.isnan(g_), np.isnan(r_))
+            ok = ~np.isnan(r_)
+            g_, r_ = g_[ok], r_[ok]
+        if k == 2:
+            # maxnumf leaves the sign of a zero maximum unspecified
+            assert np.array_equal(g_, r_)
+        else:
+            assert np.array_equal(g_.view(np.uint32), r_.view(np.uint32))
