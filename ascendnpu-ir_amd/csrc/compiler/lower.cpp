@@ -941,10 +941,13 @@ struct RowEmitter {
       initExpr = at(init, "");
     } else if (init->isConst) {
       initExpr = constExpr(init, t);
+    } else if (init->def && init->def->name == "tensor.empty") {
+      initExpr = "EMPTY"; // uninitialised destination: the combiner's identity
     } else {
       unsupported(op, "reduction init must be a linalg.fill or an argument");
     }
     Combiner cb = combinerFor(op, op->combiner, t);
+    if (initExpr == "EMPTY") initExpr = cb.identity;
     const Value *res = op->results[0];
     std::string nm = fresh();
     name[res] = nm;

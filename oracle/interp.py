@@ -409,6 +409,7 @@ class Interp:
         if len(inputs) != len(args):
             raise ValueError(f"@{func} takes {len(args)} arguments")
         env = {}
+        self.empties = set()
         for (nm, (shape, elem)), x in zip(args, inputs):
             if shape is None:
                 env[nm] = T(np.asarray(x, dtype=NP[elem]), elem)
@@ -460,6 +461,7 @@ class Interp:
         if op == "tensor.empty":
             shape, elem = parse_type(rest.split(":", 1)[1])
             env[res] = T(np.zeros(shape, NP[elem]), elem)
+            self.empties.add(res)
             return
         if op == "tensor.dim":
             names = re.findall(r"%[\w.$-]+", rest)
@@ -582,6 +584,12 @@ class Interp:
             comb = re.search(r"(arith\.\w+)\s+%", rest)
         comb = comb.group(1)
         x, init = env[ins[0]], env[outs[0]]
+        if outs[0] in self.empties:
+            # reducing into an uninitialised tensor.empty: start from the identity
+            ident = {"arith.addf": -0.0, "arith.mulf": 1.0, "arith.maximumf": -np.inf, "arith.minimumf": np.inf,
+                     "arith.maxnumf": np.nan, "arith.minnumf": np.nan}
+            if x.elem == "f32":
+                init = T(np.full(init.a.shape, ident[comb], np.float32), "f32")
         rank = x.a.ndim
         keep = [d for d in range(rank) if d not in dims]
         # loop nest d0..d{r-1}: for each output element the reduced indices
