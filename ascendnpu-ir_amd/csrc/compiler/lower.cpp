@@ -14,6 +14,7 @@
 #include "lower.h"
 
 #include <algorithm>
+#include <cctype>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -270,7 +271,7 @@ std::string declaredCastExpr(const std::string &x, Elem from, Elem to, int mode,
 std::string f32UnaryFn(const std::string &fn, const std::string &x, const Op *op) {
   if (fn == "sqrt") return "__builtin_sqrtf(" + x + ")";
   if (fn == "rsqrt") return "hf::rsqrt(" + x + ")";
-  if (fn == "exp") return "expf(" + x + ")";
+  if (fn == "exp") return "hf::exp_f32(" + x + ")";
   if (fn == "exp2") return "exp2f(" + x + ")";
   if (fn == "log") return "logf(" + x + ")";
   if (fn == "log2") return "log2f(" + x + ")";
@@ -735,10 +736,15 @@ double algoBytes(const Analysis &A) {
 }
 
 // ======================================================================
-// Elementwise / row-program emitter.  Values live in one of four spaces of a
-// 2-D domain [R, C] (1-D groups use R = 1): Full (per element, an array of EPL
-// lanes' elements), Row (per row, a scalar), Col (per column, an array),
-// Scalar (a constant or kernel argument).
+// Row-program emitter (LAST_AXIS_PBR).  Domain [R, C] (1-D groups use R = 1).
+// A row group of TR threads owns RPW consecutive rows; a block holds RB row
+// groups.  Values live in one of four spaces:
+//   Full  — per element; either an array of RPW*EPL lane elements or a lazy
+//           expression re-evaluated at each use (cheap chains are recomputed
+//           rather than kept in VGPRs);
+//   Row   — per row: an array of RPW scalars;
+//   Col   — per column: an array of EPL (input) or a lazy expression;
+//   Scalar— a constant or kernel argument.
 // ======================================================================
 enum class Sp { Full, Row, Col, Scalar };
 
@@ -746,15 +752,34 @@ struct RowEmitter {
   Analysis &A;
   const LowerOptions &opt;
   std::ostringstream pre, body;
-  std::map<const Value *, std::string> name;
-  std::map<const Value *, Sp> sp;
-  std::map<const Value *, Elem> elemOf;
+  struct V {
+    Sp sp;
+    std::string name;
+    bool lazy = false;     // Full/Col: `name(e, ex)` instead of `name[e]`
+    bool fast = false;     // evaluation may raise hf_bad (fast-path ops inside)
+    bool integral = false; // holds integral values (or inf/NaN) only
+    bool guarded = false;  // non-NaN in fast mode (a NaN raises the Guard)
+    bool ranged = false;   // known to lie in [lo, hi] (or be NaN)
+    double lo = 0, hi = 0;
+    // set when the value is min/max(x, constant) of a guarded x
+    std::string clampX;
+    bool clampIsMin = false;
+    double clampC = 0;
+    // set when the value is an invariant-divisor division a / b (lazy)
+    std::string divA, divB, divR;
+  };
+  std::map<const Value *, V> val;
+  std::vector<std::string> arrays; // loaded element/column input arrays
+  std::vector<std::string> prefetchStmts; // chunk loads issued inside the serial chain
+  static constexpr int LOOKAHEAD = 2;   // LDS chunks of loads in flight per CU
+  std::map<std::string, std::set<std::string>> lazyDeps; // lazy value -> input arrays it reads
   std::set<const Value *> orderedReduce;
   int tmp = 0;
-  int nred = 0;       // LDS slots for tree reductions
+  int nred = 0; // LDS slots (per row of a row group) for tree reductions
   bool needOrdered = false;
+  bool progressive = false; // Full inputs streamed in by the first (serial) reduction
   int64_t R = 1, C = 1;
-  int TR = 64, RB = 1, VEC = 4, EPL = 4, CH = 0;
+  int TR = 64, RB = 1, RPW = 1, VEC = 4, EPL = 4, CH = 0;
   bool masked = false;
 
   RowEmitter(Analysis &a, const LowerOptions &o) : A(a), opt(o) {}
@@ -766,29 +791,68 @@ struct RowEmitter {
     return Sp::Scalar;
   }
   std::string fresh() { return "v" + std::to_string(tmp++); }
-  bool isArr(Sp s) const { return s == Sp::Full || s == Sp::Col; }
 
-  // expression of value v at element e (inside an element loop) or as scalar
-  std::string at(const Value *v, const std::string &e) {
-    auto it = name.find(v);
-    if (it == name.end()) throw CompileError("internal: value " + v->name + " not materialised");
-    return isArr(sp.at(v)) ? it->second + "[" + e + "]" : it->second;
+  // value of v at full element index e (0 <= e < RPW*EPL); `ex` names the
+  // exactness switch (hf::kFast{} / hf::kExact{} or a lambda's `ex`)
+  std::string at(const Value *v, const std::string &e, const std::string &ex = "ex") const {
+    const V &x = val.at(v);
+    switch (x.sp) {
+    case Sp::Full: return x.lazy ? x.name + "(" + e + ", " + ex + ")" : x.name + "[" + e + "]";
+    case Sp::Col: return x.lazy ? x.name + "(" + e + ", " + ex + ")" : x.name + "[(" + e + ") % EPL]";
+    case Sp::Row: return x.name + "[(" + e + ") / EPL]";
+    default: return x.name;
+    }
+  }
+  bool isFast(const Value *v) const { return val.at(v).lazy && val.at(v).fast; }
+  // an element expression written for a lambda (`ex`) evaluated in a loop
+  static std::string replaceEx(const std::string &expr, const std::string &with) {
+    std::string out;
+    for (size_t i = 0; i < expr.size();) {
+      bool word = expr.compare(i, 2, "ex") == 0 && (i == 0 || !(std::isalnum((unsigned char)expr[i - 1]) || expr[i - 1] == '_')) &&
+                  (i + 2 >= expr.size() || !(std::isalnum((unsigned char)expr[i + 2]) || expr[i + 2] == '_'));
+      if (word) { out += with; i += 2; }
+      else out += expr[i++];
+    }
+    return out;
+  }
+  // value of a Row/Scalar value for row rr of the group
+  std::string atRow(const Value *v, const std::string &rr) const {
+    const V &x = val.at(v);
+    if (x.sp == Sp::Row) return x.name + "[" + rr + "]";
+    if (x.sp == Sp::Scalar) return x.name;
+    throw CompileError("internal: per-row access to an element value");
   }
 
   std::string colExpr(const std::string &e) const {
-    return "((int64_t)((" + e + ") / VEC) * (TR * VEC) + lt * VEC + (" + e + ") % VEC)";
+    return "((int64_t)(((" + e + ") % EPL) / VEC) * (TR * VEC) + lt * VEC + (" + e + ") % VEC)";
   }
 
-  // Values that must be computed with a serial-order fp32 sum: sums whose
-  // result reaches an integer-typed group output (bit-exact outputs depend on
-  // the summation order of the reference's serial loop).
+  int uses(const Value *v) const {
+    int n = 0;
+    for (const Op *u : v->users) {
+      for (auto *i : u->ins) n += i == v;
+      for (auto *i : u->operands) n += i == v;
+    }
+    for (auto *r : A.f->returns) n += r == v;
+    return n;
+  }
+
+  static bool expensive(const Op *op) {
+    std::string fn = op->attr("fun");
+    static const std::set<std::string> costly = {"exp", "exp2", "log", "log2", "log10", "log1p", "expm1", "tanh",
+                                                 "sin", "cos", "erf", "powf", "sqrt", "rsqrt", "div", "rec",
+                                                 "reciprocal", "mod"};
+    return costly.count(fn) || op->name == "arith.divf" || op->name == "linalg.div";
+  }
+
+  // Sums whose result reaches an integer-typed group output are folded in the
+  // reference's serial order (bit-exact integer outputs depend on it).
   void markOrdered() {
     Func &f = *A.f;
     std::set<const Value *> intOut;
     for (auto *r : f.returns) if (isInt(r->type.elem)) intOut.insert(r);
     for (Op *op : f.ops) {
-      if (op->name != "linalg.reduce") continue;
-      if (op->combiner != "arith.addf") continue;
+      if (op->name != "linalg.reduce" || op->combiner != "arith.addf") continue;
       bool reaches = opt.orderedFloatSums;
       std::vector<const Value *> stack(op->results.begin(), op->results.end());
       std::set<const Value *> seen;
@@ -803,122 +867,263 @@ struct RowEmitter {
       if (reaches) orderedReduce.insert(op->results[0]);
     }
     needOrdered = !orderedReduce.empty();
+    // progressive loading is valid only when the serial chain is the first
+    // consumer that needs whole rows (no earlier reduction)
+    for (Op *op : f.ops)
+      if (op->name == "linalg.reduce") {
+        progressive = orderedReduce.count(op->results[0]) != 0;
+        break;
+      }
   }
 
   void chooseSchedule() {
     if (A.D.size() == 2) { R = A.D[0]; C = A.D[1]; }
     else if (A.D.size() == 1) { R = 1; C = A.D[0]; }
     else throw CompileError("row programs support rank-1 and rank-2 groups");
+    // vector width from the tensors that travel through HBM
     int maxBytes = 1;
-    for (auto &kv : A.map)
-      if (spaceOfMap(kv.second) == Sp::Full || spaceOfMap(kv.second) == Sp::Col)
-        maxBytes = std::max(maxBytes, elemBytes(kv.first->type.elem));
+    auto consider = [&](const Value *v) {
+      if (!v->type.tensor || !A.map.count(v)) return;
+      Sp s = spaceOfMap(A.map.at(v));
+      if (s == Sp::Full || s == Sp::Col) maxBytes = std::max(maxBytes, elemBytes(v->type.elem));
+    };
+    for (auto *a : A.f->args) consider(a);
+    for (auto *r : A.f->returns) consider(r);
     VEC = std::max(1, 16 / maxBytes);
     if (VEC > 8) VEC = 8;
     while (VEC > 1 && C % VEC) VEC /= 2;
-    // threads per row: aim for 8-32 elements per lane
-    int64_t perLaneTarget = VEC * 4;
-    int tr = 64;
-    while (tr < 1024 && (int64_t)tr * perLaneTarget < C) tr *= 2;
     if (needOrdered) {
+      // one wave per row group, 4 rows each, 8 waves: 32 rows per block with
+      // a single serial chain lane per row in wave 0 (2 waves per SIMD leave
+      // 256 VGPRs per lane for the resident rows)
       TR = 64;
       RB = 8;
+      RPW = 4;
     } else {
+      int64_t perLaneTarget = VEC * 4;
+      int tr = 64;
+      while (tr < 1024 && (int64_t)tr * perLaneTarget < C) tr *= 2;
       TR = tr;
       RB = std::max(1, 256 / TR);
-      if (R < RB) RB = (int)std::max<int64_t>(1, R);
+      RPW = 1;
     }
     int64_t span = (int64_t)TR * VEC;
     int64_t nch = (C + span - 1) / span;
     EPL = (int)(nch * VEC);
     masked = (C % span) != 0;
-    if (EPL > 256) throw CompileError("row of " + std::to_string(C) + " elements does not fit one row group (max " + std::to_string(1024 * 256) + ")");
+    if (EPL * RPW > 256)
+      throw CompileError("row of " + std::to_string(C) + " elements does not fit one row group");
     if (needOrdered) {
-      // LDS chunk for the serial chain: a whole number of vector-chunks
-      int jpc = std::max(1, (int)(1024 / span));
+      int jpc = std::max<int64_t>(1, 512 / span);
       if (jpc > nch) jpc = (int)nch;
-      while (nch % jpc) --jpc;
       CH = (int)(jpc * span);
+      // two LDS buffers of RB*RPW rows must fit next to the other stages
+      while ((int64_t)2 * RB * RPW * (CH + 4) * 4 > 140 * 1024 && jpc > 1) { --jpc; CH = (int)(jpc * span); }
+      if ((int64_t)2 * RB * RPW * (CH + 4) * 4 > 140 * 1024)
+        throw CompileError("row too wide for the serial-order staging buffer");
     }
   }
+
+  std::string rowExpr(const std::string &rr) const { return "row[" + rr + "]"; }
 
   void loadInput(const Value *a) {
     int i = a->argIdx;
     Sp s = spaceOfMap(A.map.at(a));
     std::string T = ctype(a->type.elem), M = mtype(a->type.elem);
     std::string nm = "in" + std::to_string(i);
-    name[a] = nm;
-    sp[a] = s;
-    if (s == Sp::Full || s == Sp::Col) {
-      std::string base = s == Sp::Full ? "(const " + M + "*)p" + std::to_string(i) + " + row * C" : "(const " + M + "*)p" + std::to_string(i);
-      pre << "  " << T << " " << nm << "[EPL];\n";
-      if (a->type.elem == Elem::I1) {
-        pre << "  { uint8_t t_[EPL]; hf::row_load<uint8_t, VEC, EPL / VEC, TR, MASKED>(" << base << ", lt, C, t_);\n"
-            << "    for (int e = 0; e < EPL; ++e) " << nm << "[e] = t_[e] != 0; }\n";
-      } else {
-        pre << "  hf::row_load<" << T << ", VEC, EPL / VEC, TR, MASKED>(" << base << ", lt, C, " << nm << ");\n";
-      }
+    val[a] = {s, nm, false};
+    std::string P = "(const " + M + "*)p" + std::to_string(i);
+    if ((s == Sp::Full || s == Sp::Col) && a->type.elem != Elem::I1) arrays.push_back(nm);
+    if (s == Sp::Full && progressive && a->type.elem != Elem::I1) {
+      // loaded progressively by the serial chain (LOOKAHEAD chunks ahead)
+      const int jpc = CH / (TR * VEC);
+      pre << "  " << M << " " << nm << "[RPW * EPL];\n"
+          << "  hf::rows_load_range<" << M << ", VEC, EPL / VEC, TR, RPW, MASKED>(" << P << ", row, C, lt, " << nm << ", 0, "
+          << LOOKAHEAD * jpc << ");\n";
+      prefetchStmts.push_back("hf::rows_load_range<" + M + ", VEC, EPL / VEC, TR, RPW, MASKED>(" + P + ", row, C, lt, " + nm +
+                              ", kk * " + std::to_string(jpc) + ", kk * " + std::to_string(jpc) + " + " + std::to_string(jpc) + ");");
+    } else if (s == Sp::Full) {
+      pre << "  " << M << " " << nm << (a->type.elem == Elem::I1 ? "_raw" : "") << "[RPW * EPL];\n"
+          << "  hf::rows_load<" << M << ", VEC, EPL / VEC, TR, RPW, MASKED>(" << P << ", row, C, lt, "
+          << nm << (a->type.elem == Elem::I1 ? "_raw" : "") << ");\n";
+      if (a->type.elem == Elem::I1)
+        pre << "  bool " << nm << "[RPW * EPL];\n  for (int e = 0; e < RPW * EPL; ++e) " << nm << "[e] = " << nm << "_raw[e] != 0;\n";
+    } else if (s == Sp::Col) {
+      pre << "  " << M << " " << nm << (a->type.elem == Elem::I1 ? "_raw" : "") << "[EPL];\n"
+          << "  hf::row_load<" << M << ", VEC, EPL / VEC, TR, MASKED>(" << P << ", lt, C, " << nm
+          << (a->type.elem == Elem::I1 ? "_raw" : "") << ");\n";
+      if (a->type.elem == Elem::I1)
+        pre << "  bool " << nm << "[EPL];\n  for (int e = 0; e < EPL; ++e) " << nm << "[e] = " << nm << "_raw[e] != 0;\n";
     } else if (s == Sp::Row) {
-      pre << "  const " << T << " " << nm << " = ((const " << M << "*)p" << i << ")[row];\n";
+      pre << "  " << T << " " << nm << "[RPW];\n"
+          << "#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) " << nm << "[rr] = (" << P << ")[row[rr]];\n";
     } else {
-      pre << "  const " << T << " " << nm << " = ((const " << M << "*)p" << i << ")[0];\n";
+      pre << "  const " << T << " " << nm << " = (" << P << ")[0];\n";
     }
   }
 
   void bindScalar(const Value *v) {
-    if (v->isConst) { name[v] = constExpr(v, v->type.elem); sp[v] = Sp::Scalar; return; }
-    if (v->argIdx >= 0) { name[v] = scalarArgExpr(A, v->argIdx); sp[v] = Sp::Scalar; return; }
+    if (v->isConst) { val[v] = {Sp::Scalar, constExpr(v, v->type.elem)}; return; }
+    if (v->argIdx >= 0) { val[v] = {Sp::Scalar, scalarArgExpr(A, v->argIdx)}; return; }
     throw CompileError("non-constant scalar " + v->name + " in a tensor group");
   }
 
   void ensure(const Value *v) {
-    if (name.count(v)) return;
+    if (val.count(v)) return;
     if (!v->type.tensor) { bindScalar(v); return; }
     if (v->argIdx >= 0) { loadInput(v); return; }
-    if (v->isConst) { name[v] = constExpr(v, v->type.elem); sp[v] = Sp::Scalar; return; }
+    if (v->isConst) { val[v] = {Sp::Scalar, constExpr(v, v->type.elem)}; return; }
     throw CompileError("internal: value " + v->name + " used before definition");
+  }
+
+  // division of an element value by a per-row (or constant) f32 divisor:
+  // reciprocal once per row (consumed by hf::rint_div for a rounding consumer)
+  bool isInvariantDiv(const Op *op, const std::vector<const Value *> &opsv, Elem U) const {
+    bool div = (op->name == "linalg.elemwise_binary" && op->attr("fun") == "div") || op->name == "arith.divf" ||
+               op->name == "linalg.div";
+    if (!div || U != Elem::F32 || opsv.size() != 2) return false;
+    if (opsv[0]->type.elem != Elem::F32 || opsv[1]->type.elem != Elem::F32) return false;
+    Sp s1 = val.at(opsv[1]).sp, s0 = val.at(opsv[0]).sp;
+    return (s1 == Sp::Row || s1 == Sp::Scalar) && (s0 == Sp::Full || s0 == Sp::Col);
   }
 
   void emitElementwise(const Op *op) {
     std::vector<const Value *> opsv;
     for (auto *v : op->ins) opsv.push_back(v);
     for (auto *v : op->operands) opsv.push_back(v);
-    Sp out = Sp::Scalar;
-    bool anyRow = false, anyCol = false;
+    bool anyFull = false, anyRow = false, anyCol = false;
     for (auto *v : opsv) {
       ensure(v);
-      Sp s = sp[v];
-      if (s == Sp::Full) out = Sp::Full;
-      if (s == Sp::Row) anyRow = true;
-      if (s == Sp::Col) anyCol = true;
+      Sp s = val[v].sp;
+      anyFull |= s == Sp::Full;
+      anyRow |= s == Sp::Row;
+      anyCol |= s == Sp::Col;
     }
-    if (out != Sp::Full) {
-      if (anyRow && anyCol) out = Sp::Full;
-      else if (anyRow) out = Sp::Row;
-      else if (anyCol) out = Sp::Col;
-    }
+    Sp out = anyFull || (anyRow && anyCol) ? Sp::Full : anyCol ? Sp::Col : anyRow ? Sp::Row : Sp::Scalar;
     const Value *res = op->results[0];
-    if (A.map.count(res)) {
-      Sp ms = spaceOfMap(A.map.at(res));
-      if (ms == Sp::Full && out != Sp::Full) out = Sp::Full; // broadcast by destination
-    }
+    if (A.map.count(res) && spaceOfMap(A.map.at(res)) == Sp::Full) out = Sp::Full;
     Elem U = res->type.elem;
     std::vector<Elem> at_;
     for (auto *v : opsv) at_.push_back(v->type.elem);
     std::string nm = fresh();
-    name[res] = nm;
-    sp[res] = out;
-    if (isArr(out)) {
-      std::vector<std::string> args;
-      for (auto *v : opsv) args.push_back(at(v, "e"));
-      body << "  " << ctype(U) << " " << nm << "[EPL];\n"
-           << "#pragma unroll\n  for (int e = 0; e < EPL; ++e) " << nm << "[e] = "
-           << elementExpr(op, args, at_, U) << ";\n";
-    } else {
-      std::vector<std::string> args;
-      for (auto *v : opsv) args.push_back(at(v, ""));
-      body << "  const " << ctype(U) << " " << nm << " = " << elementExpr(op, args, at_, U) << ";\n";
+    std::string T = ctype(U);
+    if (out == Sp::Full || out == Sp::Col) {
+      std::string expr;
+      bool fast = false, integral = false;
+      V nv{out, nm, true};
+      for (auto *v : opsv) fast |= val[v].fast;
+      const std::string fn = op->attr("fun");
+      if (isInvariantDiv(op, opsv, U)) {
+        const Value *b = opsv[1];
+        std::string rn = nm + "_rcp";
+        std::string bAt, rAt;
+        if (val[b].sp == Sp::Row) {
+          body << "  float " << rn << "[RPW];\n#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) { " << rn << "[rr] = 1.0f / "
+               << atRow(b, "rr") << "; if constexpr (!EXM::value) hf_g.divisor(" << rn << "[rr]); }\n";
+          bAt = at(b, "e");
+          rAt = rn + "[(e) / EPL]";
+        } else {
+          body << "  const float " << rn << " = 1.0f / " << val[b].name << ";\n  if constexpr (!EXM::value) hf_g.divisor(" << rn << ");\n";
+          bAt = val[b].name;
+          rAt = rn;
+        }
+        // the quotient itself is the IEEE division; the reciprocal serves a
+        // consuming nearbyint (hf::rint_div)
+        expr = "(" + at(opsv[0], "e") + " / " + bAt + ")";
+        nv.divA = at(opsv[0], "e");
+        nv.divB = bAt;
+        nv.divR = rAt;
+      } else if ((op->name == "hfusion.elemwise_unary" && fn == "nearbyint") && U == Elem::F32 && opsv[0]->type.elem == Elem::F32 &&
+                 val[opsv[0]].lazy && !val[opsv[0]].divA.empty() && uses(opsv[0]) == 1) {
+        // rint of a division by a per-row divisor (dynamic quantisation)
+        const V &d = val[opsv[0]];
+        expr = "hf::rint_div(" + d.divA + ", " + d.divB + ", " + d.divR + ", hf_g, ex)";
+        fast = true;
+        integral = true;
+        nv.guarded = true;
+      } else if ((fn == "maxf" || fn == "minf") && U == Elem::F32 && opsv.size() == 2 && opsv[1]->isConst &&
+                 val[opsv[0]].lazy && val[opsv[0]].guarded) {
+        // clamp of a guarded (non-NaN in fast mode) value: min/max pairs fold
+        // into one v_med3_f32
+        const V &x = val[opsv[0]];
+        double c = opsv[1]->fconst;
+        bool isMin = fn == "minf";
+        if (!x.clampX.empty() && x.clampIsMin != isMin && uses(opsv[0]) == 1 &&
+            (isMin ? x.clampC <= c : c <= x.clampC)) {
+          double lo = isMin ? x.clampC : c, hi = isMin ? c : x.clampC;
+          expr = "(ex.value ? " + elementExpr(op, {at(opsv[0], "e"), val[opsv[1]].name}, at_, U) + " : __builtin_amdgcn_fmed3f(" +
+                 x.clampX + ", " + floatLit((float)lo) + ", " + floatLit((float)hi) + "))";
+          nv.ranged = true;
+          nv.lo = lo;
+          nv.hi = hi;
+        } else {
+          expr = elementExpr(op, {at(opsv[0], "e"), val[opsv[1]].name}, at_, U);
+          nv.clampX = at(opsv[0], "e");
+          nv.clampIsMin = isMin;
+          nv.clampC = c;
+        }
+        fast = true;
+        integral = x.integral && std::floor(c) == c;
+        nv.guarded = true;
+      } else {
+        std::vector<std::string> args;
+        for (auto *v : opsv) args.push_back(at(v, "e"));
+        if (op->name == "hfusion.cast" && U != Elem::I1 && isInt(U) && opsv[0]->type.elem == Elem::F32 && val[opsv[0]].integral) {
+          bool sat = op->attr("enable_saturate") == "true";
+          const V &x = val[opsv[0]];
+          double tlo = -std::ldexp(1.0, elemBits(U) - 1), thi = std::ldexp(1.0, elemBits(U) - 1) - 1;
+          if (x.ranged && x.lo >= tlo && x.hi <= thi && elemBits(U) <= 32)
+            // integral and inside the target range: one convert (NaN -> 0)
+            expr = "(" + ctype(U) + ")(int32_t)(" + args[0] + ")";
+          else
+            expr = "hf::integral_to_int<" + ctype(U) + ", " + (sat ? "true" : "false") + ">(" + args[0] + ")";
+        } else {
+          expr = elementExpr(op, args, at_, U);
+        }
+        // integral-valued results: rounding functions, and min/max/select of
+        // integral values and integral constants
+        auto integ = [&](const Value *v) {
+          if (v->isConst) return std::floor(v->fconst) == v->fconst;
+          return val[v].integral;
+        };
+        if (fn == "nearbyint" || fn == "floor" || fn == "ceil" || fn == "round" || fn == "trunc") integral = true;
+        if ((fn == "maxf" || fn == "minf" || fn == "maxnumf" || fn == "minnumf") && integ(opsv[0]) && integ(opsv[1])) integral = true;
+        if (op->name == "hfusion.select" && integ(opsv[1]) && integ(opsv[2])) integral = true;
+      }
+      nv.fast = fast;
+      nv.integral = integral;
+      bool materialise = expensive(op) && uses(res) > 1;
+      if (materialise) {
+        std::string n = out == Sp::Full ? "RPW * EPL" : "EPL";
+        body << "  " << T << " " << nm << "[" << n << "];\n#pragma unroll\n  for (int e = 0; e < " << n << "; ++e) " << nm
+             << "[e] = " << expr << ";\n";
+        val[res] = {out, nm, false};
+        val[res].integral = integral;
+      } else {
+        body << "  auto " << nm << " = [&](int e, auto ex) -> " << T << " { return " << expr << "; };\n";
+        val[res] = nv;
+        std::set<std::string> deps;
+        for (auto *v : opsv) {
+          const V &x = val[v];
+          if (x.lazy) deps.insert(lazyDeps[x.name].begin(), lazyDeps[x.name].end());
+          else if (std::find(arrays.begin(), arrays.end(), x.name) != arrays.end()) deps.insert(x.name);
+        }
+        lazyDeps[nm] = deps;
+      }
+      return;
     }
+    if (out == Sp::Row) {
+      std::vector<std::string> args;
+      for (auto *v : opsv) args.push_back(atRow(v, "rr"));
+      body << "  " << T << " " << nm << "[RPW];\n#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) " << nm
+           << "[rr] = " << elementExpr(op, args, at_, U) << ";\n";
+      val[res] = {Sp::Row, nm};
+      return;
+    }
+    std::vector<std::string> args;
+    for (auto *v : opsv) args.push_back(val[v].name);
+    body << "  const " << T << " " << nm << " = " << elementExpr(op, args, at_, U) << ";\n";
+    val[res] = {Sp::Scalar, nm};
   }
 
   void emitReduce(const Op *op) {
@@ -927,76 +1132,85 @@ struct RowEmitter {
     if (op->dims.size() != 1 || op->dims[0] != last) unsupported(op, "reduction over a non-last axis");
     const Value *x = op->ins[0];
     ensure(x);
-    if (sp[x] != Sp::Full) unsupported(op, "reduction of a broadcast value");
+    if (val[x].sp != Sp::Full) unsupported(op, "reduction of a broadcast value");
     const Value *init = op->outs[0];
-    // init: a fill of a constant, or a row tensor argument
-    std::string initExpr;
     Elem t = x->type.elem;
+    Combiner cb = combinerFor(op, op->combiner, t);
+    std::string T = ctype(t);
+    // init per row: a fill of a constant/scalar, a row tensor argument, or an
+    // uninitialised tensor.empty (the combiner's identity)
+    std::string initAt;
     if (init->def && init->def->name == "linalg.fill") {
       const Value *c = init->def->ins[0];
-      if (!c->isConst) { ensure(c); initExpr = at(c, ""); }
-      else initExpr = constExpr(c, t);
+      ensure(c);
+      initAt = c->isConst ? constExpr(c, t) : val[c].name;
     } else if (init->argIdx >= 0) {
       ensure(init);
-      initExpr = at(init, "");
+      initAt = atRow(init, "rr");
     } else if (init->isConst) {
-      initExpr = constExpr(init, t);
+      initAt = constExpr(init, t);
     } else if (init->def && init->def->name == "tensor.empty") {
-      initExpr = "EMPTY"; // uninitialised destination: the combiner's identity
+      initAt = cb.identity;
     } else {
-      unsupported(op, "reduction init must be a linalg.fill or an argument");
+      unsupported(op, "reduction init must be a linalg.fill, an argument or tensor.empty");
     }
-    Combiner cb = combinerFor(op, op->combiner, t);
-    if (initExpr == "EMPTY") initExpr = cb.identity;
     const Value *res = op->results[0];
     std::string nm = fresh();
-    name[res] = nm;
-    sp[res] = (A.D.size() == 1) ? Sp::Scalar : Sp::Row;
-    std::string xs = name[x];
+    val[res] = {A.D.size() == 1 ? Sp::Row : Sp::Row, nm};
+    std::string xe = at(x, "e");
     if (orderedReduce.count(res)) {
-      body << "  const float " << nm << " = hf::row_sum_ordered<TR, RB, VEC, EPL, CHUNK>(" << xs << ", " << initExpr
-           << ", lds_chain, lds_bcast, rloc, lt, C);\n";
+      body << "  float " << nm << "_init[RPW];\n#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) " << nm << "_init[rr] = " << initAt
+           << ";\n  float " << nm << "[RPW];\n  hf::row_sum_ordered<TR, RB, RPW, VEC, EPL, CHUNK, " << LOOKAHEAD
+           << ">([&](int e) -> float { return " << xe << "; }, [&](int kk) {";
+      for (auto &st : prefetchStmts) body << " " << st;
+      prefetchStmts.clear(); // later chains find every chunk loaded
+      body << " }, " << nm << "_init, " << nm << ", lds_chain, lds_bcast, rloc, lt, C);\n";
+      body << "@@LAUNDER@@\n";
       return;
     }
-    std::string T = ctype(t);
     std::string p = nm + "_p";
-    body << "  " << T << " " << p << " = " << cb.identity << ";\n";
-    std::string inner = "#pragma unroll\n  for (int e = 0; e < EPL; ++e) ";
-    if (masked) inner += "if (" + colExpr("e") + " < C) ";
-    body << inner << p << " = " << subst(cb.expr, xs + "[e]", p) << ";\n";
+    body << "  " << T << " " << p << "[RPW];\n#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) " << p << "[rr] = " << cb.identity << ";\n";
+    body << "#pragma unroll\n  for (int e = 0; e < RPW * EPL; ++e) ";
+    if (masked) body << "if (" << colExpr("e") << " < C) ";
+    body << p << "[e / EPL] = " << subst(cb.expr, xe, p + "[e / EPL]") << ";\n";
     int slot = nred++;
-    body << "  " << p << " = hf::row_allreduce<TR, RB>(" << p << ", [](" << T << " A, " << T << " B) { return "
-         << cb.expr << "; }, (" << T << "*)(lds_red + " << slot << " * RB * WPR), rloc, lt);\n";
-    body << "  const " << T << " " << nm << " = " << subst(cb.expr, p, initExpr) << ";\n";
+    body << "#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) " << p << "[rr] = hf::row_allreduce<TR, RB>(" << p << "[rr], [](" << T
+         << " A, " << T << " B) { return " << cb.expr << "; }, (" << T << "*)(lds_red + (" << slot << " * RPW + rr) * RB * WPR), rloc, lt);\n";
+    body << "  " << T << " " << nm << "[RPW];\n#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) " << nm << "[rr] = "
+         << subst(cb.expr, p + "[rr]", initAt) << ";\n";
+    body << "@@LAUNDER@@\n";
   }
 
   void emitStore(size_t i) {
     const Value *v = A.f->returns[i];
-    if (v->argIdx >= 0 && A.resultTied[i] == v->argIdx) return; // returned input: nothing to write
+    if (v->argIdx >= 0 && A.resultTied[i] == v->argIdx) return;
     ensure(v);
     Elem e = v->type.elem;
     std::string ptr = resultPtr(A, i);
     std::string M = mtype(e);
-    Sp s = sp[v];
+    Sp s = val[v].sp;
     Sp ms = A.map.count(v) ? spaceOfMap(A.map.at(v)) : s;
     if (ms == Sp::Full) {
-      std::string src = name[v];
-      if (s != Sp::Full) {
-        src = fresh();
-        body << "  " << ctype(e) << " " << src << "[EPL];\n  for (int e = 0; e < EPL; ++e) " << src << "[e] = " << at(v, "e") << ";\n";
-      }
-      if (e == Elem::I1) {
-        std::string t = fresh();
-        body << "  uint8_t " << t << "[EPL];\n  for (int e = 0; e < EPL; ++e) " << t << "[e] = " << src << "[e];\n";
-        src = t;
-      }
-      body << "  if (row_ok) hf::row_store<" << M << ", VEC, EPL / VEC, TR, MASKED>((" << M << "*)" << ptr
-           << " + row * C, lt, C, " << src << ");\n";
+      // chunk by chunk: VEC values are computed, then stored with one access.
+      // Rows past R were clamped to row R-1 and recompute its exact values, so
+      // the store needs no (divergent) row guard.
+      auto storeLoop = [&](const std::string &ex, const std::string &ind) {
+        body << ind << "#pragma unroll\n" << ind << "for (int rr = 0; rr < RPW; ++rr)\n#pragma unroll\n" << ind
+             << "  for (int j = 0; j < EPL / VEC; ++j) {\n" << ind << "    " << M << " st_[VEC];\n#pragma unroll\n" << ind
+             << "    for (int v = 0; v < VEC; ++v) st_[v] = (" << M << ")(" << at(v, "rr * EPL + j * VEC + v", ex) << ");\n"
+             << ind << "    hf::row_store_chunk<" << M << ", VEC, TR, MASKED>((" << M << "*)" << ptr
+             << " + row[rr] * C, lt, C, j, st_);\n" << ind
+             << "    __builtin_amdgcn_sched_barrier(0); // bound the live range to one chunk\n" << ind << "  }\n";
+      };
+      storeLoop("ex", "  ");
     } else if (ms == Sp::Row || (ms == Sp::Scalar && A.D.size() == 1)) {
-      body << "  if (row_ok && lt == 0) ((" << M << "*)" << ptr << ")[" << (ms == Sp::Row ? "row" : "0") << "] = " << at(v, "0") << ";\n";
+      std::string idx = ms == Sp::Row ? "row[rr]" : "0";
+      body << "#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) if (row_ok[rr] && lt == 0) ((" << M << "*)" << ptr << ")[" << idx
+           << "] = " << (s == Sp::Scalar ? val[v].name : atRow(v, "rr")) << ";\n";
     } else if (ms == Sp::Col) {
-      body << "  if (blockIdx.x == 0 && rloc == 0) hf::row_store<" << M << ", VEC, EPL / VEC, TR, MASKED>((" << M << "*)" << ptr
-           << ", lt, C, " << name[v] << ");\n";
+      body << "  if (blockIdx.x == 0 && rloc == 0) {\n    " << M << " st_[EPL];\n    for (int ee = 0; ee < EPL; ++ee) st_[ee] = (" << M
+           << ")(" << at(v, "ee") << ");\n    hf::row_store<" << M << ", VEC, EPL / VEC, TR, MASKED>((" << M << "*)" << ptr
+           << ", lt, C, st_);\n  }\n";
     } else {
       throw CompileError("cannot store a scalar result");
     }
@@ -1008,20 +1222,18 @@ struct RowEmitter {
     Func &f = *A.f;
     for (Op *op : f.ops) {
       const std::string &n = op->name;
-      if (n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" || n.rfind("arith.", 0) == 0 && !op->results.empty() && !op->results[0]->type.tensor) {
+      if (n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" ||
+          (n.rfind("arith.", 0) == 0 && !op->results.empty() && !op->results[0]->type.tensor))
         continue;
-      }
       if (n == "linalg.fill") {
         const Value *c = op->ins[0];
         ensure(c);
-        name[op->results[0]] = name[c];
-        sp[op->results[0]] = Sp::Scalar;
+        val[op->results[0]] = {Sp::Scalar, c->isConst ? constExpr(c, op->results[0]->type.elem) : val[c].name};
         continue;
       }
       if (n == "linalg.broadcast") {
         ensure(op->ins[0]);
-        name[op->results[0]] = name[op->ins[0]];
-        sp[op->results[0]] = sp[op->ins[0]];
+        val[op->results[0]] = val[op->ins[0]];
         continue;
       }
       if (n == "linalg.reduce") { emitReduce(op); continue; }
@@ -1035,29 +1247,92 @@ struct RowEmitter {
     p.kind = kind;
     p.variant = needOrdered ? "row-resident, serial-order fp32 sum" : "row-resident";
     int block = TR * RB;
-    int64_t grid = (R + RB - 1) / RB;
+    int64_t rowsPerBlock = (int64_t)RB * RPW;
+    int64_t grid = (R + rowsPerBlock - 1) / rowsPerBlock;
     std::ostringstream k;
-    k << "extern \"C\" __global__ __launch_bounds__(" << block << ") void " << kname << "("
-      << kernelParamList(A, p.kargs, false) << ") {\n"
-      << "  constexpr int TR = " << TR << ", RB = " << RB << ", VEC = " << VEC << ", EPL = " << EPL
+    std::string params = kernelParamList(A, p.kargs, false);
+    std::string argNames;
+    for (size_t i = 0; i < A.params.size(); ++i) argNames += (A.params[i].role == "scalar" ? "s" : "p") + std::to_string(i) + ", ";
+    for (size_t i = 0; i < A.results.size(); ++i)
+      if (A.resultTied[i] < 0) argNames += "r" + std::to_string(i) + ", ";
+    std::string ldsParams = "uint64_t* lds_red, float* lds_chain, float* lds_bcast";
+    std::string ldsArgs = "lds_red_, lds_chain_, lds_bcast_";
+    // the row program, instantiated for a fast (kFast) and an exact (kExact) mode
+    k << "template <typename EXM>\n__device__ __forceinline__ bool " << kname << "_body(" << params << ", " << ldsParams << ") {\n"
+      << "  const EXM ex{};\n  (void)ex; (void)lds_red; (void)lds_chain; (void)lds_bcast;\n"
+      << "  constexpr int TR = " << TR << ", RB = " << RB << ", RPW = " << RPW << ", VEC = " << VEC << ", EPL = " << EPL
       << ", WPR = " << std::max(1, TR / 64) << ";\n"
       << "  constexpr bool MASKED = " << (masked ? "true" : "false") << ";\n"
       << "  constexpr int64_t R = " << R << "ll, C = " << C << "ll;\n"
-      << "  (void)R;\n"
       << "  const int tid = threadIdx.x, rloc = tid / TR, lt = tid % TR;\n"
-      << "  const int64_t row_raw = (int64_t)blockIdx.x * RB + rloc;\n"
-      << "  const bool row_ok = row_raw < R;\n"
-      << "  const int64_t row = row_ok ? row_raw : (R - 1);\n"
-      << "  (void)row_ok; (void)lt;\n";
-    if (nred) k << "  __shared__ uint64_t lds_red_[" << nred << " * RB * WPR];\n  uint64_t* lds_red = lds_red_;\n";
-    if (needOrdered)
-      k << "  constexpr int CHUNK = " << CH << ";\n"
-        << "  __shared__ float lds_chain[RB * (CHUNK + 4)];\n  __shared__ float lds_bcast[RB];\n";
-    k << pre.str() << body.str() << "}\n";
+      << "  int64_t row[RPW];\n  bool row_ok[RPW];\n"
+      << "#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) {\n"
+      << "    const int64_t r_ = ((int64_t)blockIdx.x * RB + rloc) * RPW + rr;\n"
+      << "    row_ok[rr] = r_ < R;\n    row[rr] = r_ < R ? r_ : R - 1;\n  }\n"
+      << "  (void)row_ok; (void)lt;\n"
+      << "  hf::Guard hf_g; // evidence that every fast-path element is exact\n";
+    if (needOrdered) k << "  constexpr int CHUNK = " << CH << ";\n";
+    k << pre.str() << resolveLaunder(body.str()) << "  return hf_g.bad();\n}\n";
+    // LDS of the kernel, shared by both instantiations
+    int redWords = std::max(1, nred * RPW * RB * std::max(1, TR / 64));
+    int chainWords = needOrdered ? 2 * RB * RPW * (CH + 4) : 1;
+    int bcastWords = needOrdered ? RB * RPW : 1;
+    bool anyFast = false;
+    for (auto &kv : val) anyFast |= kv.second.fast;
+    if (anyFast)
+      k << "__device__ __attribute__((noinline)) void " << kname << "_exact(" << params << ", " << ldsParams << ") {\n"
+        << "  " << kname << "_body<hf::kExact>(" << argNames << "lds_red, lds_chain, lds_bcast);\n}\n";
+    // row programs without a serial chain: ask for two resident blocks per CU
+    // so that one block's loads overlap the other's arithmetic
+    std::string occ;
+    if (!needOrdered && block >= 256)
+      occ = " __attribute__((amdgpu_waves_per_eu(" + std::to_string(std::min(8, block / 128)) + ")))";
+    k << "extern \"C\" __global__ __launch_bounds__(" << block << ")" << occ << " void " << kname << "(" << params << ") {\n"
+      << "  __shared__ uint64_t lds_red_[" << redWords << "];\n"
+      << "  __shared__ __attribute__((aligned(16))) float lds_chain_[" << chainWords << "];\n"
+      << "  __shared__ float lds_bcast_[" << bcastWords << "];\n"
+      << "  const bool bad = " << kname << "_body<hf::kFast>(" << argNames << ldsArgs << ");\n";
+    if (anyFast)
+      k << "  // rare: some element's fast path could not vouch for its exact value;\n"
+        << "  // the whole block recomputes its rows with IEEE division\n"
+        << "  if (__syncthreads_or(bad)) " << kname << "_exact(" << argNames << ldsArgs << ");\n";
+    else
+      k << "  (void)bad;\n";
+    k << "}\n";
     p.source = k.str();
     p.grid[0] = (unsigned)grid;
     p.block[0] = (unsigned)block;
     return p;
+  }
+
+  // At each reduction boundary, launder the input arrays that are still read
+  // afterwards (and only those, so dead arrays are not kept alive).
+  std::string resolveLaunder(const std::string &b) const {
+    std::string out;
+    size_t pos = 0;
+    const std::string mark = "@@LAUNDER@@\n";
+    while (true) {
+      size_t m = b.find(mark, pos);
+      if (m == std::string::npos) { out += b.substr(pos); break; }
+      out += b.substr(pos, m - pos);
+      std::string rest = b.substr(m + mark.size());
+      auto mentions = [&](const std::string &id) {
+        for (size_t q = rest.find(id); q != std::string::npos; q = rest.find(id, q + 1)) {
+          char nx = q + id.size() < rest.size() ? rest[q + id.size()] : ' ';
+          char pv = q ? rest[q - 1] : ' ';
+          if (!std::isalnum((unsigned char)nx) && nx != '_' && !std::isalnum((unsigned char)pv) && pv != '_') return true;
+        }
+        return false;
+      };
+      for (auto &a : arrays) {
+        bool used = mentions(a);
+        for (auto &kv : lazyDeps)
+          if (!used && kv.second.count(a) && mentions(kv.first)) used = true;
+        if (used) out += "  hf::launder(" + a + ");\n";
+      }
+      pos = m + mark.size();
+    }
+    return out;
   }
 };
 

@@ -13,6 +13,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -27,12 +28,8 @@ __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 // ---------------------------------------------------------------- bf16/f16
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 
-// Round-to-nearest-even f32 -> bf16; NaN stays a quiet NaN of the same sign.
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = f2u(f);
-  uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  return (f != f) ? (uint16_t)((u >> 16) | 0x40u) : (uint16_t)r;
-}
+// Round-to-nearest-even f32 -> bf16 (gfx950 v_cvt_pk_bf16_f32); NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
@@ -118,9 +115,11 @@ template <typename T, int MODE, bool SAT> __device__ __forceinline__ T f32_to_in
     d = d < lo ? lo : (d > hi ? hi : d);
     return (T)(int64_t)d;
   } else {
-    if constexpr (sizeof(T) <= 4) {
-      // in-range values convert exactly; v_cvt_i32_f32 clamps otherwise
-      if (r >= -2147483648.0f && r < 2147483648.0f) return (T)(int32_t)r;
+    if constexpr (sizeof(T) == 1) {
+      // |r| >= 2^31 is a multiple of 256: its low byte is 0
+      return __builtin_fabsf(r) < 2147483648.0f ? (T)(int32_t)r : (T)0;
+    } else if constexpr (sizeof(T) <= 4) {
+      if (__builtin_expect(__builtin_fabsf(r) < 2147483648.0f, 1)) return (T)(int32_t)r;
       return (T)(int64_t)r;
     } else {
       return (T)(int64_t)r;
@@ -150,6 +149,86 @@ __device__ __forceinline__ float div(float a, float b) { return a / b; }
 __device__ __forceinline__ float rec(float a) { return 1.0f / a; }
 __device__ __forceinline__ float relu(float a) { return maximumf(0.0f, a); }
 __device__ __forceinline__ float rsqrt(float a) { return 1.0f / __builtin_sqrtf(a); }
+
+// exp(x) in fp32 from the hardware base-2 exponential: x*log2(e) is split into
+// t + e exactly (FMA residual plus the low part of log2(e)), 2^t comes from
+// v_exp_f32 and the factor 2^e ~ 1 + e*ln2 is applied with one FMA.  Results
+// below 2^-64 are computed as 2^(t+64) * 2^-64 (one rounding into the
+// denormal range).  Branch-free; error within a few ulp of the exact value.
+__device__ __forceinline__ float exp_f32(float x) {
+  const float t = x * 0x1.715476p+0f;
+  float e = __builtin_fmaf(x, 0x1.715476p+0f, -t);
+  e = __builtin_fmaf(x, 0x1.4ae0c0p-26f, e);
+  const bool tiny = t < -64.0f;
+  float r = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t);
+  const float c = __builtin_fmaf(r, e * 0x1.62e430p-1f, r);
+  // |t| >= 126: inf, 0, NaN or a denormal; the residual is not needed there
+  r = __builtin_fabsf(t) < 126.0f ? c : r;
+  return tiny ? r * 0x1p-64f : r;
+}
+
+// Exactness switch of the element functions below: kExact evaluates the
+// IEEE result directly; kFast takes the cheap path and records in a Guard when the
+// cheap path cannot vouch for the exact result, in which case the caller
+// re-evaluates that phase with kExact (rare: out-of-range magnitudes or
+// quotients within a rounding error of a half-integer).
+using kFast = std::integral_constant<bool, false>;
+using kExact = std::integral_constant<bool, true>;
+
+// Running evidence of the fast paths (plain arithmetic, issued in program
+// order): the largest quotient magnitude seen (NaN-propagating) and the
+// exponent range of the per-row reciprocals.
+struct Guard {
+  float qmax = 0.0f;
+  int emin = 0, emax = 0;
+  __device__ __forceinline__ bool bad() const { return !(qmax <= 0x1p+100f) || emin < -96 || emax > 40; }
+  // per-row divisor check: r = RN(1/b) must be a normal number with exponent
+  // in [-96, 40] (so |b| >= 2^-41 and the reciprocal is exact-rounded normal)
+  __device__ __forceinline__ void divisor(float r) {
+    const int er = __builtin_amdgcn_frexp_expf(r);
+    asm volatile("v_min3_i32 %0, %0, %2, %2\n\tv_max3_i32 %1, %1, %2, %2" : "+v"(emin), "+v"(emax) : "v"(er));
+  }
+};
+
+// rint(RN(a / b)) (round-half-even of the correctly rounded quotient) given
+// r = RN(1/b), computed once per row.  q0 = a*r, then two Markstein
+// corrections q_{i+1} = q_i + (a - b*q_i)*r with exact FMA residuals: after
+// the first q is faithful, the second yields RN(a/b) (Markstein's theorem for a
+// correctly rounded reciprocal); v_div_fixup supplies the IEEE results for
+// zero, infinite and NaN operands.
+// Exactness envelope: the row's reciprocal passed Guard::divisor (|b| >=
+// 2^-41, normal r) and |q| <= 2^100 (recorded, NaN-propagating).  Inside it
+// the residuals are exact unless |a| < 2^-96; then |q| < 2^-55, whose
+// round-to-integral is +-0 with the sign of a/b whatever the last bits (round
+// to nearest keeps the sign of every intermediate).  Outside it the caller
+// recomputes with IEEE division.
+template <typename EX>
+__device__ __forceinline__ float rint_div(float a, float b, float r, Guard &g, EX) {
+  if constexpr (EX::value) {
+    return __builtin_roundevenf(a / b);
+  } else {
+    float q = a * r;
+    float e = __builtin_fmaf(-q, b, a);
+    q = __builtin_fmaf(e, r, q);
+    e = __builtin_fmaf(-q, b, a);
+    q = __builtin_fmaf(e, r, q);
+    q = __builtin_amdgcn_div_fixupf(q, b, a);
+    asm volatile("v_maximum3_f32 %0, %0, |%1|, |%1|" : "+v"(g.qmax) : "v"(q));
+    return __builtin_roundevenf(q);
+  }
+}
+
+// float already holding an integral value (or +-inf/NaN) -> integer type T:
+// no rounding step; saturating or wrapping as the cast requests.
+template <typename T, bool SAT> __device__ __forceinline__ T integral_to_int(float r) {
+  if constexpr (SAT) {
+    return f32_to_int<T, TRUNC, true>(r);
+  } else if constexpr (sizeof(T) == 1) {
+    return __builtin_fabsf(r) < 2147483648.0f ? (T)(int32_t)r : (T)0;
+  } else {
+    return f32_to_int<T, TRUNC, false>(r);
+  }
+}
 
 // ---------------------------------------------------------------- wave64
 // Butterfly exchange across the 64 lanes of a wavefront.

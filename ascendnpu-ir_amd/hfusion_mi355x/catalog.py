@@ -145,6 +145,27 @@ def reduce_ops(rows=48, cols=3000):
 """
 
 
+def quant_ties(rows=64, cols=1024):
+    """nearbyint(x / s[row]) with f32 output: the dynamic-quantisation
+    rounding, checked on quotients placed on and next to half-integers."""
+    X, R = _T([rows, cols], "f32"), _T([rows], "f32")
+    return f"""module {{
+  func.func @quant_ties(%x: {X}, %s: {R}, %o: {X}, %mx: {R}) -> ({X}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %f = linalg.fill ins(%ninf : f32) outs(%mx : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f : {R}) dimensions = [1]
+    %e0 = tensor.empty() : {X}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e0 : {X}) dimensions = [1]
+    %e1 = tensor.empty() : {X}
+    %q = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%x, %bs : {X}, {X}) outs(%e1 : {X}) -> {X}
+    %r = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<nearbyint>}} ins(%q : {X}) outs(%o : {X}) -> {X}
+    return %r, %m : {X}, {R}
+  }}
+}}
+"""
+
+
 def entries():
     """name -> IR text of every prebuilt group."""
     e = {}
@@ -169,6 +190,7 @@ def entries():
     e["eltwise_mix"] = eltwise_mix(64, 1000)
     e["layernorm"] = layernorm(64, 2048)
     e["reduce_ops"] = reduce_ops(48, 3000)
+    e["quant_ties"] = quant_ties(64, 1024)
     return e
 
 

@@ -222,3 +222,29 @@ def test_reduce_ops(gpu):
             assert np.array_equal(g_, r_)
         else:
             assert np.array_equal(g_.view(np.uint32), r_.view(np.uint32))
+
+
+def test_rint_of_row_division_near_ties(gpu):
+    """nearbyint(x / s[row]): quotients on, and a few ulp around, half-integers,
+    signed zeros, huge quotients (exact-path fallback) and specials."""
+    note("quant_ties")
+    rows, cols = 64, 1024
+    s = I.uniform_f32(I.SEED_BASE + 90, (rows,), 0.001, 0.02)
+    s[5] = 3.0e-39   # denormal divisor: reciprocal overflows
+    s[6] = 1.0e-30   # huge quotients -> guarded exact path for this block
+    k = (I.splitmix64(I.SEED_BASE + 91, rows * cols) % np.uint64(255)).astype(np.int64).reshape(rows, cols) - 127
+    half = (k.astype(np.float64) + 0.5) * s[:, None].astype(np.float64)
+    x = half.astype(np.float32)
+    # nudge by -3..+3 ulp around the exact tie
+    nud = ((I.splitmix64(I.SEED_BASE + 92, rows * cols) % np.uint64(7)).astype(np.int64) - 3).reshape(rows, cols)
+    xb = x.view(np.int32) + nud.astype(np.int32)
+    x = xb.view(np.float32).copy()
+    x[0, :8] = [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3e38]
+    x[1, :] = np.float32(0.5) * s[1]  # exact ties
+    args = [x, s, np.zeros((rows, cols), np.float32), np.zeros(rows, np.float32)]
+    out, mx = run_gpu("quant_ties", args, gpu)
+    ref, rmx = run_oracle("quant_ties", args)
+    assert np.array_equal(mx, rmx, equal_nan=True)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(out[ok].view(np.uint32), ref[ok].view(np.uint32)), int((out[ok] != ref[ok]).sum())
