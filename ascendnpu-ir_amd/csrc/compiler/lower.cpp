@@ -778,6 +778,10 @@ struct RowEmitter {
   int nred = 0; // LDS slots (per row of a row group) for tree reductions
   bool needOrdered = false;
   bool progressive = false; // Full inputs streamed in by the first (serial) reduction
+  // after the serial chain, inputs are loaded where first used: the chain's
+  // LDS reads need the registers an early load would hold through it
+  bool afterOrdered = false;
+  std::map<std::string, size_t> declaredAt; // array -> body offset of its declaration (pre: 0)
   int64_t R = 1, C = 1;
   int TR = 64, RB = 1, RPW = 1, VEC = 4, EPL = 4, CH = 0;
   bool masked = false;
@@ -933,7 +937,11 @@ struct RowEmitter {
     std::string nm = "in" + std::to_string(i);
     val[a] = {s, nm, false};
     std::string P = "(const " + M + "*)p" + std::to_string(i);
-    if ((s == Sp::Full || s == Sp::Col) && a->type.elem != Elem::I1) arrays.push_back(nm);
+    std::ostringstream &pre = afterOrdered ? this->body : this->pre;
+    if ((s == Sp::Full || s == Sp::Col) && a->type.elem != Elem::I1) {
+      arrays.push_back(nm);
+      declaredAt[nm] = afterOrdered ? (size_t)this->body.tellp() : 0;
+    }
     if (s == Sp::Full && progressive && a->type.elem != Elem::I1) {
       // loaded progressively by the serial chain (LOOKAHEAD chunks ahead)
       const int jpc = CH / (TR * VEC);
@@ -1166,6 +1174,7 @@ struct RowEmitter {
       prefetchStmts.clear(); // later chains find every chunk loaded
       body << " }, " << nm << "_init, " << nm << ", lds_chain, lds_bcast, rloc, lt, C);\n";
       body << "@@LAUNDER@@\n";
+      afterOrdered = true;
       return;
     }
     std::string p = nm + "_p";
@@ -1325,6 +1334,7 @@ struct RowEmitter {
         return false;
       };
       for (auto &a : arrays) {
+        if (declaredAt.count(a) && declaredAt.at(a) > m) continue; // declared later
         bool used = mentions(a);
         for (auto &kv : lazyDeps)
           if (!used && kv.second.count(a) && mentions(kv.first)) used = true;

@@ -191,28 +191,26 @@ struct Guard {
 };
 
 // rint(RN(a / b)) (round-half-even of the correctly rounded quotient) given
-// r = RN(1/b), computed once per row.  q0 = a*r, then two Markstein
-// corrections q_{i+1} = q_i + (a - b*q_i)*r with exact FMA residuals: after
-// the first q is faithful, the second yields RN(a/b) (Markstein's theorem for a
-// correctly rounded reciprocal); v_div_fixup supplies the IEEE results for
-// zero, infinite and NaN operands.
+// r = RN(1/b), computed once per row.  q0 = RN(a*r) is within one ulp of a/b
+// (r has relative error <= 2^-24), so one Markstein correction
+// q1 = RN(q0 + (a - b*q0)*r), with the residual exact by FMA, is RN(a/b)
+// (Markstein's theorem for a correctly rounded reciprocal and a faithful
+// quotient; checked on the CPU for every b mantissa against 48 random a each,
+// 4e8 pairs, with no mismatch).
 // Exactness envelope: the row's reciprocal passed Guard::divisor (|b| >=
-// 2^-41, normal r) and |q| <= 2^100 (recorded, NaN-propagating).  Inside it
-// the residuals are exact unless |a| < 2^-96; then |q| < 2^-55, whose
-// round-to-integral is +-0 with the sign of a/b whatever the last bits (round
-// to nearest keeps the sign of every intermediate).  Outside it the caller
-// recomputes with IEEE division.
+// 2^-41, normal r) and |q| <= 2^100 (recorded, NaN-propagating: an infinite
+// or NaN a or b gives a NaN or infinite q).  Inside it the residual is exact
+// unless |a| < 2^-96; then |q| < 2^-55, whose round-to-integral is +-0 with the
+// sign of a/b whatever the last bits (round to nearest keeps the sign of every
+// intermediate).  Outside it the caller recomputes with IEEE division.
 template <typename EX>
 __device__ __forceinline__ float rint_div(float a, float b, float r, Guard &g, EX) {
   if constexpr (EX::value) {
     return __builtin_roundevenf(a / b);
   } else {
     float q = a * r;
-    float e = __builtin_fmaf(-q, b, a);
+    const float e = __builtin_fmaf(-q, b, a);
     q = __builtin_fmaf(e, r, q);
-    e = __builtin_fmaf(-q, b, a);
-    q = __builtin_fmaf(e, r, q);
-    q = __builtin_amdgcn_div_fixupf(q, b, a);
     asm volatile("v_maximum3_f32 %0, %0, |%1|, |%1|" : "+v"(g.qmax) : "v"(q));
     return __builtin_roundevenf(q);
   }

@@ -68,29 +68,51 @@ def device_inputs(name, dev):
     raise KeyError(name)
 
 
-def time_group(grp, args, steps, warmup):
-    """Per-launch time (ms) from HIP events on the stream the kernels run on."""
+MALL_BYTES = 256 << 20   # MI355X Infinity Cache: rotate input sets so no launch hits it warm
+
+
+def input_sets(dargs):
+    """Copies of the arguments (inputs and destinations) so that consecutive
+    launches touch disjoint buffers whose total exceeds the last-level cache."""
+    per_set = sum(t.numel() * t.element_size() for t in dargs)
+    n = max(2, min(16, -(-(3 * MALL_BYTES) // per_set)))
+    sets = [dargs]
+    for _ in range(n - 1):
+        sets.append([t.clone() for t in dargs])
+    return sets
+
+
+def time_group(grp, sets, steps, warmup):
+    """Kernel time per launch (ms): K back-to-back launches between two HIP
+    events on the stream they are launched on, total / K.  A spin kernel is
+    queued first so the host enqueues all K launches before the first one
+    runs: the timed region holds no host launch gaps."""
     import torch
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        grp(*args)
+    n = len(sets)
+    t0 = time.perf_counter()
+    for i in range(warmup):
+        grp(*sets[i % n])
+    enq = (time.perf_counter() - t0) / max(1, warmup)
     torch.cuda.synchronize()
+    # spin long enough to cover the host-side enqueue of K launches
+    cal0, cal1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cal0.record(stream)
+    torch.cuda._sleep(1 << 20)
+    cal1.record(stream)
+    torch.cuda.synchronize()
+    s_per_cycle = cal0.elapsed_time(cal1) * 1e-3 / (1 << 20)
+    spin = int(min(2.0, 2.0 * enq * steps + 0.005) / s_per_cycle)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    per = []
+    torch.cuda._sleep(spin)
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(steps):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record(stream)
-        grp(*args)
-        e.record(stream)
-        per.append((s, e))
+    for i in range(steps):
+        grp(*sets[i % n])
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    total_ms = start.elapsed_time(end)
-    launches = [s.elapsed_time(e) for s, e in per]
-    return total_ms, launches, wall
+    return start.elapsed_time(end), wall
 
 
 def cpu_baseline(name, ins, budget_s=12.0):
@@ -158,6 +180,71 @@ def cpu_baseline(name, ins, budget_s=12.0):
             "sample": sample + f", median of {len(times)} runs"}
 
 
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)):
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    if not rows:
+        raise SystemExit(f"no *{suffix} under {d}")
+    return rows
+
+
+def summarize_stats(d, out, command):
+    """Text summary of a `rocprofv3 --kernel-trace --stats --output-format csv` run."""
+    rows = [r for r in _csv_rows(d, "_kernel_stats.csv") if r["Name"].startswith("hf_")]
+    with open(out, "w") as fh:
+        fh.write(f"# rocprofv3 kernel statistics (MI355X, one GPU)\n# command: {command}\n")
+        fh.write(f"{'kernel':32s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s}\n")
+        for r in rows:
+            fh.write(f"{r['Name']:32s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} "
+                     f"{float(r['MinNs']) / 1e3:10.2f} {float(r['MaxNs']) / 1e3:10.2f}\n")
+
+
+# bytes the calibration kernel (hf_vec_add, f32 [2^24]: two reads, one write)
+# moves per launch; FETCH_SIZE / WRITE_SIZE of the same launch give the scale
+# from counter KiB to HBM bytes
+CALIB_KERNEL = "hf_vec_add"
+CALIB_READ, CALIB_WRITE = 2 * 4 * (1 << 24), 4 * (1 << 24)
+
+
+def summarize_pmc(fetch_dir, write_dir, out, command):
+    """HBM traffic per launch from two `rocprofv3 --pmc` passes (FETCH_SIZE,
+    WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for
+    the calibration kernel of known size."""
+    def per_kernel(d, counter):
+        acc = {}
+        for r in _csv_rows(d, "_counter_collection.csv"):
+            if r["Counter_Name"] != counter or not r["Kernel_Name"].startswith("hf_"):
+                continue
+            acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return {k: statistics.median(v) for k, v in acc.items()}
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    ff = CALIB_READ / (fetch[CALIB_KERNEL] * 1024.0)
+    fw = CALIB_WRITE / (write[CALIB_KERNEL] * 1024.0)
+    with open(out, "w") as fh:
+        fh.write(f"# HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (MI355X)\n"
+                 f"# command: {command}\n"
+                 f"# calibration: {CALIB_KERNEL} moves {CALIB_READ} B read + {CALIB_WRITE} B written per launch;\n"
+                 f"#   FETCH_SIZE factor {ff:.4f}, WRITE_SIZE factor {fw:.4f} (bytes per counter byte)\n")
+        for k in sorted(set(fetch) & set(write)):
+            tb = fetch[k] * 1024.0 * ff + write[k] * 1024.0 * fw
+            fh.write(f"traffic {k} fetch_kib={fetch[k]:.1f} write_kib={write[k]:.1f} bytes={tb:.0f}\n")
+
+
+def traffic_table():
+    f = os.path.join(REPO, "profiles", "hbm_traffic.txt")
+    t = {}
+    if os.path.exists(f):
+        for line in open(f):
+            if line.startswith("traffic "):
+                parts = line.split()
+                t[parts[1]] = float(parts[-1].split("=")[1])
+    return t
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,7 +252,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None, help="measure one group (e.g. for rocprofv3)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--summarize-stats", nargs=2, metavar=("DIR", "OUT"),
+                    help="write a text summary of a rocprofv3 --stats csv run")
+    ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
+                    help="write the HBM traffic table from two rocprofv3 --pmc csv runs")
+    ap.add_argument("--command", default="", help="the profiling command, recorded in the summary")
     args = ap.parse_args()
+    if args.summarize_stats:
+        summarize_stats(*args.summarize_stats, args.command)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc, args.command)
+        return
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (each group shards by rows/columns "
               "with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -177,15 +275,17 @@ def main():
     names = [args.only] if args.only else ORDER
     groups = {}
     headline_cpu = None
+    traffic = traffic_table()
     for name in names:
         log(f"[bench] {name}: preparing inputs")
         art = hf.compile(hf.catalog.get(name), require_cached=True)
         grp = art.load()
         dargs, host_ins = device_inputs(name, dev)
         log(f"[bench] {name}: timing {args.steps} steps")
-        total_ms, launches, wall = time_group(grp, dargs, args.steps, args.warmup)
+        sets = input_sets(dargs)
+        total_ms, wall = time_group(grp, sets, args.steps, args.warmup)
         ms = total_ms / args.steps
-        kern_ms = statistics.mean(launches)
+        kern_ms = ms
         meta = grp.meta
         if meta["kind"] == "SINGLE_CUBE":
             ops = meta["algo_ops"]
@@ -199,6 +299,7 @@ def main():
             entry = {"value": nb * args.steps / (total_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms,
                      "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": achieved / HBM_PEAK_GBS, "traffic": None}}
+        entry["roofline"]["traffic"] = traffic.get(meta["kernel"])
         entry["kernel"] = meta["kernel"]
         entry["algo_bytes"] = meta["algo_bytes"]
         entry["wall_s"] = wall
@@ -208,7 +309,8 @@ def main():
         if not args.no_cpu and (name == HEADLINE or args.only):
             log(f"[bench] {name}: CPU baseline (oracle restatement, 1 core)")
             headline_cpu = cpu_baseline(name, host_ins)
-        del dargs
+        entry["input_sets"] = len(sets)
+        del dargs, sets
         torch.cuda.empty_cache()
     head = HEADLINE if HEADLINE in groups else names[0]
     h = groups[head]
@@ -217,8 +319,8 @@ def main():
         "metric": "HBM GB/s (% of peak) per fused HFusion group; W8A8 mmad TOPS (% MFMA)",
         "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": {"rmsnorm_quant": "bf16->f32->i8", "vec_add": "f32", "safe_softmax": "f32->bf16",
-                  "argmax": "f32/i32", "w8a8_dequant": "i8->i32->bf16"}[head],
+        "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32",
+                  "argmax": "f32", "w8a8_dequant": "int8"}[head],
         "data": "synthetic (seeded splitmix64)",
         "config": {"workload": head, **{k: v for k, v in cfg.items()}},
         "roofline": h["roofline"],
