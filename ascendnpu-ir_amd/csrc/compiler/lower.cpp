@@ -1563,7 +1563,10 @@ KernelPlan lowerReduceWithIndex(Analysis &A, const std::string &kname) {
   int64_t tiles = (C + 1023) / 1024;
   int64_t segs = 1;
   while (R * segs < 2048 && segs * 2 <= tiles) segs *= 2;
-  int64_t segLen = ((tiles + segs - 1) / segs) * 1024;
+  // a segment lives in registers (4 floats per lane per tile of 1024): at
+  // most 32 tiles, more segments for longer rows
+  int64_t segTiles = std::min<int64_t>(32, (tiles + segs - 1) / segs);
+  int64_t segLen = segTiles * 1024;
   segs = (C + segLen - 1) / segLen;
   bool aligned = (C % 4) == 0;
   KernelPlan p;
@@ -1577,8 +1580,8 @@ KernelPlan lowerReduceWithIndex(Analysis &A, const std::string &kname) {
     << "  constexpr int64_t R = " << R << "ll, C = " << C << "ll, SEG = " << segs << "ll, SEGLEN = " << segLen << "ll;\n"
     << "  const float init_v = " << (ivArg.empty() ? iv : "((const float*)" + ivArg + ")[blockIdx.x / SEG]") << ";\n"
     << "  const " << IT << " init_i = " << (iiArg.empty() ? ii : "((const " + IT + "*)" + iiArg + ")[blockIdx.x / SEG]") << ";\n"
-    << "  hf::argreduce_rows<" << kind << ", " << BLOCK << ", " << (aligned ? "true" : "false") << ", " << IT
-    << ">((const float*)p" << x->argIdx << ", R, C, SEG, SEGLEN, init_v, init_i, (float*)" << outV << ", (" << IT << "*)" << outI
+    << "  hf::argreduce_rows<" << kind << ", " << BLOCK << ", " << (aligned ? "true" : "false") << ", " << IT << ", "
+    << segTiles << ">((const float*)p" << x->argIdx << ", R, C, SEG, SEGLEN, init_v, init_i, (float*)" << outV << ", (" << IT << "*)" << outI
     << ", ws);\n}\n";
   p.source = k.str();
   p.grid[0] = (unsigned)(R * segs);

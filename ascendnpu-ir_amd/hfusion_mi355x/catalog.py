@@ -183,6 +183,8 @@ def entries():
     e["argmax_16"] = g.argmax(16, 152064)
     e["argmax_ragged"] = g.argmax(5, 1001)
     e["argmax_i64"] = g.argmax(8, 4096, index_type="i64")
+    e["argmin_ragged"] = g.argmax(9, 5001, kind="min")
+    e["argmax_tall"] = g.argmax(2048, 33797)
     e["w8a8_512"] = g.w8a8_dequant(512, 512, 512)
     e["w8a8_ragged"] = g.w8a8_dequant(300, 200, 160)
     e["bf16_mmad_256"] = g.bf16_mmad(256, 256, 256)

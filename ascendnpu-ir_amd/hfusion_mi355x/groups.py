@@ -128,18 +128,18 @@ def safe_softmax(rows=4096, cols=32768):
 """
 
 
-def argmax(rows=256, cols=152064, index_type="i32"):
-    """reduce_with_index <max> over the last axis, init (-inf, 0) as in
-    bishengir/test/Dialect/HFusion/canonicalize.mlir:231-237."""
+def argmax(rows=256, cols=152064, index_type="i32", kind="max"):
+    """reduce_with_index <max> (or <min>) over the last axis, init (-inf, 0)
+    (+inf for <min>) as in bishengir/test/Dialect/HFusion/canonicalize.mlir:231-237."""
     X, V, I = _t([rows, cols], "f32"), _t([rows], "f32"), _t([rows], index_type)
     return f"""module {{
   func.func @argmax(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
       {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
     %c0 = arith.constant 0 : {index_type}
-    %ninf = arith.constant 0xFF800000 : f32
+    %ninf = arith.constant {'0xFF800000' if kind == 'max' else '0x7F800000'} : f32
     %v0 = linalg.fill ins(%ninf : f32) outs(%val : {V}) -> {V}
     %i0 = linalg.fill ins(%c0 : {index_type}) outs(%idx : {I}) -> {I}
-    %r:2 = hfusion.reduce_with_index {{tie_break_left = true}} <max> ins(%x : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
+    %r:2 = hfusion.reduce_with_index {{tie_break_left = true}} <{kind}> ins(%x : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
     return %r#0, %r#1 : {V}, {I}
   }}
 }}

@@ -87,10 +87,13 @@ def argmax_special(rows, cols, seed):
 
 
 @pytest.mark.parametrize("name,rows,cols,it", [("argmax_16", 16, 152064, np.int32), ("argmax_ragged", 5, 1001, np.int32),
-                                               ("argmax_i64", 8, 4096, np.int64)])
+                                               ("argmax_i64", 8, 4096, np.int64), ("argmin_ragged", 9, 5001, np.int32),
+                                               ("argmax_tall", 2048, 33797, np.int32)])
 def test_argmax(gpu, name, rows, cols, it):
     note(name)
     x = argmax_special(rows, cols, I.SEED_BASE + 30)
+    if name.startswith("argmin"):
+        x = -x   # the same special rows, mirrored for <min> (init +inf)
     args = [x, zeros(rows, np.float32), zeros(rows, it)]
     v, i = run_gpu(name, args, gpu)
     rv, ri = run_oracle(name, args)
