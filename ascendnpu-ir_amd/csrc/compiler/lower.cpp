@@ -1611,6 +1611,8 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const int esz = elemBytes(ae);
   if ((K * esz) % 16 != 0) unsupported(mm, "matmul K must span a multiple of 16 bytes");
   if (!bT && (N * esz) % 16 != 0) unsupported(mm, "matmul N must span a multiple of 16 bytes when B is [K, N]");
+  // B [N, K] with whole 64-byte K steps: both operands stream into LDS by DMA
+  const bool dma = bT && (K * esz) % 64 == 0;
   const Value *acc0 = mm->outs[0];
   if (!(acc0->def && acc0->def->name == "linalg.fill" && acc0->def->ins[0]->isConst && acc0->def->ins[0]->fconst == 0.0))
     unsupported(mm, "matmul accumulator must start from a zero linalg.fill");
@@ -1618,7 +1620,9 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   std::set<const Value *> excl = {a, b};
   A.D = {M, N};
   inferMaps(A, excl);
-  std::ostringstream epi;
+  // per-element code, plus the operand loads split by their index: [m] once
+  // per accumulator row, [n] once per column, [m, n] per element
+  std::ostringstream epi, rowFields, rowLoads, colFields, colLoads;
   std::map<const Value *, std::string> name;
   int tmp = 0;
   auto ensure = [&](const Value *v) {
@@ -1632,10 +1636,23 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
     }
     if (v->argIdx < 0) throw CompileError("internal: epilogue value " + v->name);
     const auto &m = A.map.at(v);
-    std::string idx = m.size() == 2 ? "m * " + std::to_string(N) + "ll + n" : (m.empty() ? "0" : (m[0] == 0 ? "m" : "n"));
     std::string nm = "e" + std::to_string(tmp++);
-    epi << "    const " << ctype(v->type.elem) << " " << nm << " = ((const " << mtype(v->type.elem) << "*)P.p" << v->argIdx << ")[" << idx << "];\n";
-    name[v] = nm;
+    std::string T = ctype(v->type.elem), Mt = mtype(v->type.elem), P = "((const " + Mt + "*)P.p" + std::to_string(v->argIdx) + ")";
+    if (m.size() == 2) {
+      epi << "    const " << T << " " << nm << " = " << P << "[m * " << N << "ll + n];\n";
+      name[v] = nm;
+    } else if (m.empty()) {
+      epi << "    const " << T << " " << nm << " = " << P << "[0];\n";
+      name[v] = nm;
+    } else if (m[0] == 0) {
+      rowFields << " " << T << " " << nm << ";";
+      rowLoads << "    R." << nm << " = " << P << "[m];\n";
+      name[v] = "R." + nm;
+    } else {
+      colFields << " " << T << " " << nm << ";";
+      colLoads << "    Cv." << nm << " = " << P << "[n];\n";
+      name[v] = "Cv." + nm;
+    }
   };
   for (const Op *op : f.ops) {
     const std::string &n = op->name;
@@ -1675,8 +1692,15 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   k << " };\n"
     << "struct " << kname << "_epi {\n"
     << "  using out_t = " << mtype(oe) << ";\n"
-    << "  __device__ __forceinline__ static out_t apply(" << (i8 ? "int32_t" : "float") << " acc, int64_t m, int64_t n, const "
-    << kname << "_args& P) {\n";
+    << "  using args_t = " << kname << "_args;\n"
+    << "  struct row_t {" << rowFields.str() << " int unused_; };\n"
+    << "  struct col_t {" << colFields.str() << " int unused_; };\n"
+    << "  __device__ __forceinline__ static row_t row(int64_t m, const args_t& P) {\n    row_t R{};\n" << rowLoads.str()
+    << "    return R;\n  }\n"
+    << "  __device__ __forceinline__ static col_t col(int64_t n, const args_t& P) {\n    col_t Cv{};\n" << colLoads.str()
+    << "    return Cv;\n  }\n"
+    << "  __device__ __forceinline__ static out_t apply(" << (i8 ? "int32_t" : "float")
+    << " acc, int64_t m, int64_t n, const row_t& R, const col_t& Cv, const args_t& P) {\n";
   for (size_t i = 0; i < A.params.size(); ++i)
     if (A.params[i].role == "scalar") k << "    const uint64_t s" << i << " = P.s" << i << ";\n";
   k << epi.str() << "    return (out_t)" << name[outv] << ";\n  }\n};\n}\n";
@@ -1684,7 +1708,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
     << "  " << kname << "_args P;\n";
   for (size_t i = 0; i < A.params.size(); ++i)
     k << "  P." << (A.params[i].role == "scalar" ? "s" : "p") << i << " = " << (A.params[i].role == "scalar" ? "s" : "p") << i << ";\n";
-  k << "  hf::" << (i8 ? "mmad_i8" : "mmad_bf16") << "<" << kname << "_epi, " << (bT ? "true" : "false") << ">((const "
+  k << "  hf::" << (i8 ? "mmad_i8" : "mmad_bf16") << "<" << kname << "_epi, " << (bT ? "true" : "false") << ", " << (dma ? "true" : "false") << ">((const "
     << (i8 ? "int8_t" : "uint16_t") << "*)p" << a->argIdx << ", (const " << (i8 ? "int8_t" : "uint16_t") << "*)p" << b->argIdx
     << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
   p.source = k.str();
@@ -1692,7 +1716,8 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const int64_t TM = 256, TN = 256;
   p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
   p.block[0] = 256;
-  p.variant = std::string(i8 ? "mfma_i32_32x32x32_i8" : "mfma_f32_32x32x16_bf16") + (bT ? ", B [N,K]" : ", B [K,N]");
+  p.variant = std::string(i8 ? "mfma_i32_32x32x32_i8" : "mfma_f32_32x32x16_bf16") + (bT ? ", B [N,K]" : ", B [K,N]") +
+              (dma ? ", LDS DMA ring" : ", register staging");
   p.algoOps = 2.0 * (double)M * (double)N * (double)K;
   return p;
 }

@@ -6,8 +6,12 @@
 //   * int8 x int8 -> int32 with v_mfma_i32_32x32x32_i8 (exact integer sums);
 //   * bf16 x bf16 -> fp32 with v_mfma_f32_32x32x16_bf16.
 // One 256x256 macro-tile per workgroup of 4 waves (2 x 2, 128x128 each =
-// 4 x 4 MFMA tiles of 32x32), K advanced 64 bytes at a time through a
-// double-buffered LDS stage with register prefetch of the next K slice.
+// 4 x 4 MFMA tiles of 32x32), K advanced 64 bytes at a time.
+//   * DMA path (B [N, K], K spanning a multiple of 64 bytes): a 4-slot LDS
+//     ring filled by global_load_lds_dwordx4 four steps ahead of the MFMAs,
+//     fragments double-buffered in registers (one barrier per step);
+//   * register path (the rest): a double-buffered LDS stage with register
+//     prefetch of the next K slice.
 // Macro-tiles are numbered so that the workgroups the dispatcher sends to one
 // XCD (blockIdx % 8) cover a compact 2-D block of C and share A/B panels in
 // that XCD's L2.  The epilogue functor receives the raw accumulator and the
@@ -121,6 +125,107 @@ template <int ESZ> __device__ __forceinline__ void mm_store_nmajor(char *lds, co
   }
 }
 
+// Epilogue: accumulator register r of a 32x32 tile holds row
+// 8*(r/4) + 4*(lane/32) + r%4 and column lane%32 of that tile.  The
+// functor's per-row operands are loaded once per accumulator row and its
+// per-column operands once per column; bounds are tested per element only
+// in tiles that cross the edge of C.
+template <typename Epi, typename acc_t, typename Args>
+__device__ __forceinline__ void mm_epilogue(acc_t (&acc)[4][4], typename Epi::out_t *__restrict__ out, int64_t M,
+                                            int64_t N, int64_t m0, int64_t n0, int wm, int wn, int lane, const Args &P) {
+  const bool full = m0 + MM_TM <= M && n0 + MM_TN <= N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    typename Epi::row_t rv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t m = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+      rv[r] = Epi::row(m < M ? m : M - 1, P);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + wn * 128 + j * 32 + lane % 32;
+      const typename Epi::col_t cv = Epi::col(n < N ? n : N - 1, P);
+      // the tile leaves the accumulator registers only here: one tile's
+      // values in VGPRs at a time
+      acc_t a = acc[i][j];
+      asm volatile("" : "+a"(a)::"memory");
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+        if (full || (m < M && n < N)) out[m * N + n] = Epi::apply(a[r], m, n, rv[r], cv, P);
+      }
+    }
+  }
+}
+
+// Epilogue through LDS (the DMA path's ring is free by then): the tile's
+// outputs are computed into a row-major out_t stage, then the whole
+// workgroup writes them out as 16-byte row segments (a 256-column row is one
+// contiguous run of C).  When the whole 256x256 tile fits the stage (2-byte
+// outputs) all four waves compute at once; otherwise the two row halves
+// (waves wm = 0, then wm = 1) take turns.
+template <typename Epi, typename acc_t, typename Args>
+__device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][4], typename Epi::out_t *__restrict__ out, int64_t M,
+                                                int64_t N, int64_t m0, int64_t n0, int wm, int wn, int lane, const Args &P,
+                                                char *stage, int stage_bytes) {
+  using O = typename Epi::out_t;
+  constexpr int RB = 256 * (int)sizeof(O);       // bytes of one staged row
+  constexpr int CPR = RB / 16;                    // 16-byte chunks per row
+  constexpr int EPC = 16 / (int)sizeof(O);        // elements per chunk
+  const bool one_pass = 256 * RB <= stage_bytes;
+  const int rows_per_pass = one_pass ? 256 : 128;
+  const int RS = rows_per_pass * (RB + 16) <= stage_bytes ? RB + 16 : RB; // padded when it fits
+  const int tid = threadIdx.x;
+  for (int h = 0; h < (one_pass ? 1 : 2); ++h) {
+    __syncthreads(); // the stage is free
+    if (one_pass || wm == h) {
+      const int rbase = one_pass ? wm * 128 : 0; // this wave's first staged row
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        typename Epi::row_t rv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+          rv[r] = Epi::row(m < M ? m : M - 1, P);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = wn * 128 + j * 32 + lane % 32;
+          const int64_t n = n0 + col;
+          const typename Epi::col_t cv = Epi::col(n < N ? n : N - 1, P);
+          acc_t a = acc[i][j];
+          asm volatile("" : "+a"(a)::"memory"); // one tile in VGPRs at a time
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+            const int64_t m = m0 + wm * 128 + row;
+            // rows and columns past C are staged (from clamped operand
+            // indices) but never stored
+            *reinterpret_cast<O *>(stage + (rbase + row) * RS + col * (int)sizeof(O)) =
+                Epi::apply(a[r], m < M ? m : M - 1, n < N ? n : N - 1, rv[r], cv, P);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int64_t mrow0 = m0 + (one_pass ? 0 : h * 128);
+#pragma unroll 4
+    for (int c = tid; c < rows_per_pass * CPR; c += 256) {
+      const int row = c / CPR, ch = c % CPR;
+      const int64_t m = mrow0 + row, n = n0 + (int64_t)ch * EPC;
+      if (m >= M) continue;
+      const v4i v = *reinterpret_cast<const v4i *>(stage + row * RS + ch * 16);
+      if (n + EPC <= N) {
+        __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(out + m * N + n));
+      } else {
+        const O *e = reinterpret_cast<const O *>(&v);
+        for (int k = 0; k < EPC && n + k < N; ++k) out[m * N + n + k] = e[k];
+      }
+    }
+  }
+}
+
 template <bool I8, typename Epi, bool BT, typename ElemT, typename Args>
 __device__ void mmad_core(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
                           int64_t M, int64_t N, int64_t K, const Args &P) {
@@ -185,31 +290,155 @@ __device__ void mmad_core(const ElemT *__restrict__ A, const ElemT *__restrict__
     __syncthreads();
   }
 
-  // epilogue: accumulator register r of a 32x32 tile holds
-  // row 8*(r/4) + 4*(lane/32) + r%4, column lane%32
+  mm_epilogue<Epi>(acc, out, M, N, m0, n0, wm, wn, lane, P);
+}
+
+// ---- DMA path --------------------------------------------------------------
+// LDS layout of one operand slice (256 rows x 64 bytes = 1024 granules of 16
+// bytes): granule g of row r sits at position 4r + (g ^ ((r >> 2) & 3)).  A
+// fragment read touches one logical granule of 32 consecutive rows, and any
+// 16 consecutive rows then cover all 16 granule slots of a 256-byte bank
+// line.  global_load_lds_dwordx4 writes lane l of a wave to position
+// base + l, so the swizzle is applied by choosing which global granule each
+// lane fetches.
+constexpr int MMD_STAGES = 4;
+constexpr int MMD_SLICE = 256 * 64;  // bytes per operand per stage
+
+__device__ __forceinline__ void mmd_dma16(const void *g, uint32_t lds_addr) {
+  // M0 holds the wave's LDS destination; written here and read by the next
+  // instruction only
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory");
+}
+
+template <int N> __device__ __forceinline__ void mmd_wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// Issues this wave's 4 DMA instructions (rows 64*wave .. +63) of one operand
+// slice: rows row0.., K bytes k0..k0+63; rows past `rows` re-read the last row.
+__device__ __forceinline__ void mmd_issue_operand(const char *__restrict__ base, int64_t rows, int64_t row0, int64_t Kbytes,
+                                                  int64_t k0, uint32_t lds_slice) {
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int blk = wave * 4 + i;            // 1 KB block: rows 16*blk .. +15
+    const int r = 16 * blk + lane / 4;
+    const int g = (lane % 4) ^ ((r >> 2) & 3);
+    int64_t row = row0 + r;
+    row = row < rows ? row : rows - 1;
+    mmd_dma16(base + row * Kbytes + k0 + g * 16, __builtin_amdgcn_readfirstlane(lds_slice + blk * 1024));
+  }
+}
+
+template <bool I8, typename Epi, typename ElemT, typename Args>
+__device__ void mmad_core_dma(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
+                              int64_t M, int64_t N, int64_t K, const Args &P) {
+  using Op = MfmaOp<I8>;
+  using acc_t = typename Op::acc_t;
+  constexpr int ESZ = sizeof(ElemT);
+  __shared__ __attribute__((aligned(1024))) char lds[MMD_STAGES][2][MMD_SLICE]; // [stage][A/B]
+  const int tmt = (int)((M + MM_TM - 1) / MM_TM), tnt = (int)((N + MM_TN - 1) / MM_TN);
+  int ti, tj;
+  mm_tile_of(blockIdx.x, tmt, tnt, ti, tj);
+  const int64_t m0 = (int64_t)ti * MM_TM, n0 = (int64_t)tj * MM_TN;
+  const int64_t Kb = K * ESZ;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int wm = wave / 2, wn = wave % 2;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)&lds[0][0][0];
+  const char *Ab = reinterpret_cast<const char *>(A), *Bb = reinterpret_cast<const char *>(B);
+  const int nsteps = (int)(Kb / 64);
+
+  // every step issues the same number of DMAs (8 per wave), so one fixed
+  // vmcnt finds a stage complete; steps past the end re-read the last slice
+  // into a ring slot that is never read again
+  auto issue = [&](int s) {
+    const int sk = s < nsteps ? s : nsteps - 1;
+    const uint32_t st = lds0 + (uint32_t)((s % MMD_STAGES) * 2 * MMD_SLICE);
+    mmd_issue_operand(Ab, M, m0, Kb, (int64_t)sk * 64, st);
+    mmd_issue_operand(Bb, N, n0, Kb, (int64_t)sk * 64, st + MMD_SLICE);
+  };
+
+  acc_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t n = n0 + wn * 128 + j * 32 + lane % 32;
+    for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
+
+  // fragment of MFMA tile row/col block `blk` (32 rows), logical granule g
+  auto frag = [&](const char *slice, int blk, int g) -> v4i {
+    const int r = blk * 32 + lane % 32;
+    return *reinterpret_cast<const v4i *>(slice + (4 * r + (g ^ ((r >> 2) & 3))) * 16);
+  };
+  // all 16 fragments (2 k-halves x (4 A + 4 B)) of one stage
+  auto fetch = [&](int stage, v4i (&f)[2][8]) {
+    const char *la = lds[stage % MMD_STAGES][0], *lb = lds[stage % MMD_STAGES][1];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-        if (m < M && n < N) out[m * N + n] = Epi::apply(acc[i][j][r], m, n, P);
-      }
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[q][i] = frag(la, wm * 4 + i, 2 * q + lane / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f[q][4 + j] = frag(lb, wn * 4 + j, 2 * q + lane / 32);
     }
+  };
+  auto mfmas = [&](const v4i (&f)[2][8]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = Op::run(f[q][i], f[q][4 + j], acc[i][j]);
+  };
+  // Step s: the fragments of stage s are already in registers; the wave
+  // multiplies them while it reads stage s+1's fragments into the other set,
+  // so the matrix core never waits on LDS.  The barrier at the top of step s
+  // makes stage s+1 visible and frees the slot of stage s (its fragments were
+  // read during step s-1) for the DMA of stage s+4: three stages are in
+  // flight while one is multiplied.
+  auto step = [&](int s, const v4i (&cur)[2][8], v4i (&nxt)[2][8]) {
+    __builtin_amdgcn_sched_barrier(0);
+    mmd_wait_vm<16>();   // this wave's DMAs of stage s+1 are complete
+    __syncthreads();     // everyone's are; stage s is no longer read
+    issue(s + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(s + 1, nxt);   // at the last step: the (complete) re-read stage, unused
+    mfmas(cur);
+    // issue order inside the step: one LDS fragment read, two MFMAs, ...
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0); // MFMA
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  issue(0);
+  issue(1);
+  issue(2);
+  mmd_wait_vm<16>();     // stage 0 (this wave)
+  __syncthreads();
+  issue(3);
+  v4i f0[2][8], f1[2][8];
+  fetch(0, f0);
+#pragma unroll 1
+  for (int s = 0; s < nsteps; s += 2) {
+    step(s, f0, f1);
+    if (s + 1 >= nsteps) break;
+    step(s + 1, f1, f0);
+  }
+  mmd_wait_vm<0>();      // drain the trailing re-reads before the LDS is reused
+  mm_epilogue_lds<Epi>(acc, out, M, N, m0, n0, wm, wn, lane, P, &lds[0][0][0], (int)sizeof(lds));
 }
 
-template <typename Epi, bool BT, typename Args>
+template <typename Epi, bool BT, bool DMA, typename Args>
 __device__ __forceinline__ void mmad_i8(const int8_t *A, const int8_t *B, typename Epi::out_t *out, int64_t M, int64_t N,
                                         int64_t K, const Args &P) {
-  mmad_core<true, Epi, BT>(A, B, out, M, N, K, P);
+  if constexpr (DMA) mmad_core_dma<true, Epi>(A, B, out, M, N, K, P);
+  else mmad_core<true, Epi, BT>(A, B, out, M, N, K, P);
 }
 
-template <typename Epi, bool BT, typename Args>
+template <typename Epi, bool BT, bool DMA, typename Args>
 __device__ __forceinline__ void mmad_bf16(const uint16_t *A, const uint16_t *B, typename Epi::out_t *out, int64_t M,
                                           int64_t N, int64_t K, const Args &P) {
-  mmad_core<false, Epi, BT>(A, B, out, M, N, K, P);
+  if constexpr (DMA) mmad_core_dma<false, Epi>(A, B, out, M, N, K, P);
+  else mmad_core<false, Epi, BT>(A, B, out, M, N, K, P);
 }
 
 } // namespace hf

@@ -146,11 +146,13 @@ def argmax(rows=256, cols=152064, index_type="i32", kind="max"):
 """
 
 
-def w8a8_dequant(m=4096, n=4096, k=4096):
-    """W8A8 contraction (hivm.hir.matmul, B in the [N, K] weight layout) with
-    the per-token x per-channel dequant epilogue in IR order:
+def w8a8_dequant(m=4096, n=4096, k=4096, b_layout="nk"):
+    """W8A8 contraction (hivm.hir.matmul, B in the [N, K] weight layout, or
+    [K, N] with b_layout="kn" through linalg.matmul) with the per-token x
+    per-channel dequant epilogue in IR order:
     bf16((sitofp(C) * s_tok[m]) * s_ch[n])."""
-    A, B = _t([m, k], "i8"), _t([n, k], "i8")
+    A, B = _t([m, k], "i8"), (_t([n, k], "i8") if b_layout == "nk" else _t([k, n], "i8"))
+    mm = "linalg.matmul_transpose_b" if b_layout == "nk" else "linalg.matmul"
     C, CF, O = _t([m, n], "i32"), _t([m, n], "f32"), _t([m, n], "bf16")
     ST, SC = _t([m], "f32"), _t([n], "f32")
     return f"""module {{
@@ -159,7 +161,7 @@ def w8a8_dequant(m=4096, n=4096, k=4096):
     %c0 = arith.constant 0 : i32
     %e0 = tensor.empty() : {C}
     %acc0 = linalg.fill ins(%c0 : i32) outs(%e0 : {C}) -> {C}
-    %acc = linalg.matmul_transpose_b ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
+    %acc = {mm} ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
     %e1 = tensor.empty() : {CF}
     %cf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%acc : {C}) outs(%e1 : {CF}) -> {CF}
     %e2 = tensor.empty() : {CF}

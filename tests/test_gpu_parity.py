@@ -114,23 +114,27 @@ def test_argmax_repeat_launch(gpu):
 
 
 # ------------------------------------------------------------------ W8A8
-@pytest.mark.parametrize("name,m,n,k", [("w8a8_512", 512, 512, 512), ("w8a8_ragged", 300, 200, 160)])
+@pytest.mark.parametrize("name,m,n,k", [("w8a8_512", 512, 512, 512), ("w8a8_ragged", 300, 200, 160),
+                                        ("w8a8_ragged_dma", 300, 200, 192), ("w8a8_kn", 320, 256, 128)])
 def test_w8a8(gpu, name, m, n, k):
     note(name)
     a, b, st, sc = I.config_inputs("w8a8_dequant", m=m, n=n, k=k)
+    if name.endswith("_kn"):
+        b = np.ascontiguousarray(b.T)   # the same weights in the [K, N] layout
     args = [a, b, st, sc, zeros((m, n), np.uint16)]
     out, = run_gpu(name, args, gpu)
     ref, = run_oracle(name, args)
     assert np.array_equal(out, ref), f"max {bf16_ulp_diff(out, ref).max()} ulp"
 
 
-def test_bf16_mmad(gpu):
-    note("bf16_mmad_256")
+@pytest.mark.parametrize("name,m,n,k", [("bf16_mmad_256", 256, 256, 256), ("bf16_mmad_ragged", 200, 136, 96)])
+def test_bf16_mmad(gpu, name, m, n, k):
+    note(name)
     s = I.SEED_BASE + 40
-    a, b = I.normal_bf16(s, (256, 256)), I.normal_bf16(s + 1, (256, 256))
-    args = [a, b, zeros((256, 256), np.uint16)]
-    out, = run_gpu("bf16_mmad_256", args, gpu)
-    ref, = run_oracle("bf16_mmad_256", args)
+    a, b = I.normal_bf16(s, (m, k)), I.normal_bf16(s + 1, (n, k))
+    args = [a, b, zeros((m, n), np.uint16)]
+    out, = run_gpu(name, args, gpu)
+    ref, = run_oracle(name, args)
     # fp32 accumulation order differs from the serial k loop
     assert bf16_ulp_diff(out, ref).max() <= 1
 
