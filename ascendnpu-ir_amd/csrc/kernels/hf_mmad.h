@@ -355,6 +355,18 @@ __device__ void mmad_core_dma(const ElemT *__restrict__ A, const ElemT *__restri
     mmd_issue_operand(Ab, M, m0, Kb, (int64_t)sk * 64, st);
     mmd_issue_operand(Bb, N, n0, Kb, (int64_t)sk * 64, st + MMD_SLICE);
   };
+  // one of the 8 DMA instructions of stage s (d < 4: A, else B)
+  auto issue_one = [&](int s, int d) {
+    const int sk = s < nsteps ? s : nsteps - 1;
+    const uint32_t st = lds0 + (uint32_t)((s % MMD_STAGES) * 2 * MMD_SLICE) + (d < 4 ? 0u : (uint32_t)MMD_SLICE);
+    const int blk = wave * 4 + (d & 3);
+    const int r = 16 * blk + lane / 4;
+    const int g = (lane % 4) ^ ((r >> 2) & 3);
+    const int64_t rows = d < 4 ? M : N, row0 = d < 4 ? m0 : n0;
+    int64_t row = row0 + r;
+    row = row < rows ? row : rows - 1;
+    mmd_dma16((d < 4 ? Ab : Bb) + row * Kb + (int64_t)sk * 64 + g * 16, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+  };
 
   acc_t acc[4][4];
 #pragma unroll
@@ -396,15 +408,19 @@ __device__ void mmad_core_dma(const ElemT *__restrict__ A, const ElemT *__restri
     __builtin_amdgcn_sched_barrier(0);
     mmd_wait_vm<16>();   // this wave's DMAs of stage s+1 are complete
     __syncthreads();     // everyone's are; stage s is no longer read
-    issue(s + 4);
-    __builtin_amdgcn_sched_barrier(0);
-    fetch(s + 1, nxt);   // at the last step: the (complete) re-read stage, unused
-    mfmas(cur);
-    // issue order inside the step: one LDS fragment read, two MFMAs, ...
+    // 8 groups: one DMA of stage s+4, two fragment reads of stage s+1, four
+    // MFMAs of stage s -- a DMA that waits for a free memory queue slot
+    // then holds back at most one group's MFMAs
+    const char *la = lds[(s + 1) % MMD_STAGES][0], *lb = lds[(s + 1) % MMD_STAGES][1];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0); // MFMA
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_one(s + 4, g);
+      const int q = g / 4, i = g % 4;
+      nxt[q][i] = frag(la, wm * 4 + i, 2 * q + lane / 32);
+      nxt[q][4 + i] = frag(lb, wn * 4 + i, 2 * q + lane / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = Op::run(cur[q][i], cur[q][4 + j], acc[i][j]);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
