@@ -1558,21 +1558,20 @@ KernelPlan lowerReduceWithIndex(Analysis &A, const std::string &kname) {
     if (v->def != rw) unsupported(rw, "group returns a value other than the reduction results");
     (v->resultIdx == 0 ? outV : outI) = resultPtr(A, i);
   }
-  // schedule: split every row into SEG segments of whole 1024-element tiles
-  const int BLOCK = 256;
-  int64_t tiles = (C + 1023) / 1024;
-  int64_t segs = 1;
-  while (R * segs < 2048 && segs * 2 <= tiles) segs *= 2;
-  // a segment lives in registers (4 floats per lane per tile of 1024): at
-  // most 32 tiles, more segments for longer rows
-  int64_t segTiles = std::min<int64_t>(32, (tiles + segs - 1) / segs);
-  int64_t segLen = segTiles * 1024;
+  // schedule: with at least one row per CU, one workgroup per row (no
+  // cross-workgroup step); otherwise about two workgroups per CU, each on a
+  // segment of a row (a multiple of 4 elements, so float4 loads stay aligned)
+  const int64_t CUS = 256;
+  int64_t segs = R >= CUS ? 1 : std::max<int64_t>(1, (2 * CUS + R - 1) / R);
+  int64_t segLen = ((C + segs - 1) / segs + 3) / 4 * 4;
+  segLen = std::max<int64_t>(segLen, std::min<int64_t>((C + 3) / 4 * 4, 4096)); // no tiny segments
   segs = (C + segLen - 1) / segLen;
+  const int BLOCK = segLen >= 32768 ? 1024 : (segLen >= 8192 ? 512 : 256);
   bool aligned = (C % 4) == 0;
   KernelPlan p;
   p.kernelName = kname;
   p.kind = "REDUCE_WITH_INDEX";
-  p.variant = "split-row two-level, last-block combine";
+  p.variant = segs == 1 ? "one workgroup per row, streaming" : "split-row two-level, last-block combine";
   std::ostringstream k;
   std::string IT = ctype(idxE);
   k << "extern \"C\" __global__ __launch_bounds__(" << BLOCK << ") void " << kname << "("
@@ -1580,8 +1579,8 @@ KernelPlan lowerReduceWithIndex(Analysis &A, const std::string &kname) {
     << "  constexpr int64_t R = " << R << "ll, C = " << C << "ll, SEG = " << segs << "ll, SEGLEN = " << segLen << "ll;\n"
     << "  const float init_v = " << (ivArg.empty() ? iv : "((const float*)" + ivArg + ")[blockIdx.x / SEG]") << ";\n"
     << "  const " << IT << " init_i = " << (iiArg.empty() ? ii : "((const " + IT + "*)" + iiArg + ")[blockIdx.x / SEG]") << ";\n"
-    << "  hf::argreduce_rows<" << kind << ", " << BLOCK << ", " << (aligned ? "true" : "false") << ", " << IT << ", "
-    << segTiles << ">((const float*)p" << x->argIdx << ", R, C, SEG, SEGLEN, init_v, init_i, (float*)" << outV << ", (" << IT << "*)" << outI
+    << "  hf::argreduce_rows<" << kind << ", " << BLOCK << ", " << (aligned ? "true" : "false") << ", " << IT
+    << ">((const float*)p" << x->argIdx << ", R, C, SEG, SEGLEN, init_v, init_i, (float*)" << outV << ", (" << IT << "*)" << outI
     << ", ws);\n}\n";
   p.source = k.str();
   p.grid[0] = (unsigned)(R * segs);

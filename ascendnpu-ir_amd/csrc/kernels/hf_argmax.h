@@ -12,8 +12,10 @@
 //     maximumf(M, init_v).
 // Schedule: each row is split into SEG segments, one workgroup each; a
 // segment produces the record (M, J, has_nan) of its prefix before its first
-// NaN; the last workgroup of a row (arrival counter in the workspace) folds the
-// records left to right with the serial rule above and resets the counter.
+// NaN.  With SEG == 1 the workgroup folds it into the init and writes the row.
+// Otherwise the last workgroup of a row (arrival counter in the workspace)
+// folds the records left to right with the serial rule above and resets the
+// counter.
 // Cross-workgroup protocol: records and counters are accessed only through
 // agent-scope relaxed atomics, which the gfx942/gfx950 memory model keeps
 // coherent across the XCDs' L2 caches (sc1 accesses).  A writer waits for
@@ -118,85 +120,100 @@ __device__ __forceinline__ void arg_scan(const float *__restrict__ row, int64_t 
   }
 }
 
-// Segment record without NaNs, from registers: every lane loads its NV
-// float4 (or 4*NV scalars) of the segment at once, then
-//   pass 1: M = fold (maximumf / minimumf, NaN-propagating) over the block;
-//   pass 2: J = lowest index c with x[c] == M (IEEE ==) over the block.
-// Returns false (and leaves v, i unset) when the segment holds a NaN; the
-// caller then takes the general path.  Indices inside a segment are 32-bit.
-template <int KIND, int BLOCK, bool ALIGNED, int NV>
+// Segment record without NaNs, in one streaming pass: every lane walks its
+// elements in increasing index order, CH float4 (or 4*CH scalars) per round
+// with all loads of a round in flight together, keeping
+//   m = fold (maximumf / minimumf, NaN-propagating) of what it has seen,
+//   j = its first position whose value beats every earlier one (strictly),
+// which is its first position holding a value IEEE-equal to its final m
+// (equal values, and -0/+0, never replace j).  Lanes are then combined by
+// (better value; for IEEE-equal values the lower position).  Returns false
+// when the segment holds a NaN (m is NaN); the caller takes the general path.
+template <int KIND, int BLOCK, bool ALIGNED>
 __device__ __forceinline__ bool arg_segment_fast(const float *__restrict__ row, int64_t s0, int64_t e1, float &v, int64_t &i,
                                                  float *sv, int *si) {
+  constexpr int CH = 8;
   const float ident = KIND == 0 ? -__builtin_inff() : __builtin_inff();
   const int tid = threadIdx.x;
   const int n = (int)(e1 - s0);
-  float x[4 * NV];
-  // element k of lane tid sits at offset off(k) of the segment
-  auto off = [&](int k) -> int {
-    return ALIGNED ? ((k / 4) * BLOCK + tid) * 4 + (k % 4) : (k / 4) * 4 * BLOCK + (k % 4) * BLOCK + tid;
+  float m = ident;
+  int j = 0x7fffffff;
+  auto visit = [&](float x, int pos) {
+    j = arg_better<KIND>(x, m) ? pos : j;
+    m = arg_fold<KIND>(x, m);
   };
-  // branch-free loads (a branch per load would make the compiler wait for
-  // each): lanes past the end read a clamped in-range address and select the
-  // identity.  ALIGNED means C % 4 == 0, so n % 4 == 0 and no float4 is partial.
   if constexpr (ALIGNED) {
+    // n % 4 == 0 (C % 4 == 0): no partial float4; lanes past the end read a
+    // clamped in-range address and see the identity
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     const f32x4 *p4 = reinterpret_cast<const f32x4 *>(row + s0);
-    const int last4 = n / 4 - 1;
+    const int n4 = n / 4;
+    for (int q0 = 0; q0 < n4; q0 += CH * BLOCK) {
+      f32x4 t[CH];
 #pragma unroll
-    for (int q = 0; q < NV; ++q) {
-      const int o4 = q * BLOCK + tid;
-      const f32x4 t = __builtin_nontemporal_load(p4 + (o4 < last4 ? o4 : last4));
-      const bool in = o4 <= last4;
-      x[4 * q + 0] = in ? t.x : ident;
-      x[4 * q + 1] = in ? t.y : ident;
-      x[4 * q + 2] = in ? t.z : ident;
-      x[4 * q + 3] = in ? t.w : ident;
+      for (int c = 0; c < CH; ++c) {
+        const int o4 = q0 + c * BLOCK + tid;
+        t[c] = __builtin_nontemporal_load(p4 + (o4 < n4 ? o4 : n4 - 1));
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int o4 = q0 + c * BLOCK + tid;
+        const bool in = o4 < n4;
+        visit(in ? t[c].x : ident, 4 * o4);
+        visit(in ? t[c].y : ident, 4 * o4 + 1);
+        visit(in ? t[c].z : ident, 4 * o4 + 2);
+        visit(in ? t[c].w : ident, 4 * o4 + 3);
+      }
     }
   } else {
+    for (int o0 = 0; o0 < n; o0 += 4 * CH * BLOCK) {
+      float t[4 * CH];
 #pragma unroll
-    for (int k = 0; k < 4 * NV; ++k) {
-      const int o = off(k);
-      const float t = __builtin_nontemporal_load(row + s0 + (o < n ? o : n - 1));
-      x[k] = o < n ? t : ident;
+      for (int c = 0; c < 4 * CH; ++c) {
+        const int o = o0 + c * BLOCK + tid;
+        t[c] = __builtin_nontemporal_load(row + s0 + (o < n ? o : n - 1));
+      }
+#pragma unroll
+      for (int c = 0; c < 4 * CH; ++c) {
+        const int o = o0 + c * BLOCK + tid;
+        visit(o < n ? t[c] : ident, o);
+      }
     }
   }
-  float m = ident;
+  // a lane whose in-range values all equal the identity (e.g. -inf for
+  // <max>) never saw a strictly better one: its answer is its first position
+  {
+    const int first = ALIGNED ? 4 * tid : tid;
+    if (j == 0x7fffffff && m == ident && first < n) j = first;
+  }
+  // lanes with no element in range keep j = 0x7fffffff; a real position is
+  // always lower
+  auto combine = [&](float m2, int j2) {
+    if (arg_better<KIND>(m2, m)) { m = m2; j = j2; }
+    else if (!arg_better<KIND>(m, m2)) { m = arg_fold<KIND>(m, m2); j = j2 < j ? j2 : j; }
+  };
 #pragma unroll
-  for (int k = 0; k < 4 * NV; ++k) m = arg_fold<KIND>(x[k], m);
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) m = arg_fold<KIND>(__shfl_xor(m, s, 64), m);
+  for (int sh = 32; sh >= 1; sh >>= 1) {
+    const float m2 = __shfl_xor(m, sh, 64);
+    const int j2 = __shfl_xor(j, sh, 64);
+    combine(m2, j2);
+  }
   constexpr int NW = BLOCK / 64;
-  if (tid % 64 == 0) sv[tid / 64] = m;
+  if (tid % 64 == 0) { sv[tid / 64] = m; si[tid / 64] = j; }
   __syncthreads();
   m = sv[0];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) m = arg_fold<KIND>(sv[w], m);
-  if (m != m) return false; // a NaN somewhere in the segment
-  int j = 0x7fffffff;
-#pragma unroll
-  for (int k = 4 * NV - 1; k >= 0; --k) {
-    const int o = off(k);
-    j = (x[k] == m && o < n) ? o : j; // lane offsets grow with k: the last hit kept is the lowest
-  }
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    const int o = __shfl_xor(j, s, 64);
-    j = o < j ? o : j;
-  }
-  if (tid % 64 == 0) si[tid / 64] = j;
-  __syncthreads();
   j = si[0];
 #pragma unroll
-  for (int w = 1; w < NW; ++w) j = si[w] < j ? si[w] : j;
+  for (int w = 1; w < NW; ++w) combine(sv[w], si[w]);
+  if (m != m) return false; // a NaN somewhere in the segment
   v = m;
   i = j == 0x7fffffff ? INT64_MAX : s0 + j;
   return true;
 }
 
-template <int KIND, int BLOCK, bool ALIGNED, typename IdxT, int NV>
+template <int KIND, int BLOCK, bool ALIGNED, typename IdxT>
 __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C, int64_t SEG, int64_t SEGLEN, float init_v,
                                IdxT init_i, float *__restrict__ out_v, IdxT *__restrict__ out_i, void *ws) {
-  static_assert(NV >= 1, "segment of at least 4*BLOCK elements");
   __shared__ float sv[BLOCK / 64];
   __shared__ int64_t si[BLOCK / 64];
   __shared__ int64_t snan[BLOCK / 64];
@@ -211,7 +228,7 @@ __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C
   float v;
   int64_t i;
   bool has_nan = false;
-  if (!arg_segment_fast<KIND, BLOCK, ALIGNED, NV>(rp, s0, s1, v, i, fv, fi)) {
+  if (!arg_segment_fast<KIND, BLOCK, ALIGNED>(rp, s0, s1, v, i, fv, fi)) {
     // rare path: locate the first NaN, then rescan the prefix before it
     int64_t nan_at;
     arg_scan<KIND, BLOCK, ALIGNED>(rp, s0, s1, s1, v, i, nan_at);
@@ -229,6 +246,23 @@ __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C
     arg_block_reduce<KIND, BLOCK>(v, i, sv, si);
     has_nan = true;
   }
+  if (SEG == 1) {
+    // the whole row in this workgroup: fold the record into the init directly
+    if (threadIdx.x == 0) {
+      float V = init_v;
+      int64_t I = (int64_t)init_i;
+      if (V == V) {
+        if (i != INT64_MAX) {
+          if (arg_better<KIND>(v, V)) I = i;
+          V = arg_fold<KIND>(v, V);
+        }
+        if (has_nan) V = __builtin_nanf("");
+      }
+      if (out_v) out_v[row] = V;
+      if (out_i) out_i[row] = (IdxT)I;
+    }
+    return;
+  }
   if (threadIdx.x == 0) {
     ArgRec r;
     r.m = v;
@@ -240,19 +274,32 @@ __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C
     last = prev == (unsigned)(SEG - 1);
   }
   __syncthreads();
-  if (!last || threadIdx.x != 0) return;
-  // serial fold of the segment records, left to right
+  if (!last) return;
+  // serial fold of the segment records, left to right: the whole workgroup
+  // loads BLOCK records at a time into LDS (independent loads in flight
+  // together), thread 0 folds them
+  __shared__ ArgRec fold[BLOCK];
   float V = init_v;
   int64_t I = (int64_t)init_i;
   bool vnan = V != V;
-  for (int64_t s = 0; s < SEG && !vnan; ++s) {
-    const ArgRec r = rec_load(&recs[row * SEG + s]); // issued after the counter RMW returned
-    if (r.j != INT64_MAX) {
-      if (arg_better<KIND>(r.m, V)) I = r.j;
-      V = arg_fold<KIND>(r.m, V);
+  for (int64_t s0 = 0; s0 < SEG; s0 += BLOCK) {
+    const int64_t s = s0 + threadIdx.x;
+    if (s < SEG) fold[threadIdx.x] = rec_load(&recs[row * SEG + s]); // issued after the counter RMW returned
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int64_t n = SEG - s0 < BLOCK ? SEG - s0 : BLOCK;
+      for (int64_t t = 0; t < n && !vnan; ++t) {
+        const ArgRec r = fold[t];
+        if (r.j != INT64_MAX) {
+          if (arg_better<KIND>(r.m, V)) I = r.j;
+          V = arg_fold<KIND>(r.m, V);
+        }
+        if (r.has_nan) { V = __builtin_nanf(""); vnan = true; }
+      }
     }
-    if (r.has_nan) { V = __builtin_nanf(""); vnan = true; }
+    __syncthreads();
   }
+  if (threadIdx.x != 0) return;
   if (out_v) out_v[row] = V;
   if (out_i) out_i[row] = (IdxT)I;
   __hip_atomic_store(&counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
