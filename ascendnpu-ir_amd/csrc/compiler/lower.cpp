@@ -1035,9 +1035,10 @@ struct RowEmitter {
           bAt = val[b].name;
           rAt = rn;
         }
-        // the quotient itself is the IEEE division; the reciprocal serves a
-        // consuming nearbyint (hf::rint_div)
-        expr = "(" + at(opsv[0], "e") + " / " + bAt + ")";
+        // the quotient is RN(a/b) from the row reciprocal (hf::div_rn, exact
+        // or re-executed); a consuming nearbyint takes hf::rint_div instead
+        expr = "hf::div_rn(" + at(opsv[0], "e") + ", " + bAt + ", " + rAt + ", hf_g, ex)";
+        fast = true;
         nv.divA = at(opsv[0], "e");
         nv.divB = bAt;
         nv.divR = rAt;

@@ -150,20 +150,17 @@ __device__ __forceinline__ float rec(float a) { return 1.0f / a; }
 __device__ __forceinline__ float relu(float a) { return maximumf(0.0f, a); }
 __device__ __forceinline__ float rsqrt(float a) { return 1.0f / __builtin_sqrtf(a); }
 
-// exp(x) in fp32 from the hardware base-2 exponential: x*log2(e) is split into
-// t + e exactly (FMA residual plus the low part of log2(e)), 2^t comes from
-// v_exp_f32 and the factor 2^e ~ 1 + e*ln2 is applied with one FMA.  Results
-// below 2^-64 are computed as 2^(t+64) * 2^-64 (one rounding into the
-// denormal range).  Branch-free; error within a few ulp of the exact value.
+// exp(x) in fp32 as 2^t with t = RN(x*log2(e)) and the hardware base-2
+// exponential.  The rounding of t moves the result by a relative
+// ln(2)*|t|*2^-24 (<= 5.2e-6 for results in the normal range, |t| < 126), the
+// rounded log2(e) constant (relative 1.3e-8) by ln(2)*|t|*1.3e-8 (<= 1.1e-6),
+// plus one ulp of v_exp_f32: at most 6.5e-6 relative, inside the 1e-5 fp32
+// tolerance and far inside one bf16 ulp.  Results below 2^-64 are computed as 2^(t+64) * 2^-64
+// (one rounding into the denormal range).
 __device__ __forceinline__ float exp_f32(float x) {
   const float t = x * 0x1.715476p+0f;
-  float e = __builtin_fmaf(x, 0x1.715476p+0f, -t);
-  e = __builtin_fmaf(x, 0x1.4ae0c0p-26f, e);
   const bool tiny = t < -64.0f;
-  float r = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t);
-  const float c = __builtin_fmaf(r, e * 0x1.62e430p-1f, r);
-  // |t| >= 126: inf, 0, NaN or a denormal; the residual is not needed there
-  r = __builtin_fabsf(t) < 126.0f ? c : r;
+  const float r = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t);
   return tiny ? r * 0x1p-64f : r;
 }
 
@@ -181,7 +178,10 @@ using kExact = std::integral_constant<bool, true>;
 struct Guard {
   float qmax = 0.0f;
   int emin = 0, emax = 0;
-  __device__ __forceinline__ bool bad() const { return !(qmax <= 0x1p+100f) || emin < -96 || emax > 40; }
+  int dmin = 0, dmax = 0; // exponent range of div_rn dividends and quotients
+  __device__ __forceinline__ bool bad() const {
+    return !(qmax <= 0x1p+100f) || emin < -96 || emax > 40 || dmin < -96 || dmax > 100;
+  }
   // per-row divisor check: r = RN(1/b) must be a normal number with exponent
   // in [-96, 40] (so |b| >= 2^-41 and the reciprocal is exact-rounded normal)
   __device__ __forceinline__ void divisor(float r) {
@@ -218,6 +218,29 @@ __device__ __forceinline__ float rint_div(float a, float b, float r, Guard &g, E
 
 // float already holding an integral value (or +-inf/NaN) -> integer type T:
 // no rounding step; saturating or wrapping as the cast requests.
+// RN(a / b) given r = RN(1/b), computed once per row: one Markstein
+// correction of a*r (see rint_div), then v_div_fixup_f32 for the IEEE results
+// of zero, infinite and NaN operands (it also keeps the sign of a zero
+// quotient).  Exactness envelope: the row's reciprocal passed Guard::divisor,
+// and the dividend and quotient have frexp exponents in [-96, 100] (zero
+// counts as 0): then q0 = a*r is normal, the FMA residual a - q0*b is a
+// multiple of 2^(ea-47) >= 2^-149 below 2^(ea-23), hence representable, and
+// q1 is normal.  Outside it the caller recomputes with IEEE division.
+template <typename EX>
+__device__ __forceinline__ float div_rn(float a, float b, float r, Guard &g, EX) {
+  if constexpr (EX::value) {
+    return a / b;
+  } else {
+    float q = a * r;
+    const float e = __builtin_fmaf(-q, b, a);
+    q = __builtin_fmaf(e, r, q);
+    q = __builtin_amdgcn_div_fixupf(q, b, a);
+    const int ea = __builtin_amdgcn_frexp_expf(a), eq = __builtin_amdgcn_frexp_expf(q);
+    asm volatile("v_min3_i32 %0, %0, %2, %3\n\tv_max_i32 %1, %1, %3" : "+v"(g.dmin), "+v"(g.dmax) : "v"(ea), "v"(eq));
+    return q;
+  }
+}
+
 template <typename T, bool SAT> __device__ __forceinline__ T integral_to_int(float r) {
   if constexpr (SAT) {
     return f32_to_int<T, TRUNC, true>(r);
