@@ -190,6 +190,8 @@ def entries():
     e["w8a8_ragged_dma"] = g.w8a8_dequant(300, 200, 192)
     e["w8a8_kn"] = g.w8a8_dequant(320, 256, 128, b_layout="kn")
     e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
+    e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)
+    e["mm_i8_ragged"] = g.mm_i8(300, 200, 192)
     e["bf16_mmad_256"] = g.bf16_mmad(256, 256, 256)
     e["cast_modes"] = cast_modes(4096)
     e["eltwise_mix"] = eltwise_mix(64, 1000)

@@ -179,6 +179,22 @@ def w8a8_dequant(m=4096, n=4096, k=4096, b_layout="nk"):
 """
 
 
+def mm_i8(m=4096, n=4096, k=4096):
+    """int8 x int8 -> int32 contraction (B in the [N, K] weight layout) with no
+    epilogue: the exact accumulator is the group's output."""
+    A, B, C = _t([m, k], "i8"), _t([n, k], "i8"), _t([m, n], "i32")
+    return f"""module {{
+  func.func @mm_i8(%a: {A}, %b: {B}, %c: {C}) -> {C}
+      {_ATTRS.format(kind='SINGLE_CUBE')} {{
+    %c0 = arith.constant 0 : i32
+    %acc0 = linalg.fill ins(%c0 : i32) outs(%c : {C}) -> {C}
+    %acc = linalg.matmul_transpose_b ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
+    return %acc : {C}
+  }}
+}}
+"""
+
+
 def bf16_mmad(m=4096, n=4096, k=4096):
     """bf16 contraction (hivm.hir.mmadL1 bf16 -> f32) with a bf16 output cast."""
     A, B = _t([m, k], "bf16"), _t([n, k], "bf16")

@@ -127,6 +127,17 @@ def test_w8a8(gpu, name, m, n, k):
     assert np.array_equal(out, ref), f"max {bf16_ulp_diff(out, ref).max()} ulp"
 
 
+def test_mm_i8_ragged(gpu):
+    """int8 contraction with no epilogue: the raw int32 accumulator, exact."""
+    note("mm_i8_ragged")
+    s = I.SEED_BASE + 45
+    a, b = I.int8_uniform(s, (300, 192)), I.int8_uniform(s + 1, (200, 192))
+    c, = run_gpu("mm_i8_ragged", [a, b, zeros((300, 200), np.int32)], gpu)
+    rc, = run_oracle("mm_i8_ragged", [a, b, zeros((300, 200), np.int32)])
+    assert np.array_equal(c, rc)
+    assert np.array_equal(c.astype(np.int64), a.astype(np.int64) @ b.astype(np.int64).T)
+
+
 @pytest.mark.parametrize("name,m,n,k", [("bf16_mmad_256", 256, 256, 256), ("bf16_mmad_ragged", 200, 136, 96)])
 def test_bf16_mmad(gpu, name, m, n, k):
     note(name)
