@@ -32,6 +32,7 @@ Elem parseElem(const std::string &s); // throws on unknown
 
 struct Type {
   bool tensor = false;
+  bool memref = false; // a memref<...> (read as a tensor of the same shape)
   Elem elem = Elem::None;
   std::vector<int64_t> shape; // tensor only
   int64_t numel() const {

@@ -658,7 +658,8 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
 std::string resultKind(const Func &f, bool *hasMatmul, bool *hasRWI, bool *hasReduce) {
   *hasMatmul = *hasRWI = *hasReduce = false;
   for (const Op *op : f.ops) {
-    if (op->name == "linalg.matmul" || op->name == "linalg.matmul_transpose_b") *hasMatmul = true;
+    if (op->name == "linalg.matmul" || op->name == "linalg.matmul_transpose_b" || op->name == "hivm.hir.matmul")
+      *hasMatmul = true;
     if (op->name == "hfusion.reduce_with_index") *hasRWI = true;
     if (op->name == "linalg.reduce") *hasReduce = true;
   }
@@ -1595,31 +1596,109 @@ KernelPlan lowerReduceWithIndex(Analysis &A, const std::string &kname) {
 // ======================================================================
 // SINGLE_CUBE: matmul + elementwise epilogue
 // ======================================================================
+// Epilogue of hivm.hir.matmul (HIVMMacroOps.td:373-398): C = descale * (A*B + bias),
+// descale per channel ([N]) or per tensor ([1]) (HIVMAttrs.td:1061-1071).  The
+// op has no CPU lowering in the reference (ConvertHIVMToUpstream has no mmad
+// pattern); the arithmetic here is its documented formula with the accumulator
+// type of the inputs: an integer bias joins the int32 accumulator exactly, then
+// the sum goes to fp32 (round to nearest even); a float bias is added in fp32;
+// the descale multiplies in fp32; the result is rounded to C's type (nearest
+// even, saturating for integer C).
+void hivmMatmulEpilogue(const Op *mm, bool intAcc, std::ostringstream &epi, std::ostringstream &colFields,
+                        std::ostringstream &colLoads, std::string &outExpr) {
+  auto named = [&](const char *k) -> const Value * {
+    auto it = mm->attrs.find(std::string("operand.") + k);
+    return it == mm->attrs.end() ? nullptr : mm->operands.at(std::stoul(it->second));
+  };
+  const Value *bias = named("bias"), *descale = named("descale");
+  const std::string mode = mm->attr("descale_mode", descale ? "DescalePerChannel" : "DescaleNull");
+  if (mode != "DescaleNull" && mode != "DescalePerChannel" && mode != "DescalePerTensor")
+    unsupported(mm, "descale_mode " + mode);
+  if ((mode == "DescaleNull") != (descale == nullptr)) unsupported(mm, "descale operand and descale_mode disagree");
+  auto colLoad = [&](const Value *v, const std::string &nm) {
+    if (v->argIdx < 0) unsupported(mm, "bias/descale must be group arguments");
+    colFields << " " << ctype(v->type.elem) << " " << nm << ";";
+    colLoads << "    Cv." << nm << " = ((const " << mtype(v->type.elem) << "*)P.p" << v->argIdx << ")[n];\n";
+  };
+  auto toF32 = [&](Elem e, const std::string &x) -> std::string {
+    if (e == Elem::BF16) return "hf::bf16_to_f32(" + x + ")";
+    if (e == Elem::F16) return "hf::f16_to_f32(" + x + ")";
+    if (e == Elem::F32) return x;
+    if (isInt(e)) return "hf::int_to_f32<0>((int64_t)(" + x + "))";
+    unsupported(mm, "epilogue operand type");
+  };
+  std::string t = "acc";
+  if (bias) {
+    if (bias->type.shape.size() != 1) unsupported(mm, "bias must be a vector of shape [n]");
+    colLoad(bias, "bias");
+  }
+  if (intAcc && bias && isInt(bias->type.elem)) {
+    epi << "    const int32_t ib = acc + (int32_t)Cv.bias;\n";
+    t = "ib";
+  }
+  epi << "    float t = " << (intAcc ? "hf::int_to_f32<0>((int64_t)(" + t + "))" : t) << ";\n";
+  if (bias && !(intAcc && isInt(bias->type.elem))) epi << "    t = t + " << toF32(bias->type.elem, "Cv.bias") << ";\n";
+  if (descale) {
+    if (mode == "DescalePerChannel") {
+      colLoad(descale, "descale");
+      epi << "    t = t * " << toF32(descale->type.elem, "Cv.descale") << ";\n";
+    } else {
+      if (descale->argIdx < 0) unsupported(mm, "descale must be a group argument");
+      epi << "    t = t * " << toF32(descale->type.elem, "((const " + mtype(descale->type.elem) + "*)P.p" +
+                                                        std::to_string(descale->argIdx) + ")[0]") << ";\n";
+    }
+  }
+  Elem oe = mm->outs[0]->type.elem;
+  if (oe == Elem::F32) outExpr = "t";
+  else if (oe == Elem::BF16) outExpr = "hf::f32_to_bf16<0>(t)";
+  else if (oe == Elem::F16) outExpr = "hf::f32_to_f16<0>(t)";
+  else if (oe == Elem::I8 || oe == Elem::I16 || oe == Elem::I32)
+    outExpr = "hf::f32_to_int<" + ctype(oe) + ", 0, true>(t)";
+  else unsupported(mm, "matmul output type");
+}
+
 KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   Func &f = *A.f;
-  const Op *mm = findOp(f, [](const Op *o) { return o->name == "linalg.matmul" || o->name == "linalg.matmul_transpose_b"; });
-  bool bT = mm->name == "linalg.matmul_transpose_b";
+  const Op *mm = findOp(f, [](const Op *o) {
+    return o->name == "linalg.matmul" || o->name == "linalg.matmul_transpose_b" || o->name == "hivm.hir.matmul";
+  });
+  const bool hivm = mm->name == "hivm.hir.matmul";
+  const bool bT = hivm ? mm->attrs.count("b_transpose") != 0 : mm->name == "linalg.matmul_transpose_b";
+  const bool aT = hivm && mm->attrs.count("a_transpose") != 0;
   const Value *a = mm->ins[0], *b = mm->ins[1];
   if (a->argIdx < 0 || b->argIdx < 0) unsupported(mm, "matmul operands must be group arguments");
-  int64_t M = a->type.shape[0], K = a->type.shape[1];
+  if (a->type.shape.size() != 2 || b->type.shape.size() != 2) unsupported(mm, "matmul operands must be rank 2");
+  int64_t M = aT ? a->type.shape[1] : a->type.shape[0], K = aT ? a->type.shape[0] : a->type.shape[1];
   int64_t N = bT ? b->type.shape[0] : b->type.shape[1];
   if ((bT ? b->type.shape[1] : b->type.shape[0]) != K) unsupported(mm, "matmul shapes");
-  Elem ae = a->type.elem, be = b->type.elem, ce = mm->results[0]->type.elem;
-  bool i8 = ae == Elem::I8 && be == Elem::I8 && ce == Elem::I32;
-  bool bf = ae == Elem::BF16 && be == Elem::BF16 && ce == Elem::F32;
-  if (!i8 && !bf) unsupported(mm, "matmul element types (supported: i8 x i8 -> i32, bf16 x bf16 -> f32)");
+  Elem ae = a->type.elem, be = b->type.elem;
+  int mk = -1;
+  if (ae == Elem::I8 && be == Elem::I8) mk = 0;
+  else if (ae == Elem::BF16 && be == Elem::BF16) mk = 1;
+  else if (ae == Elem::F16 && be == Elem::F16) mk = 2;
+  if (mk < 0) unsupported(mm, "matmul element types (supported: i8 x i8, bf16 x bf16, f16 x f16)");
+  const bool i8 = mk == 0;
+  if (!hivm) {
+    Elem ce = mm->results[0]->type.elem;
+    if (ce != (i8 ? Elem::I32 : Elem::F32)) unsupported(mm, "matmul accumulator type (i32 for i8, f32 for bf16/f16)");
+  }
   const int esz = elemBytes(ae);
   if ((K * esz) % 16 != 0) unsupported(mm, "matmul K must span a multiple of 16 bytes");
   if (!bT && (N * esz) % 16 != 0) unsupported(mm, "matmul N must span a multiple of 16 bytes when B is [K, N]");
-  // B [N, K] with whole 64-byte K steps: both operands stream into LDS by DMA
-  const bool dma = bT && (K * esz) % 64 == 0;
-  const Value *acc0 = mm->outs[0];
-  if (!(acc0->def && acc0->def->name == "linalg.fill" && acc0->def->ins[0]->isConst && acc0->def->ins[0]->fconst == 0.0))
-    unsupported(mm, "matmul accumulator must start from a zero linalg.fill");
+  if (aT && (M * esz) % 16 != 0) unsupported(mm, "matmul M must span a multiple of 16 bytes when A is [K, M]");
+  // B [N, K] and A [M, K] with whole 64-byte K steps: both operands stream into LDS by DMA
+  const bool dma = bT && !aT && (K * esz) % 64 == 0;
+  if (!hivm) {
+    const Value *acc0 = mm->outs[0];
+    if (!(acc0->def && acc0->def->name == "linalg.fill" && acc0->def->ins[0]->isConst && acc0->def->ins[0]->fconst == 0.0))
+      unsupported(mm, "matmul accumulator must start from a zero linalg.fill");
+  } else if (mm->outs.empty() || mm->outs[0]->argIdx < 0 || mm->outs[0]->type.shape != std::vector<int64_t>{M, N}) {
+    unsupported(mm, "hivm.hir.matmul writes a [M, N] group argument");
+  }
   // epilogue over D = [M, N] with the matmul result as the accumulator
   std::set<const Value *> excl = {a, b};
   A.D = {M, N};
-  inferMaps(A, excl);
+  if (!hivm) inferMaps(A, excl);
   // per-element code, plus the operand loads split by their index: [m] once
   // per accumulator row, [n] once per column, [m, n] per element
   std::ostringstream epi, rowFields, rowLoads, colFields, colLoads;
@@ -1654,7 +1733,14 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
       name[v] = "Cv." + nm;
     }
   };
+  std::string hivmOut;
+  if (hivm) {
+    for (const Op *op : f.ops)
+      if (op != mm && !isAlias(op)) unsupported(op, "op beside hivm.hir.matmul in a group");
+    hivmMatmulEpilogue(mm, i8, epi, colFields, colLoads, hivmOut);
+  }
   for (const Op *op : f.ops) {
+    if (hivm) break;
     const std::string &n = op->name;
     if (op == mm || n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" || n == "linalg.fill") continue;
     if (n.rfind("arith.", 0) == 0 && !op->results[0]->type.tensor) continue;
@@ -1678,7 +1764,8 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   if (f.returns.size() != 1) unsupported(mm, "matmul groups must return exactly one tensor");
   const Value *outv = f.returns[0];
   if (outv->type.shape != std::vector<int64_t>{M, N}) unsupported(mm, "matmul group result shape");
-  ensure(outv);
+  if (hivm) name[outv] = hivmOut;
+  else ensure(outv);
   Elem oe = outv->type.elem;
   KernelPlan p;
   p.kernelName = kname;
@@ -1708,16 +1795,17 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
     << "  " << kname << "_args P;\n";
   for (size_t i = 0; i < A.params.size(); ++i)
     k << "  P." << (A.params[i].role == "scalar" ? "s" : "p") << i << " = " << (A.params[i].role == "scalar" ? "s" : "p") << i << ";\n";
-  k << "  hf::" << (i8 ? "mmad_i8" : "mmad_bf16") << "<" << kname << "_epi, " << (bT ? "true" : "false") << ", " << (dma ? "true" : "false") << ">((const "
-    << (i8 ? "int8_t" : "uint16_t") << "*)p" << a->argIdx << ", (const " << (i8 ? "int8_t" : "uint16_t") << "*)p" << b->argIdx
+  k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (aT ? "true" : "false") << ", " << (bT ? "true" : "false") << ", "
+    << (dma ? "true" : "false") << ">((const " << (i8 ? "int8_t" : "uint16_t") << "*)p" << a->argIdx << ", (const "
+    << (i8 ? "int8_t" : "uint16_t") << "*)p" << b->argIdx
     << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
   p.source = k.str();
   // 256x256 macro-tiles, one workgroup each (XCD-aware order inside the kernel)
   const int64_t TM = 256, TN = 256;
   p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
   p.block[0] = 256;
-  p.variant = std::string(i8 ? "mfma_i32_32x32x32_i8" : "mfma_f32_32x32x16_bf16") + (bT ? ", B [N,K]" : ", B [K,N]") +
-              (dma ? ", LDS DMA ring" : ", register staging");
+  p.variant = std::string(mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
+              (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") + (dma ? ", LDS DMA ring" : ", register staging");
   p.algoOps = 2.0 * (double)M * (double)N * (double)K;
   return p;
 }
@@ -1734,6 +1822,18 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     foldConstants(f);
     Analysis A;
     A.f = &f;
+    // destination-style hivm ops on memrefs (no SSA result): the written
+    // `outs` argument becomes the group's result, tied to that argument
+    for (Op *op : f.ops)
+      if (op->name.rfind("hivm.hir.", 0) == 0 && op->results.empty() && !op->outs.empty()) {
+        Value *r = m.newValue();
+        r->type = op->outs[0]->type;
+        r->def = op;
+        r->resultIdx = 0;
+        r->name = op->outs[0]->name + "#written";
+        op->results.push_back(r);
+        if (f.returns.empty()) f.returns.push_back(r);
+      }
     describeBuffers(A);
     bool hasMM, hasRWI, hasRed;
     std::string kind = resultKind(f, &hasMM, &hasRWI, &hasRed);

@@ -192,8 +192,12 @@ std::vector<Token> lex(const std::string &t) {
 
 Type parseTypeText(const std::string &s, int line) {
   Type ty;
-  if (s.rfind("tensor<", 0) == 0) {
-    std::string inner = s.substr(7, s.size() - 8);
+  // memref<...> (destination-style hivm ops on global memory) reads like a
+  // tensor: the shape and element type; the layout / address space after the
+  // first comma is dropped
+  const bool isMemref = s.rfind("memref<", 0) == 0;
+  if (s.rfind("tensor<", 0) == 0 || isMemref) {
+    std::string inner = isMemref ? s.substr(7, s.size() - 8) : s.substr(7, s.size() - 8);
     // strip optional encoding ", #enc"
     auto comma = inner.find(',');
     if (comma != std::string::npos) inner = inner.substr(0, comma);
@@ -201,6 +205,7 @@ Type parseTypeText(const std::string &s, int line) {
     for (char c : inner)
       if (!std::isspace((unsigned char)c)) cleaned += c;
     ty.tensor = true;
+    ty.memref = isMemref;
     size_t p = 0;
     while (true) {
       size_t x = cleaned.find('x', p);
@@ -465,6 +470,27 @@ private:
         ++pos_;
         if (isIns) parseOperandList(op->ins, op->insTypes);
         else parseOperandList(op->outs, op->outsTypes);
+        continue;
+      }
+      // named operand of an hivm op: `bias = %v : type`, `descale = %v : type`
+      if (t.kind == Tok::Ident && isP(peek(1), "=") && peek(2).kind == Tok::Value) {
+        op->attrs["operand." + t.text] = std::to_string(op->operands.size());
+        pos_ += 2;
+        op->operands.push_back(lookup(peek().text, peek().line));
+        ++pos_;
+        if (isP(peek(), ":")) { ++pos_; parseType(); }
+        continue;
+      }
+      // `descale_mode = #hivm.descale_mode<DescalePerChannel>`
+      if (t.kind == Tok::Ident && isP(peek(1), "=") && peek(2).kind == Tok::Hash) {
+        op->attrs[t.text] = normAttr(peek(2).text);
+        pos_ += 3;
+        continue;
+      }
+      // unit flags of hivm matmuls
+      if (t.kind == Tok::Ident && (t.text == "a_transpose" || t.text == "b_transpose")) {
+        op->attrs[t.text] = "unit";
+        ++pos_;
         continue;
       }
       if (t.kind == Tok::Ident && t.text == "dimensions" && isP(peek(1), "=")) {

@@ -1,10 +1,12 @@
 // Dense contraction (hivm.hir.mmadL1 / linalg.matmul) with a fused epilogue on
 // CDNA4 matrix cores.
 //
-// C[m, n] = sum_k A[m, k] * B(k, n), A row-major [M, K], B either [N, K]
-// (matmul_transpose_b, the weight layout) or [K, N] (linalg.matmul).
+// C[m, n] = sum_k A(m, k) * B(k, n), A row-major [M, K] (or [K, M],
+// hivm a_transpose), B either [N, K] (matmul_transpose_b / b_transpose, the
+// weight layout) or [K, N] (linalg.matmul).
 //   * int8 x int8 -> int32 with v_mfma_i32_32x32x32_i8 (exact integer sums);
-//   * bf16 x bf16 -> fp32 with v_mfma_f32_32x32x16_bf16.
+//   * bf16 x bf16 -> fp32 with v_mfma_f32_32x32x16_bf16;
+//   * f16 x f16 -> fp32 with v_mfma_f32_32x32x16_f16.
 // One 256x256 macro-tile per workgroup of 4 waves (2 x 2, 128x128 each =
 // 4 x 4 MFMA tiles of 32x32), K advanced 64 bytes at a time.
 //   * DMA path (B [N, K], K spanning a multiple of 64 bytes): a 4-slot LDS
@@ -31,19 +33,31 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr int MM_TM = 256, MM_TN = 256, MM_BK = 64; // BK in bytes
 constexpr int MM_LDS_STRIDE = MM_BK + 16;             // 80 B rows: conflict-free b128 reads
 
-template <bool I8> struct MfmaOp;
-template <> struct MfmaOp<true> {
+// Matrix-core kinds: int8 -> int32, bf16 -> fp32, f16 -> fp32 (32x32 tiles;
+// each lane feeds 16 bytes of A and of B per instruction, 32 bytes of K).
+enum MmadKind : int { MK_I8 = 0, MK_BF16 = 1, MK_F16 = 2 };
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+template <int MK> struct MfmaOp;
+template <> struct MfmaOp<MK_I8> {
   using acc_t = v16i;
   using scalar_t = int32_t;
   __device__ __forceinline__ static acc_t run(v4i a, v4i b, acc_t c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
   }
 };
-template <> struct MfmaOp<false> {
+template <> struct MfmaOp<MK_BF16> {
   using acc_t = v16f;
   using scalar_t = float;
   __device__ __forceinline__ static acc_t run(v4i a, v4i b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+  }
+};
+template <> struct MfmaOp<MK_F16> {
+  using acc_t = v16f;
+  using scalar_t = float;
+  __device__ __forceinline__ static acc_t run(v4i a, v4i b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
   }
 };
 
@@ -226,10 +240,10 @@ __device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][4], typename Epi
   }
 }
 
-template <bool I8, typename Epi, bool BT, typename ElemT, typename Args>
+template <int MK, typename Epi, bool AT, bool BT, typename ElemT, typename Args>
 __device__ void mmad_core(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
                           int64_t M, int64_t N, int64_t K, const Args &P) {
-  using Op = MfmaOp<I8>;
+  using Op = MfmaOp<MK>;
   using acc_t = typename Op::acc_t;
   constexpr int ESZ = sizeof(ElemT);
   __shared__ __attribute__((aligned(16))) char lds[2][2][MM_TM * MM_LDS_STRIDE]; // [buf][A/B]
@@ -248,10 +262,12 @@ __device__ void mmad_core(const ElemT *__restrict__ A, const ElemT *__restrict__
     for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
 
   v4i ra[4], rb[4];
-  mm_load_kmajor(A, M, m0, Kb, 0, ra);
+  if constexpr (!AT) mm_load_kmajor(A, M, m0, Kb, 0, ra);
+  else mm_load_nmajor<ESZ>(reinterpret_cast<const char *>(A), M, K, m0, 0, ra);
   if constexpr (BT) mm_load_kmajor(B, N, n0, Kb, 0, rb);
   else mm_load_nmajor<ESZ>(reinterpret_cast<const char *>(B), N, K, n0, 0, rb);
-  mm_store_kmajor(lds[0][0], ra);
+  if constexpr (!AT) mm_store_kmajor(lds[0][0], ra);
+  else mm_store_nmajor<ESZ>(lds[0][0], ra);
   if constexpr (BT) mm_store_kmajor(lds[0][1], rb);
   else mm_store_nmajor<ESZ>(lds[0][1], rb);
   __syncthreads();
@@ -262,7 +278,8 @@ __device__ void mmad_core(const ElemT *__restrict__ A, const ElemT *__restrict__
     const bool more = s + 1 < nsteps;
     if (more) {
       const int64_t k0 = (int64_t)(s + 1) * MM_BK;
-      mm_load_kmajor(A, M, m0, Kb, k0, ra);
+      if constexpr (!AT) mm_load_kmajor(A, M, m0, Kb, k0, ra);
+      else mm_load_nmajor<ESZ>(reinterpret_cast<const char *>(A), M, K, m0, k0, ra);
       if constexpr (BT) mm_load_kmajor(B, N, n0, Kb, k0, rb);
       else mm_load_nmajor<ESZ>(reinterpret_cast<const char *>(B), N, K, n0, k0, rb);
     }
@@ -283,7 +300,8 @@ __device__ void mmad_core(const ElemT *__restrict__ A, const ElemT *__restrict__
         for (int j = 0; j < 4; ++j) acc[i][j] = Op::run(fa[i], fb[j], acc[i][j]);
     }
     if (more) {
-      mm_store_kmajor(lds[cur ^ 1][0], ra);
+      if constexpr (!AT) mm_store_kmajor(lds[cur ^ 1][0], ra);
+      else mm_store_nmajor<ESZ>(lds[cur ^ 1][0], ra);
       if constexpr (BT) mm_store_kmajor(lds[cur ^ 1][1], rb);
       else mm_store_nmajor<ESZ>(lds[cur ^ 1][1], rb);
     }
@@ -328,10 +346,10 @@ __device__ __forceinline__ void mmd_issue_operand(const char *__restrict__ base,
   }
 }
 
-template <bool I8, typename Epi, typename ElemT, typename Args>
+template <int MK, typename Epi, typename ElemT, typename Args>
 __device__ void mmad_core_dma(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
                               int64_t M, int64_t N, int64_t K, const Args &P) {
-  using Op = MfmaOp<I8>;
+  using Op = MfmaOp<MK>;
   using acc_t = typename Op::acc_t;
   constexpr int ESZ = sizeof(ElemT);
   __shared__ __attribute__((aligned(1024))) char lds[MMD_STAGES][2][MMD_SLICE]; // [stage][A/B]
@@ -443,18 +461,15 @@ __device__ void mmad_core_dma(const ElemT *__restrict__ A, const ElemT *__restri
   mm_epilogue_lds<Epi>(acc, out, M, N, m0, n0, wm, wn, lane, P, &lds[0][0][0], (int)sizeof(lds));
 }
 
-template <typename Epi, bool BT, bool DMA, typename Args>
-__device__ __forceinline__ void mmad_i8(const int8_t *A, const int8_t *B, typename Epi::out_t *out, int64_t M, int64_t N,
-                                        int64_t K, const Args &P) {
-  if constexpr (DMA) mmad_core_dma<true, Epi>(A, B, out, M, N, K, P);
-  else mmad_core<true, Epi, BT>(A, B, out, M, N, K, P);
-}
-
-template <typename Epi, bool BT, bool DMA, typename Args>
-__device__ __forceinline__ void mmad_bf16(const uint16_t *A, const uint16_t *B, typename Epi::out_t *out, int64_t M,
-                                          int64_t N, int64_t K, const Args &P) {
-  if constexpr (DMA) mmad_core_dma<false, Epi>(A, B, out, M, N, K, P);
-  else mmad_core<false, Epi, BT>(A, B, out, M, N, K, P);
+// Entry: MK selects the matrix-core kind; A is [M, K] (or [K, M] with AT), B is
+// [N, K] with BT (the weight layout) or [K, N]; DMA selects the LDS DMA ring
+// (requires !AT, BT and K spanning a multiple of 64 bytes).
+template <int MK, typename Epi, bool AT, bool BT, bool DMA, typename ElemT, typename Args>
+__device__ __forceinline__ void mmad(const ElemT *A, const ElemT *B, typename Epi::out_t *out, int64_t M, int64_t N, int64_t K,
+                                     const Args &P) {
+  static_assert(!DMA || (!AT && BT), "the DMA ring takes K-contiguous A and B");
+  if constexpr (DMA) mmad_core_dma<MK, Epi>(A, B, out, M, N, K, P);
+  else mmad_core<MK, Epi, AT, BT>(A, B, out, M, N, K, P);
 }
 
 } // namespace hf

@@ -191,6 +191,16 @@ def entries():
     e["w8a8_kn"] = g.w8a8_dequant(320, 256, 128, b_layout="kn")
     e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
     e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)
+    # hivm.hir.matmul forms of bishengir/test/Dialect/HIVM/IR/ops.mlir (16x16 f16) and wider
+    e["hivm_mm_f16_null"] = g.hivm_matmul(16, 16, 16)
+    e["hivm_mm_f16_bias_pc"] = g.hivm_matmul(16, 16, 16, bias="f16", descale="f16", descale_mode="DescalePerChannel")
+    e["hivm_mm_f16_bias_pt_t"] = g.hivm_matmul(16, 16, 16, bias="f16", descale="f16", descale_mode="DescalePerTensor",
+                                               a_t=True, b_t=True)
+    e["hivm_mm_i8_pc"] = g.hivm_matmul(300, 200, 192, elem="i8", out="bf16", bias="i32", descale="f32",
+                                       descale_mode="DescalePerChannel", b_t=True)
+    e["hivm_mm_i8_pt_i8out"] = g.hivm_matmul(256, 320, 128, elem="i8", out="i8", descale="f32",
+                                             descale_mode="DescalePerTensor", b_t=True)
+    e["hivm_mm_bf16_at"] = g.hivm_matmul(160, 96, 64, elem="bf16", out="f32", bias="f32", a_t=True)
     e["mm_i8_ragged"] = g.mm_i8(300, 200, 192)
     e["bf16_mmad_256"] = g.bf16_mmad(256, 256, 256)
     e["cast_modes"] = cast_modes(4096)

@@ -195,6 +195,45 @@ def mm_i8(m=4096, n=4096, k=4096):
 """
 
 
+def hivm_matmul(m, n, k, elem="f16", out="f16", bias=None, descale=None, descale_mode=None, a_t=False, b_t=False,
+                name="hivm_matmul"):
+    """hivm.hir.matmul on global memrefs (HIVMMacroOps.td:410-446), written like
+    bishengir/test/Dialect/HIVM/IR/ops.mlir:135-167: C = descale * (A*B + bias)
+    with optional bias [n], descale [n] (per channel) or [1] (per tensor), and
+    optional a_transpose / b_transpose."""
+    gm = ", #hivm.address_space<gm>"
+    mr = lambda shape, e: "memref<" + "".join(f"{d}x" for d in shape) + e + gm + ">"
+    A = mr([k, m] if a_t else [m, k], elem)
+    B = mr([n, k] if b_t else [k, n], elem)
+    C = mr([m, n], out)
+    args = [f"%A_gm: {A}", f"%B_gm: {B}"]
+    extra = []
+    if bias:
+        args.append(f"%bias_gm: {mr([n], bias)}")
+        extra.append(f"bias = %bias_gm : {mr([n], bias)}")
+    if descale:
+        dshape = [n] if descale_mode == "DescalePerChannel" else [1]
+        args.append(f"%descale_gm: {mr(dshape, descale)}")
+        extra.append(f"descale = %descale_gm : {mr(dshape, descale)}")
+    if a_t:
+        extra.append("a_transpose")
+    if b_t:
+        extra.append("b_transpose")
+    extra.append(f"descale_mode = #hivm.descale_mode<{descale_mode or 'DescaleNull'}>")
+    args.append(f"%res_gm: {C}")
+    tail = "\n       ".join(extra)
+    return f"""module {{
+  func.func @{name}({", ".join(args)}) {{
+    hivm.hir.matmul
+       ins(%A_gm, %B_gm : {A}, {B})
+       outs(%res_gm : {C})
+       {tail}
+    return
+  }}
+}}
+"""
+
+
 def bf16_mmad(m=4096, n=4096, k=4096):
     """bf16 contraction (hivm.hir.mmadL1 bf16 -> f32) with a bf16 output cast."""
     A, B = _t([m, k], "bf16"), _t([n, k], "bf16")

@@ -115,9 +115,10 @@ class T:
 
 def parse_type(s):
     s = s.strip()
-    m = re.fullmatch(r"tensor<(.*)>", s)
+    m = re.fullmatch(r"(?:tensor|memref)<(.*)>", s)
     if m:
-        parts = m.group(1).replace(" ", "").split("x")
+        body = _split_top(m.group(1))[0]  # memref layout / address space after the first comma
+        parts = body.replace(" ", "").split("x")
         return tuple(int(p) for p in parts[:-1]), parts[-1]
     return None, s
 
@@ -305,11 +306,17 @@ def _statements(body):
             cur, depth = "", 0
     merged = []
     for s in out:
-        if merged and s.strip().startswith("("):
+        st = s.strip()
+        if merged and (st.startswith("(") or st.startswith(_HIVM_CONT)):
             merged[-1] += " " + s
         else:
             merged.append(s)
     return merged
+
+
+# clause keywords that continue a multi-line hivm op (HIVMMacroOps.td:432-446)
+_HIVM_CONT = ("ins(", "outs(", "bias", "descale", "a_transpose", "b_transpose", "tiling_params", "block_sizes",
+              "process_sizes", "swizzle_", "epilogue_p_tiles")
 
 
 def _split_top(s, sep=","):
@@ -418,13 +425,60 @@ class Interp:
                 if a.shape != shape:
                     raise ValueError(f"{nm}: expected shape {shape}, got {a.shape}")
                 env[nm] = T(a.copy(), elem)
+        self.written = []
         for st in _statements(body):
             s = st.strip()
             if s.startswith("return") or s.startswith("func.return"):
                 names = re.findall(r"%[\w.$#-]+", s.split(":")[0])
-                return [env[n].a for n in names]
+                # destination-style (memref) groups return what their ops wrote
+                return [env[n].a for n in names] if names else [env[n].a for n in self.written]
+            if s.startswith("hivm.hir.matmul"):
+                self._hivm_matmul(s, env)
+                continue
             self._exec(s, env)
         raise ValueError("function without return")
+
+    def _hivm_matmul(self, s, env):
+        """hivm.hir.matmul (HIVMMacroOps.td:373-398): C = descale * (A*B + bias),
+        written into the `outs` memref.  The reference has no CPU lowering for
+        it; this is the documented formula with the accumulator of the input
+        type (exact int32 for i8, serial fp32 over k for bf16/f16); an integer
+        bias joins the int32 accumulator, then fp32 (RNE); a float bias is
+        added in fp32; the descale (per channel [N] or per tensor [1])
+        multiplies in fp32; the result rounds to C's type (RNE, saturating for
+        integer C)."""
+        ins, _ = _operands(_group(s, "ins"))
+        outs, _ = _operands(_group(s, "outs"))
+        A, B, C = env[ins[0]], env[ins[1]], env[outs[0]]
+        at, bt = "a_transpose" in s, "b_transpose" in s
+        a = np.ascontiguousarray(A.a.T if at else A.a)
+        M, K = a.shape
+        N = C.a.shape[1]
+        # the serial matmul takes B as [K, N] (bt=0) or [N, K] (bt=1)
+        b = np.ascontiguousarray(B.a)
+        if A.elem == "i8":
+            acc = np.zeros((M, N), np.int32)
+            lib().hfref_matmul_i8_i32(ptr(a), ptr(b), ptr(acc), M, N, K, int(bt))
+        else:
+            acc = np.zeros((M, N), np.float32)
+            lib().hfref_matmul_f32(ptr(np.ascontiguousarray(to_f32(T(a, A.elem)))), ptr(np.ascontiguousarray(to_f32(T(b, B.elem)))),
+                                   ptr(acc), M, N, K, int(bt))
+        bm = re.search(r"\bbias\s*=\s*(%[\w.$-]+)", s)
+        dm = re.search(r"\bdescale\s*=\s*(%[\w.$-]+)", s)
+        mode = _attr(s, "descale_mode") or ("DescalePerChannel" if dm else "DescaleNull")
+        bias = env[bm.group(1)] if bm else None
+        if A.elem == "i8" and bias is not None and bias.elem in BITS:
+            acc = (acc.astype(np.int64) + bias.a.astype(np.int64)[None, :]).astype(np.int32)
+            bias = None
+        t = convert(T(acc, "i32" if A.elem == "i8" else "f32"), "f32").a
+        if bias is not None:
+            t = (t + to_f32(bias)[None, :]).astype(np.float32)
+        if dm:
+            d = to_f32(env[dm.group(1)])
+            t = (t * (d[None, :] if mode == "DescalePerChannel" else d[0])).astype(np.float32)
+        tf = T(np.ascontiguousarray(t, np.float32), "f32")
+        env[outs[0]] = declared_cast(tf, C.elem, 0, True) if C.elem in BITS else convert(tf, C.elem)
+        self.written.append(outs[0])
 
     def _exec(self, s, env):
         m = re.match(r"^\s*(%[\w.$-]+)(?::(\d+))?\s*=\s*([\w.]+)(.*)$", s)

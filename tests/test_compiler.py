@@ -142,7 +142,41 @@ func.func @rms_norm_f32(%x: tensor<256x128xf32>, %gamma: tensor<128xf32>, %out0:
     assert "0x1p-7f" in src  # 1/128 folded from tensor.dim -> uitofp -> divf
 
 
+HIVM_OPS_MLIR = """// hivm.hir.matmul as written in bishengir/test/Dialect/HIVM/IR/ops.mlir:135-149
+func.func @test_matmul_descale_perchannel(%A_gm : memref<16x16xf16, #hivm.address_space<gm>>,
+                               %B_gm :  memref<16x16xf16, #hivm.address_space<gm>>,
+                               %bias_gm : memref<16xf16, #hivm.address_space<gm>>,
+                               %descale_perchannel_gm :  memref<16xf16, #hivm.address_space<gm>>,
+                               %res_gm :memref<16x16xf16, #hivm.address_space<gm>> ) {
+  hivm.hir.matmul
+       ins(%A_gm, %B_gm:
+           memref<16x16xf16, #hivm.address_space<gm>>, memref<16x16xf16, #hivm.address_space<gm>>)
+       outs(%res_gm : memref<16x16xf16, #hivm.address_space<gm>>)
+       bias = %bias_gm : memref<16xf16, #hivm.address_space<gm>>
+       descale = %descale_perchannel_gm :  memref<16xf16, #hivm.address_space<gm>>
+       descale_mode = #hivm.descale_mode<DescalePerChannel>
+  return
+}
+"""
+
+
+def test_hivm_matmul_reference_form_lowers(tmp_path):
+    """The destination-style op on memrefs: the `outs` argument is the written
+    result (tied), bias and descale are per-column loads of the epilogue."""
+    rc, err, prefix = emit(HIVM_OPS_MLIR, tmp_path)
+    assert rc == 0, err
+    b = hf.parse_manifest(prefix + ".manifest")[0]
+    assert b["kind"] == "SINGLE_CUBE" and "f16" in b["variant"]
+    assert [p["role"] for p in b["params"]] == ["in", "in", "in", "in", "out"]
+    assert [r["tied"] for r in b["results"]] == [4]
+    src = open(prefix + ".hip").read()
+    assert "Cv.bias" in src and "Cv.descale" in src and "hf::f32_to_f16<0>(t)" in src
+
+
 @pytest.mark.parametrize("ir,code,msg", [
+    (HIVM_OPS_MLIR.replace("       descale = %descale_perchannel_gm :  memref<16xf16, #hivm.address_space<gm>>\n", ""), -2,
+     "descale operand and descale_mode disagree"),
+    (HIVM_OPS_MLIR.replace("xf16", "xf64"), -2, "matmul element types"),
     ("func.func @f(%a: tensor<?xf32>) -> tensor<?xf32> { return %a : tensor<?xf32> }", -1, "dynamic shapes"),
     ("module { }", -1, "no func.func"),
     ("""func.func @f(%a: tensor<4x4xf32>, %o: tensor<4xf32>) -> tensor<4xf32> {

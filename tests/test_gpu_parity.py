@@ -138,6 +138,48 @@ def test_mm_i8_ragged(gpu):
     assert np.array_equal(c.astype(np.int64), a.astype(np.int64) @ b.astype(np.int64).T)
 
 
+def _hivm_inputs(name):
+    """Inputs of the hivm.hir.matmul catalog cases, argument order A, B,
+    [bias], [descale], C."""
+    s = I.SEED_BASE + 48
+    f16 = lambda a: np.asarray(a, np.float16).view(np.uint16)
+    if name.startswith("hivm_mm_f16"):
+        a, b = I.normal_f32(s, (16, 16)), I.normal_f32(s + 1, (16, 16))
+        args = [f16(a), f16(b)]
+        if name != "hivm_mm_f16_null":
+            args.append(f16(I.normal_f32(s + 2, (16,))))
+            args.append(f16(I.uniform_f32(s + 3, (16 if name.endswith("_pc") else 1,), 0.5, 2.0)))
+        return args + [np.zeros((16, 16), np.uint16)]
+    if name == "hivm_mm_i8_pc":
+        return [I.int8_uniform(s, (300, 192)), I.int8_uniform(s + 1, (200, 192)),
+                (I.splitmix64(s + 2, 200) % np.uint64(2001)).astype(np.int32) - 1000,
+                I.uniform_f32(s + 3, (200,), 0.001, 0.02), np.zeros((300, 200), np.uint16)]
+    if name == "hivm_mm_i8_pt_i8out":
+        return [I.int8_uniform(s, (256, 128)), I.int8_uniform(s + 1, (320, 128)), np.array([2e-3], np.float32),
+                np.zeros((256, 320), np.int8)]
+    if name == "hivm_mm_bf16_at":
+        return [I.normal_bf16(s, (64, 160)), I.normal_bf16(s + 1, (64, 96)), I.normal_f32(s + 2, (96,)),
+                np.zeros((160, 96), np.float32)]
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["hivm_mm_f16_null", "hivm_mm_f16_bias_pc", "hivm_mm_f16_bias_pt_t", "hivm_mm_i8_pc",
+                                  "hivm_mm_i8_pt_i8out", "hivm_mm_bf16_at"])
+def test_hivm_matmul(gpu, name):
+    """hivm.hir.matmul with bias / descale modes / transposes (written in place
+    into the `outs` memref argument)."""
+    note(name)
+    args = _hivm_inputs(name)
+    out, = run_gpu(name, args, gpu)
+    ref, = run_oracle(name, args)
+    if name.startswith("hivm_mm_i8"):
+        assert np.array_equal(out, ref)               # exact int32 accumulator, same fp32 epilogue
+    elif name.startswith("hivm_mm_f16"):
+        assert bf16_ulp_diff(out, ref).max() <= 1      # f16 bits; fp32 sums in another order
+    else:
+        np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
 @pytest.mark.parametrize("name,m,n,k", [("bf16_mmad_256", 256, 256, 256), ("bf16_mmad_ragged", 200, 136, 96)])
 def test_bf16_mmad(gpu, name, m, n, k):
     note(name)

@@ -485,3 +485,55 @@ def test_cpu_vs_declared_cast_quirk():
     dec, = interp.run(ir, x, np.zeros(4096, np.int8), func="cast_i8_rint", cast_semantics="declared")
     assert cpu[:4].tolist() == [2, -2, 2, 3]
     assert dec[:4].tolist() == [3, -3, 2, 4]
+
+
+# ---------------------------------------------------------------- hivm.hir.matmul
+def _f16(a):
+    return np.asarray(a, np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("name", ["hivm_mm_f16_bias_pc", "hivm_mm_f16_bias_pt_t", "hivm_mm_f16_null"])
+def test_hivm_matmul_f16_formula(name):
+    """C = descale * (A*B + bias) (HIVMMacroOps.td:397) against a float64
+    restatement; the fp32 serial accumulation stays within one f16 ulp."""
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((16, 16)).astype(np.float16)
+    b = rng.standard_normal((16, 16)).astype(np.float16)
+    bias = rng.standard_normal(16).astype(np.float16)
+    ds = rng.uniform(0.5, 2.0, 16).astype(np.float16)
+    if name == "hivm_mm_f16_null":
+        args, ref = [_f16(a), _f16(b)], a.astype(np.float64) @ b.astype(np.float64)
+    elif name == "hivm_mm_f16_bias_pc":
+        args = [_f16(a), _f16(b), _f16(bias), _f16(ds)]
+        ref = (a.astype(np.float64) @ b.astype(np.float64) + bias) * ds.astype(np.float64)[None, :]
+    else:  # a_transpose, b_transpose, per-tensor descale: A given [K, M], B given [N, K]
+        args = [_f16(a.T.copy()), _f16(b.T.copy()), _f16(bias), _f16(ds[:1])]
+        ref = (a.astype(np.float64) @ b.astype(np.float64) + bias) * float(ds[0])
+    out, = interp.run(hf.catalog.get(name), *args, np.zeros((16, 16), np.uint16))
+    got = out.view(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= ulp)
+
+
+def test_hivm_matmul_i8_int_bias_and_saturation():
+    """int8 inputs: an i32 bias joins the exact accumulator; per-tensor descale
+    in fp32; an i8 result rounds half to even and saturates."""
+    rng = np.random.default_rng(8)
+    a = rng.integers(-127, 128, (256, 128)).astype(np.int8)
+    b = rng.integers(-127, 128, (320, 128)).astype(np.int8)
+    ds = np.array([2e-3], np.float32)
+    out, = interp.run(hf.catalog.get("hivm_mm_i8_pt_i8out"), a, b, ds, np.zeros((256, 320), np.int8))
+    acc = a.astype(np.int64) @ b.astype(np.int64).T
+    t = (acc.astype(np.float32) * ds[0]).astype(np.float32)
+    assert np.array_equal(out, np.clip(np.rint(t), -128, 127).astype(np.int8))
+    assert (np.abs(t) > 127.5).any()  # the case exercises saturation
+    bias = rng.integers(-1000, 1000, 200).astype(np.int32)
+    a2 = rng.integers(-127, 128, (300, 192)).astype(np.int8)
+    b2 = rng.integers(-127, 128, (200, 192)).astype(np.int8)
+    dsc = rng.uniform(0.001, 0.02, 200).astype(np.float32)
+    out2, = interp.run(hf.catalog.get("hivm_mm_i8_pc"), a2, b2, bias, dsc, np.zeros((300, 200), np.uint16))
+    acc2 = a2.astype(np.int64) @ b2.astype(np.int64).T + bias.astype(np.int64)
+    t2 = (acc2.astype(np.float32) * dsc[None, :]).astype(np.float32)
+    import torch
+    ref2 = torch.from_numpy(t2).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(out2, ref2)
