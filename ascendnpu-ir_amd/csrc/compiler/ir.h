@@ -21,7 +21,7 @@ struct CompileError : std::runtime_error {
   using std::runtime_error::runtime_error;
 };
 
-enum class Elem { F32, F16, BF16, F64, I1, I8, I16, I32, I64, Index, None };
+enum class Elem { F32, F16, BF16, F64, F8E4M3FN, F8E5M2, I1, I8, I16, I32, I64, Index, None };
 
 const char *elemName(Elem e);
 int elemBytes(Elem e);

@@ -34,6 +34,7 @@ std::string ctype(Elem e) {
   case Elem::F32: return "float";
   case Elem::F64: return "double";
   case Elem::F16: case Elem::BF16: return "uint16_t";
+  case Elem::F8E4M3FN: case Elem::F8E5M2: return "uint8_t";
   case Elem::I1: return "bool";
   case Elem::I8: return "int8_t";
   case Elem::I16: return "int16_t";
@@ -194,6 +195,8 @@ std::string castExpr(const std::string &x, Elem from, Elem to, bool unsignedCast
     if (f == Elem::BF16) return "hf::bf16_to_f32(" + s + ")";
     if (f == Elem::F16) return "hf::f16_to_f32(" + s + ")";
     if (f == Elem::F64) return "((float)(" + s + "))";
+    if (f == Elem::F8E4M3FN) return "hf::fp8_to_f32<0>(" + s + ")";
+    if (f == Elem::F8E5M2) return "hf::fp8_to_f32<1>(" + s + ")";
     throw CompileError("internal: toF32");
   };
   if (isFloat(from) && isFloat(to)) {
@@ -201,6 +204,8 @@ std::string castExpr(const std::string &x, Elem from, Elem to, bool unsignedCast
     std::string f = toF32(x, from);
     if (to == Elem::F32) return f;
     if (to == Elem::BF16) return "hf::f32_to_bf16<0>(" + f + ")";
+    if (to == Elem::F8E4M3FN) return "hf::f32_to_fp8<0, 0, false>(" + f + ")";
+    if (to == Elem::F8E5M2) return "hf::f32_to_fp8<1, 0, false>(" + f + ")";
     return "hf::f32_to_f16<0>(" + f + ")";
   }
   if (isInt(from) && isFloat(to)) {
@@ -210,6 +215,8 @@ std::string castExpr(const std::string &x, Elem from, Elem to, bool unsignedCast
     if (from == Elem::I1) iv = "(int64_t)(" + x + ")";
     if (to == Elem::F64) return "((double)" + iv + ")";
     if (to == Elem::F32) return "hf::int_to_f32<0>(" + iv + ")";
+    if (to == Elem::F8E4M3FN) return "hf::to_fp8<0, 0, false>((double)" + iv + ")";
+    if (to == Elem::F8E5M2) return "hf::to_fp8<1, 0, false>((double)" + iv + ")";
     if (to == Elem::BF16) return "hf::f32_to_bf16<0>((float)hf::round_to_format((double)" + iv + ", 8, -126, 127, 0))";
     return "hf::f32_to_f16<0>((float)hf::round_to_format((double)" + iv + ", 11, -14, 15, 0))";
   }
@@ -242,6 +249,9 @@ std::string declaredCastExpr(const std::string &x, Elem from, Elem to, int mode,
     if (to == Elem::F64) return "((double)" + f + ")";
     if (from == Elem::F64) f = "((float)(" + x + "))";
     if (to == Elem::BF16) return "hf::f32_to_bf16<" + M + ">(" + f + ")";
+    if (to == Elem::F8E4M3FN || to == Elem::F8E5M2)
+      return std::string("hf::f32_to_fp8<") + (to == Elem::F8E4M3FN ? "0" : "1") + ", " + M + ", " + (sat ? "true" : "false") +
+             ">(" + f + ")";
     return "hf::f32_to_f16<" + M + ">(" + f + ")";
   }
   if (isFloat(from) && isInt(to)) {
@@ -255,6 +265,9 @@ std::string declaredCastExpr(const std::string &x, Elem from, Elem to, int mode,
                          : "(int64_t)(" + x + ")";
     if (to == Elem::F32) return "hf::int_to_f32<" + M + ">(" + iv + ")";
     if (to == Elem::F64) return "((double)" + iv + ")";
+    if (to == Elem::F8E4M3FN || to == Elem::F8E5M2)
+      return std::string("hf::to_fp8<") + (to == Elem::F8E4M3FN ? "0" : "1") + ", " + M + ", " + (sat ? "true" : "false") +
+             ">((double)" + iv + ")";
     if (to == Elem::BF16) return "hf::f32_to_bf16<0>((float)hf::round_to_format((double)" + iv + ", 8, -126, 127, " + M + "))";
     return "hf::f32_to_f16<0>((float)hf::round_to_format((double)" + iv + ", 11, -14, 15, " + M + "))";
   }
@@ -1822,6 +1835,20 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     foldConstants(f);
     Analysis A;
     A.f = &f;
+    // annotation.mark {overflow_mode = "saturate"} on a cast's result makes
+    // that cast saturate (Normalize.cpp:4285-4301); the mark itself is dropped
+    for (size_t i = 0; i < f.ops.size();) {
+      Op *op = f.ops[i];
+      if (op->name != "annotation.mark") { ++i; continue; }
+      const std::string mode = op->attr("overflow_mode");
+      for (Value *v : op->operands) {
+        if (mode.find("saturate") != std::string::npos && v->def && v->def->name == "hfusion.cast")
+          v->def->attrs["enable_saturate"] = "true";
+        auto &u = v->users;
+        u.erase(std::remove(u.begin(), u.end(), op), u.end());
+      }
+      f.ops.erase(f.ops.begin() + i);
+    }
     // destination-style hivm ops on memrefs (no SSA result): the written
     // `outs` argument becomes the group's result, tied to that argument
     for (Op *op : f.ops)

@@ -21,6 +21,8 @@ const char *elemName(Elem e) {
   case Elem::F16: return "f16";
   case Elem::BF16: return "bf16";
   case Elem::F64: return "f64";
+  case Elem::F8E4M3FN: return "f8E4M3FN";
+  case Elem::F8E5M2: return "f8E5M2";
   case Elem::I1: return "i1";
   case Elem::I8: return "i8";
   case Elem::I16: return "i16";
@@ -35,7 +37,7 @@ int elemBits(Elem e) {
   case Elem::F32: case Elem::I32: return 32;
   case Elem::F16: case Elem::BF16: case Elem::I16: return 16;
   case Elem::F64: case Elem::I64: case Elem::Index: return 64;
-  case Elem::I8: return 8;
+  case Elem::I8: case Elem::F8E4M3FN: case Elem::F8E5M2: return 8;
   case Elem::I1: return 1;
   default: return 0;
   }
@@ -45,7 +47,8 @@ int elemBytes(Elem e) {
   return b == 1 ? 1 : b / 8;
 }
 bool isFloat(Elem e) {
-  return e == Elem::F32 || e == Elem::F16 || e == Elem::BF16 || e == Elem::F64;
+  return e == Elem::F32 || e == Elem::F16 || e == Elem::BF16 || e == Elem::F64 || e == Elem::F8E4M3FN ||
+         e == Elem::F8E5M2;
 }
 bool isInt(Elem e) {
   return e == Elem::I1 || e == Elem::I8 || e == Elem::I16 || e == Elem::I32 ||
@@ -56,7 +59,7 @@ Elem parseElem(const std::string &s) {
       {"f32", Elem::F32}, {"f16", Elem::F16},   {"bf16", Elem::BF16},
       {"f64", Elem::F64}, {"i1", Elem::I1},     {"i8", Elem::I8},
       {"i16", Elem::I16}, {"i32", Elem::I32},   {"i64", Elem::I64},
-      {"index", Elem::Index}};
+      {"index", Elem::Index}, {"f8E4M3FN", Elem::F8E4M3FN}, {"f8E5M2", Elem::F8E5M2}};
   auto it = m.find(s);
   if (it == m.end()) throw CompileError("unsupported element type '" + s + "'");
   return it->second;
@@ -465,6 +468,9 @@ private:
       if (isP(t, "}")) break; // end of function body
       if (t.kind == Tok::Ident && (t.text == "return" || t.text == "func.return")) break;
       if (t.kind == Tok::Value && statementStart(pos_)) break;
+      // an op name on a later line starts the next statement (ops without
+      // results, such as annotation.mark or hivm.hir.*)
+      if (t.kind == Tok::Ident && t.line > line && t.text.find('.') != std::string::npos) break;
       if (t.kind == Tok::Ident && (t.text == "ins" || t.text == "outs") && isP(peek(1), "(")) {
         bool isIns = t.text == "ins";
         ++pos_;

@@ -90,6 +90,50 @@ template <int MODE> __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   }
 }
 
+// ---------------------------------------------------------------- fp8
+// FMT 0: f8E4M3FN (sign, 4 exponent bits, bias 7, 3 mantissa bits; no
+// infinities, S.1111.111 is NaN, largest finite 448); FMT 1: f8E5M2 (bias 15,
+// 2 mantissa bits, IEEE-style infinities and NaNs, largest finite 57344).
+template <int FMT> __device__ __forceinline__ float fp8_to_f32(uint8_t b) {
+  const float sgn = (b & 0x80) ? -1.0f : 1.0f;
+  if constexpr (FMT == 0) {
+    const int e = (b >> 3) & 15, m = b & 7;
+    if (e == 15 && m == 7) return __builtin_nanf("");
+    return sgn * (e == 0 ? (float)m * 0x1p-9f : __builtin_ldexpf(1.0f + (float)m * 0.125f, e - 7));
+  } else {
+    const int e = (b >> 2) & 31, m = b & 3;
+    if (e == 31) return m == 0 ? sgn * __builtin_inff() : __builtin_nanf("");
+    return sgn * (e == 0 ? (float)m * 0x1p-16f : __builtin_ldexpf(1.0f + (float)m * 0.25f, e - 15));
+  }
+}
+
+// Rounds the exact value x to the fp8 precision under MODE with no upper
+// exponent bound (round_to_format above), then IEEE 754 overflow (7.4) past the
+// largest finite value: nearest modes give infinity (NaN in E4M3FN), trunc and
+// odd the largest finite value, floor / ceil one or the other by sign; SAT
+// clamps to the largest finite value instead.  NaN maps to 0x7F (NaN in both).
+template <int FMT, int MODE, bool SAT> __device__ __forceinline__ uint8_t to_fp8(double x) {
+  constexpr int P = FMT == 0 ? 4 : 3, EMIN = FMT == 0 ? -6 : -14;
+  constexpr double MAXF = FMT == 0 ? 448.0 : 57344.0;
+  if (x != x) return 0x7F;
+  const bool neg = __builtin_signbit(x);
+  const uint8_t s = neg ? 0x80 : 0;
+  double v = __builtin_fabs(round_to_format(x, P, EMIN, 1023, MODE));
+  if (v > MAXF) {
+    const bool to_inf = !SAT && (MODE == RINT || MODE == ROUND || (MODE == FLOOR && neg) || (MODE == CEIL && !neg));
+    if (!to_inf) return (uint8_t)(s | (FMT == 0 ? 0x7E : 0x7B));
+    return (uint8_t)(s | (FMT == 0 ? 0x7F : 0x7C));
+  }
+  if (v == 0.0) return s;
+  int e = ilogb(v);
+  if (e < EMIN) return (uint8_t)(s | (uint8_t)(v * ldexp(1.0, (P - 1) - EMIN)));  // subnormal
+  const int m = (int)((v * ldexp(1.0, -e) - 1.0) * (double)(1 << (P - 1)));
+  return (uint8_t)(s | ((e + (FMT == 0 ? 7 : 15)) << (P - 1)) | m);
+}
+template <int FMT, int MODE, bool SAT> __device__ __forceinline__ uint8_t f32_to_fp8(float f) {
+  return to_fp8<FMT, MODE, SAT>((double)f);
+}
+
 // ---------------------------------------------------------------- ints
 template <int MODE> __device__ __forceinline__ float round_integral(float x) {
   if constexpr (MODE == RINT) return __builtin_roundevenf(x);

@@ -166,6 +166,89 @@ def quant_ties(rows=64, cols=1024):
 """
 
 
+FP8_TYPES = {"e4m3": "f8E4M3FN", "e5m2": "f8E5M2"}
+
+
+def cast_fp8(n=4096):
+    """fp8 casts: f32 -> f8E4M3FN / f8E5M2 under every round mode, with and
+    without saturation; fp8 -> f32; f16 <-> f8E5M2 through f32 (the form of
+    hfusion-normalize-casting-ops.mlir:321-339); and f32 -> i16 / i8 casts whose
+    result carries annotation.mark {overflow_mode = "saturate"}
+    (hfusion-normalize-casting-ops.mlir:53-74)."""
+    X, H = _T([n], "f32"), _T([n], "f16")
+    funcs = []
+    for short, ty in FP8_TYPES.items():
+        O = _T([n], ty)
+        for m in ["rint", "round", "floor", "ceil", "trunc", "odd"]:
+            for sat in (False, True):
+                satattr = ", enable_saturate = true" if sat else ""
+                funcs.append(f"""  func.func @cast_{short}_{m}{"_sat" if sat else ""}(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>{satattr}}} ins(%x : {X}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+        funcs.append(f"""  func.func @dec_{short}(%x: {O}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {O}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    E = _T([n], "f8E5M2")
+    funcs.append(f"""  func.func @f16_to_e5m2(%x: {H}, %o: {E}) -> {E}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {X}
+    %t = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {H}) outs(%e : {X}) -> {X}
+    %r = hfusion.cast {{enable_overflow = true, enable_saturate = false, round_mode = #hfusion.round_mode<rint>}} ins(%t : {X}) outs(%o : {E}) -> {E}
+    return %r : {E}
+  }}""")
+    funcs.append(f"""  func.func @e5m2_to_f16(%x: {E}, %o: {H}) -> {H}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {X}
+    %t = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {E}) outs(%e : {X}) -> {X}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%t : {X}) outs(%o : {H}) -> {H}
+    return %r : {H}
+  }}""")
+    for it in ("i16", "i8"):
+        O = _T([n], it)
+        funcs.append(f"""  func.func @ovf_{it}_trunc(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{enable_overflow = true, round_mode = #hfusion.round_mode<trunc>}} ins(%x : {X}) outs(%o : {O}) -> {O}
+    annotation.mark %r {{overflow_mode = "saturate"}} : {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+def fp8_quant(rows=64, cols=4096):
+    """Dynamic per-token fp8 quantisation (the fp8 counterpart of the int8
+    group): scale = max|x| / 448, q = f8E4M3FN(x / scale) with round to
+    nearest even and saturation."""
+    X, R = _T([rows, cols], "bf16"), _T([rows], "f32")
+    XF, Q = _T([rows, cols], "f32"), _T([rows, cols], "f8E4M3FN")
+    return f"""module {{
+  func.func @fp8_quant(%x: {X}, %q: {Q}, %scale: {R}) -> ({Q}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %zero = arith.constant 0.000000e+00 : f32
+    %fmax = arith.constant 4.480000e+02 : f32
+    %e0 = tensor.empty() : {XF}
+    %xf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {X}) outs(%e0 : {XF}) -> {XF}
+    %e1 = tensor.empty() : {XF}
+    %ax = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%xf : {XF}) outs(%e1 : {XF}) -> {XF}
+    %e2 = tensor.empty() : {R}
+    %i0 = linalg.fill ins(%zero : f32) outs(%e2 : {R}) -> {R}
+    %amax = linalg.reduce {{arith.maximumf}} ins(%ax : {XF}) outs(%i0 : {R}) dimensions = [1]
+    %e3 = tensor.empty() : {R}
+    %sc = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%amax, %fmax : {R}, f32) outs(%scale : {R}) -> {R}
+    %e4 = tensor.empty() : {XF}
+    %bs = linalg.broadcast ins(%sc : {R}) outs(%e4 : {XF}) dimensions = [1]
+    %e5 = tensor.empty() : {XF}
+    %y = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%xf, %bs : {XF}, {XF}) outs(%e5 : {XF}) -> {XF}
+    %qq = hfusion.cast {{round_mode = #hfusion.round_mode<rint>, enable_saturate = true}} ins(%y : {XF}) outs(%q : {Q}) -> {Q}
+    return %qq, %sc : {Q}, {R}
+  }}
+}}
+"""
+
+
 def entries():
     """name -> IR text of every prebuilt group."""
     e = {}
@@ -208,6 +291,9 @@ def entries():
     e["layernorm"] = layernorm(64, 2048)
     e["reduce_ops"] = reduce_ops(48, 3000)
     e["quant_ties"] = quant_ties(64, 1024)
+    e["cast_fp8"] = cast_fp8(4096)
+    e["fp8_quant"] = fp8_quant(64, 4096)
+    e["fp8_quant_ragged"] = fp8_quant(13, 1000)
     return e
 
 

@@ -24,7 +24,8 @@ def torch_dtype(elem):
     if _DTYPES is None:
         _DTYPES = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16, "f64": torch.float64,
                    "i1": torch.bool, "i8": torch.int8, "i16": torch.int16, "i32": torch.int32,
-                   "i64": torch.int64, "index": torch.int64}
+                   "i64": torch.int64, "index": torch.int64, "f8E4M3FN": torch.float8_e4m3fn,
+                   "f8E5M2": torch.float8_e5m2}
     return _DTYPES[elem]
 
 

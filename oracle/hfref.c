@@ -339,6 +339,64 @@ void hfref_compare_i64(int fn, const int64_t *a, const int64_t *b,
   }
 }
 
+/* fp8 (fmt 0: f8E4M3FN, 4-bit exponent bias 7, 3 mantissa bits, no
+   infinities, S.1111.111 = NaN, max 448; fmt 1: f8E5M2, bias 15, 2 mantissa
+   bits, IEEE-style inf/NaN, max 57344).  Encoding rounds the exact value to
+   the format's precision with no upper exponent bound (round_to_format, with
+   subnormals below 2^emin), then applies IEEE 754 overflow (section 7.4) when
+   the result passes the largest finite value: nearest modes give infinity,
+   toward-zero modes (trunc, odd) the largest finite value, floor/ceil one or
+   the other by sign; "infinity" is NaN in E4M3FN.  Saturation clamps to the
+   largest finite value instead. */
+float hfref_fp8_to_f32(uint8_t b, int fmt) {
+  const float sgn = (b & 0x80) ? -1.0f : 1.0f;
+  if (fmt == 0) {
+    int e = (b >> 3) & 15, m = b & 7;
+    if (e == 15 && m == 7) return NAN;
+    return sgn * (e == 0 ? (float)m * 0x1p-9f : ldexpf(1.0f + (float)m / 8.0f, e - 7));
+  }
+  int e = (b >> 2) & 31, m = b & 3;
+  if (e == 31) return m == 0 ? sgn * INFINITY : NAN;
+  return sgn * (e == 0 ? (float)m * 0x1p-16f : ldexpf(1.0f + (float)m / 4.0f, e - 15));
+}
+
+static uint8_t to_fp8(long double x, int fmt, int mode, int sat) {
+  const int P = fmt == 0 ? 4 : 3, EMIN = fmt == 0 ? -6 : -14;
+  const long double MAXF = fmt == 0 ? 448.0L : 57344.0L;
+  if (isnan(x)) return 0x7F;
+  const int neg = signbit(x) != 0;
+  const uint8_t s = neg ? 0x80 : 0;
+  const uint8_t big = (uint8_t)(s | (fmt == 0 ? 0x7E : 0x7B));  /* largest finite */
+  const uint8_t inf = (uint8_t)(s | (fmt == 0 ? 0x7F : 0x7C));  /* inf, or NaN in E4M3FN */
+  long double v = fabsl(round_to_format(x, P, EMIN, 16383, mode)); /* unbounded above */
+  if (v > MAXF) {
+    if (sat) return big;
+    int to_inf;
+    switch (mode) {
+    case 0: case 1: to_inf = 1; break; /* nearest */
+    case 2: to_inf = neg; break;       /* floor */
+    case 3: to_inf = !neg; break;      /* ceil */
+    default: to_inf = 0;               /* trunc, odd */
+    }
+    return to_inf ? inf : big;
+  }
+  if (v == 0.0L) return s;
+  int e = ilogbl(v);
+  if (e < EMIN) return (uint8_t)(s | (uint8_t)ldexpl(v, (P - 1) - EMIN));
+  int m = (int)((ldexpl(v, -e) - 1.0L) * (long double)(1 << (P - 1)));
+  return (uint8_t)(s | ((e + (fmt == 0 ? 7 : 15)) << (P - 1)) | m);
+}
+
+void hfref_fp8_to_f32_n(const uint8_t *in, float *out, int64_t n, int fmt) {
+  for (int64_t i = 0; i < n; ++i) out[i] = hfref_fp8_to_f32(in[i], fmt);
+}
+void hfref_f32_to_fp8_n(const float *in, uint8_t *out, int64_t n, int fmt, int mode, int sat) {
+  for (int64_t i = 0; i < n; ++i) out[i] = to_fp8((long double)in[i], fmt, mode, sat);
+}
+void hfref_int_to_fp8_n(const int64_t *in, uint8_t *out, int64_t n, int fmt, int mode, int sat) {
+  for (int64_t i = 0; i < n; ++i) out[i] = to_fp8((long double)in[i], fmt, mode, sat);
+}
+
 void hfref_bf16_to_f32_n(const uint16_t *in, float *out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = hfref_bf16_to_f32(in[i]);
 }

@@ -76,6 +76,11 @@ void hfref_compare_i64(int fn, const int64_t *a, const int64_t *b,
                        uint8_t *out, int64_t n);
 
 /* conversions over arrays */
+/* fp8: fmt 0 = f8E4M3FN, 1 = f8E5M2 */
+float hfref_fp8_to_f32(uint8_t b, int fmt);
+void hfref_fp8_to_f32_n(const uint8_t *in, float *out, int64_t n, int fmt);
+void hfref_f32_to_fp8_n(const float *in, uint8_t *out, int64_t n, int fmt, int mode, int sat);
+void hfref_int_to_fp8_n(const int64_t *in, uint8_t *out, int64_t n, int fmt, int mode, int sat);
 void hfref_bf16_to_f32_n(const uint16_t *in, float *out, int64_t n);
 void hfref_f32_to_bf16_n(const float *in, uint16_t *out, int64_t n, int mode);
 void hfref_f16_to_f32_n(const uint16_t *in, float *out, int64_t n);

@@ -49,6 +49,9 @@ def lib():
             "hfref_compare_f32": [INT, P, P, P, I64],
             "hfref_compare_i64": [INT, P, P, P, I64],
             "hfref_bf16_to_f32_n": [P, P, I64],
+            "hfref_fp8_to_f32_n": [P, P, I64, INT],
+            "hfref_f32_to_fp8_n": [P, P, I64, INT, INT, INT],
+            "hfref_int_to_fp8_n": [P, P, I64, INT, INT, INT],
             "hfref_f32_to_bf16_n": [P, P, I64, INT],
             "hfref_f16_to_f32_n": [P, P, I64],
             "hfref_f32_to_f16_n": [P, P, I64, INT],
@@ -98,10 +101,12 @@ def ptr(a):
 
 
 # ---------------------------------------------------------------- types
-NP = {"f32": np.float32, "f64": np.float64, "bf16": np.uint16, "f16": np.uint16, "i1": np.bool_,
+FP8 = {"f8E4M3FN": 0, "f8E5M2": 1}
+NP = {"f32": np.float32, "f64": np.float64, "bf16": np.uint16, "f16": np.uint16, "f8E4M3FN": np.uint8, "f8E5M2": np.uint8,
+      "i1": np.bool_,
       "i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64, "index": np.int64}
 BITS = {"i1": 1, "i8": 8, "i16": 16, "i32": 32, "i64": 64, "index": 64}
-FLOATS = ("f32", "f64", "bf16", "f16")
+FLOATS = ("f32", "f64", "bf16", "f16", "f8E4M3FN", "f8E5M2")
 ROUND = {"rint": 0, "round": 1, "floor": 2, "ceil": 3, "trunc": 4, "odd": 5, "truncwithoverflow": 6}
 
 
@@ -137,13 +142,21 @@ def to_f32(v):
         return out
     if v.elem == "f64":
         return a.astype(np.float32)
+    if v.elem in FP8:
+        out = np.empty(a.shape, np.float32)
+        lib().hfref_fp8_to_f32_n(ptr(np.ascontiguousarray(a, np.uint8)), ptr(out), a.size, FP8[v.elem])
+        return out
     raise TypeError(v.elem)
 
 
-def from_f32(f, elem, mode=0):
+def from_f32(f, elem, mode=0, sat=False):
     f = np.ascontiguousarray(f, dtype=np.float32)
     if elem == "f32":
         return f
+    if elem in FP8:
+        out = np.empty(f.shape, np.uint8)
+        lib().hfref_f32_to_fp8_n(ptr(f), ptr(out), f.size, FP8[elem], mode, int(sat))
+        return out
     if elem in ("bf16", "f16"):
         out = np.empty(f.shape, np.uint16)
         getattr(lib(), "hfref_f32_to_bf16_n" if elem == "bf16" else "hfref_f32_to_f16_n")(ptr(f), ptr(out), f.size, mode)
@@ -216,7 +229,7 @@ def declared_cast(v, elem, mode, sat, unsigned=False):
             return T(from_f32(r, elem), elem)
         if elem == "f32":
             return T(f, elem)
-        return T(from_f32(f, elem, mode), elem)
+        return T(from_f32(f, elem, mode, sat), elem)
     if v.elem in FLOATS and elem not in FLOATS:
         f = np.ascontiguousarray(to_f32(v))
         out = np.empty(f.shape, np.int64)
@@ -226,6 +239,10 @@ def declared_cast(v, elem, mode, sat, unsigned=False):
         a64 = np.ascontiguousarray(np.asarray(v.a).astype(np.int64))
         if unsigned or v.elem == "i1":
             a64 = a64 & ((1 << BITS[v.elem]) - 1) if BITS[v.elem] < 64 else a64
+        if elem in FP8:  # one rounding, from the exact integer
+            out = np.empty(a64.shape, np.uint8)
+            lib().hfref_int_to_fp8_n(ptr(a64), ptr(out), a64.size, FP8[elem], mode, int(sat))
+            return T(out, elem)
         f = np.empty(a64.shape, np.float32)
         lib().hfref_int_to_f32_n(ptr(a64), ptr(f), a64.size, mode)
         return T(from_f32(f, elem), elem)
@@ -426,6 +443,13 @@ class Interp:
                     raise ValueError(f"{nm}: expected shape {shape}, got {a.shape}")
                 env[nm] = T(a.copy(), elem)
         self.written = []
+        # annotation.mark {overflow_mode = "saturate"} makes the marked value's
+        # cast saturate (Normalize.cpp:4285-4301)
+        self.sat_marks = set()
+        for st in _statements(body):
+            m = re.match(r"\s*annotation\.mark\s+(%[\w.$-]+).*overflow_mode\s*=\s*\"(\w*)\"", st)
+            if m and "saturate" in m.group(2):
+                self.sat_marks.add(m.group(1))
         for st in _statements(body):
             s = st.strip()
             if s.startswith("return") or s.startswith("func.return"):
@@ -434,6 +458,8 @@ class Interp:
                 return [env[n].a for n in names] if names else [env[n].a for n in self.written]
             if s.startswith("hivm.hir.matmul"):
                 self._hivm_matmul(s, env)
+                continue
+            if s.startswith("annotation.mark"):
                 continue
             self._exec(s, env)
         raise ValueError("function without return")
@@ -591,7 +617,7 @@ class Interp:
             r = T(np.where(np.broadcast_to(c.a, shape), np.broadcast_to(a.a, shape), np.broadcast_to(b.a, shape)).astype(NP[U]), U)
         elif op == "hfusion.cast":
             mode = ROUND[_attr(rest, "round_mode") or "rint"]
-            sat = (_attr(rest, "enable_saturate") == "true")
+            sat = (_attr(rest, "enable_saturate") == "true") or res in self.sat_marks
             x = T(np.broadcast_to(xs[0].a, shape), xs[0].elem)
             if self.cast_semantics == "cpu":
                 if x.elem == U and U in FLOATS:

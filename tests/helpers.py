@@ -19,6 +19,8 @@ def to_dev(a, elem, device):
     t = torch.from_numpy(np.ascontiguousarray(a))
     if elem in ("bf16", "f16"):
         t = t.view(torch.bfloat16 if elem == "bf16" else torch.float16)
+    if elem in ("f8E4M3FN", "f8E5M2"):
+        t = t.view(torch.uint8).view(torch.float8_e4m3fn if elem == "f8E4M3FN" else torch.float8_e5m2)
     return t.to(device)
 
 
@@ -27,6 +29,8 @@ def to_host(t, elem):
     if elem in ("bf16", "f16"):
         t = t.view(torch.int16)
         return t.cpu().numpy().view(np.uint16)
+    if elem in ("f8E4M3FN", "f8E5M2"):
+        return t.view(torch.uint8).cpu().numpy()
     if elem == "i1":
         return t.cpu().numpy().astype(np.bool_)
     return t.cpu().numpy()

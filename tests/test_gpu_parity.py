@@ -233,6 +233,72 @@ def test_cast_int_and_same_type(gpu, mode):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+# ------------------------------------------------------------------ fp8
+def fp8_cast_inputs(n, maxf, seed):
+    """Values across the fp8 range: random, ties of the grid, subnormals,
+    the overflow boundaries, signed zeros, inf and NaN."""
+    r = I.normal_f32(seed, (n - 64,), std=maxf / 8)
+    sp = np.float32([0.0, -0.0, np.inf, -np.inf, np.nan, maxf, -maxf, maxf * 1.03, maxf * 1.04, maxf * 1.0714, maxf * 1.2,
+                     -maxf * 1.2, 1e-9, -1e-9, 2.0 ** -9, 1.5 * 2.0 ** -9, 2.0 ** -16, 2.5 * 2.0 ** -16, 0.5625, 0.59375,
+                     1.0625, 1.1875, 3.25, 13.0, 17.0, 52.0, 416.0, 432.0, 464.0, 240.0, 3e4, 6e4])
+    return np.concatenate([sp, np.resize(sp, 64 - sp.size), r]).astype(np.float32)
+
+
+FP8_FUNCS = [f"cast_{t}_{m}{s}" for t in ("e4m3", "e5m2") for m in ("rint", "round", "floor", "ceil", "trunc", "odd")
+             for s in ("", "_sat")]
+
+
+@pytest.mark.parametrize("func", FP8_FUNCS)
+def test_cast_fp8(gpu, func):
+    note(func)
+    n = 4096
+    maxf = 448.0 if "e4m3" in func else 57344.0
+    x = fp8_cast_inputs(n, maxf, I.SEED_BASE + 80)
+    out, = run_gpu("cast_fp8", [x, zeros(n, np.uint8)], gpu, func=func)
+    ref, = run_oracle("cast_fp8", [x, zeros(n, np.uint8)], func=func)
+    assert np.array_equal(out, ref), f"{int((out != ref).sum())} differ, e.g. x={x[out != ref][:4]}"
+
+
+@pytest.mark.parametrize("func", ["dec_e4m3", "dec_e5m2", "f16_to_e5m2", "e5m2_to_f16", "ovf_i16_trunc", "ovf_i8_trunc"])
+def test_cast_fp8_decode_and_marks(gpu, func):
+    note(func)
+    n = 4096
+    if func.startswith("dec_") or func == "e5m2_to_f16":
+        x = np.resize(np.arange(256, dtype=np.uint8), n)
+    elif func == "f16_to_e5m2":
+        x = fp8_cast_inputs(n, 57344.0, I.SEED_BASE + 81).astype(np.float16).view(np.uint16)
+    else:
+        x = I.normal_f32(I.SEED_BASE + 82, (n,), std=3e4 if "i16" in func else 300.0)
+    o_dt = {"dec": np.float32, "f16_to_e5m2": np.uint8, "e5m2_to_f16": np.uint16, "ovf_i16_trunc": np.int16,
+            "ovf_i8_trunc": np.int8}
+    dt = o_dt["dec"] if func.startswith("dec_") else o_dt[func]
+    out, = run_gpu("cast_fp8", [x, zeros(n, dt)], gpu, func=func)
+    ref, = run_oracle("cast_fp8", [x, zeros(n, dt)], func=func)
+    if dt == np.float32:
+        assert np.array_equal(np.isnan(out), np.isnan(ref))
+        ok = ~np.isnan(ref)
+        assert np.array_equal(out[ok].view(np.uint32), ref[ok].view(np.uint32))
+    elif func == "e5m2_to_f16":
+        nan = (ref & 0x7C00) == 0x7C00
+        assert np.array_equal(out[~nan | ((ref & 0x3FF) == 0)], ref[~nan | ((ref & 0x3FF) == 0)])
+    else:
+        assert np.array_equal(out, ref)
+    if func.startswith("ovf_"):
+        info = np.iinfo(dt)
+        assert (out == info.max).any() and (out == info.min).any()  # saturation happened
+
+
+@pytest.mark.parametrize("name,rows,cols", [("fp8_quant", 64, 4096), ("fp8_quant_ragged", 13, 1000)])
+def test_fp8_quant(gpu, name, rows, cols):
+    note(name)
+    x = I.normal_bf16(I.SEED_BASE + 83, (rows, cols))
+    args = [x, zeros((rows, cols), np.uint8), zeros(rows, np.float32)]
+    q, s = run_gpu(name, args, gpu)
+    rq, rs = run_oracle(name, args)
+    assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(q, rq), f"{int((q != rq).sum())} fp8 codes differ"
+
+
 # ------------------------------------------------------------------ generic lowering
 def test_eltwise_mix(gpu):
     note("eltwise_mix")

@@ -537,3 +537,114 @@ def test_hivm_matmul_i8_int_bias_and_saturation():
     import torch
     ref2 = torch.from_numpy(t2).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(out2, ref2)
+
+
+# ---------------------------------------------------------------- fp8
+FP8_FMT = {"f8E4M3FN": 0, "f8E5M2": 1}
+
+
+def _fp8_values(fmt):
+    """All 256 codes decoded in float64 by enumeration of the bit fields."""
+    out = np.empty(256)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        if fmt == 0:
+            e, m = (b >> 3) & 15, b & 7
+            out[b] = np.nan if (e == 15 and m == 7) else s * (m / 8 * 2.0 ** -6 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
+        else:
+            e, m = (b >> 2) & 31, b & 3
+            out[b] = (s * np.inf if m == 0 else np.nan) if e == 31 else s * (m / 4 * 2.0 ** -14 if e == 0 else (1 + m / 4) * 2.0 ** (e - 15))
+    return out
+
+
+@pytest.mark.parametrize("elem", ["f8E4M3FN", "f8E5M2"])
+def test_fp8_decode_matches_torch(elem):
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    ours = interp.to_f32(interp.T(codes, elem))
+    tdt = torch.float8_e4m3fn if elem == "f8E4M3FN" else torch.float8_e5m2
+    theirs = torch.from_numpy(codes).view(tdt).to(torch.float32).numpy()
+    assert np.array_equal(np.isnan(ours), np.isnan(theirs))
+    ok = ~np.isnan(theirs)
+    assert np.array_equal(ours[ok].view(np.uint32), theirs[ok].view(np.uint32))
+    assert np.array_equal(ours[ok].astype(np.float64), _fp8_values(FP8_FMT[elem])[ok])
+
+
+@pytest.mark.parametrize("elem", ["f8E4M3FN", "f8E5M2"])
+def test_fp8_rint_encode_matches_torch(elem):
+    """arith.truncf f32 -> fp8: nearest-even; E4M3FN overflows to NaN, E5M2 to inf."""
+    import torch
+    x = special_f32(20000, seed=90) / np.float32(1000.0)  # most values in the fp8 range
+    vals = _fp8_values(FP8_FMT[elem])
+    fin = np.unique(np.abs(vals[np.isfinite(vals)]))
+    mids = ((fin[1:] + fin[:-1]) / 2).astype(np.float32)  # exact ties
+    x = np.concatenate([x, mids, -mids, np.float32([448, 464, 465, 480, 500, 57344, 61440, 61441, 1e9, -1e9]),
+                        fin.astype(np.float32)]).astype(np.float32)
+    ours = interp.from_f32(x, elem)
+    tdt = torch.float8_e4m3fn if elem == "f8E4M3FN" else torch.float8_e5m2
+    theirs = torch.from_numpy(x).to(tdt).view(torch.uint8).numpy()
+    dec_o, dec_t = vals[ours], vals[theirs]
+    assert np.array_equal(np.isnan(dec_o), np.isnan(dec_t))
+    ok = ~np.isnan(dec_t)
+    assert np.array_equal(ours[ok], theirs[ok])
+
+
+@pytest.mark.parametrize("elem", ["f8E4M3FN", "f8E5M2"])
+@pytest.mark.parametrize("mode", list(MODES))
+@pytest.mark.parametrize("sat", [False, True])
+def test_fp8_modes_brute_force(elem, mode, sat):
+    """Every round mode against neighbour search on the format's grid extended
+    without an upper exponent bound, then IEEE 754 overflow (7.4) past the
+    largest finite value (infinity is NaN in E4M3FN; saturation clamps)."""
+    fmt = FP8_FMT[elem]
+    vals = _fp8_values(fmt)
+    finite = np.isfinite(vals)
+    maxf = np.nanmax(vals[finite])
+    p, e_hi = (4, 8) if fmt == 0 else (3, 15)
+    # the same precision continued upward: 1.m * 2^e for e above the format
+    ext = [(1 + k / 2 ** (p - 1)) * 2.0 ** e for e in range(e_hi, e_hi + 4) for k in range(2 ** (p - 1))]
+    pos = np.unique(np.concatenate([np.abs(vals[finite]), ext]))
+    grid = np.unique(np.concatenate([pos, -pos]))
+    lsb_odd = {}
+    for g in pos:  # parity of the last significand bit on the extended grid
+        if g == 0:
+            lsb_odd[g] = False
+            continue
+        e = max(int(np.floor(np.log2(g))), -6 if fmt == 0 else -14)
+        lsb_odd[g] = int(round(g / 2.0 ** (e - (p - 1)))) % 2 == 1
+    rng = np.random.default_rng(fmt * 100 + MODES[mode] * 2 + int(sat))
+    x = np.concatenate([rng.uniform(-1.2 * maxf, 1.2 * maxf, 3000), rng.uniform(-2 ** -5, 2 ** -5, 1000),
+                        vals[finite]]).astype(np.float32)
+    ours = interp.declared_cast(interp.T(x, "f32"), elem, MODES[mode], sat).a
+    for xi, o in zip(x.astype(np.float64), ours):
+        lo, hi = grid[grid <= xi].max(), grid[grid >= xi].min()
+        odd = lambda g: lsb_odd[abs(g)]
+        if lo == hi:
+            r = lo
+        elif mode == "floor":
+            r = lo
+        elif mode == "ceil":
+            r = hi
+        elif mode == "trunc":
+            r = lo if xi >= 0 else hi
+        elif mode in ("rint", "round"):
+            dl, dh = xi - lo, hi - xi
+            if dl != dh:
+                r = lo if dl < dh else hi
+            elif mode == "round":
+                r = hi if xi > 0 else lo
+            else:
+                r = hi if odd(lo) else lo
+        else:  # odd: the neighbour with an odd last bit
+            r = lo if odd(lo) else hi
+        if abs(r) > maxf:
+            toward_inf = mode in ("rint", "round") or (mode == "floor" and xi < 0) or (mode == "ceil" and xi > 0)
+            if sat or not toward_inf:
+                r = np.sign(xi) * maxf
+            else:
+                r = np.nan if fmt == 0 else np.sign(xi) * np.inf
+        got = vals[o]
+        if np.isnan(r):
+            assert np.isnan(got), (elem, mode, xi)
+        else:
+            assert got == r and (r != 0 or np.signbit(got) == np.signbit(xi)), (elem, mode, sat, xi, got, r)
