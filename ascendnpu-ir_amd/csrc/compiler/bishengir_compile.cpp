@@ -43,6 +43,8 @@ int main(int argc, char **argv) {
       opts += "hipcc=" + b.substr(7) + ";";
     } else if (startsWith(b, "-emit=")) {
       opts += "emit=" + b.substr(6) + ";";
+    } else if (startsWith(b, "-fusion-kind=")) {
+      opts += "fusion_kind=" + b.substr(13) + ";";
     } else if (b == "-ordered-fp-sums") {
       opts += "ordered_fp_sums=1;";
     } else if (startsWith(b, "-kernel-include=")) {

@@ -1,6 +1,7 @@
 // hfc C-ABI: parse -> ConvertHFusionToHIP -> write P.hip / P.manifest ->
 // hipcc --genco for gfx950 -> P.hsaco.  See include/hfc.h.
 #include "../../../include/hfc.h"
+#include "fusion.h"
 #include "lower.h"
 
 #include <dlfcn.h>
@@ -95,6 +96,30 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
     setErr(err, errlen, std::string("parse error: ") + e.what());
     return HFC_ERR_PARSE;
   }
+  // fusion front-end: functions that are not one group yet are split into
+  // outlined groups plus a launch program
+  std::vector<hfc::ProgramPlan> programs;
+  try {
+    std::string outlined = hfc::outlineFusedGroups(*mod, programs, opts.count("fusion_kind") ? opts["fusion_kind"] : "");
+    if (opts.count("emit") && opts["emit"] == "outlined") {
+      std::string man;
+      for (auto &p : programs) man += hfc::emitProgramManifest(p);
+      if (!writeFile(std::string(outPrefix) + ".outlined.mlir", outlined) ||
+          !writeFile(std::string(outPrefix) + ".programs", man)) {
+        setErr(err, errlen, "cannot write outputs with prefix " + std::string(outPrefix));
+        return HFC_ERR_IO;
+      }
+      return HFC_OK;
+    }
+    if (!programs.empty()) {
+      // kept beside the code object for inspection
+      writeFile(std::string(outPrefix) + ".outlined.mlir", outlined);
+      mod = hfc::parseModule(outlined);
+    }
+  } catch (const hfc::CompileError &e) {
+    setErr(err, errlen, std::string("fusion error: ") + e.what());
+    return HFC_ERR_LOWER;
+  }
   std::vector<hfc::KernelPlan> plans;
   try {
     hfc::LowerOptions lo;
@@ -109,6 +134,7 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
   std::string hsacoName = hsacoPath.substr(hsacoPath.find_last_of('/') == std::string::npos ? 0 : hsacoPath.find_last_of('/') + 1);
   std::string man;
   for (auto &p : plans) man += hfc::emitManifest(p, hsacoName);
+  for (auto &p : programs) man += hfc::emitProgramManifest(p);
   if (!writeFile(hipPath, hfc::emitTranslationUnit(plans)) || !writeFile(manPath, man)) {
     setErr(err, errlen, "cannot write outputs with prefix " + prefix);
     return HFC_ERR_IO;

@@ -62,6 +62,7 @@ struct Value {
 
 struct Op {
   std::string name;                       // e.g. "hfusion.elemwise_binary"
+  size_t srcBegin = 0, srcEnd = 0;        // the statement's span in Module::source
   std::vector<Value *> ins, outs, operands; // operands: non ins/outs operands
   std::vector<Type> insTypes, outsTypes;
   std::vector<Value *> results;
@@ -88,6 +89,7 @@ struct Func {
   std::map<std::string, std::string> attrs;
   std::vector<Op *> ops;
   std::vector<Value *> returns;
+  size_t srcBegin = 0, srcEnd = 0; // `func.func ... }` span in Module::source
   bool isEntry() const { return attrs.count("hacc.entry") != 0; }
   std::string fusionKind() const {
     auto it = attrs.find("hfusion.fusion_kind");
@@ -96,6 +98,7 @@ struct Func {
 };
 
 struct Module {
+  std::string source; // the text the module was read from
   std::vector<std::unique_ptr<Func>> funcs;
   std::vector<std::unique_ptr<Value>> values;
   std::vector<std::unique_ptr<Op>> ops;

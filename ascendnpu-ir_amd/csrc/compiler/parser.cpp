@@ -80,6 +80,7 @@ struct Token {
   Tok kind;
   std::string text;
   int line;
+  size_t off = 0, end = 0; // source span [off, end)
 };
 
 bool identStart(char c) { return std::isalpha((unsigned char)c) || c == '_'; }
@@ -120,7 +121,7 @@ std::vector<Token> lex(const std::string &t) {
       size_t j = i + 1;
       while (j < t.size() && (identChar(t[j]) || t[j] == '-' || t[j] == '#'))
         ++j;
-      out.push_back({c == '%' ? Tok::Value : Tok::Symbol, t.substr(i, j - i), line});
+      out.push_back({c == '%' ? Tok::Value : Tok::Symbol, t.substr(i, j - i), line, i, j});
       i = j;
       continue;
     }
@@ -130,9 +131,9 @@ std::vector<Token> lex(const std::string &t) {
       std::string name = t.substr(i, j - i);
       if (j < t.size() && t[j] == '<') {
         std::string inner = readAngle(t, j, line);
-        out.push_back({Tok::Hash, name + "<" + inner + ">", line});
+        out.push_back({Tok::Hash, name + "<" + inner + ">", line, i, j});
       } else {
-        out.push_back({Tok::Hash, name, line});
+        out.push_back({Tok::Hash, name, line, i, j});
       }
       i = j;
       continue;
@@ -140,7 +141,7 @@ std::vector<Token> lex(const std::string &t) {
     if (c == '"') {
       size_t j = i + 1;
       while (j < t.size() && t[j] != '"') ++j;
-      out.push_back({Tok::String, t.substr(i + 1, j - i - 1), line});
+      out.push_back({Tok::String, t.substr(i + 1, j - i - 1), line, i, j + 1});
       i = j + 1;
       continue;
     }
@@ -162,7 +163,7 @@ std::vector<Token> lex(const std::string &t) {
           while (j < t.size() && std::isdigit((unsigned char)t[j])) ++j;
         }
       }
-      out.push_back({Tok::Number, t.substr(i, j - i), line});
+      out.push_back({Tok::Number, t.substr(i, j - i), line, i, j});
       i = j;
       continue;
     }
@@ -174,22 +175,22 @@ std::vector<Token> lex(const std::string &t) {
            id == "affine_map" || id == "vector") &&
           j < t.size() && t[j] == '<') {
         std::string inner = readAngle(t, j, line);
-        out.push_back({Tok::Raw, id + "<" + inner + ">", line});
+        out.push_back({Tok::Raw, id + "<" + inner + ">", line, i, j});
       } else {
-        out.push_back({Tok::Ident, id, line});
+        out.push_back({Tok::Ident, id, line, i, j});
       }
       i = j;
       continue;
     }
     if (c == '-' && i + 1 < t.size() && t[i + 1] == '>') {
-      out.push_back({Tok::Punct, "->", line});
+      out.push_back({Tok::Punct, "->", line, i, i + 2});
       i += 2;
       continue;
     }
-    out.push_back({Tok::Punct, std::string(1, c), line});
+    out.push_back({Tok::Punct, std::string(1, c), line, i, i + 1});
     ++i;
   }
-  out.push_back({Tok::End, "", line});
+  out.push_back({Tok::End, "", line, t.size(), t.size()});
   return out;
 }
 
@@ -341,9 +342,11 @@ private:
   }
 
   void parseFunc() {
+    const size_t begin = toks_[pos_].off;
     ++pos_; // func.func
     scope_.clear();
     auto f = std::make_unique<Func>();
+    f->srcBegin = begin;
     if (peek().kind == Tok::Ident) ++pos_; // visibility
     if (peek().kind != Tok::Symbol) fail("expected function name");
     f->name = next().text.substr(1);
@@ -400,6 +403,7 @@ private:
       parseStatement(*f);
     }
     expectP("}");
+    f->srcEnd = toks_[pos_ - 1].end;
     if (f->returns.size() != f->resultTypes.size())
       throw CompileError("function @" + f->name + ": return arity does not match its signature");
     mod_->funcs.push_back(std::move(f));
@@ -441,6 +445,7 @@ private:
 
   void parseStatement(Func &f) {
     int line = peek().line;
+    const size_t firstTok = pos_;
     std::vector<std::string> resNames;
     int multi = 0;
     if (peek().kind == Tok::Value) {
@@ -557,7 +562,7 @@ private:
         ++pos_;
         op->literalType = parseType();
         while (isP(peek(), ",")) { ++pos_; parseType(); }
-        if (peek().kind == Tok::Ident && peek().text == "to") {
+        if (peek().kind == Tok::Ident && (peek().text == "to" || peek().text == "into")) {
           ++pos_;
           op->toType = parseType();
         }
@@ -603,6 +608,8 @@ private:
     for (auto *v : op->ins) v->users.push_back(op);
     for (auto *v : op->outs) v->users.push_back(op);
     for (auto *v : op->operands) v->users.push_back(op);
+    op->srcBegin = toks_[firstTok].off;
+    op->srcEnd = pos_ > firstTok ? toks_[pos_ - 1].end : toks_[firstTok].end;
     f.ops.push_back(op);
   }
 };
@@ -611,7 +618,9 @@ private:
 
 std::unique_ptr<Module> parseModule(const std::string &text) {
   Parser p(text);
-  return p.run();
+  auto m = p.run();
+  m->source = text;
+  return m;
 }
 
 } // namespace hfc

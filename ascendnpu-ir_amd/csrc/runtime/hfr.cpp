@@ -48,6 +48,29 @@ struct hfr_group {
   int ownWsDevice = -1;
 };
 
+// A buffer binding inside a launch program: program parameter, workspace
+// temporary or program result.
+struct Binding {
+  enum Kind { Param, Temp, Result } kind;
+  int index;
+};
+
+struct ProgramStep {
+  hfr_group *group = nullptr;
+  std::vector<Binding> args, results;
+};
+
+struct hfr_program {
+  std::string name;
+  std::vector<std::string> paramRoles;  // in | out | inout | scalar
+  std::vector<int> resultParam;         // param a result is written into, or -1
+  std::vector<uint64_t> tempOffset;
+  uint64_t wsBytes = 0;
+  std::vector<ProgramStep> steps;
+  void *ownWs = nullptr;
+  int ownWsDevice = -1;
+};
+
 namespace {
 
 thread_local std::string g_err;
@@ -103,6 +126,34 @@ int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
     if (a.kind == Karg::Result && (a.index < 0 || a.index >= (int)g.resultTied.size()))
       return fail(HFR_ERR_MANIFEST, "karg refers to a missing result");
   }
+  return HFR_OK;
+}
+
+// Splits a manifest into group blocks ("hfr-manifest 1") and launch-program
+// blocks ("hfr-program 1").
+int readManifest(const char *path, std::vector<std::vector<std::string>> &groups,
+                 std::vector<std::vector<std::string>> &programs) {
+  std::ifstream f(path);
+  if (!f) return fail(HFR_ERR_IO, std::string("cannot open manifest ") + path);
+  std::vector<std::string> *cur = nullptr;
+  std::string ln;
+  while (std::getline(f, ln)) {
+    if (ln.rfind("hfr-manifest", 0) == 0) {
+      if (ln != "hfr-manifest 1") return fail(HFR_ERR_MANIFEST, "unsupported manifest version: " + ln);
+      groups.emplace_back();
+      cur = &groups.back();
+      continue;
+    }
+    if (ln.rfind("hfr-program", 0) == 0) {
+      if (ln != "hfr-program 1") return fail(HFR_ERR_MANIFEST, "unsupported program version: " + ln);
+      programs.emplace_back();
+      cur = &programs.back();
+      continue;
+    }
+    if (!cur) return fail(HFR_ERR_MANIFEST, "manifest must start with 'hfr-manifest 1'");
+    if (!ln.empty()) cur->push_back(ln);
+  }
+  if (groups.empty() && programs.empty()) return fail(HFR_ERR_MANIFEST, "empty manifest");
   return HFR_OK;
 }
 
@@ -165,20 +216,10 @@ int hfr_launch(hfr_kernel_t k, const hfr_launch_cfg *cfg, const uint64_t *args, 
 
 int hfr_group_load(const char *manifest_path, const char *func, hfr_group_t *out) {
   if (!manifest_path || !out) return fail(HFR_ERR_INVALID, "null argument to hfr_group_load");
-  std::ifstream f(manifest_path);
-  if (!f) return fail(HFR_ERR_IO, std::string("cannot open manifest ") + manifest_path);
-  std::vector<std::vector<std::string>> blocks;
-  std::string ln;
-  while (std::getline(f, ln)) {
-    if (ln.rfind("hfr-manifest", 0) == 0) {
-      if (ln != "hfr-manifest 1") return fail(HFR_ERR_MANIFEST, "unsupported manifest version: " + ln);
-      blocks.emplace_back();
-      continue;
-    }
-    if (blocks.empty()) return fail(HFR_ERR_MANIFEST, "manifest must start with 'hfr-manifest 1'");
-    if (!ln.empty()) blocks.back().push_back(ln);
-  }
-  if (blocks.empty()) return fail(HFR_ERR_MANIFEST, "empty manifest");
+  std::vector<std::vector<std::string>> blocks, programs;
+  int rc = readManifest(manifest_path, blocks, programs);
+  if (rc) return rc;
+  if (blocks.empty()) return fail(HFR_ERR_MANIFEST, "manifest holds no group");
   auto g = std::make_unique<hfr_group>();
   bool found = false;
   for (auto &b : blocks) {
@@ -194,7 +235,7 @@ int hfr_group_load(const char *manifest_path, const char *func, hfr_group_t *out
   }
   if (!found) return fail(HFR_ERR_NOT_FOUND, std::string("group '") + (func ? func : "") + "' not in manifest");
   std::string hsaco = g->hsaco[0] == '/' ? g->hsaco : dirOf(manifest_path) + "/" + g->hsaco;
-  int rc = hfr_module_load(hsaco.c_str(), &g->mod);
+  rc = hfr_module_load(hsaco.c_str(), &g->mod);
   if (rc) return rc;
   hipError_t e = hipModuleGetFunction(&g->fn, g->mod->mod, g->kernel.c_str());
   if (e != hipSuccess) {
@@ -276,6 +317,192 @@ int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void
     }
   }
   return launchRaw(g->fn, g->cfg, args.data(), args.size(), stream);
+}
+
+} // extern "C"
+
+namespace {
+
+int parseBinding(const std::string &s, const hfr_program &p, Binding &b) {
+  if (s.size() < 2) return fail(HFR_ERR_MANIFEST, "bad binding '" + s + "'");
+  int i = std::atoi(s.c_str() + 1);
+  switch (s[0]) {
+  case 'p': b = {Binding::Param, i}; return i >= 0 && i < (int)p.paramRoles.size() ? HFR_OK : fail(HFR_ERR_MANIFEST, "binding " + s + " out of range");
+  case 't': b = {Binding::Temp, i}; return i >= 0 && i < (int)p.tempOffset.size() ? HFR_OK : fail(HFR_ERR_MANIFEST, "binding " + s + " out of range");
+  case 'r': b = {Binding::Result, i}; return i >= 0 && i < (int)p.resultParam.size() ? HFR_OK : fail(HFR_ERR_MANIFEST, "binding " + s + " out of range");
+  default: return fail(HFR_ERR_MANIFEST, "bad binding '" + s + "'");
+  }
+}
+
+bool sameBinding(const Binding &a, const Binding &b) { return a.kind == b.kind && a.index == b.index; }
+
+void freeProgram(hfr_program *p) {
+  for (auto &st : p->steps)
+    if (st.group) hfr_group_unload(st.group);
+  if (p->ownWs) {
+    int cur = 0;
+    hipGetDevice(&cur);
+    if (p->ownWsDevice >= 0) hipSetDevice(p->ownWsDevice);
+    hipFree(p->ownWs);
+    hipSetDevice(cur);
+  }
+  delete p;
+}
+
+} // namespace
+
+extern "C" {
+
+int hfr_program_load(const char *manifest_path, const char *name, hfr_program_t *out) {
+  if (!manifest_path || !out) return fail(HFR_ERR_INVALID, "null argument to hfr_program_load");
+  std::vector<std::vector<std::string>> groups, programs;
+  int rc = readManifest(manifest_path, groups, programs);
+  if (rc) return rc;
+  const std::vector<std::string> *blk = nullptr;
+  for (auto &b : programs) {
+    std::string pname;
+    for (auto &ln : b)
+      if (ln.rfind("program ", 0) == 0) pname = ln.substr(8);
+    if (!name || pname == name) {
+      if (!name && programs.size() > 1) return fail(HFR_ERR_INVALID, "manifest holds several programs; name one");
+      blk = &b;
+      break;
+    }
+  }
+  if (!blk) return fail(HFR_ERR_NOT_FOUND, std::string("program '") + (name ? name : "") + "' not in manifest");
+  auto *p = new hfr_program();
+  std::vector<std::vector<std::string>> stepLines;
+  for (auto &ln : *blk) {
+    std::istringstream is(ln);
+    std::string key;
+    is >> key;
+    if (key == "program") is >> p->name;
+    else if (key == "pworkspace") is >> p->wsBytes;
+    else if (key == "pparam") { int i; std::string role; is >> i >> role; p->paramRoles.push_back(role); }
+    else if (key == "presult") {
+      int i; std::string role;
+      is >> i >> role;
+      p->resultParam.push_back(role[0] == 'p' ? std::atoi(role.c_str() + 1) : -1);
+    } else if (key == "ptemp") { int i; uint64_t off; is >> i >> off; p->tempOffset.push_back(off); }
+    else if (key == "pstep") {
+      std::vector<std::string> toks;
+      std::string t;
+      while (is >> t) toks.push_back(t);
+      stepLines.push_back(toks);
+    }
+    if (is.fail() && key != "pstep") { freeProgram(p); return fail(HFR_ERR_MANIFEST, "malformed program line: " + ln); }
+  }
+  for (int rp : p->resultParam)
+    if (rp >= (int)p->paramRoles.size()) { freeProgram(p); return fail(HFR_ERR_MANIFEST, "program result bound to a missing param"); }
+  // pstep <group> <kind> <nargs> <bindings...> <nresults> <bindings...>
+  for (auto &toks : stepLines) {
+    ProgramStep st;
+    size_t k = 2;
+    auto bad = [&]() { freeProgram(p); return fail(HFR_ERR_MANIFEST, "malformed pstep line"); };
+    if (toks.size() < 4) return bad();
+    int na = std::atoi(toks[k++].c_str());
+    if (na < 0 || k + na >= toks.size()) return bad();
+    for (int i = 0; i < na; ++i) {
+      Binding b;
+      if ((rc = parseBinding(toks[k++], *p, b))) { freeProgram(p); return rc; }
+      st.args.push_back(b);
+    }
+    int nr = std::atoi(toks[k++].c_str());
+    if (nr < 0 || k + nr != toks.size()) return bad();
+    for (int i = 0; i < nr; ++i) {
+      Binding b;
+      if ((rc = parseBinding(toks[k++], *p, b))) { freeProgram(p); return rc; }
+      st.results.push_back(b);
+    }
+    p->steps.push_back(st);
+    if ((rc = hfr_group_load(manifest_path, toks[0].c_str(), &p->steps.back().group))) {
+      p->steps.back().group = nullptr;
+      freeProgram(p);
+      return rc;
+    }
+    hfr_group *g = p->steps.back().group;
+    if (g->paramRoles.size() != st.args.size() || g->resultTied.size() != st.results.size()) {
+      freeProgram(p);
+      return fail(HFR_ERR_MANIFEST, "step @" + toks[0] + " does not match its group's signature");
+    }
+    // a result the group writes into one of its arguments must be bound to
+    // that argument's buffer
+    for (size_t j = 0; j < st.results.size(); ++j) {
+      int t = g->resultTied[j];
+      if (t >= 0 && !sameBinding(st.args[t], st.results[j])) {
+        freeProgram(p);
+        return fail(HFR_ERR_MANIFEST, "step @" + toks[0] + " result " + std::to_string(j) + " is written into argument " +
+                                          std::to_string(t) + " but bound elsewhere");
+      }
+    }
+  }
+  *out = p;
+  return HFR_OK;
+}
+
+int hfr_program_unload(hfr_program_t p) {
+  if (!p) return fail(HFR_ERR_INVALID, "null program");
+  freeProgram(p);
+  return HFR_OK;
+}
+
+int hfr_program_info_get(hfr_program_t p, hfr_program_info *info) {
+  if (!p || !info) return fail(HFR_ERR_INVALID, "null argument to hfr_program_info_get");
+  info->nparams = (int)p->paramRoles.size();
+  info->nresults = (int)p->resultParam.size();
+  info->nsteps = (int)p->steps.size();
+  info->workspace_bytes = p->wsBytes;
+  return HFR_OK;
+}
+
+int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
+                       void *workspace, void *stream) {
+  if (!p) return fail(HFR_ERR_INVALID, "null program");
+  if (nparams != p->paramRoles.size())
+    return fail(HFR_ERR_INVALID, "program @" + p->name + " takes " + std::to_string(p->paramRoles.size()) +
+                                     " arguments, got " + std::to_string(nparams));
+  if (nresults != p->resultParam.size())
+    return fail(HFR_ERR_INVALID, "program @" + p->name + " has " + std::to_string(p->resultParam.size()) +
+                                     " results, got " + std::to_string(nresults));
+  if (nparams && !params) return fail(HFR_ERR_INVALID, "null params array");
+  for (size_t i = 0; i < nparams; ++i)
+    if (p->paramRoles[i] != "scalar" && params[i] == 0)
+      return fail(HFR_ERR_INVALID, "null device pointer for argument " + std::to_string(i));
+  for (size_t i = 0; i < nresults; ++i)
+    if (p->resultParam[i] < 0 && (!results || !results[i]))
+      return fail(HFR_ERR_INVALID, "null device pointer for result " + std::to_string(i));
+  char *ws = (char *)workspace;
+  if (p->wsBytes && !ws) {
+    int dev = 0;
+    hipGetDevice(&dev);
+    if (!p->ownWs || p->ownWsDevice != dev) {
+      if (p->ownWs) return fail(HFR_ERR_INVALID, "program workspace belongs to another device");
+      hipError_t e = hipMalloc(&p->ownWs, p->wsBytes);
+      if (e != hipSuccess) return hipFail(e, "hipMalloc(program workspace)");
+      p->ownWsDevice = dev;
+    }
+    ws = (char *)p->ownWs;
+  }
+  auto resolve = [&](const Binding &b) -> uint64_t {
+    switch (b.kind) {
+    case Binding::Param: return params[b.index];
+    case Binding::Temp: return (uint64_t)(uintptr_t)(ws + p->tempOffset[b.index]);
+    case Binding::Result:
+      return p->resultParam[b.index] >= 0 ? params[p->resultParam[b.index]] : (uint64_t)(uintptr_t)results[b.index];
+    }
+    return 0;
+  };
+  std::vector<uint64_t> args;
+  std::vector<void *> res;
+  for (auto &st : p->steps) {
+    args.clear();
+    res.clear();
+    for (auto &b : st.args) args.push_back(resolve(b));
+    for (auto &b : st.results) res.push_back((void *)(uintptr_t)resolve(b));
+    int rc = hfr_group_launch(st.group, args.data(), args.size(), res.data(), res.size(), nullptr, stream);
+    if (rc) return rc;
+  }
+  return HFR_OK;
 }
 
 } // extern "C"

@@ -294,6 +294,12 @@ def entries():
     e["cast_fp8"] = cast_fp8(4096)
     e["fp8_quant"] = fp8_quant(64, 4096)
     e["fp8_quant_ragged"] = fp8_quant(13, 1000)
+    # un-fused host functions: the fusion front-end splits them into launch
+    # programs of several groups
+    e["prog_gemm_rmsnorm_quant"] = g.gemm_rmsnorm_quant(256, 512, 256)
+    e["prog_gemm_rmsnorm_quant_ragged"] = g.gemm_rmsnorm_quant(100, 320, 192)
+    e["prog_scores_softmax"] = g.scores_softmax(128, 1024, 128)
+    e["prog_scores_softmax_ragged"] = g.scores_softmax(72, 1000, 64)
     return e
 
 

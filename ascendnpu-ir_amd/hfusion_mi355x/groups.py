@@ -260,3 +260,116 @@ CONFIGS = {
     "argmax": dict(fn=argmax, kw=dict(rows=256, cols=152064)),
     "w8a8_dequant": dict(fn=w8a8_dequant, kw=dict(m=4096, n=4096, k=4096)),
 }
+
+
+_HOST = "attributes {hacc.function_kind = #hacc.function_kind<HOST>}"
+
+
+def gemm_rmsnorm_quant(m=4096, n=4096, k=4096, alpha=1.0 / 4096):
+    """An un-fused host function (no fusion kind): W8A8 contraction, scale,
+    RMSNorm over the output rows and dynamic int8 quantisation.  The fusion
+    front-end splits it into a MIX_CV group (contraction + dequant epilogue)
+    and a LAST_AXIS_PBR group (norm + quant), joined by a workspace tensor."""
+    A, B, C = _t([m, k], "i8"), _t([n, k], "i8"), _t([m, n], "i32")
+    XF, RF, GF, G, Q = _t([m, n], "f32"), _t([m], "f32"), _t([n], "f32"), _t([n], "bf16"), _t([m, n], "i8")
+    return f"""module {{
+  func.func @gemm_rmsnorm_quant(%a: {A}, %b: {B}, %gamma: {G}, %q: {Q}, %scale: {RF}) -> ({Q}, {RF})
+      {_HOST} {{
+    %c0 = arith.constant 0 : i32
+    %alpha = arith.constant {alpha:.9e} : f32
+    %zero = arith.constant 0.000000e+00 : f32
+    %cols = arith.constant {float(n):.6e} : f32
+    %eps = arith.constant 9.999999970e-07 : f32
+    %qmax = arith.constant 1.270000e+02 : f32
+    %qmin = arith.constant -1.270000e+02 : f32
+    %e0 = tensor.empty() : {C}
+    %acc0 = linalg.fill ins(%c0 : i32) outs(%e0 : {C}) -> {C}
+    %acc = linalg.matmul_transpose_b ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
+    %e1 = tensor.empty() : {XF}
+    %cf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%acc : {C}) outs(%e1 : {XF}) -> {XF}
+    %e2 = tensor.empty() : {XF}
+    %x = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%cf, %alpha : {XF}, f32) outs(%e2 : {XF}) -> {XF}
+    %e3 = tensor.empty() : {XF}
+    %sq = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%x, %x : {XF}, {XF}) outs(%e3 : {XF}) -> {XF}
+    %e4 = tensor.empty() : {RF}
+    %i4 = linalg.fill ins(%zero : f32) outs(%e4 : {RF}) -> {RF}
+    %ss = linalg.reduce {{arith.addf}} ins(%sq : {XF}) outs(%i4 : {RF}) dimensions = [1]
+    %e5 = tensor.empty() : {RF}
+    %mean = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%ss, %cols : {RF}, f32) outs(%e5 : {RF}) -> {RF}
+    %e6 = tensor.empty() : {RF}
+    %ms = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%mean, %eps : {RF}, f32) outs(%e6 : {RF}) -> {RF}
+    %e7 = tensor.empty() : {RF}
+    %rt = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%ms : {RF}) outs(%e7 : {RF}) -> {RF}
+    %e8 = tensor.empty() : {RF}
+    %inv = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<rec>}} ins(%rt : {RF}) outs(%e8 : {RF}) -> {RF}
+    %e9 = tensor.empty() : {XF}
+    %binv = linalg.broadcast ins(%inv : {RF}) outs(%e9 : {XF}) dimensions = [1]
+    %e10 = tensor.empty() : {XF}
+    %y1 = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%x, %binv : {XF}, {XF}) outs(%e10 : {XF}) -> {XF}
+    %e11 = tensor.empty() : {GF}
+    %gf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%gamma : {G}) outs(%e11 : {GF}) -> {GF}
+    %e12 = tensor.empty() : {XF}
+    %bg = linalg.broadcast ins(%gf : {GF}) outs(%e12 : {XF}) dimensions = [0]
+    %e13 = tensor.empty() : {XF}
+    %y = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%y1, %bg : {XF}, {XF}) outs(%e13 : {XF}) -> {XF}
+    %e14 = tensor.empty() : {XF}
+    %ay = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%y : {XF}) outs(%e14 : {XF}) -> {XF}
+    %e15 = tensor.empty() : {RF}
+    %i15 = linalg.fill ins(%zero : f32) outs(%e15 : {RF}) -> {RF}
+    %amax = linalg.reduce {{arith.maximumf}} ins(%ay : {XF}) outs(%i15 : {RF}) dimensions = [1]
+    %sc = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%amax, %qmax : {RF}, f32) outs(%scale : {RF}) -> {RF}
+    %e16 = tensor.empty() : {XF}
+    %bsc = linalg.broadcast ins(%sc : {RF}) outs(%e16 : {XF}) dimensions = [1]
+    %e17 = tensor.empty() : {XF}
+    %ys = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%y, %bsc : {XF}, {XF}) outs(%e17 : {XF}) -> {XF}
+    %e18 = tensor.empty() : {XF}
+    %r = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<nearbyint>}} ins(%ys : {XF}) outs(%e18 : {XF}) -> {XF}
+    %e19 = tensor.empty() : {XF}
+    %c1 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<minf>}} ins(%r, %qmax : {XF}, f32) outs(%e19 : {XF}) -> {XF}
+    %e20 = tensor.empty() : {XF}
+    %c2 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<maxf>}} ins(%c1, %qmin : {XF}, f32) outs(%e20 : {XF}) -> {XF}
+    %qv = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%c2 : {XF}) outs(%q : {Q}) -> {Q}
+    return %qv, %sc : {Q}, {RF}
+  }}
+}}
+"""
+
+
+def scores_softmax(m=1024, n=4096, k=128, scale=0.08838834764831845):
+    """An un-fused host function: bf16 scores = Q·Kᵀ·scale and a row softmax
+    written to bf16.  Split into a MIX_CV group (contraction + scale) and a
+    LAST_AXIS_PBR group (softmax) joined by a workspace tensor."""
+    QT, KT, S = _t([m, k], "bf16"), _t([n, k], "bf16"), _t([m, n], "f32")
+    R, O = _t([m], "f32"), _t([m, n], "bf16")
+    return f"""module {{
+  func.func @scores_softmax(%qm: {QT}, %km: {KT}, %p: {O}) -> {O}
+      {_HOST} {{
+    %zero = arith.constant 0.000000e+00 : f32
+    %ninf = arith.constant 0xFF800000 : f32
+    %sc = arith.constant {scale:.9e} : f32
+    %e0 = tensor.empty() : {S}
+    %acc0 = linalg.fill ins(%zero : f32) outs(%e0 : {S}) -> {S}
+    %acc = linalg.matmul_transpose_b ins(%qm, %km : {QT}, {KT}) outs(%acc0 : {S}) -> {S}
+    %e1 = tensor.empty() : {S}
+    %x = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%acc, %sc : {S}, f32) outs(%e1 : {S}) -> {S}
+    %e2 = tensor.empty() : {R}
+    %i2 = linalg.fill ins(%ninf : f32) outs(%e2 : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {S}) outs(%i2 : {R}) dimensions = [1]
+    %e3 = tensor.empty() : {S}
+    %bm = linalg.broadcast ins(%m : {R}) outs(%e3 : {S}) dimensions = [1]
+    %e4 = tensor.empty() : {S}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%x, %bm : {S}, {S}) outs(%e4 : {S}) -> {S}
+    %e5 = tensor.empty() : {S}
+    %ex = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%d : {S}) outs(%e5 : {S}) -> {S}
+    %e6 = tensor.empty() : {R}
+    %i6 = linalg.fill ins(%zero : f32) outs(%e6 : {R}) -> {R}
+    %s = linalg.reduce {{arith.addf}} ins(%ex : {S}) outs(%i6 : {R}) dimensions = [1]
+    %e7 = tensor.empty() : {S}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e7 : {S}) dimensions = [1]
+    %e8 = tensor.empty() : {S}
+    %pr = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%ex, %bs : {S}, {S}) outs(%e8 : {S}) -> {S}
+    %o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%pr : {S}) outs(%p : {O}) -> {O}
+    return %o : {O}
+  }}
+}}
+"""

@@ -51,6 +51,11 @@ class GroupInfo(ctypes.Structure):
                 ("algo_ops", ctypes.c_uint64), ("cfg", LaunchCfg)]
 
 
+class ProgramInfo(ctypes.Structure):
+    _fields_ = [("nparams", ctypes.c_int), ("nresults", ctypes.c_int), ("nsteps", ctypes.c_int),
+                ("workspace_bytes", ctypes.c_uint64)]
+
+
 def hfr():
     """The runtime library (hipModuleLoad / hipModuleLaunchKernel)."""
     global _hfr
@@ -66,8 +71,14 @@ def hfr():
         lib.hfr_group_info_get.argtypes = [vp, ctypes.POINTER(GroupInfo)]
         lib.hfr_group_launch.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t,
                                          ctypes.POINTER(vp), ctypes.c_size_t, vp, vp]
+        lib.hfr_program_load.argtypes = [cp, cp, ctypes.POINTER(vp)]
+        lib.hfr_program_unload.argtypes = [vp]
+        lib.hfr_program_info_get.argtypes = [vp, ctypes.POINTER(ProgramInfo)]
+        lib.hfr_program_launch.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t,
+                                           ctypes.POINTER(vp), ctypes.c_size_t, vp, vp]
         for fn in ("hfr_module_load", "hfr_module_unload", "hfr_kernel_get", "hfr_launch", "hfr_group_load",
-                   "hfr_group_unload", "hfr_group_info_get", "hfr_group_launch"):
+                   "hfr_group_unload", "hfr_group_info_get", "hfr_group_launch", "hfr_program_load",
+                   "hfr_program_unload", "hfr_program_info_get", "hfr_program_launch"):
             getattr(lib, fn).restype = ctypes.c_int
         lib.hfr_last_error.restype = cp
         lib.hfr_version.restype = cp

@@ -56,12 +56,22 @@ class Artifact:
         self.manifest = prefix + ".manifest"
         self.hsaco = prefix + ".hsaco"
         self.source = prefix + ".hip"
-        self.blocks = parse_manifest(self.manifest)
+        self.blocks, self.programs = parse_manifest(self.manifest, with_programs=True)
+        outlined = prefix + ".outlined.mlir"
+        self.outlined = outlined if os.path.exists(outlined) else None
 
     def funcs(self):
         return [b["func"] for b in self.blocks]
 
+    def program_names(self):
+        return [p["name"] for p in self.programs]
+
     def load(self, func=None):
+        """The group kernel named `func`, or, when `func` names a function the
+        fusion front-end split (or is None and the module was split into
+        exactly one program), its launch program."""
+        if self.programs and (func is None or func in self.program_names()):
+            return Program(self, func)
         return Group(self, func)
 
 
@@ -81,19 +91,51 @@ def compile(ir_text, options="", cache=True, require_cached=False):
     return Artifact(prefix)
 
 
-def parse_manifest(path):
-    blocks = []
+def _shape(parts, at):
+    n = int(parts[at])
+    return tuple(int(x) for x in parts[at + 1:at + 1 + n])
+
+
+def parse_manifest(path, with_programs=False):
+    blocks, programs = [], []
+    cur = None
     with open(path) as f:
         for ln in f:
             ln = ln.rstrip("\n")
             if not ln:
                 continue
             if ln.startswith("hfr-manifest"):
-                blocks.append({"params": [], "results": [], "kargs": []})
+                cur = {"params": [], "results": [], "kargs": []}
+                blocks.append(cur)
+                continue
+            if ln.startswith("hfr-program"):
+                cur = {"params": [], "results": [], "temps": [], "steps": [], "program": True}
+                programs.append(cur)
                 continue
             key, _, rest = ln.partition(" ")
-            b = blocks[-1]
+            b = cur
             parts = rest.split()
+            if b.get("program"):
+                if key == "program":
+                    b["name"] = rest
+                elif key == "pworkspace":
+                    b["workspace"] = int(parts[0])
+                elif key == "pparam":
+                    b["params"].append(dict(role=parts[1], elem=parts[2], shape=_shape(parts, 3)))
+                elif key == "presult":
+                    role = parts[1]
+                    b["results"].append(dict(tied=int(role[1:]) if role.startswith("p") else -1, elem=parts[2],
+                                             shape=_shape(parts, 3)))
+                elif key == "ptemp":
+                    b["temps"].append(dict(offset=int(parts[1]), bytes=int(parts[2]), elem=parts[3],
+                                           shape=_shape(parts, 4)))
+                elif key == "pstep":
+                    na = int(parts[2])
+                    args = parts[3:3 + na]
+                    nr = int(parts[3 + na])
+                    b["steps"].append(dict(group=parts[0], kind=parts[1], args=args,
+                                           results=parts[4 + na:4 + na + nr]))
+                continue
             if key in ("func", "kernel", "hsaco", "kind"):
                 b[key] = rest
             elif key == "variant":
@@ -106,14 +148,12 @@ def parse_manifest(path):
                 b["workspace"] = int(parts[0])
                 b["workspace_zero"] = bool(int(parts[1]))
             elif key == "param":
-                n = int(parts[3])
-                b["params"].append(dict(role=parts[1], elem=parts[2], shape=tuple(int(x) for x in parts[4:4 + n])))
+                b["params"].append(dict(role=parts[1], elem=parts[2], shape=_shape(parts, 3)))
             elif key == "result":
-                n = int(parts[3])
-                b["results"].append(dict(tied=int(parts[1]), elem=parts[2], shape=tuple(int(x) for x in parts[4:4 + n])))
+                b["results"].append(dict(tied=int(parts[1]), elem=parts[2], shape=_shape(parts, 3)))
             elif key == "karg":
                 b["kargs"].append(parts[0])
-    return blocks
+    return (blocks, programs) if with_programs else blocks
 
 
 def _scalar_bits(v, elem):
@@ -195,6 +235,83 @@ class Group:
             stream = torch.cuda.current_stream(device).cuda_stream
         ws = workspace.data_ptr() if workspace is not None else None
         native.check(native.hfr().hfr_group_launch(self._h, slots, len(params), rptrs, len(res_meta), ws, stream))
+        return outs[0] if len(outs) == 1 else tuple(outs)
+
+
+def _check_arg(i, a, p, name):
+    import torch
+    if not isinstance(a, torch.Tensor) or not a.is_cuda:
+        raise TypeError(f"argument {i} of @{name} must be a device tensor")
+    if a.dtype != torch_dtype(p["elem"]) or tuple(a.shape) != p["shape"] or not a.is_contiguous():
+        raise ValueError(f"argument {i} of @{name}: expected contiguous {p['elem']}{list(p['shape'])}, "
+                         f"got {a.dtype}{list(a.shape)}")
+
+
+class Program:
+    """A function the fusion front-end split into fused groups (hfr_program_t):
+    one call launches every group kernel in order on the current stream."""
+
+    def __init__(self, artifact, name=None):
+        progs = artifact.programs
+        if name is None:
+            if len(progs) != 1:
+                raise ValueError("artifact holds several programs; name one of " + ", ".join(artifact.program_names()))
+            self.meta = progs[0]
+        else:
+            self.meta = [p for p in progs if p["name"] == name][0]
+        self.name = self.meta["name"]
+        self.steps = self.meta["steps"]
+        self._h = ctypes.c_void_p()
+        native.check(native.hfr().hfr_program_load(artifact.manifest.encode(), self.name.encode(),
+                                                   ctypes.byref(self._h)))
+        info = native.ProgramInfo()
+        native.check(native.hfr().hfr_program_info_get(self._h, ctypes.byref(info)))
+        self.info = info
+
+    @property
+    def workspace_bytes(self):
+        return self.info.workspace_bytes
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and h.value and native._hfr is not None:
+            native.hfr().hfr_program_unload(h)
+            self._h = None
+
+    def __call__(self, *args, results=None, stream=None, workspace=None):
+        import torch
+        params = self.meta["params"]
+        if len(args) != len(params):
+            raise TypeError(f"@{self.name} takes {len(params)} arguments ({len(args)} given)")
+        device = None
+        slots = (ctypes.c_uint64 * max(1, len(params)))()
+        for i, (a, p) in enumerate(zip(args, params)):
+            if p["role"] == "scalar":
+                slots[i] = _scalar_bits(a, p["elem"])
+                continue
+            _check_arg(i, a, p, self.name)
+            device = a.device if device is None else device
+            slots[i] = a.data_ptr()
+        res_meta = self.meta["results"]
+        outs = []
+        rptrs = (ctypes.c_void_p * max(1, len(res_meta)))()
+        for j, r in enumerate(res_meta):
+            if r["tied"] >= 0:
+                outs.append(args[r["tied"]])
+                rptrs[j] = None
+            else:
+                t = results[j] if results is not None else torch.empty(r["shape"], dtype=torch_dtype(r["elem"]),
+                                                                      device=device)
+                if tuple(t.shape) != r["shape"] or t.dtype != torch_dtype(r["elem"]) or not t.is_cuda:
+                    raise ValueError(f"result {j} of @{self.name}: expected {r['elem']}{list(r['shape'])}")
+                outs.append(t)
+                rptrs[j] = t.data_ptr()
+        if stream is None:
+            stream = torch.cuda.current_stream(device).cuda_stream
+        if workspace is not None and workspace.numel() * workspace.element_size() < self.workspace_bytes:
+            raise ValueError(f"@{self.name} needs a workspace of {self.workspace_bytes} bytes")
+        ws = workspace.data_ptr() if workspace is not None else None
+        native.check(native.hfr().hfr_program_launch(self._h, slots, len(params), rptrs, len(res_meta), ws, stream))
         return outs[0] if len(outs) == 1 else tuple(outs)
 
 

@@ -12,14 +12,31 @@
  * Outputs for an output prefix P:
  *   P.hip       generated HIP translation unit (kernels of every entry func)
  *   P.hsaco     gfx950 code object (hipModuleLoad-able)
- *   P.manifest  launch manifest(s): one "hfr-manifest 1" block per entry func
+ *   P.manifest  launch manifest(s): one "hfr-manifest 1" block per entry func,
+ *               then one "hfr-program 1" block per host function that the
+ *               fusion front-end split into groups
+ *
+ * Fusion front-end (the reference's HFusion auto-fusion: InferFuncFusionKind
+ * + HFusionOpFusion + OutlineSingleOp, bishengir/lib/Dialect/HFusion/
+ * Transforms/InferFuncFusionKind.cpp:70-103, OpFusion.cpp:68-229): a function
+ * without `hfusion.fusion_kind` that is marked
+ * `hacc.function_kind = #hacc.function_kind<HOST>`, or whose ops fit no single
+ * fusion kind, is outlined into fused groups (`<func>_g<k>`, each one kernel)
+ * and a launch program named after the function (see hfr_program_* in hfr.h).
  *
  * Options string: ';'-separated key=value pairs
  *   hipcc=<path>            (default /opt/rocm/bin/hipcc)
  *   include=<dir>           kernel library headers (default: located next to
  *                           this library, ../csrc/kernels)
  *   arch=<gfx>              (default gfx950)
- *   emit=hip|hsaco          stop after writing P.hip, or build the code object
+ *   emit=hip|hsaco|outlined stop after writing P.hip, or build the code object,
+ *                           or stop after the fusion front-end, writing the
+ *                           outlined module (P.outlined.mlir) and the launch
+ *                           programs (P.programs)
+ *   fusion_kind=<KIND>      outline every function without a declared kind
+ *                           by this one kind (PURE_ELEMWISE, ANY_PB,
+ *                           LAST_AXIS_PBR, ANY_PBR, MIX_CV), as the
+ *                           reference's --test-assign-fusion-kind does
  *   ordered_fp_sums=0|1     serial-order fp32 sums for every linalg.reduce addf
  *
  * Returns 0 on success; a negative code with a message in `err` otherwise

@@ -39,6 +39,7 @@ extern "C" {
 typedef struct hfr_module *hfr_module_t;
 typedef struct hfr_kernel *hfr_kernel_t;
 typedef struct hfr_group *hfr_group_t;
+typedef struct hfr_program *hfr_program_t;
 
 typedef struct hfr_launch_cfg {
   unsigned grid[3];
@@ -76,6 +77,33 @@ int hfr_group_info_get(hfr_group_t g, hfr_group_info *info);
  * use when the group requires it). */
 int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
                      void *workspace, void *stream);
+
+/* ---- launch programs (an un-fused function split into fused groups)
+ * Replaces the host function the reference's HFusion auto-fusion leaves
+ * behind after outlining: a sequence of `func.call`s to the outlined groups
+ * with tensors passed between them
+ * (bishengir/lib/Dialect/HFusion/Transforms/OpFusion.cpp:68-229,
+ * OpFusion/FusibleBlockOutliner.cpp:211-290).  Here the steps launch the
+ * groups' kernels in order on one stream; tensors passed between groups live
+ * in one program workspace. */
+typedef struct hfr_program_info {
+  int nparams;
+  int nresults;
+  int nsteps;
+  uint64_t workspace_bytes; /* intermediate tensors, 256-byte aligned */
+} hfr_program_info;
+
+/* name may be NULL when the manifest holds one program. */
+int hfr_program_load(const char *manifest_path, const char *name, hfr_program_t *out);
+int hfr_program_unload(hfr_program_t p);
+int hfr_program_info_get(hfr_program_t p, hfr_program_info *info);
+/* params: one slot per argument of the original function; results: one
+ * pointer per result (ignored for results written into an argument);
+ * workspace: NULL to use the program's own (allocated on first use), or a
+ * caller buffer of workspace_bytes.  Steps are enqueued on `stream`; each
+ * group uses its own internal workspace. */
+int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
+                       void *workspace, void *stream);
 
 const char *hfr_last_error(void);
 const char *hfr_version(void);

@@ -374,3 +374,40 @@ def test_rint_of_row_division_near_ties(gpu):
     assert np.array_equal(np.isnan(out), np.isnan(ref))
     ok = ~np.isnan(ref)
     assert np.array_equal(out[ok].view(np.uint32), ref[ok].view(np.uint32)), int((out[ok] != ref[ok]).sum())
+
+
+# ------------------------------------------------------ launch programs
+# Un-fused host functions split by the fusion front-end into several groups;
+# the whole program runs on the GPU (hfr_program_launch) and is compared with
+# the oracle run over the un-fused function.
+def _gemm_args(m, n, k):
+    s = I.SEED_BASE + 70
+    return [I.int8_uniform(s, (m, k)), I.int8_uniform(s + 1, (n, k)), I.uniform_bf16(s + 2, (n,), 0.5, 1.5),
+            zeros((m, n), np.int8), zeros(m, np.float32)]
+
+
+@pytest.mark.parametrize("name,shape", [("prog_gemm_rmsnorm_quant", (256, 512, 256)),
+                                        ("prog_gemm_rmsnorm_quant_ragged", (100, 320, 192))])
+def test_program_gemm_rmsnorm_quant(gpu, name, shape):
+    """int8 contraction (exact) -> dequant -> RMSNorm -> int8 quant: every
+    output bit-exact."""
+    note(name)
+    args = _gemm_args(*shape)
+    q, sc = run_gpu(name, args, gpu)
+    rq, rsc = run_oracle(name, args)
+    assert np.array_equal(sc.view(np.uint32), rsc.view(np.uint32))
+    assert np.array_equal(q, rq)
+
+
+@pytest.mark.parametrize("name,shape", [("prog_scores_softmax", (128, 1024, 128)),
+                                        ("prog_scores_softmax_ragged", (72, 1000, 64))])
+def test_program_scores_softmax(gpu, name, shape):
+    """bf16 contraction (fp32 accumulation order differs from the serial k
+    loop) -> scale -> softmax -> bf16: within 1 bf16 ulp."""
+    note(name)
+    s = I.SEED_BASE + 80
+    m, n, k = shape
+    args = [I.normal_bf16(s, (m, k)), I.normal_bf16(s + 1, (n, k)), zeros((m, n), np.uint16)]
+    out, = run_gpu(name, args, gpu)
+    ref, = run_oracle(name, args)
+    assert bf16_ulp_diff(out, ref).max() <= 1
