@@ -7,13 +7,27 @@
 // code object <output>.hsaco plus <output>.manifest and <output>.hip instead
 // of the Ascend ELF produced through `hivmc`.
 //
+// --enable-cpu-runner[=<options>], --enable-cpu-runner-before=<pass>[,<n>][,<options>]
+// and --enable-cpu-runner-after=… (BiShengIRCompileConfig.cpp:100-125,
+// PassManager.cpp:56-93) run the input after compiling it: the host function
+// (or the only group) is executed with generated inputs and the arguments and
+// results are written in the reference runner's text format (runner.cpp).  The
+// execution happens on the MI355X; every cut point of the pipeline computes the
+// same function, so <pass> and <n> are checked for form only.  The files are
+// --runner-inputs=<path> and --runner-outputs=<path> (defaults
+// <output>.runner_inputs.txt / <output>.runner_outputs.txt), --runner-func
+// picks a function when the module holds several.
+//
 // Reference flags that configure the Ascend pipeline (-enable-hfusion-compile,
 // -enable-hivm-compile, -enable-lir-compile, -block-dim, ...;
 // bishengir/include/bishengir/Tools/bishengir-compile/Options.td) are
 // accepted and have no effect here: fusion kinds, tiling and block counts are
 // chosen by the MI355X lowering.
 #include "../../../include/hfc.h"
+#include "../runtime/runner.h"
 
+#include <algorithm>
+#include <cctype>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -25,6 +39,8 @@ static bool startsWith(const std::string &s, const char *p) { return s.rfind(p, 
 int main(int argc, char **argv) {
   std::string input, output, target = "mi355x";
   std::string opts;
+  int runnerFlags = 0;
+  std::string runnerIn, runnerOut, runnerFunc;
   static const char *ignored[] = {"-enable-hfusion-compile", "-enable-hivm-compile", "-enable-lir-compile",
                                   "-block-dim", "-enable-auto-multi-buffer", "-enable-static-bare-ptr",
                                   "-enable-triton-kernel-compile", "-enable-bin-relocation", "-enable-sanitizer",
@@ -43,6 +59,33 @@ int main(int argc, char **argv) {
       opts += "hipcc=" + b.substr(7) + ";";
     } else if (startsWith(b, "-emit=")) {
       opts += "emit=" + b.substr(6) + ";";
+    } else if (b == "-enable-cpu-runner" || startsWith(b, "-enable-cpu-runner=")) {
+      ++runnerFlags;
+    } else if (startsWith(b, "-enable-cpu-runner-before") || startsWith(b, "-enable-cpu-runner-after")) {
+      ++runnerFlags;
+      auto eq = b.find('=');
+      std::string spec = eq == std::string::npos ? "" : b.substr(eq + 1);
+      std::string pass = spec.substr(0, spec.find(','));
+      if (pass.empty()) { std::fprintf(stderr, "[ERROR] At least the pass name should be provided!\n"); return EXIT_FAILURE; }
+      for (char c : pass)
+        if (!(std::isalnum((unsigned char)c) || c == '-' || c == '_' || c == '.')) {
+          std::fprintf(stderr, "[ERROR] \"%s\" is not a pass!\n", pass.c_str());
+          return EXIT_FAILURE;
+        }
+      std::string rest = spec.find(',') == std::string::npos ? "" : spec.substr(spec.find(',') + 1);
+      std::string idx = rest.substr(0, rest.find(','));
+      if (!idx.empty() && std::all_of(idx.begin(), idx.end(), [](char c) { return std::isdigit((unsigned char)c) || c == '-'; })) {
+        if (std::atol(idx.c_str()) <= 0) {
+          std::fprintf(stderr, "[ERROR] Pass index should be a positive non-zero integer, but found %s!\n", idx.c_str());
+          return EXIT_FAILURE;
+        }
+      }
+    } else if (startsWith(b, "-runner-inputs=")) {
+      runnerIn = b.substr(15);
+    } else if (startsWith(b, "-runner-outputs=")) {
+      runnerOut = b.substr(16);
+    } else if (startsWith(b, "-runner-func=")) {
+      runnerFunc = b.substr(13);
     } else if (startsWith(b, "-fusion-kind=")) {
       opts += "fusion_kind=" + b.substr(13) + ";";
     } else if (b == "-ordered-fp-sums") {
@@ -62,6 +105,10 @@ int main(int argc, char **argv) {
     }
   }
   if (input.empty()) { std::fprintf(stderr, "[ERROR] no input file\n"); return EXIT_FAILURE; }
+  if (runnerFlags > 1) {
+    std::fprintf(stderr, "[ERROR] Cannot combine any of multible cpu-runner options.\n");
+    return EXIT_FAILURE;
+  }
   if (target != "mi355x" && target != "gfx950") {
     std::fprintf(stderr, "[ERROR] unsupported target '%s' (this build targets mi355x)\n", target.c_str());
     return EXIT_FAILURE;
@@ -77,6 +124,15 @@ int main(int argc, char **argv) {
   if (rc != HFC_OK) {
     std::fprintf(stderr, "[ERROR] %s\n", err.data());
     return EXIT_FAILURE;
+  }
+  if (runnerFlags) {
+    std::string msg;
+    if (runnerIn.empty()) runnerIn = output + ".runner_inputs.txt";
+    if (runnerOut.empty()) runnerOut = output + ".runner_outputs.txt";
+    if (hfusionRun(output + ".manifest", runnerFunc, runnerIn, runnerOut, msg) != 0) {
+      std::fprintf(stderr, "[ERROR] [Runner] %s\n", msg.c_str());
+      return EXIT_FAILURE;
+    }
   }
   return EXIT_SUCCESS;
 }

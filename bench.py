@@ -234,6 +234,26 @@ def summarize_pmc(fetch_dir, write_dir, out, command):
             fh.write(f"traffic {k} fetch_kib={fetch[k]:.1f} write_kib={write[k]:.1f} bytes={tb:.0f}\n")
 
 
+def summarize_counters(d, out, command):
+    """Median per dispatch of every counter of one `rocprofv3 --pmc` csv run,
+    per hf_ kernel.  SQ_INSTS_VALU_MFMA_MOPS_I8 counts int8 matrix operations
+    in units of 512; SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x 256 CUs
+    x 4 SIMDs is the MFMA-busy fraction."""
+    acc = {}
+    for r in _csv_rows(d, "_counter_collection.csv"):
+        if r["Kernel_Name"].startswith("hf_"):
+            acc.setdefault(r["Kernel_Name"], {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    with open(out, "w") as fh:
+        fh.write(f"# rocprofv3 --pmc counters per dispatch, median over dispatches (MI355X)\n# command: {command}\n")
+        for k in sorted(acc):
+            med = {c: statistics.median(v) for c, v in acc[k].items()}
+            fh.write(f"{k}: " + " ".join(f"{c}={v:.0f}" for c, v in sorted(med.items())) + "\n")
+            if "SQ_INSTS_VALU_MFMA_MOPS_I8" in med:
+                fh.write(f"  int8 matrix ops = {med['SQ_INSTS_VALU_MFMA_MOPS_I8'] * 512:.4e}\n")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in med and med.get("GRBM_GUI_ACTIVE"):
+                fh.write(f"  MFMA busy = {med['SQ_VALU_MFMA_BUSY_CYCLES'] / (med['GRBM_GUI_ACTIVE'] * 256 * 4):.3f}\n")
+
+
 def traffic_table():
     f = os.path.join(REPO, "profiles", "hbm_traffic.txt")
     t = {}
@@ -256,10 +276,15 @@ def main():
                     help="write a text summary of a rocprofv3 --stats csv run")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
                     help="write the HBM traffic table from two rocprofv3 --pmc csv runs")
+    ap.add_argument("--summarize-counters", nargs=2, metavar=("DIR", "OUT"),
+                    help="write per-kernel medians of a rocprofv3 --pmc csv run")
     ap.add_argument("--command", default="", help="the profiling command, recorded in the summary")
     args = ap.parse_args()
     if args.summarize_stats:
         summarize_stats(*args.summarize_stats, args.command)
+        return
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters, args.command)
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc, args.command)

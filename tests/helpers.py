@@ -64,3 +64,63 @@ def bf16_ulp_diff(a, b):
     ma = np.where(ia & 0x8000, -(ia & 0x7FFF), ia & 0x7FFF)
     mb = np.where(ib & 0x8000, -(ib & 0x7FFF), ib & 0x7FFF)
     return np.abs(ma - mb)
+
+
+# --------------------------------------------- reference runner text format
+# printData of bishengir/lib/ExecutionEngine/BiShengIRRunnerUtils.cpp:72-97:
+# rank, sizes, then the elements; integers in decimal except int8, which is
+# written as its raw byte; floats as "%.9e" of their float value.
+def print_data(arr, elem):
+    arr = np.asarray(arr)
+    out = [str(arr.ndim)]
+    if arr.ndim:
+        out.append("\n" + " ".join(str(d) for d in arr.shape))
+    flat = arr.reshape(-1)
+    if elem == "bf16":
+        vals = [f"{v:.9e}" for v in (flat.astype(np.uint32) << 16).view(np.float32)]
+    elif elem in ("f32", "f64"):
+        vals = [f"{v:.9e}" for v in flat.astype(np.float64 if elem == "f64" else np.float32)]
+    elif elem == "f16":
+        vals = [f"{v:.9e}" for v in flat.view(np.float16).astype(np.float32)]
+    elif elem == "i8":
+        vals = [bytes([int(v) & 0xFF]).decode("latin-1") for v in flat]
+    elif elem == "i1":
+        vals = [str(int(bool(v))) for v in flat]
+    else:
+        vals = [str(int(v)) for v in flat]
+    body = "".join(("\n" if i == 0 else " ") + v for i, v in enumerate(vals))
+    return ("".join(out) + body + "\n").encode("latin-1")
+
+
+def parse_data_file(raw, elems, shapes):
+    """Reads the tensors of a printData file back, given their element types
+    and shapes (int8 elements are single raw bytes, so the layout is needed)."""
+    pos, out = 0, []
+    for elem, shape in zip(elems, shapes):
+        n = int(np.prod(shape)) if shape else 1
+        header = str(len(shape)) + ("\n" + " ".join(str(d) for d in shape) if shape else "")
+        assert raw[pos:pos + len(header)].decode() == header, (raw[pos:pos + 40], header)
+        pos += len(header)
+        if elem == "i8":
+            body = raw[pos:pos + 2 * n]
+            vals = np.frombuffer(body[1::2], np.int8).copy()
+            pos += 2 * n
+        else:
+            end = raw.index(b"\n", pos + 1)
+            toks = raw[pos + 1:end].split(b" ")
+            pos = end
+            if elem in ("f32", "f64", "bf16", "f16"):
+                f = np.array([float(t) for t in toks], np.float64)
+                if elem == "bf16":
+                    vals = (f.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+                elif elem == "f16":
+                    vals = f.astype(np.float16).view(np.uint16)
+                else:
+                    vals = f.astype(np.float32 if elem == "f32" else np.float64)
+            else:
+                vals = np.array([int(t) for t in toks], np_of(elem))
+        assert raw[pos:pos + 1] == b"\n"
+        pos += 1
+        out.append(vals.reshape(shape))
+    assert pos == len(raw)
+    return out
