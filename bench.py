@@ -237,8 +237,8 @@ def summarize_pmc(fetch_dir, write_dir, out, command):
 def summarize_counters(d, out, command):
     """Median per dispatch of every counter of one `rocprofv3 --pmc` csv run,
     per hf_ kernel.  SQ_INSTS_VALU_MFMA_MOPS_I8 counts int8 matrix operations
-    in units of 512; SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x 256 CUs
-    x 4 SIMDs is the MFMA-busy fraction."""
+    in units of 512; SQ_VALU_MFMA_BUSY_CYCLES is summed over the 1024 SIMDs
+    (256 CUs x 4), so / 1024 gives the busy cycles of one SIMD."""
     acc = {}
     for r in _csv_rows(d, "_counter_collection.csv"):
         if r["Kernel_Name"].startswith("hf_"):
@@ -250,8 +250,8 @@ def summarize_counters(d, out, command):
             fh.write(f"{k}: " + " ".join(f"{c}={v:.0f}" for c, v in sorted(med.items())) + "\n")
             if "SQ_INSTS_VALU_MFMA_MOPS_I8" in med:
                 fh.write(f"  int8 matrix ops = {med['SQ_INSTS_VALU_MFMA_MOPS_I8'] * 512:.4e}\n")
-            if "SQ_VALU_MFMA_BUSY_CYCLES" in med and med.get("GRBM_GUI_ACTIVE"):
-                fh.write(f"  MFMA busy = {med['SQ_VALU_MFMA_BUSY_CYCLES'] / (med['GRBM_GUI_ACTIVE'] * 256 * 4):.3f}\n")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+                fh.write(f"  MFMA busy cycles per SIMD = {med['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024:.0f}\n")
 
 
 def traffic_table():
