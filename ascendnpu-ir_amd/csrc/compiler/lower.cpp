@@ -781,6 +781,12 @@ struct RowEmitter {
     double clampC = 0;
     // set when the value is an invariant-divisor division a / b (lazy)
     std::string divA, divB, divR;
+    // set along rint(a / b) -> clamp -> cast: the dividend and the reciprocal
+    // (`qRcp` indexed by row when qRcpRow), for the packed int8 fast path
+    const Value *qSrc = nullptr;
+    std::string qRcp, qDiv; // reciprocal array (or scalar) and the divisor's per-row access
+    bool qRcpRow = false;
+    bool quant8 = false; // an int8 cast of clamp(rint(a / b)), lo/hi the clamp
   };
   std::map<const Value *, V> val;
   std::vector<std::string> arrays; // loaded element/column input arrays
@@ -1056,6 +1062,10 @@ struct RowEmitter {
         nv.divA = at(opsv[0], "e");
         nv.divB = bAt;
         nv.divR = rAt;
+        nv.qSrc = opsv[0];
+        nv.qRcp = rn;
+        nv.qRcpRow = val[b].sp == Sp::Row;
+        nv.qDiv = val[b].sp == Sp::Row ? atRow(b, "rr") : val[b].name;
       } else if ((op->name == "hfusion.elemwise_unary" && fn == "nearbyint") && U == Elem::F32 && opsv[0]->type.elem == Elem::F32 &&
                  val[opsv[0]].lazy && !val[opsv[0]].divA.empty() && uses(opsv[0]) == 1) {
         // rint of a division by a per-row divisor (dynamic quantisation)
@@ -1064,6 +1074,10 @@ struct RowEmitter {
         fast = true;
         integral = true;
         nv.guarded = true;
+        nv.qSrc = d.qSrc;
+        nv.qRcp = d.qRcp;
+        nv.qRcpRow = d.qRcpRow;
+        nv.qDiv = d.qDiv;
       } else if ((fn == "maxf" || fn == "minf") && U == Elem::F32 && opsv.size() == 2 && opsv[1]->isConst &&
                  val[opsv[0]].lazy && val[opsv[0]].guarded) {
         // clamp of a guarded (non-NaN in fast mode) value: min/max pairs fold
@@ -1088,6 +1102,12 @@ struct RowEmitter {
         fast = true;
         integral = x.integral && std::floor(c) == c;
         nv.guarded = true;
+        if (integral && uses(opsv[0]) == 1) {
+          nv.qSrc = x.qSrc;
+          nv.qRcp = x.qRcp;
+          nv.qRcpRow = x.qRcpRow;
+          nv.qDiv = x.qDiv;
+        }
       } else {
         std::vector<std::string> args;
         for (auto *v : opsv) args.push_back(at(v, "e"));
@@ -1098,6 +1118,16 @@ struct RowEmitter {
           if (x.ranged && x.lo >= tlo && x.hi <= thi && elemBits(U) <= 32)
             // integral and inside the target range: one convert (NaN -> 0)
             expr = "(" + ctype(U) + ")(int32_t)(" + args[0] + ")";
+          if (U == Elem::I8 && x.ranged && x.qSrc && x.lo >= -128 && x.hi <= 127 && x.lo <= x.hi &&
+              std::floor(x.lo) == x.lo && std::floor(x.hi) == x.hi && uses(opsv[0]) == 1) {
+            nv.quant8 = true;
+            nv.qSrc = x.qSrc;
+            nv.qRcp = x.qRcp;
+            nv.qRcpRow = x.qRcpRow;
+            nv.qDiv = x.qDiv;
+            nv.lo = x.lo;
+            nv.hi = x.hi;
+          }
           else
             expr = "hf::integral_to_int<" + ctype(U) + ", " + (sat ? "true" : "false") + ">(" + args[0] + ")";
         } else {
@@ -1226,7 +1256,25 @@ struct RowEmitter {
              << " + row[rr] * C, lt, C, j, st_);\n" << ind
              << "    __builtin_amdgcn_sched_barrier(0); // bound the live range to one chunk\n" << ind << "  }\n";
       };
-      storeLoop("ex", "  ");
+      const V &q = val[v];
+      if (q.quant8 && e == Elem::I8) {
+        // int8 quantisation: four elements per packed word through
+        // hf::quant8x4 in the fast pass; the exact pass stores element-wise
+        body << "  if constexpr (EXM::value || VEC % 4 != 0) {\n";
+        storeLoop("ex", "    ");
+        const std::string rcp = q.qRcpRow ? q.qRcp + "[rr]" : q.qRcp;
+        body << "  } else {\n#pragma unroll\n    for (int rr = 0; rr < RPW; ++rr)\n#pragma unroll\n"
+             << "      for (int j = 0; j < EPL / VEC; ++j) {\n        uint32_t st_[VEC / 4];\n#pragma unroll\n"
+             << "        for (int w = 0; w < VEC / 4; ++w) {\n          float a_[4];\n#pragma unroll\n"
+             << "          for (int i = 0; i < 4; ++i) a_[i] = " << at(q.qSrc, "rr * EPL + j * VEC + 4 * w + i") << ";\n"
+             << "          st_[w] = hf::quant8x4<" << (int)q.lo << ", " << (int)q.hi << ">(a_, " << q.qDiv << ", " << rcp
+             << ", hf_g);\n"
+             << "        }\n        hf::row_store_chunk<int8_t, VEC, TR, MASKED>((int8_t*)" << ptr
+             << " + row[rr] * C, lt, C, j, (const int8_t*)st_);\n"
+             << "        __builtin_amdgcn_sched_barrier(0); // bound the live range to one chunk\n      }\n  }\n";
+      } else {
+        storeLoop("ex", "  ");
+      }
     } else if (ms == Sp::Row || (ms == Sp::Scalar && A.D.size() == 1)) {
       std::string idx = ms == Sp::Row ? "row[rr]" : "0";
       body << "#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) if (row_ok[rr] && lt == 0) ((" << M << "*)" << ptr << ")[" << idx

@@ -223,13 +223,19 @@ struct Guard {
   float qmax = 0.0f;
   int emin = 0, emax = 0;
   int dmin = 0, dmax = 0; // exponent range of div_rn dividends and quotients
+  // quant8x4: range of the biased quotients next to the clamp bounds they
+  // must respect
+  float tmin = __builtin_inff(), tmax = -__builtin_inff();
+  float tmin_need = -__builtin_inff(), tmax_need = __builtin_inff();
   __device__ __forceinline__ bool bad() const {
-    return !(qmax <= 0x1p+100f) || emin < -96 || emax > 40 || dmin < -96 || dmax > 100;
+    return !(qmax <= 0x1p+100f) || emin < -96 || emax > 40 || dmin < -96 || dmax > 100 ||
+           !(tmin >= tmin_need) || !(tmax <= tmax_need);
   }
-  // per-row divisor check: r = RN(1/b) must be a normal number with exponent
-  // in [-96, 40] (so |b| >= 2^-41 and the reciprocal is exact-rounded normal)
+  // per-row divisor check: r = RN(1/b) must be a finite normal number with
+  // exponent in [-96, 40] (so |b| >= 2^-41 and the reciprocal is
+  // exact-rounded normal); frexp reports 0 for inf/NaN, hence the extra test
   __device__ __forceinline__ void divisor(float r) {
-    const int er = __builtin_amdgcn_frexp_expf(r);
+    const int er = __builtin_fabsf(r) <= 0x1.fffffep+127f ? __builtin_amdgcn_frexp_expf(r) : -1000;
     asm volatile("v_min3_i32 %0, %0, %2, %2\n\tv_max3_i32 %1, %1, %2, %2" : "+v"(emin), "+v"(emax) : "v"(er));
   }
 };
@@ -258,6 +264,59 @@ __device__ __forceinline__ float rint_div(float a, float b, float r, Guard &g, E
     asm volatile("v_maximum3_f32 %0, %0, |%1|, |%1|" : "+v"(g.qmax) : "v"(q));
     return __builtin_roundevenf(q);
   }
+}
+
+// int8 dynamic quantisation, four elements to one packed word:
+//   (int8)clamp(rint(RN(a_i / b)), LO, HI),  LO >= -128, HI <= 127,
+// given r = RN(1/b) (passed Guard::divisor).  With Q = a/b exact,
+// tl = RN(a*r + 128 - 2^-15) and th = RN(a*r + 128 + 2^-15) bracket Q + 128:
+// a*r = Q(1 + e) with |e| <= 2^-24, so for |Q| < 128 the product is within
+// 2^-17 of Q and each sum within 2^-17 more of its target, while RN(Q) + 128
+// is within 2^-18 of Q + 128 -- strictly between tl and th.
+// v_cvt_pk_u8_f32 rounds half to even and clamps to [0, 255]; RNE is
+// monotonic, so when the two packed words agree every byte is
+// RNE(RN(Q) + 128) = rint(RN(Q)) + 128 (128 is even) and XOR 0x80 gives the
+// int8 value.  A word that disagrees holds a quotient near a half-integer
+// (about one element in 10^4): its four elements are recomputed with the
+// exact quotient (rint_div) in place.
+// Clamps: HI = 127 is the converter's own upper clamp (+inf included);
+// LO > -128 and HI < 127 are checked on the tracked extremes, and the
+// NaN-propagating minimum also catches NaN quotients: those blocks take the
+// exact path.
+template <int LO, int HI>
+__device__ __forceinline__ uint32_t quant8x4(const float (&a)[4], float b, float r, Guard &g) {
+  static_assert(-128 <= LO && LO <= HI && HI <= 127, "int8 clamp bounds");
+  constexpr float D = 0x1p-15f;
+  float tl[4], th[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    tl[i] = __builtin_fmaf(a[i], r, 128.0f - D);
+    th[i] = __builtin_fmaf(a[i], r, 128.0f + D);
+  }
+  uint32_t wl = __builtin_amdgcn_cvt_pk_u8_f32(tl[0], 0, 0u), wh = __builtin_amdgcn_cvt_pk_u8_f32(th[0], 0, 0u);
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    wl = __builtin_amdgcn_cvt_pk_u8_f32(tl[i], i, wl);
+    wh = __builtin_amdgcn_cvt_pk_u8_f32(th[i], i, wh);
+  }
+  asm volatile("v_minimum3_f32 %0, %0, %1, %2\n\tv_minimum3_f32 %0, %0, %3, %4"
+               : "+v"(g.tmin) : "v"(tl[0]), "v"(tl[1]), "v"(tl[2]), "v"(tl[3]));
+  g.tmin_need = (float)LO + 127.5f + 0x1p-12f;
+  if constexpr (HI < 127) {
+    asm volatile("v_maximum3_f32 %0, %0, %1, %2\n\tv_maximum3_f32 %0, %0, %3, %4"
+                 : "+v"(g.tmax) : "v"(th[0]), "v"(th[1]), "v"(th[2]), "v"(th[3]));
+    g.tmax_need = (float)HI + 128.5f - 0x1p-12f;
+  }
+  uint32_t w = wl ^ 0x80808080u;
+  if (__builtin_expect(wl != wh, 0)) {
+    w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float q = __builtin_amdgcn_fmed3f(rint_div(a[i], b, r, g, kFast{}), (float)LO, (float)HI);
+      w |= ((uint32_t)(int32_t)q & 0xFFu) << (8 * i);
+    }
+  }
+  return w;
 }
 
 // float already holding an integral value (or +-inf/NaN) -> integer type T:

@@ -201,29 +201,710 @@ __device__ __forceinline__ T row_allreduce(T v, F comb, T *lds, int rloc, int lt
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // acc + rp[0] + rp[1] + ... + rp[N-1], strictly in that order, from LDS.
-// The dependent adds run at the VALU latency; to keep LDS latency off that
-// path, PF ds_read_b128 are kept in flight with explicit lgkmcnt waits (the
-// compiler would otherwise wait for each read right after issuing it when
-// registers are scarce).  Each wait names the register it guards as an
-// in/out operand, so the adds that consume it cannot move above the wait, and
-// each refill names the running sum, so it cannot move above those adds.
-// Serial fold of N floats of one LDS row into acc, left to right.  Plain
-// code on purpose: with a 16-read unroll the compiler keeps enough
-// ds_read_b128 in flight to hide their latency behind the dependent adds
-// (measured on gfx950: 7.3-7.7 cycles per add, the v_add_f32 dependency
-// latency), while hand-placed s_waitcnt variants ran at 12-14 cycles.
+// The dependent adds run at the v_add_f32 latency (7.3-7.7 cycles on gfx950)
+// only if the LDS reads never stall them.  The compiler, short of registers
+// in this kernel, reuses one 4-register buffer and waits on every read, so
+// the 512-float case is one asm statement: two fixed buffers, the reads of the
+// next 16 floats in flight while the 16 adds of the current ones run (about
+// 10 -> 7.7 cycles per add measured in the RMSNorm kernel).
 template <int N>
 __device__ __forceinline__ float lds_chain_sum(const float *rp, float acc) {
   static_assert(N % 64 == 0, "chunk must be a multiple of 64 floats");
+  if constexpr (N == 512) {
+    // 32 groups of 16 floats through two fixed register buffers
+    // (v224-v239, v240-v255): the four reads of group g+1 are in flight
+    // while the 16 dependent adds of group g run, so the LDS latency stays
+    // hidden behind the chain.  One asm statement, so no compiler code runs
+    // between a read and the wait that covers it.
+    const uint32_t p = (uint32_t)(uintptr_t)rp;
+    asm volatile(
+      "ds_read_b128 v[224:227], %[p] offset:0\n"
+      "ds_read_b128 v[228:231], %[p] offset:16\n"
+      "ds_read_b128 v[232:235], %[p] offset:32\n"
+      "ds_read_b128 v[236:239], %[p] offset:48\n"
+      "ds_read_b128 v[240:243], %[p] offset:64\n"
+      "ds_read_b128 v[244:247], %[p] offset:80\n"
+      "ds_read_b128 v[248:251], %[p] offset:96\n"
+      "ds_read_b128 v[252:255], %[p] offset:112\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:128\n"
+      "ds_read_b128 v[228:231], %[p] offset:144\n"
+      "ds_read_b128 v[232:235], %[p] offset:160\n"
+      "ds_read_b128 v[236:239], %[p] offset:176\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:192\n"
+      "ds_read_b128 v[244:247], %[p] offset:208\n"
+      "ds_read_b128 v[248:251], %[p] offset:224\n"
+      "ds_read_b128 v[252:255], %[p] offset:240\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:256\n"
+      "ds_read_b128 v[228:231], %[p] offset:272\n"
+      "ds_read_b128 v[232:235], %[p] offset:288\n"
+      "ds_read_b128 v[236:239], %[p] offset:304\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:320\n"
+      "ds_read_b128 v[244:247], %[p] offset:336\n"
+      "ds_read_b128 v[248:251], %[p] offset:352\n"
+      "ds_read_b128 v[252:255], %[p] offset:368\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:384\n"
+      "ds_read_b128 v[228:231], %[p] offset:400\n"
+      "ds_read_b128 v[232:235], %[p] offset:416\n"
+      "ds_read_b128 v[236:239], %[p] offset:432\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:448\n"
+      "ds_read_b128 v[244:247], %[p] offset:464\n"
+      "ds_read_b128 v[248:251], %[p] offset:480\n"
+      "ds_read_b128 v[252:255], %[p] offset:496\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:512\n"
+      "ds_read_b128 v[228:231], %[p] offset:528\n"
+      "ds_read_b128 v[232:235], %[p] offset:544\n"
+      "ds_read_b128 v[236:239], %[p] offset:560\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:576\n"
+      "ds_read_b128 v[244:247], %[p] offset:592\n"
+      "ds_read_b128 v[248:251], %[p] offset:608\n"
+      "ds_read_b128 v[252:255], %[p] offset:624\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:640\n"
+      "ds_read_b128 v[228:231], %[p] offset:656\n"
+      "ds_read_b128 v[232:235], %[p] offset:672\n"
+      "ds_read_b128 v[236:239], %[p] offset:688\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:704\n"
+      "ds_read_b128 v[244:247], %[p] offset:720\n"
+      "ds_read_b128 v[248:251], %[p] offset:736\n"
+      "ds_read_b128 v[252:255], %[p] offset:752\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:768\n"
+      "ds_read_b128 v[228:231], %[p] offset:784\n"
+      "ds_read_b128 v[232:235], %[p] offset:800\n"
+      "ds_read_b128 v[236:239], %[p] offset:816\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:832\n"
+      "ds_read_b128 v[244:247], %[p] offset:848\n"
+      "ds_read_b128 v[248:251], %[p] offset:864\n"
+      "ds_read_b128 v[252:255], %[p] offset:880\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:896\n"
+      "ds_read_b128 v[228:231], %[p] offset:912\n"
+      "ds_read_b128 v[232:235], %[p] offset:928\n"
+      "ds_read_b128 v[236:239], %[p] offset:944\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:960\n"
+      "ds_read_b128 v[244:247], %[p] offset:976\n"
+      "ds_read_b128 v[248:251], %[p] offset:992\n"
+      "ds_read_b128 v[252:255], %[p] offset:1008\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1024\n"
+      "ds_read_b128 v[228:231], %[p] offset:1040\n"
+      "ds_read_b128 v[232:235], %[p] offset:1056\n"
+      "ds_read_b128 v[236:239], %[p] offset:1072\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1088\n"
+      "ds_read_b128 v[244:247], %[p] offset:1104\n"
+      "ds_read_b128 v[248:251], %[p] offset:1120\n"
+      "ds_read_b128 v[252:255], %[p] offset:1136\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1152\n"
+      "ds_read_b128 v[228:231], %[p] offset:1168\n"
+      "ds_read_b128 v[232:235], %[p] offset:1184\n"
+      "ds_read_b128 v[236:239], %[p] offset:1200\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1216\n"
+      "ds_read_b128 v[244:247], %[p] offset:1232\n"
+      "ds_read_b128 v[248:251], %[p] offset:1248\n"
+      "ds_read_b128 v[252:255], %[p] offset:1264\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1280\n"
+      "ds_read_b128 v[228:231], %[p] offset:1296\n"
+      "ds_read_b128 v[232:235], %[p] offset:1312\n"
+      "ds_read_b128 v[236:239], %[p] offset:1328\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1344\n"
+      "ds_read_b128 v[244:247], %[p] offset:1360\n"
+      "ds_read_b128 v[248:251], %[p] offset:1376\n"
+      "ds_read_b128 v[252:255], %[p] offset:1392\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1408\n"
+      "ds_read_b128 v[228:231], %[p] offset:1424\n"
+      "ds_read_b128 v[232:235], %[p] offset:1440\n"
+      "ds_read_b128 v[236:239], %[p] offset:1456\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1472\n"
+      "ds_read_b128 v[244:247], %[p] offset:1488\n"
+      "ds_read_b128 v[248:251], %[p] offset:1504\n"
+      "ds_read_b128 v[252:255], %[p] offset:1520\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1536\n"
+      "ds_read_b128 v[228:231], %[p] offset:1552\n"
+      "ds_read_b128 v[232:235], %[p] offset:1568\n"
+      "ds_read_b128 v[236:239], %[p] offset:1584\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1600\n"
+      "ds_read_b128 v[244:247], %[p] offset:1616\n"
+      "ds_read_b128 v[248:251], %[p] offset:1632\n"
+      "ds_read_b128 v[252:255], %[p] offset:1648\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1664\n"
+      "ds_read_b128 v[228:231], %[p] offset:1680\n"
+      "ds_read_b128 v[232:235], %[p] offset:1696\n"
+      "ds_read_b128 v[236:239], %[p] offset:1712\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1728\n"
+      "ds_read_b128 v[244:247], %[p] offset:1744\n"
+      "ds_read_b128 v[248:251], %[p] offset:1760\n"
+      "ds_read_b128 v[252:255], %[p] offset:1776\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1792\n"
+      "ds_read_b128 v[228:231], %[p] offset:1808\n"
+      "ds_read_b128 v[232:235], %[p] offset:1824\n"
+      "ds_read_b128 v[236:239], %[p] offset:1840\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1856\n"
+      "ds_read_b128 v[244:247], %[p] offset:1872\n"
+      "ds_read_b128 v[248:251], %[p] offset:1888\n"
+      "ds_read_b128 v[252:255], %[p] offset:1904\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "ds_read_b128 v[224:227], %[p] offset:1920\n"
+      "ds_read_b128 v[228:231], %[p] offset:1936\n"
+      "ds_read_b128 v[232:235], %[p] offset:1952\n"
+      "ds_read_b128 v[236:239], %[p] offset:1968\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      "ds_read_b128 v[240:243], %[p] offset:1984\n"
+      "ds_read_b128 v[244:247], %[p] offset:2000\n"
+      "ds_read_b128 v[248:251], %[p] offset:2016\n"
+      "ds_read_b128 v[252:255], %[p] offset:2032\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[acc], v224, %[acc]\n"
+      "v_add_f32 %[acc], v225, %[acc]\n"
+      "v_add_f32 %[acc], v226, %[acc]\n"
+      "v_add_f32 %[acc], v227, %[acc]\n"
+      "v_add_f32 %[acc], v228, %[acc]\n"
+      "v_add_f32 %[acc], v229, %[acc]\n"
+      "v_add_f32 %[acc], v230, %[acc]\n"
+      "v_add_f32 %[acc], v231, %[acc]\n"
+      "v_add_f32 %[acc], v232, %[acc]\n"
+      "v_add_f32 %[acc], v233, %[acc]\n"
+      "v_add_f32 %[acc], v234, %[acc]\n"
+      "v_add_f32 %[acc], v235, %[acc]\n"
+      "v_add_f32 %[acc], v236, %[acc]\n"
+      "v_add_f32 %[acc], v237, %[acc]\n"
+      "v_add_f32 %[acc], v238, %[acc]\n"
+      "v_add_f32 %[acc], v239, %[acc]\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "v_add_f32 %[acc], v240, %[acc]\n"
+      "v_add_f32 %[acc], v241, %[acc]\n"
+      "v_add_f32 %[acc], v242, %[acc]\n"
+      "v_add_f32 %[acc], v243, %[acc]\n"
+      "v_add_f32 %[acc], v244, %[acc]\n"
+      "v_add_f32 %[acc], v245, %[acc]\n"
+      "v_add_f32 %[acc], v246, %[acc]\n"
+      "v_add_f32 %[acc], v247, %[acc]\n"
+      "v_add_f32 %[acc], v248, %[acc]\n"
+      "v_add_f32 %[acc], v249, %[acc]\n"
+      "v_add_f32 %[acc], v250, %[acc]\n"
+      "v_add_f32 %[acc], v251, %[acc]\n"
+      "v_add_f32 %[acc], v252, %[acc]\n"
+      "v_add_f32 %[acc], v253, %[acc]\n"
+      "v_add_f32 %[acc], v254, %[acc]\n"
+      "v_add_f32 %[acc], v255, %[acc]\n"
+      : [acc] "+v"(acc)
+      : [p] "v"(p)
+      : "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", "v254", "v255", "memory");
+    return acc;
+  } else {
 #pragma unroll 16
-  for (int c = 0; c < N; c += 4) {
-    const f32x4 q = *reinterpret_cast<const f32x4 *>(rp + c);
-    acc = q.x + acc;
-    acc = q.y + acc;
-    acc = q.z + acc;
-    acc = q.w + acc;
+    for (int c = 0; c < N; c += 4) {
+      const f32x4 q = *reinterpret_cast<const f32x4 *>(rp + c);
+      acc = q.x + acc;
+      acc = q.y + acc;
+      acc = q.z + acc;
+      acc = q.w + acc;
+    }
+    return acc;
   }
-  return acc;
 }
 
 // Serial-order fp32 sums of the RB*RPW rows of a block, bit-identical to the

@@ -169,6 +169,36 @@ def quant_ties(rows=64, cols=1024):
 FP8_TYPES = {"e4m3": "f8E4M3FN", "e5m2": "f8E5M2"}
 
 
+def quant_i8_ties(rows=64, cols=1024, lo=-127, hi=127, name="quant_i8_ties"):
+    """(int8)clamp(nearbyint(x / s[row]), lo, hi): the int8 dynamic-quant tail
+    on its own (with a row max beside it, so the group is a row program),
+    for quotients on and next to half-integers and beyond the clamp bounds."""
+    X, R, Q = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i8")
+    return f"""module {{
+  func.func @{name}(%x: {X}, %s: {R}, %q: {Q}, %mx: {R}) -> ({Q}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %f = linalg.fill ins(%ninf : f32) outs(%mx : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f : {R}) dimensions = [1]
+    %hi = arith.constant {float(hi):.6e} : f32
+    %lo = arith.constant {float(lo):.6e} : f32
+    %e0 = tensor.empty() : {X}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e0 : {X}) dimensions = [1]
+    %e1 = tensor.empty() : {X}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%x, %bs : {X}, {X}) outs(%e1 : {X}) -> {X}
+    %e2 = tensor.empty() : {X}
+    %r = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<nearbyint>}} ins(%d : {X}) outs(%e2 : {X}) -> {X}
+    %e3 = tensor.empty() : {X}
+    %c1 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<minf>}} ins(%r, %hi : {X}, f32) outs(%e3 : {X}) -> {X}
+    %e4 = tensor.empty() : {X}
+    %c2 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<maxf>}} ins(%c1, %lo : {X}, f32) outs(%e4 : {X}) -> {X}
+    %o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%c2 : {X}) outs(%q : {Q}) -> {Q}
+    return %o, %m : {Q}, {R}
+  }}
+}}
+"""
+
+
 def cast_fp8(n=4096):
     """fp8 casts: f32 -> f8E4M3FN / f8E5M2 under every round mode, with and
     without saturation; fp8 -> f32; f16 <-> f8E5M2 through f32 (the form of
@@ -291,6 +321,9 @@ def entries():
     e["layernorm"] = layernorm(64, 2048)
     e["reduce_ops"] = reduce_ops(48, 3000)
     e["quant_ties"] = quant_ties(64, 1024)
+    e["quant_i8_ties"] = quant_i8_ties(64, 1024)
+    e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")
+    e["quant_i8_ties_narrow"] = quant_i8_ties(64, 1000, lo=-100, hi=100, name="quant_i8_ties_narrow")
     e["cast_fp8"] = cast_fp8(4096)
     e["fp8_quant"] = fp8_quant(64, 4096)
     e["fp8_quant_ragged"] = fp8_quant(13, 1000)

@@ -411,3 +411,32 @@ def test_program_scores_softmax(gpu, name, shape):
     out, = run_gpu(name, args, gpu)
     ref, = run_oracle(name, args)
     assert bf16_ulp_diff(out, ref).max() <= 1
+
+
+@pytest.mark.parametrize("name,cols", [("quant_i8_ties", 1024), ("quant_i8_ties_m128", 1024),
+                                       ("quant_i8_ties_narrow", 1000)])
+def test_int8_quant_near_ties(gpu, name, cols):
+    """(int8)clamp(nearbyint(x / s[row])) through the packed fast path:
+    quotients on and a few ulp around half-integers (the bracketing check
+    sends those blocks to the exact path), beyond the clamp bounds, specials."""
+    note(name)
+    rows = 64
+    s = I.uniform_f32(I.SEED_BASE + 95, (rows,), 0.001, 0.02)
+    s[5] = 3.0e-39   # denormal divisor: reciprocal overflows
+    s[6] = 1.0e-30   # huge quotients
+    k = (I.splitmix64(I.SEED_BASE + 96, rows * cols) % np.uint64(301)).astype(np.int64).reshape(rows, cols) - 150
+    x = ((k.astype(np.float64) + 0.5) * s[:, None].astype(np.float64)).astype(np.float32)
+    nud = ((I.splitmix64(I.SEED_BASE + 97, rows * cols) % np.uint64(7)).astype(np.int64) - 3).reshape(rows, cols)
+    x = (x.view(np.int32) + nud.astype(np.int32)).view(np.float32).copy()
+    # rows 10..39: quotients well inside the range and away from ties, so
+    # those blocks stay on the fast path
+    fr = (I.splitmix64(I.SEED_BASE + 98, 30 * cols) % np.uint64(1000)).astype(np.float64).reshape(30, cols) / 1000.0
+    kk = k[10:40] % 200 - 100
+    x[10:40] = ((kk + 0.05 + 0.4 * fr) * s[10:40, None].astype(np.float64)).astype(np.float32)
+    x[0, :8] = [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3e38]
+    x[1, :] = np.float32(0.5) * s[1]  # exact ties
+    args = [x, s, np.zeros((rows, cols), np.int8), np.zeros(rows, np.float32)]
+    out, mx = run_gpu(name, args, gpu)
+    ref, rmx = run_oracle(name, args)
+    assert np.array_equal(mx, rmx, equal_nan=True)
+    assert np.array_equal(out, ref), int((out != ref).sum())
