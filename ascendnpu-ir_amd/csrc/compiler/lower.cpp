@@ -1748,7 +1748,10 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   if (!bT && (N * esz) % 16 != 0) unsupported(mm, "matmul N must span a multiple of 16 bytes when B is [K, N]");
   if (aT && (M * esz) % 16 != 0) unsupported(mm, "matmul M must span a multiple of 16 bytes when A is [K, M]");
   // B [N, K] and A [M, K] with whole 64-byte K steps: both operands stream into LDS by DMA
-  const bool dma = bT && !aT && (K * esz) % 64 == 0;
+  // LDS DMA ring: 128-byte K slices with two waves per SIMD when K allows,
+  // else 64-byte slices
+  const int dma = !(bT && !aT) ? 0 : (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
+  const int threads = dma == 3 ? 512 : 256;
   if (!hivm) {
     const Value *acc0 = mm->outs[0];
     if (!(acc0->def && acc0->def->name == "linalg.fill" && acc0->def->ins[0]->isConst && acc0->def->ins[0]->fconst == 0.0))
@@ -1852,21 +1855,21 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   for (size_t i = 0; i < A.params.size(); ++i)
     if (A.params[i].role == "scalar") k << "    const uint64_t s" << i << " = P.s" << i << ";\n";
   k << epi.str() << "    return (out_t)" << name[outv] << ";\n  }\n};\n}\n";
-  k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+  k << "extern \"C\" __global__ __launch_bounds__(" << threads << ") void " << kname << "(" << params << ") {\n"
     << "  " << kname << "_args P;\n";
   for (size_t i = 0; i < A.params.size(); ++i)
     k << "  P." << (A.params[i].role == "scalar" ? "s" : "p") << i << " = " << (A.params[i].role == "scalar" ? "s" : "p") << i << ";\n";
   k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (aT ? "true" : "false") << ", " << (bT ? "true" : "false") << ", "
-    << (dma ? "true" : "false") << ">((const " << (i8 ? "int8_t" : "uint16_t") << "*)p" << a->argIdx << ", (const "
+    << dma << ">((const " << (i8 ? "int8_t" : "uint16_t") << "*)p" << a->argIdx << ", (const "
     << (i8 ? "int8_t" : "uint16_t") << "*)p" << b->argIdx
     << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
   p.source = k.str();
   // 256x256 macro-tiles, one workgroup each (XCD-aware order inside the kernel)
   const int64_t TM = 256, TN = 256;
   p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
-  p.block[0] = 256;
+  p.block[0] = (unsigned)threads;
   p.variant = std::string(mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
-              (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") + (dma ? ", LDS DMA ring" : ", register staging");
+              (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") + (dma == 3 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD)" : dma == 1 ? ", LDS DMA ring" : ", register staging");
   p.algoOps = 2.0 * (double)M * (double)N * (double)K;
   return p;
 }

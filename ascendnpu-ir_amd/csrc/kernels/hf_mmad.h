@@ -175,12 +175,13 @@ __device__ __forceinline__ void mm_epilogue(acc_t (&acc)[4][4], typename Epi::ou
 
 // Epilogue through LDS (the DMA path's ring is free by then): the tile's
 // outputs are computed into a row-major out_t stage, then the whole
-// workgroup writes them out as 16-byte row segments (a 256-column row is one
-// contiguous run of C).  When the whole 256x256 tile fits the stage (2-byte
-// outputs) all four waves compute at once; otherwise the two row halves
-// (waves wm = 0, then wm = 1) take turns.
-template <typename Epi, typename acc_t, typename Args>
-__device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][4], typename Epi::out_t *__restrict__ out, int64_t M,
+// workgroup (NT threads) writes them out as 16-byte row segments (a
+// 256-column row is one contiguous run of C).  Each wave holds 128 rows x
+// 32*JT columns.  When the whole 256x256 tile fits the stage (2-byte
+// outputs) all waves compute at once; otherwise the two row halves (waves
+// wm = 0, then wm = 1) take turns.
+template <typename Epi, int JT = 4, int NT = 256, typename acc_t, typename Args>
+__device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][JT], typename Epi::out_t *__restrict__ out, int64_t M,
                                                 int64_t N, int64_t m0, int64_t n0, int wm, int wn, int lane, const Args &P,
                                                 char *stage, int stage_bytes) {
   using O = typename Epi::out_t;
@@ -204,8 +205,8 @@ __device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][4], typename Epi
           rv[r] = Epi::row(m < M ? m : M - 1, P);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = wn * 128 + j * 32 + lane % 32;
+        for (int j = 0; j < JT; ++j) {
+          const int col = wn * (32 * JT) + j * 32 + lane % 32;
           const int64_t n = n0 + col;
           const typename Epi::col_t cv = Epi::col(n < N ? n : N - 1, P);
           acc_t a = acc[i][j];
@@ -225,7 +226,7 @@ __device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][4], typename Epi
     __syncthreads();
     const int64_t mrow0 = m0 + (one_pass ? 0 : h * 128);
 #pragma unroll 4
-    for (int c = tid; c < rows_per_pass * CPR; c += 256) {
+    for (int c = tid; c < rows_per_pass * CPR; c += NT) {
       const int row = c / CPR, ch = c % CPR;
       const int64_t m = mrow0 + row, n = n0 + (int64_t)ch * EPC;
       if (m >= M) continue;
@@ -461,14 +462,134 @@ __device__ void mmad_core_dma(const ElemT *__restrict__ A, const ElemT *__restri
   mm_epilogue_lds<Epi>(acc, out, M, N, m0, n0, wm, wn, lane, P, &lds[0][0][0], (int)sizeof(lds));
 }
 
+// ---- DMA path, 128-byte K slices --------------------------------------------
+// Same tile and MFMA layout as above, but each stage carries 128 bytes of K
+// per row: every row read is a whole 128-byte line, which on gfx950 feeds a
+// CU about 1.5x faster than 64-byte halves (the per-CU feed is bounded by the
+// L1's outstanding requests).  Two stages of 2 x 32 KB (mmad_core_pp below).
+// Slice layout: 256 rows x 8 granules of 16 bytes; logical granule g of row r
+// sits at 8r + (g ^ ((r >> 1) & 7)), so the 16 lanes a ds_read_b128 serves
+// per cycle (16 consecutive rows, one logical granule) cover 16 distinct
+// 4-bank groups.  A DMA instruction writes 8 rows (lane l -> row l/8,
+// position l%8), and each lane fetches the global granule that belongs there.
+constexpr int MMD2_SLICE = 256 * 128;
+
+// ---- DMA path, 128-byte K slices, two waves per SIMD -------------------------
+// With one wave per SIMD, a DMA that waits for a free memory-queue slot also
+// holds back that wave's MFMAs, so feed and multiply add up instead of
+// overlapping.  Here 8 waves (512 threads) share the 256x256 tile, two per
+// SIMD, each 128 rows x 64 columns (4 x 2 MFMA tiles, 128 accumulator
+// registers): while one wave of a SIMD waits on memory, the other issues
+// MFMAs.  Ring: two stages of 128-byte K slices, swizzled as described above;
+// each wave issues 8 DMAs per stage (its 32 rows of A and of B).
+template <int MK, typename Epi, typename ElemT, typename Args>
+__device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
+                             int64_t M, int64_t N, int64_t K, const Args &P) {
+  using Op = MfmaOp<MK>;
+  using acc_t = typename Op::acc_t;
+  constexpr int ESZ = sizeof(ElemT);
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][MMD2_SLICE]; // [stage][A/B]
+  const int tmt = (int)((M + MM_TM - 1) / MM_TM), tnt = (int)((N + MM_TN - 1) / MM_TN);
+  int ti, tj;
+  mm_tile_of(blockIdx.x, tmt, tnt, ti, tj);
+  const int64_t m0 = (int64_t)ti * MM_TM, n0 = (int64_t)tj * MM_TN;
+  const int64_t Kb = K * ESZ;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int wm = wave / 4, wn = wave % 4; // waves w and w+4 share a SIMD
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)&lds[0][0][0];
+  const char *Ab = reinterpret_cast<const char *>(A), *Bb = reinterpret_cast<const char *>(B);
+  const int nsteps = (int)(Kb / 128);
+
+  // DMA d (0..7) of K slice s into ring slot `slot`: d < 4 this wave's A
+  // rows (32 * wave ..), else its B rows, 8 rows per instruction
+  auto issue_one = [&](int s, int slot, int d) {
+    const uint32_t st = lds0 + (uint32_t)(slot * 2 * MMD2_SLICE) + (d < 4 ? 0u : (uint32_t)MMD2_SLICE);
+    const int blk = wave * 4 + (d & 3);
+    const int r = 8 * blk + lane / 8;
+    const int g = (lane % 8) ^ ((r >> 1) & 7);
+    const int64_t rows = d < 4 ? M : N, row0 = d < 4 ? m0 : n0;
+    int64_t row = row0 + r;
+    row = row < rows ? row : rows - 1;
+    mmd_dma16((d < 4 ? Ab : Bb) + row * Kb + (int64_t)s * 128 + g * 16, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+  };
+  auto issue_stage = [&](int s) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) issue_one(s < nsteps ? s : nsteps - 1, s & 1, d);
+  };
+
+  acc_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+
+  auto frag = [&](const char *slice, int blk, int g) -> v4i {
+    const int r = blk * 32 + lane % 32;
+    return *reinterpret_cast<const v4i *>(slice + (8 * r + (g ^ ((r >> 1) & 7))) * 16);
+  };
+  // the 12 fragments (2 k-blocks x (4 A + 2 B)) of half h of stage s
+  auto fetch = [&](int s, int h, v4i (&f)[2][6]) {
+    const char *la = lds[s & 1][0], *lb = lds[s & 1][1];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[q][i] = frag(la, wm * 4 + i, 4 * h + 2 * q + lane / 32);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) f[q][4 + j] = frag(lb, wn * 2 + j, 4 * h + 2 * q + lane / 32);
+    }
+  };
+
+  // Step s: wait for stage s (stage s+1 may be in flight); multiply its first
+  // half while reading the second half's fragments; after a barrier (all of
+  // stage s is in registers everywhere) issue stage s+2 into the freed slot
+  // while the second half is multiplied.
+  v4i f0[2][6], f1[2][6];
+  issue_stage(0);
+  issue_stage(1);
+#pragma unroll 1
+  for (int s = 0; s < nsteps; ++s) {
+    __builtin_amdgcn_sched_barrier(0);
+    mmd_wait_vm<8>();
+    __syncthreads();
+    fetch(s, 0, f0);
+    fetch(s, 1, f1);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = Op::run(f0[q][i], f0[q][4 + j], acc[i][j]);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads(); // every wave holds stage s in registers: its slot is free
+    const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue_one(s2, s & 1, q * 4 + i);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = Op::run(f1[q][i], f1[q][4 + j], acc[i][j]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  mmd_wait_vm<0>();
+  __syncthreads();
+  mm_epilogue_lds<Epi, 2, 512>(acc, out, M, N, m0, n0, wm, wn, lane, P, &lds[0][0][0], (int)sizeof(lds));
+}
+
 // Entry: MK selects the matrix-core kind; A is [M, K] (or [K, M] with AT), B is
-// [N, K] with BT (the weight layout) or [K, N]; DMA selects the LDS DMA ring
-// (requires !AT, BT and K spanning a multiple of 64 bytes).
-template <int MK, typename Epi, bool AT, bool BT, bool DMA, typename ElemT, typename Args>
+// [N, K] with BT (the weight layout) or [K, N]; DMA selects the LDS DMA ring:
+// 0 none (register staging), 1 with 64-byte K slices (256 threads), 3 with
+// 128-byte slices and two waves per SIMD (512 threads); both require !AT, BT
+// and K spanning a multiple of 64 resp. 128 bytes.
+template <int MK, typename Epi, bool AT, bool BT, int DMA, typename ElemT, typename Args>
 __device__ __forceinline__ void mmad(const ElemT *A, const ElemT *B, typename Epi::out_t *out, int64_t M, int64_t N, int64_t K,
                                      const Args &P) {
-  static_assert(!DMA || (!AT && BT), "the DMA ring takes K-contiguous A and B");
-  if constexpr (DMA) mmad_core_dma<MK, Epi>(A, B, out, M, N, K, P);
+  static_assert(DMA == 0 || (!AT && BT), "the DMA ring takes K-contiguous A and B");
+  static_assert(DMA == 0 || DMA == 1 || DMA == 3, "DMA mode");
+  if constexpr (DMA == 3) mmad_core_pp<MK, Epi>(A, B, out, M, N, K, P);
+  else if constexpr (DMA == 1) mmad_core_dma<MK, Epi>(A, B, out, M, N, K, P);
   else mmad_core<MK, Epi, AT, BT>(A, B, out, M, N, K, P);
 }
 

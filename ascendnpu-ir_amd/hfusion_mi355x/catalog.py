@@ -301,8 +301,10 @@ def entries():
     e["w8a8_512"] = g.w8a8_dequant(512, 512, 512)
     e["w8a8_ragged"] = g.w8a8_dequant(300, 200, 160)
     e["w8a8_ragged_dma"] = g.w8a8_dequant(300, 200, 192)
+    e["w8a8_ragged_dma128"] = g.w8a8_dequant(300, 200, 384)
     e["w8a8_kn"] = g.w8a8_dequant(320, 256, 128, b_layout="kn")
     e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
+    e["bf16_mmad_ragged128"] = g.bf16_mmad(200, 136, 192)
     e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)
     # hivm.hir.matmul forms of bishengir/test/Dialect/HIVM/IR/ops.mlir (16x16 f16) and wider
     e["hivm_mm_f16_null"] = g.hivm_matmul(16, 16, 16)

@@ -115,7 +115,8 @@ def test_argmax_repeat_launch(gpu):
 
 # ------------------------------------------------------------------ W8A8
 @pytest.mark.parametrize("name,m,n,k", [("w8a8_512", 512, 512, 512), ("w8a8_ragged", 300, 200, 160),
-                                        ("w8a8_ragged_dma", 300, 200, 192), ("w8a8_kn", 320, 256, 128)])
+                                        ("w8a8_ragged_dma", 300, 200, 192), ("w8a8_ragged_dma128", 300, 200, 384),
+                                        ("w8a8_kn", 320, 256, 128)])
 def test_w8a8(gpu, name, m, n, k):
     note(name)
     a, b, st, sc = I.config_inputs("w8a8_dequant", m=m, n=n, k=k)
@@ -180,7 +181,8 @@ def test_hivm_matmul(gpu, name):
         np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("name,m,n,k", [("bf16_mmad_256", 256, 256, 256), ("bf16_mmad_ragged", 200, 136, 96)])
+@pytest.mark.parametrize("name,m,n,k", [("bf16_mmad_256", 256, 256, 256), ("bf16_mmad_ragged", 200, 136, 96),
+                                        ("bf16_mmad_ragged128", 200, 136, 192)])
 def test_bf16_mmad(gpu, name, m, n, k):
     note(name)
     s = I.SEED_BASE + 40
