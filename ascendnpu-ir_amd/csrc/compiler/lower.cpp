@@ -1339,7 +1339,9 @@ struct RowEmitter {
       << "  const int tid = threadIdx.x, rloc = tid / TR, lt = tid % TR;\n"
       << "  int64_t row[RPW];\n  bool row_ok[RPW];\n"
       << "#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) {\n"
-      << "    const int64_t r_ = ((int64_t)blockIdx.x * RB + rloc) * RPW + rr;\n"
+      << "    // a row group of whole waves has wave-uniform rows: keep them in SGPRs\n"
+      << "    const int rl_ = TR % 64 == 0 ? __builtin_amdgcn_readfirstlane(rloc) : rloc;\n"
+      << "    const int64_t r_ = ((int64_t)blockIdx.x * RB + rl_) * RPW + rr;\n"
       << "    row_ok[rr] = r_ < R;\n    row[rr] = r_ < R ? r_ : R - 1;\n  }\n"
       << "  (void)row_ok; (void)lt;\n"
       << "  hf::Guard hf_g; // evidence that every fast-path element is exact\n";
