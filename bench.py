@@ -8,6 +8,7 @@ measured the same way and reported under "groups" (GB/s, or TOPS for the W8A8
 contraction) with its roofline fraction.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+    python bench.py --vendor OUT   # each group vs its eager PyTorch equivalent
 """
 import argparse
 import json
@@ -254,6 +255,74 @@ def summarize_counters(d, out, command):
                 fh.write(f"  MFMA busy cycles per SIMD = {med['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024:.0f}\n")
 
 
+def vendor_equivalent(name):
+    """The same group written as eager PyTorch on ROCm (hipBLASLt for the int8
+    GEMM, PyTorch's own reduction kernels otherwise), over the same device
+    arguments.  A reported comparison only: its outputs are not checked
+    against the oracle, and nothing in the product calls it."""
+    import torch
+
+    if name == "vec_add":
+        return lambda a, b, o: torch.add(a, b, out=o)
+    if name == "rmsnorm_quant":
+        def f(x, g, q, s):
+            xf = x.float()
+            r = torch.rsqrt((xf * xf).mean(-1, keepdim=True) + 1e-6)
+            y = xf * r * g.float()
+            sc = y.abs().amax(-1, keepdim=True) / 127.0
+            q.copy_(torch.round(y / sc).clamp_(-127, 127).to(torch.int8))
+            s.copy_(sc.squeeze(-1))
+        return f
+    if name == "safe_softmax":
+        return lambda x, o: o.copy_(torch.softmax(x, -1))
+    if name == "argmax":
+        def f(x, v, i):
+            mv, mi = torch.max(x, -1)
+            v.copy_(mv)
+            i.copy_(mi)
+        return f
+    if name == "w8a8_dequant":
+        def f(a, b, st, sc, o):
+            c = torch._int_mm(a, b.t())
+            o.copy_(c.float() * st[:, None] * sc[None, :])
+        return f
+    raise KeyError(name)
+
+
+def vendor_report(out, steps, warmup, command):
+    """Kernel time of each fused group next to its eager PyTorch equivalent
+    (and, for W8A8, hipBLASLt's int8 GEMM alone), same inputs, same timing
+    method; written as a text table."""
+    import torch
+
+    import hfusion_mi355x as hf
+    dev = torch.device("cuda:0")
+    lines = ["# fused group (this backend) vs the same group in eager PyTorch on ROCm, MI355X",
+             f"# command: {command}" if command else "# command: python bench.py --vendor OUT",
+             "# group            ours_us  eager_us  speedup"]
+    for name in ORDER:
+        log(f"[bench] vendor comparison: {name}")
+        grp = hf.compile(hf.catalog.get(name), require_cached=True).load()
+        dargs, _ = device_inputs(name, dev)
+        sets = input_sets(dargs)
+        ours = time_group(grp, sets, steps, warmup)[0] / steps * 1e3
+        eager = time_group(vendor_equivalent(name), sets, steps, warmup)[0] / steps * 1e3
+        lines.append(f"{name:18s} {ours:8.2f} {eager:9.2f} {eager / ours:8.2f}x")
+        if name == "w8a8_dequant":
+            gemm = time_group(lambda a, b, st, sc, o: torch._int_mm(a, b.t()), sets, steps, warmup)[0] / steps * 1e3
+            ops = grp.meta["algo_ops"]
+            lines.append(f"  hipBLASLt int8 GEMM alone (torch._int_mm, int32 out): {gemm:.2f} us = "
+                         f"{ops / (gemm * 1e-6) / 1e12:.0f} TOPS; fused W8A8 here: {ops / (ours * 1e-6) / 1e12:.0f} TOPS")
+        del dargs, sets
+        torch.cuda.empty_cache()
+    text = "\n".join(lines) + "\n"
+    if out == "-":
+        sys.stdout.write(text)
+    else:
+        with open(out, "w") as f:
+            f.write(text)
+
+
 def traffic_table():
     f = os.path.join(REPO, "profiles", "hbm_traffic.txt")
     t = {}
@@ -279,6 +348,8 @@ def main():
     ap.add_argument("--summarize-counters", nargs=2, metavar=("DIR", "OUT"),
                     help="write per-kernel medians of a rocprofv3 --pmc csv run")
     ap.add_argument("--command", default="", help="the profiling command, recorded in the summary")
+    ap.add_argument("--vendor", metavar="OUT", default=None,
+                    help="time each group against its eager PyTorch/hipBLASLt equivalent, write a table to OUT")
     args = ap.parse_args()
     if args.summarize_stats:
         summarize_stats(*args.summarize_stats, args.command)
@@ -288,6 +359,9 @@ def main():
         return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc, args.command)
+        return
+    if args.vendor:
+        vendor_report(args.vendor, args.steps, args.warmup, args.command)
         return
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (each group shards by rows/columns "
