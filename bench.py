@@ -239,7 +239,8 @@ def summarize_counters(d, out, command):
     """Median per dispatch of every counter of one `rocprofv3 --pmc` csv run,
     per hf_ kernel.  SQ_INSTS_VALU_MFMA_MOPS_I8 counts int8 matrix operations
     in units of 512; SQ_VALU_MFMA_BUSY_CYCLES is summed over the 1024 SIMDs
-    (256 CUs x 4), so / 1024 gives the busy cycles of one SIMD."""
+    (256 CUs x 4), so / 1024 gives the busy cycles of one SIMD; SQ_BUSY_CYCLES
+    is summed over the 32 shader engines (8 XCDs x 4)."""
     acc = {}
     for r in _csv_rows(d, "_counter_collection.csv"):
         if r["Kernel_Name"].startswith("hf_"):
@@ -253,6 +254,11 @@ def summarize_counters(d, out, command):
                 fh.write(f"  int8 matrix ops = {med['SQ_INSTS_VALU_MFMA_MOPS_I8'] * 512:.4e}\n")
             if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
                 fh.write(f"  MFMA busy cycles per SIMD = {med['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024:.0f}\n")
+            if "SQ_BUSY_CYCLES" in med:
+                fh.write(f"  SQ busy cycles per shader engine (/ 32 SEs) = {med['SQ_BUSY_CYCLES'] / 32:.0f}\n")
+            if "SQ_LDS_IDX_ACTIVE" in med and "SQ_LDS_BANK_CONFLICT" in med:
+                fh.write(f"  LDS bank-conflict cycles / LDS active cycles = "
+                         f"{med['SQ_LDS_BANK_CONFLICT'] / max(1.0, med['SQ_LDS_IDX_ACTIVE']):.3f}\n")
 
 
 def vendor_equivalent(name):
