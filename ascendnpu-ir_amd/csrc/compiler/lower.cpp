@@ -305,6 +305,11 @@ std::string f32UnaryFn(const std::string &fn, const std::string &x, const Op *op
   if (fn == "round") return "__builtin_roundf(" + x + ")";
   if (fn == "square") return "((" + x + ") * (" + x + "))";
   if (fn == "trunc") return "__builtin_truncf(" + x + ")";
+  // math.tan .. math.cosh: the device libm (HFusionOps.cpp:443-480)
+  static const std::set<std::string> libm = {"tan", "acos", "acosh", "asin", "asinh", "atan", "atanh",
+                                             "sinh", "cosh", "lgamma"};
+  if (libm.count(fn)) return fn + "f(" + x + ")";
+  if (fn == "ilogb") return "hf::ilogb_f(" + x + ")";
   unsupported(op, "unary function '" + fn + "' on f32");
 }
 
@@ -320,6 +325,9 @@ std::string f32BinaryFn(const std::string &fn, const std::string &a, const std::
   if (fn == "powf") return "powf(" + a + ", " + b + ")";
   if (fn == "mod" || fn == "modui") return "fmodf(" + a + ", " + b + ")";
   if (fn == "copysign") return "copysignf(" + a + ", " + b + ")";
+  if (fn == "atan2") return "atan2f(" + a + ", " + b + ")";
+  if (fn == "ldexp") return "hf::ldexp_f(" + a + ", " + b + ")";
+  if (fn == "divfhp") return "(" + a + " / " + b + ")";
   unsupported(op, "binary function '" + fn + "' on floats");
 }
 
@@ -344,6 +352,9 @@ std::string intBinaryFn(const std::string &fn, const std::string &a, const std::
   if (fn == "shrui") return "(" + T + ")((" + U + ")(" + a + ") >> " + B + ")";
   if (fn == "floordivsi") return "(" + T + ")hf_floordiv(" + A + ", " + B + ")";
   if (fn == "ceildivsi") return "(" + T + ")hf_ceildiv(" + A + ", " + B + ")";
+  if (fn == "powi") return "(" + T + ")hf::ipowi(" + A + ", " + B + ")";
+  if (fn == "ceildivui") return "(" + T + ")hf::ceildivu((" + U + ")(" + a + "), (" + U + ")(" + b + "))";
+  if (fn == "modui") return "(" + T + ")hf::remu((" + U + ")(" + a + "), (" + U + ")(" + b + "))";
   unsupported(op, "binary function '" + fn + "' on integers");
 }
 
@@ -398,14 +409,23 @@ bool isElementwiseOp(const Op *op) {
   return s.count(op->name) != 0;
 }
 
+// arith.bitcast (the `bitcast` type_fn, HFusionOps.cpp:752-756): the same
+// bits read as a type of the same width.
+std::string bitcastExpr(const std::string &x, Elem from, Elem to, const Op *op) {
+  if (from == to) return x;
+  if (from == Elem::I1 || to == Elem::I1 || elemBits(from) != elemBits(to)) unsupported(op, "bitcast between widths");
+  return "__builtin_bit_cast(" + ctype(to) + ", (" + ctype(from) + ")(" + x + "))";
+}
+
 // Element expression of an elementwise op's result from operand expressions.
 std::string elementExpr(const Op *op, const std::vector<std::string> &a, const std::vector<Elem> &at, Elem U) {
   const std::string &n = op->name;
   bool uns = op->attr("cast") == "cast_unsigned";
+  bool bits = op->attr("cast") == "bitcast";
   auto named = [&](const std::string &fn, int arity) -> std::string {
     if ((int)a.size() != arity) unsupported(op, "operand count");
     std::vector<std::string> xs;
-    for (int i = 0; i < arity; ++i) xs.push_back(castExpr(a[i], at[i], U, uns));
+    for (int i = 0; i < arity; ++i) xs.push_back(bits ? bitcastExpr(a[i], at[i], U, op) : castExpr(a[i], at[i], U, uns));
     if (isFloat(U)) {
       if (arity == 1) return inFloatType(U, xs, [&](const std::vector<std::string> &y) { return f32UnaryFn(fn, y[0], op); });
       if (arity == 2) return inFloatType(U, xs, [&](const std::vector<std::string> &y) { return f32BinaryFn(fn, y[0], y[1], op); });
@@ -865,7 +885,9 @@ struct RowEmitter {
     std::string fn = op->attr("fun");
     static const std::set<std::string> costly = {"exp", "exp2", "log", "log2", "log10", "log1p", "expm1", "tanh",
                                                  "sin", "cos", "erf", "powf", "sqrt", "rsqrt", "div", "rec",
-                                                 "reciprocal", "mod"};
+                                                 "reciprocal", "mod", "modui", "tan", "acos", "acosh", "asin",
+                                                 "asinh", "atan", "atanh", "sinh", "cosh", "lgamma", "atan2",
+                                                 "divfhp", "powi"};
     return costly.count(fn) || op->name == "arith.divf" || op->name == "linalg.div";
   }
 

@@ -191,6 +191,38 @@ __device__ __forceinline__ float sub(float a, float b) { return a - b; }
 __device__ __forceinline__ float mul(float a, float b) { return a * b; }
 __device__ __forceinline__ float div(float a, float b) { return a / b; }
 __device__ __forceinline__ float rec(float a) { return 1.0f / a; }
+
+// mathExt.ilogb (MathExtOps.td:79-91): floor(log2|x|) as a float; -inf at
+// zero, +inf at infinity, NaN kept.  The frexp exponent e has |x| = m * 2^e
+// with m in [0.5, 1), denormals included, so floor(log2|x|) = e - 1.
+__device__ __forceinline__ float ilogb_f(float x) {
+  if (__builtin_isnan(x)) return x;
+  if (x == 0.0f) return -__builtin_inff();
+  if (__builtin_isinf(x)) return __builtin_inff();
+  int e;
+  (void)__builtin_frexpf(x, &e);
+  return (float)(e - 1);
+}
+// mathExt.ldexp folder (MathExtOps.cpp:70-85): ldexpf(a, int(b)); the count
+// saturates to int and NaN counts as 0.
+__device__ __forceinline__ float ldexp_f(float a, float b) {
+  const int n = __builtin_isnan(b) ? 0 : b >= 2147483647.0f ? 2147483647 : b <= -2147483648.0f ? (-2147483647 - 1) : (int)b;
+  return __builtin_ldexpf(a, n);
+}
+// math.ipowi: a^b in two's complement (the caller truncates to its width);
+// a negative exponent gives the integer 1 / a^|b|: 1, +-1 or 0 (0 for a == 0).
+__device__ __forceinline__ int64_t ipowi(int64_t a, int64_t b) {
+  if (b < 0) return a == 1 ? 1 : a == -1 ? ((b & 1) ? -1 : 1) : 0;
+  uint64_t acc = 1, base = (uint64_t)a;
+  for (uint64_t e = (uint64_t)b; e; e >>= 1) {
+    if (e & 1) acc *= base;
+    base *= base;
+  }
+  return (int64_t)acc;
+}
+// arith.ceildivui / arith.remui on unsigned operand bits (0 for a zero divisor)
+__device__ __forceinline__ uint64_t ceildivu(uint64_t a, uint64_t b) { return b == 0 ? 0 : a / b + (a % b != 0); }
+__device__ __forceinline__ uint64_t remu(uint64_t a, uint64_t b) { return b == 0 ? 0 : a % b; }
 __device__ __forceinline__ float relu(float a) { return maximumf(0.0f, a); }
 __device__ __forceinline__ float rsqrt(float a) { return 1.0f / __builtin_sqrtf(a); }
 

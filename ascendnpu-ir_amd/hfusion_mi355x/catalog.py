@@ -122,6 +122,53 @@ def layernorm(rows=64, cols=2048, eps=1e-5):
 """
 
 
+# elementwise functions of the HFusion region builder (HFusionOps.cpp:434-640)
+# that the headline groups do not use: (function, dialect) per unary/binary op
+MATH_UNARY = [("tan", "hfusion"), ("acos", "hfusion"), ("acosh", "hfusion"), ("asin", "hfusion"),
+              ("asinh", "hfusion"), ("atan", "hfusion"), ("atanh", "hfusion"), ("sinh", "hfusion"),
+              ("cosh", "hfusion"), ("lgamma", "hfusion"), ("ilogb", "hfusion"), ("tanh", "hfusion"),
+              ("sin", "hfusion"), ("cos", "hfusion"), ("erf", "hfusion"), ("log2", "hfusion"),
+              ("log10", "hfusion"), ("log1p", "hfusion"), ("exp2", "hfusion"), ("expm1", "hfusion"),
+              ("rsqrt", "hfusion"), ("log", "linalg")]
+MATH_BINARY = ["atan2", "ldexp", "divfhp", "powf", "copysign", "mod"]
+INT_BINARY = [("powi", "i32"), ("powi", "i16"), ("ceildivui", "i32"), ("modui", "i32"), ("ceildivui", "i8")]
+
+
+def math_fns(n=4096):
+    """One module, one PURE_ELEMWISE group per elementwise function (f32
+    unary and binary, integer binary on several widths) plus an operand
+    `bitcast` type_fn (i32 bits read as f32)."""
+    X = _T([n], "f32")
+    funcs = []
+    for fn, dia in MATH_UNARY:
+        attr = f"#{dia}.unary_fn<{fn}>"
+        funcs.append(f"""  func.func @u_{fn}(%x: {X}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = {dia}.elemwise_unary {{fun = {attr}}} ins(%x : {X}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    for fn in MATH_BINARY:
+        funcs.append(f"""  func.func @b_{fn}(%x: {X}, %y: {X}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<{fn}>}} ins(%x, %y : {X}, {X}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    for fn, t in INT_BINARY:
+        I = _T([n], t)
+        funcs.append(f"""  func.func @i_{fn}_{t}(%x: {I}, %y: {I}, %o: {I}) -> {I}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<{fn}>}} ins(%x, %y : {I}, {I}) outs(%o : {I}) -> {I}
+    return %r : {I}
+  }}""")
+    I = _T([n], "i32")
+    funcs.append(f"""  func.func @bitcast_add(%x: {I}, %y: {I}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>, cast = #linalg.type_fn<bitcast>}} ins(%x, %y : {I}, {I}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -322,6 +369,7 @@ def entries():
     e["eltwise_mix"] = eltwise_mix(64, 1000)
     e["layernorm"] = layernorm(64, 2048)
     e["reduce_ops"] = reduce_ops(48, 3000)
+    e["math_fns"] = math_fns(4096)
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

@@ -204,6 +204,13 @@ static inline float minnumf(float a, float b) {
   return minimumf(a, b);
 }
 
+static inline int ldexp_count(float b) {
+  if (isnan(b)) return 0;
+  if (b >= 2147483647.0f) return 2147483647;
+  if (b <= -2147483648.0f) return -2147483647 - 1;
+  return (int)b;
+}
+
 static inline float unary_f32(int fn, float x) {
   switch (fn) {
   case HFU_SQRT: return sqrtf(x);
@@ -229,6 +236,26 @@ static inline float unary_f32(int fn, float x) {
   case HFU_ROUND: return roundf(x);
   case HFU_SQUARE: return x * x;
   case HFU_TRUNC: return truncf(x);
+  /* math.tan .. math.cosh lower through MathToLLVM to the libm calls
+     (HFusionOps.cpp:443-480) */
+  case HFU_TAN: return tanf(x);
+  case HFU_ACOS: return acosf(x);
+  case HFU_ACOSH: return acoshf(x);
+  case HFU_ASIN: return asinf(x);
+  case HFU_ASINH: return asinhf(x);
+  case HFU_ATAN: return atanf(x);
+  case HFU_ATANH: return atanhf(x);
+  case HFU_SINH: return sinhf(x);
+  case HFU_COSH: return coshf(x);
+  /* mathExt.lgamma: log|Gamma(x)| (MathExtOps.td:96-106) */
+  case HFU_LGAMMA: return lgammaf(x);
+  /* mathExt.ilogb: floor(log2|x|) as a float of the operand's type
+     (MathExtOps.td:79-91): -inf at zero, +inf at infinity, NaN kept */
+  case HFU_ILOGB:
+    if (isnan(x)) return x;
+    if (x == 0.0f) return -INFINITY;
+    if (isinf(x)) return INFINITY;
+    return (float)ilogbf(x);
   }
   abort();
 }
@@ -246,6 +273,12 @@ static inline float binary_f32(int fn, float a, float b) {
   case HFB_POWF: return powf(a, b);
   case HFB_MODF: return fmodf(a, b);
   case HFB_COPYSIGN: return copysignf(a, b);
+  case HFB_ATAN2: return atan2f(a, b);
+  /* mathExt.ldexp folder: ldexpf(a, static_cast<int>(b))
+     (MathExtOps.cpp:70-85); the conversion saturates, NaN -> 0 */
+  case HFB_LDEXP: return ldexpf(a, ldexp_count(b));
+  /* mathExt.divfhp folder: IEEE division, nearest-even (MathExtOps.cpp:91-99) */
+  case HFB_DIVFHP: return a / b;
   }
   abort();
 }
@@ -282,6 +315,31 @@ static inline int64_t binary_i64(int fn, int64_t a, int64_t b, int bits) {
     r = a / b;
     if ((a % b != 0) && ((a < 0) == (b < 0))) r += 1;
     break;
+  /* math.ipowi (HFusionOps.cpp:588-591): a^b with wrap-around; a negative
+     exponent gives 1 / a^|b| in integers (0 unless |a| == 1; 0 for a == 0) */
+  case HFB_IPOW:
+    if (b < 0) {
+      r = a == 1 ? 1 : a == -1 ? ((b & 1) ? -1 : 1) : 0;
+    } else {
+      uint64_t acc = 1, base = (uint64_t)a;
+      for (uint64_t e = (uint64_t)b; e; e >>= 1) {
+        if (e & 1) acc *= base;
+        base *= base;
+      }
+      r = (int64_t)acc;
+    }
+    break;
+  /* arith.ceildivui / arith.remui on the operands' unsigned bits */
+  case HFB_ICEILDIVU: {
+    uint64_t ua = ubits(a, bits), ub = ubits(b, bits);
+    r = ub == 0 ? 0 : (int64_t)(ua / ub + (ua % ub != 0));
+    break;
+  }
+  case HFB_IREMU: {
+    uint64_t ua = ubits(a, bits), ub = ubits(b, bits);
+    r = ub == 0 ? 0 : (int64_t)(ua % ub);
+    break;
+  }
   default: abort();
   }
   return wrap_bits(r, bits);

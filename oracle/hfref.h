@@ -48,16 +48,19 @@ enum {
   HFU_SQRT = 0, HFU_RSQRT, HFU_EXP, HFU_EXP2, HFU_LOG, HFU_LOG2, HFU_LOG10,
   HFU_LOG1P, HFU_EXPM1, HFU_ABS, HFU_NEG, HFU_RELU, HFU_REC, HFU_TANH,
   HFU_SIN, HFU_COS, HFU_ERF, HFU_NEARBYINT, HFU_CEIL, HFU_FLOOR, HFU_ROUND,
-  HFU_SQUARE, HFU_TRUNC
+  HFU_SQUARE, HFU_TRUNC, HFU_TAN, HFU_ACOS, HFU_ACOSH, HFU_ASIN, HFU_ASINH,
+  HFU_ATAN, HFU_ATANH, HFU_SINH, HFU_COSH, HFU_LGAMMA, HFU_ILOGB
 };
 /* binary fn codes */
 enum {
   HFB_ADD = 0, HFB_SUB, HFB_MUL, HFB_DIV, HFB_MAXF, HFB_MINF, HFB_MAXNUMF,
-  HFB_MINNUMF, HFB_POWF, HFB_MODF, HFB_COPYSIGN,
+  HFB_MINNUMF, HFB_POWF, HFB_MODF, HFB_COPYSIGN, HFB_ATAN2, HFB_LDEXP,
+  HFB_DIVFHP,
   /* integer */
   HFB_IADD = 32, HFB_ISUB, HFB_IMUL, HFB_IDIV, HFB_IMAX, HFB_IMIN, HFB_IAND,
   HFB_IOR, HFB_IXOR, HFB_ISHL, HFB_ISHRS, HFB_ISHRU, HFB_IREM,
-  HFB_IFLOORDIV, HFB_ICEILDIV, HFB_IMAXU, HFB_IMINU
+  HFB_IFLOORDIV, HFB_ICEILDIV, HFB_IMAXU, HFB_IMINU, HFB_IPOW, HFB_ICEILDIVU,
+  HFB_IREMU
 };
 /* compare fn codes */
 enum { HFC_EQ = 0, HFC_NE, HFC_LT, HFC_LE, HFC_GT, HFC_GE };

@@ -172,6 +172,17 @@ def wrap_int(a64, elem):
     return a64.astype(NP[elem])  # numpy astype wraps two's-complement
 
 
+def bitcast(v, elem):
+    """arith.bitcast — the `bitcast` type_fn of named ops: the same bits read
+    as a type of the same width (HFusionOps.cpp:752-756)."""
+    if v.elem == elem:
+        return v
+    src, dst = np.dtype(NP[v.elem]), np.dtype(NP[elem])
+    if v.elem == "i1" or elem == "i1" or src.itemsize != dst.itemsize:
+        raise NotImplementedError(f"bitcast {v.elem} -> {elem}")
+    return T(np.ascontiguousarray(v.a).view(dst), elem)
+
+
 def convert(v, elem, unsigned=False):
     """convertScalarToDtype (upstream MLIR) — the `cast` type_fn of named ops."""
     if v.elem == elem or {v.elem, elem} <= {"i64", "index"}:
@@ -255,12 +266,16 @@ def declared_cast(v, elem, mode, sat, unsigned=False):
 
 UNARY = {"sqrt": 0, "rsqrt": 1, "exp": 2, "exp2": 3, "log": 4, "log2": 5, "log10": 6, "log1p": 7, "expm1": 8,
          "abs": 9, "absf": 9, "negf": 10, "neg": 10, "relu": 11, "rec": 12, "reciprocal": 12, "tanh": 13,
-         "sin": 14, "cos": 15, "erf": 16, "nearbyint": 17, "ceil": 18, "floor": 19, "round": 20, "square": 21}
+         "sin": 14, "cos": 15, "erf": 16, "nearbyint": 17, "ceil": 18, "floor": 19, "round": 20, "square": 21,
+         "trunc": 22, "tan": 23, "acos": 24, "acosh": 25, "asin": 26, "asinh": 27, "atan": 28, "atanh": 29,
+         "sinh": 30, "cosh": 31, "lgamma": 32, "ilogb": 33}
 BINARY_F = {"add": 0, "sub": 1, "mul": 2, "div": 3, "maxf": 4, "max_signed": 4, "minf": 5, "min_signed": 5,
-            "maxnumf": 6, "minnumf": 7, "powf": 8, "mod": 9, "copysign": 10}
+            "maxnumf": 6, "minnumf": 7, "powf": 8, "mod": 9, "modui": 9, "copysign": 10, "atan2": 11,
+            "ldexp": 12, "divfhp": 13}
 BINARY_I = {"add": 32, "sub": 33, "mul": 34, "div": 35, "max_signed": 36, "maxsi": 36, "min_signed": 37,
             "vand": 38, "vor": 39, "vxor": 40, "shli": 41, "shrsi": 42, "shrui": 43, "mod": 44,
-            "floordivsi": 45, "ceildivsi": 46, "max_unsigned": 47, "min_unsigned": 48}
+            "floordivsi": 45, "ceildivsi": 46, "max_unsigned": 47, "min_unsigned": 48, "powi": 49,
+            "ceildivui": 50, "modui": 51}
 COMPARE = {"veq": 0, "vne": 1, "vlt": 2, "vle": 3, "vgt": 4, "vge": 5}
 REDUCE_F = {"arith.addf": 0, "arith.mulf": 1, "arith.maximumf": 2, "arith.minimumf": 3, "arith.maxnumf": 4,
             "arith.minnumf": 5}
@@ -592,12 +607,16 @@ class Interp:
         U, shape = o.elem, o.a.shape
         xs = [get(n) for n in ins]
         uns = _attr(rest, "cast") == "cast_unsigned"
+        if _attr(rest, "cast") == "bitcast":
+            cv = lambda v: bitcast(v, U)  # noqa: E731
+        else:
+            cv = lambda v: convert(v, U, uns)  # noqa: E731
         if op in ("hfusion.elemwise_unary", "linalg.elemwise_unary"):
             fn = _attr(rest, "fun") or ("sqrt" if op.startswith("hfusion") else "exp")
-            r = apply_unary(fn, convert(T(np.broadcast_to(xs[0].a, shape), xs[0].elem), U, uns), U)
+            r = apply_unary(fn, cv(T(np.broadcast_to(xs[0].a, shape), xs[0].elem)), U)
         elif op in ("hfusion.elemwise_binary", "linalg.elemwise_binary"):
             fn = _attr(rest, "fun") or ("vand" if op.startswith("hfusion") else "add")
-            r = apply_binary(fn, convert(xs[0], U, uns), convert(xs[1], U, uns), U, shape)
+            r = apply_binary(fn, cv(xs[0]), cv(xs[1]), U, shape)
         elif op == "hfusion.compare":
             fn = _attr(rest, "compare_fn") or "veq"
             a, b = xs

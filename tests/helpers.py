@@ -124,3 +124,108 @@ def parse_data_file(raw, elems, shapes):
         out.append(vals.reshape(shape))
     assert pos == len(raw)
     return out
+
+
+# ------------------------------------------------ inputs of the math_fns module
+def _logu(rng, n, lo, hi):
+    return np.exp(rng.uniform(np.log(lo), np.log(hi), n))
+
+
+def math_inputs(func, n=4096, seed=0x4D415448):
+    """Seeded operands for function `func` of catalog module math_fns, over
+    the function's domain plus its edges (zeros, infinities, NaN, poles,
+    out-of-domain points)."""
+    rng = np.random.default_rng(seed + sum(map(ord, func)))
+    sgn = lambda m: rng.choice([-1.0, 1.0], m)  # noqa: E731
+    f32 = lambda a: np.asarray(a, np.float32)  # noqa: E731
+    edges = [0.0, -0.0, np.inf, -np.inf, np.nan]
+    if func.startswith("u_"):
+        fn = func[2:]
+        if fn == "tan":
+            x = rng.uniform(-1.5, 1.5, n)
+        elif fn in ("acos", "asin", "atanh"):
+            x = rng.uniform(-1.0, 1.0, n)
+            x[:6] = [1.0, -1.0, 1.0000001, -1.0000001, 0.5, -0.5]
+        elif fn == "acosh":
+            x = 1.0 + _logu(rng, n, 1e-6, 1e3)
+            x[:3] = [1.0, 0.999, -2.0]
+        elif fn in ("asinh", "atan", "sinh", "cosh", "tanh"):
+            x = sgn(n) * _logu(rng, n, 1e-4, 100.0)
+        elif fn == "lgamma":
+            x = rng.uniform(-10.0, 30.0, n)
+            x[:6] = [1.0, 2.0, -3.0, 0.5, 1e-3, 100.0]
+        elif fn == "ilogb":
+            x = sgn(n) * _logu(rng, n, 1e-44, 3e38)
+        elif fn in ("sin", "cos"):
+            x = rng.uniform(-1e3, 1e3, n)
+        elif fn == "erf":
+            x = rng.uniform(-5.0, 5.0, n)
+        elif fn in ("log", "log2", "log10", "rsqrt"):
+            x = _logu(rng, n, 1e-30, 1e30)
+            x[:3] = [-1.0, 1.0, 4.0]
+        elif fn == "log1p":
+            x = np.concatenate([rng.uniform(-0.999, 1.0, n // 2), _logu(rng, n - n // 2, 1.0, 1e6)])
+            x[:3] = [-1.0, -2.0, 1e-8]
+        elif fn == "exp2":
+            x = rng.uniform(-140.0, 130.0, n)
+        elif fn == "expm1":
+            x = rng.uniform(-20.0, 89.0, n)
+            x[:2] = [1e-8, -1e-8]
+        else:
+            raise KeyError(func)
+        x = f32(x)
+        x[-len(edges):] = edges
+        return [x, np.zeros(n, np.float32)]
+    if func.startswith("b_"):
+        fn = func[2:]
+        if fn == "atan2":
+            a, b = rng.normal(0, 10, n), rng.normal(0, 10, n)
+            a[:4], b[:4] = [0.0, -0.0, 1.0, -1.0], [0.0, 0.0, 0.0, -0.0]
+        elif fn == "ldexp":
+            a = sgn(n) * _logu(rng, n, 1e-40, 1e38)
+            b = np.floor(rng.uniform(-160, 160, n))
+            b[:3] = [1e10, -1e10, np.nan]
+        elif fn == "divfhp":
+            a, b = rng.normal(0, 1e3, n), rng.normal(0, 1, n)
+            b[:2] = [0.0, -0.0]
+        elif fn == "powf":
+            a, b = _logu(rng, n, 1e-3, 1e3), rng.uniform(-10.0, 10.0, n)
+            a[:4], b[:4] = [-2.0, -2.0, 0.0, 1.0], [3.0, 0.5, -1.0, np.inf]
+        elif fn == "copysign":
+            a, b = rng.normal(0, 10, n), rng.normal(0, 1, n)
+            b[:2] = [-0.0, 0.0]
+        elif fn == "mod":
+            a, b = rng.normal(0, 100, n), rng.normal(0, 10, n)
+            b[:2] = [0.0, np.inf]
+        else:
+            raise KeyError(func)
+        return [f32(a), f32(b), np.zeros(n, np.float32)]
+    if func.startswith("i_"):
+        fn, t = func[2:].rsplit("_", 1)
+        dt = {"i8": np.int8, "i16": np.int16, "i32": np.int32}[t]
+        info = np.iinfo(dt)
+        if fn == "powi":
+            a = rng.integers(-20, 21, n)
+            b = rng.integers(-3, 16 if t == "i32" else 21, n)
+            a[:4], b[:4] = [1, -1, -1, 0], [-5, -5, -4, 0]
+        else:
+            a = rng.integers(info.min, info.max + 1, n)
+            b = rng.integers(info.min, info.max + 1, n)
+            b[:4] = [0, 1, -1, 7]
+        return [a.astype(dt), b.astype(dt), np.zeros(n, dt)]
+    if func == "bitcast_add":
+        a = rng.normal(0, 1e3, n).astype(np.float32).view(np.int32)
+        b = rng.normal(0, 1e3, n).astype(np.float32).view(np.int32)
+        return [a, b, np.zeros(n, np.float32)]
+    raise KeyError(func)
+
+
+def math_funcs():
+    """Names of the functions of catalog module math_fns."""
+    c = hf.catalog
+    return ([f"u_{fn}" for fn, _ in c.MATH_UNARY] + [f"b_{fn}" for fn in c.MATH_BINARY]
+            + [f"i_{fn}_{t}" for fn, t in c.INT_BINARY] + ["bitcast_add"])
+
+
+# functions of math_fns whose result is exactly rounded (bit-exact bar)
+MATH_EXACT = {"u_ilogb", "b_ldexp", "b_divfhp", "b_copysign", "b_mod", "bitcast_add"}

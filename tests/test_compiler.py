@@ -183,10 +183,14 @@ def test_hivm_matmul_reference_form_lowers(tmp_path):
   %r = linalg.reduce {arith.addf} ins(%a : tensor<4x4xf32>) outs(%o : tensor<4xf32>) dimensions = [0]
   return %r : tensor<4xf32>
 }""", -2, "non-last axis"),
-    ("""func.func @f(%a: tensor<4xf32>, %o: tensor<4xf32>) -> tensor<4xf32> {
-  %r = hfusion.elemwise_unary {fun = #hfusion.unary_fn<lgamma>} ins(%a : tensor<4xf32>) outs(%o : tensor<4xf32>) -> tensor<4xf32>
-  return %r : tensor<4xf32>
+    ("""func.func @f(%a: tensor<4xi32>, %o: tensor<4xi32>) -> tensor<4xi32> {
+  %r = hfusion.elemwise_unary {fun = #hfusion.unary_fn<lgamma>} ins(%a : tensor<4xi32>) outs(%o : tensor<4xi32>) -> tensor<4xi32>
+  return %r : tensor<4xi32>
 }""", -2, "lgamma"),
+    ("""func.func @f(%a: tensor<4xi32>, %o: tensor<4xf64>) -> tensor<4xf64> {
+  %r = hfusion.elemwise_unary {fun = #hfusion.unary_fn<tan>, cast = #hfusion.type_fn<bitcast>} ins(%a : tensor<4xi32>) outs(%o : tensor<4xf64>) -> tensor<4xf64>
+  return %r : tensor<4xf64>
+}""", -2, "bitcast"),
     ("""func.func @f(%a: tensor<4xf32>) -> tensor<4xf32> {
   return %b : tensor<4xf32>
 }""", -1, "undefined value"),

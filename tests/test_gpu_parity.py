@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import bf16_ulp_diff, run_gpu, run_oracle
+from helpers import MATH_EXACT, bf16_ulp_diff, math_funcs, math_inputs, run_gpu, run_oracle
 
 pytestmark = pytest.mark.gpu
 I = hf.inputs
@@ -442,3 +442,26 @@ def test_int8_quant_near_ties(gpu, name, cols):
     ref, rmx = run_oracle(name, args)
     assert np.array_equal(mx, rmx, equal_nan=True)
     assert np.array_equal(out, ref), int((out != ref).sum())
+
+
+# ------------------------------------------------- elementwise function coverage
+@pytest.mark.parametrize("func", math_funcs())
+def test_math_fns(gpu, func):
+    """Each elementwise function of the region builder on its domain and
+    edges.  Integer functions, bitcast operands and the exactly rounded float
+    functions are bit-exact; the transcendental ones (device libm against
+    glibc) are within 1e-5 relative, with an absolute 1e-6 bar where the
+    result crosses zero, and agree on NaN and infinity positions."""
+    note(f"math_fns {func}")
+    args = math_inputs(func)
+    out, = run_gpu("math_fns", args, gpu, func=func)
+    ref, = run_oracle("math_fns", args, func=func)
+    if func in MATH_EXACT or func.startswith("i_"):
+        assert np.array_equal(out.view(np.uint8), ref.view(np.uint8)) or np.array_equal(out, ref, equal_nan=True), \
+            f"{int((out != ref).sum())} differ"
+        return
+    assert np.array_equal(np.isnan(out), np.isnan(ref)), "NaN positions differ"
+    inf = np.isinf(ref) | np.isinf(out)
+    assert np.array_equal(out[inf], ref[inf]), "infinities differ"
+    fin = np.isfinite(ref) & np.isfinite(out)
+    np.testing.assert_allclose(out[fin], ref[fin], rtol=1e-5, atol=1e-6)
