@@ -405,7 +405,9 @@ bool isElementwiseOp(const Op *op) {
       "arith.negf",             "arith.extf",              "arith.truncf", "arith.sitofp",
       "arith.fptosi",           "arith.addi",              "arith.subi", "arith.muli",
       "linalg.add", "linalg.sub", "linalg.mul", "linalg.div", "linalg.max", "linalg.min",
-      "linalg.exp", "linalg.abs", "linalg.negf", "linalg.sqrt", "linalg.rsqrt", "linalg.reciprocal"};
+      "linalg.exp", "linalg.abs", "linalg.negf", "linalg.sqrt", "linalg.rsqrt", "linalg.reciprocal",
+      "hfusion.isinf", "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot", "hfusion.erfinv",
+      "hfusion.bitcast"};
   return s.count(op->name) != 0;
 }
 
@@ -459,6 +461,36 @@ std::string elementExpr(const Op *op, const std::vector<std::string> &a, const s
     }
     return named(fn, 3);
   }
+  // float predicates and math ops of HFusionOps.td:251-305, 1309-1400 (no outs:
+  // operands and result type come from the op's own syntax)
+  if (n == "hfusion.isinf" || n == "hfusion.isnan" || n == "hfusion.isfinite") {
+    if (a.size() != 1 || !isFloat(at[0])) unsupported(op, "operand of " + n);
+    std::string f = castExpr(a[0], at[0], Elem::F32, false);
+    std::string pred = n == "hfusion.isinf" ? "__builtin_isinf" : n == "hfusion.isnan" ? "__builtin_isnan" : "__builtin_isfinite";
+    return castExpr("(bool)" + pred + "(" + f + ")", Elem::I1, U, false);
+  }
+  if (n == "hfusion.nextafter") {
+    if (a.size() != 2 || at[0] != U || at[1] != U) unsupported(op, "operands of hfusion.nextafter");
+    if (U == Elem::F32) return "nextafterf(" + a[0] + ", " + a[1] + ")";
+    if (U == Elem::F16) return "hf::nextafter_h(" + a[0] + ", " + a[1] + ")";
+    unsupported(op, "hfusion.nextafter on this type");
+  }
+  if (n == "hfusion.hypot") {
+    if ((a.size() != 2 && a.size() != 3)) unsupported(op, "operand count of hfusion.hypot");
+    for (auto e : at) if (e != U) unsupported(op, "mixed operand types of hfusion.hypot");
+    if (U != Elem::F32 && U != Elem::F16) unsupported(op, "hfusion.hypot on this type");
+    std::vector<std::string> f;
+    for (size_t i = 0; i < a.size(); ++i) f.push_back(castExpr(a[i], at[i], Elem::F32, false));
+    std::string z = a.size() == 3 ? f[2] : "0.0f";
+    std::string e = std::string(U == Elem::F32 ? "hf::hypot_scaled(" : "hf::hypot_direct(") + f[0] + ", " + f[1] + ", " + z +
+                    ", " + std::to_string(a.size()) + ")";
+    return castExpr(e, Elem::F32, U, false);
+  }
+  if (n == "hfusion.erfinv") {
+    if (a.size() != 1 || at[0] != U || (U != Elem::F32 && U != Elem::F16)) unsupported(op, "operand of hfusion.erfinv");
+    return castExpr("hf::erfinv_f(" + castExpr(a[0], U, Elem::F32, false) + ")", Elem::F32, U, false);
+  }
+  if (n == "hfusion.bitcast") return bitcastExpr(a[0], at[0], U, op);
   if (n == "hfusion.select") return "(" + a[0] + " ? " + a[1] + " : " + a[2] + ")";
   if (n == "hfusion.compare") {
     std::string fn = op->attr("compare_fn", "veq");
@@ -888,6 +920,7 @@ struct RowEmitter {
                                                  "reciprocal", "mod", "modui", "tan", "acos", "acosh", "asin",
                                                  "asinh", "atan", "atanh", "sinh", "cosh", "lgamma", "atan2",
                                                  "divfhp", "powi"};
+    if (op->name == "hfusion.hypot" || op->name == "hfusion.erfinv") return true;
     return costly.count(fn) || op->name == "arith.divf" || op->name == "linalg.div";
   }
 

@@ -220,6 +220,72 @@ __device__ __forceinline__ int64_t ipowi(int64_t a, int64_t b) {
   }
   return (int64_t)acc;
 }
+// hfusion.hypot, f32 (the lowering of Normalize.cpp:8969-9036): the largest
+// magnitude s scales the others, terms (a_i / s)^2 (1 for a_i == s, 0 when
+// s == 0) are summed in operand order, result s * sqrt(sum); any NaN operand
+// gives NaN and any infinite one +inf, infinity winning.
+__device__ __forceinline__ float hypot_scaled(float x, float y, float z, int n) {
+  const float a0 = __builtin_fabsf(x), a1 = __builtin_fabsf(y), a2 = n == 3 ? __builtin_fabsf(z) : 0.0f;
+  const bool nan = __builtin_isnan(x) || __builtin_isnan(y) || (n == 3 && __builtin_isnan(z));
+  const bool inf = a0 == __builtin_inff() || a1 == __builtin_inff() || (n == 3 && a2 == __builtin_inff());
+  float s = a0 > a1 ? a0 : a1;
+  if (n == 3) s = s > a2 ? s : a2;
+  const float safe = s == 0.0f ? 1.0f : s;
+  auto term = [&](float a) -> float {
+    if (s == 0.0f) return 0.0f;
+    if (a == s) return 1.0f;
+    const float q = a / safe;
+    return q * q;
+  };
+  float sum = term(a0) + term(a1);
+  if (n == 3) sum = sum + term(a2);
+  float r = s * __builtin_sqrtf(sum);
+  if (nan) r = __builtin_nanf("");
+  if (inf) r = __builtin_inff();
+  return r;
+}
+// f16 hypot: the direct path in f32, sqrt(sum_i a_i * a_i) (then rounded to
+// f16 by the caller), with the same NaN / infinity rules.
+__device__ __forceinline__ float hypot_direct(float x, float y, float z, int n) {
+  const float a0 = __builtin_fabsf(x), a1 = __builtin_fabsf(y), a2 = n == 3 ? __builtin_fabsf(z) : 0.0f;
+  const bool nan = __builtin_isnan(x) || __builtin_isnan(y) || (n == 3 && __builtin_isnan(z));
+  const bool inf = a0 == __builtin_inff() || a1 == __builtin_inff() || (n == 3 && a2 == __builtin_inff());
+  float sum = a0 * a0 + a1 * a1;
+  if (n == 3) sum = sum + a2 * a2;
+  float r = __builtin_sqrtf(sum);
+  if (nan) r = __builtin_nanf("");
+  if (inf) r = __builtin_inff();
+  return r;
+}
+// nextafter on f16 bits (IEEE nextafter: NaN in, NaN out; x == y gives y;
+// from zero the smallest denormal with y's sign; else one ulp toward y).
+__device__ __forceinline__ uint16_t nextafter_h(uint16_t x, uint16_t y) {
+  const bool xn = (x & 0x7FFF) > 0x7C00, yn = (y & 0x7FFF) > 0x7C00;
+  if (xn) return x;
+  if (yn) return y;
+  const float fx = hf::f16_to_f32(x), fy = hf::f16_to_f32(y);
+  if (fx == fy) return y;
+  if ((x & 0x7FFF) == 0) return (uint16_t)((y & 0x8000) | 1);
+  const bool away = (__builtin_fabsf(fx) < __builtin_fabsf(fy)) && ((x ^ y) & 0x8000) == 0;
+  return (uint16_t)(away ? x + 1 : x - 1);
+}
+// erfinv(y) in f32: Winitzki's closed-form estimate (a = 0.147), then Newton
+// steps on erf(x) - y in double, x -= (erf(x) - y) / (2/sqrt(pi) exp(-x^2)),
+// rounded once to f32.  |y| > 1 and NaN give NaN, y = +-1 gives +-inf.
+__device__ __forceinline__ float erfinv_f(float yf) {
+  if (__builtin_isnan(yf) || __builtin_fabsf(yf) > 1.0f) return __builtin_nanf("");
+  if (yf == 1.0f) return __builtin_inff();
+  if (yf == -1.0f) return -__builtin_inff();
+  if (yf == 0.0f) return yf;
+  const double y = (double)yf, a = 0.147, pi = 3.14159265358979323846;
+  const double l = log((1.0 - y) * (1.0 + y));
+  const double t = 2.0 / (pi * a) + 0.5 * l;
+  double x = sqrt(sqrt(t * t - l / a) - t);
+  if (y < 0) x = -x;
+  const double k = 2.0 / sqrt(pi);
+  for (int i = 0; i < 4; ++i) x -= (erf(x) - y) / (k * exp(-x * x));
+  return (float)x;
+}
 // arith.ceildivui / arith.remui on unsigned operand bits (0 for a zero divisor)
 __device__ __forceinline__ uint64_t ceildivu(uint64_t a, uint64_t b) { return b == 0 ? 0 : a / b + (a % b != 0); }
 __device__ __forceinline__ uint64_t remu(uint64_t a, uint64_t b) { return b == 0 ? 0 : a % b; }

@@ -169,6 +169,45 @@ def math_fns(n=4096):
     return "module {\n" + "\n".join(funcs) + "\n}\n"
 
 
+FP_OPS = [("isinf", "f32"), ("isnan", "f32"), ("isfinite", "f32"), ("isinf", "bf16"), ("isnan", "f16"),
+          ("nextafter", "f32"), ("nextafter", "f16"), ("hypot", "f32"), ("hypot3", "f32"), ("hypot", "f16"),
+          ("erfinv", "f32"), ("erfinv", "f16"), ("bitcast", "f32")]
+
+
+def fp_ops(n=4096):
+    """One module, one group per HFusion float op without outs (predicates,
+    nextafter, hypot with 2 and 3 operands, erfinv) and hfusion.bitcast."""
+    funcs = []
+    for op, t in FP_OPS:
+        X, B = _T([n], t), _T([n], "i1")
+        name = f"{op}_{t}"
+        attrs = _ATTRS.format(kind='PURE_ELEMWISE')
+        if op in ("isinf", "isnan", "isfinite"):
+            body = f"%r = hfusion.{op} %x : {X} -> {B}\n    return %r : {B}"
+            sig = f"(%x: {X}) -> {B}"
+        elif op == "nextafter":
+            body = f"%r = hfusion.nextafter %x, %y : {X}, {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}, %y: {X}) -> {X}"
+        elif op == "hypot":
+            body = f"%r = hfusion.hypot %x, %y : {X}, {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}, %y: {X}) -> {X}"
+        elif op == "hypot3":
+            body = f"%r = hfusion.hypot %x, %y, %z : {X}, {X}, {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}, %y: {X}, %z: {X}) -> {X}"
+        elif op == "erfinv":
+            body = f"%r = hfusion.erfinv %x : {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}) -> {X}"
+        else:
+            I = _T([n], "i32")
+            body = f"%r = hfusion.bitcast ins(%x : {I}) outs(%o : {X}) -> {X}\n    return %r : {X}"
+            sig = f"(%x: {I}, %o: {X}) -> {X}"
+        funcs.append(f"""  func.func @{name}{sig}
+      {attrs} {{
+    {body}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -370,6 +409,7 @@ def entries():
     e["layernorm"] = layernorm(64, 2048)
     e["reduce_ops"] = reduce_ops(48, 3000)
     e["math_fns"] = math_fns(4096)
+    e["fp_ops"] = fp_ops(4096)
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

@@ -283,6 +283,63 @@ REDUCE_I = {"arith.addi": 0, "arith.muli": 1, "arith.maxsi": 2, "arith.minsi": 3
             "arith.ori": 5, "arith.xori": 6, "arith.maxui": 7, "arith.minui": 8}
 
 
+_NON_DPS = ("hfusion.isinf", "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot",
+            "hfusion.erfinv")
+
+
+def _non_dps(op, xs, shape, elem):
+    """HFusion float ops without outs (HFusionOps.td:251-305, 1309-1400)."""
+    f32 = np.float32
+    if op in ("hfusion.isinf", "hfusion.isnan", "hfusion.isfinite"):
+        f = to_f32(xs[0])
+        return {"hfusion.isinf": np.isinf, "hfusion.isnan": np.isnan, "hfusion.isfinite": np.isfinite}[op](f)
+    if op == "hfusion.nextafter":
+        # IEEE nextafter (Normalize.cpp:8640-8660): one ulp from x toward y
+        if elem == "f32":
+            return np.nextafter(xs[0].a.astype(f32), xs[1].a.astype(f32))
+        h = [np.ascontiguousarray(x.a, np.uint16).view(np.float16) for x in xs]
+        return np.nextafter(h[0], h[1]).view(np.uint16)
+    if op == "hfusion.hypot":
+        # Normalize.cpp:8969-9330: f32 takes the scaled path, f16 the direct one
+        fs = [to_f32(x) for x in xs]
+        a = [np.abs(f) for f in fs]
+        nan = np.zeros(shape, bool)
+        inf = np.zeros(shape, bool)
+        for f, ai in zip(fs, a):
+            nan |= np.isnan(f)
+            inf |= ai == np.inf
+        with np.errstate(all="ignore"):
+            if elem == "f32":
+                sc = np.where(a[0] > a[1], a[0], a[1])
+                for ai in a[2:]:
+                    sc = np.where(sc > ai, sc, ai)
+                safe = np.where(sc == 0, f32(1), sc).astype(f32)
+
+                def term(ai):
+                    q = (ai / safe).astype(f32)
+                    return np.where(sc == 0, f32(0), np.where(ai == sc, f32(1), (q * q).astype(f32))).astype(f32)
+                sm = (term(a[0]) + term(a[1])).astype(f32)
+                for ai in a[2:]:
+                    sm = (sm + term(ai)).astype(f32)
+                r = (sc * np.sqrt(sm)).astype(f32)
+            elif elem == "f16":
+                sm = (a[0] * a[0] + a[1] * a[1]).astype(f32)
+                for ai in a[2:]:
+                    sm = (sm + ai * ai).astype(f32)
+                r = np.sqrt(sm).astype(f32)
+            else:
+                raise NotImplementedError(f"hypot on {elem}")
+        r[nan] = np.nan
+        r[inf] = np.inf
+        return from_f32(r, elem)
+    if op == "hfusion.erfinv":
+        import scipy.special
+        with np.errstate(all="ignore"):
+            r = scipy.special.erfinv(to_f32(xs[0]).astype(np.float64)).astype(f32)
+        return from_f32(r, elem)
+    raise NotImplementedError(op)
+
+
 def _full(v, shape):
     return np.ascontiguousarray(np.broadcast_to(v.a, shape))
 
@@ -565,6 +622,12 @@ class Interp:
         if op.startswith("arith.") and "ins(" not in rest:
             self._scalar_arith(res, op, rest, env)
             return
+        if op in _NON_DPS:
+            names = re.findall(r"%[\w.$-]+", rest.split(":", 1)[0])
+            shape, elem = parse_type(rest.rsplit("->", 1)[1])
+            xs = [T(np.broadcast_to(env[n].a, shape), env[n].elem) for n in names]
+            env[res] = T(np.ascontiguousarray(_non_dps(op, xs, shape, elem)), elem)
+            return
         ins, ins_t = _operands(_group(rest, "ins"))
         outs, outs_t = _operands(_group(rest, "outs"))
         if op == "linalg.fill":
@@ -631,6 +694,8 @@ class Interp:
                 out = np.empty(shape, np.uint8)
                 lib().hfref_compare_i64(COMPARE[fn], ptr(ia), ptr(ib), ptr(out), out.size)
             r = T(out.astype(np.bool_), "i1")
+        elif op == "hfusion.bitcast":
+            r = bitcast(T(np.ascontiguousarray(np.broadcast_to(xs[0].a, shape)), xs[0].elem), U)
         elif op == "hfusion.select":
             c, a, b = xs
             r = T(np.where(np.broadcast_to(c.a, shape), np.broadcast_to(a.a, shape), np.broadcast_to(b.a, shape)).astype(NP[U]), U)

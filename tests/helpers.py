@@ -229,3 +229,53 @@ def math_funcs():
 
 # functions of math_fns whose result is exactly rounded (bit-exact bar)
 MATH_EXACT = {"u_ilogb", "b_ldexp", "b_divfhp", "b_copysign", "b_mod", "bitcast_add"}
+
+
+def fp_inputs(func, n=4096, seed=0x46504F50):
+    """Seeded operands for group `func` of catalog module fp_ops, with
+    specials (signed zeros, infinities, NaN, denormals, extremes)."""
+    rng = np.random.default_rng(seed + sum(map(ord, func)))
+    op, t = func.rsplit("_", 1)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3.4e38, -3.4e38, 1.0], np.float32)
+
+    def enc(f):
+        f = np.asarray(f, np.float32)
+        if t == "f32":
+            return f
+        if t == "f16":
+            return f.astype(np.float16).view(np.uint16)
+        if t == "bf16":
+            return (f.view(np.uint32) >> 16).astype(np.uint16)  # truncation: exact bf16 values
+        raise KeyError(t)
+    if op in ("isinf", "isnan", "isfinite"):
+        x = (rng.normal(0, 1e3, n)).astype(np.float32)
+        x[:len(specials)] = specials
+        x[rng.integers(0, n, 64)] = np.inf
+        x[rng.integers(0, n, 64)] = np.nan
+        return [enc(x)]
+    if op == "nextafter":
+        x = rng.normal(0, 10, n).astype(np.float32)
+        y = rng.normal(0, 10, n).astype(np.float32)
+        x[:len(specials)] = specials
+        y[:len(specials)] = specials[::-1]
+        x[20:30] = y[20:30]          # x == y
+        x[30:34], y[30:34] = [0.0, -0.0, 0.0, 65504.0], [-1.0, 1.0, 0.0, np.inf]
+        return [enc(x), enc(y)]
+    if op in ("hypot", "hypot3"):
+        k = 3 if op == "hypot3" else 2
+        lim = 30 if t == "f32" else 4
+        vs = [(rng.choice([-1.0, 1.0], n) * np.exp(rng.uniform(-lim, lim, n))).astype(np.float32) for _ in range(k)]
+        vs[0][:6], vs[1][:6] = [0.0, np.inf, np.nan, 3.0, 1e-30, 1e30], [0.0, np.nan, 1.0, 4.0, 1e-30, 1e30]
+        vs[0][6:10] = vs[1][6:10]    # equal magnitudes
+        return [enc(v) for v in vs]
+    if op == "erfinv":
+        x = rng.uniform(-1.0, 1.0, n).astype(np.float32)
+        x[:8] = [0.0, -0.0, 1.0, -1.0, 1.5, np.nan, 0.9999999, -1e-30]
+        return [enc(x)]
+    if op == "bitcast":
+        return [rng.integers(-2**31, 2**31, n, dtype=np.int64).astype(np.int32), np.zeros(n, np.float32)]
+    raise KeyError(func)
+
+
+def fp_funcs():
+    return [f"{op}_{t}" for op, t in hf.catalog.FP_OPS]

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import MATH_EXACT, bf16_ulp_diff, math_funcs, math_inputs, run_gpu, run_oracle
+from helpers import MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, math_funcs, math_inputs, run_gpu, run_oracle
 
 pytestmark = pytest.mark.gpu
 I = hf.inputs
@@ -465,3 +465,30 @@ def test_math_fns(gpu, func):
     assert np.array_equal(out[inf], ref[inf]), "infinities differ"
     fin = np.isfinite(ref) & np.isfinite(out)
     np.testing.assert_allclose(out[fin], ref[fin], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("func", fp_funcs())
+def test_fp_ops(gpu, func):
+    """HFusion float ops without outs and hfusion.bitcast: predicates,
+    nextafter, hypot (the reference lowering's scaled f32 / direct f16
+    algorithm) and bitcast are bit-exact; erfinv (double Newton on erf)
+    within 1e-5 relative of the oracle's float64 erfinv, NaN/inf positions
+    equal."""
+    note(f"fp_ops {func}")
+    args = fp_inputs(func)
+    out, = run_gpu("fp_ops", args, gpu, func=func)
+    ref, = run_oracle("fp_ops", args, func=func)
+    if not func.startswith("erfinv"):
+        same = out.view(np.uint8) == ref.view(np.uint8)
+        if not same.all():
+            # any NaN matches any NaN
+            f = (lambda a: a.view(np.float16)) if func.endswith("f16") else (lambda a: a)
+            a, b = f(out), f(ref)
+            ok = (a == b) | (np.isnan(a.astype(np.float32)) & np.isnan(b.astype(np.float32)))
+            assert ok.all(), f"{int((~ok).sum())} differ"
+        return
+    a = out.view(np.float16).astype(np.float32) if func.endswith("f16") else out
+    b = ref.view(np.float16).astype(np.float32) if func.endswith("f16") else ref
+    assert np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[np.isinf(b)], b[np.isinf(b)])
+    fin = np.isfinite(b)
+    np.testing.assert_allclose(a[fin], b[fin], rtol=1e-5 if func.endswith("f32") else 1e-3, atol=1e-7)

@@ -115,3 +115,95 @@ def test_math_module_lists_every_function():
         assert f"b_{fn}" in names
     assert {"i_powi_i32", "i_ceildivui_i32", "i_modui_i32"} <= names
     assert hf.catalog.get("math_fns").count("func.func") == len(names)
+
+
+# --------------------------------------------------------------------- fp_ops
+from helpers import fp_funcs, fp_inputs  # noqa: E402
+
+
+def _f32(x, t):
+    if t == "f32":
+        return x
+    if t == "f16":
+        return x.view(np.float16).astype(np.float32)
+    return (x.astype(np.uint32) << 16).view(np.float32)
+
+
+def test_fp_predicates_specials():
+    x = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, 3.4e38, -1.0], np.float32)
+    want = {"isinf": [0, 0, 1, 1, 0, 0, 0, 0], "isnan": [0, 0, 0, 0, 1, 0, 0, 0], "isfinite": [1, 1, 0, 0, 0, 1, 1, 1]}
+    for op, w in want.items():
+        ir = hf.catalog.fp_ops(8)
+        got, = run_oracle_ir(ir, [x], f"{op}_f32")
+        assert got.astype(int).tolist() == w, op
+
+
+def run_oracle_ir(ir, args, func):
+    from oracle import interp
+    return interp.run(ir, *args, func=func)
+
+
+@pytest.mark.parametrize("func", [f for f in fp_funcs() if f.startswith("nextafter")])
+def test_nextafter_steps_one_ulp_toward_y(func):
+    t = func.split("_")[1]
+    x, y = fp_inputs(func)
+    got, = run_oracle("fp_ops", [x, y], func=func)
+    fx, fy, fg = _f32(x, t), _f32(y, t), _f32(got, t)
+    nan = np.isnan(fx) | np.isnan(fy)
+    assert np.isnan(fg[nan]).all()
+    eq = ~nan & (fx == fy)
+    assert np.array_equal(got[eq], y[eq])                      # x == y -> y
+    m = ~nan & ~eq
+    assert ((fg[m] - fx[m]) * (fy[m] - fx[m]) > 0).all()       # moved toward y
+    # exactly one step: nothing representable strictly between x and the result
+    xb = x.astype(np.int64) if t != "f32" else x.view(np.int32).astype(np.int64)
+    gb = got.astype(np.int64) if t != "f32" else got.view(np.int32).astype(np.int64)
+    sgn_bit = 0x8000 if t != "f32" else -2**31
+    mag = lambda b: np.where(b < 0, b & 0x7FFFFFFF, b) if t == "f32" else b & 0x7FFF  # noqa: E731
+    zero = m & (fx == 0)
+    assert (mag(gb[zero]) == 1).all()                          # from zero: the smallest denormal
+    nz = m & (fx != 0)
+    assert (np.abs(mag(gb[nz]) - mag(xb[nz])) == 1).all()
+    del sgn_bit
+
+
+@pytest.mark.parametrize("func", [f for f in fp_funcs() if f.startswith("hypot")])
+def test_hypot_against_double(func):
+    t = func.split("_")[1]
+    vs = fp_inputs(func)
+    got, = run_oracle("fp_ops", vs, func=func)
+    fs = [_f32(v, t).astype(np.float64) for v in vs]
+    with np.errstate(all="ignore"):
+        ref = np.sqrt(sum(f * f for f in fs))
+        big = np.maximum.reduce([np.abs(f) for f in fs])
+        ref = np.where(np.isfinite(ref) | ~np.isfinite(big), ref,
+                       big * np.sqrt(sum((f / big) ** 2 for f in fs)))
+    anynan = np.logical_or.reduce([np.isnan(f) for f in fs])
+    anyinf = np.logical_or.reduce([np.isinf(f) for f in fs])
+    ref = np.where(anyinf, np.inf, np.where(anynan, np.nan, ref))
+    g = _f32(got, t).astype(np.float64)
+    refr = ref.astype(np.float32) if t == "f32" else ref.astype(np.float16).astype(np.float32)
+    ulps = 2 if t == "f32" else 1
+    sp = np.spacing(np.abs(refr)).astype(np.float64)
+    ok = np.where(np.isfinite(refr), np.abs(g - refr) <= ulps * sp, (g == refr) | (np.isnan(g) & np.isnan(refr)))
+    assert ok.all(), f"{int((~ok).sum())} off"
+
+
+@pytest.mark.parametrize("func", [f for f in fp_funcs() if f.startswith("erfinv")])
+def test_erfinv_round_trip(func):
+    t = func.split("_")[1]
+    x, = fp_inputs(func)
+    got, = run_oracle("fp_ops", [x], func=func)
+    fx, fg = _f32(x, t).astype(np.float64), _f32(got, t).astype(np.float64)
+    inside = np.abs(fx) < 0.999
+    back = scipy.special.erf(fg[inside])
+    tol = (1e-6 if t == "f32" else 2e-3) * np.maximum(np.abs(fx[inside]), 1e-3) + 1e-7
+    assert (np.abs(back - fx[inside]) <= tol * 10).all()
+    assert np.isposinf(fg[fx == 1.0]).all() and np.isneginf(fg[fx == -1.0]).all()
+    assert np.isnan(fg[(np.abs(fx) > 1) | np.isnan(fx)]).all()
+
+
+def test_bitcast_op():
+    x, o = fp_inputs("bitcast_f32")
+    got, = run_oracle("fp_ops", [x, o], func="bitcast_f32")
+    assert np.array_equal(got.view(np.int32), x)
