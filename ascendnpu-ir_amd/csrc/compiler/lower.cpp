@@ -1933,6 +1933,156 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
 
 } // namespace
 
+// ======================================================================
+// Single-op kernels: cumulative ops, histogram, (de)interleave
+// ======================================================================
+bool isSingleOpKernel(const std::string &n) {
+  return n == "hfusion.cumsum" || n == "hfusion.cumprod" || n == "hfusion.cummax" || n == "hfusion.cummin" ||
+         n == "hfusion.histogram" || n == "hfusion.deinterleave" || n == "hfusion.interleave";
+}
+
+std::vector<int64_t> intList(const std::string &s) {
+  std::vector<int64_t> v;
+  std::stringstream ss(s);
+  std::string tok;
+  while (std::getline(ss, tok, ',')) if (!tok.empty()) v.push_back(std::stoll(tok));
+  return v;
+}
+
+KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op *op) {
+  Func &f = *A.f;
+  for (const Op *o : f.ops)
+    if (o != op && o->name != "tensor.empty" && o->name != "arith.constant") unsupported(o, "op in a group with " + op->name);
+  for (const Value *v : op->operands)
+    if (v->argIdx < 0) unsupported(op, "operand that is not a group argument");
+  std::vector<std::string> outPtr(op->results.size());
+  for (size_t i = 0; i < f.returns.size(); ++i) {
+    const Value *v = f.returns[i];
+    if (v->def != op) unsupported(op, "group returns a value other than the op's results");
+    outPtr[v->resultIdx] = resultPtr(A, i);
+  }
+  for (auto &s : outPtr) if (s.empty()) unsupported(op, "a result the group does not return");
+  auto inPtr = [&](size_t i) { return "p" + std::to_string(op->operands.at(i)->argIdx); };
+  auto numel = [](const std::vector<int64_t> &sh) { int64_t n = 1; for (auto d : sh) n *= d; return n; };
+  const std::string n = op->name.substr(std::string("hfusion.").size());
+  KernelPlan p;
+  p.kernelName = kname;
+  std::ostringstream k;
+  if (n == "cumsum" || n == "cumprod" || n == "cummax" || n == "cummin") {
+    // CPU meaning (cumprod: ConvertHFusionToUpstream.cpp:385-450): along the
+    // cumulation dim, in index order (reverse: from the end), acc_0 = x_0 and
+    // acc_l = acc_{l-1} (op) x_l, each step rounded to the element type.
+    const Value *x = op->operands.at(0);
+    Elem ie = x->type.elem, oe = op->results[0]->type.elem;
+    auto dims = intList(op->attr("cum_dims"));
+    const auto &sh = x->type.shape;
+    if (dims.size() != 1 || dims[0] < 0 || dims[0] >= (int64_t)sh.size()) unsupported(op, "one cumulation dim");
+    if (ie != oe && !(n == "cumsum" && !isFloat(ie) && !isFloat(oe) && elemBits(oe) >= elemBits(ie)))
+      unsupported(op, "result type differing from the input");
+    int64_t d = dims[0], L = sh[d], outer = 1, inner = 1;
+    for (int64_t i = 0; i < d; ++i) outer *= sh[i];
+    for (size_t i = d + 1; i < sh.size(); ++i) inner *= sh[i];
+    const bool rev = op->attr("reverse") == "true", nan = op->attr("propagate_nan", "true") != "false";
+    std::string comb;
+    if (isFloat(oe)) {
+      std::string fn = n == "cumsum" ? "add" : n == "cumprod" ? "mul" : n == "cummax" ? (nan ? "maxf" : "maxnumf")
+                                                                                      : (nan ? "minf" : "minnumf");
+      comb = inFloatType(oe, {"acc", "xv"}, [&](const std::vector<std::string> &y) { return f32BinaryFn(fn, y[0], y[1], op); });
+    } else {
+      std::string fn = n == "cumsum" ? "add" : n == "cumprod" ? "mul" : n == "cummax" ? "max_signed" : "min_signed";
+      comb = intBinaryFn(fn, "acc", "xv", oe, op);
+    }
+    const std::string IT = mtype(ie), OT = ctype(oe);
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  constexpr int64_t OUTER = " << outer << "ll, L = " << L << "ll, INNER = " << inner << "ll;\n"
+      << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
+      << "  if (t >= OUTER * INNER) return;\n"
+      << "  const int64_t o = t / INNER, i = t % INNER;\n"
+      << "  const " << IT << " *src = (const " << IT << " *)" << inPtr(0) << " + o * L * INNER + i;\n"
+      << "  " << OT << " *dst = (" << OT << " *)" << outPtr[0] << " + o * L * INNER + i;\n"
+      << "  " << OT << " acc = 0;\n"
+      << "  for (int64_t s = 0; s < L; ++s) {\n"
+      << "    const int64_t l = " << (rev ? "L - 1 - s" : "s") << ";\n"
+      << "    const " << OT << " xv = " << castExpr("(" + ctype(ie) + ")src[l * INNER]", ie, oe, false) << ";\n"
+      << "    acc = s == 0 ? xv : (" << OT << ")(" << comb << ");\n"
+      << "    dst[l * INNER] = acc;\n  }\n}\n";
+    p.kind = "SCAN";
+    p.variant = "one thread per line, " + std::string(rev ? "reverse" : "forward") + " serial order";
+    p.grid[0] = (unsigned)std::max<int64_t>(1, (outer * inner + 255) / 256);
+    p.block[0] = 256;
+  } else if (n == "histogram") {
+    const Value *x = op->operands.at(0);
+    const Value *mk = op->operands.size() > 1 ? op->operands[1] : nullptr;
+    if (op->literal.empty()) unsupported(op, "histogram without num_bins");
+    const int64_t bins = std::stoll(op->literal);
+    Elem ie = x->type.elem, oe = op->results[0]->type.elem;
+    if (isFloat(ie) || ie == Elem::I1) unsupported(op, "histogram of a non-integer input");
+    if (isFloat(oe) || oe == Elem::I1) unsupported(op, "histogram counts of a non-integer type");
+    if (op->results[0]->type.shape.size() != 1 || op->results[0]->type.shape[0] != bins)
+      unsupported(op, "histogram output must be [num_bins]");
+    const int64_t N = numel(x->type.shape);
+    const int ldsb = bins <= 8192 ? (int)bins : 0;
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(1024, (N + 256 * 16 - 1) / (256 * 16)));
+    const std::string MT = mk ? mtype(mk->type.elem) : "uint8_t";
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, true) << ") {\n"
+      << "  hf::histogram<256, " << ldsb << ", " << (mk ? "true" : "false") << ">((const " << mtype(ie) << " *)" << inPtr(0)
+      << ", (const " << MT << " *)" << (mk ? inPtr(1) : "nullptr") << ", " << N << "ll, " << bins << "ll, (" << ctype(oe)
+      << " *)" << outPtr[0] << ", (unsigned long long *)ws);\n}\n";
+    p.kind = "HISTOGRAM";
+    p.variant = ldsb ? "LDS bins, last-workgroup copy" : "global bins, last-workgroup copy";
+    p.grid[0] = (unsigned)grid;
+    p.block[0] = 256;
+    p.workspaceBytes = (uint64_t)bins * 8 + 256;
+    p.workspaceZeroInit = true;
+  } else {
+    // (de)interleave along the last dim (HFusionOps.td:160-220; CPU meaning of
+    // deinterleave ConvertHFusionToUpstream.cpp:268-335: out[.., j] =
+    // in[.., 2j + channel])
+    const bool de = n == "deinterleave";
+    const Value *x = op->operands.at(0);
+    Elem e = x->type.elem;
+    for (auto *v : op->operands) if (v->type.elem != e) unsupported(op, "operands of different types");
+    for (auto *r : op->results) if (r->type.elem != e) unsupported(op, "result type differing from the input");
+    const std::string T = mtype(e);
+    int64_t R = 1, J;
+    const auto &sh = x->type.shape;
+    for (size_t i = 0; i + 1 < sh.size(); ++i) R *= sh[i];
+    std::ostringstream body;
+    if (de) {
+      if (sh.back() % 2) unsupported(op, "deinterleave of an odd last dim");
+      J = sh.back() / 2;
+      int ch = op->angleKind == "all" ? -1 : (op->literal.empty() ? -1 : std::stoi(op->literal));
+      if (ch < -1 || ch > 1) unsupported(op, "deinterleave channel");
+      if ((ch == -1) != (op->results.size() == 2)) unsupported(op, "deinterleave result count for its channel");
+      body << "  const " << T << " *src = (const " << T << " *)" << inPtr(0) << " + r * (2 * J) + 2 * j;\n";
+      if (ch == -1)
+        body << "  ((" << T << " *)" << outPtr[0] << ")[t] = src[0];\n  ((" << T << " *)" << outPtr[1] << ")[t] = src[1];\n";
+      else
+        body << "  ((" << T << " *)" << outPtr[0] << ")[t] = src[" << ch << "];\n";
+      p.variant = "deinterleave channel " + std::string(ch == -1 ? "all" : std::to_string(ch));
+    } else {
+      if (op->operands.size() != 2) unsupported(op, "interleave of other than two tensors");
+      if (op->operands[1]->type.shape != sh) unsupported(op, "interleave operands of different shapes");
+      J = sh.back();
+      body << "  " << T << " *dst = (" << T << " *)" << outPtr[0] << " + r * (2 * J) + 2 * j;\n"
+           << "  dst[0] = ((const " << T << " *)" << inPtr(0) << ")[t];\n"
+           << "  dst[1] = ((const " << T << " *)" << inPtr(1) << ")[t];\n";
+      p.variant = "interleave";
+    }
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  constexpr int64_t R = " << R << "ll, J = " << J << "ll;\n"
+      << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
+      << "  if (t >= R * J) return;\n"
+      << "  const int64_t r = t / J, j = t % J;\n  (void)r; (void)j;\n"
+      << body.str() << "}\n";
+    p.kind = de ? "DEINTERLEAVE" : "INTERLEAVE";
+    p.grid[0] = (unsigned)std::max<int64_t>(1, (R * J + 255) / 256);
+    p.block[0] = 256;
+  }
+  p.source = k.str();
+  return p;
+}
+
 std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
   std::vector<KernelPlan> out;
   bool anyEntry = false;
@@ -1970,11 +2120,14 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
         if (f.returns.empty()) f.returns.push_back(r);
       }
     describeBuffers(A);
-    bool hasMM, hasRWI, hasRed;
-    std::string kind = resultKind(f, &hasMM, &hasRWI, &hasRed);
     std::string kname = "hf_" + f.name;
     KernelPlan p;
-    if (kind == "SINGLE_CUBE") {
+    const Op *single = findOp(f, [](const Op *o) { return isSingleOpKernel(o->name); });
+    bool hasMM = false, hasRWI = false, hasRed = false;
+    std::string kind = single ? "" : resultKind(f, &hasMM, &hasRWI, &hasRed);
+    if (single) {
+      p = lowerSingleOp(A, kname, single);
+    } else if (kind == "SINGLE_CUBE") {
       p = lowerMatmul(A, kname);
     } else if (kind == "REDUCE_WITH_INDEX") {
       p = lowerReduceWithIndex(A, kname);
@@ -2010,7 +2163,7 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
 std::string emitTranslationUnit(const std::vector<KernelPlan> &plans) {
   std::ostringstream s;
   s << "// Generated by bishengir-compile --target=mi355x (ConvertHFusionToHIP).\n"
-    << "#include \"hf_ops.h\"\n#include \"hf_row.h\"\n#include \"hf_argmax.h\"\n#include \"hf_mmad.h\"\n\n";
+    << "#include \"hf_ops.h\"\n#include \"hf_row.h\"\n#include \"hf_argmax.h\"\n#include \"hf_mmad.h\"\n#include \"hf_misc.h\"\n\n";
   for (auto &p : plans) s << "// group @" << p.funcName << ": " << p.kind << " (" << p.variant << ")\n" << p.source << "\n";
   return s.str();
 }

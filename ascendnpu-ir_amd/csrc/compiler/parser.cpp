@@ -515,6 +515,26 @@ private:
         op->hasDims = true;
         continue;
       }
+      // `cum_dims = [1]` (integer list) and `reverse = false` / `num = 4`
+      // operands written outside the attribute dictionary
+      if (t.kind == Tok::Ident && isP(peek(1), "=") && isP(peek(2), "[")) {
+        const std::string key = t.text;
+        pos_ += 3;
+        std::string v;
+        while (!isP(peek(), "]") && peek().kind != Tok::End) {
+          if (peek().kind == Tok::Number) v += (v.empty() ? "" : ",") + peek().text;
+          ++pos_;
+        }
+        expectP("]");
+        op->attrs[key] = v;
+        continue;
+      }
+      if (t.kind == Tok::Ident && isP(peek(1), "=") &&
+          (peek(2).kind == Tok::Number || (peek(2).kind == Tok::Ident && (peek(2).text == "true" || peek(2).text == "false")))) {
+        op->attrs[t.text] = peek(2).text;
+        pos_ += 3;
+        continue;
+      }
       if (isP(t, "(") && peek(1).kind == Tok::Value) {
         // region block arguments `(%in: f32, %init: f32)`
         int depth = 0;

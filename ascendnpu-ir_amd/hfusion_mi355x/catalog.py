@@ -208,6 +208,84 @@ def fp_ops(n=4096):
     return "module {\n" + "\n".join(funcs) + "\n}\n"
 
 
+# (name, op, elem in, elem out, shape, dim, reverse, extra attr)
+SCAN_OPS = [("cumsum_f32_d1", "cumsum", "f32", "f32", [64, 1000], 1, False, ""),
+            ("cumsum_f32_d0_rev", "cumsum", "f32", "f32", [64, 1000], 0, True, ""),
+            ("cumprod_f32", "cumprod", "f32", "f32", [32, 64], 1, False, ""),
+            ("cumprod_bf16_rev", "cumprod", "bf16", "bf16", [16, 256], 1, True, ""),
+            ("cummax_f32", "cummax", "f32", "f32", [64, 512], 1, False, ""),
+            ("cummin_f32_num", "cummin", "f32", "f32", [64, 512], 0, False, "{propagate_nan = false} "),
+            ("cumsum_i32_i64", "cumsum", "i32", "i64", [4096], 0, False, ""),
+            ("cumprod_i16", "cumprod", "i16", "i16", [8, 300], 1, False, ""),
+            ("cummax_i8_rev", "cummax", "i8", "i8", [64, 100], 1, True, "")]
+
+
+def scan_ops():
+    """One module, one group per cumulative op (cumsum/cumprod/cummax/cummin)
+    over several types, dims and directions."""
+    funcs = []
+    for name, op, ie, oe, shape, dim, rev, extra in SCAN_OPS:
+        X, O = _T(shape, ie), _T(shape, oe)
+        funcs.append(f"""  func.func @{name}(%x: {X}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %r = hfusion.{op} %x {extra}: {X} cum_dims = [{dim}] reverse = {str(rev).lower()} -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+# (name, input elem, input shape, bins, count elem, mask elem or None)
+HIST_OPS = [("hist_i32", "i32", [100000], 64, "i32", None),
+            ("hist_mask_i64", "i32", [300, 700], 10000, "i64", "i1"),
+            ("hist_i8_wrap", "i8", [5000], 16, "i8", None)]
+INTERLEAVE_OPS = [("deint_f32_c0", "f32", 0), ("deint_f32_c1", "f32", 1), ("deint_bf16_all", "bf16", -1),
+                  ("inter_f32", "f32", None), ("inter_i8", "i8", None)]
+
+
+def misc_ops():
+    """histogram (LDS and global bin paths, optional mask, wrapping counts)
+    and (de)interleave along the last dim."""
+    funcs = []
+    for name, ie, shape, bins, ce, me in HIST_OPS:
+        X, O = _T(shape, ie), _T([bins], ce)
+        if me:
+            M = _T(shape, me)
+            funcs.append(f"""  func.func @{name}(%x: {X}, %m: {M}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %r = hfusion.histogram %x, {bins}, %m : {X}, {M} -> {O}
+    return %r : {O}
+  }}""")
+        else:
+            funcs.append(f"""  func.func @{name}(%x: {X}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %r = hfusion.histogram %x, {bins} : {X} -> {O}
+    return %r : {O}
+  }}""")
+    for name, e, ch in INTERLEAVE_OPS:
+        if ch is None:
+            X, O = _T([64, 500], e), _T([64, 1000], e)
+            funcs.append(f"""  func.func @{name}(%a: {X}, %b: {X}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.interleave %a, %b : {X}, {X} -> {O}
+    return %r : {O}
+  }}""")
+        elif ch == -1:
+            X, O = _T([64, 1000], e), _T([64, 500], e)
+            funcs.append(f"""  func.func @{name}(%x: {X}) -> ({O}, {O})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r:2 = hfusion.deinterleave %x channel<all> : {X} -> {O}, {O}
+    return %r#0, %r#1 : {O}, {O}
+  }}""")
+        else:
+            X, O = _T([64, 1000], e), _T([64, 500], e)
+            funcs.append(f"""  func.func @{name}(%x: {X}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.deinterleave %x channel<{ch}> : {X} -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -410,6 +488,8 @@ def entries():
     e["reduce_ops"] = reduce_ops(48, 3000)
     e["math_fns"] = math_fns(4096)
     e["fp_ops"] = fp_ops(4096)
+    e["scan_ops"] = scan_ops()
+    e["misc_ops"] = misc_ops()
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

@@ -283,6 +283,58 @@ REDUCE_I = {"arith.addi": 0, "arith.muli": 1, "arith.maxsi": 2, "arith.minsi": 3
             "arith.ori": 5, "arith.xori": 6, "arith.maxui": 7, "arith.minui": 8}
 
 
+_SINGLE = ("hfusion.cumsum", "hfusion.cumprod", "hfusion.cummax", "hfusion.cummin", "hfusion.histogram",
+           "hfusion.deinterleave", "hfusion.interleave")
+
+
+def _single_op(op, rest, xs, rtypes):
+    """HFusion ops with their own syntax: cumulative ops, histogram and
+    (de)interleave (HFusionOps.td:160-420, 637-660)."""
+    shape, elem = rtypes[0]
+    name = op.split(".", 1)[1]
+    if name.startswith("cum"):
+        # CPU meaning (cumprod: ConvertHFusionToUpstream.cpp:385-450): in index
+        # order along the dim (reverse: from the end), acc_0 = x_0,
+        # acc_l = acc_{l-1} (op) x_l rounded to the element type at each step
+        d = int(re.search(r"cum_dims\s*=\s*\[\s*(-?\d+)", rest).group(1))
+        rev = re.search(r"reverse\s*=\s*true", rest) is not None
+        nan = re.search(r"propagate_nan\s*=\s*false", rest) is None
+        x = convert(xs[0], elem)
+        a = np.ascontiguousarray(np.moveaxis(np.asarray(x.a), d, 0))
+        order = range(a.shape[0] - 1, -1, -1) if rev else range(a.shape[0])
+        out = np.empty_like(a)
+        if elem in FLOATS:
+            fn = {"cumsum": "add", "cumprod": "mul", "cummax": "maxf" if nan else "maxnumf",
+                  "cummin": "minf" if nan else "minnumf"}[name]
+        else:
+            fn = {"cumsum": "add", "cumprod": "mul", "cummax": "max_signed", "cummin": "min_signed"}[name]
+        acc = None
+        for l in order:
+            xv = T(np.array(a[l]), elem)
+            acc = xv if acc is None else apply_binary(fn, acc, xv, elem, a[l].shape)
+            out[l] = acc.a
+        return [T(np.ascontiguousarray(np.moveaxis(out, 0, d)), elem)]
+    if name == "histogram":
+        bins = int(re.search(r"^\s*%[\w.$-]+\s*,\s*(\d+)", rest).group(1))
+        v = np.asarray(xs[0].a).astype(np.int64).ravel()
+        ok = (v >= 0) & (v < bins)
+        if len(xs) > 1:
+            ok &= np.asarray(xs[1].a).ravel().astype(np.int64) != 0
+        counts = np.bincount(v[ok], minlength=bins).astype(np.int64)
+        return [T(wrap_int(counts, elem), elem)]
+    if name == "deinterleave":
+        m = re.search(r"channel\s*<\s*(all|-?\d+)\s*>", rest)
+        ch = -1 if m.group(1) == "all" else int(m.group(1))
+        a = np.asarray(xs[0].a)
+        if ch == -1:
+            return [T(np.ascontiguousarray(a[..., 0::2]), elem), T(np.ascontiguousarray(a[..., 1::2]), elem)]
+        return [T(np.ascontiguousarray(a[..., ch::2]), elem)]
+    a, b = np.asarray(xs[0].a), np.asarray(xs[1].a)
+    out = np.empty(a.shape[:-1] + (2 * a.shape[-1],), a.dtype)
+    out[..., 0::2], out[..., 1::2] = a, b
+    return [T(out, elem)]
+
+
 _NON_DPS = ("hfusion.isinf", "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot",
             "hfusion.erfinv")
 
@@ -621,6 +673,17 @@ class Interp:
             return
         if op.startswith("arith.") and "ins(" not in rest:
             self._scalar_arith(res, op, rest, env)
+            return
+        if op in _SINGLE:
+            names = re.findall(r"%[\w.$-]+", rest.split(":", 1)[0])
+            rtypes = [parse_type(t) for t in _split_top(rest.rsplit("->", 1)[1])]
+            outs = _single_op(op, rest, [env[n] for n in names], rtypes)
+            if len(outs) == 1:
+                env[res] = outs[0]
+            else:
+                for i, o in enumerate(outs):
+                    env[f"{res}#{i}"] = o
+                env[res] = outs[0]
             return
         if op in _NON_DPS:
             names = re.findall(r"%[\w.$-]+", rest.split(":", 1)[0])

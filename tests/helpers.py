@@ -279,3 +279,50 @@ def fp_inputs(func, n=4096, seed=0x46504F50):
 
 def fp_funcs():
     return [f"{op}_{t}" for op, t in hf.catalog.FP_OPS]
+
+
+def scan_inputs(name, seed=0x5343414E):
+    """Seeded input of group `name` of catalog module scan_ops."""
+    spec = {s[0]: s for s in hf.catalog.SCAN_OPS}[name]
+    _, op, ie, _, shape, _, _, _ = spec
+    rng = np.random.default_rng(seed + sum(map(ord, name)))
+    if ie in ("f32", "bf16"):
+        if op == "cumprod":
+            x = rng.uniform(0.9, 1.1, shape)
+        else:
+            x = rng.normal(0, 10, shape)
+        x = x.astype(np.float32)
+        flat = x.reshape(-1)
+        if op in ("cummax", "cummin"):
+            flat[rng.integers(0, flat.size, 40)] = np.nan
+        if op == "cumprod":
+            flat[rng.integers(0, flat.size, 8)] = 0.0
+        if ie == "bf16":
+            return [(x.view(np.uint32) >> 16).astype(np.uint16)]
+        return [x]
+    dt = {"i8": np.int8, "i16": np.int16, "i32": np.int32}[ie]
+    lo, hi = {"cumprod": (-3, 4), "cumsum": (-2**31, 2**31), "cummax": (-128, 128)}[op]
+    return [rng.integers(lo, hi, shape).astype(dt)]
+
+
+def misc_inputs(name, seed=0x4D495343):
+    """Seeded inputs of group `name` of catalog module misc_ops."""
+    rng = np.random.default_rng(seed + sum(map(ord, name)))
+    hist = {h[0]: h for h in hf.catalog.HIST_OPS}
+    if name in hist:
+        _, ie, shape, bins, _, me = hist[name]
+        dt = {"i8": np.int8, "i32": np.int32}[ie]
+        x = rng.integers(-5, bins + 5, shape).astype(dt)
+        if me:
+            return [x, rng.random(shape) < 0.7]
+        return [x]
+    _, e, ch = {i[0]: i for i in hf.catalog.INTERLEAVE_OPS}[name]
+    def gen(shape):
+        if e == "f32":
+            return rng.normal(0, 1, shape).astype(np.float32)
+        if e == "bf16":
+            return rng.integers(0, 65536, shape).astype(np.uint16)
+        return rng.integers(-128, 128, shape).astype(np.int8)
+    if ch is None:
+        return [gen((64, 500)), gen((64, 500))]
+    return [gen((64, 1000))]

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, math_funcs, math_inputs, run_gpu, run_oracle
+from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, math_funcs, math_inputs, misc_inputs,
+                     run_gpu, run_oracle, scan_inputs)
 
 pytestmark = pytest.mark.gpu
 I = hf.inputs
@@ -492,3 +493,31 @@ def test_fp_ops(gpu, func):
     assert np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[np.isinf(b)], b[np.isinf(b)])
     fin = np.isfinite(b)
     np.testing.assert_allclose(a[fin], b[fin], rtol=1e-5 if func.endswith("f32") else 1e-3, atol=1e-7)
+
+
+# ----------------------------------------- scans, histogram, (de)interleave
+@pytest.mark.parametrize("name", [s[0] for s in hf.catalog.SCAN_OPS])
+def test_scan_ops(gpu, name):
+    """Cumulative ops in the serial order and per-step rounding of the CPU
+    loop: bit-exact (NaN positions included)."""
+    note(f"scan_ops {name}")
+    args = scan_inputs(name)
+    out, = run_gpu("scan_ops", args, gpu, func=name)
+    ref, = run_oracle("scan_ops", args, func=name)
+    if out.dtype.kind == "f":
+        assert np.array_equal(out, ref, equal_nan=True), f"{int((out != ref).sum())} differ"
+    else:
+        assert np.array_equal(out, ref), f"{int((out != ref).sum())} differ"
+
+
+@pytest.mark.parametrize("name", [h[0] for h in hf.catalog.HIST_OPS] + [i[0] for i in hf.catalog.INTERLEAVE_OPS])
+def test_misc_ops(gpu, name):
+    """histogram counts (twice in a row: the workspace is left cleared) and
+    (de)interleave: bit-exact."""
+    note(f"misc_ops {name}")
+    args = misc_inputs(name)
+    refs = run_oracle("misc_ops", args, func=name)
+    for _ in range(2):
+        outs = run_gpu("misc_ops", args, gpu, func=name)
+        for o, r in zip(outs, refs):
+            assert np.array_equal(o, r), f"{int((o != r).sum())} differ"

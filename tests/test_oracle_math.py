@@ -207,3 +207,61 @@ def test_bitcast_op():
     x, o = fp_inputs("bitcast_f32")
     got, = run_oracle("fp_ops", [x, o], func="bitcast_f32")
     assert np.array_equal(got.view(np.int32), x)
+
+
+# ------------------------------------------------- scans, histogram, (de)interleave
+from helpers import misc_inputs, scan_inputs  # noqa: E402
+
+
+@pytest.mark.parametrize("spec", hf.catalog.SCAN_OPS, ids=[s[0] for s in hf.catalog.SCAN_OPS])
+def test_scan_against_numpy_accumulate(spec):
+    """numpy's accumulate is a left-to-right loop in the array's dtype, so it
+    pins the serial order and the per-step rounding (bf16 excepted: numpy has
+    no bf16; that group rests on the f32 path plus the pinned RNE cast)."""
+    name, op, ie, oe, shape, dim, rev, extra = spec
+    if ie == "bf16":
+        pytest.skip("no independent bf16 accumulate")
+    x, = scan_inputs(name)
+    got, = run_oracle("scan_ops", [x], func=name)
+    a = x.astype({"i64": np.int64}.get(oe, x.dtype))
+    if rev:
+        a = np.flip(a, dim)
+    if op == "cumsum":
+        r = np.cumsum(a, axis=dim, dtype=a.dtype)
+    elif op == "cumprod":
+        r = np.cumprod(a, axis=dim, dtype=a.dtype)
+    elif op == "cummax":
+        r = np.maximum.accumulate(a, axis=dim)
+    else:
+        r = (np.fmin if "propagate_nan = false" in extra else np.minimum).accumulate(a, axis=dim)
+    if rev:
+        r = np.flip(r, dim)
+    assert np.array_equal(got, r, equal_nan=True)
+
+
+@pytest.mark.parametrize("spec", hf.catalog.HIST_OPS, ids=[h[0] for h in hf.catalog.HIST_OPS])
+def test_histogram_counts(spec):
+    name, ie, shape, bins, ce, me = spec
+    args = misc_inputs(name)
+    got, = run_oracle("misc_ops", args, func=name)
+    v = args[0].ravel().astype(np.int64)
+    keep = (v >= 0) & (v < bins)
+    if me:
+        keep &= args[1].ravel()
+    want = np.zeros(bins, np.int64)
+    for b in v[keep].tolist():
+        want[b] += 1
+    assert np.array_equal(got.astype(np.int64), want.astype({"i8": np.int8, "i32": np.int32, "i64": np.int64}[ce]).astype(np.int64))
+
+
+def test_deinterleave_interleave_closed_form():
+    for name, e, ch in hf.catalog.INTERLEAVE_OPS:
+        args = misc_inputs(name)
+        outs = run_oracle("misc_ops", args, func=name)
+        if ch is None:
+            a, b = args
+            assert np.array_equal(outs[0][:, 0::2], a) and np.array_equal(outs[0][:, 1::2], b)
+        elif ch == -1:
+            assert np.array_equal(outs[0], args[0][:, 0::2]) and np.array_equal(outs[1], args[0][:, 1::2])
+        else:
+            assert np.array_equal(outs[0], args[0][:, ch::2])
