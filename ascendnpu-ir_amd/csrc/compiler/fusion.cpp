@@ -1,5 +1,6 @@
 // HFusion fusion front-end (see fusion.h).
 #include "fusion.h"
+#include "lower.h"
 
 #include <algorithm>
 #include <climits>
@@ -618,6 +619,13 @@ std::string outlineFusedGroups(const Module &m, std::vector<ProgramPlan> &progra
         names.push_back("");
         groups.push_back({(int)i});
         kinds.push_back(-1);
+        continue;
+      }
+      if (p == Pat::Opaque && isSingleOpKernel(f.ops[i]->name)) {
+        // an op with a kernel of its own (scan, histogram, (de)interleave)
+        names.push_back(f.name + "_single_outlined_" + std::to_string(singles++) + "_0");
+        groups.push_back({(int)i});
+        kinds.push_back(Unknown);
         continue;
       }
       if (p == Pat::Opaque && f.ops[i]->name != "arith.constant")

@@ -1941,7 +1941,7 @@ bool isSingleOpKernel(const std::string &n) {
          n == "hfusion.histogram" || n == "hfusion.deinterleave" || n == "hfusion.interleave";
 }
 
-std::vector<int64_t> intList(const std::string &s) {
+static std::vector<int64_t> intList(const std::string &s) {
   std::vector<int64_t> v;
   std::stringstream ss(s);
   std::string tok;
@@ -1949,7 +1949,7 @@ std::vector<int64_t> intList(const std::string &s) {
   return v;
 }
 
-KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op *op) {
+static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op *op) {
   Func &f = *A.f;
   for (const Op *o : f.ops)
     if (o != op && o->name != "tensor.empty" && o->name != "arith.constant") unsupported(o, "op in a group with " + op->name);

@@ -44,6 +44,10 @@ struct LowerOptions {
   bool orderedFloatSums = false; // force serial-order fp sums everywhere
 };
 
+// Ops lowered as a kernel of their own (cumulative ops, histogram,
+// (de)interleave): they never fuse with other ops.
+bool isSingleOpKernel(const std::string &opName);
+
 // Lowers every `hacc.entry` function (or every function if none is tagged).
 std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt);
 

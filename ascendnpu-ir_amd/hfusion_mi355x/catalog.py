@@ -503,6 +503,7 @@ def entries():
     e["prog_gemm_rmsnorm_quant_ragged"] = g.gemm_rmsnorm_quant(100, 320, 192)
     e["prog_scores_softmax"] = g.scores_softmax(128, 1024, 128)
     e["prog_scores_softmax_ragged"] = g.scores_softmax(72, 1000, 64)
+    e["prog_exp_cumsum_scale"] = g.exp_cumsum_scale(64, 1000)
     return e
 
 

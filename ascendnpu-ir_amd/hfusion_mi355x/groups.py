@@ -373,3 +373,22 @@ def scores_softmax(m=1024, n=4096, k=128, scale=0.08838834764831845):
   }}
 }}
 """
+
+
+def exp_cumsum_scale(rows=64, cols=1000):
+    """An un-fused host function with a cumulative sum between two
+    elementwise ops: y = cumsum(exp(x), dim 1) * w.  The front-end outlines
+    the scan as a kernel of its own between the two elementwise groups."""
+    X = _t([rows, cols], "f32")
+    return f"""module {{
+  func.func @exp_cumsum_scale(%x: {X}, %w: {X}) -> {X}
+      {_HOST} {{
+    %e0 = tensor.empty() : {X}
+    %a = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%x : {X}) outs(%e0 : {X}) -> {X}
+    %c = hfusion.cumsum %a : {X} cum_dims = [1] reverse = false -> {X}
+    %e1 = tensor.empty() : {X}
+    %b = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%c, %w : {X}, {X}) outs(%e1 : {X}) -> {X}
+    return %b : {X}
+  }}
+}}
+"""

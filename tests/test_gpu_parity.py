@@ -521,3 +521,17 @@ def test_misc_ops(gpu, name):
         outs = run_gpu("misc_ops", args, gpu, func=name)
         for o, r in zip(outs, refs):
             assert np.array_equal(o, r), f"{int((o != r).sum())} differ"
+
+
+def test_program_with_scan(gpu):
+    """Host function exp -> cumsum -> mul: three launches (the scan is a
+    kernel of its own); exp on the GPU is within 6.5e-6 relative of glibc's,
+    and the serial sum carries that, so 1e-5 relative (plus a row-scaled
+    absolute term) bounds the result."""
+    note("prog_exp_cumsum_scale")
+    s = I.SEED_BASE + 90
+    x = I.normal_f32(s, (64, 1000))
+    w = I.uniform_f32(s + 1, (64, 1000), 0.5, 1.5)
+    out, = run_gpu("prog_exp_cumsum_scale", [x, w], gpu)
+    ref, = run_oracle("prog_exp_cumsum_scale", [x, w])
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
