@@ -1938,7 +1938,8 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
 // ======================================================================
 bool isSingleOpKernel(const std::string &n) {
   return n == "hfusion.cumsum" || n == "hfusion.cumprod" || n == "hfusion.cummax" || n == "hfusion.cummin" ||
-         n == "hfusion.histogram" || n == "hfusion.deinterleave" || n == "hfusion.interleave";
+         n == "hfusion.histogram" || n == "hfusion.deinterleave" || n == "hfusion.interleave" || n == "hfusion.flip" ||
+         n == "hfusion.mulext" || n == "hfusion.mulextui" || n == "hfusion.arange";
 }
 
 static std::vector<int64_t> intList(const std::string &s) {
@@ -1952,9 +1953,11 @@ static std::vector<int64_t> intList(const std::string &s) {
 static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op *op) {
   Func &f = *A.f;
   for (const Op *o : f.ops)
-    if (o != op && o->name != "tensor.empty" && o->name != "arith.constant") unsupported(o, "op in a group with " + op->name);
-  for (const Value *v : op->operands)
-    if (v->argIdx < 0) unsupported(op, "operand that is not a group argument");
+    if (o != op && o->name != "tensor.empty" && o->name != "arith.constant" && o->name.rfind("arith.index", 0) != 0)
+      unsupported(o, "op in a group with " + op->name);
+  if (op->name != "hfusion.arange")
+    for (const Value *v : op->operands)
+      if (v->argIdx < 0) unsupported(op, "operand that is not a group argument");
   std::vector<std::string> outPtr(op->results.size());
   for (size_t i = 0; i < f.returns.size(); ++i) {
     const Value *v = f.returns[i];
@@ -2009,6 +2012,94 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
     p.kind = "SCAN";
     p.variant = "one thread per line, " + std::string(rev ? "reverse" : "forward") + " serial order";
     p.grid[0] = (unsigned)std::max<int64_t>(1, (outer * inner + 255) / 256);
+    p.block[0] = 256;
+  } else if (n == "flip") {
+    // reverse along flip_axis (HFusionOps.td:226-245: the last dimension)
+    const Value *x = op->operands.at(0);
+    const auto &sh = x->type.shape;
+    int64_t ax = op->attrs.count("flip_axis") ? std::stoll(op->attr("flip_axis")) : (int64_t)sh.size() - 1;
+    if (ax < 0) ax += (int64_t)sh.size();
+    if (ax < 0 || ax >= (int64_t)sh.size()) unsupported(op, "flip_axis");
+    if (op->results[0]->type.elem != x->type.elem) unsupported(op, "flip result type");
+    int64_t L = sh[ax], outer = 1, inner = 1;
+    for (int64_t i = 0; i < ax; ++i) outer *= sh[i];
+    for (size_t i = ax + 1; i < sh.size(); ++i) inner *= sh[i];
+    const std::string T = mtype(x->type.elem);
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  constexpr int64_t L = " << L << "ll, INNER = " << inner << "ll, N = " << outer * L * inner << "ll;\n"
+      << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
+      << "  if (t >= N) return;\n"
+      << "  const int64_t i = t % INNER, l = (t / INNER) % L, o = t / (INNER * L);\n"
+      << "  ((" << T << " *)" << outPtr[0] << ")[t] = ((const " << T << " *)" << inPtr(0) << ")[(o * L + (L - 1 - l)) * INNER + i];\n}\n";
+    p.kind = "FLIP";
+    p.variant = "one thread per element";
+    p.grid[0] = (unsigned)std::max<int64_t>(1, (outer * L * inner + 255) / 256);
+    p.block[0] = 256;
+  } else if (n == "mulext" || n == "mulextui") {
+    // (2N)-bit product of sign- (mulext) or zero-extended (mulextui) operands,
+    // low and high N-bit halves (HFusionOps.td:114-158)
+    const Value *a0 = op->operands.at(0), *b0 = op->operands.at(1);
+    Elem e = a0->type.elem;
+    if (isFloat(e) || e == Elem::I1 || b0->type.elem != e || a0->type.shape != b0->type.shape) unsupported(op, "operands");
+    const int bits = elemBits(e);
+    const bool sgn = n == "mulext";
+    const std::string T = ctype(e), U = "uint" + std::to_string(bits) + "_t";
+    std::string lo, hi;
+    if (bits == 64) {
+      lo = "(" + T + ")((uint64_t)a * (uint64_t)b)";
+      hi = sgn ? "(" + T + ")__mul64hi((long long)a, (long long)b)" : "(" + T + ")__umul64hi((unsigned long long)a, (unsigned long long)b)";
+    } else {
+      std::string pr = sgn ? "((int64_t)a * (int64_t)b)" : "(int64_t)((uint64_t)(" + U + ")a * (uint64_t)(" + U + ")b)";
+      lo = "(" + T + ")" + pr;
+      hi = "(" + T + ")(" + pr + " >> " + std::to_string(bits) + ")";
+    }
+    const int64_t N = numel(a0->type.shape);
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
+      << "  if (t >= " << N << "ll) return;\n"
+      << "  const " << T << " a = ((const " << T << " *)" << inPtr(0) << ")[t], b = ((const " << T << " *)" << inPtr(1) << ")[t];\n";
+    if (!outPtr.empty() && op->results.size() == 2) {
+      k << "  ((" << T << " *)" << outPtr[0] << ")[t] = " << lo << ";\n"
+        << "  ((" << T << " *)" << outPtr[1] << ")[t] = " << hi << ";\n}\n";
+    } else {
+      unsupported(op, "mulext without both results");
+    }
+    p.kind = "MULEXT";
+    p.variant = sgn ? "signed" : "unsigned";
+    p.grid[0] = (unsigned)std::max<int64_t>(1, (N + 255) / 256);
+    p.block[0] = 256;
+  } else if (n == "arange") {
+    // value at index (i0, i1, ...) = offset + sum_d stride_d * i_d
+    // (HFusionStructuredOps.td:163-175), converted to the element type
+    if (op->outs.size() != 1) unsupported(op, "arange without one outs");
+    const Value *o = op->outs[0];
+    const auto &sh = o->type.shape;
+    const bool hasOff = op->attr("arange.offset") == "1";
+    if (op->operands.size() != sh.size() + (hasOff ? 1 : 0)) unsupported(op, "arange needs one stride per dimension");
+    auto idx = [&](const Value *v) -> std::string {
+      if (v->isConst) return "(int64_t)" + std::to_string(v->iconst) + "ll";
+      if (v->argIdx >= 0 && A.params[v->argIdx].role == "scalar") return "(int64_t)" + scalarArgExpr(A, v->argIdx);
+      unsupported(op, "arange offset/stride that is not a constant or scalar argument");
+    };
+    std::string off = hasOff ? idx(op->operands[0]) : "(int64_t)0";
+    std::ostringstream val;
+    val << off;
+    int64_t inner = 1;
+    std::vector<std::string> terms;
+    for (int d = (int)sh.size() - 1; d >= 0; --d) {
+      val << " + " << idx(op->operands[(hasOff ? 1 : 0) + d]) << " * ((t / " << inner << "ll) % " << sh[d] << "ll)";
+      inner *= sh[d];
+    }
+    Elem e = o->type.elem;
+    const int64_t N = numel(sh);
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
+      << "  if (t >= " << N << "ll) return;\n"
+      << "  const int64_t v = " << val.str() << ";\n"
+      << "  ((" << mtype(e) << " *)" << outPtr[0] << ")[t] = " << castExpr("v", Elem::I64, e, false) << ";\n}\n";
+    p.kind = "ARANGE";
+    p.variant = "one thread per element";
+    p.grid[0] = (unsigned)std::max<int64_t>(1, (N + 255) / 256);
     p.block[0] = 256;
   } else if (n == "histogram") {
     const Value *x = op->operands.at(0);

@@ -515,6 +515,13 @@ private:
         op->hasDims = true;
         continue;
       }
+      // hfusion.arange `offset[%o] strides[%s0, ...]`: the offset operand
+      // comes first when present
+      if (t.kind == Tok::Ident && t.text == "offset" && isP(peek(1), "[")) {
+        op->attrs["arange.offset"] = "1";
+        ++pos_;
+        continue;
+      }
       // `cum_dims = [1]` (integer list) and `reverse = false` / `num = 4`
       // operands written outside the attribute dictionary
       if (t.kind == Tok::Ident && isP(peek(1), "=") && isP(peek(2), "[")) {
@@ -612,6 +619,8 @@ private:
       else if (op->toType.elem != Elem::None) rtypes.push_back(op->toType);
       else if (op->literalType.elem != Elem::None) rtypes.push_back(op->literalType);
     }
+    // hfusion.mulext / mulextui: two results of the operands' type
+    if ((op->name == "hfusion.mulext" || op->name == "hfusion.mulextui") && rtypes.size() == 1) rtypes.push_back(rtypes[0]);
     size_t nres = multi ? (size_t)multi : resNames.size();
     if (nres > rtypes.size() && !resNames.empty())
       throw CompileError("cannot infer result types of '" + op->name + "' at line " + std::to_string(line));

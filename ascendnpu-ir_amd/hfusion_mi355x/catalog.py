@@ -283,7 +283,36 @@ def misc_ops():
     %r = hfusion.deinterleave %x channel<{ch}> : {X} -> {O}
     return %r : {O}
   }}""")
+    # flip, mulext / mulextui, arange
+    for e in ("f32", "bf16"):
+        X = _T([64, 1000], e)
+        funcs.append(f"""  func.func @flip_{e}(%x: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.flip %x : {X} flip_axis = 1 -> {X}
+    return %r : {X}
+  }}""")
+    for op in ("mulext", "mulextui"):
+        for e in ("i8", "i32", "i64"):
+            X = _T([4096], e)
+            funcs.append(f"""  func.func @{op}_{e}(%a: {X}, %b: {X}) -> ({X}, {X})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %lo, %hi = hfusion.{op} %a, %b : {X}
+    return %lo, %hi : {X}, {X}
+  }}""")
+    for e in ("i32", "f32"):
+        O = _T([48, 130], e)
+        funcs.append(f"""  func.func @arange_{e}(%o: {O}, %off: index) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %s0 = arith.constant 1000 : index
+    %s1 = arith.constant -3 : index
+    %r = hfusion.arange offset[%off] strides[%s0, %s1] outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
     return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+MISC_EXTRA = (["flip_f32", "flip_bf16"] + [f"{op}_{e}" for op in ("mulext", "mulextui") for e in ("i8", "i32", "i64")]
+              + ["arange_i32", "arange_f32"])
 
 
 def reduce_ops(rows=48, cols=3000):

@@ -284,7 +284,7 @@ REDUCE_I = {"arith.addi": 0, "arith.muli": 1, "arith.maxsi": 2, "arith.minsi": 3
 
 
 _SINGLE = ("hfusion.cumsum", "hfusion.cumprod", "hfusion.cummax", "hfusion.cummin", "hfusion.histogram",
-           "hfusion.deinterleave", "hfusion.interleave")
+           "hfusion.deinterleave", "hfusion.interleave", "hfusion.flip", "hfusion.mulext", "hfusion.mulextui")
 
 
 def _single_op(op, rest, xs, rtypes):
@@ -314,6 +314,24 @@ def _single_op(op, rest, xs, rtypes):
             acc = xv if acc is None else apply_binary(fn, acc, xv, elem, a[l].shape)
             out[l] = acc.a
         return [T(np.ascontiguousarray(np.moveaxis(out, 0, d)), elem)]
+    if name == "flip":
+        # reverse along flip_axis (HFusionOps.td:226-245)
+        m = re.search(r"flip_axis\s*=\s*(-?\d+)", rest)
+        ax = int(m.group(1)) if m else -1
+        return [T(np.ascontiguousarray(np.flip(np.asarray(xs[0].a), ax)), elem)]
+    if name in ("mulext", "mulextui"):
+        # (2N)-bit product of sign- or zero-extended operands: low and high halves
+        bits = BITS[elem]
+        a, b = (np.asarray(v.a).astype(object).ravel() for v in xs)
+        m = 1 << bits
+        if name == "mulextui":
+            a, b = [x % m for x in a], [x % m for x in b]
+        prod = [int(x) * int(y) for x, y in zip(a, b)]
+        wrap = lambda v: (v % m) - m if (v % m) >= m // 2 else v % m  # noqa: E731
+        lo = np.array([wrap(p) for p in prod], np.int64)
+        hi = np.array([wrap(p >> bits) for p in prod], np.int64)
+        sh = np.shape(xs[0].a)
+        return [T(wrap_int(lo.reshape(sh), elem), elem), T(wrap_int(hi.reshape(sh), elem), elem)]
     if name == "histogram":
         bins = int(re.search(r"^\s*%[\w.$-]+\s*,\s*(\d+)", rest).group(1))
         v = np.asarray(xs[0].a).astype(np.int64).ravel()
@@ -631,10 +649,11 @@ class Interp:
         self.written.append(outs[0])
 
     def _exec(self, s, env):
-        m = re.match(r"^\s*(%[\w.$-]+)(?::(\d+))?\s*=\s*([\w.]+)(.*)$", s)
+        m = re.match(r"^\s*(%[\w.$-]+)(?::(\d+))?((?:\s*,\s*%[\w.$-]+)*)\s*=\s*([\w.]+)(.*)$", s)
         if not m:
             raise ValueError(f"cannot parse statement: {s}")
-        res, nres, op, rest = m.group(1), m.group(2), m.group(3), m.group(4)
+        res, nres, op, rest = m.group(1), m.group(2), m.group(4), m.group(5)
+        more = re.findall(r"%[\w.$-]+", m.group(3) or "")
 
         def get(n):
             return env[n]
@@ -676,9 +695,12 @@ class Interp:
             return
         if op in _SINGLE:
             names = re.findall(r"%[\w.$-]+", rest.split(":", 1)[0])
-            rtypes = [parse_type(t) for t in _split_top(rest.rsplit("->", 1)[1])]
+            rtypes = [parse_type(t) for t in _split_top(rest.rsplit("->", 1)[1] if "->" in rest else rest.rsplit(":", 1)[1])]
             outs = _single_op(op, rest, [env[n] for n in names], rtypes)
-            if len(outs) == 1:
+            if more:
+                for nm, o in zip([res] + more, outs):
+                    env[nm] = o
+            elif len(outs) == 1:
                 env[res] = outs[0]
             else:
                 for i, o in enumerate(outs):
@@ -693,6 +715,19 @@ class Interp:
             return
         ins, ins_t = _operands(_group(rest, "ins"))
         outs, outs_t = _operands(_group(rest, "outs"))
+        if op == "hfusion.arange":
+            # value at (i0, i1, ...) = offset + sum_d stride_d * i_d
+            # (HFusionStructuredOps.td:163-175), converted to the element type
+            o = get(outs[0])
+            head = rest.split("outs(", 1)[0]
+            vals = [int(np.asarray(env[n].a)) for n in re.findall(r"%[\w.$-]+", head)]
+            off = vals.pop(0) if "offset[" in head else 0
+            grids = np.indices(o.a.shape, dtype=np.int64)
+            v = np.full(o.a.shape, off, np.int64)
+            for st, g in zip(vals, grids):
+                v = v + st * g
+            env[res] = convert(T(v, "i64"), o.elem)
+            return
         if op == "linalg.fill":
             o = get(outs[0])
             v = convert(get(ins[0]), o.elem)

@@ -326,3 +326,21 @@ def misc_inputs(name, seed=0x4D495343):
     if ch is None:
         return [gen((64, 500)), gen((64, 500))]
     return [gen((64, 1000))]
+
+
+def misc_extra_inputs(name, seed=0x45585452):
+    """Seeded arguments of the flip / mulext / arange groups of misc_ops."""
+    rng = np.random.default_rng(seed + sum(map(ord, name)))
+    if name.startswith("flip"):
+        if name.endswith("bf16"):
+            return [rng.integers(0, 65536, (64, 1000)).astype(np.uint16)]
+        return [rng.normal(0, 1, (64, 1000)).astype(np.float32)]
+    if name.startswith("mulext"):
+        dt = {"i8": np.int8, "i32": np.int32, "i64": np.int64}[name.rsplit("_", 1)[1]]
+        info = np.iinfo(dt)
+        a = rng.integers(info.min, info.max, 4096, dtype=np.int64, endpoint=True).astype(dt)
+        b = rng.integers(info.min, info.max, 4096, dtype=np.int64, endpoint=True).astype(dt)
+        a[:4], b[:4] = [info.min, info.min, info.max, -1], [info.min, -1, info.max, -1]
+        return [a, b]
+    dt = np.int32 if name.endswith("i32") else np.float32
+    return [np.zeros((48, 130), dt), np.int64(-77)]

@@ -13,8 +13,8 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, math_funcs, math_inputs, misc_inputs,
-                     run_gpu, run_oracle, scan_inputs)
+from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, math_funcs, math_inputs, misc_extra_inputs,
+                     misc_inputs, run_gpu, run_oracle, scan_inputs)
 
 pytestmark = pytest.mark.gpu
 I = hf.inputs
@@ -535,3 +535,16 @@ def test_program_with_scan(gpu):
     out, = run_gpu("prog_exp_cumsum_scale", [x, w], gpu)
     ref, = run_oracle("prog_exp_cumsum_scale", [x, w])
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("name", hf.catalog.MISC_EXTRA)
+def test_flip_mulext_arange(gpu, name):
+    """flip, mulext / mulextui (both halves) and arange (offset argument,
+    negative stride, i32 and f32 results): bit-exact."""
+    note(f"misc_ops {name}")
+    args = misc_extra_inputs(name)
+    outs = run_gpu("misc_ops", args, gpu, func=name)
+    refs = run_oracle("misc_ops", args, func=name)
+    assert len(outs) == len(refs)
+    for o, r in zip(outs, refs):
+        assert np.array_equal(o, r), f"{int((o != r).sum())} differ"

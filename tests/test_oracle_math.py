@@ -265,3 +265,31 @@ def test_deinterleave_interleave_closed_form():
             assert np.array_equal(outs[0], args[0][:, 0::2]) and np.array_equal(outs[1], args[0][:, 1::2])
         else:
             assert np.array_equal(outs[0], args[0][:, ch::2])
+
+
+from helpers import misc_extra_inputs  # noqa: E402
+
+
+def test_mulext_halves_recompose_the_product():
+    """lo + hi * 2^N equals the exact product of the sign- (mulext) or
+    zero-extended (mulextui) operands, with lo read unsigned."""
+    for name in [n for n in hf.catalog.MISC_EXTRA if n.startswith("mulext")]:
+        a, b = misc_extra_inputs(name)
+        lo, hi = run_oracle("misc_ops", [a, b], func=name)
+        bits = a.dtype.itemsize * 8
+        m = 1 << bits
+        for x, y, l, h in zip(a.tolist()[:512], b.tolist()[:512], lo.tolist()[:512], hi.tolist()[:512]):
+            if name.startswith("mulextui"):
+                x, y = x % m, y % m
+                h %= m
+            assert (l % m) + h * m == x * y, (name, x, y, l, h)
+
+
+def test_flip_and_arange_closed_forms():
+    x, = misc_extra_inputs("flip_f32")
+    got, = run_oracle("misc_ops", [x], func="flip_f32")
+    assert np.array_equal(got, x[:, ::-1])
+    o, off = misc_extra_inputs("arange_i32")
+    got, = run_oracle("misc_ops", [o, off], func="arange_i32")
+    i, j = np.meshgrid(np.arange(48), np.arange(130), indexing="ij")
+    assert np.array_equal(got, (off + 1000 * i - 3 * j).astype(np.int32))
