@@ -1939,7 +1939,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
 bool isSingleOpKernel(const std::string &n) {
   return n == "hfusion.cumsum" || n == "hfusion.cumprod" || n == "hfusion.cummax" || n == "hfusion.cummin" ||
          n == "hfusion.histogram" || n == "hfusion.deinterleave" || n == "hfusion.interleave" || n == "hfusion.flip" ||
-         n == "hfusion.mulext" || n == "hfusion.mulextui" || n == "hfusion.arange";
+         n == "hfusion.mulext" || n == "hfusion.mulextui" || n == "hfusion.arange" || n == "hfusion.gather";
 }
 
 static std::vector<int64_t> intList(const std::string &s) {
@@ -1955,6 +1955,9 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
   for (const Op *o : f.ops)
     if (o != op && o->name != "tensor.empty" && o->name != "arith.constant" && o->name.rfind("arith.index", 0) != 0)
       unsupported(o, "op in a group with " + op->name);
+  if (op->name == "hfusion.gather")
+    for (const Value *v : op->ins)
+      if (v->argIdx < 0) unsupported(op, "operand that is not a group argument");
   if (op->name != "hfusion.arange")
     for (const Value *v : op->operands)
       if (v->argIdx < 0) unsupported(op, "operand that is not a group argument");
@@ -2099,6 +2102,48 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
       << "  ((" << mtype(e) << " *)" << outPtr[0] << ")[t] = " << castExpr("v", Elem::I64, e, false) << ";\n}\n";
     p.kind = "ARANGE";
     p.variant = "one thread per element";
+    p.grid[0] = (unsigned)std::max<int64_t>(1, (N + 255) / 256);
+    p.block[0] = 256;
+  } else if (n == "gather") {
+    // out[p] = src[p with the axis coordinate replaced by index[p]] when
+    // 0 <= index[p] < src.shape[axis], else the init value (the loop of
+    // HFusionStructuredOps.td:222-238 assigns only on a matching k)
+    if (op->ins.size() != 2 || op->outs.size() != 1) unsupported(op, "gather operands");
+    const Value *src = op->ins[0], *ix = op->ins[1], *init = op->outs[0];
+    const auto &ss = src->type.shape, &is = ix->type.shape;
+    const int64_t rank = (int64_t)is.size();
+    int64_t ax = op->attrs.count("axis") ? std::stoll(op->attr("axis")) : rank - 1;
+    if (ax < 0) ax += rank;
+    if ((int64_t)ss.size() != rank || ax < 0 || ax >= rank || init->type.shape != is) unsupported(op, "gather shapes");
+    for (int64_t d = 0; d < rank; ++d)
+      if (d != ax && ss[d] != is[d]) unsupported(op, "gather shapes differing off the axis");
+    if (isFloat(ix->type.elem) || ix->type.elem == Elem::I1) unsupported(op, "gather index type");
+    const std::string T = mtype(src->type.elem);
+    // strides of the index/output and of src
+    std::vector<int64_t> istr(rank, 1), sstr(rank, 1);
+    for (int64_t d = rank - 2; d >= 0; --d) { istr[d] = istr[d + 1] * is[d + 1]; sstr[d] = sstr[d + 1] * ss[d + 1]; }
+    const int64_t N = numel(is);
+    std::ostringstream sofs;
+    sofs << "(int64_t)0";
+    for (int64_t d = 0; d < rank; ++d) {
+      if (d == ax) sofs << " + k * " << sstr[d] << "ll";
+      else sofs << " + ((t / " << istr[d] << "ll) % " << is[d] << "ll) * " << sstr[d] << "ll";
+    }
+    const std::string initPtr = init->argIdx >= 0 ? "p" + std::to_string(init->argIdx) : "";
+    std::string fallback = initPtr.empty() ? (init->def && init->def->name == "tensor.empty" ? "" : "") : "((const " + T + " *)" + initPtr + ")[t]";
+    if (fallback.empty()) {
+      // init from tensor.empty: its contents are unspecified; keep what the result buffer holds
+      fallback = "((" + T + " *)" + outPtr[0] + ")[t]";
+    }
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
+      << "  if (t >= " << N << "ll) return;\n"
+      << "  const int64_t k = (int64_t)((const " << mtype(ix->type.elem) << " *)p" << ix->argIdx << ")[t];\n"
+      << "  const " << T << " v = (k >= 0 && k < " << ss[ax] << "ll) ? ((const " << T << " *)p" << src->argIdx << ")[" << sofs.str()
+      << "] : " << fallback << ";\n"
+      << "  ((" << T << " *)" << outPtr[0] << ")[t] = v;\n}\n";
+    p.kind = "GATHER";
+    p.variant = "one thread per output element";
     p.grid[0] = (unsigned)std::max<int64_t>(1, (N + 255) / 256);
     p.block[0] = 256;
   } else if (n == "histogram") {

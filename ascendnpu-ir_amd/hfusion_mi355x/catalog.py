@@ -311,6 +311,26 @@ def misc_ops():
     return "module {\n" + "\n".join(funcs) + "\n}\n"
 
 
+# (name, src elem, src shape, index elem, index shape, axis)
+GATHER_OPS = [("gather_f16_ax1", "f16", [5, 6], "i32", [5, 3], 1),
+              ("gather_f32_ax1", "f32", [64, 1000], "i32", [64, 100], 1),
+              ("gather_bf16_ax0", "bf16", [100, 32], "i64", [50, 32], 0)]
+
+
+def gather_ops():
+    """hfusion.gather along axis 1 and 0, i32 and i64 indices, the init
+    (fallback for out-of-range indices) passed as the outs argument."""
+    funcs = []
+    for name, se, ss, ie, ish, ax in GATHER_OPS:
+        S, I, O = _T(ss, se), _T(ish, ie), _T(ish, se)
+        funcs.append(f"""  func.func @{name}(%src: {S}, %idx: {I}, %init: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.gather {{operandSegmentSizes = array<i32: 2, 1>}} ins(%src, %idx : {S}, {I}) outs(%init : {O}) axis = {ax} -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
 MISC_EXTRA = (["flip_f32", "flip_bf16"] + [f"{op}_{e}" for op in ("mulext", "mulextui") for e in ("i8", "i32", "i64")]
               + ["arange_i32", "arange_f32"])
 
@@ -519,6 +539,7 @@ def entries():
     e["fp_ops"] = fp_ops(4096)
     e["scan_ops"] = scan_ops()
     e["misc_ops"] = misc_ops()
+    e["gather_ops"] = gather_ops()
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

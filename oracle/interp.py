@@ -715,6 +715,17 @@ class Interp:
             return
         ins, ins_t = _operands(_group(rest, "ins"))
         outs, outs_t = _operands(_group(rest, "outs"))
+        if op == "hfusion.gather":
+            # out[p] = src[p with axis coordinate index[p]] when the index is in
+            # range, else init[p] (HFusionStructuredOps.td:222-238)
+            src, ix = get(ins[0]), get(ins[1])
+            o = get(outs[0])
+            ax = int(re.search(r"axis\s*=\s*(-?\d+)", rest).group(1))
+            k = np.asarray(ix.a).astype(np.int64)
+            ok = (k >= 0) & (k < np.asarray(src.a).shape[ax])
+            g = np.take_along_axis(np.asarray(src.a), np.where(ok, k, 0), axis=ax)
+            env[res] = T(np.where(ok, g, np.asarray(o.a)).astype(NP[o.elem]), o.elem)
+            return
         if op == "hfusion.arange":
             # value at (i0, i1, ...) = offset + sum_d stride_d * i_d
             # (HFusionStructuredOps.td:163-175), converted to the element type

@@ -344,3 +344,17 @@ def misc_extra_inputs(name, seed=0x45585452):
         return [a, b]
     dt = np.int32 if name.endswith("i32") else np.float32
     return [np.zeros((48, 130), dt), np.int64(-77)]
+
+
+def gather_inputs(name, seed=0x47415448):
+    """Seeded (src, index, init) of group `name` of catalog module gather_ops;
+    about one index in ten is out of range (negative or past the axis)."""
+    spec = {g[0]: g for g in hf.catalog.GATHER_OPS}[name]
+    _, se, ss, ie, ish, ax = spec
+    rng = np.random.default_rng(seed + sum(map(ord, name)))
+    src = rng.integers(0, 65536, ss).astype(np.uint16) if se in ("f16", "bf16") else rng.normal(0, 1, ss).astype(np.float32)
+    if se == "f16":
+        src = rng.normal(0, 1, ss).astype(np.float16).view(np.uint16)
+    idx = rng.integers(-ss[ax] // 10, ss[ax] + ss[ax] // 10 + 1, ish).astype({"i32": np.int32, "i64": np.int64}[ie])
+    init = np.full(ish, 0x7777 if se != "f32" else 7.0, src.dtype)
+    return [src, idx, init]

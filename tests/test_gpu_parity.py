@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, math_funcs, math_inputs, misc_extra_inputs,
+from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, gather_inputs, math_funcs, math_inputs,
+                     misc_extra_inputs,
                      misc_inputs, run_gpu, run_oracle, scan_inputs)
 
 pytestmark = pytest.mark.gpu
@@ -548,3 +549,14 @@ def test_flip_mulext_arange(gpu, name):
     assert len(outs) == len(refs)
     for o, r in zip(outs, refs):
         assert np.array_equal(o, r), f"{int((o != r).sum())} differ"
+
+
+@pytest.mark.parametrize("name", [g[0] for g in hf.catalog.GATHER_OPS])
+def test_gather(gpu, name):
+    """hfusion.gather along axis 1 and 0 with out-of-range indices (init
+    kept): bit-exact."""
+    note(f"gather_ops {name}")
+    args = gather_inputs(name)
+    out, = run_gpu("gather_ops", args, gpu, func=name)
+    ref, = run_oracle("gather_ops", args, func=name)
+    assert np.array_equal(out, ref), f"{int((out != ref).sum())} differ"

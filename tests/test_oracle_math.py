@@ -293,3 +293,24 @@ def test_flip_and_arange_closed_forms():
     got, = run_oracle("misc_ops", [o, off], func="arange_i32")
     i, j = np.meshgrid(np.arange(48), np.arange(130), indexing="ij")
     assert np.array_equal(got, (off + 1000 * i - 3 * j).astype(np.int32))
+
+
+from helpers import gather_inputs  # noqa: E402
+
+
+@pytest.mark.parametrize("spec", hf.catalog.GATHER_OPS, ids=[g[0] for g in hf.catalog.GATHER_OPS])
+def test_gather_loop_form(spec):
+    """The op description's loop (HFusionStructuredOps.td:222-238), run
+    literally on the group's inputs: output[p] = src[.. k ..] for the k with
+    index[p] == k, else the init value."""
+    name, se, ss, ie, ish, ax = spec
+    src, idx, init = gather_inputs(name)
+    got, = run_oracle("gather_ops", [src, idx, init], func=name)
+    want = init.copy()
+    for p in np.ndindex(*ish):
+        for k in range(ss[ax]):
+            if idx[p] == k:
+                q = list(p)
+                q[ax] = k
+                want[p] = src[tuple(q)]
+    assert np.array_equal(got, want)
