@@ -2061,12 +2061,9 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
       << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
       << "  if (t >= " << N << "ll) return;\n"
       << "  const " << T << " a = ((const " << T << " *)" << inPtr(0) << ")[t], b = ((const " << T << " *)" << inPtr(1) << ")[t];\n";
-    if (!outPtr.empty() && op->results.size() == 2) {
-      k << "  ((" << T << " *)" << outPtr[0] << ")[t] = " << lo << ";\n"
-        << "  ((" << T << " *)" << outPtr[1] << ")[t] = " << hi << ";\n}\n";
-    } else {
-      unsupported(op, "mulext without both results");
-    }
+    if (op->results.size() != 2) unsupported(op, "mulext without both results");
+    k << "  ((" << T << " *)" << outPtr[0] << ")[t] = " << lo << ";\n"
+      << "  ((" << T << " *)" << outPtr[1] << ")[t] = " << hi << ";\n}\n";
     p.kind = "MULEXT";
     p.variant = sgn ? "signed" : "unsigned";
     p.grid[0] = (unsigned)std::max<int64_t>(1, (N + 255) / 256);
@@ -2088,7 +2085,6 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
     std::ostringstream val;
     val << off;
     int64_t inner = 1;
-    std::vector<std::string> terms;
     for (int d = (int)sh.size() - 1; d >= 0; --d) {
       val << " + " << idx(op->operands[(hasOff ? 1 : 0) + d]) << " * ((t / " << inner << "ll) % " << sh[d] << "ll)";
       inner *= sh[d];
@@ -2129,12 +2125,10 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
       if (d == ax) sofs << " + k * " << sstr[d] << "ll";
       else sofs << " + ((t / " << istr[d] << "ll) % " << is[d] << "ll) * " << sstr[d] << "ll";
     }
-    const std::string initPtr = init->argIdx >= 0 ? "p" + std::to_string(init->argIdx) : "";
-    std::string fallback = initPtr.empty() ? (init->def && init->def->name == "tensor.empty" ? "" : "") : "((const " + T + " *)" + initPtr + ")[t]";
-    if (fallback.empty()) {
-      // init from tensor.empty: its contents are unspecified; keep what the result buffer holds
-      fallback = "((" + T + " *)" + outPtr[0] + ")[t]";
-    }
+    // out-of-range positions keep the init: the outs argument when it is one,
+    // else (a tensor.empty, whose contents are unspecified) the result buffer
+    const std::string fallback = init->argIdx >= 0 ? "((const " + T + " *)p" + std::to_string(init->argIdx) + ")[t]"
+                                                   : "((" + T + " *)" + outPtr[0] + ")[t]";
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
       << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
       << "  if (t >= " << N << "ll) return;\n"
