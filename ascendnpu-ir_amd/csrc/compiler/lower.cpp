@@ -1969,6 +1969,10 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
   }
   for (auto &s : outPtr) if (s.empty()) unsupported(op, "a result the group does not return");
   auto inPtr = [&](size_t i) { return "p" + std::to_string(op->operands.at(i)->argIdx); };
+  for (const Value *v : op->operands)
+    if (v->type.tensor && v->type.shape.empty()) unsupported(op, "rank-0 operand");
+  for (const Value *v : op->ins)
+    if (v->type.tensor && v->type.shape.empty()) unsupported(op, "rank-0 operand");
   auto numel = [](const std::vector<int64_t> &sh) { int64_t n = 1; for (auto d : sh) n *= d; return n; };
   const std::string n = op->name.substr(std::string("hfusion.").size());
   KernelPlan p;
@@ -2237,18 +2241,42 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
       }
       f.ops.erase(f.ops.begin() + i);
     }
-    // destination-style hivm ops on memrefs (no SSA result): the written
-    // `outs` argument becomes the group's result, tied to that argument
-    for (Op *op : f.ops)
-      if (op->name.rfind("hivm.hir.", 0) == 0 && op->results.empty() && !op->outs.empty()) {
-        Value *r = m.newValue();
-        r->type = op->outs[0]->type;
-        r->def = op;
-        r->resultIdx = 0;
-        r->name = op->outs[0]->name + "#written";
-        op->results.push_back(r);
-        if (f.returns.empty()) f.returns.push_back(r);
+    // destination-style ops on memrefs (no SSA result): each write gives the
+    // `outs` buffer a new value, later reads of the buffer see the latest
+    // value, and with no `return` operands the last value of every written
+    // argument is a group result tied to that argument
+    {
+      std::map<Value *, Value *> latest; // buffer (func argument) -> its current value
+      std::vector<Value *> written;      // written arguments in first-write order
+      const bool noReturns = f.returns.empty();
+      for (Op *op : f.ops) {
+        for (auto *lst : {&op->ins, &op->operands})
+          for (Value *&v : *lst) {
+            auto it = latest.find(v);
+            if (it == latest.end()) continue;
+            auto &u = v->users;
+            u.erase(std::remove(u.begin(), u.end(), op), u.end());
+            v = it->second;
+            v->users.push_back(op);
+          }
+        if (!op->results.empty() || op->outs.empty()) continue;
+        for (size_t j = 0; j < op->outs.size(); ++j) {
+          Value *buf = op->outs[j];
+          Value *r = m.newValue();
+          r->type = buf->type;
+          r->def = op;
+          r->resultIdx = (int)j;
+          r->name = buf->name + "#written";
+          op->results.push_back(r);
+          if (buf->argIdx >= 0) {
+            if (!latest.count(buf)) written.push_back(buf);
+            latest[buf] = r;
+          }
+        }
       }
+      if (noReturns)
+        for (Value *b : written) f.returns.push_back(latest[b]);
+    }
     describeBuffers(A);
     std::string kname = "hf_" + f.name;
     KernelPlan p;

@@ -335,6 +335,21 @@ MISC_EXTRA = (["flip_f32", "flip_bf16"] + [f"{op}_{e}" for op in ("mulext", "mul
               + ["arange_i32", "arange_f32"])
 
 
+def memref_chain(n=4096):
+    """Destination-style ops on memrefs with no SSA results: the second op
+    reads the buffer the first one wrote; both written buffers are results."""
+    M = f"memref<{n}xf32>"
+    return f"""module {{
+  func.func @memref_chain(%x: {M}, %tmp: {M}, %y: {M})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%x : {M}) outs(%tmp : {M})
+    linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%tmp, %x : {M}, {M}) outs(%y : {M})
+    return
+  }}
+}}
+"""
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -540,6 +555,7 @@ def entries():
     e["scan_ops"] = scan_ops()
     e["misc_ops"] = misc_ops()
     e["gather_ops"] = gather_ops()
+    e["memref_chain"] = memref_chain(4096)
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

@@ -603,6 +603,14 @@ class Interp:
                 continue
             if s.startswith("annotation.mark"):
                 continue
+            if not s.startswith("%") and "outs(" in s:
+                # a destination-style op on a memref: it writes its outs
+                # buffer, which later statements read under the same name
+                buf = _operands(_group(s.split(None, 1)[1], "outs"))[0][0]
+                self._exec(f"{buf} = {s}", env)
+                if buf not in self.written:
+                    self.written.append(buf)
+                continue
             self._exec(s, env)
         raise ValueError("function without return")
 

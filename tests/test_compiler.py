@@ -194,6 +194,10 @@ def test_hivm_matmul_reference_form_lowers(tmp_path):
     ("""func.func @f(%a: tensor<4xf32>) -> tensor<4xf32> {
   return %b : tensor<4xf32>
 }""", -1, "undefined value"),
+    ("""func.func @deinterleave_rank0(%arg0: tensor<f32>) -> tensor<f32> {
+  %res = hfusion.deinterleave %arg0 channel<0> : tensor<f32> -> tensor<f32>
+  return %res : tensor<f32>
+}""", -2, "rank-0"),
 ])
 def test_compile_errors(ir, code, msg, tmp_path):
     rc, err, _ = emit(ir, tmp_path)
@@ -237,3 +241,21 @@ def test_host_api_validates_before_launch():
         g(torch.zeros(1001), torch.zeros(1001))
     with pytest.raises(TypeError):  # host tensors are refused
         g(torch.zeros(1001), torch.zeros(1001), torch.zeros(1001))
+
+
+def test_memref_form_groups_compile(tmp_path):
+    """Destination-style ops on memrefs with a bare `return` (no SSA results):
+    each written buffer becomes a result tied to its argument, and a later
+    read of a buffer sees the value written to it."""
+    ir = """func.func @f(%src : memref<6xf32>, %dst : memref<6xi32>) {
+  hfusion.bitcast ins(%src : memref<6xf32>) outs(%dst : memref<6xi32>)
+  return
+}"""
+    rc, err, prefix = emit(ir, tmp_path)
+    assert rc == 0, err
+    man = open(prefix + ".manifest").read()
+    assert "result 0 1 i32 1 6" in man, man
+    rc, err, prefix = emit(hf.catalog.get("memref_chain"), tmp_path, "chain")
+    assert rc == 0, err
+    man = open(prefix + ".manifest").read()
+    assert "result 0 1 f32" in man and "result 1 2 f32" in man, man

@@ -560,3 +560,17 @@ def test_gather(gpu, name):
     out, = run_gpu("gather_ops", args, gpu, func=name)
     ref, = run_oracle("gather_ops", args, func=name)
     assert np.array_equal(out, ref), f"{int((out != ref).sum())} differ"
+
+
+def test_memref_chain(gpu):
+    """Memref-form group: sqrt into %tmp, then %tmp + %x into %y; both written
+    buffers come back, bit-exact."""
+    note("memref_chain")
+    x = np.abs(I.normal_f32(I.SEED_BASE + 95, (4096,)))
+    args = [x, np.zeros(4096, np.float32), np.zeros(4096, np.float32)]
+    outs = run_gpu("memref_chain", args, gpu)
+    refs = run_oracle("memref_chain", args)
+    assert len(outs) == 2 and len(refs) == 2
+    for o, r in zip(outs, refs):
+        assert np.array_equal(o, r)
+    assert np.array_equal(refs[1], np.sqrt(x) + x)
