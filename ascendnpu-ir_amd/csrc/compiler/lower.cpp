@@ -358,12 +358,14 @@ std::string intBinaryFn(const std::string &fn, const std::string &a, const std::
   unsupported(op, "binary function '" + fn + "' on integers");
 }
 
-// Applies a float-domain expression builder in element type U (f16/bf16 are
-// computed in f32 and rounded back, as LLVM promotes them on the CPU).
+// Applies a float-domain expression builder in element type U (f16/bf16/fp8
+// are computed in f32 and rounded back, as LLVM promotes them on the CPU).
 std::string inFloatType(Elem U, const std::vector<std::string> &xs,
                         const std::function<std::string(const std::vector<std::string> &)> &f32fn) {
   if (U == Elem::F32) return f32fn(xs);
-  if (U == Elem::BF16 || U == Elem::F16) {
+  // bf16, f16 and the fp8 formats compute in f32 and round back to nearest
+  // even after each op, as the CPU lowering's float emulation does
+  if (U == Elem::BF16 || U == Elem::F16 || U == Elem::F8E4M3FN || U == Elem::F8E5M2) {
     std::vector<std::string> ys;
     for (auto &x : xs) ys.push_back(castExpr(x, U, Elem::F32, false));
     return castExpr(f32fn(ys), Elem::F32, U, false);
@@ -2217,6 +2219,53 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
   return p;
 }
 
+// A group of elementwise ops whose tensors are reshaped views of each other
+// (tensor.expand_shape / collapse_shape of row-major data) and all hold the
+// same number of elements: every tensor shares the flat element index, so the
+// group runs over one flat dimension and the reshapes vanish.  The buffer
+// descriptors (taken before this) keep the arguments' own shapes.
+static void flattenReshapeGroup(Func &f) {
+  bool anyReshape = false;
+  int64_t n = -1;
+  auto numelOf = [](const Type &t) { int64_t k = 1; for (auto d : t.shape) k *= d; return k; };
+  auto same = [&](const Value *v) {
+    if (!v->type.tensor) return true;
+    int64_t k = numelOf(v->type);
+    if (n < 0) n = k;
+    return k == n;
+  };
+  for (const Op *op : f.ops) {
+    const std::string &nm = op->name;
+    const bool reshape = nm == "tensor.expand_shape" || nm == "tensor.collapse_shape";
+    anyReshape |= reshape;
+    if (!reshape && !isElementwiseOp(op) && nm != "tensor.empty" && nm != "arith.constant" && nm != "linalg.fill")
+      return;
+    for (auto *lst : {&op->ins, &op->outs, &op->operands, &op->results})
+      for (const Value *v : *lst) if (!same(v)) return;
+  }
+  for (const Value *v : f.args) if (!same(v)) return;
+  if (!anyReshape || n <= 0) return;
+  for (size_t i = 0; i < f.ops.size();) {
+    Op *op = f.ops[i];
+    if (op->name != "tensor.expand_shape" && op->name != "tensor.collapse_shape") { ++i; continue; }
+    Value *src = op->operands.at(0), *dst = op->results.at(0);
+    auto &su = src->users;
+    su.erase(std::remove(su.begin(), su.end(), op), su.end());
+    for (Op *u : dst->users) {
+      for (auto *lst : {&u->ins, &u->outs, &u->operands})
+        for (Value *&v : *lst) if (v == dst) v = src;
+      su.push_back(u);
+    }
+    for (Value *&r : f.returns) if (r == dst) r = src;
+    f.ops.erase(f.ops.begin() + i);
+  }
+  auto flat = [&](Value *v) { if (v->type.tensor) v->type.shape = {n}; };
+  for (Value *v : f.args) flat(v);
+  for (Op *op : f.ops)
+    for (auto *lst : {&op->ins, &op->outs, &op->operands, &op->results})
+      for (Value *v : *lst) flat(v);
+}
+
 std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
   std::vector<KernelPlan> out;
   bool anyEntry = false;
@@ -2290,6 +2339,7 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     } else if (kind == "REDUCE_WITH_INDEX") {
       p = lowerReduceWithIndex(A, kname);
     } else {
+      flattenReshapeGroup(f);
       A.D = largestShape(f, {});
       if (A.D.empty()) throw CompileError("group @" + f.name + " has no tensor to iterate over");
       inferMaps(A, {});

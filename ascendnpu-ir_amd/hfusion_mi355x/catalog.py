@@ -350,6 +350,27 @@ def memref_chain(n=4096):
 """
 
 
+def reshape_chain():
+    """Elementwise ops joined by expand_shape / collapse_shape views: the
+    group runs over the shared flat index."""
+    A, B3 = _T([128, 256], "f32"), _T([32, 4, 256], "f32")
+    return f"""module {{
+  func.func @reshape_chain(%a: {A}, %b: {A}, %c: {B3}) -> {A}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e0 = tensor.empty() : {A}
+    %s = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%a, %b : {A}, {A}) outs(%e0 : {A}) -> {A}
+    %x = tensor.expand_shape %s [[0, 1], [2]] output_shape [32, 4, 256] : {A} into {B3}
+    %e1 = tensor.empty() : {B3}
+    %m = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%x, %c : {B3}, {B3}) outs(%e1 : {B3}) -> {B3}
+    %y = tensor.collapse_shape %m [[0, 1], [2]] : {B3} into {A}
+    %e2 = tensor.empty() : {A}
+    %r = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%y : {A}) outs(%e2 : {A}) -> {A}
+    return %r : {A}
+  }}
+}}
+"""
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -556,6 +577,7 @@ def entries():
     e["misc_ops"] = misc_ops()
     e["gather_ops"] = gather_ops()
     e["memref_chain"] = memref_chain(4096)
+    e["reshape_chain"] = reshape_chain()
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

@@ -698,6 +698,12 @@ class Interp:
             names = re.findall(r"%[\w.$-]+", rest)
             env[res] = T(np.int64(env[names[0]].a.shape[int(env[names[1]].a)]), "index")
             return
+        if op in ("tensor.expand_shape", "tensor.collapse_shape"):
+            # a row-major view with the result type after `into`
+            src = re.findall(r"%[\w.$#-]+", rest)[0]
+            shape, elem = parse_type(rest.rsplit("into", 1)[1])
+            env[res] = T(np.ascontiguousarray(env[src].a).reshape(shape), elem)
+            return
         if op.startswith("arith.") and "ins(" not in rest:
             self._scalar_arith(res, op, rest, env)
             return

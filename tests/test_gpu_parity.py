@@ -574,3 +574,15 @@ def test_memref_chain(gpu):
     for o, r in zip(outs, refs):
         assert np.array_equal(o, r)
     assert np.array_equal(refs[1], np.sqrt(x) + x)
+
+
+def test_reshape_chain(gpu):
+    """add -> expand_shape -> mul -> collapse_shape -> abs in one group: the
+    reshapes are views of the flat index; bit-exact."""
+    note("reshape_chain")
+    s = I.SEED_BASE + 97
+    args = [I.normal_f32(s, (128, 256)), I.normal_f32(s + 1, (128, 256)), I.normal_f32(s + 2, (32, 4, 256))]
+    out, = run_gpu("reshape_chain", args, gpu)
+    ref, = run_oracle("reshape_chain", args)
+    assert np.array_equal(out, ref)
+    assert np.array_equal(ref, np.abs(((args[0] + args[1]).reshape(32, 4, 256) * args[2]).reshape(128, 256)))
