@@ -36,7 +36,20 @@
 
 static bool startsWith(const std::string &s, const char *p) { return s.rfind(p, 0) == 0; }
 
+static int compileMain(int argc, char **argv);
+
+// Any exception escaping the compiler or the runner is reported the way the
+// reference tool reports errors: `[ERROR] ...` on stderr and EXIT_FAILURE.
 int main(int argc, char **argv) {
+  try {
+    return compileMain(argc, argv);
+  } catch (const std::exception &e) {
+    std::fprintf(stderr, "[ERROR] internal error: %s\n", e.what());
+    return EXIT_FAILURE;
+  }
+}
+
+static int compileMain(int argc, char **argv) {
   std::string input, output, target = "mi355x";
   std::string opts;
   int runnerFlags = 0;

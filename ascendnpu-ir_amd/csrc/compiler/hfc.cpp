@@ -95,6 +95,9 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
   } catch (const hfc::CompileError &e) {
     setErr(err, errlen, std::string("parse error: ") + e.what());
     return HFC_ERR_PARSE;
+  } catch (const std::exception &e) {
+    setErr(err, errlen, std::string("parse error (internal): ") + e.what());
+    return HFC_ERR_PARSE;
   }
   // fusion front-end: functions that are not one group yet are split into
   // outlined groups plus a launch program
@@ -119,6 +122,9 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
   } catch (const hfc::CompileError &e) {
     setErr(err, errlen, std::string("fusion error: ") + e.what());
     return HFC_ERR_LOWER;
+  } catch (const std::exception &e) {
+    setErr(err, errlen, std::string("fusion error (internal): ") + e.what());
+    return HFC_ERR_LOWER;
   }
   std::vector<hfc::KernelPlan> plans;
   try {
@@ -127,6 +133,9 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
     plans = hfc::lowerModule(*mod, lo);
   } catch (const hfc::CompileError &e) {
     setErr(err, errlen, std::string("lowering error: ") + e.what());
+    return HFC_ERR_LOWER;
+  } catch (const std::exception &e) {
+    setErr(err, errlen, std::string("lowering error (internal): ") + e.what());
     return HFC_ERR_LOWER;
   }
   std::string prefix = outPrefix;

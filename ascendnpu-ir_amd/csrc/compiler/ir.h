@@ -99,6 +99,7 @@ struct Func {
 
 struct Module {
   std::string source; // the text the module was read from
+  std::map<std::string, std::string> aliases; // `#map = affine_map<...>` -> "affine_map<...>"
   std::vector<std::unique_ptr<Func>> funcs;
   std::vector<std::unique_ptr<Value>> values;
   std::vector<std::unique_ptr<Op>> ops;

@@ -398,7 +398,70 @@ int roundModeOf(const std::string &s) {
   throw CompileError("unknown round_mode '" + s + "'");
 }
 
+// ---- linalg.generic (elementwise subset) ---------------------------------
+// A map `affine_map<(d0, d1) -> (d1)>` as its result dims ({1}); false for
+// results that are not plain dims.
+bool parseAffineMap(const std::string &txt, int &nd, std::vector<int> &res) {
+  const size_t arrow = txt.find("->");
+  if (arrow == std::string::npos) return false;
+  const std::string lhs = txt.substr(0, arrow), rhs = txt.substr(arrow + 2);
+  nd = 0;
+  for (size_t i = 0; i + 1 < lhs.size(); ++i) if (lhs[i] == 'd' && std::isdigit((unsigned char)lhs[i + 1])) ++nd;
+  res.clear();
+  const size_t a = rhs.find('('), b = rhs.rfind(')');
+  if (a == std::string::npos || b == std::string::npos || b < a) return false;
+  std::stringstream ss(rhs.substr(a + 1, b - a - 1));
+  std::string tok;
+  while (std::getline(ss, tok, ',')) {
+    tok.erase(std::remove_if(tok.begin(), tok.end(), [](char c) { return std::isspace((unsigned char)c); }), tok.end());
+    if (tok.empty()) continue;
+    if (tok.size() < 2 || tok[0] != 'd') return false;
+    for (size_t i = 1; i < tok.size(); ++i) if (!std::isdigit((unsigned char)tok[i])) return false;
+    res.push_back(std::stoi(tok.substr(1)));
+  }
+  return true;
+}
+
+// indexing maps of a linalg.generic, one per ins then outs operand
+bool genericMaps(const Op *op, std::vector<std::vector<int>> &maps, int &nd) {
+  const std::string s = op->attr("indexing_maps");
+  maps.clear();
+  size_t q = 0;
+  while ((q = s.find("affine_map<", q)) != std::string::npos) {
+    const size_t arrow = s.find("->", q);
+    if (arrow == std::string::npos) return false;
+    size_t e = s.find('>', arrow + 2);
+    if (e == std::string::npos) return false;
+    std::vector<int> r;
+    int n;
+    if (!parseAffineMap(s.substr(q + 11, e - q - 11), n, r)) return false;
+    nd = n;
+    maps.push_back(r);
+    q = e;
+  }
+  return maps.size() == op->ins.size() + op->outs.size();
+}
+
+// a linalg.generic the elementwise emitters take: parallel loops only, every
+// output indexed by the identity map, inputs by plain-dim projections in
+// increasing order (broadcasts; a transposed input is rejected)
+bool genericIsElementwise(const Op *op) {
+  if (op->name != "linalg.generic" || op->attr("region").empty() || op->outs.size() != 1) return false;
+  if (op->attr("iterator_types").find("reduction") != std::string::npos) return false;
+  std::vector<std::vector<int>> maps;
+  int nd = 0;
+  if (!genericMaps(op, maps, nd)) return false;
+  const auto &om = maps.back();
+  if ((int)om.size() != nd) return false;
+  for (int i = 0; i < nd; ++i) if (om[i] != i) return false;
+  // inputs: dims in increasing order (broadcasts, no transposes)
+  for (size_t i = 0; i + 1 < maps.size(); ++i)
+    for (size_t k = 1; k < maps[i].size(); ++k) if (maps[i][k] <= maps[i][k - 1]) return false;
+  return true;
+}
+
 bool isElementwiseOp(const Op *op) {
+  if (op->name == "linalg.generic") return genericIsElementwise(op);
   static const std::set<std::string> s = {
       "hfusion.elemwise_unary", "hfusion.elemwise_binary", "hfusion.elemwise_ternary",
       "linalg.elemwise_unary",  "linalg.elemwise_binary",  "hfusion.compare",
@@ -421,9 +484,176 @@ std::string bitcastExpr(const std::string &x, Elem from, Elem to, const Op *op) 
   return "__builtin_bit_cast(" + ctype(to) + ", (" + ctype(from) + ")(" + x + "))";
 }
 
+// Element expression of a linalg.generic's result: its region's scalar
+// arith / math statements, each translated with the same helpers as the
+// named ops (f16/bf16/fp8 computed in f32 and rounded back per op).
+// `a`/`at` hold the ins operands, then the captured outer values in the
+// order of attrs["captures"].
+std::string genericExpr(const Op *op, const std::vector<std::string> &a, const std::vector<Elem> &at, Elem U) {
+  const std::string body = op->attr("region");
+  const size_t lp = body.find('('), rp = body.find(')');
+  if (lp == std::string::npos || rp == std::string::npos) unsupported(op, "linalg.generic region header");
+  struct V { std::string e; Elem t; };
+  std::map<std::string, V> env;
+  {
+    std::stringstream ss(body.substr(lp + 1, rp - lp - 1));
+    std::string arg;
+    size_t i = 0;
+    while (std::getline(ss, arg, ',')) {
+      const size_t c = arg.find(':');
+      if (c == std::string::npos) continue;
+      std::string nm = arg.substr(0, c), ty = arg.substr(c + 1);
+      nm.erase(std::remove_if(nm.begin(), nm.end(), ::isspace), nm.end());
+      ty.erase(std::remove_if(ty.begin(), ty.end(), ::isspace), ty.end());
+      if (i < op->ins.size()) env[nm] = {a.at(i), parseElem(ty)};
+      else env[nm] = {"", Elem::None}; // the output's block argument: not readable here
+      ++i;
+    }
+  }
+  {
+    std::stringstream ss(op->attr("captures"));
+    std::string nm;
+    size_t j = op->ins.size();
+    while (ss >> nm) { env[nm] = {a.at(j), at.at(j)}; ++j; }
+  }
+  auto get = [&](const std::string &nm) -> V {
+    auto it = env.find(nm);
+    if (it == env.end()) unsupported(op, "region value " + nm);
+    if (it->second.t == Elem::None) unsupported(op, "a region that reads its output");
+    return it->second;
+  };
+  static const std::map<std::string, std::string> fbin = {
+      {"arith.addf", "add"}, {"arith.subf", "sub"}, {"arith.mulf", "mul"}, {"arith.divf", "div"},
+      {"arith.maximumf", "maxf"}, {"arith.minimumf", "minf"}, {"arith.maxnumf", "maxnumf"}, {"arith.minnumf", "minnumf"},
+      {"arith.remf", "mod"}, {"math.powf", "powf"}, {"math.atan2", "atan2"}, {"math.copysign", "copysign"}};
+  static const std::map<std::string, std::string> fun = {
+      {"arith.negf", "negf"}, {"math.exp", "exp"}, {"math.exp2", "exp2"}, {"math.log", "log"}, {"math.log2", "log2"},
+      {"math.log10", "log10"}, {"math.log1p", "log1p"}, {"math.expm1", "expm1"}, {"math.sqrt", "sqrt"},
+      {"math.rsqrt", "rsqrt"}, {"math.tanh", "tanh"}, {"math.sin", "sin"}, {"math.cos", "cos"}, {"math.tan", "tan"},
+      {"math.erf", "erf"}, {"math.absf", "abs"}, {"math.floor", "floor"}, {"math.ceil", "ceil"}, {"math.round", "round"},
+      {"math.roundeven", "nearbyint"}, {"math.trunc", "trunc"}, {"math.atan", "atan"}, {"math.asin", "asin"},
+      {"math.acos", "acos"}, {"math.sinh", "sinh"}, {"math.cosh", "cosh"}, {"math.asinh", "asinh"},
+      {"math.acosh", "acosh"}, {"math.atanh", "atanh"}};
+  static const std::map<std::string, std::string> ibin = {
+      {"arith.addi", "add"}, {"arith.subi", "sub"}, {"arith.muli", "mul"}, {"arith.divsi", "div"}, {"arith.remsi", "mod"},
+      {"arith.remui", "modui"}, {"arith.andi", "vand"}, {"arith.ori", "vor"}, {"arith.xori", "vxor"},
+      {"arith.shli", "shli"}, {"arith.shrsi", "shrsi"}, {"arith.shrui", "shrui"}, {"arith.maxsi", "max_signed"},
+      {"arith.minsi", "min_signed"}, {"arith.maxui", "max_unsigned"}, {"arith.minui", "min_unsigned"},
+      {"arith.ceildivsi", "ceildivsi"}, {"arith.floordivsi", "floordivsi"}, {"arith.ceildivui", "ceildivui"},
+      {"math.ipowi", "powi"}};
+  std::stringstream lines(body.substr(body.find(':', rp) == std::string::npos ? rp + 1 : body.find(':', rp) + 1));
+  std::string line;
+  while (std::getline(lines, line)) {
+    const size_t b0 = line.find_first_not_of(" \t");
+    if (b0 == std::string::npos) continue;
+    line = line.substr(b0);
+    // strip `fastmath<...>` and attribute dictionaries
+    for (size_t q; (q = line.find("fastmath<")) != std::string::npos;) line.erase(q, line.find('>', q) - q + 1);
+    for (size_t q; (q = line.find('{')) != std::string::npos;) line.erase(q, line.find('}', q) - q + 1);
+    const size_t colon = line.rfind(':');
+    std::string head = colon == std::string::npos ? line : line.substr(0, colon);
+    std::string tail = colon == std::string::npos ? "" : line.substr(colon + 1);
+    auto trim = [](std::string x) {
+      x.erase(0, x.find_first_not_of(" \t"));
+      x.erase(x.find_last_not_of(" \t") + 1);
+      return x;
+    };
+    std::string toTy;
+    if (tail.find(" to ") != std::string::npos) {
+      toTy = trim(tail.substr(tail.find(" to ") + 4));
+      tail = tail.substr(0, tail.find(" to "));
+    }
+    tail = trim(tail);
+    std::vector<std::string> names;
+    for (size_t q = 0; (q = head.find('%', q)) != std::string::npos;) {
+      size_t e = q + 1;
+      while (e < head.size() && (std::isalnum((unsigned char)head[e]) || head[e] == '_' || head[e] == '.' || head[e] == '#')) ++e;
+      names.push_back(head.substr(q, e - q));
+      q = e;
+    }
+    if (line.rfind("linalg.yield", 0) == 0) {
+      if (names.size() != 1) unsupported(op, "linalg.yield of other than one value");
+      V y = get(names[0]);
+      return castExpr(y.e, y.t, U, false);
+    }
+    const size_t eq = head.find('=');
+    if (eq == std::string::npos || names.empty()) unsupported(op, "region statement '" + line + "'");
+    const std::string res = names[0];
+    std::string rest = trim(head.substr(eq + 1));
+    const std::string opn = rest.substr(0, rest.find_first_of(" \t"));
+    rest = trim(rest.substr(opn.size()));
+    std::vector<V> xs;
+    for (size_t i = 1; i < names.size(); ++i) xs.push_back(get(names[i]));
+    const Elem ty = tail.empty() ? (xs.empty() ? Elem::None : xs[0].t) : parseElem(tail);
+    V out;
+    if (opn == "arith.constant") {
+      Value tmp;
+      tmp.type.elem = ty;
+      std::string lit = rest;
+      if (!parseLiteral(lit, ty, &tmp)) unsupported(op, "region constant '" + lit + "'");
+      out = {constExpr(&tmp, ty), ty};
+    } else if (fbin.count(opn)) {
+      out = {inFloatType(ty, {xs.at(0).e, xs.at(1).e}, [&](const std::vector<std::string> &y) {
+               return f32BinaryFn(fbin.at(opn), y[0], y[1], op); }), ty};
+    } else if (fun.count(opn)) {
+      out = {inFloatType(ty, {xs.at(0).e}, [&](const std::vector<std::string> &y) { return f32UnaryFn(fun.at(opn), y[0], op); }), ty};
+    } else if (opn == "math.fma") {
+      out = {inFloatType(ty, {xs.at(0).e, xs.at(1).e, xs.at(2).e}, [&](const std::vector<std::string> &y) {
+               return "fmaf(" + y[0] + ", " + y[1] + ", " + y[2] + ")"; }), ty};
+    } else if (ibin.count(opn)) {
+      out = {intBinaryFn(ibin.at(opn), xs.at(0).e, xs.at(1).e, ty, op), ty};
+    } else if (opn == "arith.select") {
+      const Elem vt = xs.at(1).t;
+      out = {"(" + xs.at(0).e + " ? " + xs.at(1).e + " : " + xs.at(2).e + ")", vt};
+    } else if (opn == "arith.cmpf" || opn == "arith.cmpi") {
+      const std::string pred = trim(rest.substr(0, rest.find(',')));
+      const Elem ot = xs.at(0).t;
+      std::string e;
+      if (opn == "arith.cmpf") {
+        const std::string x = castExpr(xs[0].e, ot, Elem::F32, false), y = castExpr(xs[1].e, ot, Elem::F32, false);
+        static const std::map<std::string, std::string> P = {
+            {"oeq", "(@X == @Y)"}, {"one", "(@X < @Y || @X > @Y)"}, {"olt", "(@X < @Y)"}, {"ole", "(@X <= @Y)"},
+            {"ogt", "(@X > @Y)"}, {"oge", "(@X >= @Y)"}, {"ord", "(@X == @X && @Y == @Y)"},
+            {"ueq", "!(@X < @Y || @X > @Y)"}, {"une", "!(@X == @Y)"}, {"ult", "!(@X >= @Y)"}, {"ule", "!(@X > @Y)"},
+            {"ugt", "!(@X <= @Y)"}, {"uge", "!(@X < @Y)"}, {"uno", "(@X != @X || @Y != @Y)"}, {"true", "true"},
+            {"false", "false"}};
+        if (!P.count(pred)) unsupported(op, "cmpf predicate " + pred);
+        e = P.at(pred);
+        for (size_t q; (q = e.find("@X")) != std::string::npos;) e.replace(q, 2, "(" + x + ")");
+        for (size_t q; (q = e.find("@Y")) != std::string::npos;) e.replace(q, 2, "(" + y + ")");
+      } else {
+        const std::string x = "(int64_t)(" + xs[0].e + ")", y = "(int64_t)(" + xs[1].e + ")";
+        const int bits = elemBits(ot == Elem::Index ? Elem::I64 : ot);
+        const std::string mask = bits >= 64 ? "" : " & " + std::to_string((1ull << bits) - 1) + "ull";
+        const std::string UX = "((uint64_t)(" + x + ")" + mask + ")", UY = "((uint64_t)(" + y + ")" + mask + ")";
+        static const std::map<std::string, std::string> P = {
+            {"eq", "=="}, {"ne", "!="}, {"slt", "<"}, {"sle", "<="}, {"sgt", ">"}, {"sge", ">="},
+            {"ult", "<"}, {"ule", "<="}, {"ugt", ">"}, {"uge", ">="}};
+        if (!P.count(pred)) unsupported(op, "cmpi predicate " + pred);
+        e = pred[0] == 'u' ? "(" + UX + " " + P.at(pred) + " " + UY + ")" : "(" + x + " " + P.at(pred) + " " + y + ")";
+      }
+      out = {"(bool)" + e, Elem::I1};
+    } else if (opn == "arith.extf" || opn == "arith.truncf" || opn == "arith.sitofp" || opn == "arith.uitofp" ||
+               opn == "arith.fptosi" || opn == "arith.fptoui" || opn == "arith.extsi" || opn == "arith.extui" ||
+               opn == "arith.trunci" || opn == "arith.index_cast" || opn == "arith.index_castui") {
+      const Elem to = parseElem(toTy);
+      const bool uns = opn == "arith.uitofp" || opn == "arith.fptoui" || opn == "arith.extui" || opn == "arith.index_castui";
+      out = {castExpr(xs.at(0).e, xs.at(0).t, to, uns), to};
+    } else if (opn == "arith.bitcast") {
+      const Elem to = parseElem(toTy);
+      out = {bitcastExpr(xs.at(0).e, xs.at(0).t, to, op), to};
+    } else {
+      unsupported(op, "region op '" + opn + "'");
+    }
+    env[res] = out;
+  }
+  unsupported(op, "linalg.generic region without linalg.yield");
+}
+
 // Element expression of an elementwise op's result from operand expressions.
 std::string elementExpr(const Op *op, const std::vector<std::string> &a, const std::vector<Elem> &at, Elem U) {
   const std::string &n = op->name;
+  if (n == "linalg.generic") return genericExpr(op, a, at, U);
   bool uns = op->attr("cast") == "cast_unsigned";
   bool bits = op->attr("cast") == "bitcast";
   auto named = [&](const std::string &fn, int arity) -> std::string {
@@ -693,6 +923,25 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
       if (n == "linalg.reduce" || n == "hfusion.reduce_with_index") {
         for (auto *o : op->outs) changed |= setMap(o, minus(op->dims), op);
         for (auto *o : op->results) changed |= setMap(o, minus(op->dims), op);
+        continue;
+      }
+      if (n == "linalg.generic" && genericIsElementwise(op)) {
+        std::vector<std::vector<int>> maps;
+        int nd = 0;
+        genericMaps(op, maps, nd);
+        const Value *o = op->results.empty() ? op->outs[0] : op->results[0];
+        const std::vector<int> *known = A.map.count(o) ? &A.map[o] : (A.map.count(op->outs[0]) ? &A.map[op->outs[0]] : nullptr);
+        if (known) {
+          std::vector<int> mo = *known;
+          changed |= setMap(op->outs[0], mo, op);
+          for (auto *v : op->results) changed |= setMap(v, mo, op);
+          for (size_t i = 0; i < op->ins.size(); ++i) {
+            if (!op->ins[i]->type.tensor) continue;
+            std::vector<int> mi;
+            for (int d : maps[i]) mi.push_back(mo.at(d));
+            changed |= setMap(op->ins[i], mi, op);
+          }
+        }
         continue;
       }
       if (n == "linalg.fill") {
@@ -2238,7 +2487,9 @@ static void flattenReshapeGroup(Func &f) {
     const std::string &nm = op->name;
     const bool reshape = nm == "tensor.expand_shape" || nm == "tensor.collapse_shape";
     anyReshape |= reshape;
-    if (!reshape && !isElementwiseOp(op) && nm != "tensor.empty" && nm != "arith.constant" && nm != "linalg.fill")
+    // (a linalg.generic's maps name the dims of its own rank: not flattened)
+    if (!reshape && (!isElementwiseOp(op) || nm == "linalg.generic") && nm != "tensor.empty" &&
+        nm != "arith.constant" && nm != "linalg.fill")
       return;
     for (auto *lst : {&op->ins, &op->outs, &op->operands, &op->results})
       for (const Value *v : *lst) if (!same(v)) return;

@@ -253,13 +253,17 @@ std::string normAttr(const std::string &v) {
 
 class Parser {
 public:
-  Parser(const std::string &text) : toks_(lex(text)) {}
+  Parser(const std::string &text) : toks_(lex(text)), src_(text) {}
 
   std::unique_ptr<Module> run() {
     mod_.reset(new Module());
     while (peek().kind != Tok::End) {
       if (peek().kind == Tok::Ident && peek().text == "func.func") {
         parseFunc();
+      } else if (peek().kind == Tok::Hash && isP(peek(1), "=") && peek(2).kind == Tok::Raw) {
+        // attribute alias, e.g. `#map = affine_map<(d0, d1) -> (d1)>`
+        mod_->aliases[peek().text] = peek(2).text;
+        pos_ += 3;
       } else {
         ++pos_;
       }
@@ -270,6 +274,7 @@ public:
 
 private:
   std::vector<Token> toks_;
+  std::string src_;
   size_t pos_ = 0;
   std::unique_ptr<Module> mod_;
   std::map<std::string, Value *> scope_;
@@ -553,6 +558,27 @@ private:
         sawRegionArgs = true;
         continue;
       }
+      // the body of a linalg.generic: kept as text (attrs["region"]); values
+      // of the enclosing function it reads become operands (attrs["captures"])
+      if (isP(t, "{") && peek(1).kind == Tok::Symbol && peek(1).text.rfind("^", 0) == 0) {
+        const size_t open = pos_;
+        int depth = 0;
+        std::string caps;
+        do {
+          const Token &r = peek();
+          if (r.kind == Tok::End) fail("unterminated region");
+          if (isP(r, "{")) ++depth;
+          if (isP(r, "}")) --depth;
+          if (r.kind == Tok::Value && scope_.count(r.text) && caps.find(" " + r.text + " ") == std::string::npos) {
+            caps += " " + r.text + " ";
+            op->operands.push_back(scope_[r.text]);
+          }
+          ++pos_;
+        } while (depth > 0);
+        op->attrs["region"] = src_.substr(toks_[open].end, toks_[pos_ - 1].off - toks_[open].end);
+        op->attrs["captures"] = caps;
+        continue;
+      }
       if (isP(t, "{")) {
         if (sawRegionArgs) {
           int depth = 0;
@@ -570,7 +596,19 @@ private:
         auto m = parseAttrDict();
         for (auto &kv : m) {
           if (kv.first.rfind("arith.", 0) == 0 && kv.second == "unit") op->combiner = kv.first;
-          op->attrs[kv.first] = kv.second;
+          std::string v = kv.second;
+          if (kv.first == "indexing_maps")
+            for (auto &al : mod_->aliases) {
+              // whole alias names only (#map vs #map1)
+              size_t q = 0;
+              while ((q = v.find(al.first, q)) != std::string::npos) {
+                size_t e = q + al.first.size();
+                if (e < v.size() && (std::isalnum((unsigned char)v[e]) || v[e] == '_')) { q = e; continue; }
+                v.replace(q, al.first.size(), al.second);
+                q += al.second.size();
+              }
+            }
+          op->attrs[kv.first] = v;
         }
         continue;
       }

@@ -371,6 +371,67 @@ def reshape_chain():
 """
 
 
+def generic_ops():
+    """linalg.generic with a region of scalar arith / math ops: a row bias
+    (map (d0, d1) -> (d1)), a column scale ((d0, d1) -> (d0)), a captured
+    scalar constant and scalar argument, compare/select, f16 <-> f32 casts
+    and integer ops."""
+    X, B, XT = _T([64, 1000], "f32"), _T([1000], "f32"), _T([64], "f32")
+    H, I = _T([64, 1000], "f16"), _T([64, 1000], "i32")
+    M = _T([64, 1000], "i1")
+    return f"""#id = affine_map<(d0, d1) -> (d0, d1)>
+#row = affine_map<(d0, d1) -> (d1)>
+#col = affine_map<(d0, d1) -> (d0)>
+module {{
+  func.func @generic_bias_act(%x: {X}, %b: {B}, %xt: {XT}, %s: f32, %o: {X}) -> {X}
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %c05 = arith.constant 5.000000e-01 : f32
+    %r = linalg.generic {{indexing_maps = [#id, #row, #col, #id], iterator_types = ["parallel", "parallel"]}}
+        ins(%x, %b, %xt : {X}, {B}, {XT}) outs(%o : {X}) {{
+    ^bb0(%in: f32, %bias: f32, %t: f32, %out: f32):
+      %0 = arith.addf %in, %bias : f32
+      %1 = arith.mulf %0, %c05 : f32
+      %2 = math.tanh %1 : f32
+      %3 = arith.cmpf ogt, %0, %t : f32
+      %4 = arith.mulf %t, %s : f32
+      %5 = arith.select %3, %2, %4 : f32
+      %c1 = arith.constant 1.000000e+00 : f32
+      %6 = arith.maximumf %5, %c1 : f32
+      %7 = math.exp %0 : f32
+      %8 = arith.divf %7, %6 : f32
+      linalg.yield %8 : f32
+    }} -> {X}
+    return %r : {X}
+  }}
+  func.func @generic_f16_int(%h: {H}, %i: {I}, %o: {H}, %m: {M}) -> ({H}, {M})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>], iterator_types = ["parallel", "parallel"]}}
+        ins(%h, %i : {H}, {I}) outs(%o : {H}) {{
+    ^bb0(%a: f16, %n: i32, %out: f16):
+      %0 = arith.extf %a : f16 to f32
+      %1 = arith.sitofp %n : i32 to f32
+      %2 = arith.mulf %0, %1 : f32
+      %3 = arith.truncf %2 : f32 to f16
+      %4 = arith.addf %3, %a : f16
+      linalg.yield %4 : f16
+    }} -> {H}
+    %q = linalg.generic {{indexing_maps = [#id, #id], iterator_types = ["parallel", "parallel"]}}
+        ins(%i : {I}) outs(%m : {M}) {{
+    ^bb0(%n: i32, %out: i1):
+      %c3 = arith.constant 3 : i32
+      %0 = arith.remsi %n, %c3 : i32
+      %1 = arith.shli %n, %c3 : i32
+      %2 = arith.xori %0, %1 : i32
+      %c0 = arith.constant 0 : i32
+      %3 = arith.cmpi slt, %2, %c0 : i32
+      linalg.yield %3 : i1
+    }} -> {M}
+    return %r, %q : {H}, {M}
+  }}
+}}
+"""
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -578,6 +639,7 @@ def entries():
     e["gather_ops"] = gather_ops()
     e["memref_chain"] = memref_chain(4096)
     e["reshape_chain"] = reshape_chain()
+    e["generic_ops"] = generic_ops()
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

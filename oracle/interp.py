@@ -563,6 +563,8 @@ class Interp:
     def __init__(self, text, cast_semantics="declared"):
         self.funcs = parse_funcs(text)
         self.cast_semantics = cast_semantics
+        # module-level attribute aliases (`#map = affine_map<...>`)
+        self.aliases = dict(re.findall(r"^\s*(#[\w.$-]+)\s*=\s*(affine_map<.*>)\s*$", text, re.M))
 
     def run(self, func=None, *inputs):
         """Runs group `func` with numpy inputs (one per argument; bf16/f16
@@ -729,6 +731,9 @@ class Interp:
             return
         ins, ins_t = _operands(_group(rest, "ins"))
         outs, outs_t = _operands(_group(rest, "outs"))
+        if op == "linalg.generic":
+            env[res] = self._generic(rest, ins, outs, env)
+            return
         if op == "hfusion.gather":
             # out[p] = src[p with axis coordinate index[p]] when the index is in
             # range, else init[p] (HFusionStructuredOps.td:222-238)
@@ -839,6 +844,131 @@ class Interp:
         else:
             raise NotImplementedError(f"op {op}")
         env[res] = T(np.ascontiguousarray(np.broadcast_to(r.a, shape)).astype(NP[U], copy=False), U)
+
+    def _generic(self, rest, ins, outs, env):
+        """linalg.generic with parallel loops, identity output map and
+        plain-dim input maps: the region's scalar ops evaluated over the loop
+        domain, each rounded to its type (the CPU loop body of
+        convert-linalg-to-loops)."""
+        head, region = rest.split("{", 1)[0], rest
+        attrs = rest[rest.index("{"):]
+        maps_txt = re.search(r"indexing_maps\s*=\s*\[(.*?)\]\s*,\s*iterator_types", attrs, re.S)
+        maps_src = maps_txt.group(1) if maps_txt else ""
+        for k in sorted(self.aliases, key=len, reverse=True):
+            maps_src = re.sub(re.escape(k) + r"(?![\w])", self.aliases[k], maps_src)
+        maps = []
+        for m in re.finditer(r"affine_map<\(([^)]*)\)\s*->\s*\(([^)]*)\)>", maps_src):
+            maps.append([int(d.strip()[1:]) for d in m.group(2).split(",") if d.strip()])
+        its = re.search(r"iterator_types\s*=\s*\[([^\]]*)\]", attrs).group(1)
+        if "reduction" in its:
+            raise NotImplementedError("linalg.generic with reductions")
+        o = env[outs[0]]
+        dom = np.asarray(o.a).shape
+        nd = len(dom)
+
+        def place(v, mp):
+            a = np.asarray(v.a)
+            if a.ndim == 0:
+                return T(np.broadcast_to(a, dom), v.elem)
+            order = np.argsort(mp)
+            a = a.transpose(order)
+            sm = sorted(mp)
+            full = [dom[d] if d in sm else 1 for d in range(nd)]
+            return T(np.broadcast_to(a.reshape(full), dom), v.elem)
+        body = region[region.index("^"):]
+        hdr = re.match(r"\^\w+\(([^)]*)\)\s*:", body)
+        bargs = [x.split(":")[0].strip() for x in hdr.group(1).split(",") if ":" in x]
+        local = {}
+        for i, nm in enumerate(bargs[:len(ins)]):
+            local[nm] = place(env[ins[i]], maps[i]) if np.ndim(env[ins[i]].a) else T(np.broadcast_to(env[ins[i]].a, dom), env[ins[i]].elem)
+
+        def get(nm):
+            if nm in local:
+                return local[nm]
+            v = env[nm]
+            return T(np.broadcast_to(v.a, dom), v.elem)
+        fb = {"arith.addf": "add", "arith.subf": "sub", "arith.mulf": "mul", "arith.divf": "div",
+              "arith.maximumf": "maxf", "arith.minimumf": "minf", "arith.maxnumf": "maxnumf",
+              "arith.minnumf": "minnumf", "arith.remf": "mod", "math.powf": "powf", "math.atan2": "atan2",
+              "math.copysign": "copysign"}
+        fu = {"arith.negf": "negf", "math.exp": "exp", "math.exp2": "exp2", "math.log": "log", "math.log2": "log2",
+              "math.log10": "log10", "math.log1p": "log1p", "math.expm1": "expm1", "math.sqrt": "sqrt",
+              "math.rsqrt": "rsqrt", "math.tanh": "tanh", "math.sin": "sin", "math.cos": "cos", "math.tan": "tan",
+              "math.erf": "erf", "math.absf": "abs", "math.floor": "floor", "math.ceil": "ceil", "math.round": "round",
+              "math.roundeven": "nearbyint", "math.trunc": "trunc", "math.atan": "atan", "math.asin": "asin",
+              "math.acos": "acos", "math.sinh": "sinh", "math.cosh": "cosh", "math.asinh": "asinh",
+              "math.acosh": "acosh", "math.atanh": "atanh"}
+        ib = {"arith.addi": "add", "arith.subi": "sub", "arith.muli": "mul", "arith.divsi": "div", "arith.remsi": "mod",
+              "arith.remui": "modui", "arith.andi": "vand", "arith.ori": "vor", "arith.xori": "vxor",
+              "arith.shli": "shli", "arith.shrsi": "shrsi", "arith.shrui": "shrui", "arith.maxsi": "max_signed",
+              "arith.minsi": "min_signed", "arith.maxui": "max_unsigned", "arith.minui": "min_unsigned",
+              "arith.ceildivsi": "ceildivsi", "arith.floordivsi": "floordivsi", "arith.ceildivui": "ceildivui",
+              "math.ipowi": "powi"}
+        stmts = re.split(r"\n|(?<=[\w>)\]])\s+(?=%[\w.$-]+\s*=|linalg\.yield)", body[hdr.end():])
+        for st in stmts:
+            st = re.sub(r"fastmath<[^>]*>", "", st).strip().rstrip("}").strip()
+            if not st:
+                continue
+            if st.startswith("linalg.yield"):
+                v = get(re.findall(r"%[\w.$-]+", st)[0])
+                return convert(v, o.elem) if v.elem != o.elem else T(np.ascontiguousarray(v.a), v.elem)
+            m = re.match(r"(%[\w.$-]+)\s*=\s*([\w.]+)\s*(.*)$", st)
+            r_, opn, tail = m.group(1), m.group(2), m.group(3)
+            lhs, _, ty = tail.rpartition(":")
+            to = None
+            if " to " in ty:
+                ty, to = ty.split(" to ")
+                to = to.strip()
+            ty = ty.strip()
+            names = re.findall(r"%[\w.$-]+", lhs)
+            xs = [get(n) for n in names]
+            if opn == "arith.constant":
+                lit = lhs.strip()
+                if lit in ("true", "false"):
+                    val = lit == "true"
+                elif lit.lower().startswith("0x") and ty in FLOATS:
+                    val = np.array([int(lit, 16)], np.uint32).view(np.float32)[0]
+                elif ty in FLOATS:
+                    val = float(lit)
+                else:
+                    val = int(lit, 0)
+                arr = from_f32(np.array(val, np.float32), ty) if ty in ("bf16", "f16") else np.array(val, NP[ty])
+                local[r_] = T(np.broadcast_to(arr, dom), ty)
+            elif opn in fb:
+                local[r_] = apply_binary(fb[opn], xs[0], xs[1], ty, dom)
+            elif opn in fu:
+                local[r_] = apply_unary(fu[opn], xs[0], ty)
+            elif opn in ib:
+                local[r_] = apply_binary(ib[opn], xs[0], xs[1], ty, dom)
+            elif opn == "arith.select":
+                local[r_] = T(np.where(np.asarray(xs[0].a), np.asarray(xs[1].a), np.asarray(xs[2].a)), xs[1].elem)
+            elif opn in ("arith.cmpf", "arith.cmpi"):
+                pred = lhs.strip().split(",")[0].strip()
+                if opn == "arith.cmpf":
+                    x, y = to_f32(xs[0]), to_f32(xs[1])
+                    with np.errstate(invalid="ignore"):
+                        res_ = {"oeq": x == y, "one": (x < y) | (x > y), "olt": x < y, "ole": x <= y, "ogt": x > y,
+                                "oge": x >= y, "ord": (x == x) & (y == y), "ueq": ~((x < y) | (x > y)), "une": ~(x == y),
+                                "ult": ~(x >= y), "ule": ~(x > y), "ugt": ~(x <= y), "uge": ~(x < y),
+                                "uno": (x != x) | (y != y)}[pred]
+                else:
+                    x, y = np.asarray(xs[0].a).astype(np.int64), np.asarray(xs[1].a).astype(np.int64)
+                    if pred[0] == "u":
+                        b = BITS.get(xs[0].elem, 64)
+                        msk = (1 << b) - 1 if b < 64 else -1
+                        x, y = (x & msk).astype(np.uint64), (y & msk).astype(np.uint64)
+                    res_ = {"eq": x == y, "ne": x != y, "slt": x < y, "sle": x <= y, "sgt": x > y, "sge": x >= y,
+                            "ult": x < y, "ule": x <= y, "ugt": x > y, "uge": x >= y}[pred]
+                local[r_] = T(np.asarray(res_, np.bool_), "i1")
+            elif opn == "arith.bitcast":
+                local[r_] = bitcast(T(np.ascontiguousarray(xs[0].a), xs[0].elem), to)
+            elif opn in ("arith.extf", "arith.truncf", "arith.sitofp", "arith.uitofp", "arith.fptosi", "arith.fptoui",
+                         "arith.extsi", "arith.extui", "arith.trunci", "arith.index_cast", "arith.index_castui"):
+                uns = opn in ("arith.uitofp", "arith.fptoui", "arith.extui", "arith.index_castui")
+                local[r_] = convert(T(np.ascontiguousarray(xs[0].a), xs[0].elem), to, uns)
+            else:
+                raise NotImplementedError(f"region op {opn}")
+        raise ValueError("linalg.generic region without linalg.yield")
 
     def _scalar_arith(self, res, op, rest, env):
         names = re.findall(r"%[\w.$-]+", rest)

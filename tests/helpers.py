@@ -358,3 +358,15 @@ def gather_inputs(name, seed=0x47415448):
     idx = rng.integers(-ss[ax] // 10, ss[ax] + ss[ax] // 10 + 1, ish).astype({"i32": np.int32, "i64": np.int64}[ie])
     init = np.full(ish, 0x7777 if se != "f32" else 7.0, src.dtype)
     return [src, idx, init]
+
+
+def generic_inputs(name, seed=0x47454E45):
+    """Seeded arguments of the groups of catalog module generic_ops."""
+    rng = np.random.default_rng(seed + sum(map(ord, name)))
+    if name == "generic_bias_act":
+        return [rng.normal(0, 1, (64, 1000)).astype(np.float32), rng.normal(0, 1, 1000).astype(np.float32),
+                rng.normal(0, 1, 64).astype(np.float32), np.float32(0.3), np.zeros((64, 1000), np.float32)]
+    h = rng.normal(0, 2, (64, 1000)).astype(np.float16).view(np.uint16)
+    i = rng.integers(-2**31, 2**31, (64, 1000), dtype=np.int64).astype(np.int32)
+    i[:, :100] = rng.integers(-50, 50, (64, 100))
+    return [h, i, np.zeros((64, 1000), np.uint16), np.zeros((64, 1000), np.bool_)]

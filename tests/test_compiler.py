@@ -259,3 +259,25 @@ def test_memref_form_groups_compile(tmp_path):
     assert rc == 0, err
     man = open(prefix + ".manifest").read()
     assert "result 0 1 f32" in man and "result 1 2 f32" in man, man
+
+
+def test_generic_after_reshape_does_not_crash(tmp_path):
+    """A linalg.generic fed by an expand_shape, with scalar operands mapped by
+    `() ` maps: compiled or rejected with an error code, never a crash."""
+    ir = """#map = affine_map<(d0, d1) -> (d0, d1)>
+#scalar_map = affine_map<(d0, d1) -> ()>
+func.func @f(%arg0: tensor<64xi1>) -> tensor<64x1xf32> {
+  %t = arith.constant 1.000000e+00 : f32
+  %f = arith.constant 0.000000e+00 : f32
+  %x = tensor.expand_shape %arg0 [[0, 1]] output_shape [64, 1] : tensor<64xi1> into tensor<64x1xi1>
+  %e = tensor.empty() : tensor<64x1xf32>
+  %r = linalg.generic {indexing_maps = [#map, #scalar_map, #scalar_map, #map], iterator_types = ["parallel", "parallel"]}
+      ins(%x, %t, %f : tensor<64x1xi1>, f32, f32) outs(%e : tensor<64x1xf32>) {
+  ^bb0(%in: i1, %a: f32, %b: f32, %out: f32):
+    %s = arith.select %in, %a, %b : f32
+    linalg.yield %s : f32
+  } -> tensor<64x1xf32>
+  return %r : tensor<64x1xf32>
+}"""
+    rc, err, _ = emit(ir, tmp_path)
+    assert rc in (0, -1, -2), (rc, err)

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, gather_inputs, math_funcs, math_inputs,
+from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, gather_inputs, generic_inputs, math_funcs,
+                     math_inputs,
                      misc_extra_inputs,
                      misc_inputs, run_gpu, run_oracle, scan_inputs)
 
@@ -586,3 +587,19 @@ def test_reshape_chain(gpu):
     ref, = run_oracle("reshape_chain", args)
     assert np.array_equal(out, ref)
     assert np.array_equal(ref, np.abs(((args[0] + args[1]).reshape(32, 4, 256) * args[2]).reshape(128, 256)))
+
+
+def test_generic_ops(gpu):
+    """linalg.generic regions: the f16/int group bit-exact; the exp/tanh group
+    (device exp and tanh against glibc) within 1e-5 relative."""
+    note("generic_ops generic_bias_act")
+    args = generic_inputs("generic_bias_act")
+    out, = run_gpu("generic_ops", args, gpu, func="generic_bias_act")
+    ref, = run_oracle("generic_ops", args, func="generic_bias_act")
+    np.testing.assert_allclose(out, ref, rtol=1e-5)
+    note("generic_ops generic_f16_int")
+    args = generic_inputs("generic_f16_int")
+    outs = run_gpu("generic_ops", args, gpu, func="generic_f16_int")
+    refs = run_oracle("generic_ops", args, func="generic_f16_int")
+    for o, r in zip(outs, refs):
+        assert np.array_equal(o, r), f"{int((o != r).sum())} differ"

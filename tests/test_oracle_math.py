@@ -314,3 +314,28 @@ def test_gather_loop_form(spec):
                 q[ax] = k
                 want[p] = src[tuple(q)]
     assert np.array_equal(got, want)
+
+
+from helpers import generic_inputs  # noqa: E402
+
+
+def test_generic_regions_closed_form():
+    """linalg.generic regions evaluated by the oracle against numpy closed
+    forms of the same scalar programs (float64 for the transcendental one)."""
+    x, b, t, s, o = generic_inputs("generic_bias_act")
+    got, = run_oracle("generic_ops", [x, b, t, s, o], func="generic_bias_act")
+    z = x.astype(np.float64) + b
+    tt = t[:, None].astype(np.float64)
+    ref = np.exp(z) / np.maximum(np.where(z > tt, np.tanh(z * 0.5), tt * 0.3), 1.0)
+    np.testing.assert_allclose(got, ref, rtol=2e-6)
+    h, i, oh, om = generic_inputs("generic_f16_int")
+    gh, gm = run_oracle("generic_ops", [h, i, oh, om], func="generic_f16_int")
+    hf16 = h.view(np.float16)
+    with np.errstate(all="ignore"):
+        p = (hf16.astype(np.float32) * i.astype(np.float32)).astype(np.float16)
+    with np.errstate(all="ignore"):
+        assert np.array_equal(gh.view(np.float16), p + hf16, equal_nan=True)
+    i64 = i.astype(np.int64)
+    rem = np.fmod(i64, 3)
+    shl = ((i64 << 3) & 0xFFFFFFFF).astype(np.uint32).view(np.int32).astype(np.int64)
+    assert np.array_equal(gm, (rem ^ shl).astype(np.int32) < 0)
