@@ -2592,7 +2592,13 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     } else {
       flattenReshapeGroup(f);
       A.D = largestShape(f, {});
-      if (A.D.empty()) throw CompileError("group @" + f.name + " has no tensor to iterate over");
+      if (A.D.empty()) {
+        // rank-0 tensors only: one element
+        bool anyTensor = false;
+        for (const Value *v : f.args) anyTensor |= v->type.tensor;
+        for (const Value *v : f.returns) anyTensor |= v->type.tensor;
+        if (!anyTensor) throw CompileError("group @" + f.name + " has no tensor to iterate over");
+      }
       inferMaps(A, {});
       if (kind == "LAST_AXIS_PBR") {
         RowEmitter e(A, opt);

@@ -640,6 +640,17 @@ def entries():
     e["memref_chain"] = memref_chain(4096)
     e["reshape_chain"] = reshape_chain()
     e["generic_ops"] = generic_ops()
+    e["rank0"] = """module {
+  func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
+      """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {
+    %e = tensor.empty() : tensor<f32>
+    %r = linalg.elemwise_binary {fun = #linalg.binary_fn<mul>} ins(%a, %b : tensor<f32>, tensor<f32>) outs(%e : tensor<f32>) -> tensor<f32>
+    %e2 = tensor.empty() : tensor<f32>
+    %s = hfusion.elemwise_unary {fun = #hfusion.unary_fn<sqrt>} ins(%r : tensor<f32>) outs(%e2 : tensor<f32>) -> tensor<f32>
+    return %s : tensor<f32>
+  }
+}
+"""
     e["quant_ties"] = quant_ties(64, 1024)
     e["quant_i8_ties"] = quant_i8_ties(64, 1024)
     e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")

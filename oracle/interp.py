@@ -100,6 +100,13 @@ def ptr(a):
     return a.ctypes.data_as(ctypes.c_void_p)
 
 
+def _contig(a, dtype=None):
+    """C-contiguous array of `a` (rank 0 stays rank 0, unlike
+    numpy.ascontiguousarray)."""
+    a = np.asarray(a, dtype=dtype)
+    return a if a.flags.c_contiguous else a.copy(order="C")
+
+
 # ---------------------------------------------------------------- types
 FP8 = {"f8E4M3FN": 0, "f8E5M2": 1}
 NP = {"f32": np.float32, "f64": np.float64, "bf16": np.uint16, "f16": np.uint16, "f8E4M3FN": np.uint8, "f8E5M2": np.uint8,
@@ -129,7 +136,7 @@ def parse_type(s):
 
 
 def to_f32(v):
-    a = np.ascontiguousarray(v.a)
+    a = _contig(v.a)
     if v.elem == "f32":
         return a.astype(np.float32, copy=False)
     if v.elem == "bf16":
@@ -144,13 +151,13 @@ def to_f32(v):
         return a.astype(np.float32)
     if v.elem in FP8:
         out = np.empty(a.shape, np.float32)
-        lib().hfref_fp8_to_f32_n(ptr(np.ascontiguousarray(a, np.uint8)), ptr(out), a.size, FP8[v.elem])
+        lib().hfref_fp8_to_f32_n(ptr(_contig(a, np.uint8)), ptr(out), a.size, FP8[v.elem])
         return out
     raise TypeError(v.elem)
 
 
 def from_f32(f, elem, mode=0, sat=False):
-    f = np.ascontiguousarray(f, dtype=np.float32)
+    f = _contig(f, dtype=np.float32)
     if elem == "f32":
         return f
     if elem in FP8:
@@ -180,7 +187,7 @@ def bitcast(v, elem):
     src, dst = np.dtype(NP[v.elem]), np.dtype(NP[elem])
     if v.elem == "i1" or elem == "i1" or src.itemsize != dst.itemsize:
         raise NotImplementedError(f"bitcast {v.elem} -> {elem}")
-    return T(np.ascontiguousarray(v.a).view(dst), elem)
+    return T(_contig(v.a).view(dst), elem)
 
 
 def convert(v, elem, unsigned=False):
@@ -192,20 +199,20 @@ def convert(v, elem, unsigned=False):
             return T(to_f32(v).astype(np.float64) if v.elem != "f64" else v.a, elem)
         return T(from_f32(to_f32(v), elem), elem)
     if v.elem not in FLOATS and elem in FLOATS:
-        a = np.ascontiguousarray(v.a)
+        a = _contig(v.a)
         if unsigned or v.elem == "i1":
             bits = BITS[v.elem]
             a64 = a.astype(np.int64) & ((1 << bits) - 1) if bits < 64 else a.astype(np.int64)
         else:
             a64 = a.astype(np.int64)
-        a64 = np.ascontiguousarray(a64)
+        a64 = _contig(a64)
         if elem == "f64":
             return T(a64.astype(np.float64), elem)
         f = np.empty(a64.shape, np.float32)
         lib().hfref_int_to_f32_n(ptr(a64), ptr(f), a64.size, 0)
         return T(from_f32(f, elem), elem)
     if v.elem in FLOATS and elem not in FLOATS:
-        f = np.ascontiguousarray(to_f32(v))
+        f = _contig(to_f32(v))
         if elem == "i1":
             return T(f != 0, elem)
         out = np.empty(f.shape, np.int64)
@@ -232,7 +239,7 @@ def declared_cast(v, elem, mode, sat, unsigned=False):
                 # round to an integral value in float: via the int rounding on exact values
                 r = f.copy()
                 fin = np.isfinite(f) & (np.abs(f) < 2.0 ** 23)
-                tmp = np.ascontiguousarray(f[fin])
+                tmp = _contig(f[fin])
                 o = np.empty(tmp.shape, np.int64)
                 lib().hfref_f32_to_int_mode_n(ptr(tmp), ptr(o), tmp.size, mode, 64, 0)
                 r[fin] = o.astype(np.float32)
@@ -242,12 +249,12 @@ def declared_cast(v, elem, mode, sat, unsigned=False):
             return T(f, elem)
         return T(from_f32(f, elem, mode, sat), elem)
     if v.elem in FLOATS and elem not in FLOATS:
-        f = np.ascontiguousarray(to_f32(v))
+        f = _contig(to_f32(v))
         out = np.empty(f.shape, np.int64)
         lib().hfref_f32_to_int_mode_n(ptr(f), ptr(out), f.size, mode, BITS[elem], int(sat))
         return T(wrap_int(out, elem), elem)
     if v.elem not in FLOATS and elem in FLOATS:
-        a64 = np.ascontiguousarray(np.asarray(v.a).astype(np.int64))
+        a64 = _contig(np.asarray(v.a).astype(np.int64))
         if unsigned or v.elem == "i1":
             a64 = a64 & ((1 << BITS[v.elem]) - 1) if BITS[v.elem] < 64 else a64
         if elem in FP8:  # one rounding, from the exact integer
@@ -300,7 +307,7 @@ def _single_op(op, rest, xs, rtypes):
         rev = re.search(r"reverse\s*=\s*true", rest) is not None
         nan = re.search(r"propagate_nan\s*=\s*false", rest) is None
         x = convert(xs[0], elem)
-        a = np.ascontiguousarray(np.moveaxis(np.asarray(x.a), d, 0))
+        a = _contig(np.moveaxis(np.asarray(x.a), d, 0))
         order = range(a.shape[0] - 1, -1, -1) if rev else range(a.shape[0])
         out = np.empty_like(a)
         if elem in FLOATS:
@@ -313,12 +320,12 @@ def _single_op(op, rest, xs, rtypes):
             xv = T(np.array(a[l]), elem)
             acc = xv if acc is None else apply_binary(fn, acc, xv, elem, a[l].shape)
             out[l] = acc.a
-        return [T(np.ascontiguousarray(np.moveaxis(out, 0, d)), elem)]
+        return [T(_contig(np.moveaxis(out, 0, d)), elem)]
     if name == "flip":
         # reverse along flip_axis (HFusionOps.td:226-245)
         m = re.search(r"flip_axis\s*=\s*(-?\d+)", rest)
         ax = int(m.group(1)) if m else -1
-        return [T(np.ascontiguousarray(np.flip(np.asarray(xs[0].a), ax)), elem)]
+        return [T(_contig(np.flip(np.asarray(xs[0].a), ax)), elem)]
     if name in ("mulext", "mulextui"):
         # (2N)-bit product of sign- or zero-extended operands: low and high halves
         bits = BITS[elem]
@@ -345,8 +352,8 @@ def _single_op(op, rest, xs, rtypes):
         ch = -1 if m.group(1) == "all" else int(m.group(1))
         a = np.asarray(xs[0].a)
         if ch == -1:
-            return [T(np.ascontiguousarray(a[..., 0::2]), elem), T(np.ascontiguousarray(a[..., 1::2]), elem)]
-        return [T(np.ascontiguousarray(a[..., ch::2]), elem)]
+            return [T(_contig(a[..., 0::2]), elem), T(_contig(a[..., 1::2]), elem)]
+        return [T(_contig(a[..., ch::2]), elem)]
     a, b = np.asarray(xs[0].a), np.asarray(xs[1].a)
     out = np.empty(a.shape[:-1] + (2 * a.shape[-1],), a.dtype)
     out[..., 0::2], out[..., 1::2] = a, b
@@ -367,7 +374,7 @@ def _non_dps(op, xs, shape, elem):
         # IEEE nextafter (Normalize.cpp:8640-8660): one ulp from x toward y
         if elem == "f32":
             return np.nextafter(xs[0].a.astype(f32), xs[1].a.astype(f32))
-        h = [np.ascontiguousarray(x.a, np.uint16).view(np.float16) for x in xs]
+        h = [_contig(x.a, np.uint16).view(np.float16) for x in xs]
         return np.nextafter(h[0], h[1]).view(np.uint16)
     if op == "hfusion.hypot":
         # Normalize.cpp:8969-9330: f32 takes the scaled path, f16 the direct one
@@ -411,12 +418,12 @@ def _non_dps(op, xs, shape, elem):
 
 
 def _full(v, shape):
-    return np.ascontiguousarray(np.broadcast_to(v.a, shape))
+    return _contig(np.broadcast_to(v.a, shape))
 
 
 def apply_unary(fn, x, U):
     if U in FLOATS:
-        f = np.ascontiguousarray(np.broadcast_to(to_f32(x), np.shape(x.a)))
+        f = _contig(np.broadcast_to(to_f32(x), np.shape(x.a)))
         out = np.empty(f.shape, np.float32)
         lib().hfref_unary_f32(UNARY[fn], ptr(f), ptr(out), f.size)
         return T(from_f32(out, U), U)
@@ -434,13 +441,13 @@ def apply_unary(fn, x, U):
 
 def apply_binary(fn, x, y, U, shape):
     if U in FLOATS:
-        a = np.ascontiguousarray(np.broadcast_to(to_f32(x), shape))
-        b = np.ascontiguousarray(np.broadcast_to(to_f32(y), shape))
+        a = _contig(np.broadcast_to(to_f32(x), shape))
+        b = _contig(np.broadcast_to(to_f32(y), shape))
         out = np.empty(shape, np.float32)
         lib().hfref_binary_f32(BINARY_F[fn], ptr(a), ptr(b), ptr(out), out.size)
         return T(from_f32(out, U), U)
-    a = np.ascontiguousarray(np.broadcast_to(np.asarray(x.a).astype(np.int64), shape))
-    b = np.ascontiguousarray(np.broadcast_to(np.asarray(y.a).astype(np.int64), shape))
+    a = _contig(np.broadcast_to(np.asarray(x.a).astype(np.int64), shape))
+    b = _contig(np.broadcast_to(np.asarray(y.a).astype(np.int64), shape))
     out = np.empty(shape, np.int64)
     lib().hfref_binary_i64(BINARY_I[fn], ptr(a), ptr(b), ptr(out), out.size, BITS[U])
     return T(wrap_int(out, U), U)
@@ -582,7 +589,7 @@ class Interp:
             if shape is None:
                 env[nm] = T(np.asarray(x, dtype=NP[elem]), elem)
             else:
-                a = np.ascontiguousarray(x, dtype=NP[elem])
+                a = np.array(x, dtype=NP[elem], order="C")  # keeps rank 0
                 if a.shape != shape:
                     raise ValueError(f"{nm}: expected shape {shape}, got {a.shape}")
                 env[nm] = T(a.copy(), elem)
@@ -629,17 +636,17 @@ class Interp:
         outs, _ = _operands(_group(s, "outs"))
         A, B, C = env[ins[0]], env[ins[1]], env[outs[0]]
         at, bt = "a_transpose" in s, "b_transpose" in s
-        a = np.ascontiguousarray(A.a.T if at else A.a)
+        a = _contig(A.a.T if at else A.a)
         M, K = a.shape
         N = C.a.shape[1]
         # the serial matmul takes B as [K, N] (bt=0) or [N, K] (bt=1)
-        b = np.ascontiguousarray(B.a)
+        b = _contig(B.a)
         if A.elem == "i8":
             acc = np.zeros((M, N), np.int32)
             lib().hfref_matmul_i8_i32(ptr(a), ptr(b), ptr(acc), M, N, K, int(bt))
         else:
             acc = np.zeros((M, N), np.float32)
-            lib().hfref_matmul_f32(ptr(np.ascontiguousarray(to_f32(T(a, A.elem)))), ptr(np.ascontiguousarray(to_f32(T(b, B.elem)))),
+            lib().hfref_matmul_f32(ptr(_contig(to_f32(T(a, A.elem)))), ptr(_contig(to_f32(T(b, B.elem)))),
                                    ptr(acc), M, N, K, int(bt))
         bm = re.search(r"\bbias\s*=\s*(%[\w.$-]+)", s)
         dm = re.search(r"\bdescale\s*=\s*(%[\w.$-]+)", s)
@@ -654,7 +661,7 @@ class Interp:
         if dm:
             d = to_f32(env[dm.group(1)])
             t = (t * (d[None, :] if mode == "DescalePerChannel" else d[0])).astype(np.float32)
-        tf = T(np.ascontiguousarray(t, np.float32), "f32")
+        tf = T(_contig(t, np.float32), "f32")
         env[outs[0]] = declared_cast(tf, C.elem, 0, True) if C.elem in BITS else convert(tf, C.elem)
         self.written.append(outs[0])
 
@@ -704,7 +711,7 @@ class Interp:
             # a row-major view with the result type after `into`
             src = re.findall(r"%[\w.$#-]+", rest)[0]
             shape, elem = parse_type(rest.rsplit("into", 1)[1])
-            env[res] = T(np.ascontiguousarray(env[src].a).reshape(shape), elem)
+            env[res] = T(_contig(env[src].a).reshape(shape), elem)
             return
         if op.startswith("arith.") and "ins(" not in rest:
             self._scalar_arith(res, op, rest, env)
@@ -727,7 +734,7 @@ class Interp:
             names = re.findall(r"%[\w.$-]+", rest.split(":", 1)[0])
             shape, elem = parse_type(rest.rsplit("->", 1)[1])
             xs = [T(np.broadcast_to(env[n].a, shape), env[n].elem) for n in names]
-            env[res] = T(np.ascontiguousarray(_non_dps(op, xs, shape, elem)), elem)
+            env[res] = T(_contig(_non_dps(op, xs, shape, elem)), elem)
             return
         ins, ins_t = _operands(_group(rest, "ins"))
         outs, outs_t = _operands(_group(rest, "outs"))
@@ -783,11 +790,11 @@ class Interp:
             M, K = A.a.shape
             N = Cinit.a.shape[1]
             if A.elem == "i8" and Cinit.elem == "i32":
-                C = np.ascontiguousarray(Cinit.a.copy())
-                lib().hfref_matmul_i8_i32(ptr(np.ascontiguousarray(A.a)), ptr(np.ascontiguousarray(B.a)), ptr(C), M, N, K, bt)
+                C = _contig(Cinit.a.copy())
+                lib().hfref_matmul_i8_i32(ptr(_contig(A.a)), ptr(_contig(B.a)), ptr(C), M, N, K, bt)
             elif Cinit.elem == "f32":
-                C = np.ascontiguousarray(Cinit.a.copy())
-                lib().hfref_matmul_f32(ptr(np.ascontiguousarray(to_f32(A))), ptr(np.ascontiguousarray(to_f32(B))), ptr(C),
+                C = _contig(Cinit.a.copy())
+                lib().hfref_matmul_f32(ptr(_contig(to_f32(A))), ptr(_contig(to_f32(B))), ptr(C),
                                        M, N, K, bt)
             else:
                 raise NotImplementedError("matmul types")
@@ -812,18 +819,18 @@ class Interp:
             fn = _attr(rest, "compare_fn") or "veq"
             a, b = xs
             if a.elem in FLOATS:
-                fa = np.ascontiguousarray(np.broadcast_to(to_f32(a), shape))
-                fb = np.ascontiguousarray(np.broadcast_to(to_f32(b), shape))
+                fa = _contig(np.broadcast_to(to_f32(a), shape))
+                fb = _contig(np.broadcast_to(to_f32(b), shape))
                 out = np.empty(shape, np.uint8)
                 lib().hfref_compare_f32(COMPARE[fn], ptr(fa), ptr(fb), ptr(out), out.size)
             else:
-                ia = np.ascontiguousarray(np.broadcast_to(a.a.astype(np.int64), shape))
-                ib = np.ascontiguousarray(np.broadcast_to(b.a.astype(np.int64), shape))
+                ia = _contig(np.broadcast_to(a.a.astype(np.int64), shape))
+                ib = _contig(np.broadcast_to(b.a.astype(np.int64), shape))
                 out = np.empty(shape, np.uint8)
                 lib().hfref_compare_i64(COMPARE[fn], ptr(ia), ptr(ib), ptr(out), out.size)
             r = T(out.astype(np.bool_), "i1")
         elif op == "hfusion.bitcast":
-            r = bitcast(T(np.ascontiguousarray(np.broadcast_to(xs[0].a, shape)), xs[0].elem), U)
+            r = bitcast(T(_contig(np.broadcast_to(xs[0].a, shape)), xs[0].elem), U)
         elif op == "hfusion.select":
             c, a, b = xs
             r = T(np.where(np.broadcast_to(c.a, shape), np.broadcast_to(a.a, shape), np.broadcast_to(b.a, shape)).astype(NP[U]), U)
@@ -833,7 +840,7 @@ class Interp:
             x = T(np.broadcast_to(xs[0].a, shape), xs[0].elem)
             if self.cast_semantics == "cpu":
                 if x.elem == U and U in FLOATS:
-                    f = np.ascontiguousarray(to_f32(x))
+                    f = _contig(to_f32(x))
                     rr = np.empty_like(f)
                     lib().hfref_round_n(ptr(f), ptr(rr), f.size)
                     r = T(from_f32(rr, U), U)
@@ -843,7 +850,7 @@ class Interp:
                 r = declared_cast(x, U, mode, sat, uns or "ui2" in (_attr(rest, "unsigned_mode") or ""))
         else:
             raise NotImplementedError(f"op {op}")
-        env[res] = T(np.ascontiguousarray(np.broadcast_to(r.a, shape)).astype(NP[U], copy=False), U)
+        env[res] = T(_contig(np.broadcast_to(r.a, shape)).astype(NP[U], copy=False), U)
 
     def _generic(self, rest, ins, outs, env):
         """linalg.generic with parallel loops, identity output map and
@@ -911,7 +918,7 @@ class Interp:
                 continue
             if st.startswith("linalg.yield"):
                 v = get(re.findall(r"%[\w.$-]+", st)[0])
-                return convert(v, o.elem) if v.elem != o.elem else T(np.ascontiguousarray(v.a), v.elem)
+                return convert(v, o.elem) if v.elem != o.elem else T(_contig(v.a), v.elem)
             m = re.match(r"(%[\w.$-]+)\s*=\s*([\w.]+)\s*(.*)$", st)
             r_, opn, tail = m.group(1), m.group(2), m.group(3)
             lhs, _, ty = tail.rpartition(":")
@@ -961,11 +968,11 @@ class Interp:
                             "ult": x < y, "ule": x <= y, "ugt": x > y, "uge": x >= y}[pred]
                 local[r_] = T(np.asarray(res_, np.bool_), "i1")
             elif opn == "arith.bitcast":
-                local[r_] = bitcast(T(np.ascontiguousarray(xs[0].a), xs[0].elem), to)
+                local[r_] = bitcast(T(_contig(xs[0].a), xs[0].elem), to)
             elif opn in ("arith.extf", "arith.truncf", "arith.sitofp", "arith.uitofp", "arith.fptosi", "arith.fptoui",
                          "arith.extsi", "arith.extui", "arith.trunci", "arith.index_cast", "arith.index_castui"):
                 uns = opn in ("arith.uitofp", "arith.fptoui", "arith.extui", "arith.index_castui")
-                local[r_] = convert(T(np.ascontiguousarray(xs[0].a), xs[0].elem), to, uns)
+                local[r_] = convert(T(_contig(xs[0].a), xs[0].elem), to, uns)
             else:
                 raise NotImplementedError(f"region op {opn}")
         raise ValueError("linalg.generic region without linalg.yield")
@@ -1011,18 +1018,18 @@ class Interp:
         keep = [d for d in range(rank) if d not in dims]
         # loop nest d0..d{r-1}: for each output element the reduced indices
         # are visited in ascending lexicographic order
-        xt = np.ascontiguousarray(np.transpose(x.a, dims + keep))
+        xt = _contig(np.transpose(x.a, dims + keep))
         K = int(np.prod([x.a.shape[d] for d in dims]))
         N = int(np.prod([x.a.shape[d] for d in keep])) if keep else 1
         if x.elem == "f32":
-            acc = np.ascontiguousarray(init.a.astype(np.float32).reshape(N)).copy()
+            acc = _contig(init.a.astype(np.float32).reshape(N)).copy()
             lib().hfref_reduce_f32(REDUCE_F[comb], ptr(xt.reshape(K, N)), ptr(acc), K, N)
             env[res] = T(acc.reshape(init.a.shape), "f32")
         elif x.elem in ("bf16", "f16"):
             raise NotImplementedError("16-bit float reductions")
         else:
-            acc = np.ascontiguousarray(init.a.astype(np.int64).reshape(N)).copy()
-            xi = np.ascontiguousarray(xt.reshape(K, N).astype(np.int64))
+            acc = _contig(init.a.astype(np.int64).reshape(N)).copy()
+            xi = _contig(xt.reshape(K, N).astype(np.int64))
             lib().hfref_reduce_i64(REDUCE_I[comb], ptr(xi), ptr(acc), K, N, BITS[x.elem])
             env[res] = T(wrap_int(acc, x.elem).reshape(init.a.shape), x.elem)
 
@@ -1035,20 +1042,20 @@ class Interp:
         d = dims[0]
         rank = x.a.ndim
         keep = [k for k in range(rank) if k != d]
-        xt = np.ascontiguousarray(np.transpose(x.a, [d] + keep))
+        xt = _contig(np.transpose(x.a, [d] + keep))
         K = x.a.shape[d]
         N = int(np.prod([x.a.shape[k] for k in keep])) if keep else 1
-        val = np.ascontiguousarray(v0.a.reshape(N)).copy()
-        idx = np.ascontiguousarray(i0.a.astype(np.int64).reshape(N)).copy()
+        val = _contig(v0.a.reshape(N)).copy()
+        idx = _contig(i0.a.astype(np.int64).reshape(N)).copy()
         ii = None
         if idx_in is not None:
-            ii = np.ascontiguousarray(np.transpose(idx_in.a, [d] + keep).astype(np.int64).reshape(K, N))
+            ii = _contig(np.transpose(idx_in.a, [d] + keep).astype(np.int64).reshape(K, N))
         if x.elem == "f32":
             lib().hfref_reduce_with_index_f32({"max": 0, "min": 1}[kind], ptr(xt.reshape(K, N)),
                                               ptr(ii) if ii is not None else None, ptr(val), ptr(idx), K, N)
         else:
-            xi = np.ascontiguousarray(xt.reshape(K, N).astype(np.int64))
-            v64 = np.ascontiguousarray(val.astype(np.int64))
+            xi = _contig(xt.reshape(K, N).astype(np.int64))
+            v64 = _contig(val.astype(np.int64))
             lib().hfref_reduce_with_index_i64({"max": 0, "min": 1, "maxui": 2, "minui": 3}[kind], ptr(xi),
                                               ptr(ii) if ii is not None else None, ptr(v64), ptr(idx), K, N, BITS[x.elem])
             val = wrap_int(v64, x.elem)

@@ -16,7 +16,8 @@ def empty_like_param(p):
 
 def to_dev(a, elem, device):
     import torch
-    t = torch.from_numpy(np.ascontiguousarray(a))
+    a = np.asarray(a)
+    t = torch.from_numpy(a if a.flags.c_contiguous else a.copy(order="C"))  # rank 0 stays rank 0
     if elem in ("bf16", "f16"):
         t = t.view(torch.bfloat16 if elem == "bf16" else torch.float16)
     if elem in ("f8E4M3FN", "f8E5M2"):

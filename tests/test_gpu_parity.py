@@ -603,3 +603,13 @@ def test_generic_ops(gpu):
     refs = run_oracle("generic_ops", args, func="generic_f16_int")
     for o, r in zip(outs, refs):
         assert np.array_equal(o, r), f"{int((o != r).sum())} differ"
+
+
+def test_rank0_group(gpu):
+    """A group over rank-0 tensors runs as one element: bit-exact."""
+    note("rank0")
+    args = [np.array(2.5, np.float32), np.array(3.0, np.float32)]
+    out, = run_gpu("rank0", args, gpu)
+    ref, = run_oracle("rank0", args)
+    assert np.array_equal(np.asarray(out).reshape(()), np.asarray(ref).reshape(()))
+    assert float(np.asarray(ref)) == float(np.sqrt(np.float32(7.5)))
