@@ -432,6 +432,60 @@ module {{
 """
 
 
+def fuzz_generic(count=12, seed=20261201, shape=(32, 257)):
+    """Seeded random elementwise groups: linalg.generic regions over f32 / f16
+    / i32 operands (a row-broadcast operand among them) built only from
+    exactly rounded ops (add, sub, mul, div, max/min, abs, neg, sqrt,
+    compare + select, extf/truncf, sitofp), so every result is bit-exact
+    against the oracle."""
+    import random
+    rnd = random.Random(seed)
+    r, c = shape
+    funcs = []
+    fops = ["arith.addf", "arith.subf", "arith.mulf", "arith.divf", "arith.maximumf", "arith.minimumf"]
+    for n in range(count):
+        ft = rnd.choice(["f32", "f16"])
+        X, B, I, O = _T([r, c], ft), _T([c], ft), _T([r, c], "i32"), _T([r, c], ft)
+        body, vals, k = [], ["%a", "%b", "%bb"], 0
+
+        def new(stmt):
+            nonlocal k
+            nm = f"%v{k}"
+            k += 1
+            body.append(f"      {nm} = {stmt}")
+            return nm
+        vals.append(new(f"arith.sitofp %n : i32 to {ft}"))
+        for _ in range(rnd.randint(3, 7)):
+            kind = rnd.random()
+            x, y = rnd.choice(vals), rnd.choice(vals)
+            if kind < 0.55:
+                vals.append(new(f"{rnd.choice(fops)} {x}, {y} : {ft}"))
+            elif kind < 0.7:
+                vals.append(new(f"{rnd.choice(['math.absf', 'arith.negf', 'math.sqrt'])} {x} : {ft}"))
+            elif kind < 0.85:
+                cnd = new(f"arith.cmpf {rnd.choice(['olt', 'oge', 'une', 'ugt'])}, {x}, {y} : {ft}")
+                vals.append(new(f"arith.select {cnd}, {x}, {rnd.choice(vals)} : {ft}"))
+            elif ft == "f16":
+                e = new(f"arith.extf {x} : f16 to f32")
+                m = new(f"arith.mulf {e}, {e} : f32")
+                vals.append(new(f"arith.truncf {m} : f32 to f16"))
+            else:
+                vals.append(new(f"arith.addf {x}, {x} : {ft}"))
+        body.append(f"      linalg.yield {vals[-1]} : {ft}")
+        region = "\n".join(body)
+        funcs.append(f"""  func.func @fuzz{n}(%x: {X}, %bias: {B}, %i: {I}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %r = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d1)>, affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>], iterator_types = ["parallel", "parallel"]}}
+        ins(%x, %bias, %i : {X}, {B}, {I}) outs(%o : {O}) {{
+    ^bb0(%a: {ft}, %bb: {ft}, %n: i32, %out: {ft}):
+      %b = arith.addf %a, %bb : {ft}
+{region}
+    }} -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -640,6 +694,7 @@ def entries():
     e["memref_chain"] = memref_chain(4096)
     e["reshape_chain"] = reshape_chain()
     e["generic_ops"] = generic_ops()
+    e["fuzz_generic"] = fuzz_generic()
     e["rank0"] = """module {
   func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
       """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {

@@ -371,3 +371,19 @@ def generic_inputs(name, seed=0x47454E45):
     i = rng.integers(-2**31, 2**31, (64, 1000), dtype=np.int64).astype(np.int32)
     i[:, :100] = rng.integers(-50, 50, (64, 100))
     return [h, i, np.zeros((64, 1000), np.uint16), np.zeros((64, 1000), np.bool_)]
+
+
+def fuzz_inputs(n, seed=0x46555A5A):
+    """Arguments of group fuzz<n> of catalog module fuzz_generic (its float
+    type read from the group's signature)."""
+    import re
+    ir = hf.catalog.get("fuzz_generic")
+    ft = re.search(r"@fuzz%d\(%%x: tensor<32x257x(\w+)>" % n, ir).group(1)
+    rng = np.random.default_rng(seed + n)
+    x = rng.normal(0, 3, (32, 257)).astype(np.float32)
+    b = rng.normal(0, 3, 257).astype(np.float32)
+    x[0, :4] = [0.0, -0.0, np.inf, np.nan]
+    i = rng.integers(-100, 100, (32, 257)).astype(np.int32)
+    if ft == "f16":
+        x, b = x.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+    return [x, b, i, np.zeros_like(x)], ft

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, gather_inputs, generic_inputs, math_funcs,
+from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, fuzz_inputs, gather_inputs, generic_inputs,
+                     math_funcs,
                      math_inputs,
                      misc_extra_inputs,
                      misc_inputs, run_gpu, run_oracle, scan_inputs)
@@ -613,3 +614,18 @@ def test_rank0_group(gpu):
     ref, = run_oracle("rank0", args)
     assert np.array_equal(np.asarray(out).reshape(()), np.asarray(ref).reshape(()))
     assert float(np.asarray(ref)) == float(np.sqrt(np.float32(7.5)))
+
+
+@pytest.mark.parametrize("n", range(12))
+def test_fuzz_generic(gpu, n):
+    """Seeded random linalg.generic regions of exactly rounded ops over f32 /
+    f16 with a row-broadcast operand and an i32 operand: bit-exact (any NaN
+    matches any NaN)."""
+    note(f"fuzz_generic fuzz{n}")
+    args, ft = fuzz_inputs(n)
+    out, = run_gpu("fuzz_generic", args, gpu, func=f"fuzz{n}")
+    ref, = run_oracle("fuzz_generic", args, func=f"fuzz{n}")
+    a = out.view(np.float16).astype(np.float32) if ft == "f16" else out
+    b = ref.view(np.float16).astype(np.float32) if ft == "f16" else ref
+    same = (out == ref) | (np.isnan(a) & np.isnan(b))
+    assert same.all(), f"{int((~same).sum())} differ, e.g. gpu={a[~same][:3]} oracle={b[~same][:3]}"
