@@ -486,6 +486,61 @@ def fuzz_generic(count=12, seed=20261201, shape=(32, 257)):
     return "module {\n" + "\n".join(funcs) + "\n}\n"
 
 
+def fuzz_rows(count=8, seed=20261202):
+    """Seeded random LAST_AXIS_PBR groups from named ops: an elementwise chain
+    with a row-broadcast operand, a max or min row reduction, its broadcast
+    back into a second chain, results both the row values and the reduction.
+    Exactly rounded, order-free ops only, so results are bit-exact."""
+    import random
+    rnd = random.Random(seed)
+    funcs = []
+    for n in range(count):
+        r, c = rnd.choice([(64, 1000), (13, 4096), (256, 96), (7, 33000)])
+        X, B, R = _T([r, c], "f32"), _T([c], "f32"), _T([r], "f32")
+        lines, k = [], 0
+
+        def ew(op, ins):
+            nonlocal k
+            k += 1
+            e, v = f"%e{k}", f"%v{k}"
+            fam = "linalg" if op in ("add", "sub", "mul", "div", "max_signed", "min_signed", "abs", "negf") else "hfusion"
+            if op in ("abs", "negf", "sqrt"):
+                attr = f"#{'linalg' if fam == 'linalg' else 'hfusion'}.unary_fn<{op}>"
+                kind = f"{fam}.elemwise_unary"
+                tys = X
+            else:
+                attr = f"#linalg.binary_fn<{op}>" if fam == "linalg" else f"#hfusion.binary_fn<{op}>"
+                kind = f"{fam}.elemwise_binary"
+                tys = ", ".join([X] * len(ins))
+            lines.append(f"    {e} = tensor.empty() : {X}")
+            lines.append(f"    {v} = {kind} {{fun = {attr}}} ins({', '.join(ins)} : {tys}) outs({e} : {X}) -> {X}")
+            return v
+        lines.append(f"    %eb = tensor.empty() : {X}")
+        lines.append(f"    %bb = linalg.broadcast ins(%b : {B}) outs(%eb : {X}) dimensions = [0]")
+        vals = ["%x", "%bb"]
+        for _ in range(rnd.randint(2, 4)):
+            op = rnd.choice(["add", "sub", "mul", "max_signed", "min_signed", "abs", "negf"])
+            vals.append(ew(op, [rnd.choice(vals)] if op in ("abs", "negf") else [rnd.choice(vals), rnd.choice(vals)]))
+        red = rnd.choice(["maximumf", "minimumf"])
+        init = "0xFF800000" if red == "maximumf" else "0x7F800000"
+        lines.append(f"    %init = arith.constant {init} : f32")
+        lines.append(f"    %f = linalg.fill ins(%init : f32) outs(%m : {R}) -> {R}")
+        lines.append(f"    %red = linalg.reduce {{arith.{red}}} ins({vals[-1]} : {X}) outs(%f : {R}) dimensions = [1]")
+        lines.append(f"    %er = tensor.empty() : {X}")
+        lines.append(f"    %rb = linalg.broadcast ins(%red : {R}) outs(%er : {X}) dimensions = [1]")
+        vals.append("%rb")
+        for _ in range(rnd.randint(1, 3)):
+            op = rnd.choice(["sub", "add", "mul", "max_signed", "abs"])
+            vals.append(ew(op, [rnd.choice(vals[-3:])] if op == "abs" else [rnd.choice(vals[-3:]), rnd.choice(vals)]))
+        body = "\n".join(lines)
+        funcs.append(f"""  func.func @frow{n}(%x: {X}, %b: {B}, %m: {R}) -> ({X}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+{body}
+    return {vals[-1]}, %red : {X}, {R}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -695,6 +750,7 @@ def entries():
     e["reshape_chain"] = reshape_chain()
     e["generic_ops"] = generic_ops()
     e["fuzz_generic"] = fuzz_generic()
+    e["fuzz_rows"] = fuzz_rows()
     e["rank0"] = """module {
   func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
       """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {

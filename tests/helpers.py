@@ -387,3 +387,18 @@ def fuzz_inputs(n, seed=0x46555A5A):
     if ft == "f16":
         x, b = x.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
     return [x, b, i, np.zeros_like(x)], ft
+
+
+def fuzz_row_inputs(n, seed=0x46524F57):
+    """Arguments of group frow<n> of catalog module fuzz_rows (shape read
+    from its signature), with ±0, ±inf and a NaN row among the values."""
+    import re
+    ir = hf.catalog.get("fuzz_rows")
+    r, c = map(int, re.search(r"@frow%d\(%%x: tensor<(\d+)x(\d+)xf32>" % n, ir).groups())
+    rng = np.random.default_rng(seed + n)
+    x = rng.normal(0, 5, (r, c)).astype(np.float32)
+    b = rng.normal(0, 5, c).astype(np.float32)
+    x[0, :3] = [0.0, -0.0, np.inf]
+    if r > 2:
+        x[2, c // 2] = np.nan
+    return [x, b, np.zeros(r, np.float32)]

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
-from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, fuzz_inputs, gather_inputs, generic_inputs,
+from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, fuzz_inputs, fuzz_row_inputs, gather_inputs,
+                     generic_inputs,
                      math_funcs,
                      math_inputs,
                      misc_extra_inputs,
@@ -629,3 +630,17 @@ def test_fuzz_generic(gpu, n):
     b = ref.view(np.float16).astype(np.float32) if ft == "f16" else ref
     same = (out == ref) | (np.isnan(a) & np.isnan(b))
     assert same.all(), f"{int((~same).sum())} differ, e.g. gpu={a[~same][:3]} oracle={b[~same][:3]}"
+
+
+@pytest.mark.parametrize("n", range(8))
+def test_fuzz_rows(gpu, n):
+    """Seeded random row programs (elementwise chain -> max/min row reduce ->
+    broadcast -> chain) over several row widths incl. ragged ones and 33000
+    columns: bit-exact, NaN rows included."""
+    note(f"fuzz_rows frow{n}")
+    args = fuzz_row_inputs(n)
+    outs = run_gpu("fuzz_rows", args, gpu, func=f"frow{n}")
+    refs = run_oracle("fuzz_rows", args, func=f"frow{n}")
+    for o, r in zip(outs, refs):
+        same = (o == r) | (np.isnan(o) & np.isnan(r))
+        assert same.all(), f"{int((~same).sum())} differ, e.g. gpu={o[~same][:3]} oracle={r[~same][:3]}"
