@@ -181,6 +181,45 @@ def cpu_baseline(name, ins, budget_s=12.0):
             "sample": sample + f", median of {len(times)} runs"}
 
 
+def cpu_baseline_mt(name, ins, budget_s=10.0):
+    """The same C restatement run row-parallel on the host's cores (the
+    reference CPU runner is single-threaded; this is the secondary figure):
+    the full workload split into one row slice per thread, the C calls
+    releasing the GIL.  Headline group only."""
+    import ctypes
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    sys.path.insert(0, REPO)
+    from oracle.interp import lib, ptr
+    if name != "rmsnorm_quant":
+        return None
+    L = lib()
+    x, g = ins
+    rows, cols = x.shape
+    threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
+    xs = np.ascontiguousarray(x)
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    step = -(-rows // threads)
+
+    def part(t):
+        r0, r1 = t * step, min(rows, (t + 1) * step)
+        if r0 < r1:
+            L.hfref_rmsnorm_quant(ptr(xs[r0:]), ptr(g), ctypes.c_float(1e-6), ptr(q[r0:]), ptr(s[r0:]), r1 - r0, cols)
+    nbytes = xs.nbytes + g.nbytes + q.nbytes + s.nbytes
+    times = []
+    with ThreadPoolExecutor(threads) as ex:
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+            t0 = time.perf_counter()
+            list(ex.map(part, range(threads)))
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"all {rows} rows x {cols}, {threads} row slices in parallel, median of {len(times)} runs"}
+
+
 def _csv_rows(d, suffix):
     import csv
     import glob
@@ -380,6 +419,7 @@ def main():
     names = [args.only] if args.only else ORDER
     groups = {}
     headline_cpu = None
+    headline_cpu_mt = None
     traffic = traffic_table()
     for name in names:
         log(f"[bench] {name}: preparing inputs")
@@ -414,6 +454,7 @@ def main():
         if not args.no_cpu and (name == HEADLINE or args.only):
             log(f"[bench] {name}: CPU baseline (oracle restatement, 1 core)")
             headline_cpu = cpu_baseline(name, host_ins)
+            headline_cpu_mt = cpu_baseline_mt(name, host_ins)
         entry["input_sets"] = len(sets)
         del dargs, sets
         torch.cuda.empty_cache()
@@ -430,6 +471,7 @@ def main():
         "config": {"workload": head, **{k: v for k, v in cfg.items()}},
         "roofline": h["roofline"],
         "cpu_baseline": headline_cpu,
+        "cpu_baseline_mt": headline_cpu_mt,
         "groups": groups,
     }
     print(json.dumps(line), flush=True)
