@@ -2517,6 +2517,182 @@ static void flattenReshapeGroup(Func &f) {
       for (Value *v : *lst) flat(v);
 }
 
+// linalg.generic with a reduction over the last loop dim whose region ends
+// in `%y = <combine> %v, %out` (or `%out, %v`), %out read nowhere else:
+// rewritten as an elementwise linalg.generic computing %v over the full loop
+// domain, then linalg.reduce with that combiner into the original outs.  The
+// row programs then schedule it like any row reduction.
+static void splitGenericReductions(Module &m, Func &f) {
+  static const std::map<std::string, std::string> comb = {
+      {"arith.addf", "arith.addf"}, {"arith.mulf", "arith.mulf"}, {"arith.maximumf", "arith.maximumf"},
+      {"arith.minimumf", "arith.minimumf"}, {"arith.maxnumf", "arith.maxnumf"}, {"arith.minnumf", "arith.minnumf"},
+      {"arith.addi", "arith.addi"}, {"arith.muli", "arith.muli"}, {"arith.maxsi", "arith.maxsi"},
+      {"arith.minsi", "arith.minsi"}, {"arith.andi", "arith.andi"}, {"arith.ori", "arith.ori"},
+      {"arith.xori", "arith.xori"}};
+  for (size_t oi = 0; oi < f.ops.size(); ++oi) {
+    Op *g = f.ops[oi];
+    if (g->name != "linalg.generic" || g->attr("iterator_types").find("reduction") == std::string::npos) continue;
+    if (g->outs.size() != 1 || g->results.size() != 1) continue;
+    std::vector<std::vector<int>> maps;
+    int nd = 0;
+    if (!genericMaps(g, maps, nd) || nd < 1) continue;
+    // reduction over exactly the last loop dim; outs indexed by d0..d(nd-2)
+    std::vector<std::string> it;
+    {
+      std::string its = g->attr("iterator_types");
+      for (size_t q = 0; q < its.size();) {
+        size_t p = its.find_first_of("pr", q);
+        if (p == std::string::npos) break;
+        if (its.compare(p, 8, "parallel") == 0) { it.push_back("parallel"); q = p + 8; }
+        else if (its.compare(p, 9, "reduction") == 0) { it.push_back("reduction"); q = p + 9; }
+        else q = p + 1;
+      }
+    }
+    if ((int)it.size() != nd || it.back() != "reduction") continue;
+    bool ok = true;
+    for (int i = 0; i + 1 < nd; ++i) ok &= it[i] == "parallel";
+    const auto &om = maps.back();
+    ok &= (int)om.size() == nd - 1;
+    for (int i = 0; ok && i < nd - 1; ++i) ok = om[i] == i;
+    if (!ok) continue;
+    int64_t L = -1;
+    for (size_t i = 0; i < g->ins.size(); ++i)
+      for (size_t ax = 0; ax < maps[i].size(); ++ax)
+        if (maps[i][ax] == nd - 1 && g->ins[i]->type.tensor) L = g->ins[i]->type.shape[ax];
+    if (L < 0) continue;
+    // the region: header, statements, yield
+    const std::string region = g->attr("region");
+    const size_t hp = region.find(')'), colon = region.find(':', hp);
+    if (hp == std::string::npos || colon == std::string::npos) continue;
+    std::string header = region.substr(0, colon + 1);
+    std::vector<std::string> lines;
+    {
+      std::stringstream ss(region.substr(colon + 1));
+      std::string ln;
+      while (std::getline(ss, ln)) {
+        const size_t b0 = ln.find_first_not_of(" \t");
+        if (b0 != std::string::npos) lines.push_back(ln.substr(b0));
+      }
+    }
+    // block argument names; the last one is %out
+    std::vector<std::string> bnames;
+    {
+      const size_t lp = header.find('(');
+      std::stringstream ss(header.substr(lp + 1, hp - lp - 1));
+      std::string arg;
+      while (std::getline(ss, arg, ',')) {
+        std::string nm = arg.substr(0, arg.find(':'));
+        nm.erase(std::remove_if(nm.begin(), nm.end(), ::isspace), nm.end());
+        bnames.push_back(nm);
+      }
+    }
+    if (bnames.size() != g->ins.size() + 1 || lines.empty() || lines.back().rfind("linalg.yield", 0) != 0) continue;
+    const std::string outArg = bnames.back();
+    auto valueNames = [](const std::string &t) {
+      std::vector<std::string> v;
+      for (size_t q = 0; (q = t.find('%', q)) != std::string::npos;) {
+        size_t e = q + 1;
+        while (e < t.size() && (std::isalnum((unsigned char)t[e]) || t[e] == '_' || t[e] == '.' || t[e] == '#')) ++e;
+        v.push_back(t.substr(q, e - q));
+        q = e;
+      }
+      return v;
+    };
+    const auto yv = valueNames(lines.back());
+    if (yv.size() != 1) continue;
+    int si = -1;
+    for (int i = 0; i + 1 < (int)lines.size(); ++i)
+      if (lines[i].rfind(yv[0] + " ", 0) == 0 || lines[i].rfind(yv[0] + "=", 0) == 0) si = i;
+    if (si < 0) continue;
+    const std::string &S = lines[si];
+    const size_t eq = S.find('=');
+    std::string rest = S.substr(eq + 1);
+    rest.erase(0, rest.find_first_not_of(" \t"));
+    const std::string opn = rest.substr(0, rest.find_first_of(" \t"));
+    if (!comb.count(opn)) continue;
+    const auto sv = valueNames(S);
+    if (sv.size() != 3) continue;
+    std::string v;
+    if (sv[1] == outArg && sv[2] != outArg) v = sv[2];
+    else if (sv[2] == outArg && sv[1] != outArg) v = sv[1];
+    else continue;
+    bool outElsewhere = false;
+    for (int i = 0; i + 1 < (int)lines.size(); ++i)
+      if (i != si) for (auto &nm : valueNames(lines[i])) outElsewhere |= nm == outArg;
+    if (outElsewhere) continue;
+    const std::string ty = S.substr(S.rfind(':') + 1);
+    Elem vt;
+    try { std::string t = ty; t.erase(std::remove_if(t.begin(), t.end(), ::isspace), t.end()); vt = parseElem(t); }
+    catch (const CompileError &) { continue; }
+    // build: %e = tensor.empty, %V = linalg.generic (elementwise), linalg.reduce
+    Type full;
+    full.tensor = true;
+    full.elem = vt;
+    full.shape = g->outs[0]->type.shape;
+    full.shape.push_back(L);
+    Op *empty = m.newOp();
+    empty->name = "tensor.empty";
+    Value *ev = m.newValue();
+    ev->type = full;
+    ev->def = empty;
+    ev->name = g->results[0]->name + "#elem_init";
+    empty->results.push_back(ev);
+    Op *eg = m.newOp();
+    eg->name = "linalg.generic";
+    eg->line = g->line;
+    eg->ins = g->ins;
+    eg->insTypes = g->insTypes;
+    eg->operands = g->operands;
+    eg->outs = {ev};
+    eg->attrs = g->attrs;
+    // maps: the ins maps, then the identity over all nd loops
+    std::string im = "[";
+    for (size_t i = 0; i < g->ins.size(); ++i) {
+      im += "affine_map<(";
+      for (int d = 0; d < nd; ++d) im += (d ? ", d" : "d") + std::to_string(d);
+      im += ") -> (";
+      for (size_t k = 0; k < maps[i].size(); ++k) im += (k ? ", d" : "d") + std::to_string(maps[i][k]);
+      im += ")>, ";
+    }
+    im += "affine_map<(";
+    for (int d = 0; d < nd; ++d) im += (d ? ", d" : "d") + std::to_string(d);
+    im += ") -> (";
+    for (int d = 0; d < nd; ++d) im += (d ? ", d" : "d") + std::to_string(d);
+    im += ")>]";
+    eg->attrs["indexing_maps"] = im;
+    eg->attrs["iterator_types"] = "[parallel]";
+    std::string nr = header + "\n";
+    for (int i = 0; i + 1 < (int)lines.size(); ++i)
+      if (i != si) nr += "  " + lines[i] + "\n";
+    nr += "  linalg.yield " + v + " : " + elemName(vt) + "\n";
+    eg->attrs["region"] = nr;
+    Value *vv = m.newValue();
+    vv->type = full;
+    vv->def = eg;
+    vv->name = g->results[0]->name + "#elem";
+    eg->results.push_back(vv);
+    ev->users.push_back(eg);
+    Op *rd = m.newOp();
+    rd->name = "linalg.reduce";
+    rd->line = g->line;
+    rd->ins = {vv};
+    rd->outs = g->outs;
+    rd->dims = {nd - 1};
+    rd->hasDims = true;
+    rd->combiner = comb.at(opn);
+    rd->results = g->results;
+    for (Value *r : rd->results) r->def = rd;
+    vv->users.push_back(rd);
+    for (auto *lst : {&g->ins, &g->operands})
+      for (Value *x : *lst) std::replace(x->users.begin(), x->users.end(), (Op *)g, eg);
+    for (Value *x : g->outs) std::replace(x->users.begin(), x->users.end(), (Op *)g, rd);
+    f.ops[oi] = rd;
+    f.ops.insert(f.ops.begin() + oi, eg);
+    f.ops.insert(f.ops.begin() + oi, empty);
+    oi += 2;
+  }
+}
+
 std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
   std::vector<KernelPlan> out;
   bool anyEntry = false;
@@ -2577,6 +2753,7 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
       if (noReturns)
         for (Value *b : written) f.returns.push_back(latest[b]);
     }
+    splitGenericReductions(m, f);
     describeBuffers(A);
     std::string kname = "hf_" + f.name;
     KernelPlan p;

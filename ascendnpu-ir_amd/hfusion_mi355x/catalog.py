@@ -541,6 +541,29 @@ def fuzz_rows(count=8, seed=20261202):
     return "module {\n" + "\n".join(funcs) + "\n}\n"
 
 
+def generic_reduce():
+    """linalg.generic row reductions: max of x*w (exact) and sum of
+    x*w (a float sum: the row program's order differs from the serial loop)."""
+    X, W, R = _T([64, 1000], "f32"), _T([1000], "f32"), _T([64], "f32")
+    funcs = []
+    for name, comb, init in (("gred_max", "arith.maximumf", "0xFF800000"), ("gred_sum", "arith.addf", "0.000000e+00")):
+        funcs.append(f"""  func.func @{name}(%x: {X}, %w: {W}, %o: {R}) -> {R}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %init = arith.constant {init} : f32
+    %f = linalg.fill ins(%init : f32) outs(%o : {R}) -> {R}
+    %r = linalg.generic {{indexing_maps = [#in, #row, #out], iterator_types = ["parallel", "reduction"]}}
+        ins(%x, %w : {X}, {W}) outs(%f : {R}) {{
+    ^bb0(%a: f32, %b: f32, %acc: f32):
+      %p = arith.mulf %a, %b : f32
+      %m = {comb} %p, %acc : f32
+      linalg.yield %m : f32
+    }} -> {R}
+    return %r : {R}
+  }}""")
+    return ("#in = affine_map<(d0, d1) -> (d0, d1)>\n#row = affine_map<(d0, d1) -> (d1)>\n"
+            "#out = affine_map<(d0, d1) -> (d0)>\nmodule {\n" + "\n".join(funcs) + "\n}\n")
+
+
 def reduce_ops(rows=48, cols=3000):
     """Row reductions with each f32 combiner and an i32 sum (exact)."""
     X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
@@ -751,6 +774,7 @@ def entries():
     e["generic_ops"] = generic_ops()
     e["fuzz_generic"] = fuzz_generic()
     e["fuzz_rows"] = fuzz_rows()
+    e["generic_reduce"] = generic_reduce()
     e["rank0"] = """module {
   func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
       """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {

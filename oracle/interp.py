@@ -866,10 +866,10 @@ class Interp:
         maps = []
         for m in re.finditer(r"affine_map<\(([^)]*)\)\s*->\s*\(([^)]*)\)>", maps_src):
             maps.append([int(d.strip()[1:]) for d in m.group(2).split(",") if d.strip()])
-        its = re.search(r"iterator_types\s*=\s*\[([^\]]*)\]", attrs).group(1)
-        if "reduction" in its:
-            raise NotImplementedError("linalg.generic with reductions")
+        its = [t.strip().strip('"') for t in re.search(r"iterator_types\s*=\s*\[([^\]]*)\]", attrs).group(1).split(",")]
         o = env[outs[0]]
+        if "reduction" in its:
+            return self._generic_reduce(region, ins, outs, env, maps, its)
         dom = np.asarray(o.a).shape
         nd = len(dom)
 
@@ -888,6 +888,12 @@ class Interp:
         local = {}
         for i, nm in enumerate(bargs[:len(ins)]):
             local[nm] = place(env[ins[i]], maps[i]) if np.ndim(env[ins[i]].a) else T(np.broadcast_to(env[ins[i]].a, dom), env[ins[i]].elem)
+        return self._run_region_body(body[hdr.end():], local, dom, env, o.elem)
+
+    def _run_region_body(self, text, local, dom, env, out_elem):
+        """Evaluates the statements of a linalg.generic region (after its block
+        header) with the block arguments in `local`; returns the yielded
+        value converted to `out_elem`."""
 
         def get(nm):
             if nm in local:
@@ -911,14 +917,14 @@ class Interp:
               "arith.minsi": "min_signed", "arith.maxui": "max_unsigned", "arith.minui": "min_unsigned",
               "arith.ceildivsi": "ceildivsi", "arith.floordivsi": "floordivsi", "arith.ceildivui": "ceildivui",
               "math.ipowi": "powi"}
-        stmts = re.split(r"\n|(?<=[\w>)\]])\s+(?=%[\w.$-]+\s*=|linalg\.yield)", body[hdr.end():])
+        stmts = re.split(r"\n|(?<=[\w>)\]])\s+(?=%[\w.$-]+\s*=|linalg\.yield)", text)
         for st in stmts:
             st = re.sub(r"fastmath<[^>]*>", "", st).strip().rstrip("}").strip()
             if not st:
                 continue
             if st.startswith("linalg.yield"):
                 v = get(re.findall(r"%[\w.$-]+", st)[0])
-                return convert(v, o.elem) if v.elem != o.elem else T(_contig(v.a), v.elem)
+                return convert(v, out_elem) if v.elem != out_elem else T(_contig(v.a), v.elem)
             m = re.match(r"(%[\w.$-]+)\s*=\s*([\w.]+)\s*(.*)$", st)
             r_, opn, tail = m.group(1), m.group(2), m.group(3)
             lhs, _, ty = tail.rpartition(":")
@@ -976,6 +982,58 @@ class Interp:
             else:
                 raise NotImplementedError(f"region op {opn}")
         raise ValueError("linalg.generic region without linalg.yield")
+
+    def _generic_reduce(self, region, ins, outs, env, maps, its):
+        """linalg.generic with reduction loops, as convert-linalg-to-loops runs
+        it: for every point of the parallel dims, the reduction dims in
+        increasing order, each step's region evaluated with %out = the value
+        so far (initially the outs tensor)."""
+        o = env[outs[0]]
+        nd = len(its)
+        red = [d for d in range(nd) if its[d] == "reduction"]
+        # loop extents from the inputs' shapes through their maps
+        ext = [None] * nd
+        for nm, mp in zip(ins, maps):
+            sh = np.shape(env[nm].a)
+            for ax, d in enumerate(mp):
+                ext[d] = sh[ax]
+        for ax, d in enumerate(maps[len(ins)]):
+            ext[d] = np.shape(o.a)[ax]
+        if any(e is None for e in ext):
+            raise NotImplementedError("linalg.generic loop without an extent")
+        acc = T(np.array(o.a, copy=True), o.elem)
+        omap = maps[len(ins)]
+        pdom = tuple(ext[d] for d in omap)
+        for idx in np.ndindex(*[ext[d] for d in red]):
+            # views of the inputs at this reduction point, over the output's dims
+            def slice_in(nm, mp):
+                a = np.asarray(env[nm].a)
+                sel, keep = [], []
+                for ax, d in enumerate(mp):
+                    if d in red:
+                        sel.append(idx[red.index(d)])
+                    else:
+                        sel.append(slice(None))
+                        keep.append(d)
+                v = a[tuple(sel)]
+                order = [keep.index(d) for d in omap if d in keep]
+                v = np.transpose(v, order) if v.ndim else v
+                full = [pdom[i] if omap[i] in keep else 1 for i in range(len(omap))]
+                return T(np.broadcast_to(np.reshape(v, full), pdom), env[nm].elem)
+            step_ins = {nm: slice_in(nm, mp) for nm, mp in zip(ins, maps)}
+            acc = self._eval_region(region, ins, step_ins, acc, pdom, env)
+        return acc
+
+    def _eval_region(self, region, ins, vals, out_val, dom, env):
+        """One evaluation of a linalg.generic region over `dom` with the ins
+        block arguments bound to `vals` and the outs argument to `out_val`."""
+        body = region[region.index("^"):]
+        hdr = re.match(r"\^\w+\(([^)]*)\)\s*:", body)
+        bargs = [x.split(":")[0].strip() for x in hdr.group(1).split(",") if ":" in x]
+        sub = {}
+        for i, nm in enumerate(bargs):
+            sub[nm] = vals[ins[i]] if i < len(ins) else out_val
+        return self._run_region_body(body[hdr.end():], sub, dom, env, out_val.elem)
 
     def _scalar_arith(self, res, op, rest, env):
         names = re.findall(r"%[\w.$-]+", rest)

@@ -644,3 +644,20 @@ def test_fuzz_rows(gpu, n):
     for o, r in zip(outs, refs):
         same = (o == r) | (np.isnan(o) & np.isnan(r))
         assert same.all(), f"{int((~same).sum())} differ, e.g. gpu={o[~same][:3]} oracle={r[~same][:3]}"
+
+
+def test_generic_reduce(gpu):
+    """linalg.generic row reductions (split into an elementwise generic and a
+    row reduction): max bit-exact; the float sum within 1e-5 relative plus a
+    row-scaled absolute term (reduction order differs from the serial loop)."""
+    note("generic_reduce")
+    rng = np.random.default_rng(11)
+    x = rng.normal(size=(64, 1000)).astype(np.float32)
+    w = rng.normal(size=1000).astype(np.float32)
+    args = [x, w, np.zeros(64, np.float32)]
+    out, = run_gpu("generic_reduce", args, gpu, func="gred_max")
+    ref, = run_oracle("generic_reduce", args, func="gred_max")
+    assert np.array_equal(out, ref)
+    out, = run_gpu("generic_reduce", args, gpu, func="gred_sum")
+    ref, = run_oracle("generic_reduce", args, func="gred_sum")
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5 * np.abs(x * w).sum(axis=1).max())

@@ -339,3 +339,20 @@ def test_generic_regions_closed_form():
     rem = np.fmod(i64, 3)
     shl = ((i64 << 3) & 0xFFFFFFFF).astype(np.uint32).view(np.int32).astype(np.int64)
     assert np.array_equal(gm, (rem ^ shl).astype(np.int32) < 0)
+
+
+def test_generic_reduction_serial_loop():
+    """linalg.generic reductions run by the oracle as the CPU loop nest does:
+    max of x*w equals numpy's (exact); the sum equals a float32 left-to-right
+    loop bit for bit."""
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(64, 1000)).astype(np.float32)
+    w = rng.normal(size=1000).astype(np.float32)
+    o = np.zeros(64, np.float32)
+    mx, = run_oracle("generic_reduce", [x, w, o], func="gred_max")
+    assert np.array_equal(mx, np.max(x * w, axis=1))
+    sm, = run_oracle("generic_reduce", [x, w, o], func="gred_sum")
+    acc = np.zeros(64, np.float32)
+    for k in range(1000):
+        acc = (acc + (x[:, k] * w[k]).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(sm, acc)
