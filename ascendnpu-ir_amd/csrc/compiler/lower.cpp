@@ -472,7 +472,7 @@ bool isElementwiseOp(const Op *op) {
       "linalg.add", "linalg.sub", "linalg.mul", "linalg.div", "linalg.max", "linalg.min",
       "linalg.exp", "linalg.abs", "linalg.negf", "linalg.sqrt", "linalg.rsqrt", "linalg.reciprocal",
       "hfusion.isinf", "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot", "hfusion.erfinv",
-      "hfusion.bitcast"};
+      "hfusion.bitcast", "hfusion.signbit"};
   return s.count(op->name) != 0;
 }
 
@@ -700,6 +700,13 @@ std::string elementExpr(const Op *op, const std::vector<std::string> &a, const s
     std::string f = castExpr(a[0], at[0], Elem::F32, false);
     std::string pred = n == "hfusion.isinf" ? "__builtin_isinf" : n == "hfusion.isnan" ? "__builtin_isnan" : "__builtin_isfinite";
     return castExpr("(bool)" + pred + "(" + f + ")", Elem::I1, U, false);
+  }
+  if (n == "hfusion.signbit") {
+    // HFusionOps.td:1295: 1 / true where the sign bit is set (f16 -> f32 keeps it)
+    if (a.size() != 1 || (at[0] != Elem::F32 && at[0] != Elem::F16)) unsupported(op, "operand of hfusion.signbit");
+    if (U != Elem::I1 && U != Elem::I8) unsupported(op, "result type of hfusion.signbit");
+    std::string f = castExpr(a[0], at[0], Elem::F32, false);
+    return castExpr("(bool)__builtin_signbitf(" + f + ")", Elem::I1, U, false);
   }
   if (n == "hfusion.nextafter") {
     if (a.size() != 2 || at[0] != U || at[1] != U) unsupported(op, "operands of hfusion.nextafter");

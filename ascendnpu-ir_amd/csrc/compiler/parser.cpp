@@ -356,6 +356,21 @@ private:
     if (peek().kind != Tok::Symbol) fail("expected function name");
     f->name = next().text.substr(1);
     expectP("(");
+    if (peek().kind != Tok::Value && !isP(peek(), ")")) {
+      // an external declaration (`func.func private @f(f32) -> f32`): no
+      // body, nothing to lower
+      int depth = 1;
+      while (depth > 0 && peek().kind != Tok::End) {
+        if (isP(peek(), "(")) ++depth;
+        if (isP(peek(), ")")) --depth;
+        ++pos_;
+      }
+      while (peek().kind != Tok::End && !(peek().kind == Tok::Ident && peek().text == "func.func") && !isP(peek(), "}") &&
+             !isP(peek(), "{"))
+        ++pos_;
+      if (isP(peek(), "{")) fail("function body with unnamed arguments");
+      return;
+    }
     while (!isP(peek(), ")")) {
       if (peek().kind != Tok::Value) fail("expected function argument");
       std::string nm = next().text;
@@ -465,6 +480,60 @@ private:
         break;
       }
       expectP("=");
+    }
+    if (peek().kind == Tok::String && isP(peek(1), "(")) {
+      // generic form: "dialect.op"(%a, %b) {attrs} : (T1, T2) -> T3
+      Op *op = mod_->newOp();
+      op->name = next().text;
+      if (op->name.size() >= 2 && op->name.front() == '"') op->name = op->name.substr(1, op->name.size() - 2);
+      op->line = line;
+      expectP("(");
+      while (!isP(peek(), ")")) {
+        if (peek().kind == Tok::Value) op->operands.push_back(lookup(peek().text, peek().line));
+        ++pos_;
+      }
+      expectP(")");
+      if (isP(peek(), "{")) {
+        auto m = parseAttrDict();
+        for (auto &kv : m) op->attrs[kv.first] = kv.second;
+      }
+      expectP(":");
+      expectP("(");
+      while (!isP(peek(), ")")) {
+        if (!isP(peek(), ",")) parseType();
+        else ++pos_;
+      }
+      expectP(")");
+      if (!isP(peek(), "->")) fail("expected '->' in a generic operation type");
+      ++pos_;
+      std::vector<Type> rtypes;
+      if (isP(peek(), "(")) {
+        ++pos_;
+        while (!isP(peek(), ")")) {
+          if (isP(peek(), ",")) { ++pos_; continue; }
+          rtypes.push_back(parseType());
+        }
+        ++pos_;
+      } else {
+        rtypes.push_back(parseType());
+      }
+      size_t nres = multi ? (size_t)multi : resNames.size();
+      if (nres > rtypes.size()) fail("result count of '" + op->name + "'");
+      for (size_t i = 0; i < nres; ++i) {
+        Value *v = mod_->newValue();
+        v->type = rtypes[i];
+        v->def = op;
+        v->resultIdx = (int)i;
+        op->results.push_back(v);
+        if (multi) define(resNames[0] + "#" + std::to_string(i), v);
+        else define(resNames[i], v);
+      }
+      if (multi) scope_[resNames[0]] = op->results[0];
+      for (auto *v : op->operands) v->users.push_back(op);
+      op->srcBegin = toks_[firstTok].off;
+      op->srcEnd = toks_[pos_ - 1].end;
+      f.ops.push_back(op);
+      return;
     }
     if (peek().kind != Tok::Ident) fail("expected an operation name");
     Op *op = mod_->newOp();

@@ -171,12 +171,13 @@ def math_fns(n=4096):
 
 FP_OPS = [("isinf", "f32"), ("isnan", "f32"), ("isfinite", "f32"), ("isinf", "bf16"), ("isnan", "f16"),
           ("nextafter", "f32"), ("nextafter", "f16"), ("hypot", "f32"), ("hypot3", "f32"), ("hypot", "f16"),
-          ("erfinv", "f32"), ("erfinv", "f16"), ("bitcast", "f32")]
+          ("erfinv", "f32"), ("erfinv", "f16"), ("bitcast", "f32"), ("signbit", "f32"), ("signbit", "f16"),
+          ("signbit8", "f32")]
 
 
 def fp_ops(n=4096):
     """One module, one group per HFusion float op without outs (predicates,
-    nextafter, hypot with 2 and 3 operands, erfinv) and hfusion.bitcast."""
+    nextafter, hypot with 2 and 3 operands, erfinv, signbit) and hfusion.bitcast."""
     funcs = []
     for op, t in FP_OPS:
         X, B = _T([n], t), _T([n], "i1")
@@ -194,6 +195,11 @@ def fp_ops(n=4096):
         elif op == "hypot3":
             body = f"%r = hfusion.hypot %x, %y, %z : {X}, {X}, {X} -> {X}\n    return %r : {X}"
             sig = f"(%x: {X}, %y: {X}, %z: {X}) -> {X}"
+        elif op in ("signbit", "signbit8"):
+            # generic op form, as the reference's own tests write it
+            R = B if op == "signbit" else _T([n], "i8")
+            body = f'%r = "hfusion.signbit"(%x) : ({X}) -> {R}\n    return %r : {R}'
+            sig = f"(%x: {X}) -> {R}"
         elif op == "erfinv":
             body = f"%r = hfusion.erfinv %x : {X} -> {X}\n    return %r : {X}"
             sig = f"(%x: {X}) -> {X}"

@@ -361,7 +361,7 @@ def _single_op(op, rest, xs, rtypes):
 
 
 _NON_DPS = ("hfusion.isinf", "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot",
-            "hfusion.erfinv")
+            "hfusion.erfinv", "hfusion.signbit")
 
 
 def _non_dps(op, xs, shape, elem):
@@ -370,6 +370,12 @@ def _non_dps(op, xs, shape, elem):
     if op in ("hfusion.isinf", "hfusion.isnan", "hfusion.isfinite"):
         f = to_f32(xs[0])
         return {"hfusion.isinf": np.isinf, "hfusion.isnan": np.isnan, "hfusion.isfinite": np.isfinite}[op](f)
+    if op == "hfusion.signbit":
+        # HFusionOps.td:1295, expanded in hfusion-normalize-ops.mlir:3055-3080 as
+        # (bits & sign_mask) != 0 on the operand's own width
+        a = _contig(xs[0].a)
+        bits = a.view(np.uint32) >> 31 if xs[0].elem == "f32" else a.view(np.uint16) >> 15
+        return bits.astype(np.int8 if elem == "i8" else np.bool_)
     if op == "hfusion.nextafter":
         # IEEE nextafter (Normalize.cpp:8640-8660): one ulp from x toward y
         if elem == "f32":
@@ -472,6 +478,8 @@ def _statements(body):
             cur, depth = "", 0
     merged = []
     for s in out:
+        # generic op form `%r = "dialect.op"(%a) : (T) -> R` reads as `%r = dialect.op (%a) : ...`
+        s = re.sub(r'=\s*"([\w.]+)"\s*\(', r'= \1 (', s, count=1)
         st = s.strip()
         if merged and (st.startswith("(") or st.startswith(_HIVM_CONT)):
             merged[-1] += " " + s
@@ -544,8 +552,11 @@ def parse_funcs(text):
         while depth:
             depth += {"(": 1, ")": -1}.get(text[j], 0)
             j += 1
+        parts = _split_top(text[i:j - 1])
+        if parts and ":" not in parts[0]:
+            continue  # an external declaration `func.func private @f(f32) -> f32`
         args = []
-        for a in _split_top(text[i:j - 1]):
+        for a in parts:
             nm, ty = a.split(":", 1)
             args.append((nm.strip(), parse_type(ty.split("{")[0])))
         # body: first '{' after `attributes {...}` (or after the signature)

@@ -248,11 +248,12 @@ def fp_inputs(func, n=4096, seed=0x46504F50):
         if t == "bf16":
             return (f.view(np.uint32) >> 16).astype(np.uint16)  # truncation: exact bf16 values
         raise KeyError(t)
-    if op in ("isinf", "isnan", "isfinite"):
+    if op in ("isinf", "isnan", "isfinite", "signbit", "signbit8"):
         x = (rng.normal(0, 1e3, n)).astype(np.float32)
         x[:len(specials)] = specials
         x[rng.integers(0, n, 64)] = np.inf
         x[rng.integers(0, n, 64)] = np.nan
+        x[rng.integers(0, n, 64)] = -np.nan
         return [enc(x)]
     if op == "nextafter":
         x = rng.normal(0, 10, n).astype(np.float32)

@@ -203,6 +203,20 @@ def test_erfinv_round_trip(func):
     assert np.isnan(fg[(np.abs(fx) > 1) | np.isnan(fx)]).all()
 
 
+@pytest.mark.parametrize("func", ["signbit_f32", "signbit_f16", "signbit8_f32"])
+def test_signbit_against_numpy(func):
+    """hfusion.signbit (HFusionOps.td:1295), written in generic op form: the
+    sign bit of every value, -0.0 and -NaN included, as numpy's signbit reads
+    it from the float value."""
+    x, = fp_inputs(func)
+    got, = run_oracle("fp_ops", [x], func=func)
+    xf = x if x.dtype == np.float32 else x.view(np.float16).astype(np.float32)
+    want = np.signbit(xf)
+    assert want[3] and want.sum() > 1000 and np.signbit(xf[np.isnan(xf)]).any()
+    assert got.dtype == (np.int8 if func.startswith("signbit8") else np.bool_)
+    assert np.array_equal(got.astype(bool), want)
+
+
 def test_bitcast_op():
     x, o = fp_inputs("bitcast_f32")
     got, = run_oracle("fp_ops", [x, o], func="bitcast_f32")
