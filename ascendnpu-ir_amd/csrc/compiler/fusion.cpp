@@ -32,7 +32,7 @@ size_t rankOf(const Value *v) { return v->type.tensor ? v->type.shape.size() : 0
 bool isElementwiseName(const std::string &n) {
   static const std::set<std::string> s = {"linalg.elemwise_unary", "linalg.elemwise_binary", "linalg.fill",
                                           "hfusion.elemwise_unary", "hfusion.elemwise_binary", "hfusion.compare",
-                                          "hfusion.cast", "hfusion.select", "hfusion.bitcast", "hfusion.signbit", "hfusion.isinf",
+                                          "hfusion.cast", "hfusion.select", "hfusion.bitcast", "hfusion.signbit", "hfusion.cyl_bessel_i0", "hfusion.isinf",
                                           "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot",
                                           "hfusion.erfinv"};
   return s.count(n) != 0;

@@ -472,7 +472,7 @@ bool isElementwiseOp(const Op *op) {
       "linalg.add", "linalg.sub", "linalg.mul", "linalg.div", "linalg.max", "linalg.min",
       "linalg.exp", "linalg.abs", "linalg.negf", "linalg.sqrt", "linalg.rsqrt", "linalg.reciprocal",
       "hfusion.isinf", "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot", "hfusion.erfinv",
-      "hfusion.bitcast", "hfusion.signbit"};
+      "hfusion.bitcast", "hfusion.signbit", "hfusion.cyl_bessel_i0"};
   return s.count(op->name) != 0;
 }
 
@@ -724,6 +724,10 @@ std::string elementExpr(const Op *op, const std::vector<std::string> &a, const s
     std::string e = std::string(U == Elem::F32 ? "hf::hypot_scaled(" : "hf::hypot_direct(") + f[0] + ", " + f[1] + ", " + z +
                     ", " + std::to_string(a.size()) + ")";
     return castExpr(e, Elem::F32, U, false);
+  }
+  if (n == "hfusion.cyl_bessel_i0") {
+    if (a.size() != 1 || at[0] != U || (U != Elem::F32 && U != Elem::F16)) unsupported(op, "operand of hfusion.cyl_bessel_i0");
+    return castExpr("hf::cyl_bessel_i0_f(" + castExpr(a[0], U, Elem::F32, false) + ")", Elem::F32, U, false);
   }
   if (n == "hfusion.erfinv") {
     if (a.size() != 1 || at[0] != U || (U != Elem::F32 && U != Elem::F16)) unsupported(op, "operand of hfusion.erfinv");
@@ -1178,7 +1182,9 @@ struct RowEmitter {
                                                  "reciprocal", "mod", "modui", "tan", "acos", "acosh", "asin",
                                                  "asinh", "atan", "atanh", "sinh", "cosh", "lgamma", "atan2",
                                                  "divfhp", "powi"};
-    if (op->name == "hfusion.hypot" || op->name == "hfusion.erfinv") return true;
+    if (op->name == "hfusion.hypot" || op->name == "hfusion.erfinv" ||
+        op->name == "hfusion.cyl_bessel_i0")
+      return true;
     return costly.count(fn) || op->name == "arith.divf" || op->name == "linalg.div";
   }
 

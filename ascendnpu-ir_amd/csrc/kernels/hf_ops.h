@@ -272,6 +272,27 @@ __device__ __forceinline__ uint16_t nextafter_h(uint16_t x, uint16_t y) {
 // erfinv(y) in f32: Winitzki's closed-form estimate (a = 0.147), then Newton
 // steps on erf(x) - y in double, x -= (erf(x) - y) / (2/sqrt(pi) exp(-x^2)),
 // rounded once to f32.  |y| > 1 and NaN give NaN, y = +-1 gives +-inf.
+__device__ __forceinline__ float erfinv_f(float yf);
+
+// Modified Bessel function of the first kind, order 0: the power series
+// sum_k (x^2/4)^k / (k!)^2, every term positive (no cancellation), summed in
+// double until a term no longer changes the sum, rounded once to f32.  i0 is
+// even; |x| > 100 overflows f32 (i0(92) > FLT_MAX already) and gives +inf.
+// +-inf gives NaN, as the Chebyshev form e^x * c(x) / sqrt(x) of the reference
+// lowering does (inf / inf).
+__device__ __forceinline__ float cyl_bessel_i0_f(float xf) {
+  if (__builtin_isnan(xf) || __builtin_isinf(xf)) return __builtin_nanf("");
+  double x = __builtin_fabs((double)xf);
+  if (x > 100.0) return __builtin_inff();
+  double q = 0.25 * x * x, term = 1.0, sum = 1.0;
+  for (int k = 1; k < 400; ++k) {
+    term *= q / ((double)k * (double)k);
+    sum += term;
+    if (term < sum * 1e-17) break;
+  }
+  return (float)sum;
+}
+
 __device__ __forceinline__ float erfinv_f(float yf) {
   if (__builtin_isnan(yf) || __builtin_fabsf(yf) > 1.0f) return __builtin_nanf("");
   if (yf == 1.0f) return __builtin_inff();

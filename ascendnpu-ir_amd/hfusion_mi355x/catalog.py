@@ -172,12 +172,12 @@ def math_fns(n=4096):
 FP_OPS = [("isinf", "f32"), ("isnan", "f32"), ("isfinite", "f32"), ("isinf", "bf16"), ("isnan", "f16"),
           ("nextafter", "f32"), ("nextafter", "f16"), ("hypot", "f32"), ("hypot3", "f32"), ("hypot", "f16"),
           ("erfinv", "f32"), ("erfinv", "f16"), ("bitcast", "f32"), ("signbit", "f32"), ("signbit", "f16"),
-          ("signbit8", "f32")]
+          ("signbit8", "f32"), ("cylbesseli0", "f32"), ("cylbesseli0", "f16")]
 
 
 def fp_ops(n=4096):
     """One module, one group per HFusion float op without outs (predicates,
-    nextafter, hypot with 2 and 3 operands, erfinv, signbit) and hfusion.bitcast."""
+    nextafter, hypot with 2 and 3 operands, erfinv, signbit, cyl_bessel_i0) and hfusion.bitcast."""
     funcs = []
     for op, t in FP_OPS:
         X, B = _T([n], t), _T([n], "i1")
@@ -200,6 +200,9 @@ def fp_ops(n=4096):
             R = B if op == "signbit" else _T([n], "i8")
             body = f'%r = "hfusion.signbit"(%x) : ({X}) -> {R}\n    return %r : {R}'
             sig = f"(%x: {X}) -> {R}"
+        elif op == "cylbesseli0":
+            body = f"%r = hfusion.cyl_bessel_i0 %x : {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}) -> {X}"
         elif op == "erfinv":
             body = f"%r = hfusion.erfinv %x : {X} -> {X}\n    return %r : {X}"
             sig = f"(%x: {X}) -> {X}"

@@ -361,7 +361,7 @@ def _single_op(op, rest, xs, rtypes):
 
 
 _NON_DPS = ("hfusion.isinf", "hfusion.isnan", "hfusion.isfinite", "hfusion.nextafter", "hfusion.hypot",
-            "hfusion.erfinv", "hfusion.signbit")
+            "hfusion.erfinv", "hfusion.signbit", "hfusion.cyl_bessel_i0")
 
 
 def _non_dps(op, xs, shape, elem):
@@ -414,6 +414,14 @@ def _non_dps(op, xs, shape, elem):
                 raise NotImplementedError(f"hypot on {elem}")
         r[nan] = np.nan
         r[inf] = np.inf
+        return from_f32(r, elem)
+    if op == "hfusion.cyl_bessel_i0":
+        # hfusion-normalize-ops.mlir:3586-3830 expands it as the Cephes
+        # Chebyshev series of i0 (Clenshaw, Cephes `i0`); scipy.special.i0 is
+        # the same published algorithm, evaluated here in float64
+        import scipy.special
+        with np.errstate(all="ignore"):
+            r = scipy.special.i0(to_f32(xs[0]).astype(np.float64)).astype(f32)
         return from_f32(r, elem)
     if op == "hfusion.erfinv":
         import scipy.special

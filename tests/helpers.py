@@ -248,6 +248,11 @@ def fp_inputs(func, n=4096, seed=0x46504F50):
         if t == "bf16":
             return (f.view(np.uint32) >> 16).astype(np.uint16)  # truncation: exact bf16 values
         raise KeyError(t)
+    if op == "cylbesseli0":
+        x = rng.normal(0, 20, n).astype(np.float32)
+        x[:len(specials)] = specials
+        x[len(specials):len(specials) + 6] = [85.0, 92.0, -95.0, 100.5, 13.5, 1e-3]
+        return [enc(x)]
     if op in ("isinf", "isnan", "isfinite", "signbit", "signbit8"):
         x = (rng.normal(0, 1e3, n)).astype(np.float32)
         x[:len(specials)] = specials

@@ -217,6 +217,29 @@ def test_signbit_against_numpy(func):
     assert np.array_equal(got.astype(bool), want)
 
 
+def test_cyl_bessel_i0_closed_forms():
+    """hfusion.cyl_bessel_i0 against what fixes i0: i0(0) = 1, evenness,
+    the series sum_k (x^2/4)^k/(k!)^2 by brute force in exact rationals, the
+    large-x asymptote e^x/sqrt(2 pi x), f32 overflow past x ~ 91.9, and NaN
+    at +-inf (the Cephes form e^x * chbevl / sqrt(x) is inf / inf there)."""
+    from fractions import Fraction
+    xs = np.array([0.0, 0.5, -0.5, 1.0, 2.5, -7.0, 20.0, 60.0, 91.0, 92.0, np.inf, -np.inf, np.nan], np.float32)
+    got, = run_oracle("fp_ops", [np.resize(xs, 4096)], func="cylbesseli0_f32")
+    got = got[:len(xs)]
+    assert got[0] == 1.0 and got[1] == got[2]
+    for i in (1, 3, 4, 5, 6):
+        q = Fraction(float(xs[i])) ** 2 / 4
+        s, t = Fraction(0), Fraction(1)
+        for k in range(1, 200):
+            s += t
+            t = t * q / (k * k)
+        assert abs(float(got[i]) / float(s) - 1) < 1e-6, (xs[i], got[i], float(s))
+    x = 60.0
+    asym = math.exp(x) / math.sqrt(2 * math.pi * x) * (1 + 1 / (8 * x) + 9 / (2 * (8 * x) ** 2))
+    assert abs(float(got[7]) / asym - 1) < 1e-5
+    assert np.isfinite(got[8]) and np.isinf(got[9]) and np.isnan(got[10]) and np.isnan(got[11]) and np.isnan(got[12])
+
+
 def test_bitcast_op():
     x, o = fp_inputs("bitcast_f32")
     got, = run_oracle("fp_ops", [x, o], func="bitcast_f32")
