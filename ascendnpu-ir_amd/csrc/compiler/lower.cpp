@@ -891,6 +891,29 @@ bool isAlias(const Op *op) {
          op->name == "arith.constant" || op->name == "tensor.dim" || op->name.rfind("arith.index", 0) == 0;
 }
 
+// `permutation = [...]` of a linalg.transpose (out dim i is in dim perm[i]).
+std::vector<int64_t> permutationOf(const Op *op) {
+  std::vector<int64_t> perm;
+  std::string p = op->attr("permutation");
+  for (size_t i = 0; i < p.size();) {
+    size_t j = p.find(',', i);
+    if (j == std::string::npos) j = p.size();
+    perm.push_back(std::stoll(p.substr(i, j - i)));
+    i = j + 1;
+  }
+  if (op->ins.size() != 1 || op->outs.size() != 1) unsupported(op, "transpose operand form");
+  const size_t n = op->ins[0]->type.shape.size();
+  std::vector<bool> seen(n, false);
+  if (perm.size() != n) unsupported(op, "permutation length");
+  for (auto d : perm) {
+    if (d < 0 || d >= (int64_t)n || seen[d]) unsupported(op, "not a permutation");
+    seen[d] = true;
+  }
+  for (size_t i = 0; i < n; ++i)
+    if (op->outs[0]->type.shape[i] != op->ins[0]->type.shape[perm[i]]) unsupported(op, "transpose shapes");
+  return perm;
+}
+
 // Propagates D-dim maps through broadcasts, reductions and elementwise ops.
 void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
   Func &f = *A.f;
@@ -910,12 +933,20 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
     A.map[v] = m;
     return true;
   };
-  // seeds: full-rank tensors
-  for (Value *a : f.args)
-    if (a->type.tensor && a->type.shape == A.D && !exclude.count(a)) A.map[a] = all;
-  for (Op *op : f.ops)
-    for (Value *v : op->results)
+  // seeds: full-rank tensors (in a group with transposes, only its results:
+  // a tensor of the domain's shape may reach them through a permutation)
+  bool hasTranspose = false;
+  for (Op *op : f.ops) hasTranspose |= op->name == "linalg.transpose";
+  if (hasTranspose) {
+    for (Value *v : f.returns)
       if (v->type.tensor && v->type.shape == A.D && !exclude.count(v)) A.map[v] = all;
+  } else {
+    for (Value *a : f.args)
+      if (a->type.tensor && a->type.shape == A.D && !exclude.count(a)) A.map[a] = all;
+    for (Op *op : f.ops)
+      for (Value *v : op->results)
+        if (v->type.tensor && v->type.shape == A.D && !exclude.count(v)) A.map[v] = all;
+  }
   bool changed = true;
   while (changed) {
     changed = false;
@@ -929,6 +960,25 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
       };
       if (n == "linalg.broadcast") {
         if (!op->ins.empty()) changed |= setMap(op->ins[0], minus(op->dims), op);
+        continue;
+      }
+      if (n == "linalg.transpose") {
+        // out dim i is in dim perm[i]: in[perm[i]] spans what out[i] spans
+        std::vector<int64_t> perm = permutationOf(op);
+        const Value *o = op->results.empty() ? op->outs[0] : op->results[0];
+        const Value *in = op->ins[0];
+        if (A.map.count(o)) {
+          std::vector<int> mi(perm.size());
+          for (size_t i = 0; i < perm.size(); ++i) mi[perm[i]] = A.map[o][i];
+          changed |= setMap(in, mi, op);
+          for (auto *v : op->results) changed |= setMap(v, A.map[o], op);
+          changed |= setMap(op->outs[0], A.map[o], op);
+        } else if (A.map.count(in)) {
+          std::vector<int> mo(perm.size());
+          for (size_t i = 0; i < perm.size(); ++i) mo[i] = A.map[in][perm[i]];
+          changed |= setMap(o, mo, op);
+          for (auto *v : op->results) changed |= setMap(v, mo, op);
+        }
         continue;
       }
       if (n == "linalg.reduce" || n == "hfusion.reduce_with_index") {
@@ -1005,6 +1055,14 @@ std::vector<int64_t> largestShape(const Func &f, const std::set<const Value *> &
   };
   for (auto *a : f.args) consider(a);
   for (auto *op : f.ops) for (auto *v : op->results) consider(v);
+  bool hasTranspose = false;
+  for (auto *op : f.ops) hasTranspose |= op->name == "linalg.transpose";
+  if (hasTranspose) {
+    // the domain is the results' shape (results are stored contiguously)
+    for (auto *r : f.returns)
+      if (r->type.tensor && r->type.shape.size() == best.size()) return r->type.shape;
+    return best;
+  }
   for (auto *op : f.ops) for (auto *v : op->results)
     if (v->type.tensor && !exclude.count(v) && v->type.shape.size() == best.size() && v->type.shape != best)
       throw CompileError("group mixes full-rank tensors of different shapes (" + v->type.str() + ")");
@@ -1741,6 +1799,11 @@ struct EltwiseEmitter {
   int tmp = 0;
   int VEC = 4;
   int64_t N = 1;
+  // transposed inputs: tiles of 64 (dim TQ) x 64 (last dim) staged through
+  // LDS, read along TQ (their contiguous dim) and consumed along the last dim
+  int TQ = -1;
+  std::vector<const Value *> staged;
+  static constexpr int TILE = 64, PITCH = 65; // words; the odd pitch spreads both access patterns over all banks
 
   EltwiseEmitter(Analysis &a) : A(a) {}
   std::string fresh() { return "v" + std::to_string(tmp++); }
@@ -1750,7 +1813,11 @@ struct EltwiseEmitter {
   // flat index of the chunk base inside an input spanning dims `m`
   std::string indexFor(const std::vector<int> &m) {
     int r = (int)A.D.size();
-    if ((int)m.size() == r) return "base";
+    if ((int)m.size() == r) {
+      bool ident = true;
+      for (int i = 0; i < r; ++i) ident &= m[i] == i;
+      if (ident) return "base";
+    }
     if (m.empty()) return "0";
     std::string s;
     int64_t stride = 1;
@@ -1761,6 +1828,25 @@ struct EltwiseEmitter {
     }
     return s;
   }
+  // element stride of D dim d inside a tensor spanning dims `m` (0: absent)
+  int64_t strideOf(const std::vector<int> &m, int d) const {
+    int64_t stride = 1;
+    for (int i = (int)m.size() - 1; i >= 0; --i) {
+      if (m[i] == d) return stride;
+      stride *= A.D[m[i]];
+    }
+    return 0;
+  }
+  static std::string wordType(Elem e) { return elemBytes(e) == 8 ? "uint64_t" : "uint32_t"; }
+  static std::string uintOf(Elem e) {
+    switch (elemBytes(e)) {
+    case 1: return "uint8_t";
+    case 2: return "uint16_t";
+    case 4: return "uint32_t";
+    default: return "uint64_t";
+    }
+  }
+  std::string ldsName(const Value *v) const { return "lds_in" + std::to_string(v->argIdx); }
 
   void ensure(const Value *v) {
     if (name.count(v)) return;
@@ -1779,7 +1865,16 @@ struct EltwiseEmitter {
     std::string nm = "in" + std::to_string(i);
     name[v] = nm;
     bool hasLast = !m.empty() && m.back() == r - 1;
-    if (hasLast) {
+    int64_t sLast = r ? strideOf(m, r - 1) : 0;
+    const bool isStaged = std::find(staged.begin(), staged.end(), v) != staged.end();
+    std::string P = "((const " + M + "*)p" + std::to_string(i) + ")";
+    std::string cvt = v->type.elem == Elem::I1 ? " != 0" : "";
+    if (isStaged) {
+      vec[v] = true;
+      body << "    " << T << " " << nm << "[VEC];\n#pragma unroll\n    for (int e = 0; e < VEC; ++e) " << nm
+           << "[e] = __builtin_bit_cast(" << M << ", (" << uintOf(v->type.elem) << ")" << ldsName(v) << "[lq * " << PITCH
+           << " + ll + e])" << cvt << ";\n";
+    } else if (hasLast) {
       vec[v] = true;
       if (v->type.elem == Elem::I1) {
         body << "    " << T << " " << nm << "[VEC]; { uint8_t t_[VEC]; hf::vec_load<uint8_t, VEC>((const uint8_t*)p" << i << " + " << indexFor(m)
@@ -1787,36 +1882,43 @@ struct EltwiseEmitter {
       } else {
         body << "    " << T << " " << nm << "[VEC]; hf::vec_load<" << M << ", VEC>((const " << M << "*)p" << i << " + " << indexFor(m) << ", " << nm << ");\n";
       }
+    } else if (sLast) {
+      // a permuted input not staged through LDS: one load per element
+      vec[v] = true;
+      body << "    " << T << " " << nm << "[VEC];\n#pragma unroll\n    for (int e = 0; e < VEC; ++e) " << nm << "[e] = " << P << "["
+           << indexFor(m) << " + (int64_t)e * " << sLast << "ll]" << cvt << ";\n";
     } else {
       vec[v] = false;
-      body << "    const " << T << " " << nm << " = ((const " << M << "*)p" << i << ")[" << indexFor(m) << "];\n";
+      body << "    const " << T << " " << nm << " = " << P << "[" << indexFor(m) << "]" << cvt << ";\n";
     }
   }
 
-  KernelPlan run(const std::string &kname, const std::string &kind) {
-    Func &f = *A.f;
-    int r = (int)A.D.size();
-    N = 1;
-    for (auto d : A.D) N *= d;
-    int maxBytes = 1;
-    for (auto &kv : A.map) maxBytes = std::max(maxBytes, elemBytes(kv.first->type.elem));
-    VEC = std::max(1, 16 / maxBytes);
-    if (VEC > 8) VEC = 8;
-    int64_t L = r ? A.D[r - 1] : 1;
-    while (VEC > 1 && L % VEC) VEC /= 2;
-    // coordinates of the chunk base
-    std::ostringstream coords;
-    if (r > 1) {
-      coords << "    int64_t t_ = base;\n";
-      for (int d = r - 1; d >= 0; --d) {
-        coords << "    const int64_t c" << d << " = t_ % " << A.D[d] << "ll; t_ /= " << A.D[d] << "ll;\n";
-      }
-      coords << "    (void)t_;\n";
-      for (int d = 0; d < r; ++d) coords << "    (void)c" << d << ";\n";
-    } else if (r == 1) {
-      coords << "    const int64_t c0 = base; (void)c0;\n";
+  // Inputs whose contiguous dim is not the domain's last one (transposed
+  // loads): the most common such dim becomes TQ and its inputs are staged.
+  void chooseStaging() {
+    const int r = (int)A.D.size();
+    if (r < 2) return;
+    std::map<int, int> count;
+    for (const Value *a : A.f->args) {
+      if (!a->type.tensor || !A.map.count(a) || a->users.empty()) continue;
+      const auto &m = A.map.at(a);
+      if (m.empty() || m.back() == r - 1 || !strideOf(m, r - 1)) continue;
+      if (elemBytes(a->type.elem) > 8) continue;
+      ++count[m.back()];
     }
-    body << coords.str();
+    if (count.empty()) return;
+    int best = -1, bc = 0;
+    for (auto &kv : count) if (kv.second > bc) { best = kv.first; bc = kv.second; }
+    TQ = best;
+    for (const Value *a : A.f->args) {
+      if (!a->type.tensor || !A.map.count(a) || a->users.empty()) continue;
+      const auto &m = A.map.at(a);
+      if (!m.empty() && m.back() == TQ && strideOf(m, r - 1)) staged.push_back(a);
+    }
+  }
+
+  void emitOps() {
+    Func &f = *A.f;
     for (Op *op : f.ops) {
       const std::string &n = op->name;
       if (n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" || (n.rfind("arith.", 0) == 0 && !op->results[0]->type.tensor))
@@ -1827,14 +1929,14 @@ struct EltwiseEmitter {
         vec[op->results[0]] = false;
         continue;
       }
-      if (n == "linalg.broadcast") {
+      if (n == "linalg.broadcast" || n == "linalg.transpose") {
+        // both are views: the value at a domain point is the operand's value
+        // at the point its own map selects
         const Value *in = op->ins[0];
         ensure(in);
-        name[op->results[0]] = name[in];
-        vec[op->results[0]] = vec[in];
-        if (!vec[in]) {
-          // a broadcast value constant along the last dim stays uniform
-        }
+        const Value *res = op->results.empty() ? op->outs[0] : op->results[0];
+        name[res] = name[in];
+        vec[res] = vec[in];
         continue;
       }
       if (!isElementwiseOp(op)) unsupported(op, "op in an elementwise group");
@@ -1862,6 +1964,11 @@ struct EltwiseEmitter {
       const Value *v = f.returns[i];
       if (v->argIdx >= 0) continue;
       if (v->type.shape != A.D) throw CompileError("elementwise group result must span the whole domain");
+      if (A.map.count(v)) {
+        const auto &m = A.map.at(v);
+        for (size_t d = 0; d < m.size(); ++d)
+          if (m[d] != (int)d) throw CompileError("elementwise group result stored in a permuted layout");
+      }
       ensure(v);
       std::string src = name[v];
       Elem e = v->type.elem;
@@ -1872,6 +1979,34 @@ struct EltwiseEmitter {
       }
       body << "    hf::vec_store<" << mtype(e) << ", VEC>((" << mtype(e) << "*)" << resultPtr(A, i) << " + base, " << src << ");\n";
     }
+  }
+
+  KernelPlan run(const std::string &kname, const std::string &kind) {
+    int r = (int)A.D.size();
+    N = 1;
+    for (auto d : A.D) N *= d;
+    int maxBytes = 1;
+    for (auto &kv : A.map) maxBytes = std::max(maxBytes, elemBytes(kv.first->type.elem));
+    VEC = std::max(1, 16 / maxBytes);
+    if (VEC > 8) VEC = 8;
+    int64_t L = r ? A.D[r - 1] : 1;
+    while (VEC > 1 && L % VEC) VEC /= 2;
+    chooseStaging();
+    if (TQ >= 0) return runTiled(kname, kind);
+    // coordinates of the chunk base
+    std::ostringstream coords;
+    if (r > 1) {
+      coords << "    int64_t t_ = base;\n";
+      for (int d = r - 1; d >= 0; --d) {
+        coords << "    const int64_t c" << d << " = t_ % " << A.D[d] << "ll; t_ /= " << A.D[d] << "ll;\n";
+      }
+      coords << "    (void)t_;\n";
+      for (int d = 0; d < r; ++d) coords << "    (void)c" << d << ";\n";
+    } else if (r == 1) {
+      coords << "    const int64_t c0 = base; (void)c0;\n";
+    }
+    body << coords.str();
+    emitOps();
     KernelPlan p;
     p.kernelName = kname;
     p.kind = kind;
@@ -1891,6 +2026,79 @@ struct EltwiseEmitter {
     if (grid > (1 << 20)) grid = 1 << 20;
     if (grid < 1) grid = 1;
     p.grid[0] = (unsigned)grid;
+    p.block[0] = block;
+    return p;
+  }
+
+  // Tiles of 64 (TQ) x 64 (last dim) of the domain.  Each staged input's
+  // tile is read with loads along TQ (its own contiguous dim, VQ elements a
+  // lane) into an LDS tile [TQ][last] of 32/64-bit words; then each lane
+  // computes VEC consecutive elements along the last dim from LDS and the
+  // other inputs, and stores them with one access.  Replaces the Ascend
+  // Transpose2D / Transpose3D templates
+  // (bishengir/lib/Template/lib/Vector/Transpose/Transpose2D.cpp).
+  KernelPlan runTiled(const std::string &kname, const std::string &kind) {
+    const int r = (int)A.D.size(), LD = r - 1;
+    const int64_t DQ = A.D[TQ], DL = A.D[LD];
+    const int64_t NTQ = (DQ + TILE - 1) / TILE, NTL = (DL + TILE - 1) / TILE;
+    int64_t NO = 1;
+    for (int d = 0; d < r; ++d) if (d != TQ && d != LD) NO *= A.D[d];
+    const int64_t NT = NO * NTQ * NTL;
+    const int block = 256;
+    // the per-element body (coordinates c<d> and `base` set by the loop)
+    emitOps();
+    std::ostringstream k;
+    KernelPlan p;
+    p.kernelName = kname;
+    p.kind = kind;
+    p.variant = "LDS-staged transpose tiles (64x64)";
+    k << "extern \"C\" __global__ __launch_bounds__(" << block << ") void " << kname << "("
+      << kernelParamList(A, p.kargs, false) << ") {\n"
+      << "  constexpr int VEC = " << VEC << ";\n";
+    for (const Value *v : staged)
+      k << "  __shared__ " << wordType(v->type.elem) << " " << ldsName(v) << "[" << TILE * PITCH << "];\n";
+    k << "  for (int64_t tile = blockIdx.x; tile < " << NT << "ll; tile += gridDim.x) {\n"
+      << "    int64_t t_ = tile;\n"
+      << "    const int64_t tl_ = t_ % " << NTL << "ll; t_ /= " << NTL << "ll;\n"
+      << "    const int64_t tq_ = t_ % " << NTQ << "ll; t_ /= " << NTQ << "ll;\n";
+    for (int d = r - 1; d >= 0; --d) {
+      if (d == TQ || d == LD) continue;
+      k << "    const int64_t c" << d << " = t_ % " << A.D[d] << "ll; t_ /= " << A.D[d] << "ll; (void)c" << d << ";\n";
+    }
+    k << "    __syncthreads(); // the previous tile's LDS reads are done\n";
+    for (const Value *v : staged) {
+      const auto &m = A.map.at(v);
+      std::string M = mtype(v->type.elem), U = uintOf(v->type.elem), W = wordType(v->type.elem);
+      int VQ = std::max(1, 16 / elemBytes(v->type.elem));
+      if (VQ > 8) VQ = 8;
+      while (VQ > 1 && DQ % VQ) VQ /= 2;
+      const int lanesPerRow = TILE / VQ;
+      k << "    for (int i_ = threadIdx.x; i_ < " << TILE * lanesPerRow << "; i_ += " << block << ") {\n"
+        << "      const int lq0 = (i_ % " << lanesPerRow << ") * " << VQ << ", ll = i_ / " << lanesPerRow << ";\n"
+        << "      const int64_t c" << TQ << " = tq_ * " << TILE << " + lq0, c" << LD << " = tl_ * " << TILE << " + ll;\n"
+        << "      if (c" << LD << " >= " << DL << "ll || c" << TQ << " >= " << DQ << "ll) continue;\n"
+        << "      const " << M << "* src_ = (const " << M << "*)p" << v->argIdx << " + (" << indexFor(m) << ");\n"
+        << "      " << M << " w_[" << VQ << "];\n";
+      if (VQ > 1)
+        k << "      hf::vec_load<" << M << ", " << VQ << ">(src_, w_);\n";
+      else
+        k << "      w_[0] = src_[0];\n";
+      k << "#pragma unroll\n      for (int j = 0; j < " << VQ << "; ++j) " << ldsName(v) << "[(lq0 + j) * " << PITCH
+        << " + ll] = (" << W << ")__builtin_bit_cast(" << U << ", w_[j]);\n"
+        << "    }\n";
+    }
+    const int lanesPerRow = TILE / VEC;
+    k << "    __syncthreads();\n"
+      << "    for (int i_ = threadIdx.x; i_ < " << TILE * lanesPerRow << "; i_ += " << block << ") {\n"
+      << "      const int lq = i_ / " << lanesPerRow << ", ll = (i_ % " << lanesPerRow << ") * VEC;\n"
+      << "      const int64_t c" << TQ << " = tq_ * " << TILE << " + lq, c" << LD << " = tl_ * " << TILE << " + ll;\n"
+      << "      if (c" << LD << " >= " << DL << "ll || c" << TQ << " >= " << DQ << "ll) continue;\n"
+      << "      (void)lq; (void)ll;\n"
+      << "      int64_t base = 0;\n";
+    for (int d = 0; d < r; ++d) k << "      base = base * " << A.D[d] << "ll + c" << d << ";\n";
+    k << "      {\n" << body.str() << "      }\n    }\n  }\n}\n";
+    p.source = k.str();
+    p.grid[0] = (unsigned)std::max<int64_t>(1, std::min<int64_t>(NT, 8192));
     p.block[0] = block;
     return p;
   }
@@ -2486,6 +2694,28 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
 // same number of elements: every tensor shares the flat element index, so the
 // group runs over one flat dimension and the reshapes vanish.  The buffer
 // descriptors (taken before this) keep the arguments' own shapes.
+// A linalg.transpose that only moves unit dims keeps the row-major element
+// order: it becomes a reshape view (as compile-pure-elemwise-with-foldable-
+// transpose.mlir:5-12 has it, between an expand and a collapse).
+static void foldTrivialTransposes(Func &f) {
+  for (Op *op : f.ops) {
+    if (op->name != "linalg.transpose") continue;
+    std::vector<int64_t> perm = permutationOf(op);
+    const auto &in = op->ins[0]->type.shape;
+    std::vector<int64_t> order;
+    for (auto d : perm) if (in[d] != 1) order.push_back(d);
+    if (!std::is_sorted(order.begin(), order.end())) continue;
+    Value *src = op->ins[0], *dst = op->outs[0];
+    auto &du = dst->users;
+    du.erase(std::remove(du.begin(), du.end(), op), du.end());
+    op->name = "tensor.collapse_shape";
+    op->operands = {src};
+    op->ins.clear();
+    op->outs.clear();
+    if (op->results.empty()) unsupported(op, "transpose without a result");
+  }
+}
+
 static void flattenReshapeGroup(Func &f) {
   bool anyReshape = false;
   int64_t n = -1;
@@ -2706,6 +2936,391 @@ static void splitGenericReductions(Module &m, Func &f) {
   }
 }
 
+// ======================================================================
+// Domain collapse.  Unit dims are dropped and adjacent dims that every
+// tensor of the group treats alike (spans both, consecutively, or neither)
+// merge into one, so a rank-N group becomes the smallest equivalent domain:
+// a last-axis reduction over [B, S, H] becomes rows x H, a middle-axis one
+// over [A, R, B] keeps three dims.  Value shapes and the `dimensions` of
+// reduce / broadcast ops follow; buffer descriptors (taken before) keep the
+// arguments' own shapes, and row-major buffers are unchanged by the merge.
+// ======================================================================
+bool collapseDomain(Analysis &A) {
+  const std::vector<int64_t> D = A.D;
+  const int r = (int)D.size();
+  if (r == 0) return false;
+  // indexing maps of generics and transposes are not rewritten: such groups
+  // keep their domain
+  for (const Op *op : A.f->ops)
+    if (op->name == "linalg.generic" || op->name == "linalg.transpose") return false;
+  auto nonUnit = [&](const std::vector<int> &m) {
+    std::vector<int> k;
+    for (int x : m) if (D[x] != 1) k.push_back(x);
+    return k;
+  };
+  std::vector<int> keep;
+  for (int d = 0; d < r; ++d) if (D[d] != 1) keep.push_back(d);
+  std::vector<int> grp(r, -1);
+  int g = -1;
+  for (size_t idx = 0; idx < keep.size(); ++idx) {
+    const int d = keep[idx];
+    bool merge = idx > 0;
+    if (merge) {
+      const int p = keep[idx - 1];
+      for (auto &kv : A.map) {
+        std::vector<int> mk = nonUnit(kv.second);
+        auto ip = std::find(mk.begin(), mk.end(), p), id = std::find(mk.begin(), mk.end(), d);
+        const bool hp = ip != mk.end(), hd = id != mk.end();
+        if (hp != hd || (hp && id != ip + 1)) { merge = false; break; }
+      }
+    }
+    if (!merge) ++g;
+    grp[d] = g;
+  }
+  const int ng = g + 1;
+  std::vector<int64_t> nD(std::max(ng, 1), 1);
+  for (int d = 0; d < r; ++d) if (grp[d] >= 0) nD[grp[d]] *= D[d];
+  auto newMap = [&](const std::vector<int> &m) {
+    std::vector<int> out;
+    for (int x : m) {
+      if (D[x] == 1) continue;
+      if (out.empty() || out.back() != grp[x]) out.push_back(grp[x]);
+    }
+    if (ng == 0 && !m.empty()) out.push_back(0);
+    return out;
+  };
+  if (nD == D) return false;
+  // op dims first (they need the old maps)
+  for (Op *op : A.f->ops) {
+    if (op->name == "linalg.reduce" || op->name == "hfusion.reduce_with_index") {
+      if (op->ins.empty() || !A.map.count(op->ins[0])) continue;
+      const auto &mi = A.map.at(op->ins[0]);
+      std::vector<int> nm = newMap(mi);
+      std::vector<int64_t> nd;
+      for (int64_t pos : op->dims) {
+        if (pos < 0 || pos >= (int64_t)mi.size()) unsupported(op, "reduction dimension out of range");
+        int x = mi[pos];
+        if (D[x] == 1) continue;
+        int q = (int)(std::find(nm.begin(), nm.end(), grp[x]) - nm.begin());
+        if (nd.empty() || nd.back() != q) nd.push_back(q);
+      }
+      if (nd.empty()) unsupported(op, "reduction over unit dimensions only");
+      op->dims = nd;
+    } else if (op->name == "linalg.broadcast") {
+      if (op->results.empty() || !A.map.count(op->results[0]) || !A.map.count(op->ins[0])) continue;
+      std::vector<int> no = newMap(A.map.at(op->results[0])), ni = newMap(A.map.at(op->ins[0]));
+      std::vector<int64_t> nd;
+      for (size_t q = 0; q < no.size(); ++q)
+        if (std::find(ni.begin(), ni.end(), no[q]) == ni.end()) nd.push_back((int64_t)q);
+      op->dims = nd;
+    }
+  }
+  for (auto &kv : A.map) {
+    Value *v = const_cast<Value *>(kv.first);
+    kv.second = newMap(kv.second);
+    std::vector<int64_t> s;
+    for (int x : kv.second) s.push_back(nD[x]);
+    v->type.shape = s;
+  }
+  A.D = nD;
+  return true;
+}
+
+// ======================================================================
+// Column programs (ANY_PBR): reductions over one (collapsed) dim k that is
+// not the innermost one, reduce_with_index along any dim, and row groups
+// whose broadcast layout the row programs do not take.  Each thread owns
+// one point of the other dims and walks dim k in increasing order, so every
+// fold runs in the CPU loop nest's order (linalg-to-loops visits the reduced
+// index serially per output element); consecutive threads take consecutive
+// points of the innermost kept dim, so each step's loads coalesce.  Values
+// that vary along k are lambdas of r re-evaluated in each pass (inputs are
+// re-read from memory rather than kept); values that do not are computed
+// once per thread.  Replaces the Ascend ReduceRA / ReduceARA /
+// ReduceRA_With_Index templates
+// (bishengir/lib/Template/lib/Vector/Reduction/ReduceRA.cpp, ReduceARA.cpp,
+// ReduceRA_With_Index.cpp); kind inference "other reduce -> ANY_PBR" is
+// FusibleHelper.cpp:63-64.
+// ======================================================================
+struct ColumnEmitter {
+  Analysis &A;
+  int K = -1; // the reduced dim of D
+  std::ostringstream body;
+  struct CV {
+    std::string name;
+    bool lazy = false; // a lambda of r
+  };
+  std::map<const Value *, CV> val;
+  int tmp = 0;
+
+  explicit ColumnEmitter(Analysis &a) : A(a) {}
+  std::string fresh() { return "v" + std::to_string(tmp++); }
+
+  // element strides of a tensor spanning D dims `m` (row-major)
+  std::vector<int64_t> strides(const std::vector<int> &m) const {
+    std::vector<int64_t> s(m.size(), 1);
+    for (int i = (int)m.size() - 2; i >= 0; --i) s[i] = s[i + 1] * A.D[m[i + 1]];
+    return s;
+  }
+  // flat offset of the thread's point (coordinate of K excluded) and the
+  // stride along K
+  std::pair<std::string, int64_t> offsetOf(const std::vector<int> &m) const {
+    std::vector<int64_t> s = strides(m);
+    std::string off;
+    int64_t sk = 0;
+    for (size_t i = 0; i < m.size(); ++i) {
+      if (m[i] == K) { sk = s[i]; continue; }
+      std::string t = "c" + std::to_string(m[i]) + " * " + std::to_string(s[i]) + "ll";
+      off = off.empty() ? t : off + " + " + t;
+    }
+    return {off.empty() ? "0ll" : off, sk};
+  }
+  bool spansK(const Value *v) const {
+    auto it = A.map.find(v);
+    return it != A.map.end() && std::find(it->second.begin(), it->second.end(), K) != it->second.end();
+  }
+  std::string at(const Value *v, const std::string &r = "r") const {
+    const CV &x = val.at(v);
+    return x.lazy ? x.name + "(" + r + ")" : x.name;
+  }
+
+  void ensure(const Value *v) {
+    if (val.count(v)) return;
+    if (!v->type.tensor || v->isConst) {
+      if (v->isConst) val[v] = {constExpr(v, v->type.elem), false};
+      else if (v->argIdx >= 0) val[v] = {scalarArgExpr(A, v->argIdx), false};
+      else throw CompileError("non-constant scalar " + v->name);
+      return;
+    }
+    if (v->argIdx < 0) throw CompileError("internal: value " + v->name + " used before definition");
+    const int i = v->argIdx;
+    auto [off, sk] = offsetOf(A.map.at(v));
+    std::string T = ctype(v->type.elem), M = mtype(v->type.elem);
+    std::string nm = "in" + std::to_string(i);
+    std::string P = "((const " + M + "*)p" + std::to_string(i) + ")";
+    std::string cvt = v->type.elem == Elem::I1 ? " != 0" : "";
+    if (spansK(v)) {
+      body << "    const int64_t " << nm << "_o = " << off << ";\n"
+           << "    auto " << nm << " = [&](int64_t r) -> " << T << " { return " << P << "[" << nm << "_o + r * " << sk << "ll]" << cvt
+           << "; };\n";
+      val[v] = {nm, true};
+    } else {
+      body << "    const " << T << " " << nm << " = " << P << "[" << off << "]" << cvt << ";\n";
+      val[v] = {nm, false};
+    }
+  }
+
+  std::string initOf(const Op *op, const Value *init, Elem t, const std::string &identity) {
+    if (init->def && init->def->name == "linalg.fill") {
+      const Value *c = init->def->ins[0];
+      ensure(c);
+      return c->isConst ? constExpr(c, t) : val[c].name;
+    }
+    if (init->argIdx >= 0) {
+      ensure(init);
+      if (val[init].lazy) unsupported(op, "reduction init varying along the reduced dim");
+      return val[init].name;
+    }
+    if (init->isConst) return constExpr(init, t);
+    if (init->def && init->def->name == "tensor.empty") return identity;
+    unsupported(op, "reduction init must be a linalg.fill, an argument or tensor.empty");
+  }
+
+  void emitReduce(const Op *op, int64_t RK) {
+    if (op->ins.size() != 1 || op->outs.size() != 1) unsupported(op, "multi-operand linalg.reduce");
+    const Value *x = op->ins[0];
+    ensure(x);
+    Elem t = x->type.elem;
+    Combiner cb = combinerFor(op, op->combiner, t);
+    std::string T = ctype(t), nm = fresh();
+    std::string init = initOf(op, op->outs[0], t, cb.identity);
+    body << "    " << T << " " << nm << " = " << init << ";\n";
+    if (val[x].lazy)
+      body << "    for (int64_t r = 0; r < " << RK << "ll; ++r) " << nm << " = " << subst(cb.expr, at(x), nm) << ";\n";
+    else // a value constant along the reduced dim still folds RK times
+      body << "    for (int64_t r = 0; r < " << RK << "ll; ++r) " << nm << " = " << subst(cb.expr, val[x].name, nm) << ";\n";
+    val[op->results[0]] = {nm, false};
+  }
+
+  // hfusion.reduce_with_index: the region of HFusionOps.cpp:1507-1653 folded
+  // serially from the init: res = max/min(in, v); upd = res OGT/OLT v (sgt,
+  // slt, ugt, ult for integers); i = upd ? index : i; v = res.
+  void emitReduceWithIndex(const Op *op, int64_t RK) {
+    if (op->ins.empty() || op->ins.size() > 2 || op->outs.size() != 2 || op->results.size() != 2)
+      unsupported(op, "reduce_with_index operand form");
+    const Value *x = op->ins[0];
+    ensure(x);
+    const Value *xi = op->ins.size() == 2 ? op->ins[1] : nullptr;
+    if (xi) ensure(xi);
+    Elem t = x->type.elem, it = op->outs[1]->type.elem;
+    std::string kindS = op->angleKind.empty() ? op->attr("reduce_kind", "max") : op->angleKind;
+    std::string T = ctype(t), IT = ctype(it);
+    std::string fold, cmp;
+    if (t == Elem::F32) {
+      if (kindS == "max") { fold = "hf::maximumf(X, V)"; cmp = "(R_ > V)"; }
+      else if (kindS == "min") { fold = "hf::minimumf(X, V)"; cmp = "(R_ < V)"; }
+      else unsupported(op, "reduce_with_index kind '" + kindS + "' on floats");
+    } else if (isInt(t) && t != Elem::I1) {
+      std::string UT = t == Elem::I8 ? "uint8_t" : t == Elem::I16 ? "uint16_t" : t == Elem::I32 ? "uint32_t" : "uint64_t";
+      if (kindS == "max") { fold = "((X) > (V) ? (X) : (V))"; cmp = "(R_ > V)"; }
+      else if (kindS == "min") { fold = "((X) < (V) ? (X) : (V))"; cmp = "(R_ < V)"; }
+      else if (kindS == "max_unsigned" || kindS == "maxui") {
+        fold = "((" + UT + ")(X) > (" + UT + ")(V) ? (X) : (V))"; cmp = "((" + UT + ")R_ > (" + UT + ")V)";
+      } else if (kindS == "min_unsigned" || kindS == "minui") {
+        fold = "((" + UT + ")(X) < (" + UT + ")(V) ? (X) : (V))"; cmp = "((" + UT + ")R_ < (" + UT + ")V)";
+      } else unsupported(op, "reduce_with_index kind '" + kindS + "'");
+    } else {
+      unsupported(op, std::string("reduce_with_index over ") + elemName(t));
+    }
+    if (!isInt(it) || it == Elem::I1) unsupported(op, "reduce_with_index index type");
+    auto repl = [](std::string e, const std::string &from, const std::string &to) {
+      for (size_t p = e.find(from); p != std::string::npos; p = e.find(from, p + to.size())) e.replace(p, from.size(), to);
+      return e;
+    };
+    std::string nv = fresh(), ni = fresh();
+    body << "    " << T << " " << nv << " = " << initOf(op, op->outs[0], t, "0") << ";\n"
+         << "    " << IT << " " << ni << " = " << initOf(op, op->outs[1], it, "0") << ";\n"
+         << "    for (int64_t r = 0; r < " << RK << "ll; ++r) {\n"
+         << "      const " << T << " x_ = " << at(x) << ";\n"
+         << "      const " << T << " R_ = " << repl(repl(fold, "X", "x_"), "V", nv) << ";\n"
+         << "      if (" << repl(cmp, "V", nv) << ") " << ni << " = (" << IT << ")("
+         << (xi ? at(xi) : std::string("r")) << ");\n"
+         << "      " << nv << " = R_;\n    }\n";
+    val[op->results[0]] = {nv, false};
+    val[op->results[1]] = {ni, false};
+  }
+
+  void emitElementwise(const Op *op) {
+    std::vector<const Value *> opsv;
+    for (auto *v : op->ins) opsv.push_back(v);
+    for (auto *v : op->operands) opsv.push_back(v);
+    bool lazy = false;
+    for (auto *v : opsv) { ensure(v); lazy |= val[v].lazy; }
+    const Value *res = op->results[0];
+    Elem U = res->type.elem;
+    std::vector<Elem> at_;
+    std::vector<std::string> args;
+    for (auto *v : opsv) { at_.push_back(v->type.elem); args.push_back(at(v)); }
+    std::string nm = fresh(), T = ctype(U);
+    if (lazy)
+      body << "    auto " << nm << " = [&](int64_t r) -> " << T << " { return " << elementExpr(op, args, at_, U) << "; };\n";
+    else
+      body << "    const " << T << " " << nm << " = " << elementExpr(op, args, at_, U) << ";\n";
+    val[res] = {nm, lazy};
+  }
+
+  KernelPlan run(const std::string &kname, const std::string &kind) {
+    Func &f = *A.f;
+    const int n = (int)A.D.size();
+    // the reduced dim: the one every reduction folds
+    for (const Op *op : f.ops) {
+      if (op->name != "linalg.reduce" && op->name != "hfusion.reduce_with_index") continue;
+      if (!A.map.count(op->ins[0])) unsupported(op, "reduction input outside the group's domain");
+      const auto &mi = A.map.at(op->ins[0]);
+      if (op->dims.size() != 1) unsupported(op, "reduction over non-adjacent dimensions");
+      int d = mi.at(op->dims[0]);
+      if (K >= 0 && K != d) unsupported(op, "reductions over different dimensions in one group");
+      K = d;
+    }
+    if (K < 0) throw CompileError("internal: column program without a reduction");
+    const int64_t RK = A.D[K];
+    // thread -> point of the other dims (innermost kept dim fastest)
+    int64_t P = 1;
+    for (int d = 0; d < n; ++d) if (d != K) P *= A.D[d];
+    std::ostringstream coords;
+    coords << "    int64_t t_ = pt; (void)t_;\n";
+    for (int d = n - 1; d >= 0; --d) {
+      if (d == K) continue;
+      coords << "    const int64_t c" << d << " = t_ % " << A.D[d] << "ll; t_ /= " << A.D[d] << "ll; (void)c" << d << ";\n";
+    }
+    body << coords.str();
+    for (Op *op : f.ops) {
+      const std::string &nmo = op->name;
+      if (nmo == "tensor.empty" || nmo == "arith.constant" || nmo == "tensor.dim" ||
+          (nmo.rfind("arith.", 0) == 0 && !op->results.empty() && !op->results[0]->type.tensor))
+        continue;
+      if (nmo == "linalg.fill") {
+        ensure(op->ins[0]);
+        val[op->results[0]] = val[op->ins[0]];
+        continue;
+      }
+      if (nmo == "linalg.broadcast") {
+        ensure(op->ins[0]);
+        val[op->results[0]] = val[op->ins[0]];
+        continue;
+      }
+      if (nmo == "linalg.reduce") { emitReduce(op, RK); continue; }
+      if (nmo == "hfusion.reduce_with_index") { emitReduceWithIndex(op, RK); continue; }
+      if (!isElementwiseOp(op)) unsupported(op, "op in a reduction group");
+      emitElementwise(op);
+    }
+    for (size_t i = 0; i < f.returns.size(); ++i) {
+      const Value *v = f.returns[i];
+      if (v->argIdx >= 0 && A.resultTied[i] == v->argIdx) continue;
+      ensure(v);
+      if (!A.map.count(v)) throw CompileError("cannot place result " + v->name + " in the group's domain");
+      auto [off, sk] = offsetOf(A.map.at(v));
+      Elem e = v->type.elem;
+      std::string M = mtype(e), ptr = "((" + M + "*)" + resultPtr(A, i) + ")";
+      if (spansK(v))
+        body << "    for (int64_t r = 0; r < " << RK << "ll; ++r) " << ptr << "[" << off << " + r * " << sk << "ll] = (" << M << ")("
+             << at(v) << ");\n";
+      else
+        body << "    " << ptr << "[" << off << "] = (" << M << ")(" << at(v) << ");\n";
+    }
+    KernelPlan p;
+    p.kernelName = kname;
+    p.kind = kind;
+    p.variant = "column program, serial along dim " + std::to_string(K) + " of " + std::to_string(n);
+    const int block = 256;
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(" << block << ") void " << kname << "(" << kernelParamList(A, p.kargs, false)
+      << ") {\n"
+      << "  for (int64_t pt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; pt < " << P
+      << "ll; pt += (int64_t)gridDim.x * blockDim.x) {\n"
+      << body.str() << "  }\n}\n";
+    p.source = k.str();
+    int64_t grid = (P + block - 1) / block;
+    p.grid[0] = (unsigned)std::max<int64_t>(1, std::min<int64_t>(grid, 1 << 20));
+    p.block[0] = block;
+    return p;
+  }
+};
+
+// Every linalg.reduce of the group folds exactly the last dim of its input,
+// which spans the whole domain.
+bool reducesLastDimOnly(const Analysis &A) {
+  const int last = (int)A.D.size() - 1;
+  for (const Op *op : A.f->ops) {
+    if (op->name == "hfusion.reduce_with_index") return false;
+    if (op->name != "linalg.reduce") continue;
+    if (op->ins.empty() || !A.map.count(op->ins[0])) return false;
+    const auto &mi = A.map.at(op->ins[0]);
+    if ((int)mi.size() != last + 1 || op->dims.size() != 1 || mi.at(op->dims[0]) != last) return false;
+  }
+  return true;
+}
+
+// A lone reduce_with_index (max/min, f32, no index input) over the last dim of
+// a group argument: the split-row streaming kernel of hf_argmax.h.
+bool isRowArgReduce(const Func &f) {
+  const Op *rw = nullptr;
+  for (const Op *op : f.ops) {
+    const std::string &n = op->name;
+    if (n == "tensor.empty" || n == "linalg.fill" || n == "arith.constant" || n == "tensor.dim") continue;
+    if (n != "hfusion.reduce_with_index" || rw) return false;
+    rw = op;
+  }
+  if (!rw || rw->ins.size() != 1 || rw->outs.size() != 2) return false;
+  const Value *x = rw->ins[0];
+  if (x->argIdx < 0 || x->type.elem != Elem::F32) return false;
+  const int rank = (int)x->type.shape.size();
+  if (rw->dims.size() != 1 || rw->dims[0] != rank - 1) return false;
+  std::string k = rw->angleKind.empty() ? rw->attr("reduce_kind", "max") : rw->angleKind;
+  Elem ie = rw->outs[1]->type.elem;
+  return (k == "max" || k == "min") && (ie == Elem::I32 || ie == Elem::I64);
+}
+
 std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
   std::vector<KernelPlan> out;
   bool anyEntry = false;
@@ -2777,9 +3392,10 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
       p = lowerSingleOp(A, kname, single);
     } else if (kind == "SINGLE_CUBE") {
       p = lowerMatmul(A, kname);
-    } else if (kind == "REDUCE_WITH_INDEX") {
+    } else if (kind == "REDUCE_WITH_INDEX" && isRowArgReduce(f)) {
       p = lowerReduceWithIndex(A, kname);
     } else {
+      foldTrivialTransposes(f);
       flattenReshapeGroup(f);
       A.D = largestShape(f, {});
       if (A.D.empty()) {
@@ -2790,9 +3406,22 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
         if (!anyTensor) throw CompileError("group @" + f.name + " has no tensor to iterate over");
       }
       inferMaps(A, {});
-      if (kind == "LAST_AXIS_PBR") {
-        RowEmitter e(A, opt);
-        p = e.run(kname, kind);
+      if (kind == "LAST_AXIS_PBR" || kind == "REDUCE_WITH_INDEX") {
+        // row programs take rank <= 2 groups reducing the last dim; a higher
+        // rank collapses first; anything else is a column program
+        bool rows = kind == "LAST_AXIS_PBR";
+        if (rows && (A.D.size() > 2 || !reducesLastDimOnly(A))) {
+          collapseDomain(A);
+          rows = A.D.size() <= 2 && reducesLastDimOnly(A);
+        }
+        if (rows) {
+          RowEmitter e(A, opt);
+          p = e.run(kname, "LAST_AXIS_PBR");
+        } else {
+          collapseDomain(A);
+          ColumnEmitter e(A);
+          p = e.run(kname, "ANY_PBR");
+        }
       } else {
         bool anyBrc = false;
         for (auto &kv : A.map) anyBrc |= kv.second.size() != A.D.size();
@@ -2807,7 +3436,8 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     std::string declared = f.fusionKind();
     if (!declared.empty() && declared != p.kind && !(declared == "PURE_ELEMWISE" && p.kind == "ANY_PB") &&
         !(declared == "ANY_PB" && p.kind == "PURE_ELEMWISE") && !(declared == "ANY_PBR" && p.kind == "LAST_AXIS_PBR") &&
-        !(declared == "LAST_AXIS_PBR" && p.kind == "REDUCE_WITH_INDEX"))
+        !(declared == "LAST_AXIS_PBR" && p.kind == "REDUCE_WITH_INDEX") &&
+        !(declared == "LAST_AXIS_PBR" && p.kind == "ANY_PBR"))
       p.variant += " (declared " + declared + ")";
     out.push_back(p);
   }

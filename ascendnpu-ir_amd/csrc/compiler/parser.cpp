@@ -346,6 +346,28 @@ private:
     scope_[name] = v;
   }
 
+  // After the `)` of an unnamed-argument list: an optional `-> type` or
+  // `-> (types)` and an optional `attributes {...}` of an external declaration.
+  void skipSignatureTail() {
+    if (isP(peek(), "->")) {
+      ++pos_;
+      if (isP(peek(), "(")) {
+        int depth = 0;
+        do {
+          if (isP(peek(), "(")) ++depth;
+          if (isP(peek(), ")")) --depth;
+          ++pos_;
+        } while (depth > 0 && peek().kind != Tok::End);
+      } else {
+        parseType();
+      }
+    }
+    if (peek().kind == Tok::Ident && peek().text == "attributes") {
+      ++pos_;
+      parseAttrDict();
+    }
+  }
+
   void parseFunc() {
     const size_t begin = toks_[pos_].off;
     ++pos_; // func.func
@@ -365,9 +387,7 @@ private:
         if (isP(peek(), ")")) --depth;
         ++pos_;
       }
-      while (peek().kind != Tok::End && !(peek().kind == Tok::Ident && peek().text == "func.func") && !isP(peek(), "}") &&
-             !isP(peek(), "{"))
-        ++pos_;
+      skipSignatureTail();
       if (isP(peek(), "{")) fail("function body with unnamed arguments");
       return;
     }
@@ -402,6 +422,8 @@ private:
       ++pos_;
       f->attrs = parseAttrDict();
     }
+    // a declaration with named (or no) arguments and no body
+    if (!isP(peek(), "{")) return;
     expectP("{");
     while (!isP(peek(), "}")) {
       if (peek().kind == Tok::End) fail("unterminated function body");

@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -28,6 +29,19 @@ struct hfr_kernel {
   hfr_module *owner = nullptr;
 };
 
+// element size of a manifest element type name (i1 is one byte)
+int elemSize(const std::string &e) {
+  if (e == "f64" || e == "i64" || e == "index") return 8;
+  if (e == "f32" || e == "i32") return 4;
+  if (e == "f16" || e == "bf16" || e == "i16") return 2;
+  return 1;
+}
+
+struct Buf {
+  std::string elem;
+  std::vector<int64_t> shape;
+};
+
 struct Karg {
   enum Kind { Param, Result, Workspace } kind;
   int index;
@@ -42,6 +56,7 @@ struct hfr_group {
   bool wsZero = false;
   uint64_t algoBytes = 0, algoOps = 0;
   std::vector<std::string> paramRoles;
+  std::vector<Buf> paramBufs, resultBufs;
   std::vector<int> resultTied;
   std::vector<Karg> kargs;
   void *ownWs = nullptr;
@@ -73,6 +88,8 @@ struct hfr_program {
 
 namespace {
 
+constexpr size_t HFR_MAX_KARGS = 64;
+
 thread_local std::string g_err;
 
 int fail(int code, const std::string &msg) {
@@ -81,6 +98,9 @@ int fail(int code, const std::string &msg) {
 }
 
 int hipFail(hipError_t e, const char *what) {
+  // the error is reported through the return code; clear HIP's last-error
+  // state so it does not resurface in the caller's next, unrelated HIP call
+  (void)hipGetLastError();
   return fail(HFR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
@@ -104,8 +124,18 @@ int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
     else if (key == "workspace") { int z = 0; is >> g.wsBytes >> z; g.wsZero = z != 0; }
     else if (key == "algo_bytes") is >> g.algoBytes;
     else if (key == "algo_ops") is >> g.algoOps;
-    else if (key == "param") { int i; std::string role; is >> i >> role; g.paramRoles.push_back(role); }
-    else if (key == "result") { int i, tied; is >> i >> tied; g.resultTied.push_back(tied); }
+    else if (key == "param" || key == "result") {
+      int i, tied = -1, rank = 0;
+      std::string role;
+      Buf b;
+      is >> i;
+      if (key == "param") is >> role;
+      else is >> tied;
+      is >> b.elem >> rank;
+      for (int d = 0; d < rank && is; ++d) { int64_t x; is >> x; b.shape.push_back(x); }
+      if (key == "param") { g.paramRoles.push_back(role); g.paramBufs.push_back(b); }
+      else { g.resultTied.push_back(tied); g.resultBufs.push_back(b); }
+    }
     else if (key == "karg") {
       std::string k;
       is >> k;
@@ -158,15 +188,54 @@ int readManifest(const char *path, std::vector<std::vector<std::string>> &groups
 }
 
 int launchRaw(hipFunction_t fn, const hfr_launch_cfg &cfg, const uint64_t *args, size_t nargs, void *stream) {
-  std::vector<uint64_t> buf(args, args + nargs);
-  size_t sz = buf.size() * sizeof(uint64_t);
-  void *extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, buf.empty() ? nullptr : buf.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+  // the argument buffer is copied by hipModuleLaunchKernel; a fixed array
+  // keeps launches free of heap allocation
+  uint64_t buf[HFR_MAX_KARGS];
+  if (nargs > HFR_MAX_KARGS) return fail(HFR_ERR_INVALID, "too many kernel arguments");
+  for (size_t i = 0; i < nargs; ++i) buf[i] = args[i];
+  size_t sz = nargs * sizeof(uint64_t);
+  void *extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, nargs ? buf : nullptr, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
                    HIP_LAUNCH_PARAM_END};
   hipError_t e = hipModuleLaunchKernel(fn, cfg.grid[0], cfg.grid[1] ? cfg.grid[1] : 1, cfg.grid[2] ? cfg.grid[2] : 1,
                                        cfg.block[0], cfg.block[1] ? cfg.block[1] : 1, cfg.block[2] ? cfg.block[2] : 1,
                                        cfg.lds_bytes, (hipStream_t)stream, nullptr, extra);
   if (e != hipSuccess) return hipFail(e, "hipModuleLaunchKernel");
   return HFR_OK;
+}
+
+// Checks a group launch's arguments (counts, null pointers).
+int checkGroupArgs(const hfr_group *g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults) {
+  if (!g) return fail(HFR_ERR_INVALID, "null group");
+  if (nparams != g->paramRoles.size())
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " takes " + std::to_string(g->paramRoles.size()) +
+                                     " arguments, got " + std::to_string(nparams));
+  if (nresults != g->resultTied.size())
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " has " + std::to_string(g->resultTied.size()) +
+                                     " results, got " + std::to_string(nresults));
+  if (nparams && !params) return fail(HFR_ERR_INVALID, "null params array");
+  for (size_t i = 0; i < nparams; ++i)
+    if (g->paramRoles[i] != "scalar" && params[i] == 0)
+      return fail(HFR_ERR_INVALID, "null device pointer for argument " + std::to_string(i));
+  for (size_t i = 0; i < nresults; ++i)
+    if (g->resultTied[i] < 0 && (!results || !results[i]))
+      return fail(HFR_ERR_INVALID, "null device pointer for result " + std::to_string(i));
+  return HFR_OK;
+}
+
+// Assembles the kernel arguments (params, own result buffers, workspace) and
+// launches the group's kernel.
+int launchGroup(const hfr_group *g, const uint64_t *params, void *const *results, void *ws, void *stream) {
+  uint64_t args[HFR_MAX_KARGS];
+  if (g->kargs.size() > HFR_MAX_KARGS) return fail(HFR_ERR_INVALID, "too many kernel arguments");
+  size_t n = 0;
+  for (auto &a : g->kargs) {
+    switch (a.kind) {
+    case Karg::Param: args[n++] = params[a.index]; break;
+    case Karg::Result: args[n++] = (uint64_t)(uintptr_t)results[a.index]; break;
+    case Karg::Workspace: args[n++] = (uint64_t)(uintptr_t)ws; break;
+    }
+  }
+  return launchRaw(g->fn, g->cfg, args, n, stream);
 }
 
 } // namespace
@@ -201,7 +270,10 @@ int hfr_kernel_get(hfr_module_t m, const char *name, hfr_kernel_t *out) {
   if (!m || !name || !out) return fail(HFR_ERR_INVALID, "null argument to hfr_kernel_get");
   hipFunction_t fn;
   hipError_t e = hipModuleGetFunction(&fn, m->mod, name);
-  if (e != hipSuccess) return fail(HFR_ERR_NOT_FOUND, std::string("kernel '") + name + "' not in " + m->path);
+  if (e != hipSuccess) {
+    (void)hipGetLastError(); // reported here, not by the caller's next HIP call
+    return fail(HFR_ERR_NOT_FOUND, std::string("kernel '") + name + "' not in " + m->path);
+  }
   auto k = new hfr_kernel();
   k->fn = fn;
   k->owner = m;
@@ -239,8 +311,23 @@ int hfr_group_load(const char *manifest_path, const char *func, hfr_group_t *out
   if (rc) return rc;
   hipError_t e = hipModuleGetFunction(&g->fn, g->mod->mod, g->kernel.c_str());
   if (e != hipSuccess) {
+    (void)hipGetLastError();
     hfr_module_unload(g->mod);
     return fail(HFR_ERR_NOT_FOUND, "kernel '" + g->kernel + "' not in " + hsaco);
+  }
+  // the group's own workspace lives on the device current at load time, so
+  // that launches stay asynchronous
+  if (g->wsBytes) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    e = hipMalloc(&g->ownWs, g->wsBytes);
+    if (e == hipSuccess) e = hipMemset(g->ownWs, 0, g->wsBytes);
+    if (e != hipSuccess) {
+      if (g->ownWs) (void)hipFree(g->ownWs);
+      hfr_module_unload(g->mod);
+      return hipFail(e, "workspace allocation");
+    }
+    g->ownWsDevice = dev;
   }
   *out = g.release();
   return HFR_OK;
@@ -251,10 +338,10 @@ int hfr_group_unload(hfr_group_t g) {
   int rc = HFR_OK;
   if (g->ownWs) {
     int cur = 0;
-    hipGetDevice(&cur);
-    if (g->ownWsDevice >= 0) hipSetDevice(g->ownWsDevice);
+    (void)hipGetDevice(&cur);
+    if (g->ownWsDevice >= 0) (void)hipSetDevice(g->ownWsDevice);
     hipError_t e = hipFree(g->ownWs);
-    hipSetDevice(cur);
+    (void)hipSetDevice(cur);
     if (e != hipSuccess) rc = hipFail(e, "hipFree(workspace)");
   }
   if (g->mod) {
@@ -279,44 +366,16 @@ int hfr_group_info_get(hfr_group_t g, hfr_group_info *info) {
 
 int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
                      void *workspace, void *stream) {
-  if (!g) return fail(HFR_ERR_INVALID, "null group");
-  if (nparams != g->paramRoles.size())
-    return fail(HFR_ERR_INVALID, "group @" + g->func + " takes " + std::to_string(g->paramRoles.size()) +
-                                     " arguments, got " + std::to_string(nparams));
-  if (nresults != g->resultTied.size())
-    return fail(HFR_ERR_INVALID, "group @" + g->func + " has " + std::to_string(g->resultTied.size()) +
-                                     " results, got " + std::to_string(nresults));
-  if (nparams && !params) return fail(HFR_ERR_INVALID, "null params array");
-  for (size_t i = 0; i < nparams; ++i)
-    if (g->paramRoles[i] != "scalar" && params[i] == 0)
-      return fail(HFR_ERR_INVALID, "null device pointer for argument " + std::to_string(i));
-  for (size_t i = 0; i < nresults; ++i)
-    if (g->resultTied[i] < 0 && (!results || !results[i]))
-      return fail(HFR_ERR_INVALID, "null device pointer for result " + std::to_string(i));
+  int rc = checkGroupArgs(g, params, nparams, results, nresults);
+  if (rc) return rc;
   void *ws = workspace;
   if (g->wsBytes && !ws) {
     int dev = 0;
-    hipGetDevice(&dev);
-    if (!g->ownWs || g->ownWsDevice != dev) {
-      if (g->ownWs) return fail(HFR_ERR_INVALID, "group workspace belongs to another device");
-      hipError_t e = hipMalloc(&g->ownWs, g->wsBytes);
-      if (e != hipSuccess) return hipFail(e, "hipMalloc(workspace)");
-      e = hipMemset(g->ownWs, 0, g->wsBytes);
-      if (e != hipSuccess) return hipFail(e, "hipMemset(workspace)");
-      g->ownWsDevice = dev;
-    }
+    (void)hipGetDevice(&dev);
+    if (dev != g->ownWsDevice) return fail(HFR_ERR_INVALID, "group workspace belongs to another device");
     ws = g->ownWs;
   }
-  std::vector<uint64_t> args;
-  args.reserve(g->kargs.size());
-  for (auto &a : g->kargs) {
-    switch (a.kind) {
-    case Karg::Param: args.push_back(params[a.index]); break;
-    case Karg::Result: args.push_back((uint64_t)(uintptr_t)results[a.index]); break;
-    case Karg::Workspace: args.push_back((uint64_t)(uintptr_t)ws); break;
-    }
-  }
-  return launchRaw(g->fn, g->cfg, args.data(), args.size(), stream);
+  return launchGroup(g, params, results, ws, stream);
 }
 
 } // extern "C"
@@ -341,10 +400,10 @@ void freeProgram(hfr_program *p) {
     if (st.group) hfr_group_unload(st.group);
   if (p->ownWs) {
     int cur = 0;
-    hipGetDevice(&cur);
-    if (p->ownWsDevice >= 0) hipSetDevice(p->ownWsDevice);
-    hipFree(p->ownWs);
-    hipSetDevice(cur);
+    (void)hipGetDevice(&cur);
+    if (p->ownWsDevice >= 0) (void)hipSetDevice(p->ownWsDevice);
+    (void)hipFree(p->ownWs);
+    (void)hipSetDevice(cur);
   }
   delete p;
 }
@@ -436,6 +495,17 @@ int hfr_program_load(const char *manifest_path, const char *name, hfr_program_t 
       }
     }
   }
+  if (p->wsBytes) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    hipError_t e = hipMalloc(&p->ownWs, p->wsBytes);
+    if (e != hipSuccess) {
+      p->ownWs = nullptr;
+      freeProgram(p);
+      return hipFail(e, "hipMalloc(program workspace)");
+    }
+    p->ownWsDevice = dev;
+  }
   *out = p;
   return HFR_OK;
 }
@@ -474,13 +544,8 @@ int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, 
   char *ws = (char *)workspace;
   if (p->wsBytes && !ws) {
     int dev = 0;
-    hipGetDevice(&dev);
-    if (!p->ownWs || p->ownWsDevice != dev) {
-      if (p->ownWs) return fail(HFR_ERR_INVALID, "program workspace belongs to another device");
-      hipError_t e = hipMalloc(&p->ownWs, p->wsBytes);
-      if (e != hipSuccess) return hipFail(e, "hipMalloc(program workspace)");
-      p->ownWsDevice = dev;
-    }
+    (void)hipGetDevice(&dev);
+    if (dev != p->ownWsDevice) return fail(HFR_ERR_INVALID, "program workspace belongs to another device");
     ws = (char *)p->ownWs;
   }
   auto resolve = [&](const Binding &b) -> uint64_t {
@@ -506,3 +571,72 @@ int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, 
 }
 
 } // extern "C"
+
+// ---------------------------------------------------------------------------
+// MLIR C-interface entry: ranked memref descriptors in the IR's argument order
+// (the layout `_mlir_ciface_*` functions receive; the reference runner's
+// UnrankedMemRefType wraps a pointer to one of these,
+// bishengir/lib/ExecutionEngine/BiShengIRRunnerUtils.cpp:99-110).
+// { T *allocated; T *aligned; int64_t offset; int64_t sizes[R]; int64_t strides[R]; }
+namespace {
+
+int descPointer(const Buf &b, const void *desc, const char *what, size_t idx, uint64_t &out) {
+  if (!desc) return fail(HFR_ERR_INVALID, std::string("null descriptor for ") + what + " " + std::to_string(idx));
+  const char *d = (const char *)desc;
+  const char *aligned = *(char *const *)(d + sizeof(void *));
+  const int64_t offset = *(const int64_t *)(d + 2 * sizeof(void *));
+  const int64_t *sizes = (const int64_t *)(d + 2 * sizeof(void *) + sizeof(int64_t));
+  const int64_t *strides = sizes + b.shape.size();
+  int64_t expect = 1;
+  for (size_t k = b.shape.size(); k-- > 0;) {
+    if (sizes[k] != b.shape[k])
+      return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": size " + std::to_string(sizes[k]) +
+                                       " in dim " + std::to_string(k) + ", the group expects " + std::to_string(b.shape[k]));
+    if (sizes[k] != 1 && strides[k] != expect)
+      return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) +
+                                       ": strided memref (the group reads dense row-major buffers)");
+    expect *= sizes[k];
+  }
+  if (!aligned) return fail(HFR_ERR_INVALID, std::string("null aligned pointer for ") + what + " " + std::to_string(idx));
+  if (offset < 0) return fail(HFR_ERR_INVALID, std::string("negative offset for ") + what + " " + std::to_string(idx));
+  out = (uint64_t)(uintptr_t)(aligned + offset * elemSize(b.elem));
+  return HFR_OK;
+}
+
+} // namespace
+
+extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t ndescs, void *stream) {
+  if (!g) return fail(HFR_ERR_INVALID, "null group");
+  size_t nown = 0;
+  for (int t : g->resultTied) nown += t < 0;
+  if (ndescs != g->paramRoles.size() + nown)
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " takes " + std::to_string(g->paramRoles.size() + nown) +
+                                     " descriptors, got " + std::to_string(ndescs));
+  if (ndescs && !descs) return fail(HFR_ERR_INVALID, "null descriptor array");
+  uint64_t params[HFR_MAX_KARGS];
+  void *results[HFR_MAX_KARGS];
+  if (g->paramRoles.size() > HFR_MAX_KARGS || g->resultTied.size() > HFR_MAX_KARGS)
+    return fail(HFR_ERR_INVALID, "too many group arguments");
+  for (size_t i = 0; i < g->paramRoles.size(); ++i) {
+    if (g->paramRoles[i] == "scalar") {
+      if (!descs[i]) return fail(HFR_ERR_INVALID, "null scalar pointer for argument " + std::to_string(i));
+      uint64_t bits = 0;
+      std::memcpy(&bits, descs[i], (size_t)elemSize(g->paramBufs[i].elem));
+      params[i] = bits;
+      continue;
+    }
+    int rc = descPointer(g->paramBufs[i], descs[i], "argument", i, params[i]);
+    if (rc) return rc;
+  }
+  size_t k = g->paramRoles.size();
+  for (size_t j = 0; j < g->resultTied.size(); ++j) {
+    results[j] = nullptr;
+    if (g->resultTied[j] >= 0) continue;
+    uint64_t ptr = 0;
+    int rc = descPointer(g->resultBufs[j], descs[k++], "result", j, ptr);
+    if (rc) return rc;
+    results[j] = (void *)(uintptr_t)ptr;
+  }
+  return hfr_group_launch(g, params, g->paramRoles.size(), results, g->resultTied.size(), nullptr, stream);
+}
+

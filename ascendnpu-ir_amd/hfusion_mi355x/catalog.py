@@ -730,6 +730,172 @@ def fp8_quant(rows=64, cols=4096):
 """
 
 
+
+# ------------------------------------------------------------ ANY_PBR / rank-N
+def any_pbr_ops():
+    """Reductions over a non-last axis (ANY_PBR: FusibleHelper.cpp:63-64),
+    reduce_with_index along a middle / first axis, and rank-3 last-axis
+    groups, one function each."""
+    f = []
+    # sum of squares over the middle axis of [8, 64, 100], scaled
+    X, O = _T([8, 64, 100], "f32"), _T([8, 100], "f32")
+    f.append(f"""  func.func @sumsq_mid(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %h = arith.constant 5.000000e-01 : f32
+    %e0 = tensor.empty() : {X}
+    %sq = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%x, %x : {X}, {X}) outs(%e0 : {X}) -> {X}
+    %e1 = tensor.empty() : {O}
+    %i = linalg.fill ins(%z : f32) outs(%e1 : {O}) -> {O}
+    %s = linalg.reduce {{arith.addf}} ins(%sq : {X}) outs(%i : {O}) dimensions = [1]
+    %r = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%s, %h : {O}, f32) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    # softmax along the first axis of [512, 1000] -> bf16
+    X, R, B = _T([512, 1000], "f32"), _T([1000], "f32"), _T([512, 1000], "bf16")
+    f.append(f"""  func.func @softmax_d0(%x: {X}, %o: {B}) -> {B}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %z = arith.constant 0.000000e+00 : f32
+    %e0 = tensor.empty() : {R}
+    %f0 = linalg.fill ins(%ninf : f32) outs(%e0 : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f0 : {R}) dimensions = [0]
+    %e1 = tensor.empty() : {X}
+    %bm = linalg.broadcast ins(%m : {R}) outs(%e1 : {X}) dimensions = [0]
+    %e2 = tensor.empty() : {X}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%x, %bm : {X}, {X}) outs(%e2 : {X}) -> {X}
+    %e3 = tensor.empty() : {X}
+    %ex = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%d : {X}) outs(%e3 : {X}) -> {X}
+    %e4 = tensor.empty() : {R}
+    %f1 = linalg.fill ins(%z : f32) outs(%e4 : {R}) -> {R}
+    %s = linalg.reduce {{arith.addf}} ins(%ex : {X}) outs(%f1 : {R}) dimensions = [0]
+    %e5 = tensor.empty() : {X}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e5 : {X}) dimensions = [0]
+    %e6 = tensor.empty() : {X}
+    %q = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%ex, %bs : {X}, {X}) outs(%e6 : {X}) -> {X}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%q : {X}) outs(%o : {B}) -> {B}
+    return %r : {B}
+  }}""")
+    # argmax along the middle axis of [16, 300, 40]
+    X, V, I = _T([16, 300, 40], "f32"), _T([16, 40], "f32"), _T([16, 40], "i32")
+    f.append(f"""  func.func @argmax_mid(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %c0 = arith.constant 0 : i32
+    %ninf = arith.constant 0xFF800000 : f32
+    %v0 = linalg.fill ins(%ninf : f32) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : i32) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index {{tie_break_left = true}} <max> ins(%x : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}""")
+    # argmin along the first axis of an i32 [1000, 64], i64 indices
+    X, V, I = _T([1000, 64], "i32"), _T([64], "i32"), _T([64], "i64")
+    f.append(f"""  func.func @argmin_d0_i32(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %c0 = arith.constant 0 : i64
+    %big = arith.constant 2147483647 : i32
+    %v0 = linalg.fill ins(%big : i32) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : i64) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index <min> ins(%x : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [0] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}""")
+    # argmax over the last axis of exp(x) (fused producer: not the split-row kernel)
+    X, V, I = _T([64, 777], "f32"), _T([64], "f32"), _T([64], "i32")
+    f.append(f"""  func.func @argmax_fused(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %c0 = arith.constant 0 : i32
+    %ninf = arith.constant 0xFF800000 : f32
+    %e = tensor.empty() : {X}
+    %n = linalg.elemwise_unary {{fun = #linalg.unary_fn<negf>}} ins(%x : {X}) outs(%e : {X}) -> {X}
+    %v0 = linalg.fill ins(%ninf : f32) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : i32) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index <max> ins(%n : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}""")
+    # rank-3 last-axis sum of [8, 64, 100]
+    X, O = _T([8, 64, 100], "f32"), _T([8, 64], "f32")
+    f.append(f"""  func.func @sum_rank3_last(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %i = linalg.fill ins(%z : f32) outs(%o : {O}) -> {O}
+    %s = linalg.reduce {{arith.addf}} ins(%x : {X}) outs(%i : {O}) dimensions = [2]
+    return %s : {O}
+  }}""")
+    # rank-3 last-axis max with a [S, C] operand broadcast along the batch
+    # dim: no row layout fits, the column program takes it
+    X, Bv, O = _T([4, 16, 256], "f32"), _T([16, 256], "f32"), _T([4, 16], "f32")
+    f.append(f"""  func.func @max_bias_rank3(%x: {X}, %b: {Bv}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %e0 = tensor.empty() : {X}
+    %bb = linalg.broadcast ins(%b : {Bv}) outs(%e0 : {X}) dimensions = [0]
+    %e1 = tensor.empty() : {X}
+    %a = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%x, %bb : {X}, {X}) outs(%e1 : {X}) -> {X}
+    %i = linalg.fill ins(%ninf : f32) outs(%o : {O}) -> {O}
+    %m = linalg.reduce {{arith.maximumf}} ins(%a : {X}) outs(%i : {O}) dimensions = [2]
+    return %m : {O}
+  }}""")
+    # i32 sum over the first two axes of [6, 50, 33] (one collapsed reduced dim)
+    X, O = _T([6, 50, 33], "i32"), _T([33], "i32")
+    f.append(f"""  func.func @isum_d01(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %c0 = arith.constant 0 : i32
+    %i = linalg.fill ins(%c0 : i32) outs(%o : {O}) -> {O}
+    %s = linalg.reduce {{arith.addi}} ins(%x : {X}) outs(%i : {O}) dimensions = [0, 1]
+    return %s : {O}
+  }}""")
+    return "module {\n" + "\n".join(f) + "\n}\n"
+
+
+ANY_PBR_OPS = ["sumsq_mid", "softmax_d0", "argmax_mid", "argmin_d0_i32", "argmax_fused", "sum_rank3_last",
+               "max_bias_rank3", "isum_d01"]
+
+
+def transpose_ops():
+    """Groups with linalg.transpose: 2-D and 3-D permutations fused with
+    casts and binary ops, a transpose applied after an elementwise op, a
+    permutation that only moves unit dims (a reshape), ragged tile edges."""
+    f = []
+    X, XT, O = _T([300, 200], "bf16"), _T([200, 300], "bf16"), _T([200, 300], "f32")
+    f.append(f"""  func.func @tr2d_cast(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [1, 0]
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%t : {XT}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    X, XT, Y, O = _T([8, 96, 130], "f32"), _T([8, 130, 96], "f32"), _T([8, 130, 96], "f32"), _T([8, 130, 96], "bf16")
+    f.append(f"""  func.func @tr3d_add(%x: {X}, %y: {Y}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e0 = tensor.empty() : {X}
+    %s = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%x : {X}) outs(%e0 : {X}) -> {X}
+    %e1 = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%s : {X}) outs(%e1 : {XT}) permutation = [0, 2, 1]
+    %e2 = tensor.empty() : {Y}
+    %a = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%t, %y : {XT}, {Y}) outs(%e2 : {Y}) -> {Y}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%a : {Y}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    X, XT, O = _T([16, 33, 64], "i8"), _T([64, 16, 33], "i8"), _T([64, 16, 33], "i32")
+    f.append(f"""  func.func @tr3d_rot_i8(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [2, 0, 1]
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%t : {XT}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    X, XT, O = _T([4, 1, 100], "f32"), _T([4, 100, 1], "f32"), _T([4, 100, 1], "f32")
+    f.append(f"""  func.func @tr_unit(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [0, 2, 1]
+    %r = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%t : {XT}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(f) + "\n}\n"
+
+
+TRANSPOSE_OPS = ["tr2d_cast", "tr3d_add", "tr3d_rot_i8", "tr_unit"]
+
 def entries():
     """name -> IR text of every prebuilt group."""
     e = {}
@@ -784,6 +950,10 @@ def entries():
     e["fuzz_generic"] = fuzz_generic()
     e["fuzz_rows"] = fuzz_rows()
     e["generic_reduce"] = generic_reduce()
+    e["any_pbr_ops"] = any_pbr_ops()
+    e["transpose_ops"] = transpose_ops()
+    e["transpose_cast"] = g.transpose_cast(4096, 8192)
+    e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
     e["rank0"] = """module {
   func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
       """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {

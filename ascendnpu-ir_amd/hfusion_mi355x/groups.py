@@ -30,14 +30,16 @@ def vec_add(n=1 << 24, dtype="f32"):
 """
 
 
-def rmsnorm_quant(rows=8192, cols=4096, eps=1e-6):
+def rmsnorm_quant(rows=8192, cols=4096, eps=1e-6, batch=None):
     """RMSNorm (structure of compile-rms-norm-fp32-split-n.mlir:5-47) followed by
     dynamic per-token int8 quantisation with explicit rounding
     (nearbyint -> clamp +-127 -> cast), so the CPU lowering's truncating
     fptosi and the declared RINT cast agree."""
-    X, G = _t([rows, cols], "bf16"), _t([cols], "bf16")
-    XF, GF, RF = _t([rows, cols], "f32"), _t([cols], "f32"), _t([rows], "f32")
-    Q = _t([rows, cols], "i8")
+    lead = [batch, rows // batch] if batch else [rows]  # [B, S, H] when batched
+    X, G = _t(lead + [cols], "bf16"), _t([cols], "bf16")
+    XF, GF, RF = _t(lead + [cols], "f32"), _t([cols], "f32"), _t(lead, "f32")
+    Q = _t(lead + [cols], "i8")
+    rdim, gdims = len(lead), ", ".join(str(i) for i in range(len(lead)))
     e = f"{eps:.9e}"
     return f"""module {{
   func.func @rmsnorm_quant(%x: {X}, %gamma: {G}, %q: {Q}, %scale: {RF}) -> ({Q}, {RF})
@@ -53,7 +55,7 @@ def rmsnorm_quant(rows=8192, cols=4096, eps=1e-6):
     %sq = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%xf, %xf : {XF}, {XF}) outs(%e1 : {XF}) -> {XF}
     %e2 = tensor.empty() : {RF}
     %i2 = linalg.fill ins(%zero : f32) outs(%e2 : {RF}) -> {RF}
-    %ss = linalg.reduce {{arith.addf}} ins(%sq : {XF}) outs(%i2 : {RF}) dimensions = [1]
+    %ss = linalg.reduce {{arith.addf}} ins(%sq : {XF}) outs(%i2 : {RF}) dimensions = [{rdim}]
     %e3 = tensor.empty() : {RF}
     %mean = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%ss, %cols : {RF}, f32) outs(%e3 : {RF}) -> {RF}
     %e4 = tensor.empty() : {RF}
@@ -63,23 +65,23 @@ def rmsnorm_quant(rows=8192, cols=4096, eps=1e-6):
     %e6 = tensor.empty() : {RF}
     %inv = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<rec>}} ins(%rt : {RF}) outs(%e6 : {RF}) -> {RF}
     %e7 = tensor.empty() : {XF}
-    %binv = linalg.broadcast ins(%inv : {RF}) outs(%e7 : {XF}) dimensions = [1]
+    %binv = linalg.broadcast ins(%inv : {RF}) outs(%e7 : {XF}) dimensions = [{rdim}]
     %e8 = tensor.empty() : {XF}
     %y1 = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%xf, %binv : {XF}, {XF}) outs(%e8 : {XF}) -> {XF}
     %e9 = tensor.empty() : {GF}
     %gf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%gamma : {G}) outs(%e9 : {GF}) -> {GF}
     %e10 = tensor.empty() : {XF}
-    %bg = linalg.broadcast ins(%gf : {GF}) outs(%e10 : {XF}) dimensions = [0]
+    %bg = linalg.broadcast ins(%gf : {GF}) outs(%e10 : {XF}) dimensions = [{gdims}]
     %e11 = tensor.empty() : {XF}
     %y = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%y1, %bg : {XF}, {XF}) outs(%e11 : {XF}) -> {XF}
     %e12 = tensor.empty() : {XF}
     %ay = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%y : {XF}) outs(%e12 : {XF}) -> {XF}
     %e13 = tensor.empty() : {RF}
     %i13 = linalg.fill ins(%zero : f32) outs(%e13 : {RF}) -> {RF}
-    %amax = linalg.reduce {{arith.maximumf}} ins(%ay : {XF}) outs(%i13 : {RF}) dimensions = [1]
+    %amax = linalg.reduce {{arith.maximumf}} ins(%ay : {XF}) outs(%i13 : {RF}) dimensions = [{rdim}]
     %sc = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%amax, %qmax : {RF}, f32) outs(%scale : {RF}) -> {RF}
     %e14 = tensor.empty() : {XF}
-    %bsc = linalg.broadcast ins(%sc : {RF}) outs(%e14 : {XF}) dimensions = [1]
+    %bsc = linalg.broadcast ins(%sc : {RF}) outs(%e14 : {XF}) dimensions = [{rdim}]
     %e15 = tensor.empty() : {XF}
     %ys = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%y, %bsc : {XF}, {XF}) outs(%e15 : {XF}) -> {XF}
     %e16 = tensor.empty() : {XF}
@@ -389,6 +391,22 @@ def exp_cumsum_scale(rows=64, cols=1000):
     %e1 = tensor.empty() : {X}
     %b = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%c, %w : {X}, {X}) outs(%e1 : {X}) -> {X}
     return %b : {X}
+  }}
+}}
+"""
+
+
+def transpose_cast(rows=4096, cols=8192, src="bf16", dst="f32"):
+    """PURE_ELEMWISE group with a transpose: out[j, i] = cast(x[i, j])
+    (linalg.transpose permutation [1, 0] fused with hfusion.cast)."""
+    X, XT, O = _t([rows, cols], src), _t([cols, rows], src), _t([cols, rows], dst)
+    return f"""module {{
+  func.func @transpose_cast(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [1, 0]
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%t : {XT}) outs(%o : {O}) -> {O}
+    return %r : {O}
   }}
 }}
 """

@@ -76,9 +76,10 @@ def hfr():
         lib.hfr_program_info_get.argtypes = [vp, ctypes.POINTER(ProgramInfo)]
         lib.hfr_program_launch.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t,
                                            ctypes.POINTER(vp), ctypes.c_size_t, vp, vp]
+        lib.hfr_group_launch_memref.argtypes = [vp, ctypes.POINTER(vp), ctypes.c_size_t, vp]
         for fn in ("hfr_module_load", "hfr_module_unload", "hfr_kernel_get", "hfr_launch", "hfr_group_load",
                    "hfr_group_unload", "hfr_group_info_get", "hfr_group_launch", "hfr_program_load",
-                   "hfr_program_unload", "hfr_program_info_get", "hfr_program_launch"):
+                   "hfr_program_unload", "hfr_program_info_get", "hfr_program_launch", "hfr_group_launch_memref"):
             getattr(lib, fn).restype = ctypes.c_int
         lib.hfr_last_error.restype = cp
         lib.hfr_version.restype = cp
@@ -95,3 +96,28 @@ class HfrError(RuntimeError):
 def check(rc):
     if rc != 0:
         raise HfrError(rc, hfr().hfr_last_error().decode(errors="replace"))
+
+
+def memref_descriptor(ptr, shape, offset=0, strides=None, allocated=None):
+    """An MLIR ranked memref descriptor {allocated, aligned, offset,
+    sizes[R], strides[R]} (the `_mlir_ciface_*` argument layout) for a buffer
+    at device address `ptr`; dense row-major strides unless given."""
+    rank = len(shape)
+    if strides is None:
+        strides, acc = [], 1
+        for d in reversed(shape):
+            strides.insert(0, acc)
+            acc *= d
+
+    class Desc(ctypes.Structure):
+        _fields_ = [("allocated", ctypes.c_void_p), ("aligned", ctypes.c_void_p), ("offset", ctypes.c_int64),
+                    ("sizes", ctypes.c_int64 * rank), ("strides", ctypes.c_int64 * rank)]
+
+    d = Desc()
+    d.allocated = ptr if allocated is None else allocated
+    d.aligned = ptr
+    d.offset = offset
+    for i in range(rank):
+        d.sizes[i] = shape[i]
+        d.strides[i] = strides[i]
+    return d

@@ -200,6 +200,7 @@ class Group:
             self._h = None
 
     def __call__(self, *args, results=None, stream=None, workspace=None):
+        """Launches the group on `stream` (torch's current stream by default)."""
         import torch
         params = self.meta["params"]
         if len(args) != len(params):
@@ -279,6 +280,7 @@ class Program:
             self._h = None
 
     def __call__(self, *args, results=None, stream=None, workspace=None):
+        """Launches the group on `stream` (torch's current stream by default)."""
         import torch
         params = self.meta["params"]
         if len(args) != len(params):

@@ -11,8 +11,9 @@
  * buffers for results that are not written into an argument.
  *
  * Ownership: the caller allocates and frees every tensor buffer.  The runtime
- * owns module/group handles and, when the caller passes no workspace, one
- * lazily allocated zero-initialised workspace per group handle.
+ * owns module/group handles and one zero-initialised workspace per group
+ * handle that needs one, allocated by hfr_group_load on the current device
+ * (launches never allocate).
  * Threading: launches are asynchronous on the given stream; the caller
  * synchronises.  A handle must not be used from two threads at once, and two
  * in-flight launches of one group handle that both use its internal workspace
@@ -99,11 +100,26 @@ int hfr_program_unload(hfr_program_t p);
 int hfr_program_info_get(hfr_program_t p, hfr_program_info *info);
 /* params: one slot per argument of the original function; results: one
  * pointer per result (ignored for results written into an argument);
- * workspace: NULL to use the program's own (allocated on first use), or a
+ * workspace: NULL to use the program's own (allocated at load), or a
  * caller buffer of workspace_bytes.  Steps are enqueued on `stream`; each
  * group uses its own internal workspace. */
 int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
                        void *workspace, void *stream);
+
+/* ---- MLIR C-interface form of a group launch
+ * descs: one pointer per group argument, in the IR's argument order, to the
+ * argument's ranked memref descriptor as an `_mlir_ciface_*` function receives
+ * it, then one per result not written into an argument:
+ *     struct { T *allocated; T *aligned; int64_t offset;
+ *              int64_t sizes[R]; int64_t strides[R]; }
+ * (R = the tensor's rank; a scalar argument passes a pointer to its value).
+ * The device buffer is aligned + offset elements.  Sizes must equal the
+ * group's static shape and strides must be dense row-major; otherwise
+ * HFR_ERR_INVALID.  Replaces the reference runner's memref entry points
+ * (`_mlir_ciface_getData*` / `printData*` over UnrankedMemRefType, whose
+ * descriptor field points at this ranked layout:
+ * bishengir/lib/ExecutionEngine/BiShengIRRunnerUtils.cpp:99-110). */
+int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t ndescs, void *stream);
 
 const char *hfr_last_error(void);
 const char *hfr_version(void);

@@ -789,6 +789,12 @@ class Interp:
             v = convert(get(ins[0]), o.elem)
             env[res] = T(np.broadcast_to(v.a, o.a.shape).copy(), o.elem)
             return
+        if op == "linalg.transpose":
+            # out[i_0..i_n] = in[j] with j[perm[k]] = i_k (out dim k is in dim perm[k])
+            perm = [int(d) for d in re.search(r"permutation\s*=\s*\[([^\]]*)\]", rest).group(1).split(",") if d.strip()]
+            x, o = get(ins[0]), get(outs[0])
+            env[res] = T(_contig(np.transpose(x.a, perm)), o.elem)
+            return
         if op == "linalg.broadcast":
             dims = [int(d) for d in re.search(r"dimensions\s*=\s*\[([^\]]*)\]", rest).group(1).split(",") if d.strip()]
             x, o = get(ins[0]), get(outs[0])

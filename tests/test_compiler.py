@@ -179,10 +179,12 @@ def test_hivm_matmul_reference_form_lowers(tmp_path):
     (HIVM_OPS_MLIR.replace("xf16", "xf64"), -2, "matmul element types"),
     ("func.func @f(%a: tensor<?xf32>) -> tensor<?xf32> { return %a : tensor<?xf32> }", -1, "dynamic shapes"),
     ("module { }", -1, "no func.func"),
-    ("""func.func @f(%a: tensor<4x4xf32>, %o: tensor<4xf32>) -> tensor<4xf32> {
-  %r = linalg.reduce {arith.addf} ins(%a : tensor<4x4xf32>) outs(%o : tensor<4xf32>) dimensions = [0]
-  return %r : tensor<4xf32>
-}""", -2, "non-last axis"),
+    ("""func.func @f(%a: tensor<4x8xf32>, %o: tensor<8xf32>, %p: tensor<4xf32>) -> (tensor<8xf32>, tensor<4xf32>)
+    attributes {hacc.entry, hfusion.fusion_kind = #hfusion.fusion_kind<ANY_PBR>} {
+  %r = linalg.reduce {arith.addf} ins(%a : tensor<4x8xf32>) outs(%o : tensor<8xf32>) dimensions = [0]
+  %s = linalg.reduce {arith.addf} ins(%a : tensor<4x8xf32>) outs(%p : tensor<4xf32>) dimensions = [1]
+  return %r, %s : tensor<8xf32>, tensor<4xf32>
+}""", -2, "different dimensions"),
     ("""func.func @f(%a: tensor<4xi32>, %o: tensor<4xi32>) -> tensor<4xi32> {
   %r = hfusion.elemwise_unary {fun = #hfusion.unary_fn<lgamma>} ins(%a : tensor<4xi32>) outs(%o : tensor<4xi32>) -> tensor<4xi32>
   return %r : tensor<4xi32>
@@ -281,3 +283,18 @@ func.func @f(%arg0: tensor<64xi1>) -> tensor<64x1xf32> {
 }"""
     rc, err, _ = emit(ir, tmp_path)
     assert rc in (0, -1, -2), (rc, err)
+
+
+@pytest.mark.parametrize("decl", [
+    'func.func private @triton_print(f32) -> f32 attributes {msg = "x", hex = false}',
+    "func.func private @g(tensor<4xf32>, i32) attributes {llvm.emit_c_interface}",
+    "func.func private @h() -> (f32, i32)",
+    "func.func private @k(%a: f32) -> f32 attributes {msg = \"named\"}",
+])
+def test_external_declarations_are_skipped(decl, tmp_path):
+    """External declarations (with or without an attributes dict, with named,
+    unnamed or no arguments) carry no body and lower to nothing."""
+    ir = "module {\n  " + decl + "\n" + hf.groups.vec_add(64).split("module {", 1)[1]
+    rc, err, prefix = emit(ir, tmp_path)
+    assert rc == 0, err
+    assert [b["func"] for b in hf.parse_manifest(prefix + ".manifest")] == ["vec_add"]
