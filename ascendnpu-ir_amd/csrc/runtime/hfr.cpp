@@ -640,3 +640,62 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
   return hfr_group_launch(g, params, g->paramRoles.size(), results, g->resultTied.size(), nullptr, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Launch without allocation.  `scratch` is a device array of this library's
+// own code object; each GPU holds its own copy, whose address is looked up
+// once per device (hipGetSymbolAddress) and used in place of the array's
+// host-side name.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[HFR_SCRATCH_BYTES];
+
+__global__ void hfr_zero_fill(uint4 *p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+constexpr int HFR_MAX_DEVICES = 64;
+std::mutex g_scratchMu;
+void *g_scratchPtr[HFR_MAX_DEVICES];
+
+int scratchFor(int dev, void **out) {
+  if (dev < 0 || dev >= HFR_MAX_DEVICES) return fail(HFR_ERR_INVALID, "device ordinal out of range");
+  std::lock_guard<std::mutex> lk(g_scratchMu);
+  if (!g_scratchPtr[dev]) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hipFail(e, "hipGetSymbolAddress(scratch)");
+    g_scratchPtr[dev] = ptr;
+  }
+  *out = g_scratchPtr[dev];
+  return HFR_OK;
+}
+
+} // namespace
+
+extern "C" uint64_t hfr_scratch_bytes(void) { return HFR_SCRATCH_BYTES; }
+
+extern "C" int hfr_group_launch_noalloc(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results,
+                                        size_t nresults, void *stream) {
+  int rc = checkGroupArgs(g, params, nparams, results, nresults);
+  if (rc) return rc;
+  if (g->wsBytes > HFR_SCRATCH_BYTES)
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " needs " + std::to_string(g->wsBytes) +
+                                     " workspace bytes; the static scratch holds " + std::to_string(HFR_SCRATCH_BYTES));
+  void *ws = nullptr;
+  if (g->wsBytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hipFail(e, "hipGetDevice");
+    if ((rc = scratchFor(dev, &ws))) return rc;
+    if (g->wsZero) {
+      // a fill kernel, not hipMemsetAsync: callers may capture this launch
+      const size_t n16 = (g->wsBytes + 15) / 16;
+      const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 1024);
+      hipLaunchKernelGGL(hfr_zero_fill, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (uint4 *)ws, n16);
+      e = hipGetLastError();
+      if (e != hipSuccess) return hipFail(e, "scratch fill");
+    }
+  }
+  return launchGroup(g, params, results, ws, stream);
+}

@@ -199,8 +199,10 @@ class Group:
             native.hfr().hfr_group_unload(h)
             self._h = None
 
-    def __call__(self, *args, results=None, stream=None, workspace=None):
-        """Launches the group on `stream` (torch's current stream by default)."""
+    def __call__(self, *args, results=None, stream=None, workspace=None, noalloc=False):
+        """Launches the group on `stream` (torch's current stream by default).
+        noalloc=True goes through hfr_group_launch_noalloc (the library's
+        static scratch instead of a workspace)."""
         import torch
         params = self.meta["params"]
         if len(args) != len(params):
@@ -234,8 +236,13 @@ class Group:
                 rptrs[j] = t.data_ptr()
         if stream is None:
             stream = torch.cuda.current_stream(device).cuda_stream
-        ws = workspace.data_ptr() if workspace is not None else None
-        native.check(native.hfr().hfr_group_launch(self._h, slots, len(params), rptrs, len(res_meta), ws, stream))
+        if noalloc:
+            if workspace is not None:
+                raise ValueError("noalloc launches take no workspace")
+            native.check(native.hfr().hfr_group_launch_noalloc(self._h, slots, len(params), rptrs, len(res_meta), stream))
+        else:
+            ws = workspace.data_ptr() if workspace is not None else None
+            native.check(native.hfr().hfr_group_launch(self._h, slots, len(params), rptrs, len(res_meta), ws, stream))
         return outs[0] if len(outs) == 1 else tuple(outs)
 
 
@@ -279,8 +286,10 @@ class Program:
             native.hfr().hfr_program_unload(h)
             self._h = None
 
-    def __call__(self, *args, results=None, stream=None, workspace=None):
-        """Launches the group on `stream` (torch's current stream by default)."""
+    def __call__(self, *args, results=None, stream=None, workspace=None, noalloc=False):
+        """Launches the group on `stream` (torch's current stream by default).
+        noalloc=True goes through hfr_group_launch_noalloc (the library's
+        static scratch instead of a workspace)."""
         import torch
         params = self.meta["params"]
         if len(args) != len(params):

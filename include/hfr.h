@@ -121,6 +121,22 @@ int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, 
  * bishengir/lib/ExecutionEngine/BiShengIRRunnerUtils.cpp:99-110). */
 int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t ndescs, void *stream);
 
+/* ---- launch without allocation (no counterpart in the reference)
+ * For callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments as hfr_group_launch without a workspace: a group that needs one
+ * uses the library's static per-device scratch array of HFR_SCRATCH_BYTES
+ * (held by each GPU until the process ends; groups needing more are refused
+ * with HFR_ERR_INVALID).  The scratch is cleared with a fill kernel on
+ * `stream` before the group's kernel when the group needs zeroed workspace.
+ * Calls on one GPU share its scratch: calls that overlap on one GPU (two
+ * streams, or two threads) race.  The call allocates nothing on the device
+ * (the first call on a device looks up the scratch address once). */
+#define HFR_SCRATCH_BYTES (4u << 20)
+int hfr_group_launch_noalloc(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results,
+                             size_t nresults, void *stream);
+uint64_t hfr_scratch_bytes(void);
+
 const char *hfr_last_error(void);
 const char *hfr_version(void);
 
