@@ -130,6 +130,7 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
   try {
     hfc::LowerOptions lo;
     lo.orderedFloatSums = opts.count("ordered_fp_sums") && opts["ordered_fp_sums"] == "1";
+    lo.rmsqKernel = opts.count("rmsq_kernel") && opts["rmsq_kernel"] == "1";
     plans = hfc::lowerModule(*mod, lo);
   } catch (const hfc::CompileError &e) {
     setErr(err, errlen, std::string("lowering error: ") + e.what());

@@ -3287,6 +3287,150 @@ struct ColumnEmitter {
   }
 };
 
+// ======================================================================
+// RMSNorm + dynamic int8 quantisation (hf_rmsq.h).  The group's ops are
+// matched one by one, in the order and form of the configs' IR
+// (compile-rms-norm-fp32-split-n.mlir:5-47 followed by the quantisation):
+// any deviation leaves the group to the generic row program.
+// ======================================================================
+struct RmsqMatch {
+  int x = -1, gamma = -1; // argument positions
+  size_t qRes = 0, sRes = 0;
+  double s0 = 0, K = 0, eps = 0, a0 = 0, qd = 0;
+  int lo = 0, hi = 0;
+};
+
+const Op *defOp(const Value *v) { return v ? v->def : nullptr; }
+bool isFun(const Op *op, std::initializer_list<const char *> names, const char *fn) {
+  if (!op) return false;
+  bool nm = false;
+  for (const char *n : names) nm |= op->name == n;
+  return nm && op->attr("fun") == fn && op->attr("cast").empty();
+}
+bool binOp(const Op *op, const char *fn) {
+  return isFun(op, {"linalg.elemwise_binary", "hfusion.elemwise_binary"}, fn) && op->ins.size() == 2;
+}
+bool unOp(const Op *op, const char *fn) {
+  return isFun(op, {"linalg.elemwise_unary", "hfusion.elemwise_unary"}, fn) && op->ins.size() == 1;
+}
+bool constF32(const Value *v, double &out) {
+  if (!v || !v->isConst || v->type.tensor || v->type.elem != Elem::F32) return false;
+  out = v->fconst;
+  return std::isfinite(out);
+}
+// value = broadcast of `src` along `dims`
+const Value *broadcastOf(const Value *v, std::vector<int64_t> dims) {
+  const Op *b = defOp(v);
+  if (!b || b->name != "linalg.broadcast" || b->dims != dims || b->ins.size() != 1) return nullptr;
+  return b->ins[0];
+}
+// exact widening cast of a bf16 group argument to f32
+int bf16ArgCast(const Value *v) {
+  const Op *c = defOp(v);
+  if (!c || c->name != "hfusion.cast" || c->ins.size() != 1 || v->type.elem != Elem::F32) return -1;
+  const Value *a = c->ins[0];
+  if (a->argIdx < 0 || a->type.elem != Elem::BF16) return -1;
+  return a->argIdx;
+}
+// linalg.reduce <combiner> over dim 1 with init fill(constant)
+const Value *reduceOf(const Value *v, const char *comb, double &init) {
+  const Op *r = defOp(v);
+  if (!r || r->name != "linalg.reduce" || r->combiner != comb || r->dims != std::vector<int64_t>{1} || r->ins.size() != 1)
+    return nullptr;
+  const Op *f = defOp(r->outs[0]);
+  if (!f || f->name != "linalg.fill" || !constF32(f->ins[0], init)) return nullptr;
+  return r->ins[0];
+}
+
+bool matchRmsQuant(const Analysis &A, RmsqMatch &m) {
+  const Func &f = *A.f;
+  if (A.D.size() != 2 || f.returns.size() != 2) return false;
+  const int64_t C = A.D[1];
+  if (C % 1024 != 0 || C > 4096) return false;
+  for (size_t i = 0; i < 2; ++i) {
+    if (f.returns[i]->type.elem == Elem::I8) m.qRes = i;
+    else m.sRes = i;
+  }
+  if (m.qRes == m.sRes) return false;
+  const Value *qv = f.returns[m.qRes], *sc = f.returns[m.sRes];
+  if (A.resultTied[m.qRes] < 0 || sc->type.elem != Elem::F32 || qv->type.shape != A.D ||
+      sc->type.shape != std::vector<int64_t>{A.D[0]})
+    return false;
+  // q = cast_i8(maxf(minf(nearbyint(y / bcast(sc)), HI), LO))
+  const Op *cq = defOp(qv);
+  if (!cq || cq->name != "hfusion.cast" || cq->attr("round_mode", "rint") != "rint" || cq->ins.size() != 1 ||
+      cq->attr("cast") == "cast_unsigned")
+    return false;
+  const Op *mx = defOp(cq->ins[0]);
+  double lo, hi;
+  if (!binOp(mx, "maxf") || !constF32(mx->ins[1], lo)) return false;
+  const Op *mn = defOp(mx->ins[0]);
+  if (!binOp(mn, "minf") || !constF32(mn->ins[1], hi)) return false;
+  if (lo != std::floor(lo) || hi != std::floor(hi) || lo < -128 || hi > 127 || lo > hi) return false;
+  const Op *rn = defOp(mn->ins[0]);
+  if (!unOp(rn, "nearbyint")) return false;
+  const Op *dv = defOp(rn->ins[0]);
+  if (!binOp(dv, "div") || broadcastOf(dv->ins[1], {1}) != sc) return false;
+  const Value *y = dv->ins[0];
+  // sc = amax / QD; amax = reduce maximumf |y| from a0
+  const Op *sd = defOp(sc);
+  if (!binOp(sd, "div") || !constF32(sd->ins[1], m.qd)) return false;
+  const Value *ay = reduceOf(sd->ins[0], "arith.maximumf", m.a0);
+  if (!ay || !unOp(defOp(ay), "abs") || defOp(ay)->ins[0] != y) return false;
+  // y = (xf * bcast(inv)) * bcast(gammaf)
+  const Op *ym = defOp(y);
+  if (!binOp(ym, "mul")) return false;
+  const Value *gf = broadcastOf(ym->ins[1], {0});
+  if (!gf || (m.gamma = bf16ArgCast(gf)) < 0) return false;
+  const Op *y1 = defOp(ym->ins[0]);
+  if (!binOp(y1, "mul")) return false;
+  const Value *xf = y1->ins[0];
+  if ((m.x = bf16ArgCast(xf)) < 0) return false;
+  // inv = rec(sqrt(ss / K + eps)); ss = reduce addf (xf * xf) from s0
+  const Value *inv = broadcastOf(y1->ins[1], {1});
+  const Op *rc = defOp(inv);
+  if (!unOp(rc, "rec")) return false;
+  const Op *sq = defOp(rc->ins[0]);
+  if (!unOp(sq, "sqrt")) return false;
+  const Op *ad = defOp(sq->ins[0]);
+  if (!binOp(ad, "add") || !constF32(ad->ins[1], m.eps)) return false;
+  const Op *md = defOp(ad->ins[0]);
+  if (!binOp(md, "div") || !constF32(md->ins[1], m.K)) return false;
+  const Value *x2 = reduceOf(md->ins[0], "arith.addf", m.s0);
+  const Op *mul2 = defOp(x2);
+  if (!x2 || !binOp(mul2, "mul") || mul2->ins[0] != xf || mul2->ins[1] != xf) return false;
+  if (!(m.s0 >= 0)) return false;
+  // the quotients y / (amax / QD) lie in [-QD, QD] (to a rounding): the clamps
+  // must not bind there, and the biased codes must fit a byte
+  if (!(m.qd > 0 && m.qd <= 127 && lo <= -m.qd && hi >= m.qd)) return false;
+  m.lo = (int)lo;
+  m.hi = (int)hi;
+  return A.params[m.gamma].shape == std::vector<int64_t>{C} || A.map.at(f.args[m.gamma]) == std::vector<int>{1};
+}
+
+KernelPlan lowerRmsQuant(Analysis &A, const RmsqMatch &m, const std::string &kname) {
+  const int64_t R = A.D[0], C = A.D[1];
+  constexpr int WPB = 4;
+  KernelPlan p;
+  p.kernelName = kname;
+  p.kind = "LAST_AXIS_PBR";
+  p.variant = "rmsnorm-quant: one wave per row, binade-run exact serial sum";
+  std::ostringstream k;
+  k << "extern \"C\" __global__ __launch_bounds__(" << WPB * 64 << ") __attribute__((amdgpu_waves_per_eu(3))) void " << kname
+    << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+    << "  hf::rmsq_rows<" << C << ", " << m.lo << ", " << m.hi << ", " << WPB << ">((const uint16_t*)p" << m.x
+    << ", (const uint16_t*)p" << m.gamma << ", (int8_t*)" << resultPtr(A, m.qRes) << ", (float*)" << resultPtr(A, m.sRes)
+    << ", " << R << "ll, " << floatLit((float)m.s0) << ", " << floatLit((float)m.K) << ", " << floatLit((float)m.eps) << ", "
+    << floatLit((float)m.a0) << ", " << floatLit((float)m.qd) << ");\n}\n";
+  p.source = k.str();
+  // three waves per SIMD (the occupancy the register budget allows), each
+  // walking rows
+  const int64_t waves = std::min<int64_t>(R, 3072);
+  p.grid[0] = (unsigned)((waves + WPB - 1) / WPB);
+  p.block[0] = WPB * 64;
+  return p;
+}
+
 // Every linalg.reduce of the group folds exactly the last dim of its input,
 // which spans the whole domain.
 bool reducesLastDimOnly(const Analysis &A) {
@@ -3414,7 +3558,10 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
           collapseDomain(A);
           rows = A.D.size() <= 2 && reducesLastDimOnly(A);
         }
-        if (rows) {
+        RmsqMatch rq;
+        if (rows && opt.rmsqKernel && matchRmsQuant(A, rq)) {
+          p = lowerRmsQuant(A, rq, kname);
+        } else if (rows) {
           RowEmitter e(A, opt);
           p = e.run(kname, "LAST_AXIS_PBR");
         } else {
@@ -3448,7 +3595,8 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
 std::string emitTranslationUnit(const std::vector<KernelPlan> &plans) {
   std::ostringstream s;
   s << "// Generated by bishengir-compile --target=mi355x (ConvertHFusionToHIP).\n"
-    << "#include \"hf_ops.h\"\n#include \"hf_row.h\"\n#include \"hf_argmax.h\"\n#include \"hf_mmad.h\"\n#include \"hf_misc.h\"\n\n";
+    << "#include \"hf_ops.h\"\n#include \"hf_row.h\"\n#include \"hf_argmax.h\"\n#include \"hf_mmad.h\"\n#include \"hf_misc.h\"\n"
+    << "#include \"hf_rmsq.h\"\n\n";
   for (auto &p : plans) s << "// group @" << p.funcName << ": " << p.kind << " (" << p.variant << ")\n" << p.source << "\n";
   return s.str();
 }

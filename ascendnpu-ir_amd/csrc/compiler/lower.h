@@ -42,6 +42,7 @@ struct KernelPlan {
 
 struct LowerOptions {
   bool orderedFloatSums = false; // force serial-order fp sums everywhere
+  bool rmsqKernel = false;       // RMSNorm + dynamic quantisation through hf_rmsq.h
 };
 
 // Ops lowered as a kernel of their own (cumulative ops, histogram,

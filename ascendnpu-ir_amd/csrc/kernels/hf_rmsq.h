@@ -1,0 +1,441 @@
+// RMSNorm + dynamic per-row int8 quantisation on CDNA4, one wavefront per
+// row, with the reference's serial fp32 sum of squares computed exactly but
+// without a 4096-long dependent add chain.
+//
+// Group (compile-rms-norm-fp32-split-n.mlir:5-47 followed by the dynamic
+// quantisation ops, LAST_AXIS_PBR):
+//   xf = extf(x); ss = fold_k RN(ss + RN(xf_k^2)) from s0 (serial, k = 0..C-1);
+//   inv = 1 / sqrt(ss / K + eps); y = RN(RN(xf * inv) * gammaf);
+//   amax = maximumf over |y| from a0; scale = amax / QD;
+//   q = (int8) max(min(rint(y / scale), HI), LO).
+//
+// Exact serial sum.  Every addend x^2 of a bf16 x is exact in f32 and >= 0,
+// so the running sum never decreases.  While the running sum s stays inside
+// one binade [2^p, 2^(p+1)), each step is s' = s + (x^2 rounded to the binade's
+// grid u = 2^(p-23)), ties to even: in units of u, n' = n + d(n & 1).  A run of
+// steps inside one binade is therefore the map n -> n + D[n & 1], fixed by two
+// values; runs compose (f then g: D[b] = Df[b] + Dg[b ^ (Df[b] & 1)]).  The
+// kernel:
+//   1. each lane owns C/64 consecutive elements of the row (the row lands in
+//      LDS by DMA, prefetched one row ahead, in an XOR-swizzled order that
+//      keeps the DMA reads coalesced and the segment reads free of bank
+//      conflicts), split into sub-segments of 16;
+//   2. an approximate prefix (fp32 partial sums and a wave scan) predicts the
+//      binade p of every sub-segment; sub-segments whose prediction is not
+//      clear by a 2^-10 margin are marked dirty;
+//   3. for each clean sub-segment two candidate chains, started at 2^p (n = 0)
+//      and 2^p + u (n = 1), give D[0] and D[1]: fmaf(x, x, c) = RN(x^2 + c)
+//      because x^2 is exact (for |x| < 2^-63 the square is below half an ulp
+//      of c >= 2^-60 either way);
+//   4. sub-segment maps compose inside the lane, then across lanes with a
+//      segmented scan over runs of lanes in one binade;
+//   5. a wave-uniform stitch walks the runs from s0: a run applies when the
+//      exact running sum lies in its binade and the result stays below
+//      2^(p+1) (the addends are >= 0, so every intermediate value is inside);
+//      otherwise the lane's own map, then each sub-segment's, and for a dirty
+//      sub-segment the 16 serial steps themselves.
+//   The result is the bit pattern of the serial sum for every input,
+//   including NaN and infinity (which always take the serial steps).
+// Quantisation: y stays in registers; the row maximum is a wave reduction;
+// the int8 codes go through hf::quant8x4 (bracketed fast path, exact
+// recomputation of near-tie words) and a row whose Guard reports an unsafe
+// magnitude is recomputed with IEEE division.
+#pragma once
+#include "hf_ops.h"
+
+namespace hf {
+
+typedef unsigned rq_u4 __attribute__((ext_vector_type(4)));
+
+// n -> n + D[n & 1] inside one binade (units of its ulp)
+struct BandFn {
+  int32_t d0, d1;
+};
+__device__ __forceinline__ BandFn band_compose(BandFn f, BandFn g) {
+  BandFn h;
+  h.d0 = f.d0 + ((f.d0 & 1) ? g.d1 : g.d0);
+  h.d1 = f.d1 + ((f.d1 & 1) ? g.d0 : g.d1);
+  return h;
+}
+
+// ---- wave64 DPP primitives (gfx9 DPP: row shifts, row broadcasts, wave shifts)
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ int dpp(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWMASK, 0xf, false);
+}
+constexpr int DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143, DPP_WAVE_SHR1 = 0x138, DPP_WAVE_SHL1 = 0x130;
+
+// inclusive prefix sum over the 64 lanes (f32, any association: approximate)
+__device__ __forceinline__ float wave_scan_add(float v, int lane) {
+  const int l16 = lane & 15;
+  float t;
+  t = __int_as_float(dpp<DPP_ROW_SHR1>(0, __float_as_int(v))); if (l16 >= 1) v += t;
+  t = __int_as_float(dpp<DPP_ROW_SHR2>(0, __float_as_int(v))); if (l16 >= 2) v += t;
+  t = __int_as_float(dpp<DPP_ROW_SHR4>(0, __float_as_int(v))); if (l16 >= 4) v += t;
+  t = __int_as_float(dpp<DPP_ROW_SHR8>(0, __float_as_int(v))); if (l16 >= 8) v += t;
+  t = __int_as_float(dpp<DPP_ROW_BCAST15, 0xa>(0, __float_as_int(v))); if (lane & 16) v += t;
+  t = __int_as_float(dpp<DPP_ROW_BCAST31, 0xc>(0, __float_as_int(v))); if (lane >= 32) v += t;
+  return v;
+}
+
+// NaN-propagating maximum over the 64 lanes, returned uniform
+__device__ __forceinline__ float wave_max(float v) {
+  v = maximumf(v, __int_as_float(dpp<DPP_ROW_SHR1>(__float_as_int(v), __float_as_int(v))));
+  v = maximumf(v, __int_as_float(dpp<DPP_ROW_SHR2>(__float_as_int(v), __float_as_int(v))));
+  v = maximumf(v, __int_as_float(dpp<DPP_ROW_SHR4>(__float_as_int(v), __float_as_int(v))));
+  v = maximumf(v, __int_as_float(dpp<DPP_ROW_SHR8>(__float_as_int(v), __float_as_int(v))));
+  v = maximumf(v, __int_as_float(dpp<DPP_ROW_BCAST15, 0xa>(__float_as_int(v), __float_as_int(v))));
+  v = maximumf(v, __int_as_float(dpp<DPP_ROW_BCAST31, 0xc>(__float_as_int(v), __float_as_int(v))));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Segmented inclusive composition scan over the lanes: lane j ends with the
+// composition of lanes start..j (start <= j: the head of j's run).
+__device__ __forceinline__ BandFn wave_seg_compose(BandFn g, int start, int lane) {
+  const int l16 = lane & 15, row0 = lane & ~15;
+#define HF_SEG_STEP(CTRL, MASK, COND)                                                                 \
+  {                                                                                                   \
+    const BandFn pv = {dpp<CTRL, MASK>(0, g.d0), dpp<CTRL, MASK>(0, g.d1)};                           \
+    if (COND) g = band_compose(pv, g);                                                                \
+  }
+  HF_SEG_STEP(DPP_ROW_SHR1, 0xf, l16 >= 1 && lane - 1 >= start)
+  HF_SEG_STEP(DPP_ROW_SHR2, 0xf, l16 >= 2 && lane - 2 >= start)
+  HF_SEG_STEP(DPP_ROW_SHR4, 0xf, l16 >= 4 && lane - 4 >= start)
+  HF_SEG_STEP(DPP_ROW_SHR8, 0xf, l16 >= 8 && lane - 8 >= start)
+  HF_SEG_STEP(DPP_ROW_BCAST15, 0xa, (lane & 16) && start <= row0 - 1)
+  HF_SEG_STEP(DPP_ROW_BCAST31, 0xc, lane >= 32 && start <= 31)
+#undef HF_SEG_STEP
+  return g;
+}
+
+// An item of the stitch: a binade map packed in two words,
+//   w0 = d0 | (p + 127) << 23 | valid << 31,  w1 = d1
+// (p + 127 in [67, 247]; d0, d1 < 2^23).
+__device__ __forceinline__ uint32_t band_pack(int p, int32_t d0, bool valid) {
+  return (uint32_t)d0 | ((uint32_t)(p + 127) << 23) | (valid ? 0x80000000u : 0u);
+}
+// applies a packed map; false when s is outside its binade or leaves it
+__device__ __forceinline__ bool band_apply_packed(uint32_t &s, uint32_t w0, uint32_t w1) {
+  const uint32_t lo = w0 & 0x7f800000u, hi = lo + (1u << 23);
+  const uint32_t ns = s + ((s & 1u) ? w1 : (w0 & 0x7fffffu));
+  const bool ok = (w0 >> 31) && s >= lo && ns < hi;
+  s = ok ? ns : s;
+  return ok;
+}
+
+// 16 serial steps s = RN(s + RN(x_k^2)) over lane j's elements x[0..15] (every
+// lane runs its own; lane j's result is returned).  From s >= 2^-100 on, one
+// FMA per step is the same: x^2 is exact unless |x| < 2^-63, and then it is
+// below half an ulp of s on both paths.
+__device__ __forceinline__ uint32_t serial16(uint32_t s, const float *x, int j) {
+  float sf = __uint_as_float(s);
+  if (s >= 0x0d800000u && s <= 0x7f800000u) { // [2^-100, inf]
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sf = __builtin_fmaf(x[k], x[k], sf);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      float xk = x[k];
+      asm volatile("" : "+v"(xk)); // squared here, not hoisted out of the stitch
+      const float sq = xk * xk;
+      sf = sf + sq;
+    }
+  }
+  return (uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(sf), j);
+}
+
+// int8 codes of four quotients a_i / b, as quant8x4 but without tracking the
+// clamp bounds: for callers whose quotients cannot reach them (|a_i| <= |b| * QD
+// with the clamps outside [-QD, QD]) and whose rows with a non-finite maximum
+// take the exact path.
+__device__ __forceinline__ uint32_t quant8x4_inner(const float (&a)[4], float b, float r, Guard &g) {
+  constexpr float D = 0x1p-15f;
+  uint32_t wl = 0, wh = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wl = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(a[i], r, 128.0f - D), i, wl);
+    wh = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(a[i], r, 128.0f + D), i, wh);
+  }
+  uint32_t w = wl ^ 0x80808080u;
+  if (__builtin_expect(wl != wh, 0)) {
+    w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float q = rint_div(a[i], b, r, g, kFast{});
+      w |= ((uint32_t)(int32_t)q & 0xFFu) << (8 * i);
+    }
+  }
+  return w;
+}
+
+template <int C, int LO, int HI, int WPB>
+__device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gamma,
+                                          int8_t *__restrict__ q, float *__restrict__ scale, int64_t R, float s0,
+                                          float K, float eps, float a0, float qd, float *dbg = nullptr) {
+  static_assert(C % 1024 == 0 && C <= 4096, "rows of 1024..4096 elements, multiple of 1024");
+  constexpr int SEG = C / 64;      // elements per lane
+  constexpr int NG = SEG / 8;      // 16-byte granules per lane
+  constexpr int NS = SEG / 16;     // sub-segments per lane
+  constexpr int SWD = 16 / NG;     // lanes per swizzle group
+  __shared__ rq_u4 lds_all[WPB][C / 8];
+  const int lane0 = threadIdx.x & 63;
+  rq_u4 *lds = lds_all[threadIdx.x / 64];
+  const int64_t W = (int64_t)gridDim.x * WPB;
+  int64_t row = (int64_t)blockIdx.x * WPB + threadIdx.x / 64;
+
+  // gamma as f32 in LDS for the workgroup (lane j's 4-float groups at
+  // stride 64 so that the reads are free of bank conflicts), read where used
+  __shared__ float4 lds_gamma[C / 4];
+  for (int i = threadIdx.x; i < C / 4; i += WPB * 64) {
+    const uint2 w = reinterpret_cast<const uint2 *>(gamma)[i]; // columns 4i .. 4i+3
+    const int j = i / (SEG / 4), g4 = i % (SEG / 4);
+    lds_gamma[g4 * 64 + j] = make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                                         __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+  }
+  __syncthreads();
+  // row DMA straight into this wave's LDS row buffer, in the swizzled order:
+  // instruction k, lane l fills slot 64k + l (lane j's granule g sits at slot
+  // NG*j + (g ^ sw(j))); eight consecutive lanes read one 128-byte line
+  const uint32_t ldsBase = (uint32_t)(uintptr_t)lds;
+  auto issueRow = [&](int64_t r, int lane) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); // this wave's reads of the buffer are done
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      const int slot = 64 * k + lane, j = slot / NG, g = (slot % NG) ^ ((j / SWD) & (NG - 1));
+      const uint16_t *src = x + r * C + 8 * (NG * j + g);
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+                   "s"(__builtin_amdgcn_readfirstlane(ldsBase + 1024u * k))
+                   : "memory");
+    }
+  };
+  if (row < R) issueRow(row, lane0);
+  for (; row < R; row += W) {
+    // per-lane index arithmetic is recomputed each row rather than held in
+    // registers across the loop
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the row's DMA has landed
+    __builtin_amdgcn_wave_barrier();
+    rq_u4 seg[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) seg[g] = lds[NG * lane + (g ^ ((lane / SWD) & (NG - 1)))];
+    // prefetch the next row into the buffer once these reads are done
+    if (row + W < R) issueRow(row + W, lane);
+
+    // ---- 2. approximate prefix: sub-segment sums and a wave scan
+    float xf[SEG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xf[8 * g + 2 * i] = __uint_as_float(seg[g][i] << 16);
+        xf[8 * g + 2 * i + 1] = __uint_as_float(seg[g][i] & 0xffff0000u);
+      }
+    float a[NS];
+    float tot = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float e0 = 0.0f, e1 = 0.0f; // two chains: half the latency
+#pragma unroll
+      for (int k = 16 * s; k < 16 * s + 16; k += 2) {
+        e0 = __builtin_fmaf(xf[k], xf[k], e0);
+        e1 = __builtin_fmaf(xf[k + 1], xf[k + 1], e1);
+      }
+      a[s] = e0 + e1;
+      tot += a[s];
+    }
+    const float incl = wave_scan_add(tot, lane);
+    float ps = s0 + (incl - tot);
+    // ---- 3. per sub-segment (item): binade prediction and candidate chains
+    int kt[NS];          // item key: its binade if clean, else unique
+    uint32_t w0[NS], w1[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      // predicted binade: the biased exponent of the approximate start and
+      // end agree (2^-10 margin), within [2^-60, 2^120]
+      const uint32_t elo = __float_as_uint(ps * (1.0f - 0x1p-10f)) >> 23;
+      ps += a[t];
+      const uint32_t ehi = __float_as_uint(ps * (1.0f + 0x1p-10f)) >> 23;
+      bool clean = elo == ehi && elo - 67u <= 180u;
+      const uint32_t base = (clean ? elo : 127u) << 23;
+      float c0 = __uint_as_float(base), c1 = __uint_as_float(base + 1u);
+#pragma unroll
+      for (int k = 16 * t; k < 16 * t + 16; ++k) {
+        c0 = __builtin_fmaf(xf[k], xf[k], c0);
+        c1 = __builtin_fmaf(xf[k], xf[k], c1);
+      }
+      const uint32_t d0 = __float_as_uint(c0) - base, d1 = __float_as_uint(c1) - base - 1u;
+      clean = clean && (d0 | d1) < (1u << 23);
+      kt[t] = clean ? (int)elo - 127 : -1000 - NS * lane - t;
+      w0[t] = d0 | base | (clean ? 0x80000000u : 0u); // band_pack(p, d0, clean)
+      w1[t] = d1;
+    }
+    // ---- 4. lane structure: head items (the key of item 0), middle items,
+    //         tail items (the key of the last item); runs of one key joined
+    //         across lanes by a segmented scan
+    int h = 1, sft = NS - 1;
+#pragma unroll
+    for (int t = 1; t < NS; ++t) h += (h == t && kt[t] == kt[0]) ? 1 : 0;
+#pragma unroll
+    for (int t = NS - 2; t >= 0; --t) sft -= (sft == t + 1 && kt[t] == kt[NS - 1]) ? 1 : 0;
+    const bool whole = h == NS && kt[0] > -1000;
+    if (kt[0] <= -1000) h = 0;
+    if (kt[NS - 1] <= -1000) sft = NS;
+    // prefix and suffix compositions of the items, then the head / tail parts
+    BandFn P[NS], S[NS];
+    P[0] = {(int32_t)(w0[0] & 0x7fffffu), (int32_t)w1[0]};
+#pragma unroll
+    for (int t = 1; t < NS; ++t) P[t] = band_compose(P[t - 1], BandFn{(int32_t)(w0[t] & 0x7fffffu), (int32_t)w1[t]});
+    S[NS - 1] = {(int32_t)(w0[NS - 1] & 0x7fffffu), (int32_t)w1[NS - 1]};
+#pragma unroll
+    for (int t = NS - 2; t >= 0; --t) S[t] = band_compose(BandFn{(int32_t)(w0[t] & 0x7fffffu), (int32_t)w1[t]}, S[t + 1]);
+    BandFn pre = {0, 0}, suf = {0, 0};
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      if (h == t + 1) pre = P[t];
+      if (sft == t) suf = S[t];
+    }
+    const int lastKeyPrev = dpp<DPP_WAVE_SHR1>(-2000, kt[NS - 1]);
+    const bool connIn = lane > 0 && kt[0] == lastKeyPrev;   // dirty keys are unique
+    const bool connOut = __builtin_amdgcn_update_dpp(0, (int)connIn, DPP_WAVE_SHL1, 0xf, 0xf, false) != 0 && lane < 63;
+    const bool segHead = !(whole && connIn);
+    const uint64_t heads = __ballot(segHead);
+    const int start = 63 - __builtin_clzll(heads & (lane == 63 ? ~0ull : ((2ull << lane) - 1)));
+    const BandFn A = wave_seg_compose(whole ? pre : suf, start, lane);
+    // the run ending in this lane's head items, from its head in an earlier lane
+    const BandFn Aprev = {dpp<DPP_WAVE_SHR1>(0, A.d0), dpp<DPP_WAVE_SHR1>(0, A.d1)};
+    const BandFn H = connIn ? band_compose(Aprev, pre) : pre;
+    const uint32_t hw0 = band_pack(kt[0] > -1000 ? kt[0] : 0, H.d0 & 0x7fffff,
+                                   h > 0 && ((uint32_t)H.d0 | (uint32_t)H.d1) < (1u << 23)),
+                   hw1 = (uint32_t)H.d1;
+    const int akey = whole ? kt[0] : kt[NS - 1];
+    const uint32_t aw0 = band_pack(akey > -1000 ? akey : 0, A.d0 & 0x7fffff,
+                                   (whole || sft < NS) && ((uint32_t)A.d0 | (uint32_t)A.d1) < (1u << 23)),
+                   aw1 = (uint32_t)A.d1;
+    const uint64_t visit = __ballot(segHead || !connOut);
+    // the lane's stitch events in order, each a packed map (bit 31 set), the
+    // serial marker 0x40000000 (a dirty middle item), or 0 (none):
+    //   0: the run ending in the head items;  1..NS: middle items;
+    //   NS+1: the run ending at the lane's end
+    constexpr int NE = NS + 2;
+    uint32_t ev0[NE], ev1[NE];
+    ev0[0] = (!whole && h > 0) ? hw0 : 0u;
+    ev1[0] = hw1;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const bool mid = !whole && t >= h && t < sft;
+      ev0[1 + t] = mid ? ((w0[t] >> 31) ? w0[t] : 0x40000000u) : 0u;
+      ev1[1 + t] = w1[t];
+    }
+    ev0[NS + 1] = (!connOut && (whole || sft < NS)) ? aw0 : 0u;
+    ev1[NS + 1] = aw1;
+    uint32_t evmask = 0;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) evmask |= ev0[e] ? (1u << e) : 0u;
+    // ---- 5. wave-uniform stitch from s0 (scalar code: a wave issues one
+    //         instruction per four cycles, so the step is kept short)
+    uint32_t s = __float_as_uint(s0);
+    int nslow = 0;
+    uint32_t runBad = 0;
+    for (uint64_t vm = visit; vm; vm &= vm - 1) {
+      const int j = __builtin_ctzll(vm);
+      const uint32_t m = __builtin_amdgcn_readlane(evmask, j);
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        if (!(m & (1u << e))) continue;
+        const uint32_t a0 = __builtin_amdgcn_readlane(ev0[e], j), a1 = __builtin_amdgcn_readlane(ev1[e], j);
+        const uint32_t lo = a0 & 0x7f800000u;
+        const uint32_t ns = s + ((s & 1u) ? a1 : (a0 & 0x7fffffu));
+        // zero iff the map is valid and s and its image lie in the binade
+        const uint32_t chk = ((s - lo) | (ns - lo) | (~a0 & 0x80000000u)) >> 23;
+        if (e == 0 || e == NE - 1) {
+          runBad |= chk;
+          s = chk ? s : ns;
+        } else if (chk == 0) {
+          s = ns;
+        } else {
+          // the item's own serial steps (every lane runs its own elements
+          // from s; lane j's result is kept)
+          s = serial16(s, &xf[16 * (e - 1)], j);
+          ++nslow;
+        }
+      }
+    }
+    const bool fail = runBad != 0; // a run did not hold (its binade was mispredicted)
+    if (fail) {
+      // a run did not hold (its binade was mispredicted): item by item
+      s = __float_as_uint(s0);
+      for (int j = 0; j < 64; ++j) {
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+          if (!band_apply_packed(s, __builtin_amdgcn_readlane(w0[t], j), __builtin_amdgcn_readlane(w1[t], j))) {
+            s = serial16(s, &xf[16 * t], j);
+            nslow += 1000;
+          }
+        }
+      }
+    }
+    // ---- tail: inv, y, amax, scale, codes
+    const float ss = __uint_as_float(s);
+    if (dbg && lane == 0) {
+      dbg[2 * row] = ss;
+      dbg[2 * row + 1] = (float)nslow;
+    }
+    const float inv = 1.0f / __builtin_sqrtf(ss / K + eps);
+    float m = 0.0f;
+#pragma unroll
+    for (int g4 = 0; g4 < SEG / 4; ++g4) {
+      const float4 gw = lds_gamma[g4 * 64 + lane];
+      xf[4 * g4] = (xf[4 * g4] * inv) * gw.x;
+      xf[4 * g4 + 1] = (xf[4 * g4 + 1] * inv) * gw.y;
+      xf[4 * g4 + 2] = (xf[4 * g4 + 2] * inv) * gw.z;
+      xf[4 * g4 + 3] = (xf[4 * g4 + 3] * inv) * gw.w;
+    }
+#pragma unroll
+    for (int k = 0; k < SEG; k += 2)
+      asm volatile("v_maximum3_f32 %0, %0, |%1|, |%2|" : "+v"(m) : "v"(xf[k]), "v"(xf[k + 1]));
+    const float amax = maximumf(wave_max(m), a0);
+    const float sc = amax / qd;
+    if (lane == 0) scale[row] = sc;
+    const float r = 1.0f / sc;
+    Guard gd;
+    gd.divisor(r);
+    rq_u4 *qrow = reinterpret_cast<rq_u4 *>(q + row * C) + NG / 2 * lane;
+#pragma unroll
+    for (int i = 0; i < SEG / 16; ++i) {
+      // 16 codes: the bracketing pair of packed words, one test for the chunk
+      constexpr float D = 0x1p-15f;
+      uint32_t wl[4], wh[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        wl[w] = 0;
+        wh[w] = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = xf[16 * i + 4 * w + e];
+          wl[w] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(a, r, 128.0f - D), e, wl[w]);
+          wh[w] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(a, r, 128.0f + D), e, wh[w]);
+        }
+      }
+      if (__builtin_expect(((wl[0] ^ wh[0]) | (wl[1] ^ wh[1]) | (wl[2] ^ wh[2]) | (wl[3] ^ wh[3])) != 0, 0)) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float a4[4] = {xf[16 * i + 4 * w], xf[16 * i + 4 * w + 1], xf[16 * i + 4 * w + 2], xf[16 * i + 4 * w + 3]};
+          wl[w] = quant8x4_inner(a4, sc, r, gd) ^ 0x80808080u;
+        }
+      }
+      qrow[i] = rq_u4{wl[0] ^ 0x80808080u, wl[1] ^ 0x80808080u, wl[2] ^ 0x80808080u, wl[3] ^ 0x80808080u};
+      __builtin_amdgcn_sched_barrier(0); // bound the live range to one 16-byte store
+    }
+    if (__ballot(gd.bad()) != 0 || !(amax <= 0x1.fffffep+127f)) {
+      // rare: an unsafe magnitude or a NaN quotient -- IEEE division
+      int8_t *qe = q + row * C + SEG * lane;
+#pragma unroll
+      for (int k = 0; k < SEG; ++k)
+        qe[k] = (int8_t)(int32_t)maximumf(minimumf(__builtin_roundevenf(xf[k] / sc), (float)HI), (float)LO);
+    }
+  }
+}
+
+} // namespace hf

@@ -954,6 +954,9 @@ def entries():
     e["transpose_ops"] = transpose_ops()
     e["transpose_cast"] = g.transpose_cast(4096, 8192)
     e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
+    # the same groups through the opt-in one-wave-per-row kernel (hf_rmsq.h)
+    for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3", "rmsnorm_quant_ragged"):
+        e[n + "_rmsq"] = e[n]
     e["rank0"] = """module {
   func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
       """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {
@@ -984,3 +987,8 @@ def entries():
 
 def get(name):
     return entries()[name]
+
+
+def options(name):
+    """Compiler options a prebuilt group is built with ("" for the defaults)."""
+    return "rmsq_kernel=1" if name.endswith("_rmsq") else ""

@@ -40,7 +40,7 @@ def to_host(t, elem):
 def run_gpu(name, inputs, device, func=None):
     """Runs prebuilt catalog group `name` on the GPU; `inputs` holds one numpy
     array per group argument (outputs' initial contents included)."""
-    art = hf.compile(hf.catalog.get(name), require_cached=True)
+    art = hf.compile(hf.catalog.get(name), options=hf.catalog.options(name), require_cached=True)
     grp = art.load(func)
     params = grp.meta["params"]
     devs = []

@@ -1,0 +1,104 @@
+"""The opt-in RMSNorm + dynamic int8 quantisation kernel (hf_rmsq.h, compiler
+option rmsq_kernel=1; catalog names ending in _rmsq): its exact
+serial fp32 sum of squares (binade runs composed across lanes, stitched from
+the init) on rows built to stress every path of the stitch, bit-exact against
+the CPU oracle's serial loop.
+
+Rows (bf16, 4096 wide): N(0, s) at several scales (the binade of the running
+sum crosses lane and sub-segment boundaries at different places), constants
+(every step a tie or exact), exact powers of two, zeros, a NaN, an infinity,
+squares that overflow, squares below the f32 normal range, and rows whose
+sum crosses a binade exactly at a sub-segment boundary."""
+import numpy as np
+import pytest
+
+import hfusion_mi355x as hf
+from helpers import run_gpu, run_oracle
+
+I = hf.inputs
+C = 4096
+
+
+def bf16(a):
+    a = np.asarray(a, np.float32)
+    b = a.view(np.uint32)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(np.isnan(a), np.uint16(0x7FC0), r)
+
+
+def stress_rows(rows=256, seed=0x524D53):
+    rng = np.random.default_rng(seed)
+    x = np.zeros((rows, C), np.float32)
+    for r in range(rows):
+        kind = r % 16
+        if kind < 6:
+            x[r] = rng.normal(0, [1e-3, 0.1, 1, 3, 30, 1e4][kind], C)
+        elif kind == 6:
+            x[r] = 1.5                        # x^2 = 2.25: ties at every binade past 2^22 ulps
+        elif kind == 7:
+            x[r] = 2.0 ** rng.integers(-8, 8, C)
+        elif kind == 8:
+            x[r] = 0.0
+            x[r, rng.integers(0, C)] = 1.0 if r % 32 == 8 else 0.0
+        elif kind == 9:
+            x[r] = rng.normal(0, 1, C)
+            x[r, rng.integers(0, C)] = np.nan
+        elif kind == 10:
+            x[r] = rng.normal(0, 1, C)
+            x[r, rng.integers(0, C)] = np.inf if r % 32 == 10 else -np.inf
+        elif kind == 11:
+            x[r] = rng.normal(0, 1e19, C)     # squares near the f32 maximum: the sum overflows
+        elif kind == 12:
+            x[r] = rng.normal(0, 1e-21, C)    # squares below 2^-126
+        elif kind == 13:
+            x[r] = 1.0                        # the sum reaches 2^k exactly at element 2^k
+        elif kind == 14:
+            x[r] = rng.choice([0.0, 1.0, 0.5, 0.25], C)
+        else:
+            x[r] = rng.normal(0, 1, C) * (rng.random(C) < 0.05)
+    return bf16(x)
+
+
+@pytest.mark.gpu
+def test_rmsq_stress_rows_bit_exact(gpu):
+    print("[case] rmsnorm_quant_256 stress rows", flush=True)
+    x = stress_rows()
+    g = I.uniform_bf16(I.SEED_BASE + 77, (C,), 0.5, 1.5)
+    args = [x, g, np.zeros((256, C), np.int8), np.zeros(256, np.float32)]
+    q, s = run_gpu("rmsnorm_quant_256_rmsq", args, gpu)
+    rq, rs = run_oracle("rmsnorm_quant_256", args)
+    nan = np.isnan(rs)
+    assert np.array_equal(np.isnan(s), nan)
+    assert np.array_equal(s[~nan].view(np.uint32), rs[~nan].view(np.uint32)), \
+        f"scales differ in rows {np.nonzero(s.view(np.uint32) != rs.view(np.uint32))[0][:16]}"
+    bad = np.nonzero((q != rq).any(axis=1))[0]
+    assert bad.size == 0, f"codes differ in rows {bad[:16]}"
+
+
+def test_rmsq_selected_only_when_asked():
+    for name in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3"):
+        assert "serial-order" in hf.compile(hf.catalog.get(name)).blocks[0]["variant"], name
+        v = hf.compile(hf.catalog.get(name), options="rmsq_kernel=1").blocks[0]["variant"]
+        assert "rmsnorm-quant" in v, name
+    # a width the kernel does not take keeps the generic row program
+    v = hf.compile(hf.catalog.get("rmsnorm_quant_ragged"), options="rmsq_kernel=1").blocks[0]["variant"]
+    assert "serial-order" in v
+
+
+SHAPES = {"rmsnorm_quant_rmsq": (8192, 4096), "rmsnorm_quant_rank3_rmsq": (4, 64, 1024),
+          "rmsnorm_quant_ragged_rmsq": (13, 1000)}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_rmsq_configs_bit_exact(gpu, name):
+    print(f"[case] {name}", flush=True)
+    shape = SHAPES[name]
+    rng = np.random.default_rng(11)
+    x = bf16(rng.normal(0, 1, shape))
+    g = bf16(rng.uniform(0.5, 1.5, shape[-1:]))
+    args = [x, g, np.zeros(shape, np.int8), np.zeros(shape[:-1], np.float32)]
+    q, s = run_gpu(name, args, gpu)
+    rq, rs = run_oracle(name, args)
+    assert np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(q, rq)
