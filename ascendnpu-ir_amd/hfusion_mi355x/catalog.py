@@ -953,6 +953,8 @@ def entries():
     e["any_pbr_ops"] = any_pbr_ops()
     e["transpose_ops"] = transpose_ops()
     e["transpose_cast"] = g.transpose_cast(4096, 8192)
+    # the W8A8 contraction with B in the [K, N] layout of linalg.matmul
+    e["w8a8_dequant_kn"] = g.w8a8_dequant(4096, 4096, 4096, b_layout="kn").replace("@w8a8_dequant(", "@w8a8_dequant_kn(")
     e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
     # the same groups through the opt-in one-wave-per-row kernel (hf_rmsq.h)
     for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3", "rmsnorm_quant_ragged"):

@@ -25,10 +25,35 @@ INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X
 BF16_PEAK_TFLOPS = 2500.0
 HEADLINE = "rmsnorm_quant"
 ORDER = ["rmsnorm_quant", "vec_add", "safe_softmax", "argmax", "w8a8_dequant"]
+# further groups on the hot path, measured the same way (not BASELINE configs):
+# the bf16 contraction, W8A8 with B as [K, N], a transpose fused with a cast
+EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast"]
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def generic_inputs(meta, dev, seed=7):
+    """Seeded random arguments from a group's parameter list (outputs empty)."""
+    import numpy as np
+    import torch
+    rng = np.random.default_rng(seed)
+    out = []
+    for p in meta["params"]:
+        shape, elem = tuple(p["shape"]), p["elem"]
+        if p["role"] != "in":
+            dt = {"i8": torch.int8, "bf16": torch.bfloat16, "f32": torch.float32, "i32": torch.int32}[elem]
+            out.append(torch.empty(shape, dtype=dt, device=dev))
+        elif elem == "i8":
+            out.append(torch.from_numpy(rng.integers(-128, 128, shape, dtype=np.int8)).to(dev))
+        elif elem == "bf16":
+            out.append(torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(dev).to(torch.bfloat16))
+        elif elem == "f32":
+            out.append(torch.from_numpy(rng.uniform(0.001, 0.02, shape).astype(np.float32)).to(dev))
+        else:
+            raise KeyError(elem)
+    return out
 
 
 def device_inputs(name, dev):
@@ -416,7 +441,7 @@ def main():
 
     import hfusion_mi355x as hf
     dev = torch.device("cuda:0")
-    names = [args.only] if args.only else ORDER
+    names = [args.only] if args.only else ORDER + EXTRA
     groups = {}
     headline_cpu = None
     headline_cpu_mt = None
@@ -425,7 +450,10 @@ def main():
         log(f"[bench] {name}: preparing inputs")
         art = hf.compile(hf.catalog.get(name), require_cached=True)
         grp = art.load()
-        dargs, host_ins = device_inputs(name, dev)
+        if name in EXTRA:
+            dargs, host_ins = generic_inputs(grp.meta, dev), None
+        else:
+            dargs, host_ins = device_inputs(name, dev)
         log(f"[bench] {name}: timing {args.steps} steps")
         sets = input_sets(dargs)
         total_ms, wall = time_group(grp, sets, args.steps, args.warmup)
@@ -435,9 +463,11 @@ def main():
         if meta["kind"] == "SINGLE_CUBE":
             ops = meta["algo_ops"]
             achieved = ops / (kern_ms * 1e-3) / 1e12
-            entry = {"value": ops * args.steps / (total_ms * 1e-3) / 1e12, "unit": "TOPS", "ms_per_step": ms,
-                     "roofline": {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TOPS",
-                                  "frac": achieved / INT8_PEAK_TOPS, "traffic": None}}
+            bf16 = "bf16" in meta.get("variant", "")
+            peak, unit = (BF16_PEAK_TFLOPS, "TFLOP/s") if bf16 else (INT8_PEAK_TOPS, "TOPS")
+            entry = {"value": ops * args.steps / (total_ms * 1e-3) / 1e12, "unit": unit, "ms_per_step": ms,
+                     "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": unit,
+                                  "frac": achieved / peak, "traffic": None}}
         else:
             nb = meta["algo_bytes"]
             achieved = nb / (kern_ms * 1e-3) / 1e9
@@ -451,7 +481,7 @@ def main():
         groups[name] = entry
         log(f"[bench] {name}: {entry['value']:.1f} {entry['unit']} ({entry['roofline']['frac'] * 100:.1f}% of peak), "
             f"{ms * 1e3:.1f} us/step")
-        if not args.no_cpu and (name == HEADLINE or args.only):
+        if not args.no_cpu and host_ins is not None and (name == HEADLINE or args.only):
             log(f"[bench] {name}: CPU baseline (oracle restatement, 1 core)")
             headline_cpu = cpu_baseline(name, host_ins)
             headline_cpu_mt = cpu_baseline_mt(name, host_ins)

@@ -716,3 +716,147 @@ void hfref_w8a8_dequant_rows(const int8_t *A, const int8_t *Bt,
   }
   free(acc);
 }
+
+
+/* ---------------------------------------------------------------- memref ABI
+ * Ranked descriptors as the MLIR C interface lays them out
+ * (BiShengIRRunnerUtils.cpp:99-110 passes them to `_mlir_ciface_` entries):
+ * two pointers, the offset, then R sizes and R strides, all 64-bit. */
+typedef struct {
+  char *allocated, *aligned;
+  int64_t offset;
+  int64_t dims[]; /* sizes[R] then strides[R] */
+} hfref_memref;
+
+static int64_t memref_numel(const hfref_memref *m, int rank) {
+  int64_t n = 1;
+  for (int k = 0; k < rank; ++k) n *= m->dims[k];
+  return n;
+}
+
+/* walks the elements in row-major order, copying between the strided view and
+ * a dense buffer (to_dense != 0: view -> dense) */
+static void memref_copy(const hfref_memref *m, int rank, int esz, char *dense, int to_dense) {
+  const int64_t n = memref_numel(m, rank);
+  int64_t idx[8] = {0};
+  for (int64_t e = 0; e < n; ++e) {
+    int64_t off = m->offset;
+    for (int k = 0; k < rank; ++k) off += idx[k] * m->dims[rank + k];
+    char *p = m->aligned + off * esz;
+    if (to_dense) memcpy(dense + e * esz, p, (size_t)esz);
+    else memcpy(p, dense + e * esz, (size_t)esz);
+    for (int k = rank - 1; k >= 0; --k) {
+      if (++idx[k] < m->dims[k]) break;
+      idx[k] = 0;
+    }
+  }
+}
+
+int hfref_memref_gather(const void *desc, int rank, int elem_size, void *dense) {
+  if (!desc || !dense || rank < 0 || rank > 8) return -1;
+  memref_copy((const hfref_memref *)desc, rank, elem_size, (char *)dense, 1);
+  return 0;
+}
+
+int hfref_memref_scatter(const void *dense, const void *desc, int rank, int elem_size) {
+  if (!desc || !dense || rank < 0 || rank > 8) return -1;
+  memref_copy((const hfref_memref *)desc, rank, elem_size, (char *)(uintptr_t)dense, 0);
+  return 0;
+}
+
+static int dims_are(const void *desc, int rank, const int64_t *want) {
+  const hfref_memref *m = (const hfref_memref *)desc;
+  if (!m) return 0;
+  for (int k = 0; k < rank; ++k)
+    if (m->dims[k] != want[k]) return 0;
+  return 1;
+}
+
+static void *gathered(const void *desc, int rank, int esz) {
+  const hfref_memref *m = (const hfref_memref *)desc;
+  void *d = malloc((size_t)(memref_numel(m, rank) * esz) + 1);
+  memref_copy(m, rank, esz, (char *)d, 1);
+  return d;
+}
+
+static void *dense_for(const void *desc, int rank, int esz) {
+  return malloc((size_t)(memref_numel((const hfref_memref *)desc, rank) * esz) + 1);
+}
+
+static void put_back(void *dense, const void *desc, int rank, int esz) {
+  memref_copy((const hfref_memref *)desc, rank, esz, (char *)dense, 0);
+  free(dense);
+}
+
+int hfref_vecadd_f32_memref(const void *a, const void *b, const void *out) {
+  if (!a) return -1;
+  const int64_t n[1] = {((const hfref_memref *)a)->dims[0]};
+  if (!dims_are(b, 1, n) || !dims_are(out, 1, n)) return -1;
+  float *da = gathered(a, 1, 4), *db = gathered(b, 1, 4), *dout = dense_for(out, 1, 4);
+  hfref_vecadd_f32(da, db, dout, n[0]);
+  put_back(dout, out, 1, 4);
+  free(da);
+  free(db);
+  return 0;
+}
+
+int hfref_rmsnorm_quant_memref(const void *x, const void *gamma, float eps, const void *q, const void *scale) {
+  if (!x) return -1;
+  const hfref_memref *mx = (const hfref_memref *)x;
+  const int64_t rc[2] = {mx->dims[0], mx->dims[1]}, c[1] = {rc[1]}, r[1] = {rc[0]};
+  if (!dims_are(gamma, 1, c) || !dims_are(q, 2, rc) || !dims_are(scale, 1, r)) return -1;
+  uint16_t *dx = gathered(x, 2, 2), *dg = gathered(gamma, 1, 2);
+  int8_t *dq = dense_for(q, 2, 1);
+  float *ds = dense_for(scale, 1, 4);
+  hfref_rmsnorm_quant(dx, dg, eps, dq, ds, rc[0], rc[1]);
+  put_back(dq, q, 2, 1);
+  put_back(ds, scale, 1, 4);
+  free(dx);
+  free(dg);
+  return 0;
+}
+
+int hfref_softmax_bf16_memref(const void *x, const void *out) {
+  if (!x) return -1;
+  const hfref_memref *mx = (const hfref_memref *)x;
+  const int64_t rc[2] = {mx->dims[0], mx->dims[1]};
+  if (!dims_are(out, 2, rc)) return -1;
+  float *dx = gathered(x, 2, 4);
+  uint16_t *dout = dense_for(out, 2, 2);
+  hfref_softmax_bf16(dx, dout, rc[0], rc[1]);
+  put_back(dout, out, 2, 2);
+  free(dx);
+  return 0;
+}
+
+int hfref_argmax_memref(const void *x, const void *val, const void *idx) {
+  if (!x) return -1;
+  const hfref_memref *mx = (const hfref_memref *)x;
+  const int64_t rc[2] = {mx->dims[0], mx->dims[1]}, r[1] = {rc[0]};
+  if (!dims_are(val, 1, r) || !dims_are(idx, 1, r)) return -1;
+  float *dx = gathered(x, 2, 4), *dv = dense_for(val, 1, 4);
+  int32_t *di = dense_for(idx, 1, 4);
+  hfref_argmax(dx, dv, di, rc[0], rc[1]);
+  put_back(dv, val, 1, 4);
+  put_back(di, idx, 1, 4);
+  free(dx);
+  return 0;
+}
+
+int hfref_w8a8_dequant_memref(const void *a, const void *bt, const void *s_tok, const void *s_ch, const void *out) {
+  if (!a || !bt) return -1;
+  const hfref_memref *ma = (const hfref_memref *)a, *mb = (const hfref_memref *)bt;
+  const int64_t M = ma->dims[0], K = ma->dims[1], N = mb->dims[0];
+  const int64_t nk[2] = {N, K}, m1[1] = {M}, n1[1] = {N}, mn[2] = {M, N};
+  if (!dims_are(bt, 2, nk) || !dims_are(s_tok, 1, m1) || !dims_are(s_ch, 1, n1) || !dims_are(out, 2, mn)) return -1;
+  int8_t *da = gathered(a, 2, 1), *db = gathered(bt, 2, 1);
+  float *dst = gathered(s_tok, 1, 4), *dsc = gathered(s_ch, 1, 4);
+  uint16_t *dout = dense_for(out, 2, 2);
+  hfref_w8a8_dequant_rows(da, db, dst, dsc, dout, M, N, K, 0, M);
+  put_back(dout, out, 2, 2);
+  free(da);
+  free(db);
+  free(dst);
+  free(dsc);
+  return 0;
+}

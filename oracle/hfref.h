@@ -136,6 +136,23 @@ void hfref_w8a8_dequant_rows(const int8_t *A, const int8_t *Bt,
                              uint16_t *out, int64_t M, int64_t N, int64_t K,
                              int64_t m0, int64_t m1);
 
+/* ---- host-entry ABI: MLIR ranked memref descriptors ----
+ * The reference's runner calls `_mlir_ciface_<func>` with memref descriptors
+ * (bishengir/lib/ExecutionEngine/BiShengIRRunnerUtils.cpp:99-110): for rank R
+ * the standard layout is { T *allocated; T *aligned; int64_t offset;
+ * int64_t sizes[R]; int64_t strides[R]; } (element strides).  Every
+ * descriptor argument here is a pointer to such a struct; element (i0..iR-1)
+ * lives at aligned + offset + sum_k i_k * strides[k].  Any strides are
+ * accepted (views, slices, transposes); sizes must match the group's shapes.
+ * Returns 0, or -1 when a shape does not match. */
+int hfref_memref_gather(const void *desc, int rank, int elem_size, void *dense);
+int hfref_memref_scatter(const void *dense, const void *desc, int rank, int elem_size);
+int hfref_vecadd_f32_memref(const void *a, const void *b, const void *out);
+int hfref_rmsnorm_quant_memref(const void *x, const void *gamma, float eps, const void *q, const void *scale);
+int hfref_softmax_bf16_memref(const void *x, const void *out);
+int hfref_argmax_memref(const void *x, const void *val, const void *idx);
+int hfref_w8a8_dequant_memref(const void *a, const void *bt, const void *s_tok, const void *s_ch, const void *out);
+
 #ifdef __cplusplus
 }
 #endif

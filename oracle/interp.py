@@ -71,6 +71,13 @@ def lib():
             "hfref_softmax_bf16": [P, P, I64, I64],
             "hfref_argmax": [P, P, P, I64, I64],
             "hfref_w8a8_dequant_rows": [P, P, P, P, P, I64, I64, I64, I64, I64],
+            "hfref_memref_gather": [P, INT, INT, P],
+            "hfref_memref_scatter": [P, P, INT, INT],
+            "hfref_vecadd_f32_memref": [P, P, P],
+            "hfref_rmsnorm_quant_memref": [P, P, ctypes.c_float, P, P],
+            "hfref_softmax_bf16_memref": [P, P],
+            "hfref_argmax_memref": [P, P, P],
+            "hfref_w8a8_dequant_memref": [P, P, P, P, P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -88,6 +95,9 @@ def lib():
         L.hfref_f16_to_f32.restype = ctypes.c_float
         L.hfref_f32_to_int_mode.argtypes = [ctypes.c_float, INT, INT, INT]
         L.hfref_f32_to_int_mode.restype = ctypes.c_int64
+        for name in sig:
+            if name.endswith("_memref") or name.startswith("hfref_memref_"):
+                getattr(L, name).restype = ctypes.c_int
         L.hfref_int_to_f32_mode.argtypes = [ctypes.c_int64, INT]
         L.hfref_int_to_f32_mode.restype = ctypes.c_float
         L.hfref_fold_round_to_odd.argtypes = [ctypes.c_double]
