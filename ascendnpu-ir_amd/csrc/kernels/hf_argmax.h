@@ -269,12 +269,16 @@ __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C
     r.has_nan = has_nan;
     r.j = i;
     rec_store(&recs[blockIdx.x], r);
-    __builtin_amdgcn_s_waitcnt(0); // the record stores have completed
-    unsigned prev = __hip_atomic_fetch_add(&counters[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // release: the record happens-before the count that the last arriver
+    // reads; acquire: the last arriver's reads of the other records follow it
+    unsigned prev = __hip_atomic_fetch_add(&counters[row], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == (unsigned)(SEG - 1);
   }
   __syncthreads();
   if (!last) return;
+  // every thread of the last arriver loads records: order its loads after
+  // thread 0's acquire (the barrier above) at agent scope
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   // serial fold of the segment records, left to right: the whole workgroup
   // loads BLOCK records at a time into LDS (independent loads in flight
   // together), thread 0 folds them

@@ -277,13 +277,15 @@ __device__ __forceinline__ float erfinv_f(float yf);
 // Modified Bessel function of the first kind, order 0: the power series
 // sum_k (x^2/4)^k / (k!)^2, every term positive (no cancellation), summed in
 // double until a term no longer changes the sum, rounded once to f32.  i0 is
-// even; |x| > 100 overflows f32 (i0(92) > FLT_MAX already) and gives +inf.
-// +-inf gives NaN, as the Chebyshev form e^x * c(x) / sqrt(x) of the reference
-// lowering does (inf / inf).
+// even.  The reference lowering forms exp(|x|) * i0e(|x|) in f32
+// (Normalize.cpp:8549-8573), so from |x| = 88.72283935546875 on, where the
+// f32 exp overflows, its result is +inf although i0 itself stays below
+// FLT_MAX up to |x| ~ 91.9: those inputs give +inf here too.  +-inf gives NaN,
+// as that form does (exp(inf) * 0).
 __device__ __forceinline__ float cyl_bessel_i0_f(float xf) {
   if (__builtin_isnan(xf) || __builtin_isinf(xf)) return __builtin_nanf("");
   double x = __builtin_fabs((double)xf);
-  if (x > 100.0) return __builtin_inff();
+  if (x >= 88.72283935546875) return __builtin_inff();
   double q = 0.25 * x * x, term = 1.0, sum = 1.0;
   for (int k = 1; k < 400; ++k) {
     term *= q / ((double)k * (double)k);

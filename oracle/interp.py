@@ -429,9 +429,14 @@ def _non_dps(op, xs, shape, elem):
         # hfusion-normalize-ops.mlir:3586-3830 expands it as the Cephes
         # Chebyshev series of i0 (Clenshaw, Cephes `i0`); scipy.special.i0 is
         # the same published algorithm, evaluated here in float64
+        # the lowering multiplies exp(|x|) * i0e(|x|) in f32
+        # (Normalize.cpp:8549-8573): exp overflows from |x| = 88.72283935546875
+        # (the f32 just above ln(FLT_MAX)), so the result is +inf there
         import scipy.special
+        x64 = to_f32(xs[0]).astype(np.float64)
         with np.errstate(all="ignore"):
-            r = scipy.special.i0(to_f32(xs[0]).astype(np.float64)).astype(f32)
+            r = scipy.special.i0(x64).astype(f32)
+        r[np.isfinite(x64) & (np.abs(x64) >= 88.72283935546875)] = np.inf
         return from_f32(r, elem)
     if op == "hfusion.erfinv":
         import scipy.special

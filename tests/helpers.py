@@ -251,7 +251,7 @@ def fp_inputs(func, n=4096, seed=0x46504F50):
     if op == "cylbesseli0":
         x = rng.normal(0, 20, n).astype(np.float32)
         x[:len(specials)] = specials
-        x[len(specials):len(specials) + 6] = [85.0, 92.0, -95.0, 100.5, 13.5, 1e-3]
+        x[len(specials):len(specials) + 10] = [85.0, 92.0, -95.0, 100.5, 13.5, 1e-3, 89.0, -90.0, 91.0, 88.7228317]
         return [enc(x)]
     if op in ("isinf", "isnan", "isfinite", "signbit", "signbit8"):
         x = (rng.normal(0, 1e3, n)).astype(np.float32)

@@ -220,10 +220,13 @@ def test_signbit_against_numpy(func):
 def test_cyl_bessel_i0_closed_forms():
     """hfusion.cyl_bessel_i0 against what fixes i0: i0(0) = 1, evenness,
     the series sum_k (x^2/4)^k/(k!)^2 by brute force in exact rationals, the
-    large-x asymptote e^x/sqrt(2 pi x), f32 overflow past x ~ 91.9, and NaN
-    at +-inf (the Cephes form e^x * chbevl / sqrt(x) is inf / inf there)."""
+    large-x asymptote e^x/sqrt(2 pi x), +inf from where the lowering's f32
+    exp(|x|) overflows (|x| >= 88.72283935546875, the f32 just above
+    ln(FLT_MAX); i0 itself would stay finite up to ~91.9), and NaN at +-inf
+    (the form e^x * chbevl / sqrt(x) is inf / inf there)."""
     from fractions import Fraction
-    xs = np.array([0.0, 0.5, -0.5, 1.0, 2.5, -7.0, 20.0, 60.0, 91.0, 92.0, np.inf, -np.inf, np.nan], np.float32)
+    xs = np.array([0.0, 0.5, -0.5, 1.0, 2.5, -7.0, 20.0, 60.0, 91.0, 92.0, np.inf, -np.inf, np.nan,
+                   89.0, -90.0, 88.72283172607422, 88.72283935546875], np.float32)
     got, = run_oracle("fp_ops", [np.resize(xs, 4096)], func="cylbesseli0_f32")
     got = got[:len(xs)]
     assert got[0] == 1.0 and got[1] == got[2]
@@ -237,7 +240,12 @@ def test_cyl_bessel_i0_closed_forms():
     x = 60.0
     asym = math.exp(x) / math.sqrt(2 * math.pi * x) * (1 + 1 / (8 * x) + 9 / (2 * (8 * x) ** 2))
     assert abs(float(got[7]) / asym - 1) < 1e-5
-    assert np.isfinite(got[8]) and np.isinf(got[9]) and np.isnan(got[10]) and np.isnan(got[11]) and np.isnan(got[12])
+    assert np.isinf(got[8]) and np.isinf(got[9]) and np.isnan(got[10]) and np.isnan(got[11]) and np.isnan(got[12])
+    assert np.isinf(got[13]) and np.isinf(got[14]) and np.isinf(got[16])
+    # the largest f32 below the threshold: exp(x) is finite, and so is i0
+    assert np.float32(math.exp(88.72283172607422)) < np.inf and np.isfinite(got[15])
+    asym = math.exp(88.72283172607422) / math.sqrt(2 * math.pi * 88.72283172607422)
+    assert abs(float(got[15]) / asym - 1) < 2e-3
 
 
 def test_bitcast_op():
@@ -253,11 +261,11 @@ from helpers import misc_inputs, scan_inputs  # noqa: E402
 @pytest.mark.parametrize("spec", hf.catalog.SCAN_OPS, ids=[s[0] for s in hf.catalog.SCAN_OPS])
 def test_scan_against_numpy_accumulate(spec):
     """numpy's accumulate is a left-to-right loop in the array's dtype, so it
-    pins the serial order and the per-step rounding (bf16 excepted: numpy has
-    no bf16; that group rests on the f32 path plus the pinned RNE cast)."""
+    pins the serial order and the per-step rounding (numpy has no bf16: that
+    group is pinned by test_bf16_cumprod_exact_rounding)."""
     name, op, ie, oe, shape, dim, rev, extra = spec
     if ie == "bf16":
-        pytest.skip("no independent bf16 accumulate")
+        pytest.skip("bf16: see test_bf16_cumprod_exact_rounding")
     x, = scan_inputs(name)
     got, = run_oracle("scan_ops", [x], func=name)
     a = x.astype({"i64": np.int64}.get(oe, x.dtype))
@@ -274,6 +282,43 @@ def test_scan_against_numpy_accumulate(spec):
     if rev:
         r = np.flip(r, dim)
     assert np.array_equal(got, r, equal_nan=True)
+
+
+def _bf16_round(v):
+    """Round-half-even of the exact value v onto bf16 (8 significant bits,
+    exponents down to the subnormal quantum 2^-133, overflow to inf), by
+    scaling the significand and Python's half-even round() -- a restatement
+    independent of the bit arithmetic the oracle uses."""
+    if v == 0 or math.isinf(v) or math.isnan(v):
+        return v
+    m, e = math.frexp(abs(v))                  # |v| = m * 2^e, 0.5 <= m < 1
+    q = max(e - 8, -133)                       # quantum: 8 bits below the leading one
+    r = round(abs(v) / 2.0 ** q) * 2.0 ** q    # exact: |v| / 2^q has <= 53 bits here
+    if r >= 2.0 ** 128 * (1 - 2.0 ** -9):      # at or past the rounding boundary of bf16 max
+        r = math.inf
+    return math.copysign(r, v)
+
+
+def test_bf16_cumprod_exact_rounding():
+    """cumprod over bf16 (reverse, dim 1): each step is the exact product of
+    two bf16 values (at most 16 significant bits, exact in double) rounded
+    half-even to bf16; recomputed here in double with an independent rounding."""
+    name = "cumprod_bf16_rev"
+    spec = {s[0]: s for s in hf.catalog.SCAN_OPS}[name]
+    x, = scan_inputs(name)
+    got, = run_oracle("scan_ops", [x], func=name)
+    xf = (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    want = np.empty_like(xf)
+    for r in range(xf.shape[0]):
+        acc = None
+        for c in range(xf.shape[1] - 1, -1, -1):
+            acc = xf[r, c] if acc is None else _bf16_round(acc * xf[r, c])
+            want[r, c] = acc
+    wb = (want.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    assert spec[6] and spec[5] == 1
+    assert np.array_equal(np.asarray(got).view(np.uint16), wb)
+    # the data reach products that are not representable: rounding happened
+    assert (np.abs(want[:, :-1]) > 0).sum() > 1000
 
 
 @pytest.mark.parametrize("spec", hf.catalog.HIST_OPS, ids=[h[0] for h in hf.catalog.HIST_OPS])
