@@ -2276,11 +2276,18 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   if ((K * esz) % 16 != 0) unsupported(mm, "matmul K must span a multiple of 16 bytes");
   if (!bT && (N * esz) % 16 != 0) unsupported(mm, "matmul N must span a multiple of 16 bytes when B is [K, N]");
   if (aT && (M * esz) % 16 != 0) unsupported(mm, "matmul M must span a multiple of 16 bytes when A is [K, M]");
-  // B [N, K] and A [M, K] with whole 64-byte K steps: both operands stream into LDS by DMA
-  // LDS DMA ring: 128-byte K slices with two waves per SIMD when K allows,
-  // else 64-byte slices
-  const int dma = !(bT && !aT) ? 0 : (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
+  // LDS DMA ring (operands K-contiguous: A [M, K], B [N, K]): 128-byte K
+  // slices with two waves per SIMD when K allows, else 64-byte slices.  An
+  // operand stored the other way round (B [K, N], A [K, M]) is first copied
+  // K-contiguous into the workspace by a transpose kernel of its own, when
+  // the DMA ring applies; otherwise the register-staging path reads it as is.
+  const int dma = (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
+  const bool preB = dma != 0 && !bT, preA = dma != 0 && aT;
+  const bool kT = dma != 0 || bT;          // the main kernel's B is [N, K]
+  const bool mT = dma == 0 && aT;          // the main kernel's A is [K, M]
   const int threads = dma == 3 ? 512 : 256;
+  auto align256 = [](uint64_t v) { return (v + 255) / 256 * 256; };
+  const uint64_t wsB = preB ? align256((uint64_t)(N * K * esz)) : 0, wsA = preA ? align256((uint64_t)(M * K * esz)) : 0;
   if (!hivm) {
     const Value *acc0 = mm->outs[0];
     if (!(acc0->def && acc0->def->name == "linalg.fill" && acc0->def->ins[0]->isConst && acc0->def->ins[0]->fconst == 0.0))
@@ -2364,7 +2371,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   p.kernelName = kname;
   p.kind = "SINGLE_CUBE";
   std::ostringstream k;
-  std::string params = kernelParamList(A, p.kargs, false);
+  std::string params = kernelParamList(A, p.kargs, preA || preB);
   // epilogue functor receives all kernel pointer arguments
   k << "namespace {\nstruct " << kname << "_args {";
   for (size_t i = 0; i < A.params.size(); ++i)
@@ -2388,17 +2395,35 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
     << "  " << kname << "_args P;\n";
   for (size_t i = 0; i < A.params.size(); ++i)
     k << "  P." << (A.params[i].role == "scalar" ? "s" : "p") << i << " = " << (A.params[i].role == "scalar" ? "s" : "p") << i << ";\n";
-  k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (aT ? "true" : "false") << ", " << (bT ? "true" : "false") << ", "
-    << dma << ">((const " << (i8 ? "int8_t" : "uint16_t") << "*)p" << a->argIdx << ", (const "
-    << (i8 ? "int8_t" : "uint16_t") << "*)p" << b->argIdx
-    << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
+  const std::string et = i8 ? "int8_t" : "uint16_t";
+  const std::string aPtr = preA ? "(const " + et + "*)((char*)ws + " + std::to_string(wsB) + ")" : "(const " + et + "*)p" + std::to_string(a->argIdx);
+  const std::string bPtr = preB ? "(const " + et + "*)ws" : "(const " + et + "*)p" + std::to_string(b->argIdx);
+  k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (mT ? "true" : "false") << ", " << (kT ? "true" : "false") << ", "
+    << dma << ">(" << aPtr << ", " << bPtr << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K
+    << "ll, P);\n}\n";
+  // the re-layout kernels: [K, X] -> [X, K], 64 x 64 element tiles
+  auto preKernel = [&](const char *suffix, const Value *src, int64_t X, uint64_t off) {
+    KernelPlan::PreKernel pk;
+    pk.name = kname + suffix;
+    pk.grid = (unsigned)(((K + 63) / 64) * ((X + 63) / 64));
+    pk.block = 256;
+    pk.kargs = {"param:" + std::to_string(src->argIdx), "ws"};
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << pk.name << "(const void* __restrict__ src, void* __restrict__ ws) {\n"
+      << "  hf::mm_transpose<" << esz << ">((const char*)src, (char*)ws + " << off << ", " << K << "ll, " << X << "ll);\n}\n";
+    p.pre.push_back(pk);
+  };
+  if (preB) preKernel("_relayout_b", b, N, 0);
+  if (preA) preKernel("_relayout_a", a, M, wsB);
+  p.workspaceBytes = wsB + wsA;
   p.source = k.str();
   // 256x256 macro-tiles, one workgroup each (XCD-aware order inside the kernel)
   const int64_t TM = 256, TN = 256;
   p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
   p.block[0] = (unsigned)threads;
   p.variant = std::string(mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
-              (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") + (dma == 3 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD)" : dma == 1 ? ", LDS DMA ring" : ", register staging");
+              (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") +
+              (preA || preB ? " (re-laid K-contiguous by a transpose kernel)" : "") +
+              (dma == 3 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD)" : dma == 1 ? ", LDS DMA ring" : ", register staging");
   p.algoOps = 2.0 * (double)M * (double)N * (double)K;
   return p;
 }
@@ -3624,6 +3649,11 @@ std::string emitManifest(const KernelPlan &p, const std::string &hsacoName) {
   for (size_t i = 0; i < p.results.size(); ++i)
     s << "result " << i << " " << p.results[i].tiedParam << " " << elemName(p.results[i].elem) << " " << shp(p.results[i].shape) << "\n";
   for (auto &k : p.kargs) s << "karg " << k << "\n";
+  for (auto &pk : p.pre) {
+    s << "pre " << pk.name << " " << pk.grid << " 1 1 " << pk.block << " 1 1 " << pk.kargs.size();
+    for (auto &k : pk.kargs) s << " " << k;
+    s << "\n";
+  }
   s << "variant " << p.variant << "\n";
   return s.str();
 }

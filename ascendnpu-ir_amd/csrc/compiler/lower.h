@@ -38,6 +38,14 @@ struct KernelPlan {
   std::vector<std::string> kargs;
   double algoBytes = 0;       // algorithmic HBM bytes per launch
   double algoOps = 0;         // algorithmic ops per launch (cube groups)
+  // kernels launched before the main one on the same stream (operand
+  // re-layouts into the workspace); argument lists as `kargs`
+  struct PreKernel {
+    std::string name;
+    unsigned grid = 1, block = 256;
+    std::vector<std::string> kargs;
+  };
+  std::vector<PreKernel> pre;
 };
 
 struct LowerOptions {

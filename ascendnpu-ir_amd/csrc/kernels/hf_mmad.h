@@ -578,6 +578,38 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   mm_epilogue_lds<Epi, 2, 512>(acc, out, M, N, m0, n0, wm, wn, lane, P, &lds[0][0][0], (int)sizeof(lds));
 }
 
+// [R, C] row-major operand of ESZ-byte elements -> its [C, R] transpose, one
+// 64 x 64 element tile per workgroup of 256 threads, staged through LDS (rows
+// read and written as whole 16-byte chunks; both row lengths span a multiple
+// of 16 bytes).  Used to re-lay a [K, N] (or [K, M]) matmul operand
+// K-contiguous ahead of the DMA ring.
+template <int ESZ>
+__device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char *__restrict__ dst, int64_t R, int64_t C) {
+  constexpr int T = 64, RB = T * ESZ, CH = RB / 16, EPC = 16 / ESZ;
+  __shared__ __attribute__((aligned(16))) char tile[T][RB + 16];
+  const int64_t tilesC = (C + T - 1) / T;
+  const int64_t r0 = (int64_t)(blockIdx.x / tilesC) * T, c0 = (int64_t)(blockIdx.x % tilesC) * T;
+  for (int i = threadIdx.x; i < T * CH; i += 256) {
+    const int r = i / CH, ch = i % CH;
+    const int64_t gr = r0 + r, gc = c0 + (int64_t)ch * EPC;
+    v4i v = {0, 0, 0, 0};
+    if (gr < R && gc < C) v = *reinterpret_cast<const v4i *>(src + (gr * C + gc) * ESZ);
+    *reinterpret_cast<v4i *>(&tile[r][ch * 16]) = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * CH; i += 256) {
+    const int c = i / CH, ch = i % CH;
+    const int64_t gc = c0 + c, gr = r0 + (int64_t)ch * EPC;
+    if (gc >= C || gr >= R) continue;
+    union { v4i v; char b[16]; } u;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e)
+#pragma unroll
+      for (int b = 0; b < ESZ; ++b) u.b[e * ESZ + b] = tile[ch * EPC + e][c * ESZ + b];
+    *reinterpret_cast<v4i *>(dst + (gc * R + gr) * ESZ) = u.v;
+  }
+}
+
 // Entry: MK selects the matrix-core kind; A is [M, K] (or [K, M] with AT), B is
 // [N, K] with BT (the weight layout) or [K, N]; DMA selects the LDS DMA ring:
 // 0 none (register staging), 1 with 64-byte K slices (256 threads), 3 with

@@ -47,8 +47,18 @@ struct Karg {
   int index;
 };
 
+// A kernel the group runs before its main kernel (an operand re-layout into
+// the workspace, e.g. the [N, K] copy of a [K, N] matmul operand).
+struct PreLaunch {
+  std::string kernel;
+  hipFunction_t fn = nullptr;
+  hfr_launch_cfg cfg{};
+  std::vector<Karg> kargs;
+};
+
 struct hfr_group {
   std::string func, kernel, hsaco;
+  std::vector<PreLaunch> pre;
   hfr_module *mod = nullptr;
   hipFunction_t fn = nullptr;
   hfr_launch_cfg cfg{};
@@ -109,6 +119,13 @@ std::string dirOf(const std::string &p) {
   return s == std::string::npos ? "." : p.substr(0, s);
 }
 
+bool parseKarg(const std::string &k, Karg &a) {
+  if (k == "ws") { a.kind = Karg::Workspace; a.index = 0; return true; }
+  if (k.rfind("param:", 0) == 0) { a.kind = Karg::Param; a.index = std::atoi(k.c_str() + 6); return true; }
+  if (k.rfind("result:", 0) == 0) { a.kind = Karg::Result; a.index = std::atoi(k.c_str() + 7); return true; }
+  return false;
+}
+
 // Parses one manifest block (lines after "hfr-manifest 1" until the next one).
 int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
   for (const auto &ln : lines) {
@@ -140,23 +157,43 @@ int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
       std::string k;
       is >> k;
       Karg a;
-      if (k == "ws") { a.kind = Karg::Workspace; a.index = 0; }
-      else if (k.rfind("param:", 0) == 0) { a.kind = Karg::Param; a.index = std::atoi(k.c_str() + 6); }
-      else if (k.rfind("result:", 0) == 0) { a.kind = Karg::Result; a.index = std::atoi(k.c_str() + 7); }
-      else return fail(HFR_ERR_MANIFEST, "bad karg '" + k + "'");
+      if (!parseKarg(k, a)) return fail(HFR_ERR_MANIFEST, "bad karg '" + k + "'");
       g.kargs.push_back(a);
+    }
+    else if (key == "pre") {
+      // pre <kernel> <grid x y z> <block x y z> <n> <karg>...
+      PreLaunch pl;
+      int n = 0;
+      is >> pl.kernel >> pl.cfg.grid[0] >> pl.cfg.grid[1] >> pl.cfg.grid[2] >> pl.cfg.block[0] >> pl.cfg.block[1] >>
+          pl.cfg.block[2] >> n;
+      for (int i = 0; i < n && is; ++i) {
+        std::string k;
+        is >> k;
+        Karg a;
+        if (!parseKarg(k, a)) return fail(HFR_ERR_MANIFEST, "bad karg '" + k + "'");
+        pl.kargs.push_back(a);
+      }
+      if (!pl.cfg.grid[0] || !pl.cfg.block[0]) return fail(HFR_ERR_MANIFEST, "pre kernel without launch shape");
+      g.pre.push_back(pl);
     }
     if (is.fail()) return fail(HFR_ERR_MANIFEST, "malformed manifest line: " + ln);
   }
   if (g.kernel.empty() || g.hsaco.empty()) return fail(HFR_ERR_MANIFEST, "manifest block without kernel/hsaco");
   if (!g.cfg.block[0] || !g.cfg.grid[0]) return fail(HFR_ERR_MANIFEST, "manifest block without launch shape");
-  for (auto &a : g.kargs) {
-    if (a.kind == Karg::Param && (a.index < 0 || a.index >= (int)g.paramRoles.size()))
-      return fail(HFR_ERR_MANIFEST, "karg refers to a missing param");
-    if (a.kind == Karg::Result && (a.index < 0 || a.index >= (int)g.resultTied.size()))
-      return fail(HFR_ERR_MANIFEST, "karg refers to a missing result");
-  }
-  return HFR_OK;
+  auto check = [&](const std::vector<Karg> &ks) {
+    for (auto &a : ks) {
+      if (a.kind == Karg::Param && (a.index < 0 || a.index >= (int)g.paramRoles.size()))
+        return fail(HFR_ERR_MANIFEST, "karg refers to a missing param");
+      if (a.kind == Karg::Result && (a.index < 0 || a.index >= (int)g.resultTied.size()))
+        return fail(HFR_ERR_MANIFEST, "karg refers to a missing result");
+      if (a.kind == Karg::Workspace && !g.wsBytes) return fail(HFR_ERR_MANIFEST, "karg ws without a workspace");
+    }
+    return (int)HFR_OK;
+  };
+  int rc = check(g.kargs);
+  for (auto &pl : g.pre)
+    if (!rc) rc = check(pl.kargs);
+  return rc;
 }
 
 // Splits a manifest into group blocks ("hfr-manifest 1") and launch-program
@@ -223,19 +260,27 @@ int checkGroupArgs(const hfr_group *g, const uint64_t *params, size_t nparams, v
 }
 
 // Assembles the kernel arguments (params, own result buffers, workspace) and
-// launches the group's kernel.
+// launches the group's kernels: its pre kernels in order, then the main one,
+// all on `stream`.
 int launchGroup(const hfr_group *g, const uint64_t *params, void *const *results, void *ws, void *stream) {
-  uint64_t args[HFR_MAX_KARGS];
-  if (g->kargs.size() > HFR_MAX_KARGS) return fail(HFR_ERR_INVALID, "too many kernel arguments");
-  size_t n = 0;
-  for (auto &a : g->kargs) {
-    switch (a.kind) {
-    case Karg::Param: args[n++] = params[a.index]; break;
-    case Karg::Result: args[n++] = (uint64_t)(uintptr_t)results[a.index]; break;
-    case Karg::Workspace: args[n++] = (uint64_t)(uintptr_t)ws; break;
+  auto launch = [&](hipFunction_t fn, const hfr_launch_cfg &cfg, const std::vector<Karg> &kargs) {
+    uint64_t args[HFR_MAX_KARGS];
+    if (kargs.size() > HFR_MAX_KARGS) return fail(HFR_ERR_INVALID, "too many kernel arguments");
+    size_t n = 0;
+    for (auto &a : kargs) {
+      switch (a.kind) {
+      case Karg::Param: args[n++] = params[a.index]; break;
+      case Karg::Result: args[n++] = (uint64_t)(uintptr_t)results[a.index]; break;
+      case Karg::Workspace: args[n++] = (uint64_t)(uintptr_t)ws; break;
+      }
     }
+    return launchRaw(fn, cfg, args, n, stream);
+  };
+  for (auto &pl : g->pre) {
+    const int rc = launch(pl.fn, pl.cfg, pl.kargs);
+    if (rc) return rc;
   }
-  return launchRaw(g->fn, g->cfg, args, n, stream);
+  return launch(g->fn, g->cfg, g->kargs);
 }
 
 } // namespace
@@ -310,10 +355,12 @@ int hfr_group_load(const char *manifest_path, const char *func, hfr_group_t *out
   rc = hfr_module_load(hsaco.c_str(), &g->mod);
   if (rc) return rc;
   hipError_t e = hipModuleGetFunction(&g->fn, g->mod->mod, g->kernel.c_str());
+  for (size_t i = 0; e == hipSuccess && i < g->pre.size(); ++i)
+    e = hipModuleGetFunction(&g->pre[i].fn, g->mod->mod, g->pre[i].kernel.c_str());
   if (e != hipSuccess) {
     (void)hipGetLastError();
     hfr_module_unload(g->mod);
-    return fail(HFR_ERR_NOT_FOUND, "kernel '" + g->kernel + "' not in " + hsaco);
+    return fail(HFR_ERR_NOT_FOUND, "kernel of group '" + g->func + "' not in " + hsaco);
   }
   // the group's own workspace lives on the device current at load time, so
   // that launches stay asynchronous

@@ -153,6 +153,9 @@ def parse_manifest(path, with_programs=False):
                 b["results"].append(dict(tied=int(parts[1]), elem=parts[2], shape=_shape(parts, 3)))
             elif key == "karg":
                 b["kargs"].append(parts[0])
+            elif key == "pre":
+                b.setdefault("pre", []).append(dict(kernel=parts[0], grid=tuple(int(x) for x in parts[1:4]),
+                                                    block=tuple(int(x) for x in parts[4:7]), kargs=parts[8:]))
     return (blocks, programs) if with_programs else blocks
 
 

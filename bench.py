@@ -490,13 +490,14 @@ def main():
         torch.cuda.empty_cache()
     head = HEADLINE if HEADLINE in groups else names[0]
     h = groups[head]
-    cfg = hf.groups.CONFIGS[head]["kw"]
+    cfg = hf.groups.CONFIGS[head]["kw"] if head in hf.groups.CONFIGS else {}
     line = {
         "metric": "HBM GB/s (% of peak) per fused HFusion group; W8A8 mmad TOPS (% MFMA)",
         "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32",
-                  "argmax": "f32", "w8a8_dequant": "int8"}[head],
+        "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32", "argmax": "f32",
+                  "w8a8_dequant": "int8", "w8a8_dequant_kn": "int8", "bf16_mmad": "bf16",
+                  "transpose_cast": "bf16"}[head],
         "data": "synthetic (seeded splitmix64)",
         "config": {"workload": head, **{k: v for k, v in cfg.items()}},
         "roofline": h["roofline"],

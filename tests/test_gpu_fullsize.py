@@ -96,3 +96,19 @@ def test_w8a8_dequant_full_sampled(gpu):
     for r in SAMPLE_ROWS:
         lib().hfref_w8a8_dequant_rows(ptr(a), ptr(b), ptr(st), ptr(sc), ptr(ref), m, n, k, int(r), int(r) + 1)
     assert np.array_equal(out[SAMPLE_ROWS], ref[SAMPLE_ROWS])
+
+
+def test_w8a8_dequant_kn_full_sampled(gpu):
+    """W8A8 with B stored [K, N] (linalg.matmul): the group re-lays B
+    K-contiguous with a transpose kernel, then runs the DMA-ring contraction;
+    64 sampled rows bit-exact against the oracle fed B^T."""
+    note("w8a8_dequant_kn full 4096^3 (B [K,N]), 64 sampled rows")
+    kw = CFG["w8a8_dequant"]["kw"]
+    a, b, st, sc = I.config_inputs("w8a8_dequant", **kw)
+    m, n, k = a.shape[0], b.shape[0], a.shape[1]
+    bkn = np.ascontiguousarray(b.T)
+    out, = run_gpu("w8a8_dequant_kn", [a, bkn, st, sc, np.zeros((m, n), np.uint16)], gpu)
+    ref = np.zeros((m, n), np.uint16)
+    for r in SAMPLE_ROWS:
+        lib().hfref_w8a8_dequant_rows(ptr(a), ptr(b), ptr(st), ptr(sc), ptr(ref), m, n, k, int(r), int(r) + 1)
+    assert np.array_equal(out[SAMPLE_ROWS], ref[SAMPLE_ROWS])
