@@ -2401,11 +2401,12 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (mT ? "true" : "false") << ", " << (kT ? "true" : "false") << ", "
     << dma << ">(" << aPtr << ", " << bPtr << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K
     << "ll, P);\n}\n";
-  // the re-layout kernels: [K, X] -> [X, K], 64 x 64 element tiles
+  // the re-layout kernels: [K, X] -> [X, K], 128 x 128-byte tiles
   auto preKernel = [&](const char *suffix, const Value *src, int64_t X, uint64_t off) {
     KernelPlan::PreKernel pk;
     pk.name = kname + suffix;
-    pk.grid = (unsigned)(((K + 63) / 64) * ((X + 63) / 64));
+    const int64_t T = 128 / esz; // tile edge in elements (128 bytes)
+    pk.grid = (unsigned)(((K + T - 1) / T) * ((X + T - 1) / T));
     pk.block = 256;
     pk.kargs = {"param:" + std::to_string(src->argIdx), "ws"};
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << pk.name << "(const void* __restrict__ src, void* __restrict__ ws) {\n"

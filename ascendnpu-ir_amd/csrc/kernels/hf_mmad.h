@@ -579,14 +579,18 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
 }
 
 // [R, C] row-major operand of ESZ-byte elements -> its [C, R] transpose, one
-// 64 x 64 element tile per workgroup of 256 threads, staged through LDS (rows
-// read and written as whole 16-byte chunks; both row lengths span a multiple
-// of 16 bytes).  Used to re-lay a [K, N] (or [K, M]) matmul operand
-// K-contiguous ahead of the DMA ring.
+// tile of 128 bytes x 128 bytes (T = 128 / ESZ elements each way) per
+// workgroup of 256 threads, staged through LDS: every global read is a whole
+// 128-byte line segment, so no line is fetched by two workgroups (both row
+// lengths span a multiple of 16 bytes; ragged edges are masked in 16-byte
+// chunks).  Used to re-lay a [K, N] (or [K, M]) matmul operand K-contiguous
+// ahead of the DMA ring.  Bytes (ESZ 1): each thread reads a 16-row x 4-column
+// block as 16 dwords and transposes it in registers (v_perm); wider elements
+// are gathered element by element.
 template <int ESZ>
 __device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char *__restrict__ dst, int64_t R, int64_t C) {
-  constexpr int T = 64, RB = T * ESZ, CH = RB / 16, EPC = 16 / ESZ;
-  __shared__ __attribute__((aligned(16))) char tile[T][RB + 16];
+  constexpr int T = 128 / ESZ, CH = 8, EPC = 16 / ESZ, PITCH = 136; // row pitch: the two half-waves' rows on other banks
+  __shared__ __attribute__((aligned(16))) char tile[T][PITCH];
   const int64_t tilesC = (C + T - 1) / T;
   const int64_t r0 = (int64_t)(blockIdx.x / tilesC) * T, c0 = (int64_t)(blockIdx.x % tilesC) * T;
   for (int i = threadIdx.x; i < T * CH; i += 256) {
@@ -594,19 +598,47 @@ __device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char 
     const int64_t gr = r0 + r, gc = c0 + (int64_t)ch * EPC;
     v4i v = {0, 0, 0, 0};
     if (gr < R && gc < C) v = *reinterpret_cast<const v4i *>(src + (gr * C + gc) * ESZ);
-    *reinterpret_cast<v4i *>(&tile[r][ch * 16]) = v;
+    uint2 *t2 = reinterpret_cast<uint2 *>(&tile[r][ch * 16]);
+    t2[0] = make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+    t2[1] = make_uint2((uint32_t)v[2], (uint32_t)v[3]);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < T * CH; i += 256) {
-    const int c = i / CH, ch = i % CH;
-    const int64_t gc = c0 + c, gr = r0 + (int64_t)ch * EPC;
-    if (gc >= C || gr >= R) continue;
-    union { v4i v; char b[16]; } u;
+  if constexpr (ESZ == 1) {
+    const int c4 = threadIdx.x % 32, rb = threadIdx.x / 32; // columns 4 c4 .. +3, rows 16 rb .. +15
+    uint32_t d[16];
 #pragma unroll
-    for (int e = 0; e < EPC; ++e)
+    for (int rr = 0; rr < 16; ++rr) d[rr] = *reinterpret_cast<const uint32_t *>(&tile[16 * rb + rr][4 * c4]);
+    uint32_t o[4][4]; // o[t][w]: column 4 c4 + t, rows 16 rb + 4w .. +3
 #pragma unroll
-      for (int b = 0; b < ESZ; ++b) u.b[e * ESZ + b] = tile[ch * EPC + e][c * ESZ + b];
-    *reinterpret_cast<v4i *>(dst + (gc * R + gr) * ESZ) = u.v;
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo01 = __builtin_amdgcn_perm(d[4 * w + 1], d[4 * w], 0x05010400u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(d[4 * w + 1], d[4 * w], 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(d[4 * w + 3], d[4 * w + 2], 0x05010400u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(d[4 * w + 3], d[4 * w + 2], 0x07030602u);
+      o[0][w] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+      o[1][w] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+      o[2][w] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+      o[3][w] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+    }
+    const int64_t gr = r0 + 16 * rb;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t gc = c0 + 4 * c4 + t;
+      if (gc < C && gr < R)
+        *reinterpret_cast<v4i *>(dst + gc * R + gr) = v4i{(int)o[t][0], (int)o[t][1], (int)o[t][2], (int)o[t][3]};
+    }
+  } else {
+    for (int i = threadIdx.x; i < T * CH; i += 256) {
+      const int c = i / CH, ch = i % CH;
+      const int64_t gc = c0 + c, gr = r0 + (int64_t)ch * EPC;
+      if (gc >= C || gr >= R) continue;
+      union { v4i v; char b[16]; } u;
+#pragma unroll
+      for (int e = 0; e < EPC; ++e)
+#pragma unroll
+        for (int b = 0; b < ESZ; ++b) u.b[e * ESZ + b] = tile[ch * EPC + e][c * ESZ + b];
+      *reinterpret_cast<v4i *>(dst + (gc * R + gr) * ESZ) = u.v;
+    }
   }
 }
 
