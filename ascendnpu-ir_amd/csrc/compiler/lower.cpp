@@ -1069,6 +1069,15 @@ std::vector<int64_t> largestShape(const Func &f, const std::set<const Value *> &
   return best;
 }
 
+// A tensor value a kernel would read that no op of the group defines and that
+// is no group argument: an uninitialised tensor.empty (its contents are
+// undefined in the reference too), or an internal error.
+[[noreturn]] void undefinedValue(const Value *v) {
+  if (v->def && v->def->name == "tensor.empty")
+    throw CompileError("unsupported: the group reads the uninitialised contents of tensor.empty " + v->name);
+  throw CompileError("internal: value " + v->name + " used before definition");
+}
+
 std::string kernelParamList(const Analysis &A, std::vector<std::string> &kargs, bool withWs) {
   std::ostringstream s;
   bool first = true;
@@ -1378,7 +1387,7 @@ struct RowEmitter {
     if (!v->type.tensor) { bindScalar(v); return; }
     if (v->argIdx >= 0) { loadInput(v); return; }
     if (v->isConst) { val[v] = {Sp::Scalar, constExpr(v, v->type.elem)}; return; }
-    throw CompileError("internal: value " + v->name + " used before definition");
+    undefinedValue(v);
   }
 
   // division of an element value by a per-row (or constant) f32 divisor:
@@ -1857,7 +1866,7 @@ struct EltwiseEmitter {
       vec[v] = false;
       return;
     }
-    if (v->argIdx < 0) throw CompileError("internal: value " + v->name + " used before definition");
+    if (v->argIdx < 0) undefinedValue(v);
     int i = v->argIdx;
     const auto &m = A.map.at(v);
     int r = (int)A.D.size();
@@ -3118,7 +3127,7 @@ struct ColumnEmitter {
       else throw CompileError("non-constant scalar " + v->name);
       return;
     }
-    if (v->argIdx < 0) throw CompileError("internal: value " + v->name + " used before definition");
+    if (v->argIdx < 0) undefinedValue(v);
     const int i = v->argIdx;
     auto [off, sk] = offsetOf(A.map.at(v));
     std::string T = ctype(v->type.elem), M = mtype(v->type.elem);

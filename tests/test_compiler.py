@@ -179,6 +179,11 @@ def test_hivm_matmul_reference_form_lowers(tmp_path):
     (HIVM_OPS_MLIR.replace("xf16", "xf64"), -2, "matmul element types"),
     ("func.func @f(%a: tensor<?xf32>) -> tensor<?xf32> { return %a : tensor<?xf32> }", -1, "dynamic shapes"),
     ("module { }", -1, "no func.func"),
+    ("""func.func @test_isfinite() -> tensor<8192xi1> {
+  %0 = tensor.empty() : tensor<8192xf32>
+  %2 = hfusion.isfinite %0 : tensor<8192xf32> -> tensor<8192xi1>
+  return %2 : tensor<8192xi1>
+}""", -2, "uninitialised contents of tensor.empty"),
     ("""func.func @f(%a: tensor<4x8xf32>, %o: tensor<8xf32>, %p: tensor<4xf32>) -> (tensor<8xf32>, tensor<4xf32>)
     attributes {hacc.entry, hfusion.fusion_kind = #hfusion.fusion_kind<ANY_PBR>} {
   %r = linalg.reduce {arith.addf} ins(%a : tensor<4x8xf32>) outs(%o : tensor<8xf32>) dimensions = [0]
