@@ -70,6 +70,8 @@ static int compileMain(int argc, char **argv) {
       target = b.substr(8);
     } else if (startsWith(b, "-hipcc=")) {
       opts += "hipcc=" + b.substr(7) + ";";
+    } else if (startsWith(b, "-dyn=")) {
+      opts += "dyn=" + b.substr(5) + ";";
     } else if (startsWith(b, "-emit=")) {
       opts += "emit=" + b.substr(6) + ";";
     } else if (b == "-enable-cpu-runner" || startsWith(b, "-enable-cpu-runner=")) {

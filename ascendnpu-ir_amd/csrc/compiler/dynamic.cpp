@@ -1,0 +1,209 @@
+// Dynamic dims (`?` in tensor / memref types): shape specialisation.
+//
+// The reference compiles a dynamic-shape kernel once and reads the sizes at
+// run time from the memref descriptors, with host tiling functions choosing
+// the schedule.  Here a group is compiled per size: the caller names the size
+// of every dynamic dim of the function's arguments (compiler option
+// `dyn=<func>:<arg>.<dim>=<size>,...`), this pass makes every type of the
+// function static, and the lowering runs unchanged.  Compiled groups are
+// cached by content, so a serving loop that buckets its sizes compiles each
+// bucket once.
+//
+// Sizes flow the way the IR spells them: tensor.dim folds to the argument's
+// size, index arithmetic folds, tensor.empty takes its dynamic dims from its
+// index operands in order, a destination-style op's result takes its `outs`
+// shape, an op without `outs` takes its first input's shape, and a reshape
+// (expand_shape / collapse_shape) with one dynamic dim takes it from the
+// element count.
+#include "ir.h"
+
+#include <map>
+#include <sstream>
+
+namespace hfc {
+
+bool hasDynamicDims(const Module &m) {
+  for (auto &v : m.values)
+    for (auto d : v->type.shape)
+      if (d < 0) return true;
+  return false;
+}
+
+namespace {
+
+bool isDynamic(const Type &t) {
+  for (auto d : t.shape)
+    if (d < 0) return true;
+  return false;
+}
+
+int64_t numelOf(const std::vector<int64_t> &s) {
+  int64_t n = 1;
+  for (auto d : s) n *= d;
+  return n;
+}
+
+// folds the index-typed scalar arithmetic that dynamic sizes go through
+void foldIndex(Op *op) {
+  if (op->results.empty()) return;
+  Value *r = op->results[0];
+  const std::string &n = op->name;
+  if (n == "arith.constant") {
+    // integer / index literals (the lowering folds every constant later)
+    if (!r->type.tensor && !isFloat(r->type.elem) && !op->literal.empty()) {
+      try {
+        r->iconst = std::stoll(op->literal, nullptr, 0);
+        r->fconst = (double)r->iconst;
+        r->isConst = true;
+      } catch (const std::exception &) {
+      }
+    }
+    return;
+  }
+  if (n == "tensor.dim") {
+    if (op->operands.size() == 2 && op->operands[1]->isConst) {
+      const auto &sh = op->operands[0]->type.shape;
+      const int64_t i = op->operands[1]->iconst;
+      if (i < 0 || i >= (int64_t)sh.size()) throw CompileError("tensor.dim index out of range at line " + std::to_string(op->line));
+      if (sh[i] >= 0) {
+        r->isConst = true;
+        r->iconst = sh[i];
+        r->fconst = (double)sh[i];
+      }
+    }
+    return;
+  }
+  if (r->type.tensor || r->isConst || op->operands.empty()) return;
+  for (auto *o : op->operands)
+    if (!o->isConst) return;
+  const int64_t a = op->operands[0]->iconst, b = op->operands.size() > 1 ? op->operands[1]->iconst : 0;
+  bool ok = true;
+  int64_t v = 0;
+  if (n == "arith.index_cast" || n == "arith.index_castui" || n == "arith.extsi" || n == "arith.extui" ||
+      n == "arith.trunci") v = a;
+  else if (n == "arith.addi") v = a + b;
+  else if (n == "arith.subi") v = a - b;
+  else if (n == "arith.muli") v = a * b;
+  else if ((n == "arith.divsi" || n == "arith.divui" || n == "arith.floordivsi") && b) v = a / b;
+  else if (n == "arith.ceildivsi" && b) v = (a + b - 1) / b;
+  else if (n == "arith.maxsi") v = a > b ? a : b;
+  else if (n == "arith.minsi") v = a < b ? a : b;
+  else ok = false;
+  if (ok && (r->type.elem == Elem::Index || !isFloat(r->type.elem))) {
+    r->isConst = true;
+    r->iconst = v;
+    r->fconst = (double)v;
+  }
+}
+
+[[noreturn]] void cannot(const Op *op, const Value *v) {
+  throw CompileError("cannot infer the dynamic shape of " + v->name + " ('" + op->name + "' at line " +
+                     std::to_string(op->line) + ")");
+}
+
+void specializeFunc(Func &f, const std::map<std::pair<int, int>, int64_t> &sizes) {
+  for (Value *a : f.args) {
+    for (size_t d = 0; d < a->type.shape.size(); ++d) {
+      if (a->type.shape[d] >= 0) continue;
+      auto it = sizes.find({a->argIdx, (int)d});
+      if (it == sizes.end())
+        throw CompileError("dynamic dim " + std::to_string(d) + " of argument " + std::to_string(a->argIdx) + " of @" +
+                           f.name + " has no size (compile with dyn=" + f.name + ":" + std::to_string(a->argIdx) + "." +
+                           std::to_string(d) + "=<size>)");
+      if (it->second < 0) throw CompileError("negative size for a dynamic dim of @" + f.name);
+      a->type.shape[d] = it->second;
+    }
+  }
+  for (Op *op : f.ops) {
+    foldIndex(op);
+    for (size_t ri = 0; ri < op->results.size(); ++ri) {
+      Value *r = op->results[ri];
+      if (!isDynamic(r->type)) continue;
+      auto &sh = r->type.shape;
+      const std::string &n = op->name;
+      if (n == "tensor.empty") {
+        size_t k = 0;
+        for (auto &d : sh) {
+          if (d >= 0) continue;
+          if (k >= op->operands.size() || !op->operands[k]->isConst) cannot(op, r);
+          d = op->operands[k++]->iconst;
+        }
+      } else if (n == "tensor.expand_shape" || n == "tensor.collapse_shape") {
+        const Value *src = op->operands.empty() ? nullptr : op->operands[0];
+        int unknown = 0;
+        int64_t known = 1;
+        for (auto d : sh) {
+          if (d < 0) ++unknown;
+          else known *= d;
+        }
+        if (!src || isDynamic(src->type) || unknown != 1 || known == 0) cannot(op, r);
+        for (auto &d : sh)
+          if (d < 0) d = numelOf(src->type.shape) / known;
+      } else if (ri < op->outs.size() && !isDynamic(op->outs[ri]->type) &&
+                 op->outs[ri]->type.shape.size() == sh.size()) {
+        sh = op->outs[ri]->type.shape;
+      } else if (op->outs.empty() && !op->ins.empty() && !isDynamic(op->ins[0]->type) &&
+                 op->ins[0]->type.shape.size() == sh.size()) {
+        sh = op->ins[0]->type.shape;
+      } else if (op->outs.empty() && op->ins.empty() && !op->operands.empty() && op->operands[0]->type.tensor &&
+                 !isDynamic(op->operands[0]->type) && op->operands[0]->type.shape.size() == sh.size()) {
+        sh = op->operands[0]->type.shape;
+      } else {
+        cannot(op, r);
+      }
+    }
+    // elementwise ops take operands of one shape: sizes given for different
+    // arguments must agree where the IR joins them
+    if (!op->outs.empty() && (op->name.find("elemwise") != std::string::npos || op->name == "hfusion.cast" ||
+                              op->name == "hfusion.compare" || op->name == "hfusion.select")) {
+      const auto &want = op->outs[0]->type.shape;
+      for (Value *v : op->ins)
+        if (v->type.tensor && v->type.shape.size() == want.size() && v->type.shape != want)
+          throw CompileError("the sizes given for the dynamic dims disagree: '" + op->name + "' at line " +
+                             std::to_string(op->line) + " joins " + v->type.str() + " and " + op->outs[0]->type.str());
+    }
+    for (size_t i = 0; i < op->results.size() && i < op->outs.size(); ++i)
+      if (op->outs[i]->type.tensor && op->results[i]->type.shape != op->outs[i]->type.shape)
+        throw CompileError("the sizes given for the dynamic dims disagree: the result of '" + op->name + "' at line " +
+                           std::to_string(op->line) + " is " + op->results[i]->type.str() + ", its destination " +
+                           op->outs[i]->type.str());
+    // the types kept beside the operands follow their values
+    for (size_t i = 0; i < op->ins.size() && i < op->insTypes.size(); ++i) op->insTypes[i] = op->ins[i]->type;
+    for (size_t i = 0; i < op->outs.size() && i < op->outsTypes.size(); ++i) op->outsTypes[i] = op->outs[i]->type;
+    if (isDynamic(op->literalType) && !op->results.empty()) op->literalType.shape = op->results[0]->type.shape;
+    if (isDynamic(op->toType) && !op->results.empty()) op->toType.shape = op->results[0]->type.shape;
+  }
+  for (size_t i = 0; i < f.resultTypes.size() && i < f.returns.size(); ++i) f.resultTypes[i] = f.returns[i]->type;
+}
+
+} // namespace
+
+void specializeDynamic(Module &m, const std::string &spec) {
+  // spec: <func>:<arg>.<dim>=<size>, comma-separated
+  std::map<std::string, std::map<std::pair<int, int>, int64_t>> sizes;
+  std::stringstream ss(spec);
+  std::string item;
+  while (std::getline(ss, item, ',')) {
+    if (item.empty()) continue;
+    const auto colon = item.rfind(':'), dot = item.find('.', colon == std::string::npos ? 0 : colon),
+               eq = item.find('=');
+    if (colon == std::string::npos || dot == std::string::npos || eq == std::string::npos || !(colon < dot && dot < eq))
+      throw CompileError("bad dyn entry '" + item + "' (expected <func>:<arg>.<dim>=<size>)");
+    try {
+      sizes[item.substr(0, colon)][{std::stoi(item.substr(colon + 1, dot - colon - 1)),
+                                    std::stoi(item.substr(dot + 1, eq - dot - 1))}] = std::stoll(item.substr(eq + 1));
+    } catch (const std::exception &) {
+      throw CompileError("bad dyn entry '" + item + "'");
+    }
+  }
+  for (auto &f : m.funcs) {
+    bool dyn = false;
+    for (Value *a : f->args) dyn |= isDynamic(a->type);
+    for (Op *op : f->ops)
+      for (Value *r : op->results) dyn |= isDynamic(r->type);
+    if (!dyn) continue;
+    specializeFunc(*f, sizes[f->name]);
+  }
+}
+
+} // namespace hfc

@@ -99,11 +99,24 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
     setErr(err, errlen, std::string("parse error (internal): ") + e.what());
     return HFC_ERR_PARSE;
   }
+  // dynamic dims: specialised to the sizes the caller names (option dyn=...)
+  const bool dynamic = hfc::hasDynamicDims(*mod);
+  if (dynamic) {
+    try {
+      hfc::specializeDynamic(*mod, opts.count("dyn") ? opts["dyn"] : "");
+    } catch (const hfc::CompileError &e) {
+      setErr(err, errlen, std::string("dynamic shapes: ") + e.what());
+      return HFC_ERR_PARSE;
+    }
+  }
   // fusion front-end: functions that are not one group yet are split into
   // outlined groups plus a launch program
   std::vector<hfc::ProgramPlan> programs;
   try {
     std::string outlined = hfc::outlineFusedGroups(*mod, programs, opts.count("fusion_kind") ? opts["fusion_kind"] : "");
+    if (dynamic && !programs.empty())
+      throw hfc::CompileError("a function with dynamic dims must be one group (the fusion front-end re-reads "
+                              "outlined groups from their source text, which keeps the dynamic types)");
     if (opts.count("emit") && opts["emit"] == "outlined") {
       std::string man;
       for (auto &p : programs) man += hfc::emitProgramManifest(p);

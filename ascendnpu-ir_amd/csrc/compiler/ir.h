@@ -117,4 +117,10 @@ struct Module {
 // number on anything it does not understand.
 std::unique_ptr<Module> parseModule(const std::string &text);
 
+// Dynamic dims (shape -1 after parsing): true when any value has one.
+bool hasDynamicDims(const Module &m);
+// Makes every type static from the sizes of the functions' dynamic argument
+// dims, spec "<func>:<arg>.<dim>=<size>,..." (dynamic.cpp).
+void specializeDynamic(Module &m, const std::string &spec);
+
 } // namespace hfc

@@ -213,8 +213,14 @@ Type parseTypeText(const std::string &s, int line) {
     size_t p = 0;
     while (true) {
       size_t x = cleaned.find('x', p);
-      if (x == std::string::npos || !std::isdigit((unsigned char)cleaned[p])) break;
+      if (x == std::string::npos) break;
       std::string d = cleaned.substr(p, x - p);
+      if (d == "?") { // a dynamic dim: -1 until specialised (dynamic.cpp)
+        ty.shape.push_back(-1);
+        p = x + 1;
+        continue;
+      }
+      if (!std::isdigit((unsigned char)cleaned[p])) break;
       bool alldig = !d.empty();
       for (char c : d) alldig &= std::isdigit((unsigned char)c) != 0;
       if (!alldig) break;
@@ -223,8 +229,7 @@ Type parseTypeText(const std::string &s, int line) {
     }
     std::string e = cleaned.substr(p);
     if (e.find('?') != std::string::npos)
-      throw CompileError("dynamic shapes are not supported (line " +
-                         std::to_string(line) + ")");
+      throw CompileError("unsupported dynamic type '" + s + "' at line " + std::to_string(line));
     try {
       ty.elem = parseElem(e);
     } catch (CompileError &) {
@@ -638,8 +643,9 @@ private:
         pos_ += 3;
         continue;
       }
-      if (isP(t, "(") && peek(1).kind == Tok::Value) {
-        // region block arguments `(%in: f32, %init: f32)`
+      if (isP(t, "(") && peek(1).kind == Tok::Value && isP(peek(2), ":")) {
+        // region block arguments `(%in: f32, %init: f32)` (an operand list
+        // such as tensor.empty(%d0, %d1) falls through to the value case)
         int depth = 0;
         do {
           if (isP(peek(), "(")) ++depth;

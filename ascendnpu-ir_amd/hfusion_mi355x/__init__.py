@@ -8,7 +8,7 @@ The compile step is `bishengir-compile --target=mi355x` (libhfc); the launch
 goes through the C-ABI runtime libhfr (hipModuleLaunchKernel).
 """
 from . import catalog, groups, inputs, native
-from .runtime import Artifact, CompileError, Group, Program, compile, load, parse_manifest, torch_dtype
+from .runtime import Artifact, CompileError, DynamicGroup, Group, Program, compile, load, parse_manifest, torch_dtype
 
-__all__ = ["Artifact", "CompileError", "Group", "catalog", "compile", "groups", "inputs", "load", "native",
+__all__ = ["Artifact", "CompileError", "DynamicGroup", "Group", "catalog", "compile", "groups", "inputs", "load", "native",
            "parse_manifest", "torch_dtype", "Program"]

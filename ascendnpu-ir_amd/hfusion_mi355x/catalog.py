@@ -953,6 +953,10 @@ def entries():
     e["any_pbr_ops"] = any_pbr_ops()
     e["transpose_ops"] = transpose_ops()
     e["transpose_cast"] = g.transpose_cast(4096, 8192)
+    # dynamic row counts (compiled per size: DynamicGroup / option dyn=...)
+    e["rmsnorm_quant_dyn"] = g.with_dynamic_rows(g.rmsnorm_quant(7919, 4096), 7919)
+    e["softmax_dyn"] = g.with_dynamic_rows(g.safe_softmax(7919, 1000), 7919)
+    e["vec_add_dyn"] = g.with_dynamic_rows(g.vec_add(7919), 7919)
     # the W8A8 contraction with B in the [K, N] layout of linalg.matmul
     e["w8a8_dequant_kn"] = g.w8a8_dequant(4096, 4096, 4096, b_layout="kn").replace("@w8a8_dequant(", "@w8a8_dequant_kn(")
     e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
@@ -991,6 +995,21 @@ def get(name):
     return entries()[name]
 
 
+# row counts the dynamic groups are prebuilt for (the GPU tests call them with these)
+DYN_ROWS = {"rmsnorm_quant_dyn": [1, 37, 300], "softmax_dyn": [5, 129], "vec_add_dyn": [1, 1000, 65537]}
+
+
+def dyn_options(name, rows):
+    """The specialisation option of a dynamic catalog group at `rows` rows
+    (every dynamic dim of these groups is the row count)."""
+    from .runtime import DynamicGroup
+    dg = DynamicGroup(get(name))
+    return dg.options_for([rows] * len(dg.dims))
+
+
 def options(name):
-    """Compiler options a prebuilt group is built with ("" for the defaults)."""
+    """Compiler options a prebuilt group is built with ("" for the defaults;
+    a dynamic group: its first prebuilt row count)."""
+    if name in DYN_ROWS:
+        return dyn_options(name, DYN_ROWS[name][0])
     return "rmsq_kernel=1" if name.endswith("_rmsq") else ""

@@ -30,6 +30,20 @@ def vec_add(n=1 << 24, dtype="f32"):
 """
 
 
+def with_dynamic_rows(ir, rows):
+    """The same group with its leading (row) dim `rows` dynamic: every type
+    `tensor<rows x ...>` spelled `tensor<? x ...>`, and every tensor.empty of
+    such a type sized by `tensor.dim` of the first argument (`rows` must be a
+    number no other dim of the group uses)."""
+    import re
+    out = ir.replace(f"<{rows}x", "<?x")
+    m = re.search(r"func\.func @\w+\((%[\w]+): (tensor<[^>]*>)", out)
+    arg, ty = m.group(1), m.group(2)
+    out = out.replace("tensor.empty() : tensor<?x", "tensor.empty(%rows_) : tensor<?x")
+    j = out.index("{\n", m.end()) + 2  # the body's first line
+    return out[:j] + f"    %c0_ = arith.constant 0 : index\n    %rows_ = tensor.dim {arg}, %c0_ : {ty}\n" + out[j:]
+
+
 def rmsnorm_quant(rows=8192, cols=4096, eps=1e-6, batch=None):
     """RMSNorm (structure of compile-rms-norm-fp32-split-n.mlir:5-47) followed by
     dynamic per-token int8 quantisation with explicit rounding

@@ -332,3 +332,79 @@ class Program:
 def load(ir_text, func=None, options="", require_cached=False):
     """compile() + load(): the one-call host entry."""
     return compile(ir_text, options=options, require_cached=require_cached).load(func)
+
+
+def _split_args(sig):
+    """Top-level comma split of a func signature's argument list."""
+    out, depth, cur = [], 0, ""
+    for c in sig:
+        if c in "<({[":
+            depth += 1
+        elif c in ">)}]":
+            depth -= 1
+        if c == "," and depth == 0:
+            out.append(cur)
+            cur = ""
+        else:
+            cur += c
+    if cur.strip():
+        out.append(cur)
+    return out
+
+
+def dynamic_dims(ir_text, func=None):
+    """[(func, arg, dim)] of every dynamic (`?`) dim of the arguments of the
+    module's functions (of `func` only when given), in argument order."""
+    import re
+    dims = []
+    for m in re.finditer(r"func\.func\s+(?:private\s+)?@([\w.$-]+)\s*\(", ir_text):
+        name = m.group(1)
+        if func is not None and name != func:
+            continue
+        depth, i = 1, m.end()
+        while depth:
+            depth += {"(": 1, ")": -1}.get(ir_text[i], 0)
+            i += 1
+        for a, arg in enumerate(_split_args(ir_text[m.end():i - 1])):
+            t = re.search(r"(?:tensor|memref)<([^>]*)>", arg)
+            if not t:
+                continue
+            shape = t.group(1).split(",")[0].replace(" ", "").split("x")[:-1]
+            dims += [(name, a, d) for d, s in enumerate(shape) if s == "?"]
+    return dims
+
+
+class DynamicGroup:
+    """A group whose IR has dynamic (`?`) dims, compiled per set of sizes.
+
+    The sizes of the dynamic argument dims are read from the tensors of each
+    call; the group is specialised to them (compiler option
+    `dyn=<func>:<arg>.<dim>=<size>,...`: every type of the function becomes
+    static) and compiled once per size set, content-cached like any group.
+    A serving loop that buckets its sizes compiles each bucket once.  With
+    `require_cached`, a size set that was not prebuilt raises instead of
+    compiling."""
+
+    def __init__(self, ir_text, func=None, options="", require_cached=False):
+        self.ir_text, self.func, self.options, self.require_cached = ir_text, func, options, require_cached
+        self.dims = dynamic_dims(ir_text, func)
+        if not self.dims:
+            raise ValueError("the group has no dynamic dims; use load()")
+        self._groups = {}
+
+    def options_for(self, sizes):
+        spec = ",".join(f"{f}:{a}.{d}={int(s)}" for (f, a, d), s in zip(self.dims, sizes))
+        return (self.options + ";" if self.options else "") + "dyn=" + spec
+
+    def sizes_of(self, args):
+        return tuple(int(args[a].shape[d]) for _, a, d in self.dims)
+
+    def specialise(self, sizes):
+        sizes = tuple(int(s) for s in sizes)
+        if sizes not in self._groups:
+            art = compile(self.ir_text, options=self.options_for(sizes), require_cached=self.require_cached)
+            self._groups[sizes] = art.load(self.func)
+        return self._groups[sizes]
+
+    def __call__(self, *args, **kw):
+        return self.specialise(self.sizes_of(args))(*args, **kw)

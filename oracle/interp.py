@@ -141,7 +141,8 @@ def parse_type(s):
     if m:
         body = _split_top(m.group(1))[0]  # memref layout / address space after the first comma
         parts = body.replace(" ", "").split("x")
-        return tuple(int(p) for p in parts[:-1]), parts[-1]
+        # a dynamic dim `?` is -1: its size comes from the values at run time
+        return tuple(-1 if p == "?" else int(p) for p in parts[:-1]), parts[-1]
     return None, s
 
 
@@ -624,7 +625,7 @@ class Interp:
                 env[nm] = T(np.asarray(x, dtype=NP[elem]), elem)
             else:
                 a = np.array(x, dtype=NP[elem], order="C")  # keeps rank 0
-                if a.shape != shape:
+                if len(a.shape) != len(shape) or any(d >= 0 and d != g for d, g in zip(shape, a.shape)):
                     raise ValueError(f"{nm}: expected shape {shape}, got {a.shape}")
                 env[nm] = T(a.copy(), elem)
         self.written = []
@@ -734,6 +735,10 @@ class Interp:
             return
         if op == "tensor.empty":
             shape, elem = parse_type(rest.split(":", 1)[1])
+            if -1 in shape:
+                # tensor.empty(%d0, ...): the dynamic dims in order
+                dyn = iter(int(env[n].a) for n in re.findall(r"%[\w.$-]+", rest.split(":", 1)[0]))
+                shape = tuple(next(dyn) if d < 0 else d for d in shape)
             env[res] = T(np.zeros(shape, NP[elem]), elem)
             self.empties.add(res)
             return
@@ -767,6 +772,8 @@ class Interp:
         if op in _NON_DPS:
             names = re.findall(r"%[\w.$-]+", rest.split(":", 1)[0])
             shape, elem = parse_type(rest.rsplit("->", 1)[1])
+            if -1 in shape:
+                shape = env[names[0]].a.shape
             xs = [T(np.broadcast_to(env[n].a, shape), env[n].elem) for n in names]
             env[res] = T(_contig(_non_dps(op, xs, shape, elem)), elem)
             return

@@ -15,10 +15,10 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CLI = os.path.join(native.BIN_DIR, "bishengir-compile")
 
 
-def emit(ir, tmp_path, name="g"):
+def emit(ir, tmp_path, name="g", options=""):
     prefix = str(tmp_path / name)
     err = ctypes.create_string_buffer(8192)
-    rc = native.hfc().hfc_compile(ir.encode(), prefix.encode(), b"emit=hip", err, len(err))
+    rc = native.hfc().hfc_compile(ir.encode(), prefix.encode(), ("emit=hip;" + options).encode(), err, len(err))
     return rc, err.value.decode(), prefix
 
 
@@ -54,7 +54,7 @@ def test_manifest_rejects_garbage(tmp_path):
 
 @pytest.mark.parametrize("name", sorted(hf.catalog.entries()))
 def test_every_catalog_group_lowers(name, tmp_path):
-    rc, err, prefix = emit(hf.catalog.get(name), tmp_path)
+    rc, err, prefix = emit(hf.catalog.get(name), tmp_path, options=hf.catalog.options(name))
     assert rc == 0, err
     blocks = hf.parse_manifest(prefix + ".manifest")
     for b in blocks:
