@@ -217,682 +217,60 @@ __device__ __forceinline__ float lds_chain_sum(const float *rp, float acc) {
     // hidden behind the chain.  One asm statement, so no compiler code runs
     // between a read and the wait that covers it.
     const uint32_t p = (uint32_t)(uintptr_t)rp;
+#define HF_ADD(r) "v_add_f32 %[acc], v" #r ", %[acc]\n"
+#define HF_ADD16_A HF_ADD(224) HF_ADD(225) HF_ADD(226) HF_ADD(227) HF_ADD(228) HF_ADD(229) HF_ADD(230) HF_ADD(231) \
+  HF_ADD(232) HF_ADD(233) HF_ADD(234) HF_ADD(235) HF_ADD(236) HF_ADD(237) HF_ADD(238) HF_ADD(239)
+#define HF_ADD16_B HF_ADD(240) HF_ADD(241) HF_ADD(242) HF_ADD(243) HF_ADD(244) HF_ADD(245) HF_ADD(246) HF_ADD(247) \
+  HF_ADD(248) HF_ADD(249) HF_ADD(250) HF_ADD(251) HF_ADD(252) HF_ADD(253) HF_ADD(254) HF_ADD(255)
+#define HF_RD(lo, hi, off) "ds_read_b128 v[" #lo ":" #hi "], %[p] offset:" #off "\n"
+// group g's 16 floats (bytes 64g .. 64g+63) into buffer A (v224-v239) or B (v240-v255)
+#define HF_RD_A(o0, o1, o2, o3) HF_RD(224, 227, o0) HF_RD(228, 231, o1) HF_RD(232, 235, o2) HF_RD(236, 239, o3)
+#define HF_RD_B(o0, o1, o2, o3) HF_RD(240, 243, o0) HF_RD(244, 247, o1) HF_RD(248, 251, o2) HF_RD(252, 255, o3)
+#define HF_W4 "s_waitcnt lgkmcnt(4)\n" // the older group has landed; the newer stays in flight
     asm volatile(
-      "ds_read_b128 v[224:227], %[p] offset:0\n"
-      "ds_read_b128 v[228:231], %[p] offset:16\n"
-      "ds_read_b128 v[232:235], %[p] offset:32\n"
-      "ds_read_b128 v[236:239], %[p] offset:48\n"
-      "ds_read_b128 v[240:243], %[p] offset:64\n"
-      "ds_read_b128 v[244:247], %[p] offset:80\n"
-      "ds_read_b128 v[248:251], %[p] offset:96\n"
-      "ds_read_b128 v[252:255], %[p] offset:112\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:128\n"
-      "ds_read_b128 v[228:231], %[p] offset:144\n"
-      "ds_read_b128 v[232:235], %[p] offset:160\n"
-      "ds_read_b128 v[236:239], %[p] offset:176\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:192\n"
-      "ds_read_b128 v[244:247], %[p] offset:208\n"
-      "ds_read_b128 v[248:251], %[p] offset:224\n"
-      "ds_read_b128 v[252:255], %[p] offset:240\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:256\n"
-      "ds_read_b128 v[228:231], %[p] offset:272\n"
-      "ds_read_b128 v[232:235], %[p] offset:288\n"
-      "ds_read_b128 v[236:239], %[p] offset:304\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:320\n"
-      "ds_read_b128 v[244:247], %[p] offset:336\n"
-      "ds_read_b128 v[248:251], %[p] offset:352\n"
-      "ds_read_b128 v[252:255], %[p] offset:368\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:384\n"
-      "ds_read_b128 v[228:231], %[p] offset:400\n"
-      "ds_read_b128 v[232:235], %[p] offset:416\n"
-      "ds_read_b128 v[236:239], %[p] offset:432\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:448\n"
-      "ds_read_b128 v[244:247], %[p] offset:464\n"
-      "ds_read_b128 v[248:251], %[p] offset:480\n"
-      "ds_read_b128 v[252:255], %[p] offset:496\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:512\n"
-      "ds_read_b128 v[228:231], %[p] offset:528\n"
-      "ds_read_b128 v[232:235], %[p] offset:544\n"
-      "ds_read_b128 v[236:239], %[p] offset:560\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:576\n"
-      "ds_read_b128 v[244:247], %[p] offset:592\n"
-      "ds_read_b128 v[248:251], %[p] offset:608\n"
-      "ds_read_b128 v[252:255], %[p] offset:624\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:640\n"
-      "ds_read_b128 v[228:231], %[p] offset:656\n"
-      "ds_read_b128 v[232:235], %[p] offset:672\n"
-      "ds_read_b128 v[236:239], %[p] offset:688\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:704\n"
-      "ds_read_b128 v[244:247], %[p] offset:720\n"
-      "ds_read_b128 v[248:251], %[p] offset:736\n"
-      "ds_read_b128 v[252:255], %[p] offset:752\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:768\n"
-      "ds_read_b128 v[228:231], %[p] offset:784\n"
-      "ds_read_b128 v[232:235], %[p] offset:800\n"
-      "ds_read_b128 v[236:239], %[p] offset:816\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:832\n"
-      "ds_read_b128 v[244:247], %[p] offset:848\n"
-      "ds_read_b128 v[248:251], %[p] offset:864\n"
-      "ds_read_b128 v[252:255], %[p] offset:880\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:896\n"
-      "ds_read_b128 v[228:231], %[p] offset:912\n"
-      "ds_read_b128 v[232:235], %[p] offset:928\n"
-      "ds_read_b128 v[236:239], %[p] offset:944\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:960\n"
-      "ds_read_b128 v[244:247], %[p] offset:976\n"
-      "ds_read_b128 v[248:251], %[p] offset:992\n"
-      "ds_read_b128 v[252:255], %[p] offset:1008\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1024\n"
-      "ds_read_b128 v[228:231], %[p] offset:1040\n"
-      "ds_read_b128 v[232:235], %[p] offset:1056\n"
-      "ds_read_b128 v[236:239], %[p] offset:1072\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1088\n"
-      "ds_read_b128 v[244:247], %[p] offset:1104\n"
-      "ds_read_b128 v[248:251], %[p] offset:1120\n"
-      "ds_read_b128 v[252:255], %[p] offset:1136\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1152\n"
-      "ds_read_b128 v[228:231], %[p] offset:1168\n"
-      "ds_read_b128 v[232:235], %[p] offset:1184\n"
-      "ds_read_b128 v[236:239], %[p] offset:1200\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1216\n"
-      "ds_read_b128 v[244:247], %[p] offset:1232\n"
-      "ds_read_b128 v[248:251], %[p] offset:1248\n"
-      "ds_read_b128 v[252:255], %[p] offset:1264\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1280\n"
-      "ds_read_b128 v[228:231], %[p] offset:1296\n"
-      "ds_read_b128 v[232:235], %[p] offset:1312\n"
-      "ds_read_b128 v[236:239], %[p] offset:1328\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1344\n"
-      "ds_read_b128 v[244:247], %[p] offset:1360\n"
-      "ds_read_b128 v[248:251], %[p] offset:1376\n"
-      "ds_read_b128 v[252:255], %[p] offset:1392\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1408\n"
-      "ds_read_b128 v[228:231], %[p] offset:1424\n"
-      "ds_read_b128 v[232:235], %[p] offset:1440\n"
-      "ds_read_b128 v[236:239], %[p] offset:1456\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1472\n"
-      "ds_read_b128 v[244:247], %[p] offset:1488\n"
-      "ds_read_b128 v[248:251], %[p] offset:1504\n"
-      "ds_read_b128 v[252:255], %[p] offset:1520\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1536\n"
-      "ds_read_b128 v[228:231], %[p] offset:1552\n"
-      "ds_read_b128 v[232:235], %[p] offset:1568\n"
-      "ds_read_b128 v[236:239], %[p] offset:1584\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1600\n"
-      "ds_read_b128 v[244:247], %[p] offset:1616\n"
-      "ds_read_b128 v[248:251], %[p] offset:1632\n"
-      "ds_read_b128 v[252:255], %[p] offset:1648\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1664\n"
-      "ds_read_b128 v[228:231], %[p] offset:1680\n"
-      "ds_read_b128 v[232:235], %[p] offset:1696\n"
-      "ds_read_b128 v[236:239], %[p] offset:1712\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1728\n"
-      "ds_read_b128 v[244:247], %[p] offset:1744\n"
-      "ds_read_b128 v[248:251], %[p] offset:1760\n"
-      "ds_read_b128 v[252:255], %[p] offset:1776\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1792\n"
-      "ds_read_b128 v[228:231], %[p] offset:1808\n"
-      "ds_read_b128 v[232:235], %[p] offset:1824\n"
-      "ds_read_b128 v[236:239], %[p] offset:1840\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1856\n"
-      "ds_read_b128 v[244:247], %[p] offset:1872\n"
-      "ds_read_b128 v[248:251], %[p] offset:1888\n"
-      "ds_read_b128 v[252:255], %[p] offset:1904\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "ds_read_b128 v[224:227], %[p] offset:1920\n"
-      "ds_read_b128 v[228:231], %[p] offset:1936\n"
-      "ds_read_b128 v[232:235], %[p] offset:1952\n"
-      "ds_read_b128 v[236:239], %[p] offset:1968\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
-      "ds_read_b128 v[240:243], %[p] offset:1984\n"
-      "ds_read_b128 v[244:247], %[p] offset:2000\n"
-      "ds_read_b128 v[248:251], %[p] offset:2016\n"
-      "ds_read_b128 v[252:255], %[p] offset:2032\n"
-      "s_waitcnt lgkmcnt(4)\n"
-      "v_add_f32 %[acc], v224, %[acc]\n"
-      "v_add_f32 %[acc], v225, %[acc]\n"
-      "v_add_f32 %[acc], v226, %[acc]\n"
-      "v_add_f32 %[acc], v227, %[acc]\n"
-      "v_add_f32 %[acc], v228, %[acc]\n"
-      "v_add_f32 %[acc], v229, %[acc]\n"
-      "v_add_f32 %[acc], v230, %[acc]\n"
-      "v_add_f32 %[acc], v231, %[acc]\n"
-      "v_add_f32 %[acc], v232, %[acc]\n"
-      "v_add_f32 %[acc], v233, %[acc]\n"
-      "v_add_f32 %[acc], v234, %[acc]\n"
-      "v_add_f32 %[acc], v235, %[acc]\n"
-      "v_add_f32 %[acc], v236, %[acc]\n"
-      "v_add_f32 %[acc], v237, %[acc]\n"
-      "v_add_f32 %[acc], v238, %[acc]\n"
-      "v_add_f32 %[acc], v239, %[acc]\n"
-      "s_waitcnt lgkmcnt(0)\n"
-      "v_add_f32 %[acc], v240, %[acc]\n"
-      "v_add_f32 %[acc], v241, %[acc]\n"
-      "v_add_f32 %[acc], v242, %[acc]\n"
-      "v_add_f32 %[acc], v243, %[acc]\n"
-      "v_add_f32 %[acc], v244, %[acc]\n"
-      "v_add_f32 %[acc], v245, %[acc]\n"
-      "v_add_f32 %[acc], v246, %[acc]\n"
-      "v_add_f32 %[acc], v247, %[acc]\n"
-      "v_add_f32 %[acc], v248, %[acc]\n"
-      "v_add_f32 %[acc], v249, %[acc]\n"
-      "v_add_f32 %[acc], v250, %[acc]\n"
-      "v_add_f32 %[acc], v251, %[acc]\n"
-      "v_add_f32 %[acc], v252, %[acc]\n"
-      "v_add_f32 %[acc], v253, %[acc]\n"
-      "v_add_f32 %[acc], v254, %[acc]\n"
-      "v_add_f32 %[acc], v255, %[acc]\n"
+      HF_RD_A(0, 16, 32, 48) HF_RD_B(64, 80, 96, 112)
+      HF_W4 HF_ADD16_A HF_RD_A(128, 144, 160, 176) // group 0; read group 2
+      HF_W4 HF_ADD16_B HF_RD_B(192, 208, 224, 240) // group 1; read group 3
+      HF_W4 HF_ADD16_A HF_RD_A(256, 272, 288, 304) // group 2; read group 4
+      HF_W4 HF_ADD16_B HF_RD_B(320, 336, 352, 368) // group 3; read group 5
+      HF_W4 HF_ADD16_A HF_RD_A(384, 400, 416, 432) // group 4; read group 6
+      HF_W4 HF_ADD16_B HF_RD_B(448, 464, 480, 496) // group 5; read group 7
+      HF_W4 HF_ADD16_A HF_RD_A(512, 528, 544, 560) // group 6; read group 8
+      HF_W4 HF_ADD16_B HF_RD_B(576, 592, 608, 624) // group 7; read group 9
+      HF_W4 HF_ADD16_A HF_RD_A(640, 656, 672, 688) // group 8; read group 10
+      HF_W4 HF_ADD16_B HF_RD_B(704, 720, 736, 752) // group 9; read group 11
+      HF_W4 HF_ADD16_A HF_RD_A(768, 784, 800, 816) // group 10; read group 12
+      HF_W4 HF_ADD16_B HF_RD_B(832, 848, 864, 880) // group 11; read group 13
+      HF_W4 HF_ADD16_A HF_RD_A(896, 912, 928, 944) // group 12; read group 14
+      HF_W4 HF_ADD16_B HF_RD_B(960, 976, 992, 1008) // group 13; read group 15
+      HF_W4 HF_ADD16_A HF_RD_A(1024, 1040, 1056, 1072) // group 14; read group 16
+      HF_W4 HF_ADD16_B HF_RD_B(1088, 1104, 1120, 1136) // group 15; read group 17
+      HF_W4 HF_ADD16_A HF_RD_A(1152, 1168, 1184, 1200) // group 16; read group 18
+      HF_W4 HF_ADD16_B HF_RD_B(1216, 1232, 1248, 1264) // group 17; read group 19
+      HF_W4 HF_ADD16_A HF_RD_A(1280, 1296, 1312, 1328) // group 18; read group 20
+      HF_W4 HF_ADD16_B HF_RD_B(1344, 1360, 1376, 1392) // group 19; read group 21
+      HF_W4 HF_ADD16_A HF_RD_A(1408, 1424, 1440, 1456) // group 20; read group 22
+      HF_W4 HF_ADD16_B HF_RD_B(1472, 1488, 1504, 1520) // group 21; read group 23
+      HF_W4 HF_ADD16_A HF_RD_A(1536, 1552, 1568, 1584) // group 22; read group 24
+      HF_W4 HF_ADD16_B HF_RD_B(1600, 1616, 1632, 1648) // group 23; read group 25
+      HF_W4 HF_ADD16_A HF_RD_A(1664, 1680, 1696, 1712) // group 24; read group 26
+      HF_W4 HF_ADD16_B HF_RD_B(1728, 1744, 1760, 1776) // group 25; read group 27
+      HF_W4 HF_ADD16_A HF_RD_A(1792, 1808, 1824, 1840) // group 26; read group 28
+      HF_W4 HF_ADD16_B HF_RD_B(1856, 1872, 1888, 1904) // group 27; read group 29
+      HF_W4 HF_ADD16_A HF_RD_A(1920, 1936, 1952, 1968) // group 28; read group 30
+      HF_W4 HF_ADD16_B HF_RD_B(1984, 2000, 2016, 2032) // group 29; read group 31
+      HF_W4 HF_ADD16_A                                            // group 30
+      "s_waitcnt lgkmcnt(0)\n" HF_ADD16_B                          // group 31
       : [acc] "+v"(acc)
       : [p] "v"(p)
       : "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", "v254", "v255", "memory");
+#undef HF_ADD
+#undef HF_ADD16_A
+#undef HF_ADD16_B
+#undef HF_RD
+#undef HF_RD_A
+#undef HF_RD_B
+#undef HF_W4
     return acc;
   } else {
 #pragma unroll 16
