@@ -1,0 +1,1010 @@
+"""Every HFusion group the tests compile: the product groups of
+`hfusion_mi355x.catalog` plus the parity cases -- reduced and ragged sizes of
+the headline workloads, one module per op family of the generic lowering
+(cast round modes, math functions, scans, gathers, histograms, ANY_PBR
+columns, transposes, fused programs), random generic chains, and groups with
+dynamic dims.  `__graft_entry__.build()` compiles them all ahead of time so
+the GPU tests load prebuilt code objects.
+"""
+from hfusion_mi355x import catalog as _product
+from hfusion_mi355x import groups as g
+from hfusion_mi355x.runtime import DynamicGroup
+
+_T = g._t
+_ATTRS = g._ATTRS
+
+
+def cast_modes(n=4096):
+    """One module, one group per (target type, round mode, saturate) pair."""
+    X = _T([n], "f32")
+    funcs = []
+    modes = ["rint", "round", "floor", "ceil", "trunc", "odd"]
+    for m in modes:
+        for tgt, sat in (("i8", True), ("i8", False), ("i32", False), ("bf16", False), ("f16", False)):
+            O = _T([n], tgt)
+            name = f"cast_{tgt}_{m}" + ("_sat" if sat else "")
+            satattr = ", enable_saturate = true" if sat else ""
+            funcs.append(f"""  func.func @{name}(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>{satattr}}} ins(%x : {X}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    # integer -> float round modes and same-type float rounding
+    I = _T([n], "i32")
+    for m in modes:
+        funcs.append(f"""  func.func @cast_i32_f32_{m}(%x: {I}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>}} ins(%x : {I}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+        funcs.append(f"""  func.func @cast_f32_f32_{m}(%x: {X}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>}} ins(%x : {X}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+def eltwise_mix(rows=64, cols=1000):
+    """ANY_PB group: row and column broadcasts, compare/select, unary math,
+    maximumf, an i1 output and a bf16 output."""
+    X, C, R = _T([rows, cols], "f32"), _T([cols], "f32"), _T([rows], "f32")
+    B, O, M = _T([rows, cols], "bf16"), _T([rows, cols], "f32"), _T([rows, cols], "i1")
+    return f"""module {{
+  func.func @eltwise_mix(%x: {X}, %b: {C}, %s: {R}, %y: {B}, %mask: {M}) -> ({B}, {M})
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %half = arith.constant 5.000000e-01 : f32
+    %e0 = tensor.empty() : {O}
+    %bb = linalg.broadcast ins(%b : {C}) outs(%e0 : {O}) dimensions = [0]
+    %e1 = tensor.empty() : {O}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e1 : {O}) dimensions = [1]
+    %gt = hfusion.compare {{compare_fn = #hfusion.compare_fn<vgt>}} ins(%x, %bb : {O}, {O}) outs(%mask : {M}) -> {M}
+    %e2 = tensor.empty() : {O}
+    %ex = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%x : {O}) outs(%e2 : {O}) -> {O}
+    %e3 = tensor.empty() : {O}
+    %t = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%ex, %bs : {O}, {O}) outs(%e3 : {O}) -> {O}
+    %e4 = tensor.empty() : {O}
+    %ng = linalg.elemwise_unary {{fun = #linalg.unary_fn<negf>}} ins(%x : {O}) outs(%e4 : {O}) -> {O}
+    %e5 = tensor.empty() : {O}
+    %sel = hfusion.select ins(%gt, %t, %ng : {M}, {O}, {O}) outs(%e5 : {O}) -> {O}
+    %e6 = tensor.empty() : {O}
+    %mx = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<maxf>}} ins(%sel, %half : {O}, f32) outs(%e6 : {O}) -> {O}
+    %e7 = tensor.empty() : {O}
+    %sq = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%mx : {O}) outs(%e7 : {O}) -> {O}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%sq : {O}) outs(%y : {B}) -> {B}
+    return %r, %gt : {B}, {M}
+  }}
+}}
+"""
+
+
+def layernorm(rows=64, cols=2048, eps=1e-5):
+    """LAST_AXIS_PBR group with two dependent sum reductions (mean, variance),
+    a column broadcast of weight and bias and an f32 row output (the mean)."""
+    X, W, R = _T([rows, cols], "f32"), _T([cols], "f32"), _T([rows], "f32")
+    return f"""module {{
+  func.func @layernorm(%x: {X}, %w: {W}, %bias: {W}, %y: {X}, %mu: {R}) -> ({X}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %zero = arith.constant 0.000000e+00 : f32
+    %n = arith.constant {float(cols):.6e} : f32
+    %eps = arith.constant {eps:.9e} : f32
+    %e0 = tensor.empty() : {R}
+    %f0 = linalg.fill ins(%zero : f32) outs(%e0 : {R}) -> {R}
+    %s = linalg.reduce {{arith.addf}} ins(%x : {X}) outs(%f0 : {R}) dimensions = [1]
+    %m = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%s, %n : {R}, f32) outs(%mu : {R}) -> {R}
+    %e1 = tensor.empty() : {X}
+    %bm = linalg.broadcast ins(%m : {R}) outs(%e1 : {X}) dimensions = [1]
+    %e2 = tensor.empty() : {X}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%x, %bm : {X}, {X}) outs(%e2 : {X}) -> {X}
+    %e3 = tensor.empty() : {X}
+    %d2 = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%d, %d : {X}, {X}) outs(%e3 : {X}) -> {X}
+    %e4 = tensor.empty() : {R}
+    %f4 = linalg.fill ins(%zero : f32) outs(%e4 : {R}) -> {R}
+    %v = linalg.reduce {{arith.addf}} ins(%d2 : {X}) outs(%f4 : {R}) dimensions = [1]
+    %e5 = tensor.empty() : {R}
+    %vm = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%v, %n : {R}, f32) outs(%e5 : {R}) -> {R}
+    %e6 = tensor.empty() : {R}
+    %ve = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%vm, %eps : {R}, f32) outs(%e6 : {R}) -> {R}
+    %e7 = tensor.empty() : {R}
+    %rs = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<rsqrt>}} ins(%ve : {R}) outs(%e7 : {R}) -> {R}
+    %e8 = tensor.empty() : {X}
+    %br = linalg.broadcast ins(%rs : {R}) outs(%e8 : {X}) dimensions = [1]
+    %e9 = tensor.empty() : {X}
+    %nx = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%d, %br : {X}, {X}) outs(%e9 : {X}) -> {X}
+    %e10 = tensor.empty() : {X}
+    %bw = linalg.broadcast ins(%w : {W}) outs(%e10 : {X}) dimensions = [0]
+    %e11 = tensor.empty() : {X}
+    %wx = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%nx, %bw : {X}, {X}) outs(%e11 : {X}) -> {X}
+    %e12 = tensor.empty() : {X}
+    %bb = linalg.broadcast ins(%bias : {W}) outs(%e12 : {X}) dimensions = [0]
+    %o = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%wx, %bb : {X}, {X}) outs(%y : {X}) -> {X}
+    return %o, %m : {X}, {R}
+  }}
+}}
+"""
+
+
+# elementwise functions of the HFusion region builder (HFusionOps.cpp:434-640)
+# that the headline groups do not use: (function, dialect) per unary/binary op
+MATH_UNARY = [("tan", "hfusion"), ("acos", "hfusion"), ("acosh", "hfusion"), ("asin", "hfusion"),
+              ("asinh", "hfusion"), ("atan", "hfusion"), ("atanh", "hfusion"), ("sinh", "hfusion"),
+              ("cosh", "hfusion"), ("lgamma", "hfusion"), ("ilogb", "hfusion"), ("tanh", "hfusion"),
+              ("sin", "hfusion"), ("cos", "hfusion"), ("erf", "hfusion"), ("log2", "hfusion"),
+              ("log10", "hfusion"), ("log1p", "hfusion"), ("exp2", "hfusion"), ("expm1", "hfusion"),
+              ("rsqrt", "hfusion"), ("log", "linalg")]
+MATH_BINARY = ["atan2", "ldexp", "divfhp", "powf", "copysign", "mod"]
+INT_BINARY = [("powi", "i32"), ("powi", "i16"), ("ceildivui", "i32"), ("modui", "i32"), ("ceildivui", "i8")]
+
+
+def math_fns(n=4096):
+    """One module, one PURE_ELEMWISE group per elementwise function (f32
+    unary and binary, integer binary on several widths) plus an operand
+    `bitcast` type_fn (i32 bits read as f32)."""
+    X = _T([n], "f32")
+    funcs = []
+    for fn, dia in MATH_UNARY:
+        attr = f"#{dia}.unary_fn<{fn}>"
+        funcs.append(f"""  func.func @u_{fn}(%x: {X}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = {dia}.elemwise_unary {{fun = {attr}}} ins(%x : {X}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    for fn in MATH_BINARY:
+        funcs.append(f"""  func.func @b_{fn}(%x: {X}, %y: {X}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<{fn}>}} ins(%x, %y : {X}, {X}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    for fn, t in INT_BINARY:
+        I = _T([n], t)
+        funcs.append(f"""  func.func @i_{fn}_{t}(%x: {I}, %y: {I}, %o: {I}) -> {I}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<{fn}>}} ins(%x, %y : {I}, {I}) outs(%o : {I}) -> {I}
+    return %r : {I}
+  }}""")
+    I = _T([n], "i32")
+    funcs.append(f"""  func.func @bitcast_add(%x: {I}, %y: {I}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>, cast = #linalg.type_fn<bitcast>}} ins(%x, %y : {I}, {I}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+FP_OPS = [("isinf", "f32"), ("isnan", "f32"), ("isfinite", "f32"), ("isinf", "bf16"), ("isnan", "f16"),
+          ("nextafter", "f32"), ("nextafter", "f16"), ("hypot", "f32"), ("hypot3", "f32"), ("hypot", "f16"),
+          ("erfinv", "f32"), ("erfinv", "f16"), ("bitcast", "f32"), ("signbit", "f32"), ("signbit", "f16"),
+          ("signbit8", "f32"), ("cylbesseli0", "f32"), ("cylbesseli0", "f16")]
+
+
+def fp_ops(n=4096):
+    """One module, one group per HFusion float op without outs (predicates,
+    nextafter, hypot with 2 and 3 operands, erfinv, signbit, cyl_bessel_i0) and hfusion.bitcast."""
+    funcs = []
+    for op, t in FP_OPS:
+        X, B = _T([n], t), _T([n], "i1")
+        name = f"{op}_{t}"
+        attrs = _ATTRS.format(kind='PURE_ELEMWISE')
+        if op in ("isinf", "isnan", "isfinite"):
+            body = f"%r = hfusion.{op} %x : {X} -> {B}\n    return %r : {B}"
+            sig = f"(%x: {X}) -> {B}"
+        elif op == "nextafter":
+            body = f"%r = hfusion.nextafter %x, %y : {X}, {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}, %y: {X}) -> {X}"
+        elif op == "hypot":
+            body = f"%r = hfusion.hypot %x, %y : {X}, {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}, %y: {X}) -> {X}"
+        elif op == "hypot3":
+            body = f"%r = hfusion.hypot %x, %y, %z : {X}, {X}, {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}, %y: {X}, %z: {X}) -> {X}"
+        elif op in ("signbit", "signbit8"):
+            # generic op form, as the reference's own tests write it
+            R = B if op == "signbit" else _T([n], "i8")
+            body = f'%r = "hfusion.signbit"(%x) : ({X}) -> {R}\n    return %r : {R}'
+            sig = f"(%x: {X}) -> {R}"
+        elif op == "cylbesseli0":
+            body = f"%r = hfusion.cyl_bessel_i0 %x : {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}) -> {X}"
+        elif op == "erfinv":
+            body = f"%r = hfusion.erfinv %x : {X} -> {X}\n    return %r : {X}"
+            sig = f"(%x: {X}) -> {X}"
+        else:
+            I = _T([n], "i32")
+            body = f"%r = hfusion.bitcast ins(%x : {I}) outs(%o : {X}) -> {X}\n    return %r : {X}"
+            sig = f"(%x: {I}, %o: {X}) -> {X}"
+        funcs.append(f"""  func.func @{name}{sig}
+      {attrs} {{
+    {body}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+# (name, op, elem in, elem out, shape, dim, reverse, extra attr)
+SCAN_OPS = [("cumsum_f32_d1", "cumsum", "f32", "f32", [64, 1000], 1, False, ""),
+            ("cumsum_f32_d0_rev", "cumsum", "f32", "f32", [64, 1000], 0, True, ""),
+            ("cumprod_f32", "cumprod", "f32", "f32", [32, 64], 1, False, ""),
+            ("cumprod_bf16_rev", "cumprod", "bf16", "bf16", [16, 256], 1, True, ""),
+            ("cummax_f32", "cummax", "f32", "f32", [64, 512], 1, False, ""),
+            ("cummin_f32_num", "cummin", "f32", "f32", [64, 512], 0, False, "{propagate_nan = false} "),
+            ("cumsum_i32_i64", "cumsum", "i32", "i64", [4096], 0, False, ""),
+            ("cumprod_i16", "cumprod", "i16", "i16", [8, 300], 1, False, ""),
+            ("cummax_i8_rev", "cummax", "i8", "i8", [64, 100], 1, True, "")]
+
+
+def scan_ops():
+    """One module, one group per cumulative op (cumsum/cumprod/cummax/cummin)
+    over several types, dims and directions."""
+    funcs = []
+    for name, op, ie, oe, shape, dim, rev, extra in SCAN_OPS:
+        X, O = _T(shape, ie), _T(shape, oe)
+        funcs.append(f"""  func.func @{name}(%x: {X}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %r = hfusion.{op} %x {extra}: {X} cum_dims = [{dim}] reverse = {str(rev).lower()} -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+# (name, input elem, input shape, bins, count elem, mask elem or None)
+HIST_OPS = [("hist_i32", "i32", [100000], 64, "i32", None),
+            ("hist_mask_i64", "i32", [300, 700], 10000, "i64", "i1"),
+            ("hist_i8_wrap", "i8", [5000], 16, "i8", None)]
+INTERLEAVE_OPS = [("deint_f32_c0", "f32", 0), ("deint_f32_c1", "f32", 1), ("deint_bf16_all", "bf16", -1),
+                  ("inter_f32", "f32", None), ("inter_i8", "i8", None)]
+
+
+def misc_ops():
+    """histogram (LDS and global bin paths, optional mask, wrapping counts)
+    and (de)interleave along the last dim."""
+    funcs = []
+    for name, ie, shape, bins, ce, me in HIST_OPS:
+        X, O = _T(shape, ie), _T([bins], ce)
+        if me:
+            M = _T(shape, me)
+            funcs.append(f"""  func.func @{name}(%x: {X}, %m: {M}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %r = hfusion.histogram %x, {bins}, %m : {X}, {M} -> {O}
+    return %r : {O}
+  }}""")
+        else:
+            funcs.append(f"""  func.func @{name}(%x: {X}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %r = hfusion.histogram %x, {bins} : {X} -> {O}
+    return %r : {O}
+  }}""")
+    for name, e, ch in INTERLEAVE_OPS:
+        if ch is None:
+            X, O = _T([64, 500], e), _T([64, 1000], e)
+            funcs.append(f"""  func.func @{name}(%a: {X}, %b: {X}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.interleave %a, %b : {X}, {X} -> {O}
+    return %r : {O}
+  }}""")
+        elif ch == -1:
+            X, O = _T([64, 1000], e), _T([64, 500], e)
+            funcs.append(f"""  func.func @{name}(%x: {X}) -> ({O}, {O})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r:2 = hfusion.deinterleave %x channel<all> : {X} -> {O}, {O}
+    return %r#0, %r#1 : {O}, {O}
+  }}""")
+        else:
+            X, O = _T([64, 1000], e), _T([64, 500], e)
+            funcs.append(f"""  func.func @{name}(%x: {X}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.deinterleave %x channel<{ch}> : {X} -> {O}
+    return %r : {O}
+  }}""")
+    # flip, mulext / mulextui, arange
+    for e in ("f32", "bf16"):
+        X = _T([64, 1000], e)
+        funcs.append(f"""  func.func @flip_{e}(%x: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.flip %x : {X} flip_axis = 1 -> {X}
+    return %r : {X}
+  }}""")
+    for op in ("mulext", "mulextui"):
+        for e in ("i8", "i32", "i64"):
+            X = _T([4096], e)
+            funcs.append(f"""  func.func @{op}_{e}(%a: {X}, %b: {X}) -> ({X}, {X})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %lo, %hi = hfusion.{op} %a, %b : {X}
+    return %lo, %hi : {X}, {X}
+  }}""")
+    for e in ("i32", "f32"):
+        O = _T([48, 130], e)
+        funcs.append(f"""  func.func @arange_{e}(%o: {O}, %off: index) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %s0 = arith.constant 1000 : index
+    %s1 = arith.constant -3 : index
+    %r = hfusion.arange offset[%off] strides[%s0, %s1] outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+# (name, src elem, src shape, index elem, index shape, axis)
+GATHER_OPS = [("gather_f16_ax1", "f16", [5, 6], "i32", [5, 3], 1),
+              ("gather_f32_ax1", "f32", [64, 1000], "i32", [64, 100], 1),
+              ("gather_bf16_ax0", "bf16", [100, 32], "i64", [50, 32], 0)]
+
+
+def gather_ops():
+    """hfusion.gather along axis 1 and 0, i32 and i64 indices, the init
+    (fallback for out-of-range indices) passed as the outs argument."""
+    funcs = []
+    for name, se, ss, ie, ish, ax in GATHER_OPS:
+        S, I, O = _T(ss, se), _T(ish, ie), _T(ish, se)
+        funcs.append(f"""  func.func @{name}(%src: {S}, %idx: {I}, %init: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.gather {{operandSegmentSizes = array<i32: 2, 1>}} ins(%src, %idx : {S}, {I}) outs(%init : {O}) axis = {ax} -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+MISC_EXTRA = (["flip_f32", "flip_bf16"] + [f"{op}_{e}" for op in ("mulext", "mulextui") for e in ("i8", "i32", "i64")]
+              + ["arange_i32", "arange_f32"])
+
+
+def memref_chain(n=4096):
+    """Destination-style ops on memrefs with no SSA results: the second op
+    reads the buffer the first one wrote; both written buffers are results."""
+    M = f"memref<{n}xf32>"
+    return f"""module {{
+  func.func @memref_chain(%x: {M}, %tmp: {M}, %y: {M})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%x : {M}) outs(%tmp : {M})
+    linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%tmp, %x : {M}, {M}) outs(%y : {M})
+    return
+  }}
+}}
+"""
+
+
+def reshape_chain():
+    """Elementwise ops joined by expand_shape / collapse_shape views: the
+    group runs over the shared flat index."""
+    A, B3 = _T([128, 256], "f32"), _T([32, 4, 256], "f32")
+    return f"""module {{
+  func.func @reshape_chain(%a: {A}, %b: {A}, %c: {B3}) -> {A}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e0 = tensor.empty() : {A}
+    %s = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%a, %b : {A}, {A}) outs(%e0 : {A}) -> {A}
+    %x = tensor.expand_shape %s [[0, 1], [2]] output_shape [32, 4, 256] : {A} into {B3}
+    %e1 = tensor.empty() : {B3}
+    %m = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%x, %c : {B3}, {B3}) outs(%e1 : {B3}) -> {B3}
+    %y = tensor.collapse_shape %m [[0, 1], [2]] : {B3} into {A}
+    %e2 = tensor.empty() : {A}
+    %r = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%y : {A}) outs(%e2 : {A}) -> {A}
+    return %r : {A}
+  }}
+}}
+"""
+
+
+def generic_ops():
+    """linalg.generic with a region of scalar arith / math ops: a row bias
+    (map (d0, d1) -> (d1)), a column scale ((d0, d1) -> (d0)), a captured
+    scalar constant and scalar argument, compare/select, f16 <-> f32 casts
+    and integer ops."""
+    X, B, XT = _T([64, 1000], "f32"), _T([1000], "f32"), _T([64], "f32")
+    H, I = _T([64, 1000], "f16"), _T([64, 1000], "i32")
+    M = _T([64, 1000], "i1")
+    return f"""#id = affine_map<(d0, d1) -> (d0, d1)>
+#row = affine_map<(d0, d1) -> (d1)>
+#col = affine_map<(d0, d1) -> (d0)>
+module {{
+  func.func @generic_bias_act(%x: {X}, %b: {B}, %xt: {XT}, %s: f32, %o: {X}) -> {X}
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %c05 = arith.constant 5.000000e-01 : f32
+    %r = linalg.generic {{indexing_maps = [#id, #row, #col, #id], iterator_types = ["parallel", "parallel"]}}
+        ins(%x, %b, %xt : {X}, {B}, {XT}) outs(%o : {X}) {{
+    ^bb0(%in: f32, %bias: f32, %t: f32, %out: f32):
+      %0 = arith.addf %in, %bias : f32
+      %1 = arith.mulf %0, %c05 : f32
+      %2 = math.tanh %1 : f32
+      %3 = arith.cmpf ogt, %0, %t : f32
+      %4 = arith.mulf %t, %s : f32
+      %5 = arith.select %3, %2, %4 : f32
+      %c1 = arith.constant 1.000000e+00 : f32
+      %6 = arith.maximumf %5, %c1 : f32
+      %7 = math.exp %0 : f32
+      %8 = arith.divf %7, %6 : f32
+      linalg.yield %8 : f32
+    }} -> {X}
+    return %r : {X}
+  }}
+  func.func @generic_f16_int(%h: {H}, %i: {I}, %o: {H}, %m: {M}) -> ({H}, {M})
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>], iterator_types = ["parallel", "parallel"]}}
+        ins(%h, %i : {H}, {I}) outs(%o : {H}) {{
+    ^bb0(%a: f16, %n: i32, %out: f16):
+      %0 = arith.extf %a : f16 to f32
+      %1 = arith.sitofp %n : i32 to f32
+      %2 = arith.mulf %0, %1 : f32
+      %3 = arith.truncf %2 : f32 to f16
+      %4 = arith.addf %3, %a : f16
+      linalg.yield %4 : f16
+    }} -> {H}
+    %q = linalg.generic {{indexing_maps = [#id, #id], iterator_types = ["parallel", "parallel"]}}
+        ins(%i : {I}) outs(%m : {M}) {{
+    ^bb0(%n: i32, %out: i1):
+      %c3 = arith.constant 3 : i32
+      %0 = arith.remsi %n, %c3 : i32
+      %1 = arith.shli %n, %c3 : i32
+      %2 = arith.xori %0, %1 : i32
+      %c0 = arith.constant 0 : i32
+      %3 = arith.cmpi slt, %2, %c0 : i32
+      linalg.yield %3 : i1
+    }} -> {M}
+    return %r, %q : {H}, {M}
+  }}
+}}
+"""
+
+
+def fuzz_generic(count=12, seed=20261201, shape=(32, 257)):
+    """Seeded random elementwise groups: linalg.generic regions over f32 / f16
+    / i32 operands (a row-broadcast operand among them) built only from
+    exactly rounded ops (add, sub, mul, div, max/min, abs, neg, sqrt,
+    compare + select, extf/truncf, sitofp), so every result is bit-exact
+    against the oracle."""
+    import random
+    rnd = random.Random(seed)
+    r, c = shape
+    funcs = []
+    fops = ["arith.addf", "arith.subf", "arith.mulf", "arith.divf", "arith.maximumf", "arith.minimumf"]
+    for n in range(count):
+        ft = rnd.choice(["f32", "f16"])
+        X, B, I, O = _T([r, c], ft), _T([c], ft), _T([r, c], "i32"), _T([r, c], ft)
+        body, vals, k = [], ["%a", "%b", "%bb"], 0
+
+        def new(stmt):
+            nonlocal k
+            nm = f"%v{k}"
+            k += 1
+            body.append(f"      {nm} = {stmt}")
+            return nm
+        vals.append(new(f"arith.sitofp %n : i32 to {ft}"))
+        for _ in range(rnd.randint(3, 7)):
+            kind = rnd.random()
+            x, y = rnd.choice(vals), rnd.choice(vals)
+            if kind < 0.55:
+                vals.append(new(f"{rnd.choice(fops)} {x}, {y} : {ft}"))
+            elif kind < 0.7:
+                vals.append(new(f"{rnd.choice(['math.absf', 'arith.negf', 'math.sqrt'])} {x} : {ft}"))
+            elif kind < 0.85:
+                cnd = new(f"arith.cmpf {rnd.choice(['olt', 'oge', 'une', 'ugt'])}, {x}, {y} : {ft}")
+                vals.append(new(f"arith.select {cnd}, {x}, {rnd.choice(vals)} : {ft}"))
+            elif ft == "f16":
+                e = new(f"arith.extf {x} : f16 to f32")
+                m = new(f"arith.mulf {e}, {e} : f32")
+                vals.append(new(f"arith.truncf {m} : f32 to f16"))
+            else:
+                vals.append(new(f"arith.addf {x}, {x} : {ft}"))
+        body.append(f"      linalg.yield {vals[-1]} : {ft}")
+        region = "\n".join(body)
+        funcs.append(f"""  func.func @fuzz{n}(%x: {X}, %bias: {B}, %i: {I}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %r = linalg.generic {{indexing_maps = [affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d1)>, affine_map<(d0, d1) -> (d0, d1)>, affine_map<(d0, d1) -> (d0, d1)>], iterator_types = ["parallel", "parallel"]}}
+        ins(%x, %bias, %i : {X}, {B}, {I}) outs(%o : {O}) {{
+    ^bb0(%a: {ft}, %bb: {ft}, %n: i32, %out: {ft}):
+      %b = arith.addf %a, %bb : {ft}
+{region}
+    }} -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+def fuzz_rows(count=8, seed=20261202):
+    """Seeded random LAST_AXIS_PBR groups from named ops: an elementwise chain
+    with a row-broadcast operand, a max or min row reduction, its broadcast
+    back into a second chain, results both the row values and the reduction.
+    Exactly rounded, order-free ops only, so results are bit-exact."""
+    import random
+    rnd = random.Random(seed)
+    funcs = []
+    for n in range(count):
+        r, c = rnd.choice([(64, 1000), (13, 4096), (256, 96), (7, 33000)])
+        X, B, R = _T([r, c], "f32"), _T([c], "f32"), _T([r], "f32")
+        lines, k = [], 0
+
+        def ew(op, ins):
+            nonlocal k
+            k += 1
+            e, v = f"%e{k}", f"%v{k}"
+            fam = "linalg" if op in ("add", "sub", "mul", "div", "max_signed", "min_signed", "abs", "negf") else "hfusion"
+            if op in ("abs", "negf", "sqrt"):
+                attr = f"#{'linalg' if fam == 'linalg' else 'hfusion'}.unary_fn<{op}>"
+                kind = f"{fam}.elemwise_unary"
+                tys = X
+            else:
+                attr = f"#linalg.binary_fn<{op}>" if fam == "linalg" else f"#hfusion.binary_fn<{op}>"
+                kind = f"{fam}.elemwise_binary"
+                tys = ", ".join([X] * len(ins))
+            lines.append(f"    {e} = tensor.empty() : {X}")
+            lines.append(f"    {v} = {kind} {{fun = {attr}}} ins({', '.join(ins)} : {tys}) outs({e} : {X}) -> {X}")
+            return v
+        lines.append(f"    %eb = tensor.empty() : {X}")
+        lines.append(f"    %bb = linalg.broadcast ins(%b : {B}) outs(%eb : {X}) dimensions = [0]")
+        vals = ["%x", "%bb"]
+        for _ in range(rnd.randint(2, 4)):
+            op = rnd.choice(["add", "sub", "mul", "max_signed", "min_signed", "abs", "negf"])
+            vals.append(ew(op, [rnd.choice(vals)] if op in ("abs", "negf") else [rnd.choice(vals), rnd.choice(vals)]))
+        red = rnd.choice(["maximumf", "minimumf"])
+        init = "0xFF800000" if red == "maximumf" else "0x7F800000"
+        lines.append(f"    %init = arith.constant {init} : f32")
+        lines.append(f"    %f = linalg.fill ins(%init : f32) outs(%m : {R}) -> {R}")
+        lines.append(f"    %red = linalg.reduce {{arith.{red}}} ins({vals[-1]} : {X}) outs(%f : {R}) dimensions = [1]")
+        lines.append(f"    %er = tensor.empty() : {X}")
+        lines.append(f"    %rb = linalg.broadcast ins(%red : {R}) outs(%er : {X}) dimensions = [1]")
+        vals.append("%rb")
+        for _ in range(rnd.randint(1, 3)):
+            op = rnd.choice(["sub", "add", "mul", "max_signed", "abs"])
+            vals.append(ew(op, [rnd.choice(vals[-3:])] if op == "abs" else [rnd.choice(vals[-3:]), rnd.choice(vals)]))
+        body = "\n".join(lines)
+        funcs.append(f"""  func.func @frow{n}(%x: {X}, %b: {B}, %m: {R}) -> ({X}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+{body}
+    return {vals[-1]}, %red : {X}, {R}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+def generic_reduce():
+    """linalg.generic row reductions: max of x*w (exact) and sum of
+    x*w (a float sum: the row program's order differs from the serial loop)."""
+    X, W, R = _T([64, 1000], "f32"), _T([1000], "f32"), _T([64], "f32")
+    funcs = []
+    for name, comb, init in (("gred_max", "arith.maximumf", "0xFF800000"), ("gred_sum", "arith.addf", "0.000000e+00")):
+        funcs.append(f"""  func.func @{name}(%x: {X}, %w: {W}, %o: {R}) -> {R}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %init = arith.constant {init} : f32
+    %f = linalg.fill ins(%init : f32) outs(%o : {R}) -> {R}
+    %r = linalg.generic {{indexing_maps = [#in, #row, #out], iterator_types = ["parallel", "reduction"]}}
+        ins(%x, %w : {X}, {W}) outs(%f : {R}) {{
+    ^bb0(%a: f32, %b: f32, %acc: f32):
+      %p = arith.mulf %a, %b : f32
+      %m = {comb} %p, %acc : f32
+      linalg.yield %m : f32
+    }} -> {R}
+    return %r : {R}
+  }}""")
+    return ("#in = affine_map<(d0, d1) -> (d0, d1)>\n#row = affine_map<(d0, d1) -> (d1)>\n"
+            "#out = affine_map<(d0, d1) -> (d0)>\nmodule {\n" + "\n".join(funcs) + "\n}\n")
+
+
+def reduce_ops(rows=48, cols=3000):
+    """Row reductions with each f32 combiner and an i32 sum (exact)."""
+    X, R, XI, RI = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i32"), _T([rows], "i32")
+    return f"""module {{
+  func.func @reduce_ops(%x: {X}, %xi: {XI}, %mx: {R}, %mn: {R}, %mxn: {R}, %si: {RI}) -> ({R}, {R}, {R}, {RI})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %pinf = arith.constant 0x7F800000 : f32
+    %c0 = arith.constant 0 : i32
+    %f0 = linalg.fill ins(%ninf : f32) outs(%mx : {R}) -> {R}
+    %a = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f0 : {R}) dimensions = [1]
+    %f1 = linalg.fill ins(%pinf : f32) outs(%mn : {R}) -> {R}
+    %b = linalg.reduce {{arith.minimumf}} ins(%x : {X}) outs(%f1 : {R}) dimensions = [1]
+    %f2 = linalg.fill ins(%ninf : f32) outs(%mxn : {R}) -> {R}
+    %c = linalg.reduce {{arith.maxnumf}} ins(%x : {X}) outs(%f2 : {R}) dimensions = [1]
+    %f3 = linalg.fill ins(%c0 : i32) outs(%si : {RI}) -> {RI}
+    %d = linalg.reduce {{arith.addi}} ins(%xi : {XI}) outs(%f3 : {RI}) dimensions = [1]
+    return %a, %b, %c, %d : {R}, {R}, {R}, {RI}
+  }}
+}}
+"""
+
+
+def quant_ties(rows=64, cols=1024):
+    """nearbyint(x / s[row]) with f32 output: the dynamic-quantisation
+    rounding, checked on quotients placed on and next to half-integers."""
+    X, R = _T([rows, cols], "f32"), _T([rows], "f32")
+    return f"""module {{
+  func.func @quant_ties(%x: {X}, %s: {R}, %o: {X}, %mx: {R}) -> ({X}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %f = linalg.fill ins(%ninf : f32) outs(%mx : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f : {R}) dimensions = [1]
+    %e0 = tensor.empty() : {X}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e0 : {X}) dimensions = [1]
+    %e1 = tensor.empty() : {X}
+    %q = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%x, %bs : {X}, {X}) outs(%e1 : {X}) -> {X}
+    %r = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<nearbyint>}} ins(%q : {X}) outs(%o : {X}) -> {X}
+    return %r, %m : {X}, {R}
+  }}
+}}
+"""
+
+
+FP8_TYPES = {"e4m3": "f8E4M3FN", "e5m2": "f8E5M2"}
+
+
+def quant_i8_ties(rows=64, cols=1024, lo=-127, hi=127, name="quant_i8_ties"):
+    """(int8)clamp(nearbyint(x / s[row]), lo, hi): the int8 dynamic-quant tail
+    on its own (with a row max beside it, so the group is a row program),
+    for quotients on and next to half-integers and beyond the clamp bounds."""
+    X, R, Q = _T([rows, cols], "f32"), _T([rows], "f32"), _T([rows, cols], "i8")
+    return f"""module {{
+  func.func @{name}(%x: {X}, %s: {R}, %q: {Q}, %mx: {R}) -> ({Q}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %f = linalg.fill ins(%ninf : f32) outs(%mx : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f : {R}) dimensions = [1]
+    %hi = arith.constant {float(hi):.6e} : f32
+    %lo = arith.constant {float(lo):.6e} : f32
+    %e0 = tensor.empty() : {X}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e0 : {X}) dimensions = [1]
+    %e1 = tensor.empty() : {X}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%x, %bs : {X}, {X}) outs(%e1 : {X}) -> {X}
+    %e2 = tensor.empty() : {X}
+    %r = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<nearbyint>}} ins(%d : {X}) outs(%e2 : {X}) -> {X}
+    %e3 = tensor.empty() : {X}
+    %c1 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<minf>}} ins(%r, %hi : {X}, f32) outs(%e3 : {X}) -> {X}
+    %e4 = tensor.empty() : {X}
+    %c2 = hfusion.elemwise_binary {{fun = #hfusion.binary_fn<maxf>}} ins(%c1, %lo : {X}, f32) outs(%e4 : {X}) -> {X}
+    %o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%c2 : {X}) outs(%q : {Q}) -> {Q}
+    return %o, %m : {Q}, {R}
+  }}
+}}
+"""
+
+
+def cast_fp8(n=4096):
+    """fp8 casts: f32 -> f8E4M3FN / f8E5M2 under every round mode, with and
+    without saturation; fp8 -> f32; f16 <-> f8E5M2 through f32 (the form of
+    hfusion-normalize-casting-ops.mlir:321-339); and f32 -> i16 / i8 casts whose
+    result carries annotation.mark {overflow_mode = "saturate"}
+    (hfusion-normalize-casting-ops.mlir:53-74)."""
+    X, H = _T([n], "f32"), _T([n], "f16")
+    funcs = []
+    for short, ty in FP8_TYPES.items():
+        O = _T([n], ty)
+        for m in ["rint", "round", "floor", "ceil", "trunc", "odd"]:
+            for sat in (False, True):
+                satattr = ", enable_saturate = true" if sat else ""
+                funcs.append(f"""  func.func @cast_{short}_{m}{"_sat" if sat else ""}(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<{m}>{satattr}}} ins(%x : {X}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+        funcs.append(f"""  func.func @dec_{short}(%x: {O}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {O}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    E = _T([n], "f8E5M2")
+    funcs.append(f"""  func.func @f16_to_e5m2(%x: {H}, %o: {E}) -> {E}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {X}
+    %t = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {H}) outs(%e : {X}) -> {X}
+    %r = hfusion.cast {{enable_overflow = true, enable_saturate = false, round_mode = #hfusion.round_mode<rint>}} ins(%t : {X}) outs(%o : {E}) -> {E}
+    return %r : {E}
+  }}""")
+    funcs.append(f"""  func.func @e5m2_to_f16(%x: {E}, %o: {H}) -> {H}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {X}
+    %t = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {E}) outs(%e : {X}) -> {X}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%t : {X}) outs(%o : {H}) -> {H}
+    return %r : {H}
+  }}""")
+    for it in ("i16", "i8"):
+        O = _T([n], it)
+        funcs.append(f"""  func.func @ovf_{it}_trunc(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %r = hfusion.cast {{enable_overflow = true, round_mode = #hfusion.round_mode<trunc>}} ins(%x : {X}) outs(%o : {O}) -> {O}
+    annotation.mark %r {{overflow_mode = "saturate"}} : {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
+
+def fp8_quant(rows=64, cols=4096):
+    """Dynamic per-token fp8 quantisation (the fp8 counterpart of the int8
+    group): scale = max|x| / 448, q = f8E4M3FN(x / scale) with round to
+    nearest even and saturation."""
+    X, R = _T([rows, cols], "bf16"), _T([rows], "f32")
+    XF, Q = _T([rows, cols], "f32"), _T([rows, cols], "f8E4M3FN")
+    return f"""module {{
+  func.func @fp8_quant(%x: {X}, %q: {Q}, %scale: {R}) -> ({Q}, {R})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %zero = arith.constant 0.000000e+00 : f32
+    %fmax = arith.constant 4.480000e+02 : f32
+    %e0 = tensor.empty() : {XF}
+    %xf = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%x : {X}) outs(%e0 : {XF}) -> {XF}
+    %e1 = tensor.empty() : {XF}
+    %ax = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%xf : {XF}) outs(%e1 : {XF}) -> {XF}
+    %e2 = tensor.empty() : {R}
+    %i0 = linalg.fill ins(%zero : f32) outs(%e2 : {R}) -> {R}
+    %amax = linalg.reduce {{arith.maximumf}} ins(%ax : {XF}) outs(%i0 : {R}) dimensions = [1]
+    %e3 = tensor.empty() : {R}
+    %sc = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%amax, %fmax : {R}, f32) outs(%scale : {R}) -> {R}
+    %e4 = tensor.empty() : {XF}
+    %bs = linalg.broadcast ins(%sc : {R}) outs(%e4 : {XF}) dimensions = [1]
+    %e5 = tensor.empty() : {XF}
+    %y = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%xf, %bs : {XF}, {XF}) outs(%e5 : {XF}) -> {XF}
+    %qq = hfusion.cast {{round_mode = #hfusion.round_mode<rint>, enable_saturate = true}} ins(%y : {XF}) outs(%q : {Q}) -> {Q}
+    return %qq, %sc : {Q}, {R}
+  }}
+}}
+"""
+
+
+
+# ------------------------------------------------------------ ANY_PBR / rank-N
+def any_pbr_ops():
+    """Reductions over a non-last axis (ANY_PBR: FusibleHelper.cpp:63-64),
+    reduce_with_index along a middle / first axis, and rank-3 last-axis
+    groups, one function each."""
+    f = []
+    # sum of squares over the middle axis of [8, 64, 100], scaled
+    X, O = _T([8, 64, 100], "f32"), _T([8, 100], "f32")
+    f.append(f"""  func.func @sumsq_mid(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %h = arith.constant 5.000000e-01 : f32
+    %e0 = tensor.empty() : {X}
+    %sq = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%x, %x : {X}, {X}) outs(%e0 : {X}) -> {X}
+    %e1 = tensor.empty() : {O}
+    %i = linalg.fill ins(%z : f32) outs(%e1 : {O}) -> {O}
+    %s = linalg.reduce {{arith.addf}} ins(%sq : {X}) outs(%i : {O}) dimensions = [1]
+    %r = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%s, %h : {O}, f32) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    # softmax along the first axis of [512, 1000] -> bf16
+    X, R, B = _T([512, 1000], "f32"), _T([1000], "f32"), _T([512, 1000], "bf16")
+    f.append(f"""  func.func @softmax_d0(%x: {X}, %o: {B}) -> {B}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %z = arith.constant 0.000000e+00 : f32
+    %e0 = tensor.empty() : {R}
+    %f0 = linalg.fill ins(%ninf : f32) outs(%e0 : {R}) -> {R}
+    %m = linalg.reduce {{arith.maximumf}} ins(%x : {X}) outs(%f0 : {R}) dimensions = [0]
+    %e1 = tensor.empty() : {X}
+    %bm = linalg.broadcast ins(%m : {R}) outs(%e1 : {X}) dimensions = [0]
+    %e2 = tensor.empty() : {X}
+    %d = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%x, %bm : {X}, {X}) outs(%e2 : {X}) -> {X}
+    %e3 = tensor.empty() : {X}
+    %ex = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%d : {X}) outs(%e3 : {X}) -> {X}
+    %e4 = tensor.empty() : {R}
+    %f1 = linalg.fill ins(%z : f32) outs(%e4 : {R}) -> {R}
+    %s = linalg.reduce {{arith.addf}} ins(%ex : {X}) outs(%f1 : {R}) dimensions = [0]
+    %e5 = tensor.empty() : {X}
+    %bs = linalg.broadcast ins(%s : {R}) outs(%e5 : {X}) dimensions = [0]
+    %e6 = tensor.empty() : {X}
+    %q = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%ex, %bs : {X}, {X}) outs(%e6 : {X}) -> {X}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%q : {X}) outs(%o : {B}) -> {B}
+    return %r : {B}
+  }}""")
+    # argmax along the middle axis of [16, 300, 40]
+    X, V, I = _T([16, 300, 40], "f32"), _T([16, 40], "f32"), _T([16, 40], "i32")
+    f.append(f"""  func.func @argmax_mid(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %c0 = arith.constant 0 : i32
+    %ninf = arith.constant 0xFF800000 : f32
+    %v0 = linalg.fill ins(%ninf : f32) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : i32) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index {{tie_break_left = true}} <max> ins(%x : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}""")
+    # argmin along the first axis of an i32 [1000, 64], i64 indices
+    X, V, I = _T([1000, 64], "i32"), _T([64], "i32"), _T([64], "i64")
+    f.append(f"""  func.func @argmin_d0_i32(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %c0 = arith.constant 0 : i64
+    %big = arith.constant 2147483647 : i32
+    %v0 = linalg.fill ins(%big : i32) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : i64) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index <min> ins(%x : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [0] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}""")
+    # argmax over the last axis of exp(x) (fused producer: not the split-row kernel)
+    X, V, I = _T([64, 777], "f32"), _T([64], "f32"), _T([64], "i32")
+    f.append(f"""  func.func @argmax_fused(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %c0 = arith.constant 0 : i32
+    %ninf = arith.constant 0xFF800000 : f32
+    %e = tensor.empty() : {X}
+    %n = linalg.elemwise_unary {{fun = #linalg.unary_fn<negf>}} ins(%x : {X}) outs(%e : {X}) -> {X}
+    %v0 = linalg.fill ins(%ninf : f32) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : i32) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index <max> ins(%n : {X}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}""")
+    # rank-3 last-axis sum of [8, 64, 100]
+    X, O = _T([8, 64, 100], "f32"), _T([8, 64], "f32")
+    f.append(f"""  func.func @sum_rank3_last(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %i = linalg.fill ins(%z : f32) outs(%o : {O}) -> {O}
+    %s = linalg.reduce {{arith.addf}} ins(%x : {X}) outs(%i : {O}) dimensions = [2]
+    return %s : {O}
+  }}""")
+    # rank-3 last-axis max with a [S, C] operand broadcast along the batch
+    # dim: no row layout fits, the column program takes it
+    X, Bv, O = _T([4, 16, 256], "f32"), _T([16, 256], "f32"), _T([4, 16], "f32")
+    f.append(f"""  func.func @max_bias_rank3(%x: {X}, %b: {Bv}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %e0 = tensor.empty() : {X}
+    %bb = linalg.broadcast ins(%b : {Bv}) outs(%e0 : {X}) dimensions = [0]
+    %e1 = tensor.empty() : {X}
+    %a = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%x, %bb : {X}, {X}) outs(%e1 : {X}) -> {X}
+    %i = linalg.fill ins(%ninf : f32) outs(%o : {O}) -> {O}
+    %m = linalg.reduce {{arith.maximumf}} ins(%a : {X}) outs(%i : {O}) dimensions = [2]
+    return %m : {O}
+  }}""")
+    # i32 sum over the first two axes of [6, 50, 33] (one collapsed reduced dim)
+    X, O = _T([6, 50, 33], "i32"), _T([33], "i32")
+    f.append(f"""  func.func @isum_d01(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %c0 = arith.constant 0 : i32
+    %i = linalg.fill ins(%c0 : i32) outs(%o : {O}) -> {O}
+    %s = linalg.reduce {{arith.addi}} ins(%x : {X}) outs(%i : {O}) dimensions = [0, 1]
+    return %s : {O}
+  }}""")
+    return "module {\n" + "\n".join(f) + "\n}\n"
+
+
+ANY_PBR_OPS = ["sumsq_mid", "softmax_d0", "argmax_mid", "argmin_d0_i32", "argmax_fused", "sum_rank3_last",
+               "max_bias_rank3", "isum_d01"]
+
+
+def transpose_ops():
+    """Groups with linalg.transpose: 2-D and 3-D permutations fused with
+    casts and binary ops, a transpose applied after an elementwise op, a
+    permutation that only moves unit dims (a reshape), ragged tile edges."""
+    f = []
+    X, XT, O = _T([300, 200], "bf16"), _T([200, 300], "bf16"), _T([200, 300], "f32")
+    f.append(f"""  func.func @tr2d_cast(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [1, 0]
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%t : {XT}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    X, XT, Y, O = _T([8, 96, 130], "f32"), _T([8, 130, 96], "f32"), _T([8, 130, 96], "f32"), _T([8, 130, 96], "bf16")
+    f.append(f"""  func.func @tr3d_add(%x: {X}, %y: {Y}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e0 = tensor.empty() : {X}
+    %s = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%x : {X}) outs(%e0 : {X}) -> {X}
+    %e1 = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%s : {X}) outs(%e1 : {XT}) permutation = [0, 2, 1]
+    %e2 = tensor.empty() : {Y}
+    %a = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%t, %y : {XT}, {Y}) outs(%e2 : {Y}) -> {Y}
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%a : {Y}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    X, XT, O = _T([16, 33, 64], "i8"), _T([64, 16, 33], "i8"), _T([64, 16, 33], "i32")
+    f.append(f"""  func.func @tr3d_rot_i8(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [2, 0, 1]
+    %r = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%t : {XT}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    X, XT, O = _T([4, 1, 100], "f32"), _T([4, 100, 1], "f32"), _T([4, 100, 1], "f32")
+    f.append(f"""  func.func @tr_unit(%x: {X}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='PURE_ELEMWISE')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [0, 2, 1]
+    %r = linalg.elemwise_unary {{fun = #linalg.unary_fn<abs>}} ins(%t : {XT}) outs(%o : {O}) -> {O}
+    return %r : {O}
+  }}""")
+    return "module {\n" + "\n".join(f) + "\n}\n"
+
+
+TRANSPOSE_OPS = ["tr2d_cast", "tr3d_add", "tr3d_rot_i8", "tr_unit"]
+
+def entries():
+    """name -> IR text of every group the tests run: the product groups plus
+    the parity cases below."""
+    e = dict(_product.entries())
+    # reduced / ragged parity sizes
+    e["vec_add_1m"] = g.vec_add(1 << 20)
+    e["vec_add_ragged"] = g.vec_add(1001)
+    e["vec_add_i16"] = g.vec_add(16, dtype="i16")
+    e["rmsnorm_quant_ragged"] = g.rmsnorm_quant(13, 1000)
+    e["safe_softmax_64"] = g.safe_softmax(64, 32768)
+    e["safe_softmax_ragged"] = g.safe_softmax(33, 1000)
+    e["argmax_16"] = g.argmax(16, 152064)
+    e["argmax_ragged"] = g.argmax(5, 1001)
+    e["argmax_i64"] = g.argmax(8, 4096, index_type="i64")
+    e["argmin_ragged"] = g.argmax(9, 5001, kind="min")
+    e["argmax_tall"] = g.argmax(2048, 33797)
+    e["w8a8_512"] = g.w8a8_dequant(512, 512, 512)
+    e["w8a8_ragged"] = g.w8a8_dequant(300, 200, 160)
+    e["w8a8_ragged_dma"] = g.w8a8_dequant(300, 200, 192)
+    e["w8a8_ragged_dma128"] = g.w8a8_dequant(300, 200, 384)
+    e["w8a8_kn"] = g.w8a8_dequant(320, 256, 128, b_layout="kn")
+    e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
+    e["bf16_mmad_ragged128"] = g.bf16_mmad(200, 136, 192)
+    e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)
+    # hivm.hir.matmul forms of bishengir/test/Dialect/HIVM/IR/ops.mlir (16x16 f16) and wider
+    e["hivm_mm_f16_null"] = g.hivm_matmul(16, 16, 16)
+    e["hivm_mm_f16_bias_pc"] = g.hivm_matmul(16, 16, 16, bias="f16", descale="f16", descale_mode="DescalePerChannel")
+    e["hivm_mm_f16_bias_pt_t"] = g.hivm_matmul(16, 16, 16, bias="f16", descale="f16", descale_mode="DescalePerTensor",
+                                               a_t=True, b_t=True)
+    e["hivm_mm_i8_pc"] = g.hivm_matmul(300, 200, 192, elem="i8", out="bf16", bias="i32", descale="f32",
+                                       descale_mode="DescalePerChannel", b_t=True)
+    e["hivm_mm_i8_pt_i8out"] = g.hivm_matmul(256, 320, 128, elem="i8", out="i8", descale="f32",
+                                             descale_mode="DescalePerTensor", b_t=True)
+    e["hivm_mm_bf16_at"] = g.hivm_matmul(160, 96, 64, elem="bf16", out="f32", bias="f32", a_t=True)
+    e["mm_i8_ragged"] = g.mm_i8(300, 200, 192)
+    e["bf16_mmad_256"] = g.bf16_mmad(256, 256, 256)
+    e["cast_modes"] = cast_modes(4096)
+    e["eltwise_mix"] = eltwise_mix(64, 1000)
+    e["layernorm"] = layernorm(64, 2048)
+    e["reduce_ops"] = reduce_ops(48, 3000)
+    e["math_fns"] = math_fns(4096)
+    e["fp_ops"] = fp_ops(4096)
+    e["scan_ops"] = scan_ops()
+    e["misc_ops"] = misc_ops()
+    e["gather_ops"] = gather_ops()
+    e["memref_chain"] = memref_chain(4096)
+    e["reshape_chain"] = reshape_chain()
+    e["generic_ops"] = generic_ops()
+    e["fuzz_generic"] = fuzz_generic()
+    e["fuzz_rows"] = fuzz_rows()
+    e["generic_reduce"] = generic_reduce()
+    e["any_pbr_ops"] = any_pbr_ops()
+    e["transpose_ops"] = transpose_ops()
+    # dynamic row counts (compiled per size: DynamicGroup / option dyn=...)
+    e["rmsnorm_quant_dyn"] = g.with_dynamic_rows(g.rmsnorm_quant(7919, 4096), 7919)
+    e["softmax_dyn"] = g.with_dynamic_rows(g.safe_softmax(7919, 1000), 7919)
+    e["vec_add_dyn"] = g.with_dynamic_rows(g.vec_add(7919), 7919)
+    e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
+    # the same groups through the opt-in one-wave-per-row kernel (hf_rmsq.h)
+    for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3", "rmsnorm_quant_ragged"):
+        e[n + "_rmsq"] = e[n]
+    e["rank0"] = """module {
+  func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
+      """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {
+    %e = tensor.empty() : tensor<f32>
+    %r = linalg.elemwise_binary {fun = #linalg.binary_fn<mul>} ins(%a, %b : tensor<f32>, tensor<f32>) outs(%e : tensor<f32>) -> tensor<f32>
+    %e2 = tensor.empty() : tensor<f32>
+    %s = hfusion.elemwise_unary {fun = #hfusion.unary_fn<sqrt>} ins(%r : tensor<f32>) outs(%e2 : tensor<f32>) -> tensor<f32>
+    return %s : tensor<f32>
+  }
+}
+"""
+    e["quant_ties"] = quant_ties(64, 1024)
+    e["quant_i8_ties"] = quant_i8_ties(64, 1024)
+    e["quant_i8_ties_m128"] = quant_i8_ties(64, 1024, lo=-128, name="quant_i8_ties_m128")
+    e["quant_i8_ties_narrow"] = quant_i8_ties(64, 1000, lo=-100, hi=100, name="quant_i8_ties_narrow")
+    e["cast_fp8"] = cast_fp8(4096)
+    e["fp8_quant"] = fp8_quant(64, 4096)
+    e["fp8_quant_ragged"] = fp8_quant(13, 1000)
+    # un-fused host functions: the fusion front-end splits them into launch
+    # programs of several groups
+    e["prog_gemm_rmsnorm_quant"] = g.gemm_rmsnorm_quant(256, 512, 256)
+    e["prog_gemm_rmsnorm_quant_ragged"] = g.gemm_rmsnorm_quant(100, 320, 192)
+    e["prog_scores_softmax"] = g.scores_softmax(128, 1024, 128)
+    e["prog_scores_softmax_ragged"] = g.scores_softmax(72, 1000, 64)
+    e["prog_exp_cumsum_scale"] = g.exp_cumsum_scale(64, 1000)
+    return e
+
+
+def get(name):
+    return entries()[name]
+
+
+# row counts the dynamic groups are prebuilt for (the GPU tests call them with these)
+DYN_ROWS = {"rmsnorm_quant_dyn": [1, 37, 300], "softmax_dyn": [5, 129], "vec_add_dyn": [1, 1000, 65537]}
+
+
+def dyn_options(name, rows):
+    """The specialisation option of a dynamic catalog group at `rows` rows
+    (every dynamic dim of these groups is the row count)."""
+    dg = DynamicGroup(get(name))
+    return dg.options_for([rows] * len(dg.dims))
+
+
+def options(name):
+    """Compiler options a prebuilt group is built with ("" for the defaults;
+    a dynamic group: its first prebuilt row count)."""
+    if name in DYN_ROWS:
+        return dyn_options(name, DYN_ROWS[name][0])
+    return "rmsq_kernel=1" if name.endswith("_rmsq") else ""

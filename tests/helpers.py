@@ -3,6 +3,7 @@ through the CPU oracle on the same inputs."""
 import numpy as np
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from oracle import interp
 
 
@@ -40,7 +41,7 @@ def to_host(t, elem):
 def run_gpu(name, inputs, device, func=None):
     """Runs prebuilt catalog group `name` on the GPU; `inputs` holds one numpy
     array per group argument (outputs' initial contents included)."""
-    art = hf.compile(hf.catalog.get(name), options=hf.catalog.options(name), require_cached=True)
+    art = hf.compile(cat.get(name), options=cat.options(name), require_cached=True)
     grp = art.load(func)
     params = grp.meta["params"]
     devs = []
@@ -54,7 +55,7 @@ def run_gpu(name, inputs, device, func=None):
 
 
 def run_oracle(name, inputs, func=None, cast_semantics="declared"):
-    return interp.run(hf.catalog.get(name), *inputs, func=func, cast_semantics=cast_semantics)
+    return interp.run(cat.get(name), *inputs, func=func, cast_semantics=cast_semantics)
 
 
 def bf16_ulp_diff(a, b):
@@ -223,7 +224,7 @@ def math_inputs(func, n=4096, seed=0x4D415448):
 
 def math_funcs():
     """Names of the functions of catalog module math_fns."""
-    c = hf.catalog
+    c = cat
     return ([f"u_{fn}" for fn, _ in c.MATH_UNARY] + [f"b_{fn}" for fn in c.MATH_BINARY]
             + [f"i_{fn}_{t}" for fn, t in c.INT_BINARY] + ["bitcast_add"])
 
@@ -285,12 +286,12 @@ def fp_inputs(func, n=4096, seed=0x46504F50):
 
 
 def fp_funcs():
-    return [f"{op}_{t}" for op, t in hf.catalog.FP_OPS]
+    return [f"{op}_{t}" for op, t in cat.FP_OPS]
 
 
 def scan_inputs(name, seed=0x5343414E):
     """Seeded input of group `name` of catalog module scan_ops."""
-    spec = {s[0]: s for s in hf.catalog.SCAN_OPS}[name]
+    spec = {s[0]: s for s in cat.SCAN_OPS}[name]
     _, op, ie, _, shape, _, _, _ = spec
     rng = np.random.default_rng(seed + sum(map(ord, name)))
     if ie in ("f32", "bf16"):
@@ -315,7 +316,7 @@ def scan_inputs(name, seed=0x5343414E):
 def misc_inputs(name, seed=0x4D495343):
     """Seeded inputs of group `name` of catalog module misc_ops."""
     rng = np.random.default_rng(seed + sum(map(ord, name)))
-    hist = {h[0]: h for h in hf.catalog.HIST_OPS}
+    hist = {h[0]: h for h in cat.HIST_OPS}
     if name in hist:
         _, ie, shape, bins, _, me = hist[name]
         dt = {"i8": np.int8, "i32": np.int32}[ie]
@@ -323,7 +324,7 @@ def misc_inputs(name, seed=0x4D495343):
         if me:
             return [x, rng.random(shape) < 0.7]
         return [x]
-    _, e, ch = {i[0]: i for i in hf.catalog.INTERLEAVE_OPS}[name]
+    _, e, ch = {i[0]: i for i in cat.INTERLEAVE_OPS}[name]
     def gen(shape):
         if e == "f32":
             return rng.normal(0, 1, shape).astype(np.float32)
@@ -356,7 +357,7 @@ def misc_extra_inputs(name, seed=0x45585452):
 def gather_inputs(name, seed=0x47415448):
     """Seeded (src, index, init) of group `name` of catalog module gather_ops;
     about one index in ten is out of range (negative or past the axis)."""
-    spec = {g[0]: g for g in hf.catalog.GATHER_OPS}[name]
+    spec = {g[0]: g for g in cat.GATHER_OPS}[name]
     _, se, ss, ie, ish, ax = spec
     rng = np.random.default_rng(seed + sum(map(ord, name)))
     src = rng.integers(0, 65536, ss).astype(np.uint16) if se in ("f16", "bf16") else rng.normal(0, 1, ss).astype(np.float32)
@@ -383,7 +384,7 @@ def fuzz_inputs(n, seed=0x46555A5A):
     """Arguments of group fuzz<n> of catalog module fuzz_generic (its float
     type read from the group's signature)."""
     import re
-    ir = hf.catalog.get("fuzz_generic")
+    ir = cat.get("fuzz_generic")
     ft = re.search(r"@fuzz%d\(%%x: tensor<32x257x(\w+)>" % n, ir).group(1)
     rng = np.random.default_rng(seed + n)
     x = rng.normal(0, 3, (32, 257)).astype(np.float32)
@@ -399,7 +400,7 @@ def fuzz_row_inputs(n, seed=0x46524F57):
     """Arguments of group frow<n> of catalog module fuzz_rows (shape read
     from its signature), with ±0, ±inf and a NaN row among the values."""
     import re
-    ir = hf.catalog.get("fuzz_rows")
+    ir = cat.get("fuzz_rows")
     r, c = map(int, re.search(r"@frow%d\(%%x: tensor<(\d+)x(\d+)xf32>" % n, ir).groups())
     rng = np.random.default_rng(seed + n)
     x = rng.normal(0, 5, (r, c)).astype(np.float32)

@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from helpers import bf16_ulp_diff, run_gpu, run_oracle
 
 I = hf.inputs
@@ -128,13 +129,13 @@ def test_oracle_max_bias_rank3():
 
 
 def test_lowering_kinds(tmp_path):
-    art = hf.compile(hf.catalog.get("any_pbr_ops"))
+    art = hf.compile(cat.get("any_pbr_ops"))
     kinds = {b["func"]: (b["kind"], b.get("variant", "")) for b in art.blocks}
     assert kinds["sumsq_mid"][0] == "ANY_PBR" and "dim 1 of 3" in kinds["sumsq_mid"][1]
     assert kinds["isum_d01"][0] == "ANY_PBR" and "dim 0 of 2" in kinds["isum_d01"][1]  # [6,50] collapse
     assert kinds["sum_rank3_last"][0] == "LAST_AXIS_PBR"  # rank 3 -> rows x 100
     assert kinds["max_bias_rank3"][0] == "ANY_PBR"        # [S,C] operand: no row layout
-    rq = hf.compile(hf.catalog.get("rmsnorm_quant_rank3")).blocks[0]
+    rq = hf.compile(cat.get("rmsnorm_quant_rank3")).blocks[0]
     assert rq["kind"] == "LAST_AXIS_PBR" and "serial-order" in rq.get("variant", "")
 
 

@@ -9,6 +9,7 @@ import subprocess
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from hfusion_mi355x import native
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -52,9 +53,9 @@ def test_manifest_rejects_garbage(tmp_path):
     assert native.hfr().hfr_group_load(str(p).encode(), None, ctypes.byref(h)) == -4
 
 
-@pytest.mark.parametrize("name", sorted(hf.catalog.entries()))
+@pytest.mark.parametrize("name", sorted(cat.entries()))
 def test_every_catalog_group_lowers(name, tmp_path):
-    rc, err, prefix = emit(hf.catalog.get(name), tmp_path, options=hf.catalog.options(name))
+    rc, err, prefix = emit(cat.get(name), tmp_path, options=cat.options(name))
     assert rc == 0, err
     blocks = hf.parse_manifest(prefix + ".manifest")
     for b in blocks:
@@ -69,7 +70,7 @@ def test_classification_and_ties(tmp_path):
     expect = {"vec_add": "PURE_ELEMWISE", "eltwise_mix": "ANY_PB", "rmsnorm_quant": "LAST_AXIS_PBR",
               "safe_softmax": "LAST_AXIS_PBR", "argmax": "REDUCE_WITH_INDEX", "w8a8_dequant": "SINGLE_CUBE"}
     for name, kind in expect.items():
-        rc, err, prefix = emit(hf.catalog.get(name), tmp_path, name)
+        rc, err, prefix = emit(cat.get(name), tmp_path, name)
         assert rc == 0, err
         b = hf.parse_manifest(prefix + ".manifest")[0]
         assert b["kind"] == kind, name
@@ -239,7 +240,7 @@ def test_cli_builds_code_object(tmp_path):
 def test_host_api_validates_before_launch():
     """Shape/dtype mismatches are rejected on the host, before any GPU call."""
     import torch
-    art = hf.compile(hf.catalog.get("vec_add_ragged"))
+    art = hf.compile(cat.get("vec_add_ragged"))
     meta = art.blocks[0]
     assert meta["params"][0]["shape"] == (1001,)
     g = object.__new__(hf.Group)
@@ -262,7 +263,7 @@ def test_memref_form_groups_compile(tmp_path):
     assert rc == 0, err
     man = open(prefix + ".manifest").read()
     assert "result 0 1 i32 1 6" in man, man
-    rc, err, prefix = emit(hf.catalog.get("memref_chain"), tmp_path, "chain")
+    rc, err, prefix = emit(cat.get("memref_chain"), tmp_path, "chain")
     assert rc == 0, err
     man = open(prefix + ".manifest").read()
     assert "result 0 1 f32" in man and "result 1 2 f32" in man, man

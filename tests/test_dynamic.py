@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from hfusion_mi355x.runtime import dynamic_dims
 from helpers import bf16_ulp_diff, run_oracle, to_dev
 
@@ -37,15 +38,15 @@ def emit_hip(ir, options, tmp_path):
 
 @pytest.mark.parametrize("rows", [1, 37, 8192])
 def test_specialised_equals_static(rows, tmp_path):
-    dyn = hf.catalog.get("rmsnorm_quant_dyn")
-    a, err = emit_hip(dyn, hf.catalog.dyn_options("rmsnorm_quant_dyn", rows), tmp_path / "a")
+    dyn = cat.get("rmsnorm_quant_dyn")
+    a, err = emit_hip(dyn, cat.dyn_options("rmsnorm_quant_dyn", rows), tmp_path / "a")
     assert a is not None, err
     b, err = emit_hip(G.rmsnorm_quant(rows, 4096), "", tmp_path / "b")
     assert a == b
 
 
 def test_dynamic_dims_and_errors(tmp_path):
-    dyn = hf.catalog.get("rmsnorm_quant_dyn")
+    dyn = cat.get("rmsnorm_quant_dyn")
     assert dynamic_dims(dyn) == [("rmsnorm_quant", 0, 0), ("rmsnorm_quant", 2, 0), ("rmsnorm_quant", 3, 0)]
     src, err = emit_hip(dyn, "", tmp_path)
     assert src is None and "has no size (compile with dyn=rmsnorm_quant:0.0=<size>)" in err
@@ -85,7 +86,7 @@ def test_oracle_runs_dynamic_ir():
 
 def _call(name, args, gpu):
     import torch
-    dg = hf.DynamicGroup(hf.catalog.get(name), require_cached=True)
+    dg = hf.DynamicGroup(cat.get(name), require_cached=True)
     g = dg.specialise(dg.sizes_of(args))
     devs = [to_dev(a, p["elem"], gpu) for a, p in zip(args, g.meta["params"])]
     out = dg(*devs)
@@ -100,7 +101,7 @@ def _call(name, args, gpu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows", hf.catalog.DYN_ROWS["rmsnorm_quant_dyn"])
+@pytest.mark.parametrize("rows", cat.DYN_ROWS["rmsnorm_quant_dyn"])
 def test_gpu_rmsnorm_quant_dynamic(gpu, rows):
     note(f"rmsnorm_quant_dyn rows={rows}")
     rng = np.random.default_rng(rows)
@@ -113,7 +114,7 @@ def test_gpu_rmsnorm_quant_dynamic(gpu, rows):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows", hf.catalog.DYN_ROWS["softmax_dyn"])
+@pytest.mark.parametrize("rows", cat.DYN_ROWS["softmax_dyn"])
 def test_gpu_softmax_dynamic(gpu, rows):
     note(f"softmax_dyn rows={rows}")
     x = np.random.default_rng(rows).normal(0, 2, (rows, 1000)).astype(np.float32)
@@ -123,7 +124,7 @@ def test_gpu_softmax_dynamic(gpu, rows):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", hf.catalog.DYN_ROWS["vec_add_dyn"])
+@pytest.mark.parametrize("n", cat.DYN_ROWS["vec_add_dyn"])
 def test_gpu_vec_add_dynamic(gpu, n):
     note(f"vec_add_dyn n={n}")
     rng = np.random.default_rng(n)

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from hfusion_mi355x import inputs as I
 from hfusion_mi355x import native
 from oracle import interp
@@ -278,7 +279,7 @@ def test_zero_rank_group(tmp_path):
 def test_inference_keeps_declared_groups(tmp_path):
     """A function that already carries hfusion.fusion_kind is one kernel: the
     front-end leaves the module untouched and plans no program."""
-    groups, progs, text = outline(hf.catalog.get("rmsnorm_quant_256"), tmp_path)
+    groups, progs, text = outline(cat.get("rmsnorm_quant_256"), tmp_path)
     assert progs == [] and [g[0] for g in groups] == ["rmsnorm_quant"]
 
 
@@ -294,7 +295,7 @@ def test_single_kind_host_function_is_one_group(tmp_path):
 
 # ------------------------------------------------------------- programs
 def test_program_plan_of_gemm_rmsnorm_quant(tmp_path):
-    groups, progs, text = outline(hf.catalog.get("prog_gemm_rmsnorm_quant"), tmp_path)
+    groups, progs, text = outline(cat.get("prog_gemm_rmsnorm_quant"), tmp_path)
     assert [(n, k) for n, k, _ in groups] == [("gemm_rmsnorm_quant_multi_MIX_CV_0", "MIX_CV"),
                                             ("gemm_rmsnorm_quant_multi_LAST_AXIS_PBR_0", "LAST_AXIS_PBR")]
     # the zero fill of the accumulator is emitted inside the contraction's
@@ -345,7 +346,7 @@ def scores_args(m, n, k):
     ("prog_scores_softmax_ragged", scores_args, (72, 1000, 64)),
 ])
 def test_program_equals_unfused_function_on_oracle(name, make, shape, tmp_path):
-    ir = hf.catalog.get(name)
+    ir = cat.get(name)
     args = make(*shape)
     whole = interp.run(ir, *[a.copy() for a in args])
     whole = whole if isinstance(whole, (list, tuple)) else [whole]

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from hfusion_mi355x import native
 from helpers import run_oracle, to_dev, to_host
 
@@ -60,7 +61,7 @@ def test_memref_descriptors_with_offsets(gpu):
     name, rows, cols = "rmsnorm_quant_ragged", 13, 1000
     x, gamma = I.config_inputs("rmsnorm_quant", rows=rows, cols=cols)
     args = [x, gamma, np.zeros((rows, cols), np.int8), np.zeros(rows, np.float32)]
-    grp = hf.compile(hf.catalog.get(name), require_cached=True).load()
+    grp = hf.compile(cat.get(name), require_cached=True).load()
     params = grp.meta["params"]
     offs = [3, 7, 11, 5]
     bufs, descs = [], []
@@ -88,7 +89,7 @@ def test_memref_descriptor_untied_result_and_errors(gpu):
     import torch
     s = I.SEED_BASE + 97
     args = [I.normal_f32(s, (128, 256)), I.normal_f32(s + 1, (128, 256)), I.normal_f32(s + 2, (32, 4, 256))]
-    grp = hf.compile(hf.catalog.get("reshape_chain"), require_cached=True).load()
+    grp = hf.compile(cat.get("reshape_chain"), require_cached=True).load()
     assert [r["tied"] for r in grp.meta["results"]] == [-1]
     bufs, descs = [], []
     for k, (a, p) in enumerate(zip(args, grp.meta["params"])):
@@ -124,7 +125,7 @@ def test_module_kernel_launch_by_hand(gpu):
     code object, with the launch shape and argument order of its manifest."""
     note("hfr_launch vec_add_ragged")
     import torch
-    art = hf.compile(hf.catalog.get("vec_add_ragged"), require_cached=True)
+    art = hf.compile(cat.get("vec_add_ragged"), require_cached=True)
     meta = art.blocks[0]
     hsaco = os.path.join(os.path.dirname(art.manifest), meta["hsaco"])
     lib = native.hfr()

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from helpers import (MATH_EXACT, bf16_ulp_diff, fp_funcs, fp_inputs, fuzz_inputs, fuzz_row_inputs, gather_inputs,
                      generic_inputs,
                      math_funcs,
@@ -500,7 +501,7 @@ def test_fp_ops(gpu, func):
 
 
 # ----------------------------------------- scans, histogram, (de)interleave
-@pytest.mark.parametrize("name", [s[0] for s in hf.catalog.SCAN_OPS])
+@pytest.mark.parametrize("name", [s[0] for s in cat.SCAN_OPS])
 def test_scan_ops(gpu, name):
     """Cumulative ops in the serial order and per-step rounding of the CPU
     loop: bit-exact (NaN positions included)."""
@@ -514,7 +515,7 @@ def test_scan_ops(gpu, name):
         assert np.array_equal(out, ref), f"{int((out != ref).sum())} differ"
 
 
-@pytest.mark.parametrize("name", [h[0] for h in hf.catalog.HIST_OPS] + [i[0] for i in hf.catalog.INTERLEAVE_OPS])
+@pytest.mark.parametrize("name", [h[0] for h in cat.HIST_OPS] + [i[0] for i in cat.INTERLEAVE_OPS])
 def test_misc_ops(gpu, name):
     """histogram counts (twice in a row: the workspace is left cleared) and
     (de)interleave: bit-exact."""
@@ -541,7 +542,7 @@ def test_program_with_scan(gpu):
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("name", hf.catalog.MISC_EXTRA)
+@pytest.mark.parametrize("name", cat.MISC_EXTRA)
 def test_flip_mulext_arange(gpu, name):
     """flip, mulext / mulextui (both halves) and arange (offset argument,
     negative stride, i32 and f32 results): bit-exact."""
@@ -554,7 +555,7 @@ def test_flip_mulext_arange(gpu, name):
         assert np.array_equal(o, r), f"{int((o != r).sum())} differ"
 
 
-@pytest.mark.parametrize("name", [g[0] for g in hf.catalog.GATHER_OPS])
+@pytest.mark.parametrize("name", [g[0] for g in cat.GATHER_OPS])
 def test_gather(gpu, name):
     """hfusion.gather along axis 1 and 0 with out-of-range indices (init
     kept): bit-exact."""

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from hfusion_mi355x import native
 from helpers import parse_data_file, print_data
 from oracle import interp
@@ -19,7 +20,7 @@ CLI = os.path.join(native.BIN_DIR, "bishengir-compile")
 @pytest.mark.parametrize("name", ["vec_add_ragged", "prog_gemm_rmsnorm_quant_ragged"])
 def test_runner_matches_oracle(name, tmp_path, gpu):
     print(f"[case] runner {name}", flush=True)
-    ir = hf.catalog.get(name)
+    ir = cat.get(name)
     (tmp_path / "m.mlir").write_text(ir)
     r = subprocess.run([CLI, "m.mlir", "-o", "m", "--enable-cpu-runner"], capture_output=True, text=True,
                        cwd=tmp_path, timeout=300)

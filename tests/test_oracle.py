@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from oracle import interp
 from oracle.interp import lib, ptr
 
@@ -36,7 +37,7 @@ def special_f32(n=20000, seed=1):
 def test_vecadd_i16_golden():
     g = json.load(open(os.path.join(GOLDEN, "vecadd_i16.json")))
     a, b = np.array(g["a"], np.int16), np.array(g["b"], np.int16)
-    out, = interp.run(hf.catalog.get("vec_add_i16"), a, b, np.zeros(16, np.int16))
+    out, = interp.run(cat.get("vec_add_i16"), a, b, np.zeros(16, np.int16))
     assert out.tolist() == g["expect"]
 
 
@@ -53,7 +54,7 @@ def test_cast_folds_golden():
         elif f.get("from") == "f32" and f["to"] == "f32":
             x = np.array([f["in"]], np.float32)
             for sem in ("cpu", "declared"):  # both semantics agree on this fold
-                ir = hf.catalog.get("cast_modes")
+                ir = cat.get("cast_modes")
                 pad = np.zeros(4096, np.float32)
                 pad[0] = x[0]
                 out, = interp.run(ir, pad, np.zeros(4096, np.float32), func="cast_f32_f32_rint", cast_semantics=sem)
@@ -396,7 +397,7 @@ def test_reduce_with_index_region_brute_force():
 
 def test_argmax_group_matches_composed_and_numpy():
     x = I.argmax_logits(I.SEED_BASE + 3, 8, 152064, dup_every=2)
-    v, i = interp.run(hf.catalog.get("argmax_16").replace("16x", "8x").replace("<16x", "<8x")
+    v, i = interp.run(cat.get("argmax_16").replace("16x", "8x").replace("<16x", "<8x")
                       .replace("tensor<16xf32>", "tensor<8xf32>").replace("tensor<16xi32>", "tensor<8xi32>"),
                       x, np.zeros(8, np.float32), np.zeros(8, np.int32))
     v2, i2 = np.empty(8, np.float32), np.empty(8, np.int32)
@@ -467,7 +468,7 @@ def test_interp_matches_composed_softmax_on_edge_rows():
     x[1, 5] = 0.0
     x[2] = 1e30
     x[3] = I.normal_f32(5, (1000,))
-    out, = interp.run(hf.catalog.get("safe_softmax_ragged").replace("33x", "4x").replace("tensor<33xf32>", "tensor<4xf32>"),
+    out, = interp.run(cat.get("safe_softmax_ragged").replace("33x", "4x").replace("tensor<33xf32>", "tensor<4xf32>"),
                       x, np.zeros((4, 1000), np.uint16))
     o2 = np.zeros_like(out)
     lib().hfref_softmax_bf16(ptr(x), ptr(o2), 4, 1000)
@@ -480,7 +481,7 @@ def test_cpu_vs_declared_cast_quirk():
     (fptosi), the declared RINT mode rounds to nearest even."""
     x = np.zeros(4096, np.float32)
     x[:4] = [2.7, -2.7, 2.5, 3.5]
-    ir = hf.catalog.get("cast_modes")
+    ir = cat.get("cast_modes")
     cpu, = interp.run(ir, x, np.zeros(4096, np.int8), func="cast_i8_rint", cast_semantics="cpu")
     dec, = interp.run(ir, x, np.zeros(4096, np.int8), func="cast_i8_rint", cast_semantics="declared")
     assert cpu[:4].tolist() == [2, -2, 2, 3]
@@ -509,7 +510,7 @@ def test_hivm_matmul_f16_formula(name):
     else:  # a_transpose, b_transpose, per-tensor descale: A given [K, M], B given [N, K]
         args = [_f16(a.T.copy()), _f16(b.T.copy()), _f16(bias), _f16(ds[:1])]
         ref = (a.astype(np.float64) @ b.astype(np.float64) + bias) * float(ds[0])
-    out, = interp.run(hf.catalog.get(name), *args, np.zeros((16, 16), np.uint16))
+    out, = interp.run(cat.get(name), *args, np.zeros((16, 16), np.uint16))
     got = out.view(np.float16).astype(np.float64)
     ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
     assert np.all(np.abs(got - ref) <= ulp)
@@ -522,7 +523,7 @@ def test_hivm_matmul_i8_int_bias_and_saturation():
     a = rng.integers(-127, 128, (256, 128)).astype(np.int8)
     b = rng.integers(-127, 128, (320, 128)).astype(np.int8)
     ds = np.array([2e-3], np.float32)
-    out, = interp.run(hf.catalog.get("hivm_mm_i8_pt_i8out"), a, b, ds, np.zeros((256, 320), np.int8))
+    out, = interp.run(cat.get("hivm_mm_i8_pt_i8out"), a, b, ds, np.zeros((256, 320), np.int8))
     acc = a.astype(np.int64) @ b.astype(np.int64).T
     t = (acc.astype(np.float32) * ds[0]).astype(np.float32)
     assert np.array_equal(out, np.clip(np.rint(t), -128, 127).astype(np.int8))
@@ -531,7 +532,7 @@ def test_hivm_matmul_i8_int_bias_and_saturation():
     a2 = rng.integers(-127, 128, (300, 192)).astype(np.int8)
     b2 = rng.integers(-127, 128, (200, 192)).astype(np.int8)
     dsc = rng.uniform(0.001, 0.02, 200).astype(np.float32)
-    out2, = interp.run(hf.catalog.get("hivm_mm_i8_pc"), a2, b2, bias, dsc, np.zeros((300, 200), np.uint16))
+    out2, = interp.run(cat.get("hivm_mm_i8_pc"), a2, b2, bias, dsc, np.zeros((300, 200), np.uint16))
     acc2 = a2.astype(np.int64) @ b2.astype(np.int64).T + bias.astype(np.int64)
     t2 = (acc2.astype(np.float32) * dsc[None, :]).astype(np.float32)
     import torch

@@ -11,6 +11,7 @@ import pytest
 import scipy.special
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from helpers import math_funcs, math_inputs, run_oracle
 
 _D = {
@@ -114,7 +115,7 @@ def test_math_module_lists_every_function():
     for fn in ("atan2", "ldexp", "divfhp"):
         assert f"b_{fn}" in names
     assert {"i_powi_i32", "i_ceildivui_i32", "i_modui_i32"} <= names
-    assert hf.catalog.get("math_fns").count("func.func") == len(names)
+    assert cat.get("math_fns").count("func.func") == len(names)
 
 
 # --------------------------------------------------------------------- fp_ops
@@ -133,7 +134,7 @@ def test_fp_predicates_specials():
     x = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, 3.4e38, -1.0], np.float32)
     want = {"isinf": [0, 0, 1, 1, 0, 0, 0, 0], "isnan": [0, 0, 0, 0, 1, 0, 0, 0], "isfinite": [1, 1, 0, 0, 0, 1, 1, 1]}
     for op, w in want.items():
-        ir = hf.catalog.fp_ops(8)
+        ir = cat.fp_ops(8)
         got, = run_oracle_ir(ir, [x], f"{op}_f32")
         assert got.astype(int).tolist() == w, op
 
@@ -258,7 +259,7 @@ def test_bitcast_op():
 from helpers import misc_inputs, scan_inputs  # noqa: E402
 
 
-@pytest.mark.parametrize("spec", hf.catalog.SCAN_OPS, ids=[s[0] for s in hf.catalog.SCAN_OPS])
+@pytest.mark.parametrize("spec", cat.SCAN_OPS, ids=[s[0] for s in cat.SCAN_OPS])
 def test_scan_against_numpy_accumulate(spec):
     """numpy's accumulate is a left-to-right loop in the array's dtype, so it
     pins the serial order and the per-step rounding (numpy has no bf16: that
@@ -304,7 +305,7 @@ def test_bf16_cumprod_exact_rounding():
     two bf16 values (at most 16 significant bits, exact in double) rounded
     half-even to bf16; recomputed here in double with an independent rounding."""
     name = "cumprod_bf16_rev"
-    spec = {s[0]: s for s in hf.catalog.SCAN_OPS}[name]
+    spec = {s[0]: s for s in cat.SCAN_OPS}[name]
     x, = scan_inputs(name)
     got, = run_oracle("scan_ops", [x], func=name)
     xf = (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
@@ -321,7 +322,7 @@ def test_bf16_cumprod_exact_rounding():
     assert (np.abs(want[:, :-1]) > 0).sum() > 1000
 
 
-@pytest.mark.parametrize("spec", hf.catalog.HIST_OPS, ids=[h[0] for h in hf.catalog.HIST_OPS])
+@pytest.mark.parametrize("spec", cat.HIST_OPS, ids=[h[0] for h in cat.HIST_OPS])
 def test_histogram_counts(spec):
     name, ie, shape, bins, ce, me = spec
     args = misc_inputs(name)
@@ -337,7 +338,7 @@ def test_histogram_counts(spec):
 
 
 def test_deinterleave_interleave_closed_form():
-    for name, e, ch in hf.catalog.INTERLEAVE_OPS:
+    for name, e, ch in cat.INTERLEAVE_OPS:
         args = misc_inputs(name)
         outs = run_oracle("misc_ops", args, func=name)
         if ch is None:
@@ -355,7 +356,7 @@ from helpers import misc_extra_inputs  # noqa: E402
 def test_mulext_halves_recompose_the_product():
     """lo + hi * 2^N equals the exact product of the sign- (mulext) or
     zero-extended (mulextui) operands, with lo read unsigned."""
-    for name in [n for n in hf.catalog.MISC_EXTRA if n.startswith("mulext")]:
+    for name in [n for n in cat.MISC_EXTRA if n.startswith("mulext")]:
         a, b = misc_extra_inputs(name)
         lo, hi = run_oracle("misc_ops", [a, b], func=name)
         bits = a.dtype.itemsize * 8
@@ -380,7 +381,7 @@ def test_flip_and_arange_closed_forms():
 from helpers import gather_inputs  # noqa: E402
 
 
-@pytest.mark.parametrize("spec", hf.catalog.GATHER_OPS, ids=[g[0] for g in hf.catalog.GATHER_OPS])
+@pytest.mark.parametrize("spec", cat.GATHER_OPS, ids=[g[0] for g in cat.GATHER_OPS])
 def test_gather_loop_form(spec):
     """The op description's loop (HFusionStructuredOps.td:222-238), run
     literally on the group's inputs: output[p] = src[.. k ..] for the k with

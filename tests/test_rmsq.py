@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from helpers import run_gpu, run_oracle
 
 I = hf.inputs
@@ -77,11 +78,11 @@ def test_rmsq_stress_rows_bit_exact(gpu):
 
 def test_rmsq_selected_only_when_asked():
     for name in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3"):
-        assert "serial-order" in hf.compile(hf.catalog.get(name)).blocks[0]["variant"], name
-        v = hf.compile(hf.catalog.get(name), options="rmsq_kernel=1").blocks[0]["variant"]
+        assert "serial-order" in hf.compile(cat.get(name)).blocks[0]["variant"], name
+        v = hf.compile(cat.get(name), options="rmsq_kernel=1").blocks[0]["variant"]
         assert "rmsnorm-quant" in v, name
     # a width the kernel does not take keeps the generic row program
-    v = hf.compile(hf.catalog.get("rmsnorm_quant_ragged"), options="rmsq_kernel=1").blocks[0]["variant"]
+    v = hf.compile(cat.get("rmsnorm_quant_ragged"), options="rmsq_kernel=1").blocks[0]["variant"]
     assert "serial-order" in v
 
 

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from helpers import run_gpu, run_oracle
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -53,7 +54,7 @@ def closed_form(name, args):
         return np.abs(args[0]).reshape(4, 100, 1)
 
 
-@pytest.mark.parametrize("name", hf.catalog.TRANSPOSE_OPS)
+@pytest.mark.parametrize("name", cat.TRANSPOSE_OPS)
 def test_oracle_transpose(name):
     args = inputs(name)
     ref, = run_oracle("transpose_ops", args, func=name)
@@ -73,13 +74,13 @@ def test_reference_foldable_transpose_lowers(tmp_path):
 
 
 def test_lowering_stages_transposed_inputs():
-    kinds = {b["func"]: b.get("variant", "") for b in hf.compile(hf.catalog.get("transpose_ops")).blocks}
+    kinds = {b["func"]: b.get("variant", "") for b in hf.compile(cat.get("transpose_ops")).blocks}
     assert "LDS-staged" in kinds["tr2d_cast"] and "LDS-staged" in kinds["tr3d_rot_i8"]
     assert kinds["tr_unit"] == "streaming"
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", hf.catalog.TRANSPOSE_OPS)
+@pytest.mark.parametrize("name", cat.TRANSPOSE_OPS)
 def test_gpu_transpose(gpu, name):
     note(f"transpose_ops {name}")
     args = inputs(name)

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import hfusion_mi355x as hf
+import group_catalog as cat
 from hfusion_mi355x import native
 from helpers import misc_inputs, to_dev, to_host
 
@@ -22,7 +23,7 @@ def note(msg):
 
 def _run(name, inputs, device, func=None, noalloc=False):
     import torch
-    grp = hf.compile(hf.catalog.get(name), require_cached=True).load(func)
+    grp = hf.compile(cat.get(name), require_cached=True).load(func)
     devs = [a if p["role"] == "scalar" else to_dev(a, p["elem"], device) for a, p in zip(inputs, grp.meta["params"])]
     out = grp(*devs, noalloc=noalloc)
     torch.cuda.synchronize()
