@@ -2446,7 +2446,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
 bool isSingleOpKernel(const std::string &n) {
   return n == "hfusion.cumsum" || n == "hfusion.cumprod" || n == "hfusion.cummax" || n == "hfusion.cummin" ||
          n == "hfusion.histogram" || n == "hfusion.deinterleave" || n == "hfusion.interleave" || n == "hfusion.flip" ||
-         n == "hfusion.mulext" || n == "hfusion.mulextui" || n == "hfusion.arange" || n == "hfusion.gather";
+         n == "hfusion.mulext" || n == "hfusion.mulextui" || n == "hfusion.arange" || n == "hfusion.gather" || n == "hfusion.sort";
 }
 
 static std::vector<int64_t> intList(const std::string &s) {
@@ -2462,7 +2462,7 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
   for (const Op *o : f.ops)
     if (o != op && o->name != "tensor.empty" && o->name != "arith.constant" && o->name.rfind("arith.index", 0) != 0)
       unsupported(o, "op in a group with " + op->name);
-  if (op->name == "hfusion.gather")
+  if (op->name == "hfusion.gather" || op->name == "hfusion.sort")
     for (const Value *v : op->ins)
       if (v->argIdx < 0) unsupported(op, "operand that is not a group argument");
   if (op->name != "hfusion.arange")
@@ -2651,6 +2651,54 @@ static KernelPlan lowerSingleOp(Analysis &A, const std::string &kname, const Op 
     p.variant = "one thread per output element";
     p.grid[0] = (unsigned)std::max<int64_t>(1, (N + 255) / 256);
     p.block[0] = 256;
+  } else if (n == "sort") {
+    // value sort along the last axis (HFusionOps.cpp:3341-3348 accepts only
+    // the tail axis); the reference's bubble-sort decomposition
+    // (DecomposeOpInterfaceImpl.cpp:740-830) handles one result only
+    if (op->ins.size() != 1) unsupported(op, "sort without exactly one input");
+    if (op->results.size() != 1) unsupported(op, "sort with an index result (the reference decomposes only the value sort)");
+    const Value *x = op->ins[0];
+    const Elem e = x->type.elem;
+    if (op->results[0]->type.elem != e || op->results[0]->type.shape != x->type.shape)
+      unsupported(op, "sort result type differing from the input");
+    const auto &sh = x->type.shape;
+    const int64_t rank = (int64_t)sh.size(), ax = std::stoll(op->attr("sort_axis", "-1"));
+    if (ax != -1 && ax != rank - 1) unsupported(op, "sort along an axis other than the last");
+    int kind;
+    switch (e) {
+    case Elem::F32: kind = 0; break;
+    case Elem::F16: kind = 1; break;
+    case Elem::BF16: kind = 2; break;
+    case Elem::I8: kind = 8; break;
+    case Elem::I16: kind = 16; break;
+    case Elem::I32: kind = 32; break;
+    default: unsupported(op, std::string("sort of ") + elemName(e) + " (f32, f16, bf16 and i8/i16/i32 are lowered)");
+    }
+    const int64_t L = sh.back(), R = numel(sh) / std::max<int64_t>(1, L);
+    if (L > 16384) unsupported(op, "sort axis longer than 16384 (one row is sorted in LDS)");
+    int64_t P = 1;
+    while (P < L) P <<= 1;
+    const int64_t rpw = P >= 2048 ? 1 : 2048 / P, E = rpw * P;
+    const int nt = E <= 2048 ? 256 : 1024;
+    const bool desc = op->attr("descending", "false") == "true";
+    const std::string T = mtype(e);
+    if (L <= 1) {
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+        << "  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;\n"
+        << "  if (t < " << R << "ll) ((" << T << " *)" << outPtr[0] << ")[t] = ((const " << T << " *)p" << x->argIdx << ")[t];\n}\n";
+      p.variant = "copy (one element per row)";
+      p.grid[0] = (unsigned)std::max<int64_t>(1, (R + 255) / 256);
+      p.block[0] = 256;
+    } else {
+      k << "extern \"C\" __global__ __launch_bounds__(" << nt << ") void " << kname << "(" << kernelParamList(A, p.kargs, false)
+        << ") {\n  hf::sort_rows<" << kind << ", " << (desc ? "true" : "false") << ", " << P << ", " << nt << ">((const " << T
+        << " *)p" << x->argIdx << ", (" << T << " *)" << outPtr[0] << ", " << R << "ll, " << L << ");\n}\n";
+      p.variant = "bitonic network, " + std::to_string(rpw) + " row(s) of " + std::to_string(P) +
+                  " keys per workgroup in LDS, " + (desc ? "descending" : "ascending");
+      p.grid[0] = (unsigned)std::max<int64_t>(1, (R + rpw - 1) / rpw);
+      p.block[0] = (unsigned)nt;
+    }
+    p.kind = "SORT";
   } else if (n == "histogram") {
     const Value *x = op->operands.at(0);
     const Value *mk = op->operands.size() > 1 ? op->operands[1] : nullptr;
@@ -3631,7 +3679,7 @@ std::string emitTranslationUnit(const std::vector<KernelPlan> &plans) {
   std::ostringstream s;
   s << "// Generated by bishengir-compile --target=mi355x (ConvertHFusionToHIP).\n"
     << "#include \"hf_ops.h\"\n#include \"hf_row.h\"\n#include \"hf_argmax.h\"\n#include \"hf_mmad.h\"\n#include \"hf_misc.h\"\n"
-    << "#include \"hf_rmsq.h\"\n\n";
+    << "#include \"hf_rmsq.h\"\n#include \"hf_sort.h\"\n\n";
   for (auto &p : plans) s << "// group @" << p.funcName << ": " << p.kind << " (" << p.variant << ")\n" << p.source << "\n";
   return s.str();
 }

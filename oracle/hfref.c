@@ -860,3 +860,55 @@ int hfref_w8a8_dequant_memref(const void *a, const void *bt, const void *s_tok, 
   free(dsc);
   return 0;
 }
+
+/* ---- hfusion.sort ----
+ * The reference decomposes a value sort along the last axis into a bubble
+ * sort (bishengir/lib/Dialect/HFusion/Transforms/DecomposeOpInterfaceImpl.cpp:
+ * 740-830): n-1 passes, each comparing elements j and j+1 for j = 0..n-2 in
+ * order and swapping them when `cmpf ugt` (ascending) / `cmpf ult`
+ * (descending) holds -- unordered predicates, so any comparison with a NaN
+ * swaps -- or, for integers, `cmpi sgt` / `cmpi slt`.  Restated literally. */
+static double sort_key(const void *row, int64_t j, int kind) {
+  switch (kind) {
+  case 0: return ((const float *)row)[j];
+  case 1: return hfref_f16_to_f32(((const uint16_t *)row)[j]);
+  case 2: return hfref_bf16_to_f32(((const uint16_t *)row)[j]);
+  case 8: return ((const int8_t *)row)[j];
+  case 16: return ((const int16_t *)row)[j];
+  case 32: return ((const int32_t *)row)[j];
+  default: return 0;
+  }
+}
+
+static int sort_need_swap(const void *row, int64_t j, int kind, int descending) {
+  if (kind == 64) {
+    const int64_t a = ((const int64_t *)row)[j], b = ((const int64_t *)row)[j + 1];
+    return descending ? a < b : a > b;
+  }
+  const double a = sort_key(row, j, kind), b = sort_key(row, j + 1, kind);
+  if (kind <= 2 && (a != a || b != b)) return 1; /* unordered: ugt / ult hold */
+  return descending ? a < b : a > b;
+}
+
+int hfref_sort_rows(void *data, int64_t R, int64_t L, int kind, int descending) {
+  int esz;
+  switch (kind) {
+  case 0: case 32: esz = 4; break;
+  case 1: case 2: case 16: esz = 2; break;
+  case 8: esz = 1; break;
+  case 64: esz = 8; break;
+  default: return -1;
+  }
+  for (int64_t r = 0; r < R; ++r) {
+    char *row = (char *)data + r * L * esz;
+    for (int64_t pass = 0; pass + 1 < L; ++pass)
+      for (int64_t j = 0; j + 1 < L; ++j)
+        if (sort_need_swap(row, j, kind, descending)) {
+          char t[8];
+          memcpy(t, row + j * esz, esz);
+          memcpy(row + j * esz, row + (j + 1) * esz, esz);
+          memcpy(row + (j + 1) * esz, t, esz);
+        }
+  }
+  return 0;
+}

@@ -136,6 +136,12 @@ void hfref_w8a8_dequant_rows(const int8_t *A, const int8_t *Bt,
                              uint16_t *out, int64_t M, int64_t N, int64_t K,
                              int64_t m0, int64_t m1);
 
+/* hfusion.sort of the values along the last axis of R rows of L elements, in
+ * place: the bubble sort the reference decomposes the op into.  kind: 0 f32,
+ * 1 f16, 2 bf16 (float compare after the exact widening), 8/16/32/64 signed
+ * integers of that width.  Returns 0, or -1 for an unknown kind. */
+int hfref_sort_rows(void *data, int64_t R, int64_t L, int kind, int descending);
+
 /* ---- host-entry ABI: MLIR ranked memref descriptors ----
  * The reference's runner calls `_mlir_ciface_<func>` with memref descriptors
  * (bishengir/lib/ExecutionEngine/BiShengIRRunnerUtils.cpp:99-110): for rank R

@@ -78,6 +78,7 @@ def lib():
             "hfref_softmax_bf16_memref": [P, P],
             "hfref_argmax_memref": [P, P, P],
             "hfref_w8a8_dequant_memref": [P, P, P, P, P],
+            "hfref_sort_rows": [P, I64, I64, INT, INT],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -96,7 +97,7 @@ def lib():
         L.hfref_f32_to_int_mode.argtypes = [ctypes.c_float, INT, INT, INT]
         L.hfref_f32_to_int_mode.restype = ctypes.c_int64
         for name in sig:
-            if name.endswith("_memref") or name.startswith("hfref_memref_"):
+            if name.endswith("_memref") or name.startswith("hfref_memref_") or name == "hfref_sort_rows":
                 getattr(L, name).restype = ctypes.c_int
         L.hfref_int_to_f32_mode.argtypes = [ctypes.c_int64, INT]
         L.hfref_int_to_f32_mode.restype = ctypes.c_float
@@ -302,7 +303,9 @@ REDUCE_I = {"arith.addi": 0, "arith.muli": 1, "arith.maxsi": 2, "arith.minsi": 3
 
 
 _SINGLE = ("hfusion.cumsum", "hfusion.cumprod", "hfusion.cummax", "hfusion.cummin", "hfusion.histogram",
-           "hfusion.deinterleave", "hfusion.interleave", "hfusion.flip", "hfusion.mulext", "hfusion.mulextui")
+           "hfusion.deinterleave", "hfusion.interleave", "hfusion.flip", "hfusion.mulext", "hfusion.mulextui", "hfusion.sort")
+
+_SORT_KIND = {"f32": 0, "f16": 1, "bf16": 2, "i8": 8, "i16": 16, "i32": 32, "i64": 64}
 
 
 def _single_op(op, rest, xs, rtypes):
@@ -332,6 +335,22 @@ def _single_op(op, rest, xs, rtypes):
             acc = xv if acc is None else apply_binary(fn, acc, xv, elem, a[l].shape)
             out[l] = acc.a
         return [T(_contig(np.moveaxis(out, 0, d)), elem)]
+    if name == "sort":
+        # value sort along the last axis (HFusionOps.cpp:3341-3348 accepts only
+        # the tail axis), as the bubble sort of hfref_sort_rows
+        ax = int(re.search(r"sort_axis\s*=\s*(-?\d+)", rest).group(1))
+        desc = re.search(r"descending\s*=\s*true", rest) is not None
+        a = np.asarray(xs[0].a)
+        if ax not in (-1, a.ndim - 1):
+            raise ValueError("hfusion.sort: only the last axis can be sorted")
+        if len(rtypes) != 1:
+            raise ValueError("hfusion.sort: only the value result is restated (no index result)")
+        out = _contig(a).copy()
+        L = a.shape[-1] if a.ndim else 1
+        if L > 1 and out.size:
+            if lib().hfref_sort_rows(out.ctypes.data, out.size // L, L, _SORT_KIND[xs[0].elem], int(desc)) != 0:
+                raise ValueError(f"hfusion.sort of {xs[0].elem}")
+        return [T(out, xs[0].elem)]
     if name == "flip":
         # reverse along flip_axis (HFusionOps.td:226-245)
         m = re.search(r"flip_axis\s*=\s*(-?\d+)", rest)

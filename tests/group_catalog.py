@@ -898,6 +898,29 @@ def transpose_ops():
 
 TRANSPOSE_OPS = ["tr2d_cast", "tr3d_add", "tr3d_rot_i8", "tr_unit"]
 
+# hfusion.sort cases: (name, elem, shape, descending); the shapes of
+# bishengir/test/Dialect/HFusion/test_sort.mlir (6, 4x4, 2x3x4 descending),
+# ragged and power-of-two rows, one element per row, the longest row (16384)
+SORT_OPS = [("sort_1d_asc", "f32", [6], False), ("sort_2d_asc", "f32", [4, 4], False),
+            ("sort_3d_desc", "f32", [2, 3, 4], True), ("sort_f32_asc", "f32", [64, 1000], False),
+            ("sort_f32_desc", "f32", [37, 77], True), ("sort_bf16_asc", "bf16", [16, 4096], False),
+            ("sort_f16_desc", "f16", [8, 333], True), ("sort_i8_asc", "i8", [33, 100], False),
+            ("sort_i16_desc", "i16", [5, 2048], True), ("sort_i32_asc", "i32", [3, 16384], False),
+            ("sort_i32_desc", "i32", [50, 3], True), ("sort_f32_len1", "f32", [100, 1], False)]
+
+
+def sort_ops():
+    """One module, one group per hfusion.sort case."""
+    funcs = []
+    for name, elem, shape, desc in SORT_OPS:
+        X = _T(shape, elem)
+        funcs.append(f"""  func.func @{name}(%x: {X}) -> {X}
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %r = hfusion.sort ins(%x : {X}) descending = {str(desc).lower()} sort_axis = {len(shape) - 1} -> {X}
+    return %r : {X}
+  }}""")
+    return "module {\n" + "\n".join(funcs) + "\n}\n"
+
 def entries():
     """name -> IR text of every group the tests run: the product groups plus
     the parity cases below."""
@@ -951,6 +974,7 @@ def entries():
     e["generic_reduce"] = generic_reduce()
     e["any_pbr_ops"] = any_pbr_ops()
     e["transpose_ops"] = transpose_ops()
+    e["sort_ops"] = sort_ops()
     # dynamic row counts (compiled per size: DynamicGroup / option dyn=...)
     e["rmsnorm_quant_dyn"] = g.with_dynamic_rows(g.rmsnorm_quant(7919, 4096), 7919)
     e["softmax_dyn"] = g.with_dynamic_rows(g.safe_softmax(7919, 1000), 7919)
