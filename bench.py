@@ -9,6 +9,7 @@ contraction) with its roofline fraction.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
     python bench.py --vendor OUT   # each group vs its eager PyTorch equivalent
+    python bench.py --ceilings OUT # HBM rates of PyTorch's own streaming kernels
 """
 import argparse
 import json
@@ -393,6 +394,39 @@ def vendor_report(out, steps, warmup, command):
             f.write(text)
 
 
+def ceilings_report(out, steps, warmup, command):
+    """The HBM rates PyTorch's own streaming kernels reach on this part (read
+    only: sum; write only: fill; copy; a + b), over 512 MiB per launch, inputs
+    rotated through the same number of buffer sets as the groups: what "peak"
+    means in practice next to the nominal 8 TB/s."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = (512 << 20) // 4
+    cases = [
+        ("read (torch.sum, f32)", lambda a, o: torch.sum(a, dim=0, out=o), lambda: [torch.randn(n, device=dev), torch.empty((), device=dev)], n * 4),
+        ("write (fill_, f32)", lambda a: a.fill_(1.5), lambda: [torch.empty(n, device=dev)], n * 4),
+        ("copy (copy_, f32)", lambda a, b: b.copy_(a), lambda: [torch.randn(n // 2, device=dev), torch.empty(n // 2, device=dev)], n * 4),
+        ("a + b (torch.add, f32)", lambda a, b, o: torch.add(a, b, out=o),
+         lambda: [torch.randn(n // 3, device=dev), torch.randn(n // 3, device=dev), torch.empty(n // 3, device=dev)], (n // 3) * 12),
+    ]
+    lines = ["# HBM rates of PyTorch's own streaming kernels on one MI355X (nominal peak 8 TB/s)",
+             f"# command: {command}" if command else "# command: python bench.py --ceilings OUT",
+             "# case                       us/launch   TB/s   of 8 TB/s"]
+    for name, fn, make, nbytes in cases:
+        log(f"[bench] ceiling: {name}")
+        sets = input_sets(make())
+        us = time_group(fn, sets, steps, warmup)[0] / steps * 1e3
+        lines.append(f"{name:28s} {us:9.2f} {nbytes / us / 1e6:6.2f}   {nbytes / us / 1e6 / 8:.3f}")
+        del sets
+        torch.cuda.empty_cache()
+    text = "\n".join(lines) + "\n"
+    if out == "-":
+        sys.stdout.write(text)
+    else:
+        with open(out, "w") as f:
+            f.write(text)
+
+
 def traffic_table():
     f = os.path.join(REPO, "profiles", "hbm_traffic.txt")
     t = {}
@@ -420,7 +454,12 @@ def main():
     ap.add_argument("--command", default="", help="the profiling command, recorded in the summary")
     ap.add_argument("--vendor", metavar="OUT", default=None,
                     help="time each group against its eager PyTorch/hipBLASLt equivalent, write a table to OUT")
+    ap.add_argument("--ceilings", metavar="OUT", default=None,
+                    help="time PyTorch's own streaming kernels (read/write/copy/add), write a table to OUT")
     args = ap.parse_args()
+    if args.ceilings:
+        ceilings_report(args.ceilings, args.steps, args.warmup, args.command)
+        return
     if args.summarize_stats:
         summarize_stats(*args.summarize_stats, args.command)
         return
