@@ -604,7 +604,10 @@ __device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char 
   }
   __syncthreads();
   if constexpr (ESZ == 1) {
-    const int c4 = threadIdx.x % 32, rb = threadIdx.x / 32; // columns 4 c4 .. +3, rows 16 rb .. +15
+    // columns 4 c4 .. +3, rows 16 rb .. +15; eight consecutive lanes (rb) hold
+    // one destination row's 128 bytes, so each 16-byte store instruction
+    // writes whole lines
+    const int rb = threadIdx.x % 8, c4 = threadIdx.x / 8;
     uint32_t d[16];
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) d[rr] = *reinterpret_cast<const uint32_t *>(&tile[16 * rb + rr][4 * c4]);
