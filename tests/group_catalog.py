@@ -909,6 +909,26 @@ SORT_OPS = [("sort_1d_asc", "f32", [6], False), ("sort_2d_asc", "f32", [4, 4], F
             ("sort_i32_desc", "i32", [50, 3], True), ("sort_f32_len1", "f32", [100, 1], False)]
 
 
+def neg_sort_scale(rows=37, cols=300):
+    """An un-fused host function y = 2 * sort(-x) (descending) along the last
+    axis: the front-end outlines the sort as a kernel of its own between two
+    elementwise groups."""
+    X = _T([rows, cols], "f32")
+    return f"""module {{
+  func.func @neg_sort_scale(%x: {X}) -> {X}
+      attributes {{hacc.function_kind = #hacc.function_kind<HOST>}} {{
+    %e0 = tensor.empty() : {X}
+    %a = linalg.elemwise_unary {{fun = #linalg.unary_fn<negf>}} ins(%x : {X}) outs(%e0 : {X}) -> {X}
+    %s = hfusion.sort ins(%a : {X}) descending = true sort_axis = 1 -> {X}
+    %c = arith.constant 2.000000e+00 : f32
+    %e1 = tensor.empty() : {X}
+    %b = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%s, %c : {X}, f32) outs(%e1 : {X}) -> {X}
+    return %b : {X}
+  }}
+}}
+"""
+
+
 def sort_ops():
     """One module, one group per hfusion.sort case."""
     funcs = []
@@ -975,6 +995,7 @@ def entries():
     e["any_pbr_ops"] = any_pbr_ops()
     e["transpose_ops"] = transpose_ops()
     e["sort_ops"] = sort_ops()
+    e["prog_neg_sort_scale"] = neg_sort_scale()
     # dynamic row counts (compiled per size: DynamicGroup / option dyn=...)
     e["rmsnorm_quant_dyn"] = g.with_dynamic_rows(g.rmsnorm_quant(7919, 4096), 7919)
     e["softmax_dyn"] = g.with_dynamic_rows(g.safe_softmax(7919, 1000), 7919)

@@ -11,6 +11,7 @@ import hfusion_mi355x as hf
 import group_catalog as cat
 from helpers import run_gpu, run_oracle
 from oracle import interp
+from test_fusion import outline
 
 SPEC = {s[0]: s for s in cat.SORT_OPS}
 FLOATS = ("f32", "f16", "bf16")
@@ -181,4 +182,29 @@ def test_sort_gpu_all_nan_and_sorted_rows(gpu):
     x[3, ::2] = -0.0
     got, = run_gpu("sort_ops", [x], gpu, func=name)
     want, = run_oracle("sort_ops", [x], func=name)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_sort_program_outlined(tmp_path):
+    """2 * sort(-x): the sort becomes a group of its own between the two
+    elementwise groups, and the whole function on the oracle matches the
+    closed form."""
+    groups, progs, _ = outline(cat.get("prog_neg_sort_scale"), tmp_path)
+    assert [ops for _, _, ops in groups] == [["elemwise_unary"], ["sort"], ["elemwise_binary"]]
+    rng = np.random.default_rng(3)
+    x = values("f32", (37, 300), rng)
+    got, = run_oracle("prog_neg_sort_scale", [x])
+    with np.errstate(invalid="ignore"):
+        want = (closed_form((-x).astype(np.float32), "f32", True) * np.float32(2)).astype(np.float32)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+
+
+@pytest.mark.gpu
+def test_sort_program_gpu(gpu):
+    note("prog_neg_sort_scale")
+    rng = np.random.default_rng(4)
+    x = values("f32", (37, 300), rng)
+    got, = run_gpu("prog_neg_sort_scale", [x], gpu)
+    want, = run_oracle("prog_neg_sort_scale", [x])
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
