@@ -2290,11 +2290,15 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   // operand stored the other way round (B [K, N], A [K, M]) is first copied
   // K-contiguous into the workspace by a transpose kernel of its own, when
   // the DMA ring applies; otherwise the register-staging path reads it as is.
-  const int dma = (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
-  const bool preB = dma != 0 && !bT, preA = dma != 0 && aT;
-  const bool kT = dma != 0 || bT;          // the main kernel's B is [N, K]
+  // An int8 B [K, N] with 128-byte K slices goes through the ring as it is
+  // (mode 4): whole 256-byte k-rows are staged and the matrix-core operand is
+  // formed by transposing LDS reads, so no re-layout pass is needed.
+  const int dma0 = (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
+  const int dma = dma0 == 3 && i8 && !bT && !aT && N % 16 == 0 ? 4 : dma0;
+  const bool preB = dma != 0 && dma != 4 && !bT, preA = dma != 0 && aT;
+  const bool kT = (dma != 0 && dma != 4) || bT; // the main kernel's B is [N, K]
   const bool mT = dma == 0 && aT;          // the main kernel's A is [K, M]
-  const int threads = dma == 3 ? 512 : 256;
+  const int threads = dma >= 3 ? 512 : 256;
   auto align256 = [](uint64_t v) { return (v + 255) / 256 * 256; };
   const uint64_t wsB = preB ? align256((uint64_t)(N * K * esz)) : 0, wsA = preA ? align256((uint64_t)(M * K * esz)) : 0;
   if (!hivm) {
@@ -2433,7 +2437,8 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   p.variant = std::string(mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
               (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") +
               (preA || preB ? " (re-laid K-contiguous by a transpose kernel)" : "") +
-              (dma == 3 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD)" : dma == 1 ? ", LDS DMA ring" : ", register staging");
+              (dma == 4 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD; B k-rows staged whole, transposing LDS reads)" :
+               dma == 3 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD)" : dma == 1 ? ", LDS DMA ring" : ", register staging");
   p.algoOps = 2.0 * (double)M * (double)N * (double)K;
   return p;
 }

@@ -482,9 +482,19 @@ constexpr int MMD2_SLICE = 256 * 128;
 // registers): while one wave of a SIMD waits on memory, the other issues
 // MFMAs.  Ring: two stages of 128-byte K slices, swizzled as described above;
 // each wave issues 8 DMAs per stage (its 32 rows of A and of B).
-template <int MK, typename Epi, typename ElemT, typename Args>
+// BKN: B is [K, N] (linalg.matmul, int8): a stage of B is 128 k-rows x 256
+// columns, each DMA instruction 4 whole 256-byte k-rows, kept K-major in LDS
+// (granule g of k-row r at position g ^ kn_swz(r), so the 8 k-rows x 2
+// granules one half-wave reads sit on 16 different positions).  A B fragment is read with
+// two ds_read_b64_tr_b8: in each group of 16 lanes, lane i's byte b comes from
+// the 8 bytes addressed by lane 2b + i/8, byte i % 8; so lane j addressing
+// k-row k0 + j/2 at column c0 + 8 (j % 2) gives lane i the column c0 + i at
+// k-rows k0 .. k0+7 -- eight consecutive k-bytes of one column, as the matrix
+// core takes them.
+template <int MK, typename Epi, bool BKN, typename ElemT, typename Args>
 __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
                              int64_t M, int64_t N, int64_t K, const Args &P) {
+  static_assert(!BKN || (MK == MK_I8 && sizeof(ElemT) == 1), "the [K, N] B path takes int8");
   using Op = MfmaOp<MK>;
   using acc_t = typename Op::acc_t;
   constexpr int ESZ = sizeof(ElemT);
@@ -499,6 +509,7 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)&lds[0][0][0];
   const char *Ab = reinterpret_cast<const char *>(A), *Bb = reinterpret_cast<const char *>(B);
   const int nsteps = (int)(Kb / 128);
+  auto kn_swz = [](int kr) { return ((kr & 7) << 1) | ((kr >> 3) & 1); };
 
   // DMA d (0..7) of K slice s into ring slot `slot`: d < 4 this wave's A
   // rows (32 * wave ..), else its B rows, 8 rows per instruction
@@ -507,6 +518,16 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     const int blk = wave * 4 + (d & 3);
     const int r = 8 * blk + lane / 8;
     const int g = (lane % 8) ^ ((r >> 1) & 7);
+    if (BKN && d >= 4) {
+      // 4 k-rows of 256 columns: lane l fills position l % 16 of k-row
+      // 4 blk + l / 16 with logical granule (l % 16) ^ kn_swz(k-row)
+      const int kr = 4 * blk + lane / 16;
+      const int gg = (lane % 16) ^ kn_swz(kr);
+      int64_t col = n0 + 16 * gg;
+      col = col + 16 <= N ? col : N - 16; // columns past N: any valid bytes (masked later)
+      mmd_dma16(Bb + ((int64_t)s * 128 + kr) * N + col, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+      return;
+    }
     const int64_t rows = d < 4 ? M : N, row0 = d < 4 ? m0 : n0;
     int64_t row = row0 + r;
     row = row < rows ? row : rows - 1;
@@ -527,6 +548,23 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     const int r = blk * 32 + lane % 32;
     return *reinterpret_cast<const v4i *>(slice + (8 * r + (g ^ ((r >> 1) & 7))) * 16);
   };
+  // B fragment from the K-major slice: 32 columns blk * 32 .., k-block kb
+  auto frag_kn = [&](const char *slice, int blk, int kb) -> v4i {
+    const int q = lane / 16, j = lane % 16;
+    const int col = blk * 32 + 16 * (q % 2) + 8 * (j % 2);
+    v4i r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kr = kb * 32 + 16 * (q / 2) + 8 * h + j / 2;
+      const int pos = kr * 256 + (((col >> 4) ^ kn_swz(kr)) << 4) + (col & 15);
+      typedef int v2i_ __attribute__((ext_vector_type(2)));
+      const v2i_ t = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (__attribute__((address_space(3))) v2i_ *)(uintptr_t)((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char *)slice + pos));
+      r[2 * h] = t.x;
+      r[2 * h + 1] = t.y;
+    }
+    return r;
+  };
   // the 12 fragments (2 k-blocks x (4 A + 2 B)) of half h of stage s
   auto fetch = [&](int s, int h, v4i (&f)[2][6]) {
     const char *la = lds[s & 1][0], *lb = lds[s & 1][1];
@@ -535,7 +573,8 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
 #pragma unroll
       for (int i = 0; i < 4; ++i) f[q][i] = frag(la, wm * 4 + i, 4 * h + 2 * q + lane / 32);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) f[q][4 + j] = frag(lb, wn * 2 + j, 4 * h + 2 * q + lane / 32);
+      for (int j = 0; j < 2; ++j)
+        f[q][4 + j] = BKN ? frag_kn(lb, wn * 2 + j, 2 * h + q) : frag(lb, wn * 2 + j, 4 * h + 2 * q + lane / 32);
     }
   };
 
@@ -649,13 +688,15 @@ __device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char 
 // [N, K] with BT (the weight layout) or [K, N]; DMA selects the LDS DMA ring:
 // 0 none (register staging), 1 with 64-byte K slices (256 threads), 3 with
 // 128-byte slices and two waves per SIMD (512 threads); both require !AT, BT
-// and K spanning a multiple of 64 resp. 128 bytes.
+// and K spanning a multiple of 64 resp. 128 bytes; 4 as 3 with an int8 B
+// [K, N] (!BT, N a multiple of 16) read K-major from LDS by transposing reads.
 template <int MK, typename Epi, bool AT, bool BT, int DMA, typename ElemT, typename Args>
 __device__ __forceinline__ void mmad(const ElemT *A, const ElemT *B, typename Epi::out_t *out, int64_t M, int64_t N, int64_t K,
                                      const Args &P) {
-  static_assert(DMA == 0 || (!AT && BT), "the DMA ring takes K-contiguous A and B");
-  static_assert(DMA == 0 || DMA == 1 || DMA == 3, "DMA mode");
-  if constexpr (DMA == 3) mmad_core_pp<MK, Epi>(A, B, out, M, N, K, P);
+  static_assert(DMA == 0 || (!AT && (BT || DMA == 4)), "the DMA ring takes K-contiguous A (and B unless DMA 4)");
+  static_assert(DMA == 0 || DMA == 1 || DMA == 3 || DMA == 4, "DMA mode");
+  if constexpr (DMA == 4) mmad_core_pp<MK, Epi, true>(A, B, out, M, N, K, P);
+  else if constexpr (DMA == 3) mmad_core_pp<MK, Epi, false>(A, B, out, M, N, K, P);
   else if constexpr (DMA == 1) mmad_core_dma<MK, Epi>(A, B, out, M, N, K, P);
   else mmad_core<MK, Epi, AT, BT>(A, B, out, M, N, K, P);
 }

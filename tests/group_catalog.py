@@ -962,6 +962,9 @@ def entries():
     e["w8a8_ragged_dma"] = g.w8a8_dequant(300, 200, 192)
     e["w8a8_ragged_dma128"] = g.w8a8_dequant(300, 200, 384)
     e["w8a8_kn"] = g.w8a8_dequant(320, 256, 128, b_layout="kn")
+    e["w8a8_kn_ragged"] = g.w8a8_dequant(300, 208, 384, b_layout="kn")
+    e["w8a8_kn_wide"] = g.w8a8_dequant(264, 784, 256, b_layout="kn")
+    e["w8a8_kn_dma64"] = g.w8a8_dequant(300, 208, 192, b_layout="kn")
     e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
     e["bf16_mmad_ragged128"] = g.bf16_mmad(200, 136, 192)
     e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)

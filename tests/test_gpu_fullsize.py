@@ -99,8 +99,8 @@ def test_w8a8_dequant_full_sampled(gpu):
 
 
 def test_w8a8_dequant_kn_full_sampled(gpu):
-    """W8A8 with B stored [K, N] (linalg.matmul): the group re-lays B
-    K-contiguous with a transpose kernel, then runs the DMA-ring contraction;
+    """W8A8 with B stored [K, N] (linalg.matmul): the DMA ring stages whole
+    k-rows of B and forms the matrix-core operand with transposing LDS reads;
     64 sampled rows bit-exact against the oracle fed B^T."""
     note("w8a8_dequant_kn full 4096^3 (B [K,N]), 64 sampled rows")
     kw = CFG["w8a8_dequant"]["kw"]

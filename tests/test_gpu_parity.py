@@ -122,11 +122,12 @@ def test_argmax_repeat_launch(gpu):
 # ------------------------------------------------------------------ W8A8
 @pytest.mark.parametrize("name,m,n,k", [("w8a8_512", 512, 512, 512), ("w8a8_ragged", 300, 200, 160),
                                         ("w8a8_ragged_dma", 300, 200, 192), ("w8a8_ragged_dma128", 300, 200, 384),
-                                        ("w8a8_kn", 320, 256, 128)])
+                                        ("w8a8_kn", 320, 256, 128), ("w8a8_kn_ragged", 300, 208, 384),
+                                        ("w8a8_kn_wide", 264, 784, 256), ("w8a8_kn_dma64", 300, 208, 192)])
 def test_w8a8(gpu, name, m, n, k):
     note(name)
     a, b, st, sc = I.config_inputs("w8a8_dequant", m=m, n=n, k=k)
-    if name.endswith("_kn"):
+    if "_kn" in name:
         b = np.ascontiguousarray(b.T)   # the same weights in the [K, N] layout
     args = [a, b, st, sc, zeros((m, n), np.uint16)]
     out, = run_gpu(name, args, gpu)
