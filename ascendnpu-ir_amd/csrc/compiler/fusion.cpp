@@ -55,7 +55,9 @@ Pat patternOf(const Op *op) {
     if (op->dims.size() != 1 || op->ins.empty()) return Pat::OB;
     return (size_t)op->dims[0] == rankOf(op->ins[0]) ? Pat::LB : Pat::OB;
   }
-  if (n == "linalg.matmul" || n == "linalg.matmul_transpose_a" || n == "linalg.matmul_transpose_b") return Pat::MM;
+  if (n == "linalg.matmul" || n == "linalg.matmul_transpose_a" || n == "linalg.matmul_transpose_b" ||
+      n == "hfusion.matmul_mx")
+    return Pat::MM;
   if (n == "linalg.transpose") return Pat::TR;
   if (n == "tensor.expand_shape" || n == "tensor.collapse_shape") return Pat::RS;
   if (n == "tensor.empty") return Pat::Buffer;

@@ -34,6 +34,7 @@ struct Type {
   bool tensor = false;
   bool memref = false; // a memref<...> (read as a tensor of the same shape)
   Elem elem = Elem::None;
+  bool uns = false;           // written ui8: bytes read unsigned (matmul_mx scales only)
   std::vector<int64_t> shape; // tensor only
   int64_t numel() const {
     int64_t n = 1;

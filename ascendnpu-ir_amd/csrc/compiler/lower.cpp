@@ -1035,7 +1035,8 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
 std::string resultKind(const Func &f, bool *hasMatmul, bool *hasRWI, bool *hasReduce) {
   *hasMatmul = *hasRWI = *hasReduce = false;
   for (const Op *op : f.ops) {
-    if (op->name == "linalg.matmul" || op->name == "linalg.matmul_transpose_b" || op->name == "hivm.hir.matmul")
+    if (op->name == "linalg.matmul" || op->name == "linalg.matmul_transpose_b" || op->name == "hivm.hir.matmul" ||
+        op->name == "hfusion.matmul_mx")
       *hasMatmul = true;
     if (op->name == "hfusion.reduce_with_index") *hasRWI = true;
     if (op->name == "linalg.reduce") *hasReduce = true;
@@ -2259,12 +2260,25 @@ void hivmMatmulEpilogue(const Op *mm, bool intAcc, std::ostringstream &epi, std:
 KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   Func &f = *A.f;
   const Op *mm = findOp(f, [](const Op *o) {
-    return o->name == "linalg.matmul" || o->name == "linalg.matmul_transpose_b" || o->name == "hivm.hir.matmul";
+    return o->name == "linalg.matmul" || o->name == "linalg.matmul_transpose_b" || o->name == "hivm.hir.matmul" ||
+           o->name == "hfusion.matmul_mx";
   });
   const bool hivm = mm->name == "hivm.hir.matmul";
+  const bool mx = mm->name == "hfusion.matmul_mx";
   const bool bT = hivm ? mm->attrs.count("b_transpose") != 0 : mm->name == "linalg.matmul_transpose_b";
   const bool aT = hivm && mm->attrs.count("a_transpose") != 0;
-  const Value *a = mm->ins[0], *b = mm->ins[1];
+  // matmul_mx (HFusionOps.td:1233-1291): A [M, K], B [K, N] fp8 (or bytes
+  // reinterpreted by hfusion.bitcast or by lhsFormat / rhsFormat), scales
+  // [M, K/32] and [N, K/32] e8m0
+  const Op *castA = nullptr, *castB = nullptr;
+  auto throughBitcast = [&](const Value *v, const Op *&cast) {
+    if (mx && v->def && v->def->name == "hfusion.bitcast" && !v->def->ins.empty()) {
+      cast = v->def;
+      return (const Value *)v->def->ins[0];
+    }
+    return v;
+  };
+  const Value *a = throughBitcast(mm->ins[0], castA), *b = throughBitcast(mm->ins[1], castB);
   if (a->argIdx < 0 || b->argIdx < 0) unsupported(mm, "matmul operands must be group arguments");
   if (a->type.shape.size() != 2 || b->type.shape.size() != 2) unsupported(mm, "matmul operands must be rank 2");
   int64_t M = aT ? a->type.shape[1] : a->type.shape[0], K = aT ? a->type.shape[0] : a->type.shape[1];
@@ -2272,12 +2286,44 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   if ((bT ? b->type.shape[1] : b->type.shape[0]) != K) unsupported(mm, "matmul shapes");
   Elem ae = a->type.elem, be = b->type.elem;
   int mk = -1;
-  if (ae == Elem::I8 && be == Elem::I8) mk = 0;
+  const Value *sa = nullptr, *sb = nullptr;
+  if (mx) {
+    // the matrix core's format codes: 0 e4m3, 1 e5m2 (HFusionAttrs.td:131-137
+    // numbers them FP8E5M2_T = 1, FP8E4M3_T = 2, FP4E2M1_T = 3)
+    auto fmt = [&](const Value *orig, const char *attr) -> int {
+      const Elem e = orig->type.elem;
+      if (e == Elem::F8E4M3FN) return 0;
+      if (e == Elem::F8E5M2) return 1;
+      if (e == Elem::I8) {
+        auto it = mm->attrs.find(attr);
+        const std::string v = it == mm->attrs.end() ? "" : it->second;
+        if (v.rfind("1", 0) == 0) return 1;
+        if (v.rfind("2", 0) == 0) return 0;
+        if (v.rfind("3", 0) == 0) unsupported(mm, "matmul_mx fp4 (e2m1) operands");
+        unsupported(mm, std::string("matmul_mx byte operand without ") + attr);
+      }
+      unsupported(mm, "matmul_mx operand type (f8E4M3FN, f8E5M2 or bytes with a format)");
+      return -1;
+    };
+    const int fa = fmt(mm->ins[0], "lhsFormat"), fb = fmt(mm->ins[1], "rhsFormat");
+    mk = 3 + 2 * fa + fb;
+    if (mm->ins.size() != 4) unsupported(mm, "matmul_mx takes A, B and two scale operands");
+    sa = mm->ins[2];
+    sb = mm->ins[3];
+    if (sa->argIdx < 0 || sb->argIdx < 0) unsupported(mm, "matmul_mx scales must be group arguments");
+    if (sa->type.elem != Elem::I8 || sb->type.elem != Elem::I8) unsupported(mm, "matmul_mx scales are ui8 / i8 (e8m0)");
+    if (K % 32 != 0 || sa->type.shape != std::vector<int64_t>{M, K / 32} || sb->type.shape != std::vector<int64_t>{N, K / 32})
+      unsupported(mm, "matmul_mx scales must be [M, K/32] and [N, K/32]");
+    if (K % 128 != 0) unsupported(mm, "matmul_mx K must be a multiple of 128");
+    if (N % 16 != 0) unsupported(mm, "matmul_mx N must be a multiple of 16");
+    if (mm->results[0]->type.elem != Elem::F32) unsupported(mm, "matmul_mx accumulates in f32");
+    ae = be = Elem::I8; // bytes from here on
+  } else if (ae == Elem::I8 && be == Elem::I8) mk = 0;
   else if (ae == Elem::BF16 && be == Elem::BF16) mk = 1;
   else if (ae == Elem::F16 && be == Elem::F16) mk = 2;
-  if (mk < 0) unsupported(mm, "matmul element types (supported: i8 x i8, bf16 x bf16, f16 x f16)");
+  if (mk < 0) unsupported(mm, "matmul element types (supported: i8 x i8, bf16 x bf16, f16 x f16, matmul_mx fp8)");
   const bool i8 = mk == 0;
-  if (!hivm) {
+  if (!hivm && !mx) {
     Elem ce = mm->results[0]->type.elem;
     if (ce != (i8 ? Elem::I32 : Elem::F32)) unsupported(mm, "matmul accumulator type (i32 for i8, f32 for bf16/f16)");
   }
@@ -2294,14 +2340,26 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   // (mode 4): whole 256-byte k-rows are staged and the matrix-core operand is
   // formed by transposing LDS reads, so no re-layout pass is needed.
   const int dma0 = (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
-  const int dma = dma0 == 3 && i8 && !bT && !aT && N % 16 == 0 ? 4 : dma0;
+  const int dma = mx ? 4 : dma0 == 3 && i8 && !bT && !aT && N % 16 == 0 ? 4 : dma0;
   const bool preB = dma != 0 && dma != 4 && !bT, preA = dma != 0 && aT;
   const bool kT = (dma != 0 && dma != 4) || bT; // the main kernel's B is [N, K]
   const bool mT = dma == 0 && aT;          // the main kernel's A is [K, M]
   const int threads = dma >= 3 ? 512 : 256;
   auto align256 = [](uint64_t v) { return (v + 255) / 256 * 256; };
   const uint64_t wsB = preB ? align256((uint64_t)(N * K * esz)) : 0, wsA = preA ? align256((uint64_t)(M * K * esz)) : 0;
-  if (!hivm) {
+  // matmul_mx accumulates onto its `outs`: a tensor.empty (taken as zero) or
+  // a constant fill, added after the contraction
+  std::string accInit;
+  if (mx) {
+    const Value *acc0 = mm->outs.empty() ? nullptr : mm->outs[0];
+    if (!acc0 || !acc0->def) unsupported(mm, "matmul_mx accumulator must be a tensor.empty or a constant linalg.fill");
+    if (acc0->def->name == "linalg.fill") {
+      if (!acc0->def->ins[0]->isConst) unsupported(mm, "matmul_mx accumulator fill must be a constant");
+      if (acc0->def->ins[0]->fconst != 0.0) accInit = constExpr(acc0->def->ins[0], Elem::F32);
+    } else if (acc0->def->name != "tensor.empty") {
+      unsupported(mm, "matmul_mx accumulator must be a tensor.empty or a constant linalg.fill");
+    }
+  } else if (!hivm) {
     const Value *acc0 = mm->outs[0];
     if (!(acc0->def && acc0->def->name == "linalg.fill" && acc0->def->ins[0]->isConst && acc0->def->ins[0]->fconst == 0.0))
       unsupported(mm, "matmul accumulator must start from a zero linalg.fill");
@@ -2310,6 +2368,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   }
   // epilogue over D = [M, N] with the matmul result as the accumulator
   std::set<const Value *> excl = {a, b};
+  if (mx) excl.insert({sa, sb, mm->ins[0], mm->ins[1]});
   A.D = {M, N};
   if (!hivm) inferMaps(A, excl);
   // per-element code, plus the operand loads split by their index: [m] once
@@ -2319,7 +2378,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   int tmp = 0;
   auto ensure = [&](const Value *v) {
     if (name.count(v)) return;
-    if (v == mm->results[0]) { name[v] = "acc"; return; }
+    if (v == mm->results[0]) { name[v] = accInit.empty() ? "acc" : "(acc + " + accInit + ")"; return; }
     if (v->isConst || !v->type.tensor) {
       if (v->isConst) name[v] = constExpr(v, v->type.elem);
       else if (v->argIdx >= 0) name[v] = scalarArgExpr(A, v->argIdx);
@@ -2355,7 +2414,9 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   for (const Op *op : f.ops) {
     if (hivm) break;
     const std::string &n = op->name;
-    if (op == mm || n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" || n == "linalg.fill") continue;
+    if (op == mm || op == castA || op == castB || n == "tensor.empty" || n == "arith.constant" || n == "tensor.dim" ||
+        n == "linalg.fill")
+      continue;
     if (n.rfind("arith.", 0) == 0 && !op->results[0]->type.tensor) continue;
     if (n == "linalg.broadcast") {
       ensure(op->ins[0]);
@@ -2411,9 +2472,14 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const std::string et = i8 ? "int8_t" : "uint16_t";
   const std::string aPtr = preA ? "(const " + et + "*)((char*)ws + " + std::to_string(wsB) + ")" : "(const " + et + "*)p" + std::to_string(a->argIdx);
   const std::string bPtr = preB ? "(const " + et + "*)ws" : "(const " + et + "*)p" + std::to_string(b->argIdx);
-  k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (mT ? "true" : "false") << ", " << (kT ? "true" : "false") << ", "
-    << dma << ">(" << aPtr << ", " << bPtr << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K
-    << "ll, P);\n}\n";
+  if (mx)
+    k << "  hf::mmad_mx<" << mk << ", " << kname << "_epi>((const uint8_t*)p" << a->argIdx << ", (const uint8_t*)p" << b->argIdx
+      << ", (const uint8_t*)p" << sa->argIdx << ", (const uint8_t*)p" << sb->argIdx << ", (" << mtype(oe) << "*)"
+      << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
+  else
+    k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (mT ? "true" : "false") << ", " << (kT ? "true" : "false") << ", "
+      << dma << ">(" << aPtr << ", " << bPtr << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N
+      << "ll, " << K << "ll, P);\n}\n";
   // the re-layout kernels: [K, X] -> [X, K], 128 x 128-byte tiles
   auto preKernel = [&](const char *suffix, const Value *src, int64_t X, uint64_t off) {
     KernelPlan::PreKernel pk;
@@ -2434,7 +2500,9 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const int64_t TM = 256, TN = 256;
   p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
   p.block[0] = (unsigned)threads;
-  p.variant = std::string(mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
+  static const char *mxName[4] = {"e4m3 x e4m3", "e4m3 x e5m2", "e5m2 x e4m3", "e5m2 x e5m2"};
+  p.variant = std::string(mx ? std::string("mfma_scale_f32_32x32x64_f8f6f4 (") + mxName[mk - 3] + ", e8m0 scales per 32 k)"
+                          : mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
               (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") +
               (preA || preB ? " (re-laid K-contiguous by a transpose kernel)" : "") +
               (dma == 4 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD; B k-rows staged whole, transposing LDS reads)" :
@@ -3614,6 +3682,14 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
         for (Value *b : written) f.returns.push_back(latest[b]);
     }
     splitGenericReductions(m, f);
+    // ui8 is read as raw bytes: only matmul_mx's e8m0 scales may be ui8
+    for (const Op *op : f.ops) {
+      if (op->name == "hfusion.matmul_mx" || op->name == "func.return") continue;
+      for (const Value *v : op->ins)
+        if (v->type.uns) unsupported(op, "ui8 operand outside matmul_mx scales");
+      for (const Value *v : op->operands)
+        if (v->type.uns) unsupported(op, "ui8 operand outside matmul_mx scales");
+    }
     describeBuffers(A);
     std::string kname = "hf_" + f.name;
     KernelPlan p;

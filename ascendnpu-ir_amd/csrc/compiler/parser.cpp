@@ -231,7 +231,8 @@ Type parseTypeText(const std::string &s, int line) {
     if (e.find('?') != std::string::npos)
       throw CompileError("unsupported dynamic type '" + s + "' at line " + std::to_string(line));
     try {
-      ty.elem = parseElem(e);
+      if (e == "ui8") ty.uns = true;
+      ty.elem = parseElem(e == "ui8" ? "i8" : e);
     } catch (CompileError &) {
       throw CompileError("unsupported tensor type '" + s + "' at line " +
                          std::to_string(line));

@@ -35,7 +35,10 @@ constexpr int MM_LDS_STRIDE = MM_BK + 16;             // 80 B rows: conflict-fre
 
 // Matrix-core kinds: int8 -> int32, bf16 -> fp32, f16 -> fp32 (32x32 tiles;
 // each lane feeds 16 bytes of A and of B per instruction, 32 bytes of K).
-enum MmadKind : int { MK_I8 = 0, MK_BF16 = 1, MK_F16 = 2 };
+// MK_MX + 2 * fa + fb: block-scaled fp8 (fa, fb: 0 e4m3, 1 e5m2, the
+// matrix core's format codes), 32 k per e8m0 scale
+enum MmadKind : int { MK_I8 = 0, MK_BF16 = 1, MK_F16 = 2, MK_MX = 3 };
+constexpr bool mk_is_mx(int mk) { return mk >= MK_MX && mk < MK_MX + 4; }
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 template <int MK> struct MfmaOp;
@@ -53,6 +56,22 @@ template <> struct MfmaOp<MK_BF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
   }
 };
+typedef int v8i __attribute__((ext_vector_type(8)));
+// v_mfma_scale_f32_32x32x64_f8f6f4.  Operand layout (measured on gfx950):
+// lane l holds row (col) l % 32; its bytes 0-15 are k = 16 (l / 32) + 0..15
+// and bytes 16-31 are k = 32 + 16 (l / 32) + 0..15 of the 64; the scale
+// byte of lane l applies to row (col) l % 32 at k = 32 (l / 32) .. +31, i.e.
+// to bytes 0-15 of lanes 32 (l / 32) / 32 and bytes 16-31 alike.  SEL picks
+// the byte of the scale register.
+template <int MK> struct MfmaMx {
+  static_assert(mk_is_mx(MK), "block-scaled kind");
+  using acc_t = v16f;
+  template <int SEL>
+  __device__ __forceinline__ static acc_t run(v8i a, v8i b, acc_t c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, (MK - MK_MX) / 2, (MK - MK_MX) % 2, SEL, sa, SEL, sb);
+  }
+};
+__device__ __forceinline__ v8i mx_cat(v4i lo, v4i hi) { return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}; }
 template <> struct MfmaOp<MK_F16> {
   using acc_t = v16f;
   using scalar_t = float;
@@ -329,6 +348,10 @@ __device__ __forceinline__ void mmd_dma16(const void *g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory");
 }
 
+// 4 bytes per lane into LDS at M0 + 4 * lane
+__device__ __forceinline__ void mmd_dma4(const void *g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr) : "memory");
+}
 template <int N> __device__ __forceinline__ void mmd_wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
 // Issues this wave's 4 DMA instructions (rows 64*wave .. +63) of one operand
@@ -491,14 +514,25 @@ constexpr int MMD2_SLICE = 256 * 128;
 // k-row k0 + j/2 at column c0 + 8 (j % 2) gives lane i the column c0 + i at
 // k-rows k0 .. k0+7 -- eight consecutive k-bytes of one column, as the matrix
 // core takes them.
+// Block-scaled fp8 (MK_MX..): B [K, N] as above; SA [M, K/32] and SB
+// [N, K/32] hold the e8m0 scales.  One 128-byte slice is 2 scaled MFMAs of
+// 64 k per tile, each taking the int8 path's fragments of two k-blocks.  The
+// slice's scales (bytes 4s .. 4s+3 of each row: 1 KB for the tile's 256 A
+// rows, 1 KB for its 256 B columns) ride the same ring, one 4-byte-per-lane
+// DMA per wave per stage, so every load of a stage is covered by the ring's
+// own wait.
 template <int MK, typename Epi, bool BKN, typename ElemT, typename Args>
 __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
-                             int64_t M, int64_t N, int64_t K, const Args &P) {
-  static_assert(!BKN || (MK == MK_I8 && sizeof(ElemT) == 1), "the [K, N] B path takes int8");
-  using Op = MfmaOp<MK>;
+                             int64_t M, int64_t N, int64_t K, const Args &P, const uint8_t *__restrict__ SA = nullptr,
+                             const uint8_t *__restrict__ SB = nullptr) {
+  constexpr bool MX = mk_is_mx(MK);
+  static_assert(!BKN || ((MK == MK_I8 || MX) && sizeof(ElemT) == 1), "the [K, N] B path takes bytes");
+  static_assert(!MX || BKN, "block-scaled operands come with B [K, N]");
+  using Op = typename std::conditional<MX, MfmaMx<(MX ? MK : MK_MX)>, MfmaOp<(MX ? MK_I8 : MK)>>::type;
   using acc_t = typename Op::acc_t;
   constexpr int ESZ = sizeof(ElemT);
   __shared__ __attribute__((aligned(1024))) char lds[2][2][MMD2_SLICE]; // [stage][A/B]
+  __shared__ __attribute__((aligned(1024))) uint32_t lds_sc[MX ? 2 : 1][2][MX ? 256 : 1]; // [stage][A/B][row]
   const int tmt = (int)((M + MM_TM - 1) / MM_TM), tnt = (int)((N + MM_TN - 1) / MM_TN);
   int ti, tj;
   mm_tile_of(blockIdx.x, tmt, tnt, ti, tj);
@@ -506,6 +540,7 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   const int64_t Kb = K * ESZ;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int wm = wave / 4, wn = wave % 4; // waves w and w+4 share a SIMD
+  constexpr int DPS = MX ? 9 : 8;         // DMA instructions per wave per stage
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)&lds[0][0][0];
   const char *Ab = reinterpret_cast<const char *>(A), *Bb = reinterpret_cast<const char *>(B);
   const int nsteps = (int)(Kb / 128);
@@ -533,9 +568,23 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     row = row < rows ? row : rows - 1;
     mmd_dma16((d < 4 ? Ab : Bb) + row * Kb + (int64_t)s * 128 + g * 16, __builtin_amdgcn_readfirstlane(st + blk * 1024));
   };
+  // the scales of K slice s: wave w carries 64 rows (w < 4: A rows 64 w ..,
+  // else B columns 64 (w - 4) ..), 4 bytes each
+  const uint32_t lds_sc0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t *)&lds_sc[0][0][0];
+  auto issue_scales = [&](int s, int slot) {
+    if constexpr (MX) {
+      const int op = wave / 4, r = 64 * (wave % 4) + lane;
+      const int64_t rows = op ? N : M, row0 = op ? n0 : m0;
+      int64_t row = row0 + r;
+      row = row < rows ? row : rows - 1;
+      mmd_dma4((op ? SB : SA) + row * (K / 32) + 4 * (int64_t)s,
+               __builtin_amdgcn_readfirstlane(lds_sc0 + (uint32_t)((slot * 2 + op) * 1024 + 256 * (wave % 4))));
+    }
+  };
   auto issue_stage = [&](int s) {
 #pragma unroll
     for (int d = 0; d < 8; ++d) issue_one(s < nsteps ? s : nsteps - 1, s & 1, d);
+    issue_scales(s < nsteps ? s : nsteps - 1, s & 1);
   };
 
   acc_t acc[4][2];
@@ -578,6 +627,16 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     }
   };
 
+  // this lane's scale words for stage s, shifted so that byte 2h is the scale
+  // of its k-half in half h of the slice
+  uint32_t sa_w[4], sb_w[2];
+  auto read_scales = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sa_w[i] = lds_sc[MX ? (s & 1) : 0][0][MX ? wm * 128 + i * 32 + lane % 32 : 0] >> (8 * (lane / 32));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sb_w[j] = lds_sc[MX ? (s & 1) : 0][1][MX ? (wn * 2 + j) * 32 + lane % 32 : 0] >> (8 * (lane / 32));
+  };
+
   // Step s: wait for stage s (stage s+1 may be in flight); multiply its first
   // half while reading the second half's fragments; after a barrier (all of
   // stage s is in registers everywhere) issue stage s+2 into the freed slot
@@ -588,28 +647,57 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
 #pragma unroll 1
   for (int s = 0; s < nsteps; ++s) {
     __builtin_amdgcn_sched_barrier(0);
-    mmd_wait_vm<8>();
+    mmd_wait_vm<DPS>();
     __syncthreads();
     fetch(s, 0, f0);
-    fetch(s, 1, f1);
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
+    if constexpr (!MX) fetch(s, 1, f1);
+    if constexpr (MX) {
+      // the second half's fragments are read after the first half's MFMAs
+      // are issued: a scaled MFMA takes its operands as 8-register tuples,
+      // and a whole slice of them beside the scales does not fit the 128
+      // VGPRs left next to the accumulators
+      read_scales(s);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Op::run(f0[q][i], f0[q][4 + j], acc[i][j]);
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = Op::template run<0>(mx_cat(f0[0][i], f0[1][i]), mx_cat(f0[0][4 + j], f0[1][4 + j]), acc[i][j],
+                                          (int)sa_w[i], (int)sb_w[j]);
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(s, 1, f1);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = Op::run(f0[q][i], f0[q][4 + j], acc[i][j]);
+    }
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads(); // every wave holds stage s in registers: its slot is free
     const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
+    if constexpr (MX) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_sched_barrier(0);
-        issue_one(s2, s & 1, q * 4 + i);
+        for (int j = 0; j < 2; ++j) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue_one(s2, s & 1, i * 2 + j);
+          acc[i][j] = Op::template run<2>(mx_cat(f1[0][i], f1[1][i]), mx_cat(f1[0][4 + j], f1[1][4 + j]), acc[i][j],
+                                          (int)sa_w[i], (int)sb_w[j]);
+        }
+      issue_scales(s2, s & 1);
+    } else {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Op::run(f1[q][i], f1[q][4 + j], acc[i][j]);
-      }
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue_one(s2, s & 1, q * 4 + i);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = Op::run(f1[q][i], f1[q][4 + j], acc[i][j]);
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
   mmd_wait_vm<0>();
@@ -696,9 +784,19 @@ __device__ __forceinline__ void mmad(const ElemT *A, const ElemT *B, typename Ep
   static_assert(DMA == 0 || (!AT && (BT || DMA == 4)), "the DMA ring takes K-contiguous A (and B unless DMA 4)");
   static_assert(DMA == 0 || DMA == 1 || DMA == 3 || DMA == 4, "DMA mode");
   if constexpr (DMA == 4) mmad_core_pp<MK, Epi, true>(A, B, out, M, N, K, P);
+  else if constexpr (mk_is_mx(MK)) static_assert(DMA == 4, "block-scaled kinds run on the [K, N] ring");
   else if constexpr (DMA == 3) mmad_core_pp<MK, Epi, false>(A, B, out, M, N, K, P);
   else if constexpr (DMA == 1) mmad_core_dma<MK, Epi>(A, B, out, M, N, K, P);
   else mmad_core<MK, Epi, AT, BT>(A, B, out, M, N, K, P);
+}
+
+// Block-scaled fp8 contraction: A [M, K], B [K, N] (bytes of the formats
+// MK encodes), SA [M, K/32], SB [N, K/32] e8m0; K a multiple of 128, N of 16.
+template <int MK, typename Epi, typename Args>
+__device__ __forceinline__ void mmad_mx(const uint8_t *A, const uint8_t *B, const uint8_t *SA, const uint8_t *SB,
+                                        typename Epi::out_t *out, int64_t M, int64_t N, int64_t K, const Args &P) {
+  static_assert(mk_is_mx(MK), "block-scaled kind");
+  mmad_core_pp<MK, Epi, true>(A, B, out, M, N, K, P, SA, SB);
 }
 
 } // namespace hf

@@ -410,6 +410,55 @@ def exp_cumsum_scale(rows=64, cols=1000):
 """
 
 
+def matmul_mx(m=4096, n=4096, k=4096, fa="e4m3", fb="e4m3", via="fp8", init=None, out="f32", name="matmul_mx"):
+    """Block-scaled fp8 contraction (hfusion.matmul_mx, HFusionOps.td:1233-1291):
+    C = init + (A * 2^(sa-127)) x (B * 2^(sb-127)), A [M, K], B [K, N],
+    e8m0 scales sa [M, K/32] and sb [N, K/32] (ui8).  `via` is how the fp8
+    operands arrive: typed ("fp8"), as bytes through hfusion.bitcast
+    ("bitcast", the form of the reference's conversion tests), or as bytes
+    with lhsFormat / rhsFormat ("format").  init None accumulates onto a
+    tensor.empty (zero); a number fills the accumulator first.  out "bf16"
+    adds a cast epilogue."""
+    ty = {"e4m3": "f8E4M3FN", "e5m2": "f8E5M2"}
+    code = {"e5m2": 1, "e4m3": 2}
+    FA, FB = _t([m, k], ty[fa]), _t([k, n], ty[fb])
+    IA, IB = _t([m, k], "i8"), _t([k, n], "i8")
+    SA, SB = _t([m, k // 32], "ui8"), _t([n, k // 32], "ui8")
+    C, O = _t([m, n], "f32"), _t([m, n], out)
+    pa, pb = (IA, IB) if via in ("bitcast", "format") else (FA, FB)
+    body = []
+    if via == "bitcast":
+        body += [f"%ea = tensor.empty() : {FA}",
+                 f"%a8 = hfusion.bitcast ins(%a : {IA}) outs(%ea : {FA}) -> {FA}",
+                 f"%eb = tensor.empty() : {FB}",
+                 f"%b8 = hfusion.bitcast ins(%b : {IB}) outs(%eb : {FB}) -> {FB}"]
+        xa, xb, ta, tb = "%a8", "%b8", FA, FB
+    else:
+        xa, xb, ta, tb = "%a", "%b", pa, pb
+    body.append(f"%e0 = tensor.empty() : {C}")
+    acc = "%e0"
+    if init is not None:
+        body += [f"%cinit = arith.constant {float(init):e} : f32",
+                 f"%acc0 = linalg.fill ins(%cinit : f32) outs(%e0 : {C}) -> {C}"]
+        acc = "%acc0"
+    attrs = f" {{lhsFormat = {code[fa]} : i32, rhsFormat = {code[fb]} : i32}}" if via != "fp8" else ""
+    body.append(f"%c = hfusion.matmul_mx{attrs} ins({xa}, {xb}, %sa, %sb : {ta}, {tb}, {SA}, {SB}) outs({acc} : {C}) -> {C}")
+    res, rty = "%c", C
+    if out != "f32":
+        body += [f"%e1 = tensor.empty() : {O}",
+                 f"%o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%c : {C}) outs(%e1 : {O}) -> {O}"]
+        res, rty = "%o", O
+    body.append(f"return {res} : {rty}")
+    lines = "\n".join("    " + x for x in body)
+    return f"""module {{
+  func.func @{name}(%a: {pa}, %b: {pb}, %sa: {SA}, %sb: {SB}) -> {rty}
+      {_ATTRS.format(kind='SINGLE_CUBE')} {{
+{lines}
+  }}
+}}
+"""
+
+
 def transpose_cast(rows=4096, cols=8192, src="bf16", dst="f32"):
     """PURE_ELEMWISE group with a transpose: out[j, i] = cast(x[i, j])
     (linalg.transpose permutation [1, 0] fused with hfusion.cast)."""

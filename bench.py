@@ -27,8 +27,10 @@ BF16_PEAK_TFLOPS = 2500.0
 HEADLINE = "rmsnorm_quant"
 ORDER = ["rmsnorm_quant", "vec_add", "safe_softmax", "argmax", "w8a8_dequant"]
 # further groups on the hot path, measured the same way (not BASELINE configs):
-# the bf16 contraction, W8A8 with B as [K, N], a transpose fused with a cast
-EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast"]
+# the bf16 contraction, W8A8 with B as [K, N], a transpose fused with a cast,
+# the block-scaled fp8 contraction (hfusion.matmul_mx)
+EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast", "mx_fp8"]
+FP8_PEAK_TFLOPS = 5000.0  # dense fp8 MFMA (the block-scaled form runs at the same rate)
 
 
 def log(msg):
@@ -41,8 +43,20 @@ def generic_inputs(meta, dev, seed=7):
     import torch
     rng = np.random.default_rng(seed)
     out = []
+    scaled = "e8m0" in meta.get("variant", "")
     for p in meta["params"]:
         shape, elem = tuple(p["shape"]), p["elem"]
+        if elem in ("f8E4M3FN", "f8E5M2") and p["role"] == "in":
+            # every finite code (NaN / inf codes moved to finite neighbours)
+            v = rng.integers(0, 256, shape).astype(np.uint8)
+            v[(v & 0x7F) == 0x7F if elem == "f8E4M3FN" else (v & 0x7C) == 0x7C] &= 0xF7 if elem == "f8E4M3FN" else 0xF3
+            dt = torch.float8_e4m3fn if elem == "f8E4M3FN" else torch.float8_e5m2
+            out.append(torch.from_numpy(v).view(dt).to(dev))
+            continue
+        if scaled and elem == "i8" and p["role"] == "in":
+            # e8m0 block scales around 2^0
+            out.append(torch.from_numpy(rng.integers(120, 135, shape).astype(np.uint8)).view(torch.int8).to(dev))
+            continue
         if p["role"] != "in":
             dt = {"i8": torch.int8, "bf16": torch.bfloat16, "f32": torch.float32, "i32": torch.int32}[elem]
             out.append(torch.empty(shape, dtype=dt, device=dev))
@@ -503,7 +517,9 @@ def main():
             ops = meta["algo_ops"]
             achieved = ops / (kern_ms * 1e-3) / 1e12
             bf16 = "bf16" in meta.get("variant", "")
-            peak, unit = (BF16_PEAK_TFLOPS, "TFLOP/s") if bf16 else (INT8_PEAK_TOPS, "TOPS")
+            fp8 = "mfma_scale" in meta.get("variant", "")
+            peak, unit = ((BF16_PEAK_TFLOPS, "TFLOP/s") if bf16 else (FP8_PEAK_TFLOPS, "TFLOP/s") if fp8
+                          else (INT8_PEAK_TOPS, "TOPS"))
             entry = {"value": ops * args.steps / (total_ms * 1e-3) / 1e12, "unit": unit, "ms_per_step": ms,
                      "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": unit,
                                   "frac": achieved / peak, "traffic": None}}
@@ -536,7 +552,7 @@ def main():
         "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32", "argmax": "f32",
                   "w8a8_dequant": "int8", "w8a8_dequant_kn": "int8", "bf16_mmad": "bf16",
-                  "transpose_cast": "bf16"}[head],
+                  "transpose_cast": "bf16", "mx_fp8": "fp8 (e4m3, e8m0 scales)"}[head],
         "data": "synthetic (seeded splitmix64)",
         "config": {"workload": head, **{k: v for k, v in cfg.items()}},
         "roofline": h["roofline"],

@@ -598,6 +598,37 @@ void hfref_matmul_f32(const float *A, const float *B, float *C, int64_t M,
     }
 }
 
+/* hfusion.matmul_mx (HFusionOps.td:1233-1291): C = C + (A * 2^(sa-127)) x
+ * (B * 2^(sb-127)), A [M, K] and B [K, N] fp8 bytes of formats fa / fb (0
+ * e4m3, 1 e5m2), sa [M, ceil(K/32)] and sb [N, ceil(K/32)] e8m0 bytes, one
+ * per 32 k.  Each scaled operand is rounded to f32, the product is an f32
+ * multiply and the sum runs serially over k from C's value, as the linalg.matmul
+ * region the reference's decomposition ends in (HFusionOps.cpp:3590-3790:
+ * operand * broadcast scale, then linalg.matmul).  e8m0 255 is NaN.  Where
+ * the decomposition's f16 steps are exact (scaled operands inside f16's
+ * range) this is the decomposition's value bit for bit. */
+static float mx_scale(uint8_t e) {
+  return e == 255 ? NAN : ldexpf(1.0f, (int)e - 127);
+}
+static float mx_scaled(uint8_t v, int fmt, uint8_t e) {
+  return (float)((double)hfref_fp8_to_f32(v, fmt) * (double)mx_scale(e));
+}
+void hfref_matmul_mx(const uint8_t *A, const uint8_t *B, const uint8_t *sa, const uint8_t *sb, float *C, int64_t M,
+                     int64_t N, int64_t K, int fa, int fb) {
+  const int64_t kb = (K + 31) / 32;
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = C[m * N + n];
+      for (int64_t k = 0; k < K; ++k) {
+        const float x = mx_scaled(A[m * K + k], fa, sa[m * kb + k / 32]);
+        const float y = mx_scaled(B[k * N + n], fb, sb[n * kb + k / 32]);
+        const float p = x * y;
+        acc = acc + p;
+      }
+      C[m * N + n] = acc;
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* composed groups (op-by-op loop nests, temporaries materialised)           */
 /* ------------------------------------------------------------------------ */

@@ -120,6 +120,9 @@ void hfref_matmul_i8_i32(const int8_t *A, const int8_t *B, int32_t *C,
                          int64_t M, int64_t N, int64_t K, int b_transposed);
 void hfref_matmul_f32(const float *A, const float *B, float *C, int64_t M,
                       int64_t N, int64_t K, int b_transposed);
+/* hfusion.matmul_mx: fp8 operands with e8m0 scales per 32 k, f32 serial sum */
+void hfref_matmul_mx(const uint8_t *A, const uint8_t *B, const uint8_t *sa, const uint8_t *sb, float *C, int64_t M,
+                     int64_t N, int64_t K, int fa, int fb);
 
 /* ---- composed groups: op-by-op loop nests with materialised temporaries,
  * as the CPU lowering executes them (used for the timed CPU baseline) ---- */

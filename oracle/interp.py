@@ -50,6 +50,7 @@ def lib():
             "hfref_compare_i64": [INT, P, P, P, I64],
             "hfref_bf16_to_f32_n": [P, P, I64],
             "hfref_fp8_to_f32_n": [P, P, I64, INT],
+            "hfref_matmul_mx": [P, P, P, P, P, I64, I64, I64, INT, INT],
             "hfref_f32_to_fp8_n": [P, P, I64, INT, INT, INT],
             "hfref_int_to_fp8_n": [P, P, I64, INT, INT, INT],
             "hfref_f32_to_bf16_n": [P, P, I64, INT],
@@ -122,7 +123,7 @@ def _contig(a, dtype=None):
 FP8 = {"f8E4M3FN": 0, "f8E5M2": 1}
 NP = {"f32": np.float32, "f64": np.float64, "bf16": np.uint16, "f16": np.uint16, "f8E4M3FN": np.uint8, "f8E5M2": np.uint8,
       "i1": np.bool_,
-      "i8": np.int8, "i16": np.int16, "i32": np.int32, "i64": np.int64, "index": np.int64}
+      "i8": np.int8, "ui8": np.uint8, "i16": np.int16, "i32": np.int32, "i64": np.int64, "index": np.int64}
 BITS = {"i1": 1, "i8": 8, "i16": 16, "i32": 32, "i64": 64, "index": 64}
 FLOATS = ("f32", "f64", "bf16", "f16", "f8E4M3FN", "f8E5M2")
 ROUND = {"rint": 0, "round": 1, "floor": 2, "ceil": 3, "trunc": 4, "odd": 5, "truncwithoverflow": 6}
@@ -849,6 +850,25 @@ class Interp:
             return
         if op == "hfusion.reduce_with_index":
             self._reduce_with_index(res, rest, ins, outs, env)
+            return
+        if op == "hfusion.matmul_mx":
+            # fp8 A [M, K], B [K, N] (bytes take lhsFormat / rhsFormat: 1 e5m2,
+            # 2 e4m3, HFusionAttrs.td:131-137), e8m0 scales [M|N, K/32]
+            A, B, SA, SB, Cinit = get(ins[0]), get(ins[1]), get(ins[2]), get(ins[3]), get(outs[0])
+
+            def fmt(v, attr):
+                if v.elem in FP8:
+                    return FP8[v.elem]
+                code = re.search(attr + r"\s*=\s*(\d+)", rest)
+                if v.elem not in ("i8", "ui8") or not code or code.group(1) not in ("1", "2"):
+                    raise NotImplementedError("matmul_mx operand format")
+                return 1 if code.group(1) == "1" else 0
+            M, K = A.a.shape
+            N = B.a.shape[1]
+            C = _contig(np.array(Cinit.a, np.float32, copy=True))
+            byts = [_contig(v.a).view(np.uint8) for v in (A, B, SA, SB)]  # raw bytes, sign-free
+            lib().hfref_matmul_mx(*(ptr(x) for x in byts), ptr(C), M, N, K, fmt(A, "lhsFormat"), fmt(B, "rhsFormat"))
+            env[res] = T(C, "f32")
             return
         if op in ("linalg.matmul", "linalg.matmul_transpose_b"):
             A, B, Cinit = get(ins[0]), get(ins[1]), get(outs[0])

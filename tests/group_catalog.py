@@ -965,6 +965,12 @@ def entries():
     e["w8a8_kn_ragged"] = g.w8a8_dequant(300, 208, 384, b_layout="kn")
     e["w8a8_kn_wide"] = g.w8a8_dequant(264, 784, 256, b_layout="kn")
     e["w8a8_kn_dma64"] = g.w8a8_dequant(300, 208, 192, b_layout="kn")
+    # hfusion.matmul_mx: typed fp8, bytes through hfusion.bitcast, bytes with
+    # lhsFormat / rhsFormat; ragged M and N; a fill init and a bf16 epilogue
+    e["mx_e4m3"] = g.matmul_mx(256, 256, 256, name="mx_e4m3")
+    e["mx_e5m2_bitcast"] = g.matmul_mx(300, 208, 384, fa="e5m2", fb="e4m3", via="bitcast", init=0.5, name="mx_e5m2_bitcast")
+    e["mx_format_bf16"] = g.matmul_mx(264, 784, 256, fa="e4m3", fb="e5m2", via="format", out="bf16", name="mx_format_bf16")
+    e["mx_e5m2"] = g.matmul_mx(128, 128, 128, fa="e5m2", fb="e5m2", name="mx_e5m2")
     e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
     e["bf16_mmad_ragged128"] = g.bf16_mmad(200, 136, 192)
     e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)

@@ -23,6 +23,8 @@ def to_dev(a, elem, device):
         t = t.view(torch.bfloat16 if elem == "bf16" else torch.float16)
     if elem in ("f8E4M3FN", "f8E5M2"):
         t = t.view(torch.uint8).view(torch.float8_e4m3fn if elem == "f8E4M3FN" else torch.float8_e5m2)
+    if elem == "i8" and t.dtype == torch.uint8:
+        t = t.view(torch.int8)  # ui8 in the IR: the same bytes
     return t.to(device)
 
 
