@@ -223,3 +223,34 @@ def test_mx_fp8_full_sampled(gpu):
                           len(rows), n, k, 0, 0)
     mag, _ = abs_products(ar, b, sar, sb, "e4m3", "e4m3")
     assert np.all(np.abs(got[rows].astype(np.float64) - want) <= TOL * mag + 1e-30)
+
+
+@pytest.mark.gpu
+def test_matmul_mx_gpu_special_values(gpu):
+    """NaN and infinity through the matrix core: an e8m0 scale of 255 (NaN)
+    on one A row and one B column, fp8 NaN codes in another row, and e5m2
+    infinities (same sign in one column, opposite signs in another); the
+    NaN / inf pattern of the result must be the oracle's, the rest within the
+    bar."""
+    name = "mx_e5m2"
+    m, n, k, fa, fb, _, _ = GPU_CASES[name]
+    note(name + " special values")
+    rng = np.random.default_rng(17)
+    a, b, sa, sb = mx_case(rng, m, n, k, fa, fb)
+    sa[5, 1] = 255                    # row 5: NaN
+    sb[9, 2] = 255                    # column 9: NaN
+    a[11, 40] = 0x7F                  # e5m2 NaN code: row 11 NaN
+    b[:, 20] &= 0x7F                  # column 20: non-negative, one +inf
+    b[3, 20] = 0x7C
+    a[:, 3] = 0x3C                    # every row multiplies it by +1.0
+    b[:, 30] &= 0x7F                  # column 30: +inf and -inf -> NaN
+    b[3, 30], b[4, 30] = 0x7C, 0xFC
+    a[:, 4] = 0x3C
+    got, = run_gpu(name, [a, b, sa, sb], gpu)
+    want, = run_oracle(name, [a, b, sa, sb])
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want)) and np.array_equal(got[np.isinf(got)], want[np.isinf(want)])
+    ok = np.isfinite(want)
+    with np.errstate(invalid="ignore", over="ignore"):
+        mag, _ = abs_products(a, b, sa, sb, fa, fb)
+    assert np.all(np.abs(got[ok].astype(np.float64) - want[ok]) <= TOL * mag[ok] + 1e-30)
