@@ -2336,11 +2336,13 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   // operand stored the other way round (B [K, N], A [K, M]) is first copied
   // K-contiguous into the workspace by a transpose kernel of its own, when
   // the DMA ring applies; otherwise the register-staging path reads it as is.
-  // An int8 B [K, N] with 128-byte K slices goes through the ring as it is
+  // A B [K, N] with 128-byte K slices goes through the ring as it is
   // (mode 4): whole 256-byte k-rows are staged and the matrix-core operand is
   // formed by transposing LDS reads, so no re-layout pass is needed.
   const int dma0 = (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
-  const int dma = mx ? 4 : dma0 == 3 && i8 && !bT && !aT && N % 16 == 0 ? 4 : dma0;
+  // The same holds for a bf16 / f16 B [K, N] (512-byte k-rows, 16-bit
+  // transposing reads).
+  const int dma = mx ? 4 : dma0 == 3 && !bT && !aT && (N * esz) % 16 == 0 ? 4 : dma0;
   const bool preB = dma != 0 && dma != 4 && !bT, preA = dma != 0 && aT;
   const bool kT = (dma != 0 && dma != 4) || bT; // the main kernel's B is [N, K]
   const bool mT = dma == 0 && aT;          // the main kernel's A is [K, M]

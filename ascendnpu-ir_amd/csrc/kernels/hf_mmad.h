@@ -505,7 +505,8 @@ constexpr int MMD2_SLICE = 256 * 128;
 // registers): while one wave of a SIMD waits on memory, the other issues
 // MFMAs.  Ring: two stages of 128-byte K slices, swizzled as described above;
 // each wave issues 8 DMAs per stage (its 32 rows of A and of B).
-// BKN: B is [K, N] (linalg.matmul, int8): a stage of B is 128 k-rows x 256
+// BKN: B is [K, N] (linalg.matmul; int8, fp8, or bf16 / f16 with 64 k-rows of
+// 512 bytes per stage as below): a byte stage of B is 128 k-rows x 256
 // columns, each DMA instruction 4 whole 256-byte k-rows, kept K-major in LDS
 // (granule g of k-row r at position g ^ kn_swz(r), so the 8 k-rows x 2
 // granules one half-wave reads sit on 16 different positions).  A B fragment is read with
@@ -526,7 +527,8 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
                              int64_t M, int64_t N, int64_t K, const Args &P, const uint8_t *__restrict__ SA = nullptr,
                              const uint8_t *__restrict__ SB = nullptr) {
   constexpr bool MX = mk_is_mx(MK);
-  static_assert(!BKN || ((MK == MK_I8 || MX) && sizeof(ElemT) == 1), "the [K, N] B path takes bytes");
+  static_assert(!BKN || (((MK == MK_I8 || MX) && sizeof(ElemT) == 1) || ((MK == MK_BF16 || MK == MK_F16) && sizeof(ElemT) == 2)),
+                "the [K, N] B path takes bytes or 16-bit floats");
   static_assert(!MX || BKN, "block-scaled operands come with B [K, N]");
   using Op = typename std::conditional<MX, MfmaMx<(MX ? MK : MK_MX)>, MfmaOp<(MX ? MK_I8 : MK)>>::type;
   using acc_t = typename Op::acc_t;
@@ -545,6 +547,9 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   const char *Ab = reinterpret_cast<const char *>(A), *Bb = reinterpret_cast<const char *>(B);
   const int nsteps = (int)(Kb / 128);
   auto kn_swz = [](int kr) { return ((kr & 7) << 1) | ((kr >> 3) & 1); };
+  // 16-bit [K, N]: the 4 k-rows of one transposing read on 4 different
+  // 64-byte bank groups
+  auto kn16_swz = [](int kr) { return (kr & 3) << 2; };
 
   // DMA d (0..7) of K slice s into ring slot `slot`: d < 4 this wave's A
   // rows (32 * wave ..), else its B rows, 8 rows per instruction
@@ -553,7 +558,7 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     const int blk = wave * 4 + (d & 3);
     const int r = 8 * blk + lane / 8;
     const int g = (lane % 8) ^ ((r >> 1) & 7);
-    if (BKN && d >= 4) {
+    if (BKN && d >= 4 && ESZ == 1) {
       // 4 k-rows of 256 columns: lane l fills position l % 16 of k-row
       // 4 blk + l / 16 with logical granule (l % 16) ^ kn_swz(k-row)
       const int kr = 4 * blk + lane / 16;
@@ -561,6 +566,17 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
       int64_t col = n0 + 16 * gg;
       col = col + 16 <= N ? col : N - 16; // columns past N: any valid bytes (masked later)
       mmd_dma16(Bb + ((int64_t)s * 128 + kr) * N + col, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+      return;
+    }
+    if (BKN && d >= 4 && ESZ == 2) {
+      // 16-bit elements: a 128-byte slice is 64 k-rows of 512 bytes; lane l
+      // fills position l % 32 of k-row 2 blk + l / 32 with logical granule
+      // (8 columns) (l % 32) ^ kn16_swz(k-row)
+      const int kr = 2 * blk + lane / 32;
+      const int gg = (lane % 32) ^ kn16_swz(kr);
+      int64_t col = n0 + 8 * gg;
+      col = col + 8 <= N ? col : N - 8;
+      mmd_dma16(Bb + (((int64_t)s * 64 + kr) * N + col) * 2, __builtin_amdgcn_readfirstlane(st + blk * 1024));
       return;
     }
     const int64_t rows = d < 4 ? M : N, row0 = d < 4 ? m0 : n0;
@@ -614,6 +630,29 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     }
     return r;
   };
+  // 16-bit B fragment from the K-major slice: columns blk * 32 .., k-block
+  // kb (16 k).  ds_read_b64_tr_b16: in each group of 16 lanes, lane i's
+  // element e is element i % 4 of the 4 addressed by lane 4 e + i / 4, so
+  // lane j addressing k-row k0 + j / 4 at column c0 + 4 (j % 4) gives lane i
+  // the column c0 + i at k-rows k0 .. k0+3 (measured on gfx950)
+  auto frag_kn16 = [&](const char *slice, int blk, int kb) -> v4i {
+    const int q = lane / 16, j = lane % 16;
+    const int col = blk * 32 + 16 * (q % 2) + 4 * (j % 4);
+    v4i r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kr = kb * 16 + 8 * (q / 2) + 4 * h + j / 4;
+      const int pos = kr * 512 + (((col >> 3) ^ kn16_swz(kr)) << 4) + (col & 7) * 2;
+      typedef short v4s_ __attribute__((ext_vector_type(4)));
+      const v4s_ t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4s_ *)(uintptr_t)((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char *)slice + pos));
+      typedef int v2i_ __attribute__((ext_vector_type(2)));
+      const v2i_ u = __builtin_bit_cast(v2i_, t);
+      r[2 * h] = u.x;
+      r[2 * h + 1] = u.y;
+    }
+    return r;
+  };
   // the 12 fragments (2 k-blocks x (4 A + 2 B)) of half h of stage s
   auto fetch = [&](int s, int h, v4i (&f)[2][6]) {
     const char *la = lds[s & 1][0], *lb = lds[s & 1][1];
@@ -623,7 +662,8 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
       for (int i = 0; i < 4; ++i) f[q][i] = frag(la, wm * 4 + i, 4 * h + 2 * q + lane / 32);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        f[q][4 + j] = BKN ? frag_kn(lb, wn * 2 + j, 2 * h + q) : frag(lb, wn * 2 + j, 4 * h + 2 * q + lane / 32);
+        f[q][4 + j] = !BKN ? frag(lb, wn * 2 + j, 4 * h + 2 * q + lane / 32)
+                      : ESZ == 1 ? frag_kn(lb, wn * 2 + j, 2 * h + q) : frag_kn16(lb, wn * 2 + j, 2 * h + q);
     }
   };
 
@@ -776,8 +816,8 @@ __device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char 
 // [N, K] with BT (the weight layout) or [K, N]; DMA selects the LDS DMA ring:
 // 0 none (register staging), 1 with 64-byte K slices (256 threads), 3 with
 // 128-byte slices and two waves per SIMD (512 threads); both require !AT, BT
-// and K spanning a multiple of 64 resp. 128 bytes; 4 as 3 with an int8 B
-// [K, N] (!BT, N a multiple of 16) read K-major from LDS by transposing reads.
+// and K spanning a multiple of 64 resp. 128 bytes; 4 as 3 with a B
+// [K, N] (!BT, rows of a multiple of 16 bytes) read K-major from LDS by transposing reads.
 template <int MK, typename Epi, bool AT, bool BT, int DMA, typename ElemT, typename Args>
 __device__ __forceinline__ void mmad(const ElemT *A, const ElemT *B, typename Epi::out_t *out, int64_t M, int64_t N, int64_t K,
                                      const Args &P) {

@@ -250,17 +250,21 @@ def hivm_matmul(m, n, k, elem="f16", out="f16", bias=None, descale=None, descale
 """
 
 
-def bf16_mmad(m=4096, n=4096, k=4096):
-    """bf16 contraction (hivm.hir.mmadL1 bf16 -> f32) with a bf16 output cast."""
-    A, B = _t([m, k], "bf16"), _t([n, k], "bf16")
-    C, O = _t([m, n], "f32"), _t([m, n], "bf16")
+def bf16_mmad(m=4096, n=4096, k=4096, b_layout="nk", elem="bf16"):
+    """bf16 (or f16) contraction -> f32 with an output cast back to the input
+    type; B in the [N, K] weight layout (linalg.matmul_transpose_b) or, with
+    b_layout="kn", [K, N] (linalg.matmul)."""
+    A = _t([m, k], elem)
+    B = _t([n, k], elem) if b_layout == "nk" else _t([k, n], elem)
+    mm = "linalg.matmul_transpose_b" if b_layout == "nk" else "linalg.matmul"
+    C, O = _t([m, n], "f32"), _t([m, n], elem)
     return f"""module {{
   func.func @bf16_mmad(%a: {A}, %b: {B}, %out: {O}) -> {O}
       {_ATTRS.format(kind='SINGLE_CUBE')} {{
     %c0 = arith.constant 0.000000e+00 : f32
     %e0 = tensor.empty() : {C}
     %acc0 = linalg.fill ins(%c0 : f32) outs(%e0 : {C}) -> {C}
-    %acc = linalg.matmul_transpose_b ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
+    %acc = {mm} ins(%a, %b : {A}, {B}) outs(%acc0 : {C}) -> {C}
     %o = hfusion.cast {{round_mode = #hfusion.round_mode<rint>}} ins(%acc : {C}) outs(%out : {O}) -> {O}
     return %o : {O}
   }}

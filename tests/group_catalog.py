@@ -973,6 +973,10 @@ def entries():
     e["mx_e5m2"] = g.matmul_mx(128, 128, 128, fa="e5m2", fb="e5m2", name="mx_e5m2")
     e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
     e["bf16_mmad_ragged128"] = g.bf16_mmad(200, 136, 192)
+    # B [K, N] through the ring (16-bit transposing reads), bf16 and f16
+    e["bf16_mmad_kn"] = g.bf16_mmad(256, 256, 128, b_layout="kn")
+    e["bf16_mmad_kn_ragged"] = g.bf16_mmad(200, 136, 192, b_layout="kn")
+    e["f16_mmad_kn"] = g.bf16_mmad(264, 520, 320, b_layout="kn", elem="f16")
     e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)
     # hivm.hir.matmul forms of bishengir/test/Dialect/HIVM/IR/ops.mlir (16x16 f16) and wider
     e["hivm_mm_f16_null"] = g.hivm_matmul(16, 16, 16)

@@ -201,6 +201,35 @@ def test_bf16_mmad(gpu, name, m, n, k):
     assert bf16_ulp_diff(out, ref).max() <= 1
 
 
+@pytest.mark.parametrize("name,m,n,k,elem", [("bf16_mmad_kn", 256, 256, 128, "bf16"),
+                                             ("bf16_mmad_kn_ragged", 200, 136, 192, "bf16"),
+                                             ("f16_mmad_kn", 264, 520, 320, "f16")])
+def test_mmad_16bit_kn(gpu, name, m, n, k, elem):
+    """B [K, N] (linalg.matmul) in bf16 and f16: the ring stages whole k-rows
+    and forms the operand with 16-bit transposing LDS reads."""
+    note(name)
+    s = I.SEED_BASE + 41
+    if elem == "bf16":
+        a, b = I.normal_bf16(s, (m, k)), I.normal_bf16(s + 1, (k, n))
+    else:
+        a = I.normal_f32(s, (m, k)).astype(np.float16).view(np.uint16)
+        b = I.normal_f32(s + 1, (k, n)).astype(np.float16).view(np.uint16)
+    args = [a, b, zeros((m, n), np.uint16)]
+    out, = run_gpu(name, args, gpu)
+    ref, = run_oracle(name, args)
+    if elem == "bf16":
+        # fp32 accumulation order differs from the serial k loop
+        assert bf16_ulp_diff(out, ref).max() <= 1
+    else:
+        # f16 keeps 11 bits: where a 320-term sum cancels, the f32 order
+        # difference (<= K * 2^-24 * sum|ab|) can exceed one f16 ulp, so the
+        # bar is that plus half an ulp of each rounding
+        fa, fb = (x.view(np.float16).astype(np.float64) for x in (a, b))
+        mag = np.abs(fa) @ np.abs(fb)
+        o, r = out.view(np.float16).astype(np.float64), ref.view(np.float16).astype(np.float64)
+        assert np.all(np.abs(o - r) <= k * 2.0 ** -24 * mag + 2.0 ** -10 * np.abs(r) + 2.0 ** -24)
+
+
 # ------------------------------------------------------------------ casts
 def cast_inputs(n):
     v = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 0.49999997, 126.5, 127.5, -127.5, -128.5, 128.7, 127.5, 100.3, -129.2,
