@@ -2273,6 +2273,8 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const Op *castA = nullptr, *castB = nullptr;
   auto throughBitcast = [&](const Value *v, const Op *&cast) {
     if (mx && v->def && v->def->name == "hfusion.bitcast" && !v->def->ins.empty()) {
+      if (elemBits(v->def->ins[0]->type.elem) != 8 || v->def->ins[0]->type.shape != v->type.shape)
+        unsupported(v->def, "matmul_mx operand bitcast from other than same-shape bytes");
       cast = v->def;
       return (const Value *)v->def->ins[0];
     }
@@ -2296,11 +2298,16 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
       if (e == Elem::F8E5M2) return 1;
       if (e == Elem::I8) {
         auto it = mm->attrs.find(attr);
-        const std::string v = it == mm->attrs.end() ? "" : it->second;
-        if (v.rfind("1", 0) == 0) return 1;
-        if (v.rfind("2", 0) == 0) return 0;
-        if (v.rfind("3", 0) == 0) unsupported(mm, "matmul_mx fp4 (e2m1) operands");
-        unsupported(mm, std::string("matmul_mx byte operand without ") + attr);
+        int code = -1;
+        if (it != mm->attrs.end()) {
+          size_t used = 0;
+          try { code = std::stoi(it->second, &used); } catch (...) { code = -1; }
+          if (used == 0) code = -1;
+        }
+        if (code == 1) return 1;
+        if (code == 2) return 0;
+        if (code == 3) unsupported(mm, "matmul_mx fp4 (e2m1) operands");
+        unsupported(mm, std::string("matmul_mx byte operand without a valid ") + attr);
       }
       unsupported(mm, "matmul_mx operand type (f8E4M3FN, f8E5M2 or bytes with a format)");
       return -1;

@@ -154,7 +154,7 @@ def test_matmul_mx_lowering_limits():
         text = hf.groups.matmul_mx(m, n, k, via="format" if extra_attr else "fp8")
         return text.replace("lhsFormat = 2", extra_attr) if extra_attr else text
     for text, msg in ((ir(64, 64, 96), "multiple of 128"), (ir(64, 72, 128), "N must be a multiple of 16"),
-                      (ir(64, 64, 128, "lhsFormat = 3"), "fp4")):
+                      (ir(64, 64, 128, "lhsFormat = 3"), "fp4"), (ir(64, 64, 128, "lhsFormat = 12"), "valid lhsFormat")):
         with pytest.raises(hf.CompileError, match=msg):
             hf.compile(text, options="emit=hip")
     # ui8 only as matmul_mx scales
