@@ -400,6 +400,25 @@ def vendor_report(out, steps, warmup, command):
                          f"{ops / (gemm * 1e-6) / 1e12:.0f} TOPS; fused W8A8 here: {ops / (ours * 1e-6) / 1e12:.0f} TOPS")
         del dargs, sets
         torch.cuda.empty_cache()
+    # the block-scaled fp8 group next to hipBLASLt's fp8 GEMM with one scale
+    # per tensor (torch._scaled_mm; torch has no e8m0 block-scale form here)
+    log("[bench] vendor comparison: mx_fp8")
+    grp = hf.compile(hf.catalog.get("mx_fp8"), require_cached=True).load()
+    dargs = generic_inputs(grp.meta, dev)
+    sets = input_sets(dargs)
+    ours = time_group(grp, sets, steps, warmup)[0] / steps * 1e3
+    ops = grp.meta["algo_ops"]
+    one = torch.ones((), dtype=torch.float32, device=dev)
+    bt = [[a, b.t().contiguous().t()] for a, b, _, _ in sets]   # B column-major, as _scaled_mm takes it
+    try:
+        vend = time_group(lambda a, b: torch._scaled_mm(a, b, scale_a=one, scale_b=one, out_dtype=torch.float32),
+                          bt, steps, warmup)[0] / steps * 1e3
+        lines.append(f"mx_fp8             {ours:8.2f}  (hipBLASLt fp8 GEMM, per-tensor scales, f32 out: {vend:.2f} us = "
+                     f"{ops / (vend * 1e-6) / 1e12:.0f} TFLOP/s; block-scaled here: {ops / (ours * 1e-6) / 1e12:.0f} TFLOP/s)")
+    except Exception as e:  # noqa: BLE001 - report what the platform lacks
+        lines.append(f"mx_fp8             {ours:8.2f}  (torch._scaled_mm unavailable: {type(e).__name__})")
+    del dargs, sets, bt
+    torch.cuda.empty_cache()
     text = "\n".join(lines) + "\n"
     if out == "-":
         sys.stdout.write(text)
