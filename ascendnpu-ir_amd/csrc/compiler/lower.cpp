@@ -2349,10 +2349,12 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const int dma0 = (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
   // The same holds for a bf16 / f16 B [K, N] (512-byte k-rows, 16-bit
   // transposing reads).
-  const int dma = mx ? 4 : dma0 == 3 && !bT && !aT && (N * esz) % 16 == 0 ? 4 : dma0;
-  const bool preB = dma != 0 && dma != 4 && !bT, preA = dma != 0 && aT;
+  // An A [K, M] is staged and read the same way.
+  const bool kmajOk = (bT || (N * esz) % 16 == 0) && (!aT || (M * esz) % 16 == 0);
+  const int dma = mx ? 4 : dma0 == 3 && (!bT || aT) && kmajOk ? 4 : dma0;
+  const bool preB = dma != 0 && dma != 4 && !bT, preA = dma != 0 && dma != 4 && aT;
   const bool kT = (dma != 0 && dma != 4) || bT; // the main kernel's B is [N, K]
-  const bool mT = dma == 0 && aT;          // the main kernel's A is [K, M]
+  const bool mT = (dma == 0 || dma == 4) && aT; // the main kernel's A is [K, M]
   const int threads = dma >= 3 ? 512 : 256;
   auto align256 = [](uint64_t v) { return (v + 255) / 256 * 256; };
   const uint64_t wsB = preB ? align256((uint64_t)(N * K * esz)) : 0, wsA = preA ? align256((uint64_t)(M * K * esz)) : 0;
@@ -2514,7 +2516,8 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
                           : mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
               (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") +
               (preA || preB ? " (re-laid K-contiguous by a transpose kernel)" : "") +
-              (dma == 4 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD; B k-rows staged whole, transposing LDS reads)" :
+              (dma == 4 ? std::string(", LDS DMA ring (128-byte slices, 2 waves/SIMD; ") + (aT && bT ? "A" : aT ? "A and B" : "B") +
+                              " k-rows staged whole, transposing LDS reads)" :
                dma == 3 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD)" : dma == 1 ? ", LDS DMA ring" : ", register staging");
   p.algoOps = 2.0 * (double)M * (double)N * (double)K;
   return p;

@@ -522,13 +522,17 @@ constexpr int MMD2_SLICE = 256 * 128;
 // rows, 1 KB for its 256 B columns) ride the same ring, one 4-byte-per-lane
 // DMA per wave per stage, so every load of a stage is covered by the ring's
 // own wait.
-template <int MK, typename Epi, bool BKN, typename ElemT, typename Args>
+// AKM: A is [K, M] (hivm a_transpose), staged and read exactly as a [K, N] B
+// (its M columns in place of N).
+template <int MK, typename Epi, bool BKN, bool AKM = false, typename ElemT, typename Args>
 __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
                              int64_t M, int64_t N, int64_t K, const Args &P, const uint8_t *__restrict__ SA = nullptr,
                              const uint8_t *__restrict__ SB = nullptr) {
   constexpr bool MX = mk_is_mx(MK);
-  static_assert(!BKN || (((MK == MK_I8 || MX) && sizeof(ElemT) == 1) || ((MK == MK_BF16 || MK == MK_F16) && sizeof(ElemT) == 2)),
-                "the [K, N] B path takes bytes or 16-bit floats");
+  static_assert(!AKM || !MX, "block-scaled A is [M, K]");
+  static_assert(!(BKN || AKM) || (((MK == MK_I8 || MX) && sizeof(ElemT) == 1) ||
+                                  ((MK == MK_BF16 || MK == MK_F16) && sizeof(ElemT) == 2)),
+                "the K-major operand path takes bytes or 16-bit floats");
   static_assert(!MX || BKN, "block-scaled operands come with B [K, N]");
   using Op = typename std::conditional<MX, MfmaMx<(MX ? MK : MK_MX)>, MfmaOp<(MX ? MK_I8 : MK)>>::type;
   using acc_t = typename Op::acc_t;
@@ -558,25 +562,28 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     const int blk = wave * 4 + (d & 3);
     const int r = 8 * blk + lane / 8;
     const int g = (lane % 8) ^ ((r >> 1) & 7);
-    if (BKN && d >= 4 && ESZ == 1) {
-      // 4 k-rows of 256 columns: lane l fills position l % 16 of k-row
-      // 4 blk + l / 16 with logical granule (l % 16) ^ kn_swz(k-row)
-      const int kr = 4 * blk + lane / 16;
-      const int gg = (lane % 16) ^ kn_swz(kr);
-      int64_t col = n0 + 16 * gg;
-      col = col + 16 <= N ? col : N - 16; // columns past N: any valid bytes (masked later)
-      mmd_dma16(Bb + ((int64_t)s * 128 + kr) * N + col, __builtin_amdgcn_readfirstlane(st + blk * 1024));
-      return;
-    }
-    if (BKN && d >= 4 && ESZ == 2) {
-      // 16-bit elements: a 128-byte slice is 64 k-rows of 512 bytes; lane l
-      // fills position l % 32 of k-row 2 blk + l / 32 with logical granule
-      // (8 columns) (l % 32) ^ kn16_swz(k-row)
-      const int kr = 2 * blk + lane / 32;
-      const int gg = (lane % 32) ^ kn16_swz(kr);
-      int64_t col = n0 + 8 * gg;
-      col = col + 8 <= N ? col : N - 8;
-      mmd_dma16(Bb + (((int64_t)s * 64 + kr) * N + col) * 2, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+    const bool kmaj = d >= 4 ? BKN : AKM; // this operand is stored [K, columns]
+    if (kmaj) {
+      const char *base = d >= 4 ? Bb : Ab;
+      const int64_t cols = d >= 4 ? N : M, c0 = d >= 4 ? n0 : m0;
+      if constexpr (ESZ == 1) {
+        // 4 k-rows of 256 columns: lane l fills position l % 16 of k-row
+        // 4 blk + l / 16 with logical granule (l % 16) ^ kn_swz(k-row)
+        const int kr = 4 * blk + lane / 16;
+        const int gg = (lane % 16) ^ kn_swz(kr);
+        int64_t col = c0 + 16 * gg;
+        col = col + 16 <= cols ? col : cols - 16; // columns past the end: any valid bytes (masked later)
+        mmd_dma16(base + ((int64_t)s * 128 + kr) * cols + col, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+      } else {
+        // 16-bit elements: a 128-byte slice is 64 k-rows of 512 bytes; lane l
+        // fills position l % 32 of k-row 2 blk + l / 32 with logical granule
+        // (8 columns) (l % 32) ^ kn16_swz(k-row)
+        const int kr = 2 * blk + lane / 32;
+        const int gg = (lane % 32) ^ kn16_swz(kr);
+        int64_t col = c0 + 8 * gg;
+        col = col + 8 <= cols ? col : cols - 8;
+        mmd_dma16(base + (((int64_t)s * 64 + kr) * cols + col) * 2, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+      }
       return;
     }
     const int64_t rows = d < 4 ? M : N, row0 = d < 4 ? m0 : n0;
@@ -659,7 +666,9 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) f[q][i] = frag(la, wm * 4 + i, 4 * h + 2 * q + lane / 32);
+      for (int i = 0; i < 4; ++i)
+        f[q][i] = !AKM ? frag(la, wm * 4 + i, 4 * h + 2 * q + lane / 32)
+                  : ESZ == 1 ? frag_kn(la, wm * 4 + i, 2 * h + q) : frag_kn16(la, wm * 4 + i, 2 * h + q);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         f[q][4 + j] = !BKN ? frag(lb, wn * 2 + j, 4 * h + 2 * q + lane / 32)
@@ -816,14 +825,15 @@ __device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char 
 // [N, K] with BT (the weight layout) or [K, N]; DMA selects the LDS DMA ring:
 // 0 none (register staging), 1 with 64-byte K slices (256 threads), 3 with
 // 128-byte slices and two waves per SIMD (512 threads); both require !AT, BT
-// and K spanning a multiple of 64 resp. 128 bytes; 4 as 3 with a B
-// [K, N] (!BT, rows of a multiple of 16 bytes) read K-major from LDS by transposing reads.
+// and K spanning a multiple of 64 resp. 128 bytes; 4 as 3 with a B [K, N]
+// (!BT) and / or an A [K, M] (AT), rows of a multiple of 16 bytes, staged
+// K-major and read by transposing LDS reads.
 template <int MK, typename Epi, bool AT, bool BT, int DMA, typename ElemT, typename Args>
 __device__ __forceinline__ void mmad(const ElemT *A, const ElemT *B, typename Epi::out_t *out, int64_t M, int64_t N, int64_t K,
                                      const Args &P) {
-  static_assert(DMA == 0 || (!AT && (BT || DMA == 4)), "the DMA ring takes K-contiguous A (and B unless DMA 4)");
+  static_assert(DMA == 0 || DMA == 4 || (!AT && BT), "the DMA rings 1 and 3 take K-contiguous A and B");
   static_assert(DMA == 0 || DMA == 1 || DMA == 3 || DMA == 4, "DMA mode");
-  if constexpr (DMA == 4) mmad_core_pp<MK, Epi, true>(A, B, out, M, N, K, P);
+  if constexpr (DMA == 4) mmad_core_pp<MK, Epi, !BT, AT>(A, B, out, M, N, K, P);
   else if constexpr (mk_is_mx(MK)) static_assert(DMA == 4, "block-scaled kinds run on the [K, N] ring");
   else if constexpr (DMA == 3) mmad_core_pp<MK, Epi, false>(A, B, out, M, N, K, P);
   else if constexpr (DMA == 1) mmad_core_dma<MK, Epi>(A, B, out, M, N, K, P);

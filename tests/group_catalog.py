@@ -988,6 +988,12 @@ def entries():
     e["hivm_mm_i8_pt_i8out"] = g.hivm_matmul(256, 320, 128, elem="i8", out="i8", descale="f32",
                                              descale_mode="DescalePerTensor", b_t=True)
     e["hivm_mm_bf16_at"] = g.hivm_matmul(160, 96, 64, elem="bf16", out="f32", bias="f32", a_t=True)
+    # A [K, M] staged K-major on the ring, with B [N, K] or [K, N]
+    e["hivm_mm_i8_at"] = g.hivm_matmul(272, 320, 256, elem="i8", out="bf16", descale="f32",
+                                       descale_mode="DescalePerChannel", a_t=True, b_t=True)
+    e["hivm_mm_i8_at_kn"] = g.hivm_matmul(256, 208, 384, elem="i8", out="bf16", descale="f32",
+                                          descale_mode="DescalePerTensor", a_t=True)
+    e["hivm_mm_bf16_at_bt"] = g.hivm_matmul(200, 136, 128, elem="bf16", out="f32", a_t=True, b_t=True)
     e["mm_i8_ragged"] = g.mm_i8(300, 200, 192)
     e["bf16_mmad_256"] = g.bf16_mmad(256, 256, 256)
     e["cast_modes"] = cast_modes(4096)

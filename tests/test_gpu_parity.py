@@ -165,6 +165,13 @@ def _hivm_inputs(name):
     if name == "hivm_mm_i8_pt_i8out":
         return [I.int8_uniform(s, (256, 128)), I.int8_uniform(s + 1, (320, 128)), np.array([2e-3], np.float32),
                 np.zeros((256, 320), np.int8)]
+    if name in ("hivm_mm_i8_at", "hivm_mm_i8_at_kn"):
+        m, n, k = (272, 320, 256) if name == "hivm_mm_i8_at" else (256, 208, 384)
+        bshape = (n, k) if name == "hivm_mm_i8_at" else (k, n)
+        ds = I.uniform_f32(s + 3, (n,) if name == "hivm_mm_i8_at" else (1,), 0.001, 0.02)
+        return [I.int8_uniform(s, (k, m)), I.int8_uniform(s + 1, bshape), ds, np.zeros((m, n), np.uint16)]
+    if name == "hivm_mm_bf16_at_bt":
+        return [I.normal_bf16(s, (128, 200)), I.normal_bf16(s + 1, (136, 128)), np.zeros((200, 136), np.float32)]
     if name == "hivm_mm_bf16_at":
         return [I.normal_bf16(s, (64, 160)), I.normal_bf16(s + 1, (64, 96)), I.normal_f32(s + 2, (96,)),
                 np.zeros((160, 96), np.float32)]
@@ -172,7 +179,8 @@ def _hivm_inputs(name):
 
 
 @pytest.mark.parametrize("name", ["hivm_mm_f16_null", "hivm_mm_f16_bias_pc", "hivm_mm_f16_bias_pt_t", "hivm_mm_i8_pc",
-                                  "hivm_mm_i8_pt_i8out", "hivm_mm_bf16_at"])
+                                  "hivm_mm_i8_pt_i8out", "hivm_mm_bf16_at", "hivm_mm_i8_at", "hivm_mm_i8_at_kn",
+                                  "hivm_mm_bf16_at_bt"])
 def test_hivm_matmul(gpu, name):
     """hivm.hir.matmul with bias / descale modes / transposes (written in place
     into the `outs` memref argument)."""
