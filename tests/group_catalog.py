@@ -994,6 +994,7 @@ def entries():
     e["hivm_mm_i8_at_kn"] = g.hivm_matmul(256, 208, 384, elem="i8", out="bf16", descale="f32",
                                           descale_mode="DescalePerTensor", a_t=True)
     e["hivm_mm_bf16_at_bt"] = g.hivm_matmul(200, 136, 128, elem="bf16", out="f32", a_t=True, b_t=True)
+    e["hivm_mm_f16_at_bt"] = g.hivm_matmul(152, 264, 192, elem="f16", out="f16", a_t=True, b_t=True)
     e["mm_i8_ragged"] = g.mm_i8(300, 200, 192)
     e["bf16_mmad_256"] = g.bf16_mmad(256, 256, 256)
     e["cast_modes"] = cast_modes(4096)

@@ -151,6 +151,8 @@ def _hivm_inputs(name):
     [bias], [descale], C."""
     s = I.SEED_BASE + 48
     f16 = lambda a: np.asarray(a, np.float16).view(np.uint16)
+    if name == "hivm_mm_f16_at_bt":
+        return [f16(I.normal_f32(s, (192, 152))), f16(I.normal_f32(s + 1, (264, 192))), np.zeros((152, 264), np.uint16)]
     if name.startswith("hivm_mm_f16"):
         a, b = I.normal_f32(s, (16, 16)), I.normal_f32(s + 1, (16, 16))
         args = [f16(a), f16(b)]
@@ -180,7 +182,7 @@ def _hivm_inputs(name):
 
 @pytest.mark.parametrize("name", ["hivm_mm_f16_null", "hivm_mm_f16_bias_pc", "hivm_mm_f16_bias_pt_t", "hivm_mm_i8_pc",
                                   "hivm_mm_i8_pt_i8out", "hivm_mm_bf16_at", "hivm_mm_i8_at", "hivm_mm_i8_at_kn",
-                                  "hivm_mm_bf16_at_bt"])
+                                  "hivm_mm_bf16_at_bt", "hivm_mm_f16_at_bt"])
 def test_hivm_matmul(gpu, name):
     """hivm.hir.matmul with bias / descale modes / transposes (written in place
     into the `outs` memref argument)."""
@@ -190,6 +192,14 @@ def test_hivm_matmul(gpu, name):
     ref, = run_oracle(name, args)
     if name.startswith("hivm_mm_i8"):
         assert np.array_equal(out, ref)               # exact int32 accumulator, same fp32 epilogue
+    elif name == "hivm_mm_f16_at_bt":
+        # 192-term sums: where they cancel, the f32 order difference (<= K * 2^-24 * sum|ab|)
+        # can exceed an f16 ulp
+        fa = args[0].view(np.float16).astype(np.float64).T
+        fb = args[1].view(np.float16).astype(np.float64).T
+        mag = np.abs(fa) @ np.abs(fb)
+        o, r = out.view(np.float16).astype(np.float64), ref.view(np.float16).astype(np.float64)
+        assert np.all(np.abs(o - r) <= 192 * 2.0 ** -24 * mag + 2.0 ** -10 * np.abs(r) + 2.0 ** -24)
     elif name.startswith("hivm_mm_f16"):
         assert bf16_ulp_diff(out, ref).max() <= 1      # f16 bits; fp32 sums in another order
     else:
