@@ -965,6 +965,7 @@ def entries():
     e["w8a8_kn_ragged"] = g.w8a8_dequant(300, 208, 384, b_layout="kn")
     e["w8a8_kn_wide"] = g.w8a8_dequant(264, 784, 256, b_layout="kn")
     e["w8a8_kn_dma64"] = g.w8a8_dequant(300, 208, 192, b_layout="kn")
+    e["w8a8_kn_tiny"] = g.w8a8_dequant(1, 16, 128, b_layout="kn")
     # hfusion.matmul_mx: typed fp8, bytes through hfusion.bitcast, bytes with
     # lhsFormat / rhsFormat; ragged M and N; a fill init and a bf16 epilogue
     e["mx_e4m3"] = g.matmul_mx(256, 256, 256, name="mx_e4m3")
@@ -977,6 +978,7 @@ def entries():
     e["bf16_mmad_kn"] = g.bf16_mmad(256, 256, 128, b_layout="kn")
     e["bf16_mmad_kn_ragged"] = g.bf16_mmad(200, 136, 192, b_layout="kn")
     e["f16_mmad_kn"] = g.bf16_mmad(264, 520, 320, b_layout="kn", elem="f16")
+    e["bf16_mmad_kn_tiny"] = g.bf16_mmad(3, 8, 64, b_layout="kn")
     e["mm_i8_full"] = g.mm_i8(4096, 4096, 4096)
     # hivm.hir.matmul forms of bishengir/test/Dialect/HIVM/IR/ops.mlir (16x16 f16) and wider
     e["hivm_mm_f16_null"] = g.hivm_matmul(16, 16, 16)

@@ -123,7 +123,8 @@ def test_argmax_repeat_launch(gpu):
 @pytest.mark.parametrize("name,m,n,k", [("w8a8_512", 512, 512, 512), ("w8a8_ragged", 300, 200, 160),
                                         ("w8a8_ragged_dma", 300, 200, 192), ("w8a8_ragged_dma128", 300, 200, 384),
                                         ("w8a8_kn", 320, 256, 128), ("w8a8_kn_ragged", 300, 208, 384),
-                                        ("w8a8_kn_wide", 264, 784, 256), ("w8a8_kn_dma64", 300, 208, 192)])
+                                        ("w8a8_kn_wide", 264, 784, 256), ("w8a8_kn_dma64", 300, 208, 192),
+                                        ("w8a8_kn_tiny", 1, 16, 128)])
 def test_w8a8(gpu, name, m, n, k):
     note(name)
     a, b, st, sc = I.config_inputs("w8a8_dequant", m=m, n=n, k=k)
@@ -221,7 +222,8 @@ def test_bf16_mmad(gpu, name, m, n, k):
 
 @pytest.mark.parametrize("name,m,n,k,elem", [("bf16_mmad_kn", 256, 256, 128, "bf16"),
                                              ("bf16_mmad_kn_ragged", 200, 136, 192, "bf16"),
-                                             ("f16_mmad_kn", 264, 520, 320, "f16")])
+                                             ("f16_mmad_kn", 264, 520, 320, "f16"),
+                                             ("bf16_mmad_kn_tiny", 3, 8, 64, "bf16")])
 def test_mmad_16bit_kn(gpu, name, m, n, k, elem):
     """B [K, N] (linalg.matmul) in bf16 and f16: the ring stages whole k-rows
     and forms the operand with 16-bit transposing LDS reads."""
