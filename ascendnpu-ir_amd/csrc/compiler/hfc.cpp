@@ -142,7 +142,7 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
   std::vector<hfc::KernelPlan> plans;
   try {
     hfc::LowerOptions lo;
-    lo.orderedFloatSums = opts.count("ordered_fp_sums") && opts["ordered_fp_sums"] == "1";
+    if (opts.count("ordered_fp_sums")) lo.orderedFloatSums = opts["ordered_fp_sums"] == "1" ? 1 : 0;
     lo.rmsqKernel = opts.count("rmsq_kernel") && opts["rmsq_kernel"] == "1";
     plans = hfc::lowerModule(*mod, lo);
   } catch (const hfc::CompileError &e) {

@@ -661,6 +661,11 @@ std::string elementExpr(const Op *op, const std::vector<std::string> &a, const s
     std::vector<std::string> xs;
     for (int i = 0; i < arity; ++i) xs.push_back(bits ? bitcastExpr(a[i], at[i], U, op) : castExpr(a[i], at[i], U, uns));
     if (isFloat(U)) {
+      // exp rounded onto bf16 / f16: the guarded evaluation that rounds as
+      // the CPU's f32 expf does
+      if (arity == 1 && fn == "exp" && (U == Elem::BF16 || U == Elem::F16))
+        return castExpr("hf::exp_narrow<" + std::string(U == Elem::BF16 ? "8" : "11") + ">(" + castExpr(xs[0], U, Elem::F32, false) + ")",
+                        Elem::F32, U, false);
       if (arity == 1) return inFloatType(U, xs, [&](const std::vector<std::string> &y) { return f32UnaryFn(fn, y[0], op); });
       if (arity == 2) return inFloatType(U, xs, [&](const std::vector<std::string> &y) { return f32BinaryFn(fn, y[0], y[1], op); });
       if (fn == "fma")
@@ -914,6 +919,15 @@ std::vector<int64_t> permutationOf(const Op *op) {
   return perm;
 }
 
+// `m` without the entries at `positions` (tensor dims of a reduce or
+// broadcast op's `dimensions`).
+std::vector<int> dropPositions(const std::vector<int> &m, const std::vector<int64_t> &positions) {
+  std::vector<int> o;
+  for (size_t i = 0; i < m.size(); ++i)
+    if (std::find(positions.begin(), positions.end(), (int64_t)i) == positions.end()) o.push_back(m[i]);
+  return o;
+}
+
 // Propagates D-dim maps through broadcasts, reductions and elementwise ops.
 void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
   Func &f = *A.f;
@@ -940,6 +954,14 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
   if (hasTranspose) {
     for (Value *v : f.returns)
       if (v->type.tensor && v->type.shape == A.D && !exclude.count(v)) A.map[v] = all;
+    // a reducing group whose results are all reduced: the first reduction's
+    // input spans the domain (largestShape chose its shape)
+    if (A.map.empty())
+      for (Op *op : f.ops)
+        if ((op->name == "linalg.reduce" || op->name == "hfusion.reduce_with_index") && !op->ins.empty()) {
+          if (op->ins[0]->type.shape == A.D && !exclude.count(op->ins[0])) A.map[op->ins[0]] = all;
+          break;
+        }
   } else {
     for (Value *a : f.args)
       if (a->type.tensor && a->type.shape == A.D && !exclude.count(a)) A.map[a] = all;
@@ -958,8 +980,13 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
           if (std::find(dims.begin(), dims.end(), i) == dims.end()) m.push_back(i);
         return m;
       };
+      // the operand's map is the result's without the broadcast dims (with
+      // identity maps: D minus `dimensions`)
       if (n == "linalg.broadcast") {
-        if (!op->ins.empty()) changed |= setMap(op->ins[0], minus(op->dims), op);
+        if (op->ins.empty()) continue;
+        const Value *o = op->results.empty() ? op->outs[0] : op->results[0];
+        if (A.map.count(o)) changed |= setMap(op->ins[0], dropPositions(A.map[o], op->dims), op);
+        else if (!hasTranspose) changed |= setMap(op->ins[0], minus(op->dims), op);
         continue;
       }
       if (n == "linalg.transpose") {
@@ -981,9 +1008,18 @@ void inferMaps(Analysis &A, const std::set<const Value *> &exclude) {
         }
         continue;
       }
+      // the result's map is the input's without the reduced dims
       if (n == "linalg.reduce" || n == "hfusion.reduce_with_index") {
-        for (auto *o : op->outs) changed |= setMap(o, minus(op->dims), op);
-        for (auto *o : op->results) changed |= setMap(o, minus(op->dims), op);
+        const Value *x = op->ins.empty() ? nullptr : op->ins[0];
+        if (x && A.map.count(x)) {
+          const std::vector<int> mo = dropPositions(A.map[x], op->dims);
+          for (auto *o : op->outs) changed |= setMap(o, mo, op);
+          for (auto *o : op->results) changed |= setMap(o, mo, op);
+          for (auto *i : op->ins) changed |= setMap(i, A.map[x], op);
+        } else if (!hasTranspose) {
+          for (auto *o : op->outs) changed |= setMap(o, minus(op->dims), op);
+          for (auto *o : op->results) changed |= setMap(o, minus(op->dims), op);
+        }
         continue;
       }
       if (n == "linalg.generic" && genericIsElementwise(op)) {
@@ -1059,9 +1095,14 @@ std::vector<int64_t> largestShape(const Func &f, const std::set<const Value *> &
   bool hasTranspose = false;
   for (auto *op : f.ops) hasTranspose |= op->name == "linalg.transpose";
   if (hasTranspose) {
-    // the domain is the results' shape (results are stored contiguously)
+    // the domain is the results' shape (results are stored contiguously), or
+    // in a group whose results are reduced, the first reduction's input
     for (auto *r : f.returns)
       if (r->type.tensor && r->type.shape.size() == best.size()) return r->type.shape;
+    for (auto *op : f.ops)
+      if ((op->name == "linalg.reduce" || op->name == "hfusion.reduce_with_index") && !op->ins.empty() &&
+          op->ins[0]->type.shape.size() == best.size())
+        return op->ins[0]->type.shape;
     return best;
   }
   for (auto *op : f.ops) for (auto *v : op->results)
@@ -1256,15 +1297,21 @@ struct RowEmitter {
     return costly.count(fn) || op->name == "arith.divf" || op->name == "linalg.div";
   }
 
-  // Sums whose result reaches an integer-typed group output are folded in the
-  // reference's serial order (bit-exact integer outputs depend on it).
+  // Float sums are folded in the reference's serial order (the CPU loop's
+  // left-to-right fold from the init) wherever the row fits the serial
+  // schedule (at most 4096 elements: 4 resident rows per wave), and always
+  // when the result reaches an integer-typed group output (bit-exact integer
+  // outputs depend on it).  Wider rows use tree order.
   void markOrdered() {
     Func &f = *A.f;
     std::set<const Value *> intOut;
     for (auto *r : f.returns) if (isInt(r->type.elem)) intOut.insert(r);
+    const int64_t width = A.D.empty() ? 1 : A.D.back();
+    const bool everywhere = opt.orderedFloatSums == 1 || (opt.orderedFloatSums < 0 && width <= 4096);
     for (Op *op : f.ops) {
       if (op->name != "linalg.reduce" || op->combiner != "arith.addf") continue;
-      bool reaches = opt.orderedFloatSums;
+      if (op->results.empty() || op->results[0]->type.elem != Elem::F32) continue;
+      bool reaches = everywhere;
       std::vector<const Value *> stack(op->results.begin(), op->results.end());
       std::set<const Value *> seen;
       while (!stack.empty() && !reaches) {
@@ -2928,6 +2975,198 @@ static void flattenReshapeGroup(Func &f) {
       for (Value *v : *lst) flat(v);
 }
 
+// Reshapes (tensor.expand_shape / collapse_shape) inside a group that also
+// broadcasts or reduces.  A reshape of row-major data keeps the element
+// order, so it is a view; what it changes is which dims the reduce and
+// broadcast ops name.  The full-size tensors' shapes are refined to one
+// common factorisation, the union of their dim boundaries (which must nest:
+// [24,512,16,12] and [24,512,192] refine to [24,512,16,12]).  Every tensor
+// is re-typed onto the fine dims it spans (unit dims dropped), the
+// `dimensions` of reduce and broadcast ops are rewritten on those dims, and
+// the reshapes vanish; the normal domain inference and collapsing follow.
+// The reference admits reshapes into LAST_AXIS_PBR, ANY_PBR and ANY_PB
+// groups (bishengir/lib/Dialect/HFusion/Transforms/OpFusion/
+// FusibleHelper.cpp:617-629); its model-derived group
+// bishengir/test/Dialect/HFusion/hfusion-pipeline.mlir:56-125 collapses
+// [24,512,16,12] to [24,512,192] before row sums and expands [24,512] to
+// [24,512,1,1] after them.
+static void resolveReshapes(Func &f) {
+  auto isReshape = [](const Op *op) { return op->name == "tensor.expand_shape" || op->name == "tensor.collapse_shape"; };
+  bool any = false;
+  for (const Op *op : f.ops) any |= isReshape(op);
+  if (!any) return;
+  for (const Op *op : f.ops)
+    if (op->name == "linalg.transpose" || op->name == "linalg.generic")
+      unsupported(op, "a reshape beside a transpose or linalg.generic in a reducing or broadcasting group");
+  std::vector<Value *> vals;
+  std::set<const Value *> seen;
+  auto add = [&](Value *v) { if (v->type.tensor && seen.insert(v).second) vals.push_back(v); };
+  for (Value *a : f.args) add(a);
+  for (Op *op : f.ops)
+    for (auto *lst : {&op->ins, &op->outs, &op->operands, &op->results})
+      for (Value *v : *lst) add(v);
+  int64_t N = 1;
+  for (const Value *v : vals) N = std::max(N, v->type.numel());
+  // fine dims, outermost first: the ratios of consecutive suffix products
+  std::set<int64_t> cuts;
+  for (const Value *v : vals) {
+    if (v->type.numel() != N) continue;
+    int64_t s = 1;
+    for (size_t i = v->type.shape.size(); i-- > 0;) {
+      s *= v->type.shape[i];
+      if (s > 1) cuts.insert(s);
+    }
+  }
+  std::vector<int64_t> F;
+  int64_t prev = 1;
+  for (int64_t c : cuts) {
+    if (c % prev) throw CompileError("unsupported: reshapes whose dim boundaries do not nest (" + std::to_string(prev) + " and " + std::to_string(c) + " elements)");
+    F.insert(F.begin(), c / prev);
+    prev = c;
+  }
+  using Layout = std::vector<std::vector<int>>; // fine dims spanned by each tensor dim
+  auto flat = [](const Layout &L) {
+    std::vector<int> o;
+    for (auto &g : L) o.insert(o.end(), g.begin(), g.end());
+    return o;
+  };
+  // the fine dims `fl` cut into consecutive runs of the sizes `shape`
+  auto split = [&](const std::vector<int> &fl, const std::vector<int64_t> &shape, Layout &out) {
+    out.assign(shape.size(), {});
+    size_t k = 0;
+    for (size_t i = 0; i < shape.size(); ++i) {
+      int64_t p = 1;
+      while (p < shape[i] && k < fl.size()) { out[i].push_back(fl[k]); p *= F[fl[k]]; ++k; }
+      if (p != shape[i]) return false;
+    }
+    return k == fl.size();
+  };
+  std::map<const Value *, Layout> lay;
+  bool changed = false;
+  auto set = [&](const Value *v, const Layout &L, const Op *op) {
+    if (!v->type.tensor) return;
+    auto it = lay.find(v);
+    if (it != lay.end()) {
+      if (it->second != L) unsupported(op, "a tensor placed on two different dims across reshapes");
+      return;
+    }
+    if (L.size() != v->type.shape.size()) unsupported(op, "internal: layout rank");
+    lay[v] = L;
+    changed = true;
+  };
+  std::vector<int> all;
+  for (size_t d = 0; d < F.size(); ++d) all.push_back((int)d);
+  for (const Value *v : vals) {
+    Layout L;
+    if (v->type.numel() == 1) set(v, Layout(v->type.shape.size()), nullptr);
+    else if (v->type.numel() == N && split(all, v->type.shape, L)) set(v, L, nullptr);
+  }
+  auto minus = [](const Layout &L, const std::vector<int64_t> &dims) {
+    Layout o;
+    for (size_t i = 0; i < L.size(); ++i)
+      if (std::find(dims.begin(), dims.end(), (int64_t)i) == dims.end()) o.push_back(L[i]);
+    return o;
+  };
+  changed = true;
+  while (changed) {
+    changed = false;
+    for (Op *op : f.ops) {
+      const std::string &n = op->name;
+      if (isReshape(op)) {
+        const Value *src = op->operands.at(0), *dst = op->results.at(0);
+        Layout L;
+        if (lay.count(src) && !lay.count(dst)) {
+          if (!split(flat(lay[src]), dst->type.shape, L))
+            unsupported(op, "reshape splits a dim that the group's full-size tensors keep whole");
+          set(dst, L, op);
+        } else if (lay.count(dst) && !lay.count(src)) {
+          if (!split(flat(lay[dst]), src->type.shape, L))
+            unsupported(op, "reshape splits a dim that the group's full-size tensors keep whole");
+          set(src, L, op);
+        } else if (lay.count(src) && flat(lay[src]) != flat(lay[dst])) {
+          unsupported(op, "reshape between tensors on different dims");
+        }
+        continue;
+      }
+      if (n == "linalg.broadcast") {
+        const Value *o = op->results.empty() ? op->outs.at(0) : op->results[0];
+        if (!lay.count(o) && lay.count(op->outs.at(0))) o = op->outs[0];
+        if (!lay.count(o)) continue;
+        const Layout Lo = lay[o];
+        set(op->ins.at(0), minus(Lo, op->dims), op);
+        set(op->outs[0], Lo, op);
+        for (auto *v : op->results) set(v, Lo, op);
+        continue;
+      }
+      if (n == "linalg.reduce" || n == "hfusion.reduce_with_index") {
+        const Value *known = nullptr;
+        for (auto *v : op->ins) if (lay.count(v)) known = v;
+        if (!known) continue;
+        const Layout Li = lay[known];
+        for (auto *v : op->ins) set(v, Li, op);
+        const Layout Lo = minus(Li, op->dims);
+        for (auto *v : op->outs) set(v, Lo, op);
+        for (auto *v : op->results) set(v, Lo, op);
+        continue;
+      }
+      if (n == "linalg.fill" || isElementwiseOp(op)) {
+        std::vector<const Value *> vs;
+        for (auto *lst : {&op->ins, &op->operands, &op->outs, &op->results})
+          for (auto *v : *lst) if (v->type.tensor && v->type.numel() != 1) vs.push_back(v);
+        const Value *known = nullptr;
+        for (auto *v : vs) if (lay.count(v)) { known = v; break; }
+        if (!known) continue;
+        const Layout L = lay[known];
+        for (auto *v : vs) if (v->type.shape == known->type.shape) set(v, L, op);
+      }
+    }
+  }
+  for (const Value *v : vals)
+    if (!lay.count(v) && (!v->users.empty() || std::find(f.returns.begin(), f.returns.end(), v) != f.returns.end()))
+      throw CompileError("unsupported: cannot place tensor " + v->name + " (" + v->type.str() + ") on the group's dims across its reshapes");
+  // dims of reduce / broadcast ops on the fine shapes (they need the old layouts)
+  for (Op *op : f.ops) {
+    if (op->name == "linalg.reduce" || op->name == "hfusion.reduce_with_index") {
+      const std::vector<int> fl = flat(lay.at(op->ins.at(0)));
+      const Layout &Li = lay.at(op->ins[0]);
+      std::vector<int64_t> nd;
+      for (size_t k = 0; k < fl.size(); ++k)
+        for (int64_t d : op->dims)
+          if (d >= 0 && d < (int64_t)Li.size() && std::count(Li[d].begin(), Li[d].end(), fl[k])) nd.push_back((int64_t)k);
+      if (nd.empty()) unsupported(op, "reduction over unit dimensions only");
+      op->dims = nd;
+    } else if (op->name == "linalg.broadcast") {
+      const Value *o = op->results.empty() ? op->outs.at(0) : op->results[0];
+      const std::vector<int> fo = flat(lay.at(o)), fi = flat(lay.at(op->ins.at(0)));
+      std::vector<int64_t> nd;
+      for (size_t k = 0; k < fo.size(); ++k)
+        if (std::find(fi.begin(), fi.end(), fo[k]) == fi.end()) nd.push_back((int64_t)k);
+      op->dims = nd;
+    }
+  }
+  // the reshapes become aliases of their sources
+  for (size_t i = 0; i < f.ops.size();) {
+    Op *op = f.ops[i];
+    if (!isReshape(op)) { ++i; continue; }
+    Value *src = op->operands.at(0), *dst = op->results.at(0);
+    auto &su = src->users;
+    su.erase(std::remove(su.begin(), su.end(), op), su.end());
+    for (Op *u : dst->users) {
+      for (auto *lst : {&u->ins, &u->outs, &u->operands})
+        for (Value *&v : *lst) if (v == dst) v = src;
+      su.push_back(u);
+    }
+    for (Value *&r : f.returns) if (r == dst) r = src;
+    f.ops.erase(f.ops.begin() + i);
+  }
+  for (const auto &kv : lay) {
+    Value *v = const_cast<Value *>(kv.first);
+    std::vector<int64_t> s;
+    for (int d : flat(kv.second)) s.push_back(F[d]);
+    v->type.shape = s;
+  }
+}
+
 // linalg.generic with a reduction over the last loop dim whose region ends
 // in `%y = <combine> %v, %out` (or `%out, %v`), %out read nowhere else:
 // rewritten as an elementwise linalg.generic computing %v over the full loop
@@ -3322,9 +3561,12 @@ struct ColumnEmitter {
     if (xi) ensure(xi);
     Elem t = x->type.elem, it = op->outs[1]->type.elem;
     std::string kindS = op->angleKind.empty() ? op->attr("reduce_kind", "max") : op->angleKind;
-    std::string T = ctype(t), IT = ctype(it);
+    // bf16 / f16 fold in f32: the conversion is exact and monotone, and the
+    // folded value is one of the inputs or the init, so it converts back exactly
+    const bool narrow = t == Elem::BF16 || t == Elem::F16;
+    std::string T = narrow ? "float" : ctype(t), IT = ctype(it);
     std::string fold, cmp;
-    if (t == Elem::F32) {
+    if (t == Elem::F32 || narrow) {
       if (kindS == "max") { fold = "hf::maximumf(X, V)"; cmp = "(R_ > V)"; }
       else if (kindS == "min") { fold = "hf::minimumf(X, V)"; cmp = "(R_ < V)"; }
       else unsupported(op, "reduce_with_index kind '" + kindS + "' on floats");
@@ -3346,14 +3588,20 @@ struct ColumnEmitter {
       return e;
     };
     std::string nv = fresh(), ni = fresh();
-    body << "    " << T << " " << nv << " = " << initOf(op, op->outs[0], t, "0") << ";\n"
+    const std::string init = initOf(op, op->outs[0], t, "0");
+    body << "    " << T << " " << nv << " = " << (narrow ? castExpr(init, t, Elem::F32, false) : init) << ";\n"
          << "    " << IT << " " << ni << " = " << initOf(op, op->outs[1], it, "0") << ";\n"
          << "    for (int64_t r = 0; r < " << RK << "ll; ++r) {\n"
-         << "      const " << T << " x_ = " << at(x) << ";\n"
+         << "      const " << T << " x_ = " << (narrow ? castExpr(at(x), t, Elem::F32, false) : at(x)) << ";\n"
          << "      const " << T << " R_ = " << repl(repl(fold, "X", "x_"), "V", nv) << ";\n"
          << "      if (" << repl(cmp, "V", nv) << ") " << ni << " = (" << IT << ")("
          << (xi ? at(xi) : std::string("r")) << ");\n"
          << "      " << nv << " = R_;\n    }\n";
+    if (narrow) {
+      const std::string nn = fresh();
+      body << "    const " << ctype(t) << " " << nn << " = " << castExpr(nv, Elem::F32, t, false) << ";\n";
+      nv = nn;
+    }
     val[op->results[0]] = {nv, false};
     val[op->results[1]] = {ni, false};
   }
@@ -3415,6 +3663,12 @@ struct ColumnEmitter {
       if (nmo == "linalg.broadcast") {
         ensure(op->ins[0]);
         val[op->results[0]] = val[op->ins[0]];
+        continue;
+      }
+      if (nmo == "linalg.transpose") {
+        // the same function of the point: the operand's map holds the permutation
+        ensure(op->ins[0]);
+        val[op->results.at(0)] = val[op->ins[0]];
         continue;
       }
       if (nmo == "linalg.reduce") { emitReduce(op, RK); continue; }
@@ -3717,6 +3971,7 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     } else {
       foldTrivialTransposes(f);
       flattenReshapeGroup(f);
+      resolveReshapes(f);
       A.D = largestShape(f, {});
       if (A.D.empty()) {
         // rank-0 tensors only: one element
@@ -3729,7 +3984,9 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
       if (kind == "LAST_AXIS_PBR" || kind == "REDUCE_WITH_INDEX") {
         // row programs take rank <= 2 groups reducing the last dim; a higher
         // rank collapses first; anything else is a column program
-        bool rows = kind == "LAST_AXIS_PBR";
+        // (a transposed operand: the column program, which indexes every
+        // tensor through its own map)
+        bool rows = kind == "LAST_AXIS_PBR" && !findOp(f, [](const Op *o) { return o->name == "linalg.transpose"; });
         if (rows && (A.D.size() > 2 || !reducesLastDimOnly(A))) {
           collapseDomain(A);
           rows = A.D.size() <= 2 && reducesLastDimOnly(A);

@@ -49,7 +49,11 @@ struct KernelPlan {
 };
 
 struct LowerOptions {
-  bool orderedFloatSums = false; // force serial-order fp sums everywhere
+  // fp sums in the reference's serial order: 1 everywhere the row fits the
+  // serial schedule's registers, 0 only where an integer output depends on
+  // the sum (tree order elsewhere); the default (-1) is the serial order for
+  // rows of at most 4096 elements
+  int orderedFloatSums = -1;
   bool rmsqKernel = false;       // RMSNorm + dynamic quantisation through hf_rmsq.h
 };
 

@@ -739,6 +739,11 @@ class Interp:
                 lit = dm.group(1)
             if lit in ("true", "false"):
                 val = lit == "true"
+            elif lit.lower().startswith("0x") and elem in ("bf16", "f16"):
+                # hex literal of a 16-bit float: its bit pattern
+                arr = np.array(int(lit, 16), np.uint16)
+                env[res] = T(arr if shape is None else np.broadcast_to(arr, shape).copy(), elem)
+                return
             elif lit.lower().startswith("0x") and elem in FLOATS:
                 bits = int(lit, 16)
                 val = {"f32": lambda b: np.array([b], np.uint32).view(np.float32)[0],
@@ -1130,12 +1135,12 @@ class Interp:
         _, elem = parse_type(to or ty)
         vals = [env[n].a for n in names]
         f32 = elem == "f32"
-        if op in ("arith.index_cast", "arith.index_castui", "arith.extsi", "arith.extui", "arith.trunci"):
-            v = np.array(int(vals[0]), NP[elem])
-        elif op in ("arith.sitofp", "arith.uitofp"):
-            v = np.array(float(vals[0]), NP[elem])
-        elif op in ("arith.extf", "arith.truncf"):
-            v = np.array(vals[0], NP[elem])
+        if op in ("arith.index_cast", "arith.index_castui", "arith.extsi", "arith.extui", "arith.trunci",
+                  "arith.sitofp", "arith.uitofp", "arith.extf", "arith.truncf"):
+            # scalars and tensors alike (a rank-0 tensor<i64> -> tensor<bf16>
+            # gives the bf16 bit pattern of the value)
+            env[res] = convert(env[names[0]], elem, unsigned=op in ("arith.index_castui", "arith.extui", "arith.uitofp"))
+            return
         else:
             a = [np.float32(x) if f32 else x for x in vals]
             v = {"arith.addf": lambda: a[0] + a[1], "arith.subf": lambda: a[0] - a[1],
@@ -1194,7 +1199,15 @@ class Interp:
         ii = None
         if idx_in is not None:
             ii = _contig(np.transpose(idx_in.a, [d] + keep).astype(np.int64).reshape(K, N))
-        if x.elem == "f32":
+        if x.elem in ("bf16", "f16"):
+            # the region's maximumf / cmpf on 16-bit floats run on their exact
+            # f32 extensions; the folded value converts back exactly
+            vf = _contig(to_f32(T(val, x.elem)).astype(np.float32))
+            xf = _contig(to_f32(T(xt.reshape(K, N), x.elem)).astype(np.float32))
+            lib().hfref_reduce_with_index_f32({"max": 0, "min": 1}[kind], ptr(xf),
+                                              ptr(ii) if ii is not None else None, ptr(vf), ptr(idx), K, N)
+            val = from_f32(vf, x.elem)
+        elif x.elem == "f32":
             lib().hfref_reduce_with_index_f32({"max": 0, "min": 1}[kind], ptr(xt.reshape(K, N)),
                                               ptr(ii) if ii is not None else None, ptr(val), ptr(idx), K, N)
         else:

@@ -941,6 +941,214 @@ def sort_ops():
   }}""")
     return "module {\n" + "\n".join(funcs) + "\n}\n"
 
+
+def sigmoid_grad_sums(b=24, s=512, h=16, w=12, name="sig_sums"):
+    """The model-derived LAST_AXIS_PBR group of
+    bishengir/test/Dialect/HFusion/hfusion-pipeline.mlir:56-125 at its shape
+    [24, 512, 16, 12] (parametrised): a sigmoid-gradient chain in bf16 over
+    row-broadcast [B, S, 1, 1] operands collapsed to [B, S], four f32 row sums
+    over the trailing [H, W] (two of them through a collapse to [B, S, H*W]),
+    two results expanded back to [B, S, 1, 1] and cast to bf16."""
+    X, XB = _T([b, s, h, w], "bf16"), _T([b, s, 1, 1], "bf16")
+    XF, XC = _T([b, s, h, w], "f32"), _T([b, s, h * w], "f32")
+    RB, R2, R4, R4B = _T([b, s], "bf16"), _T([b, s], "f32"), _T([b, s, 1, 1], "f32"), _T([b, s, 1, 1], "bf16")
+    XI = _T([b, s, h, w], "i64")
+    mul = "linalg.elemwise_binary {fun = #linalg.binary_fn<mul>}"
+    add = "linalg.elemwise_binary {fun = #linalg.binary_fn<add>}"
+    rint = "hfusion.cast {round_mode = #hfusion.round_mode<rint>}"
+    red = "linalg.reduce ins({x} : {t}) outs(%zs : {R2}) dimensions = {d}\n      (%in: f32, %init: f32) {{\n        %q = arith.addf %in, %init : f32\n        linalg.yield %q : f32\n      }}"
+    return f"""module {{
+  func.func @{name}(%a0: {X}, %a1: {X}, %a2: {XB}, %a3: {XB}, %a4: {XF}) -> ({R2}, {R2}, {R4}, {R4}, {R4B}, {R4B})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %one_t = arith.constant dense<1> : tensor<i64>
+    %one_i = arith.constant 1 : i64
+    %one = arith.constant 1.000000e+00 : bf16
+    %zero = arith.constant 0.000000e+00 : f32
+    %e = tensor.empty() : {X}
+    %c2 = tensor.collapse_shape %a2 [[0], [1, 2, 3]] : {XB} into {RB}
+    %b2 = linalg.broadcast ins(%c2 : {RB}) outs(%e : {X}) dimensions = [2, 3]
+    %m1 = {mul} ins(%a1, %b2 : {X}, {X}) outs(%e : {X}) -> {X}
+    %c3 = tensor.collapse_shape %a3 [[0], [1, 2, 3]] : {XB} into {RB}
+    %b3 = linalg.broadcast ins(%c3 : {RB}) outs(%e : {X}) dimensions = [2, 3]
+    %ei = tensor.empty() : {XI}
+    %fi = linalg.fill ins(%one_i : i64) outs(%ei : {XI}) -> {XI}
+    %ones = hfusion.cast {{round_mode = #hfusion.round_mode<trunc>}} ins(%fi : {XI}) outs(%e : {X}) -> {X}
+    %m5 = {mul} ins(%b3, %ones : {X}, {X}) outs(%e : {X}) -> {X}
+    %z = {add} ins(%m1, %m5 : {X}, {X}) outs(%e : {X}) -> {X}
+    %nz = linalg.elemwise_unary {{fun = #linalg.unary_fn<negf>}} ins(%z : {X}) outs(%e : {X}) -> {X}
+    %ex = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%nz : {X}) outs(%e : {X}) -> {X}
+    %den = {add} ins(%ex, %one : {X}, bf16) outs(%e : {X}) -> {X}
+    %sig = linalg.elemwise_binary {{fun = #linalg.binary_fn<div>}} ins(%one, %den : bf16, {X}) outs(%e : {X}) -> {X}
+    %one_f = arith.sitofp %one_t : tensor<i64> to tensor<bf16>
+    %bone = linalg.broadcast ins(%one_f : tensor<bf16>) outs(%e : {X}) dimensions = [0, 1, 2, 3]
+    %s12 = {mul} ins(%sig, %ones : {X}, {X}) outs(%e : {X}) -> {X}
+    %s13 = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%bone, %s12 : {X}, {X}) outs(%e : {X}) -> {X}
+    %s14 = {mul} ins(%z, %s13 : {X}, {X}) outs(%e : {X}) -> {X}
+    %s15 = {mul} ins(%ones, %ones : {X}, {X}) outs(%e : {X}) -> {X}
+    %s16 = {add} ins(%s14, %s15 : {X}, {X}) outs(%e : {X}) -> {X}
+    %s17 = {mul} ins(%sig, %s16 : {X}, {X}) outs(%e : {X}) -> {X}
+    %s18 = {mul} ins(%a0, %s17 : {X}, {X}) outs(%e : {X}) -> {X}
+    %s19 = {mul} ins(%s18, %b2 : {X}, {X}) outs(%e : {X}) -> {X}
+    %ef = tensor.empty() : {XF}
+    %f21 = {rint} ins(%s19 : {X}) outs(%ef : {XF}) -> {XF}
+    %f22 = {mul} ins(%f21, %a4 : {XF}, {XF}) outs(%ef : {XF}) -> {XF}
+    %k22 = tensor.collapse_shape %f22 [[0], [1], [2, 3]] : {XF} into {XC}
+    %er = tensor.empty() : {R2}
+    %zs = linalg.fill ins(%zero : f32) outs(%er : {R2}) -> {R2}
+    %r0 = {red.format(x="%k22", t=XC, R2=R2, d="[2]")}
+    %k21 = tensor.collapse_shape %f21 [[0], [1], [2, 3]] : {XF} into {XC}
+    %r1 = {red.format(x="%k21", t=XC, R2=R2, d="[2]")}
+    %p25 = {mul} ins(%s18, %a1 : {X}, {X}) outs(%e : {X}) -> {X}
+    %f26 = {rint} ins(%p25 : {X}) outs(%ef : {XF}) -> {XF}
+    %r2 = {red.format(x="%f26", t=XF, R2=R2, d="[2, 3]")}
+    %x2 = tensor.expand_shape %r2 [[0], [1, 2, 3]] output_shape [{b}, {s}, 1, 1] : {R2} into {R4}
+    %f27 = {rint} ins(%s18 : {X}) outs(%ef : {XF}) -> {XF}
+    %r3 = {red.format(x="%f27", t=XF, R2=R2, d="[2, 3]")}
+    %x3 = tensor.expand_shape %r3 [[0], [1, 2, 3]] output_shape [{b}, {s}, 1, 1] : {R2} into {R4}
+    %eb = tensor.empty() : {R4B}
+    %o4 = {rint} ins(%x2 : {R4}) outs(%eb : {R4B}) -> {R4B}
+    %o5 = {rint} ins(%x3 : {R4}) outs(%eb : {R4B}) -> {R4B}
+    return %r0, %r1, %x2, %x3, %o4, %o5 : {R2}, {R2}, {R4}, {R4}, {R4B}, {R4B}
+  }}
+}}
+"""
+
+
+def reshape_transpose_ops():
+    """Reshapes and transposes inside groups that reduce or broadcast (the
+    reference admits both into LAST_AXIS_PBR / ANY_PBR / ANY_PB groups,
+    FusibleHelper.cpp:617-629), one function each."""
+    f = []
+    # ANY_PB: a [R,1,1] operand collapsed to [R] and broadcast over a
+    # collapsed [R, 8*64] view of x; the product expanded back to x's shape
+    X, XC, Bv, BC = _T([16, 8, 64], "f32"), _T([16, 512], "f32"), _T([16, 1, 1], "f32"), _T([16], "f32")
+    f.append(f"""  func.func @rs_bcast_pb(%x: {X}, %b: {Bv}, %o: {X}) -> {X}
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %xc = tensor.collapse_shape %x [[0], [1, 2]] : {X} into {XC}
+    %bc = tensor.collapse_shape %b [[0, 1, 2]] : {Bv} into {BC}
+    %e = tensor.empty() : {XC}
+    %bb = linalg.broadcast ins(%bc : {BC}) outs(%e : {XC}) dimensions = [1]
+    %m = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%xc, %bb : {XC}, {XC}) outs(%e : {XC}) -> {XC}
+    %me = tensor.expand_shape %m [[0], [1, 2]] output_shape [16, 8, 64] : {XC} into {X}
+    %r = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%me, %x : {X}, {X}) outs(%o : {X}) -> {X}
+    return %r : {X}
+  }}""")
+    # ANY_PBR: a sum over a collapsed middle pair of dims, expanded to [6,1,30]
+    X, XC, O2, O3 = _T([6, 10, 20, 30], "f32"), _T([6, 200, 30], "f32"), _T([6, 30], "f32"), _T([6, 1, 30], "f32")
+    f.append(f"""  func.func @rs_sum_mid(%x: {X}, %o: {O3}) -> {O3}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %e = tensor.empty() : {X}
+    %sq = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%x, %x : {X}, {X}) outs(%e : {X}) -> {X}
+    %c = tensor.collapse_shape %sq [[0], [1, 2], [3]] : {X} into {XC}
+    %e1 = tensor.empty() : {O2}
+    %i = linalg.fill ins(%z : f32) outs(%e1 : {O2}) -> {O2}
+    %s = linalg.reduce {{arith.addf}} ins(%c : {XC}) outs(%i : {O2}) dimensions = [1]
+    %x3 = tensor.expand_shape %s [[0, 1], [2]] output_shape [6, 1, 30] : {O2} into {O3}
+    %r = hfusion.elemwise_unary {{fun = #hfusion.unary_fn<sqrt>}} ins(%x3 : {O3}) outs(%o : {O3}) -> {O3}
+    return %r : {O3}
+  }}""")
+    # LAST_AXIS_PBR: transpose -> mul -> row sum
+    X, XT, O = _T([300, 64], "f32"), _T([64, 300], "f32"), _T([64], "f32")
+    f.append(f"""  func.func @tr_mul_sum(%x: {X}, %y: {XT}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [1, 0]
+    %e1 = tensor.empty() : {XT}
+    %m = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%t, %y : {XT}, {XT}) outs(%e1 : {XT}) -> {XT}
+    %i = linalg.fill ins(%z : f32) outs(%o : {O}) -> {O}
+    %s = linalg.reduce {{arith.addf}} ins(%m : {XT}) outs(%i : {O}) dimensions = [1]
+    return %s : {O}
+  }}""")
+    # argmax along the last axis of a transposed bf16 tensor
+    X, XT, V, I = _T([500, 40], "bf16"), _T([40, 500], "bf16"), _T([40], "bf16"), _T([40], "i32")
+    f.append(f"""  func.func @tr_argmax(%x: {X}, %val: {V}, %idx: {I}) -> ({V}, {I})
+      {_ATTRS.format(kind='LAST_AXIS_PBR')} {{
+    %c0 = arith.constant 0 : i32
+    %ninf = arith.constant 0xFF80 : bf16
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [1, 0]
+    %v0 = linalg.fill ins(%ninf : bf16) outs(%val : {V}) -> {V}
+    %i0 = linalg.fill ins(%c0 : i32) outs(%idx : {I}) -> {I}
+    %r:2 = hfusion.reduce_with_index <max> ins(%t : {XT}) outs(%v0, %i0 : {V}, {I}) dimensions = [1] -> {V}, {I}
+    return %r#0, %r#1 : {V}, {I}
+  }}""")
+    # a rank-3 transpose feeding a max over the middle axis, with a bias
+    # broadcast along the transposed result's last axis
+    X, XT, Bv, O = _T([12, 40, 70], "f32"), _T([70, 12, 40], "f32"), _T([70], "f32"), _T([70, 40], "f32")
+    f.append(f"""  func.func @tr3_max_bias(%x: {X}, %b: {Bv}, %o: {O}) -> {O}
+      {_ATTRS.format(kind='ANY_PBR')} {{
+    %ninf = arith.constant 0xFF800000 : f32
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [2, 0, 1]
+    %e1 = tensor.empty() : {XT}
+    %bb = linalg.broadcast ins(%b : {Bv}) outs(%e1 : {XT}) dimensions = [1, 2]
+    %e2 = tensor.empty() : {XT}
+    %a = linalg.elemwise_binary {{fun = #linalg.binary_fn<add>}} ins(%t, %bb : {XT}, {XT}) outs(%e2 : {XT}) -> {XT}
+    %i = linalg.fill ins(%ninf : f32) outs(%o : {O}) -> {O}
+    %m = linalg.reduce {{arith.maximumf}} ins(%a : {XT}) outs(%i : {O}) dimensions = [1]
+    return %m : {O}
+  }}""")
+    # ANY_PB: a transposed operand minus a broadcast row vector
+    X, XT, Bv = _T([64, 100], "f32"), _T([100, 64], "f32"), _T([64], "f32")
+    f.append(f"""  func.func @tr_bcast_sub(%x: {X}, %b: {Bv}, %o: {XT}) -> {XT}
+      {_ATTRS.format(kind='ANY_PB')} {{
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [1, 0]
+    %e1 = tensor.empty() : {XT}
+    %bb = linalg.broadcast ins(%b : {Bv}) outs(%e1 : {XT}) dimensions = [0]
+    %r = linalg.elemwise_binary {{fun = #linalg.binary_fn<sub>}} ins(%t, %bb : {XT}, {XT}) outs(%o : {XT}) -> {XT}
+    return %r : {XT}
+  }}""")
+    return "module {\n" + "\n".join(f) + "\n}\n"
+
+
+RS_TR_OPS = ["rs_bcast_pb", "rs_sum_mid", "tr_mul_sum", "tr_argmax", "tr3_max_bias", "tr_bcast_sub"]
+
+
+def host_reshape_sum(b=8, h=16, w=32):
+    """Un-fused host IR: exp -> collapse_shape -> row sum -> expand_shape ->
+    log.  The front-end fuses it into one LAST_AXIS_PBR group whose reshapes
+    the lowering resolves."""
+    X, XC, R, R2 = _T([b, h, w], "f32"), _T([b, h * w], "f32"), _T([b], "f32"), _T([b, 1], "f32")
+    return f"""module {{
+  func.func @prog_rs_exp_sum_log(%x: {X}, %o: {R2}) -> {R2}
+      attributes {{hacc.function_kind = #hacc.function_kind<HOST>}} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %e = tensor.empty() : {X}
+    %a = linalg.elemwise_unary {{fun = #linalg.unary_fn<exp>}} ins(%x : {X}) outs(%e : {X}) -> {X}
+    %c = tensor.collapse_shape %a [[0], [1, 2]] : {X} into {XC}
+    %e1 = tensor.empty() : {R}
+    %i = linalg.fill ins(%z : f32) outs(%e1 : {R}) -> {R}
+    %s = linalg.reduce {{arith.addf}} ins(%c : {XC}) outs(%i : {R}) dimensions = [1]
+    %x2 = tensor.expand_shape %s [[0, 1]] output_shape [{b}, 1] : {R} into {R2}
+    %r = linalg.elemwise_unary {{fun = #linalg.unary_fn<log>}} ins(%x2 : {R2}) outs(%o : {R2}) -> {R2}
+    return %r : {R2}
+  }}
+}}
+"""
+
+
+def host_transpose_sum(m=300, n=64):
+    """Un-fused host IR: transpose -> mul -> row sum (one fused group)."""
+    X, XT, O = _T([m, n], "f32"), _T([n, m], "f32"), _T([n], "f32")
+    return f"""module {{
+  func.func @prog_tr_mul_sum(%x: {X}, %y: {XT}, %o: {O}) -> {O}
+      attributes {{hacc.function_kind = #hacc.function_kind<HOST>}} {{
+    %z = arith.constant 0.000000e+00 : f32
+    %e = tensor.empty() : {XT}
+    %t = linalg.transpose ins(%x : {X}) outs(%e : {XT}) permutation = [1, 0]
+    %e1 = tensor.empty() : {XT}
+    %m = linalg.elemwise_binary {{fun = #linalg.binary_fn<mul>}} ins(%t, %y : {XT}, {XT}) outs(%e1 : {XT}) -> {XT}
+    %i = linalg.fill ins(%z : f32) outs(%o : {O}) -> {O}
+    %s = linalg.reduce {{arith.addf}} ins(%m : {XT}) outs(%i : {O}) dimensions = [1]
+    return %s : {O}
+  }}
+}}
+"""
+
+
 def entries():
     """name -> IR text of every group the tests run: the product groups plus
     the parity cases below."""
@@ -1016,6 +1224,11 @@ def entries():
     e["generic_reduce"] = generic_reduce()
     e["any_pbr_ops"] = any_pbr_ops()
     e["transpose_ops"] = transpose_ops()
+    e["sig_sums"] = sigmoid_grad_sums()
+    e["sig_sums_small"] = sigmoid_grad_sums(3, 40, 4, 6, name="sig_sums_small")
+    e["rs_tr_ops"] = reshape_transpose_ops()
+    e["prog_rs_exp_sum_log"] = host_reshape_sum()
+    e["prog_tr_mul_sum"] = host_transpose_sum()
     e["sort_ops"] = sort_ops()
     e["prog_neg_sort_scale"] = neg_sort_scale()
     # dynamic row counts (compiled per size: DynamicGroup / option dyn=...)
