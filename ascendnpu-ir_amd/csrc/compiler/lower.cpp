@@ -3853,6 +3853,27 @@ KernelPlan lowerRmsQuant(Analysis &A, const RmsqMatch &m, const std::string &kna
   return p;
 }
 
+// The chain-wave kernel for the pattern (hf_rmsn.h, option rmsn_kernel=1):
+// the serial chain in a wave of its own, the product maxima reduced beside
+// it, the quantisation from registers.
+KernelPlan lowerRmsNorm(Analysis &A, const RmsqMatch &m, const std::string &kname) {
+  const int64_t R = A.D[0], C = A.D[1];
+  KernelPlan p;
+  p.kernelName = kname;
+  p.kind = "LAST_AXIS_PBR";
+  p.variant = "rmsnorm-quant: serial-order fp32 sum in a chain wave, product maxima beside it";
+  std::ostringstream k;
+  k << "extern \"C\" __global__ __launch_bounds__(576) void " << kname << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
+    << "  hf::rmsn_rows<" << C << ", " << m.lo << ", " << m.hi << ">((const uint16_t*)p" << m.x << ", (const uint16_t*)p"
+    << m.gamma << ", (int8_t*)" << resultPtr(A, m.qRes) << ", (float*)" << resultPtr(A, m.sRes) << ", " << R << "ll, "
+    << floatLit((float)m.s0) << ", " << floatLit((float)m.K) << ", " << floatLit((float)m.eps) << ", "
+    << floatLit((float)m.a0) << ", " << floatLit((float)m.qd) << ");\n}\n";
+  p.source = k.str();
+  p.grid[0] = (unsigned)((R + 31) / 32);
+  p.block[0] = 576;
+  return p;
+}
+
 // Every linalg.reduce of the group folds exactly the last dim of its input,
 // which spans the whole domain.
 bool reducesLastDimOnly(const Analysis &A) {
@@ -3994,6 +4015,8 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
         RmsqMatch rq;
         if (rows && opt.rmsqKernel && matchRmsQuant(A, rq)) {
           p = lowerRmsQuant(A, rq, kname);
+        } else if (rows && opt.rmsnKernel && matchRmsQuant(A, rq)) {
+          p = lowerRmsNorm(A, rq, kname);
         } else if (rows) {
           RowEmitter e(A, opt);
           p = e.run(kname, "LAST_AXIS_PBR");
@@ -4029,7 +4052,7 @@ std::string emitTranslationUnit(const std::vector<KernelPlan> &plans) {
   std::ostringstream s;
   s << "// Generated by bishengir-compile --target=mi355x (ConvertHFusionToHIP).\n"
     << "#include \"hf_ops.h\"\n#include \"hf_row.h\"\n#include \"hf_argmax.h\"\n#include \"hf_mmad.h\"\n#include \"hf_misc.h\"\n"
-    << "#include \"hf_rmsq.h\"\n#include \"hf_sort.h\"\n\n";
+    << "#include \"hf_rmsq.h\"\n#include \"hf_rmsn.h\"\n#include \"hf_sort.h\"\n\n";
   for (auto &p : plans) s << "// group @" << p.funcName << ": " << p.kind << " (" << p.variant << ")\n" << p.source << "\n";
   return s.str();
 }

@@ -1239,6 +1239,9 @@ def entries():
     # the same groups through the opt-in one-wave-per-row kernel (hf_rmsq.h)
     for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3", "rmsnorm_quant_ragged"):
         e[n + "_rmsq"] = e[n]
+    # ... and through the opt-in chain-wave kernel (hf_rmsn.h)
+    for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3"):
+        e[n + "_rmsn"] = e[n]
     e["rank0"] = """module {
   func.func @rank0(%a: tensor<f32>, %b: tensor<f32>) -> tensor<f32>
       """ + _ATTRS.format(kind='PURE_ELEMWISE') + """ {
@@ -1287,4 +1290,6 @@ def options(name):
     a dynamic group: its first prebuilt row count)."""
     if name in DYN_ROWS:
         return dyn_options(name, DYN_ROWS[name][0])
-    return "rmsq_kernel=1" if name.endswith("_rmsq") else ""
+    if name.endswith("_rmsq"):
+        return "rmsq_kernel=1"
+    return "rmsn_kernel=1" if name.endswith("_rmsn") else ""

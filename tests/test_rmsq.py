@@ -61,12 +61,17 @@ def stress_rows(rows=256, seed=0x524D53):
 
 
 @pytest.mark.gpu
-def test_rmsq_stress_rows_bit_exact(gpu):
-    print("[case] rmsnorm_quant_256 stress rows", flush=True)
+@pytest.mark.parametrize("name", ["rmsnorm_quant_256_rmsq", "rmsnorm_quant_256", "rmsnorm_quant_256_rmsn"])
+def test_rmsq_stress_rows_bit_exact(gpu, name):
+    """The stress rows through the three kernels of the pattern: the opt-in
+    parallel sum (hf_rmsq.h), the generic row program (the default) and the
+    opt-in chain-wave kernel (hf_rmsn.h, whose exact re-execution takes the
+    NaN, infinite, overflowing and zero rows)."""
+    print(f"[case] {name} stress rows", flush=True)
     x = stress_rows()
     g = I.uniform_bf16(I.SEED_BASE + 77, (C,), 0.5, 1.5)
     args = [x, g, np.zeros((256, C), np.int8), np.zeros(256, np.float32)]
-    q, s = run_gpu("rmsnorm_quant_256_rmsq", args, gpu)
+    q, s = run_gpu(name, args, gpu)
     rq, rs = run_oracle("rmsnorm_quant_256", args)
     nan = np.isnan(rs)
     assert np.array_equal(np.isnan(s), nan)
@@ -78,16 +83,20 @@ def test_rmsq_stress_rows_bit_exact(gpu):
 
 def test_rmsq_selected_only_when_asked():
     for name in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3"):
-        assert "serial-order" in hf.compile(cat.get(name)).blocks[0]["variant"], name
+        v = hf.compile(cat.get(name)).blocks[0]["variant"]
+        assert v.startswith("row-resident, serial-order"), name
+        v = hf.compile(cat.get(name), options="rmsn_kernel=1").blocks[0]["variant"]
+        assert "serial-order" in v and "chain wave" in v, name
         v = hf.compile(cat.get(name), options="rmsq_kernel=1").blocks[0]["variant"]
-        assert "rmsnorm-quant" in v, name
+        assert "binade-run" in v, name
     # a width the kernel does not take keeps the generic row program
     v = hf.compile(cat.get("rmsnorm_quant_ragged"), options="rmsq_kernel=1").blocks[0]["variant"]
     assert "serial-order" in v
 
 
 SHAPES = {"rmsnorm_quant_rmsq": (8192, 4096), "rmsnorm_quant_rank3_rmsq": (4, 64, 1024),
-          "rmsnorm_quant_ragged_rmsq": (13, 1000)}
+          "rmsnorm_quant_ragged_rmsq": (13, 1000), "rmsnorm_quant_rmsn": (8192, 4096),
+          "rmsnorm_quant_rank3_rmsn": (4, 64, 1024), "rmsnorm_quant_rank3": (4, 64, 1024)}
 
 
 @pytest.mark.gpu
