@@ -17,6 +17,8 @@
 // element count.
 #include "ir.h"
 
+#include <set>
+
 #include <map>
 #include <sstream>
 
@@ -84,8 +86,15 @@ void foldIndex(Op *op) {
   else if (n == "arith.addi") v = a + b;
   else if (n == "arith.subi") v = a - b;
   else if (n == "arith.muli") v = a * b;
-  else if ((n == "arith.divsi" || n == "arith.divui" || n == "arith.floordivsi") && b) v = a / b;
-  else if (n == "arith.ceildivsi" && b) v = (a + b - 1) / b;
+  else if (n == "arith.divsi" && b) v = a / b; // truncating
+  else if (n == "arith.divui" && b) v = (int64_t)((uint64_t)a / (uint64_t)b);
+  else if ((n == "arith.floordivsi" || n == "arith.ceildivsi") && b) {
+    // rounding toward -inf / +inf for any signs
+    v = a / b;
+    const bool inexact = v * b != a, neg = (a < 0) != (b < 0);
+    if (inexact && n == "arith.floordivsi" && neg) --v;
+    if (inexact && n == "arith.ceildivsi" && !neg) ++v;
+  }
   else if (n == "arith.maxsi") v = a > b ? a : b;
   else if (n == "arith.minsi") v = a < b ? a : b;
   else ok = false;
@@ -196,14 +205,37 @@ void specializeDynamic(Module &m, const std::string &spec) {
       throw CompileError("bad dyn entry '" + item + "'");
     }
   }
+  // every entry names a function with a dynamic argument dim at that place
+  for (const auto &fe : sizes) {
+    const Func *fn = nullptr;
+    for (auto &f : m.funcs)
+      if (f->name == fe.first) fn = f.get();
+    if (!fn) throw CompileError("dyn entry for @" + fe.first + ", which is not a function of the module");
+  }
+  std::set<std::string> used;
   for (auto &f : m.funcs) {
     bool dyn = false;
     for (Value *a : f->args) dyn |= isDynamic(a->type);
     for (Op *op : f->ops)
       for (Value *r : op->results) dyn |= isDynamic(r->type);
     if (!dyn) continue;
+    auto it = sizes.find(f->name);
+    if (it != sizes.end()) {
+      // every entry must name a dynamic dim of an argument
+      for (const auto &kv : it->second) {
+        const int ai = kv.first.first, di = kv.first.second;
+        if (ai < 0 || ai >= (int)f->args.size() || di < 0 || di >= (int)f->args[ai]->type.shape.size() ||
+            f->args[ai]->type.shape[di] >= 0)
+          throw CompileError("dyn entry " + f->name + ":" + std::to_string(ai) + "." + std::to_string(di) +
+                             " names no dynamic dim of @" + f->name);
+      }
+      used.insert(f->name);
+    }
     specializeFunc(*f, sizes[f->name]);
   }
+  for (const auto &kv : sizes)
+    if (!used.count(kv.first))
+      throw CompileError("dyn entry for @" + kv.first + ", which has no dynamic dims (or does not exist)");
 }
 
 } // namespace hfc

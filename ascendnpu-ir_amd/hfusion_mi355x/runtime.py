@@ -289,10 +289,11 @@ class Program:
             native.hfr().hfr_program_unload(h)
             self._h = None
 
-    def __call__(self, *args, results=None, stream=None, workspace=None, noalloc=False):
-        """Launches the group on `stream` (torch's current stream by default).
-        noalloc=True goes through hfr_group_launch_noalloc (the library's
-        static scratch instead of a workspace)."""
+    def __call__(self, *args, results=None, stream=None, workspace=None):
+        """Launches the program's groups in order on `stream` (torch's current
+        stream by default) through hfr_program_launch; intermediate tensors
+        live in `workspace` (the program's own when None).  Programs have no
+        no-allocation entry."""
         import torch
         params = self.meta["params"]
         if len(args) != len(params):

@@ -604,9 +604,14 @@ void hfref_matmul_f32(const float *A, const float *B, float *C, int64_t M,
  * per 32 k.  Each scaled operand is rounded to f32, the product is an f32
  * multiply and the sum runs serially over k from C's value, as the linalg.matmul
  * region the reference's decomposition ends in (HFusionOps.cpp:3590-3790:
- * operand * broadcast scale, then linalg.matmul).  e8m0 255 is NaN.  Where
- * the decomposition's f16 steps are exact (scaled operands inside f16's
- * range) this is the decomposition's value bit for bit. */
+ * operand * broadcast scale, then linalg.matmul).  Where the
+ * decomposition's f16 steps are exact (scaled operands inside f16's range)
+ * this is the decomposition's value bit for bit.
+ * e8m0 255 is NaN here, as in the OCP MX format and the MI355X's scaled MFMA.
+ * The reference decomposition instead shifts the byte into a bf16 exponent
+ * (ui8 -> i16, << 7, bitcast), so 255 reads as +inf there and a block of
+ * nonzero same-sign products gives +-inf rather than NaN: the 255 case is
+ * parity unpinned against the reference. */
 static float mx_scale(uint8_t e) {
   return e == 255 ? NAN : ldexpf(1.0f, (int)e - 127);
 }

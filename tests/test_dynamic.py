@@ -131,3 +131,41 @@ def test_gpu_vec_add_dynamic(gpu, n):
     a, b = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
     out, = _call("vec_add_dyn", [a, b, np.zeros(n, np.float32)], gpu)
     assert np.array_equal(out, a + b)
+
+
+def _half_ir(div):
+    """A result of ceil(d / 2) (floordivsi) or floor(d / 2) (ceildivsi)
+    elements, computed through a negative intermediate: 0 - div(0 - d, 2)."""
+    return f"""module {{
+  func.func @half(%x: tensor<?xf32>) -> tensor<?xf32>
+      attributes {{hacc.entry, hfusion.fusion_kind = #hfusion.fusion_kind<PURE_ELEMWISE>}} {{
+    %c0 = arith.constant 0 : index
+    %c2 = arith.constant 2 : index
+    %one = arith.constant 1.000000e+00 : f32
+    %d = tensor.dim %x, %c0 : tensor<?xf32>
+    %m = arith.subi %c0, %d : index
+    %q = arith.{div} %m, %c2 : index
+    %n = arith.subi %c0, %q : index
+    %e = tensor.empty(%n) : tensor<?xf32>
+    %r = linalg.fill ins(%one : f32) outs(%e : tensor<?xf32>) -> tensor<?xf32>
+    return %r : tensor<?xf32>
+  }}
+}}
+"""
+
+
+@pytest.mark.parametrize("div,size", [("floordivsi", 4), ("ceildivsi", 3)])
+def test_signed_division_folds_round_toward_minus_or_plus_infinity(div, size, tmp_path):
+    """floordivsi(-7, 2) = -4 and ceildivsi(-7, 2) = -3 (arith's semantics,
+    not C++'s truncation).  The folded size shows in the shape error the
+    group then raises (its result and argument differ in length)."""
+    hip, err = emit_hip(_half_ir(div), "dyn=half:0.0=7", tmp_path)
+    assert hip is None and f"tensor<{size}xf32>" in err
+
+
+@pytest.mark.parametrize("spec,msg", [("dyn=halff:0.0=7", "not a function"),
+                                      ("dyn=half:0.1=7", "names no dynamic dim"),
+                                      ("dyn=half:1.0=7", "names no dynamic dim")])
+def test_dyn_entries_that_name_nothing_are_refused(spec, msg, tmp_path):
+    hip, err = emit_hip(_half_ir("floordivsi"), spec, tmp_path)
+    assert hip is None and msg in err
