@@ -71,6 +71,10 @@ struct hfr_group {
   std::vector<Karg> kargs;
   void *ownWs = nullptr;
   int ownWsDevice = -1;
+  // dense staging copies of strided memref views (hfr_group_launch_memref)
+  void *stage = nullptr;
+  size_t stageBytes = 0;
+  int stageDevice = -1;
 };
 
 // A buffer binding inside a launch program: program parameter, workspace
@@ -391,6 +395,14 @@ int hfr_group_unload(hfr_group_t g) {
     (void)hipSetDevice(cur);
     if (e != hipSuccess) rc = hipFail(e, "hipFree(workspace)");
   }
+  if (g->stage) {
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    if (g->stageDevice >= 0) (void)hipSetDevice(g->stageDevice);
+    hipError_t e = hipFree(g->stage);
+    (void)hipSetDevice(cur);
+    if (e != hipSuccess && !rc) rc = hipFail(e, "hipFree(staging)");
+  }
   if (g->mod) {
     int r2 = hfr_module_unload(g->mod);
     if (!rc) rc = r2;
@@ -627,27 +639,105 @@ int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, 
 // { T *allocated; T *aligned; int64_t offset; int64_t sizes[R]; int64_t strides[R]; }
 namespace {
 
-int descPointer(const Buf &b, const void *desc, const char *what, size_t idx, uint64_t &out) {
+constexpr int HFR_MAX_RANK = 8;
+
+// A view of a memref descriptor: base address, sizes and element strides.
+struct View {
+  char *base = nullptr;
+  int rank = 0;
+  int64_t sizes[HFR_MAX_RANK] = {}, strides[HFR_MAX_RANK] = {};
+  bool dense = true;
+  int64_t numel = 1;
+};
+
+int readDesc(const Buf &b, const void *desc, const char *what, size_t idx, View &v) {
   if (!desc) return fail(HFR_ERR_INVALID, std::string("null descriptor for ") + what + " " + std::to_string(idx));
   const char *d = (const char *)desc;
-  const char *aligned = *(char *const *)(d + sizeof(void *));
+  char *aligned = *(char *const *)(d + sizeof(void *));
   const int64_t offset = *(const int64_t *)(d + 2 * sizeof(void *));
   const int64_t *sizes = (const int64_t *)(d + 2 * sizeof(void *) + sizeof(int64_t));
   const int64_t *strides = sizes + b.shape.size();
+  if (b.shape.size() > (size_t)HFR_MAX_RANK)
+    return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": rank above " + std::to_string(HFR_MAX_RANK));
+  v.rank = (int)b.shape.size();
   int64_t expect = 1;
-  for (size_t k = b.shape.size(); k-- > 0;) {
+  for (int k = v.rank; k-- > 0;) {
     if (sizes[k] != b.shape[k])
       return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": size " + std::to_string(sizes[k]) +
                                        " in dim " + std::to_string(k) + ", the group expects " + std::to_string(b.shape[k]));
-    if (sizes[k] != 1 && strides[k] != expect)
-      return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) +
-                                       ": strided memref (the group reads dense row-major buffers)");
+    v.sizes[k] = sizes[k];
+    v.strides[k] = strides[k];
+    if (sizes[k] != 1 && strides[k] != expect) v.dense = false;
     expect *= sizes[k];
+    v.numel *= sizes[k];
   }
   if (!aligned) return fail(HFR_ERR_INVALID, std::string("null aligned pointer for ") + what + " " + std::to_string(idx));
   if (offset < 0) return fail(HFR_ERR_INVALID, std::string("negative offset for ") + what + " " + std::to_string(idx));
-  out = (uint64_t)(uintptr_t)(aligned + offset * elemSize(b.elem));
+  v.base = aligned + offset * elemSize(b.elem);
   return HFR_OK;
+}
+
+// A written view must not alias itself: ordered by stride, each dim's stride
+// covers the extent of the dims below it (zero or negative strides refused).
+bool nonOverlapping(const View &v) {
+  int order[HFR_MAX_RANK];
+  int n = 0;
+  for (int k = 0; k < v.rank; ++k)
+    if (v.sizes[k] != 1) order[n++] = k;
+  std::sort(order, order + n, [&](int a, int b) { return v.strides[a] < v.strides[b]; });
+  int64_t extent = 1;
+  for (int i = 0; i < n; ++i) {
+    const int k = order[i];
+    if (v.strides[k] < extent) return false;
+    extent = v.strides[k] * v.sizes[k];
+  }
+  return true;
+}
+
+struct ViewArg {
+  int rank;
+  int64_t sizes[HFR_MAX_RANK], strides[HFR_MAX_RANK];
+};
+
+// Element i of the dense row-major order <-> the view's element at the
+// same coordinates: GATHER copies view -> dense, otherwise dense -> view.
+// Consecutive threads take consecutive dense elements.
+template <typename T, bool GATHER>
+__global__ void hfr_strided_copy(T *view, T *dense, ViewArg v, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = i, off = 0;
+    for (int k = v.rank - 1; k >= 0; --k) {
+      off += (r % v.sizes[k]) * v.strides[k];
+      r /= v.sizes[k];
+    }
+    if (GATHER) dense[i] = view[off];
+    else view[off] = dense[i];
+  }
+}
+
+int stridedCopy(const View &v, int eb, void *dense, bool gather, hipStream_t st) {
+  ViewArg a;
+  a.rank = v.rank;
+  for (int k = 0; k < v.rank; ++k) { a.sizes[k] = v.sizes[k]; a.strides[k] = v.strides[k]; }
+  if (v.numel == 0) return HFR_OK;
+  const unsigned block = 256, grid = (unsigned)std::min<int64_t>((v.numel + block - 1) / block, 65536);
+#define HFR_COPY(T)                                                                                             \
+  do {                                                                                                          \
+    if (gather)                                                                                                 \
+      hipLaunchKernelGGL((hfr_strided_copy<T, true>), dim3(grid), dim3(block), 0, st, (T *)v.base, (T *)dense, a, v.numel); \
+    else                                                                                                        \
+      hipLaunchKernelGGL((hfr_strided_copy<T, false>), dim3(grid), dim3(block), 0, st, (T *)v.base, (T *)dense, a, v.numel); \
+  } while (0)
+  switch (eb) {
+  case 1: HFR_COPY(uint8_t); break;
+  case 2: HFR_COPY(uint16_t); break;
+  case 4: HFR_COPY(uint32_t); break;
+  case 8: HFR_COPY(uint64_t); break;
+  default: return fail(HFR_ERR_INVALID, "element size " + std::to_string(eb));
+  }
+#undef HFR_COPY
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? HFR_OK : hipFail(e, "strided copy launch");
 }
 
 } // namespace
@@ -664,6 +754,25 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
   void *results[HFR_MAX_KARGS];
   if (g->paramRoles.size() > HFR_MAX_KARGS || g->resultTied.size() > HFR_MAX_KARGS)
     return fail(HFR_ERR_INVALID, "too many group arguments");
+  // a strided view is staged through a dense copy: gathered before the launch
+  // when the group reads it, scattered back after when the group writes it
+  struct Staged {
+    View v;
+    int eb;
+    size_t off;
+    bool read, written;
+  };
+  std::vector<Staged> staged;
+  std::vector<std::pair<int, size_t>> stagedParam, stagedResult; // index -> staged slot
+  size_t total = 0;
+  auto stage = [&](const View &v, const std::string &elem, bool read, bool written, const char *what, size_t idx) -> int {
+    if (written && !nonOverlapping(v))
+      return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": the written view overlaps itself");
+    const int eb = elemSize(elem);
+    staged.push_back({v, eb, total, read, written});
+    total += ((size_t)v.numel * eb + 255) & ~(size_t)255;
+    return HFR_OK;
+  };
   for (size_t i = 0; i < g->paramRoles.size(); ++i) {
     if (g->paramRoles[i] == "scalar") {
       if (!descs[i]) return fail(HFR_ERR_INVALID, "null scalar pointer for argument " + std::to_string(i));
@@ -672,19 +781,69 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
       params[i] = bits;
       continue;
     }
-    int rc = descPointer(g->paramBufs[i], descs[i], "argument", i, params[i]);
+    View v;
+    int rc = readDesc(g->paramBufs[i], descs[i], "argument", i, v);
     if (rc) return rc;
+    params[i] = (uint64_t)(uintptr_t)v.base;
+    if (!v.dense) {
+      const std::string &role = g->paramRoles[i];
+      rc = stage(v, g->paramBufs[i].elem, role != "out", role != "in", "argument", i);
+      if (rc) return rc;
+      stagedParam.push_back({(int)i, staged.size() - 1});
+    }
   }
   size_t k = g->paramRoles.size();
   for (size_t j = 0; j < g->resultTied.size(); ++j) {
     results[j] = nullptr;
     if (g->resultTied[j] >= 0) continue;
-    uint64_t ptr = 0;
-    int rc = descPointer(g->resultBufs[j], descs[k++], "result", j, ptr);
+    View v;
+    int rc = readDesc(g->resultBufs[j], descs[k++], "result", j, v);
     if (rc) return rc;
-    results[j] = (void *)(uintptr_t)ptr;
+    results[j] = v.base;
+    if (!v.dense) {
+      rc = stage(v, g->resultBufs[j].elem, false, true, "result", j);
+      if (rc) return rc;
+      stagedResult.push_back({(int)j, staged.size() - 1});
+    }
   }
-  return hfr_group_launch(g, params, g->paramRoles.size(), results, g->resultTied.size(), nullptr, stream);
+  if (staged.empty())
+    return hfr_group_launch(g, params, g->paramRoles.size(), results, g->resultTied.size(), nullptr, stream);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hipFail(e, "hipGetDevice");
+  if (g->stage && (g->stageBytes < total || g->stageDevice != dev)) {
+    // grown (or moved): the old copy is released once the device is idle
+    int cur = dev;
+    if (g->stageDevice >= 0) (void)hipSetDevice(g->stageDevice);
+    e = hipFree(g->stage);
+    (void)hipSetDevice(cur);
+    g->stage = nullptr;
+    g->stageBytes = 0;
+    if (e != hipSuccess) return hipFail(e, "hipFree(staging)");
+  }
+  if (!g->stage) {
+    e = hipMalloc(&g->stage, total);
+    if (e != hipSuccess) return hipFail(e, "hipMalloc(staging)");
+    g->stageBytes = total;
+    g->stageDevice = dev;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  char *base = (char *)g->stage;
+  for (auto &pi : stagedParam) params[pi.first] = (uint64_t)(uintptr_t)(base + staged[pi.second].off);
+  for (auto &rj : stagedResult) results[rj.first] = base + staged[rj.second].off;
+  for (auto &sv : staged)
+    if (sv.read) {
+      int rc = stridedCopy(sv.v, sv.eb, base + sv.off, true, st);
+      if (rc) return rc;
+    }
+  int rc = hfr_group_launch(g, params, g->paramRoles.size(), results, g->resultTied.size(), nullptr, stream);
+  if (rc) return rc;
+  for (auto &sv : staged)
+    if (sv.written) {
+      rc = stridedCopy(sv.v, sv.eb, base + sv.off, false, st);
+      if (rc) return rc;
+    }
+  return HFR_OK;
 }
 
 // ---------------------------------------------------------------------------

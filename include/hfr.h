@@ -114,8 +114,14 @@ int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, 
  *              int64_t sizes[R]; int64_t strides[R]; }
  * (R = the tensor's rank; a scalar argument passes a pointer to its value).
  * The device buffer is aligned + offset elements.  Sizes must equal the
- * group's static shape and strides must be dense row-major; otherwise
- * HFR_ERR_INVALID.  Replaces the reference runner's memref entry points
+ * group's static shape (otherwise HFR_ERR_INVALID).  Dense row-major views are
+ * used in place; any other strides (row pitches, transposed or broadcast
+ * views) go through a dense staging copy on `stream`: gathered before the
+ * group's kernels when the group reads the view, scattered back after them
+ * when it writes it.  A written view that overlaps itself is refused.  The
+ * staging buffer belongs to the group: allocated on the first strided launch,
+ * grown when a later one needs more (which waits for the device), freed by
+ * hfr_group_unload; calls that overlap on one group race.  Replaces the reference runner's memref entry points
  * (`_mlir_ciface_getData*` / `printData*` over UnrankedMemRefType, whose
  * descriptor field points at this ranked layout:
  * bishengir/lib/ExecutionEngine/BiShengIRRunnerUtils.cpp:99-110). */

@@ -84,7 +84,8 @@ def test_memref_descriptors_with_offsets(gpu):
 
 def test_memref_descriptor_untied_result_and_errors(gpu):
     """A result with its own buffer takes the descriptor after the arguments;
-    wrong sizes, strided layouts and a wrong descriptor count are refused."""
+    wrong sizes, a written view that overlaps itself and a wrong descriptor
+    count are refused."""
     note("memref reshape_chain")
     import torch
     s = I.SEED_BASE + 97
@@ -114,10 +115,11 @@ def test_memref_descriptor_untied_result_and_errors(gpu):
     ptrs_bad = (ctypes.c_void_p * len(descs))(*([ctypes.addressof(d) for d in descs[:-1]] + [ctypes.addressof(bad)]))
     assert lib.hfr_group_launch_memref(grp._h, ptrs_bad, len(descs), stream) == -1
     assert b"size" in lib.hfr_last_error()
-    strided = native.memref_descriptor(obase, [128, 256], offset=9, strides=[512, 1])
-    ptrs_st = (ctypes.c_void_p * len(descs))(*([ctypes.addressof(d) for d in descs[:-1]] + [ctypes.addressof(strided)]))
+    # a written view that overlaps itself (stride 0 on a dim of 128)
+    overl = native.memref_descriptor(obase, [128, 256], offset=9, strides=[0, 1])
+    ptrs_st = (ctypes.c_void_p * len(descs))(*([ctypes.addressof(d) for d in descs[:-1]] + [ctypes.addressof(overl)]))
     assert lib.hfr_group_launch_memref(grp._h, ptrs_st, len(descs), stream) == -1
-    assert b"strided" in lib.hfr_last_error()
+    assert b"overlaps" in lib.hfr_last_error()
 
 
 def test_module_kernel_launch_by_hand(gpu):
@@ -152,3 +154,66 @@ def test_module_kernel_launch_by_hand(gpu):
         assert np.array_equal(dout.cpu().numpy().view(np.uint32), ref.view(np.uint32))
     finally:
         native.check(lib.hfr_module_unload(mod))
+
+
+def _view_desc(view, base, dev_ptr):
+    """Descriptor of numpy view `view` of `base`, addressed in the device copy
+    of `base` at dev_ptr (element offset and strides as numpy has them)."""
+    es = base.itemsize
+    off = (view.__array_interface__["data"][0] - base.__array_interface__["data"][0]) // es
+    return native.memref_descriptor(dev_ptr, list(view.shape), offset=off, strides=[s // es for s in view.strides])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("x_transposed", [False, True])
+def test_memref_strided_views(gpu, x_transposed):
+    """Strided views at the GPU entry: x with a row pitch (or read through a
+    transposed view), gamma with element stride 2, the int8 codes written
+    through a transposed view and the scales at an offset.  The outputs equal
+    the oracle's memref entry on the same descriptors over host copies, and
+    no element outside the views is written."""
+    note(f"memref strided rmsnorm_quant_ragged x_transposed={x_transposed}")
+    import torch
+    from oracle.interp import lib as oracle_lib, ptr as optr
+    name, rows, cols = "rmsnorm_quant_ragged", 13, 1000
+    x, gamma = I.config_inputs("rmsnorm_quant", rows=rows, cols=cols)
+    if x_transposed:
+        XB = np.zeros((cols + 7, rows + 3), np.uint16)
+        XB[4:4 + cols, 1:1 + rows] = x.T
+        xv = XB.T[1:1 + rows, 4:4 + cols]             # strides (1, rows + 3)
+    else:
+        XB = np.zeros((rows + 5, cols + 100), np.uint16)
+        XB[2:2 + rows, 5:5 + cols] = x
+        xv = XB[2:2 + rows, 5:5 + cols]               # row pitch 1100
+    G = np.zeros(2 * cols + 3, np.uint16)
+    G[1:1 + 2 * cols:2] = gamma
+    gv = G[1:1 + 2 * cols:2]
+    Q = np.full((cols + 10, rows + 7), 0x5A, np.int8)
+    qv = Q.T[3:3 + rows, 6:6 + cols]                  # codes through a transposed view
+    S = np.full(rows + 9, -1.0, np.float32)
+    sv = S[4:4 + rows]
+    assert np.array_equal(xv, x) and np.array_equal(gv, gamma)
+    dXB, dG, dQ, dS = (torch.from_numpy(a.view(np.uint8).copy()).to(gpu) for a in (XB, G, Q, S))
+    descs = [_view_desc(xv, XB, dXB.data_ptr()), _view_desc(gv, G, dG.data_ptr()),
+             _view_desc(qv, Q, dQ.data_ptr()), _view_desc(sv, S, dS.data_ptr())]
+    grp = hf.compile(cat.get(name), require_cached=True).load()
+    ptrs = (ctypes.c_void_p * len(descs))(*[ctypes.addressof(d) for d in descs])
+    torch.cuda.synchronize()
+    native.check(native.hfr().hfr_group_launch_memref(grp._h, ptrs, len(descs), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    gQ = dQ.cpu().numpy().view(np.int8).reshape(Q.shape)
+    gS = dS.cpu().numpy().view(np.float32)
+    # the oracle's memref entry over host copies, same descriptors
+    hQ, hS = Q.copy(), S.copy()
+    L = oracle_lib()
+    hdesc = [_view_desc(v, b, b.ctypes.data) for v, b in
+             ((xv, XB), (gv, G), (hQ.T[3:3 + rows, 6:6 + cols], hQ), (hS[4:4 + rows], hS))]
+    assert L.hfref_rmsnorm_quant_memref(*[ctypes.byref(d) for d in hdesc[:2]], ctypes.c_float(1e-6),
+                                        *[ctypes.byref(d) for d in hdesc[2:]]) == 0
+    assert np.array_equal(gQ, hQ), "codes (or the bytes around the view) differ"
+    assert np.array_equal(gS.view(np.uint32), hS.view(np.uint32)), "scales (or the floats around the view) differ"
+    rq, rs = run_oracle(name, [x, gamma, np.zeros((rows, cols), np.int8), np.zeros(rows, np.float32)])
+    assert np.array_equal(gQ.T[3:3 + rows, 6:6 + cols], rq)
+    outside = np.ones(Q.shape, bool)
+    outside.T[3:3 + rows, 6:6 + cols] = False
+    assert bool((gQ[outside] == 0x5A).all()) and bool((gS[:4] == -1.0).all()) and bool((gS[4 + rows:] == -1.0).all())
