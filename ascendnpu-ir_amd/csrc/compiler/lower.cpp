@@ -1860,7 +1860,11 @@ struct EltwiseEmitter {
   // LDS, read along TQ (their contiguous dim) and consumed along the last dim
   int TQ = -1;
   std::vector<const Value *> staged;
-  static constexpr int TILE = 64, PITCH = 65; // words; the odd pitch spreads both access patterns over all banks
+  // a tile spans TILE positions of the staged inputs' contiguous dim and TL of
+  // the output's; PITCH = TL + 1 words (the odd pitch spreads both access
+  // patterns over all banks)
+  static constexpr int TILE = 64;
+  int TL = 64, PITCH = 65;
 
   EltwiseEmitter(Analysis &a) : A(a) {}
   std::string fresh() { return "v" + std::to_string(tmp++); }
@@ -2097,7 +2101,12 @@ struct EltwiseEmitter {
   KernelPlan runTiled(const std::string &kname, const std::string &kind) {
     const int r = (int)A.D.size(), LD = r - 1;
     const int64_t DQ = A.D[TQ], DL = A.D[LD];
-    const int64_t NTQ = (DQ + TILE - 1) / TILE, NTL = (DL + TILE - 1) / TILE;
+    // 128 output positions per tile when the output dim is long enough: the
+    // concurrently running workgroups (consecutive tiles run along the output's
+    // contiguous dim) then extend each output row in 512-byte runs
+    TL = DL >= 128 && staged.size() <= 2 ? 128 : 64;
+    PITCH = TL + 1;
+    const int64_t NTQ = (DQ + TILE - 1) / TILE, NTL = (DL + TL - 1) / TL;
     int64_t NO = 1;
     for (int d = 0; d < r; ++d) if (d != TQ && d != LD) NO *= A.D[d];
     const int64_t NT = NO * NTQ * NTL;
@@ -2108,7 +2117,7 @@ struct EltwiseEmitter {
     KernelPlan p;
     p.kernelName = kname;
     p.kind = kind;
-    p.variant = "LDS-staged transpose tiles (64x64)";
+    p.variant = "LDS-staged transpose tiles (64x" + std::to_string(TL) + ")";
     k << "extern \"C\" __global__ __launch_bounds__(" << block << ") void " << kname << "("
       << kernelParamList(A, p.kargs, false) << ") {\n"
       << "  constexpr int VEC = " << VEC << ";\n";
@@ -2130,25 +2139,33 @@ struct EltwiseEmitter {
       if (VQ > 8) VQ = 8;
       while (VQ > 1 && DQ % VQ) VQ /= 2;
       const int lanesPerRow = TILE / VQ;
-      k << "    for (int i_ = threadIdx.x; i_ < " << TILE * lanesPerRow << "; i_ += " << block << ") {\n"
-        << "      const int lq0 = (i_ % " << lanesPerRow << ") * " << VQ << ", ll = i_ / " << lanesPerRow << ";\n"
-        << "      const int64_t c" << TQ << " = tq_ * " << TILE << " + lq0, c" << LD << " = tl_ * " << TILE << " + ll;\n"
-        << "      if (c" << LD << " >= " << DL << "ll || c" << TQ << " >= " << DQ << "ll) continue;\n"
-        << "      const " << M << "* src_ = (const " << M << "*)p" << v->argIdx << " + (" << indexFor(m) << ");\n"
-        << "      " << M << " w_[" << VQ << "];\n";
+      const int nItems = TL * lanesPerRow, nLd = (nItems + block - 1) / block;
+      // every load of the tile in flight before the first LDS write
+      k << "    {\n      " << M << " w_[" << nLd << "][" << VQ << "];\n      bool ok_[" << nLd << "];\n"
+        << "#pragma unroll\n      for (int it_ = 0; it_ < " << nLd << "; ++it_) {\n"
+        << "        const int i_ = threadIdx.x + it_ * " << block << ";\n"
+        << "        const int lq0 = (i_ % " << lanesPerRow << ") * " << VQ << ", ll = i_ / " << lanesPerRow << ";\n"
+        << "        const int64_t c" << TQ << " = tq_ * " << TILE << " + lq0, c" << LD << " = tl_ * " << TL << " + ll;\n"
+        << "        ok_[it_] = i_ < " << nItems << " && c" << LD << " < " << DL << "ll && c" << TQ << " < " << DQ << "ll;\n"
+        << "        if (!ok_[it_]) continue;\n"
+        << "        const " << M << "* src_ = (const " << M << "*)p" << v->argIdx << " + (" << indexFor(m) << ");\n";
       if (VQ > 1)
-        k << "      hf::vec_load<" << M << ", " << VQ << ">(src_, w_);\n";
+        k << "        hf::vec_load<" << M << ", " << VQ << ">(src_, w_[it_]);\n";
       else
-        k << "      w_[0] = src_[0];\n";
-      k << "#pragma unroll\n      for (int j = 0; j < " << VQ << "; ++j) " << ldsName(v) << "[(lq0 + j) * " << PITCH
-        << " + ll] = (" << W << ")__builtin_bit_cast(" << U << ", w_[j]);\n"
-        << "    }\n";
+        k << "        w_[it_][0] = src_[0];\n";
+      k << "      }\n#pragma unroll\n      for (int it_ = 0; it_ < " << nLd << "; ++it_) {\n"
+        << "        if (!ok_[it_]) continue;\n"
+        << "        const int i_ = threadIdx.x + it_ * " << block << ";\n"
+        << "        const int lq0 = (i_ % " << lanesPerRow << ") * " << VQ << ", ll = i_ / " << lanesPerRow << ";\n"
+        << "#pragma unroll\n        for (int j = 0; j < " << VQ << "; ++j) " << ldsName(v) << "[(lq0 + j) * " << PITCH
+        << " + ll] = (" << W << ")__builtin_bit_cast(" << U << ", w_[it_][j]);\n"
+        << "      }\n    }\n";
     }
-    const int lanesPerRow = TILE / VEC;
+    const int lanesPerRow = TL / VEC;
     k << "    __syncthreads();\n"
       << "    for (int i_ = threadIdx.x; i_ < " << TILE * lanesPerRow << "; i_ += " << block << ") {\n"
       << "      const int lq = i_ / " << lanesPerRow << ", ll = (i_ % " << lanesPerRow << ") * VEC;\n"
-      << "      const int64_t c" << TQ << " = tq_ * " << TILE << " + lq, c" << LD << " = tl_ * " << TILE << " + ll;\n"
+      << "      const int64_t c" << TQ << " = tq_ * " << TILE << " + lq, c" << LD << " = tl_ * " << TL << " + ll;\n"
       << "      if (c" << LD << " >= " << DL << "ll || c" << TQ << " >= " << DQ << "ll) continue;\n"
       << "      (void)lq; (void)ll;\n"
       << "      int64_t base = 0;\n";
