@@ -2321,7 +2321,8 @@ void hivmMatmulEpilogue(const Op *mm, bool intAcc, std::ostringstream &epi, std:
   else unsupported(mm, "matmul output type");
 }
 
-KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
+constexpr int MK_BF16_CODE = 1; // hf::MK_BF16
+KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions &opt) {
   Func &f = *A.f;
   const Op *mm = findOp(f, [](const Op *o) {
     return o->name == "linalg.matmul" || o->name == "linalg.matmul_transpose_b" || o->name == "hivm.hir.matmul" ||
@@ -2422,6 +2423,12 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const int threads = dma >= 3 ? 512 : 256;
   auto align256 = [](uint64_t v) { return (v + 255) / 256 * 256; };
   const uint64_t wsB = preB ? align256((uint64_t)(N * K * esz)) : 0, wsA = preA ? align256((uint64_t)(M * K * esz)) : 0;
+  // matmul_mx with mx_exact=1: both operands scaled into bf16 by pre kernels
+  // (workspace: A' [M, K] then B' [K, N]), then the bf16 contraction, whose
+  // products are exact and whose sums are f32 (the fp8 matrix core's 64-k dot
+  // product is not: about 2^-11 of the products' magnitude sum)
+  const bool mxExact = mx && opt.mxExact;
+  const uint64_t wsXA = mxExact ? align256((uint64_t)(M * K * 2)) : 0, wsXB = mxExact ? align256((uint64_t)(K * N * 2)) : 0;
   // matmul_mx accumulates onto its `outs`: a tensor.empty (taken as zero) or
   // a constant fill, added after the contraction
   std::string accInit;
@@ -2520,7 +2527,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   p.kernelName = kname;
   p.kind = "SINGLE_CUBE";
   std::ostringstream k;
-  std::string params = kernelParamList(A, p.kargs, preA || preB);
+  std::string params = kernelParamList(A, p.kargs, preA || preB || mxExact);
   // epilogue functor receives all kernel pointer arguments
   k << "namespace {\nstruct " << kname << "_args {";
   for (size_t i = 0; i < A.params.size(); ++i)
@@ -2547,7 +2554,10 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   const std::string et = i8 ? "int8_t" : "uint16_t";
   const std::string aPtr = preA ? "(const " + et + "*)((char*)ws + " + std::to_string(wsB) + ")" : "(const " + et + "*)p" + std::to_string(a->argIdx);
   const std::string bPtr = preB ? "(const " + et + "*)ws" : "(const " + et + "*)p" + std::to_string(b->argIdx);
-  if (mx)
+  if (mxExact)
+    k << "  hf::mmad<" << MK_BF16_CODE << ", " << kname << "_epi, false, false, 4>((const uint16_t*)ws, (const uint16_t*)((char*)ws + "
+      << wsXA << "), (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
+  else if (mx)
     k << "  hf::mmad_mx<" << mk << ", " << kname << "_epi>((const uint8_t*)p" << a->argIdx << ", (const uint8_t*)p" << b->argIdx
       << ", (const uint8_t*)p" << sa->argIdx << ", (const uint8_t*)p" << sb->argIdx << ", (" << mtype(oe) << "*)"
       << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
@@ -2570,13 +2580,33 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname) {
   if (preB) preKernel("_relayout_b", b, N, 0);
   if (preA) preKernel("_relayout_a", a, M, wsB);
   p.workspaceBytes = wsB + wsA;
+  if (mxExact) {
+    auto mxPre = [&](const char *suffix, const Value *src, const Value *scl, int fmt, bool rowScale, int64_t R, int64_t Cc,
+                     uint64_t off) {
+      KernelPlan::PreKernel pk;
+      pk.name = kname + suffix;
+      pk.grid = (unsigned)std::min<int64_t>(((rowScale ? R * Cc / 8 : R / 8 * (Cc / 8)) + 255) / 256, 8192);
+      pk.block = 256;
+      pk.kargs = {"param:" + std::to_string(src->argIdx), "param:" + std::to_string(scl->argIdx), "ws"};
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << pk.name
+        << "(const void* __restrict__ src, const void* __restrict__ sc, void* __restrict__ ws) {\n"
+        << "  hf::mx_to_bf16<" << fmt << ", " << (rowScale ? "true" : "false") << ">((const uint8_t*)src, (const uint8_t*)sc, "
+        << "(uint16_t*)((char*)ws + " << off << "), " << R << "ll, " << Cc << "ll, " << K << "ll);\n}\n";
+      p.pre.push_back(pk);
+    };
+    mxPre("_mx_a", a, sa, (mk - 3) / 2, true, M, K, 0);
+    mxPre("_mx_b", b, sb, (mk - 3) % 2, false, K, N, wsXA);
+    p.workspaceBytes = wsXA + wsXB;
+  }
   p.source = k.str();
   // 256x256 macro-tiles, one workgroup each (XCD-aware order inside the kernel)
   const int64_t TM = 256, TN = 256;
   p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
   p.block[0] = (unsigned)threads;
   static const char *mxName[4] = {"e4m3 x e4m3", "e4m3 x e5m2", "e5m2 x e4m3", "e5m2 x e5m2"};
-  p.variant = std::string(mx ? std::string("mfma_scale_f32_32x32x64_f8f6f4 (") + mxName[mk - 3] + ", e8m0 scales per 32 k)"
+  p.variant = std::string(mxExact ? std::string("exact matmul_mx: ") + mxName[mk - 3] +
+                                         " with e8m0 scales per 32 k, scaled into bf16 by pre kernels, mfma_f32_32x32x16_bf16"
+                          : mx ? std::string("mfma_scale_f32_32x32x64_f8f6f4 (") + mxName[mk - 3] + ", e8m0 scales per 32 k)"
                           : mk == 0 ? "mfma_i32_32x32x32_i8" : mk == 1 ? "mfma_f32_32x32x16_bf16" : "mfma_f32_32x32x16_f16") +
               (aT ? ", A [K,M]" : "") + (bT ? ", B [N,K]" : ", B [K,N]") +
               (preA || preB ? " (re-laid K-contiguous by a transpose kernel)" : "") +
@@ -4003,7 +4033,7 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     if (single) {
       p = lowerSingleOp(A, kname, single);
     } else if (kind == "SINGLE_CUBE") {
-      p = lowerMatmul(A, kname);
+      p = lowerMatmul(A, kname, opt);
     } else if (kind == "REDUCE_WITH_INDEX" && isRowArgReduce(f)) {
       p = lowerReduceWithIndex(A, kname);
     } else {

@@ -55,6 +55,7 @@ struct LowerOptions {
   // rows of at most 4096 elements
   int orderedFloatSums = -1;
   bool rmsqKernel = false;       // RMSNorm + dynamic quantisation through hf_rmsq.h
+  bool mxExact = false;          // matmul_mx through scaled bf16 operands and the bf16 matrix core
   bool rmsnKernel = false;       // ... through hf_rmsn.h (chain wave + product maxima; opt-in)
 };
 

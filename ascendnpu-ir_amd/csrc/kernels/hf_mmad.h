@@ -763,6 +763,63 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
 // ahead of the DMA ring.  Bytes (ESZ 1): each thread reads a 16-row x 4-column
 // block as 16 dwords and transposes it in registers (v_perm); wider elements
 // are gathered element by element.
+// matmul_mx operands to bf16 for the exact contraction (compiler option
+// mx_exact=1): element (r, c) of a [R, C] byte operand in fp8 format FMT
+// becomes fp8(v) * 2^(s - 127), with s the e8m0 scale of its row r
+// (ROWSCALE, A [M, K]: k = c) or of its column c (B [K, N]: k = r), one per
+// 32 k (scale row length K/32); e8m0 255 gives NaN.  The scaled value has at
+// most 3 significant bits, so it is exact in bf16 wherever its exponent is
+// inside bf16's normal range (the range of f32).  Eight bytes per thread
+// and step, 16-byte stores.
+template <int FMT, bool ROWSCALE>
+__device__ __forceinline__ void mx_to_bf16(const uint8_t *__restrict__ src, const uint8_t *__restrict__ sc,
+                                           uint16_t *__restrict__ dst, int64_t R, int64_t C, int64_t K) {
+  const int64_t n8 = R * C / 8, ks = K / 32;
+  if constexpr (!ROWSCALE) {
+    // B [K, N]: a thread owns 8 columns of 8 rows inside one 32-row scale
+    // block; their 8 scales are loaded once for the 8 rows
+    const int64_t cg = C / 8, items = (R / 8) * cg;
+    for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < items; it += (int64_t)gridDim.x * blockDim.x) {
+      const int64_t r8 = it / cg, kb = r8 / 4, c0 = (it % cg) * 8;
+      int sx[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sx[j] = sc[(c0 + j) * ks + kb];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int64_t e0 = (r8 * 8 + r) * C + c0;
+        const uint2 w = *reinterpret_cast<const uint2 *>(src + e0);
+        uint16_t o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint8_t b = (uint8_t)((j < 4 ? w.x : w.y) >> (8 * (j % 4)));
+          const float f = sx[j] == 255 ? __builtin_nanf("") : __builtin_ldexpf(fp8_to_f32<FMT>(b), sx[j] - 127);
+          o[j] = f32_to_bf16_rne(f);
+        }
+        uint4 v;
+        __builtin_memcpy(&v, o, 16);
+        *reinterpret_cast<uint4 *>(dst + e0) = v;
+      }
+    }
+    return;
+  }
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e0 = i * 8, r = e0 / C, c0 = e0 % C;
+    const uint2 w = *reinterpret_cast<const uint2 *>(src + e0);
+    uint16_t o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint8_t b = (uint8_t)((j < 4 ? w.x : w.y) >> (8 * (j % 4)));
+      const int64_t c = c0 + j;
+      const uint8_t s = ROWSCALE ? sc[r * ks + c / 32] : sc[c * ks + r / 32];
+      const float f = s == 255 ? __builtin_nanf("") : __builtin_ldexpf(fp8_to_f32<FMT>(b), (int)s - 127);
+      o[j] = f32_to_bf16_rne(f);
+    }
+    uint4 v;
+    __builtin_memcpy(&v, o, 16);
+    *reinterpret_cast<uint4 *>(dst + e0) = v;
+  }
+}
+
 template <int ESZ>
 __device__ __forceinline__ void mm_transpose(const char *__restrict__ src, char *__restrict__ dst, int64_t R, int64_t C) {
   constexpr int T = 128 / ESZ, CH = 8, EPC = 16 / ESZ, PITCH = 136; // row pitch: the two half-waves' rows on other banks

@@ -29,7 +29,9 @@ ORDER = ["rmsnorm_quant", "vec_add", "safe_softmax", "argmax", "w8a8_dequant"]
 # further groups on the hot path, measured the same way (not BASELINE configs):
 # the bf16 contraction, W8A8 with B as [K, N], a transpose fused with a cast,
 # the block-scaled fp8 contraction (hfusion.matmul_mx)
-EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast", "mx_fp8"]
+EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast", "mx_fp8", "mx_fp8_exact"]
+# bench names that are a product group compiled with options
+VARIANTS = {"mx_fp8_exact": ("mx_fp8", "mx_exact=1")}
 FP8_PEAK_TFLOPS = 5000.0  # dense fp8 MFMA (the block-scaled form runs at the same rate)
 
 
@@ -61,7 +63,8 @@ def generic_inputs(meta, dev, seed=7):
             dt = {"i8": torch.int8, "bf16": torch.bfloat16, "f32": torch.float32, "i32": torch.int32}[elem]
             out.append(torch.empty(shape, dtype=dt, device=dev))
         elif elem == "i8":
-            out.append(torch.from_numpy(rng.integers(-128, 128, shape, dtype=np.int8)).to(dev))
+            # int8 operands as in the W8A8 config: U[-127, 127]
+            out.append(torch.from_numpy(rng.integers(-127, 128, shape, dtype=np.int8)).to(dev))
         elif elem == "bf16":
             out.append(torch.from_numpy(rng.standard_normal(shape, dtype=np.float32)).to(dev).to(torch.bfloat16))
         elif elem == "f32":
@@ -520,7 +523,8 @@ def main():
     traffic = traffic_table()
     for name in names:
         log(f"[bench] {name}: preparing inputs")
-        art = hf.compile(hf.catalog.get(name), require_cached=True)
+        base, opts = VARIANTS.get(name, (name, ""))
+        art = hf.compile(hf.catalog.get(base), options=opts, require_cached=True)
         grp = art.load()
         if name in EXTRA:
             dargs, host_ins = generic_inputs(grp.meta, dev), None
@@ -571,7 +575,8 @@ def main():
         "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32", "argmax": "f32",
                   "w8a8_dequant": "int8", "w8a8_dequant_kn": "int8", "bf16_mmad": "bf16",
-                  "transpose_cast": "bf16", "mx_fp8": "fp8 (e4m3, e8m0 scales)"}[head],
+                  "transpose_cast": "bf16", "mx_fp8": "fp8 (e4m3, e8m0 scales)",
+                  "mx_fp8_exact": "fp8 (e4m3, e8m0 scales) via bf16"}[head],
         "data": "synthetic (seeded splitmix64)",
         "config": {"workload": head, **{k: v for k, v in cfg.items()}},
         "roofline": h["roofline"],

@@ -1180,6 +1180,9 @@ def entries():
     e["mx_e5m2_bitcast"] = g.matmul_mx(300, 208, 384, fa="e5m2", fb="e4m3", via="bitcast", init=0.5, name="mx_e5m2_bitcast")
     e["mx_format_bf16"] = g.matmul_mx(264, 784, 256, fa="e4m3", fb="e5m2", via="format", out="bf16", name="mx_format_bf16")
     e["mx_e5m2"] = g.matmul_mx(128, 128, 128, fa="e5m2", fb="e5m2", name="mx_e5m2")
+    # the same through scaled bf16 operands and the bf16 matrix core (mx_exact=1)
+    for n in ("mx_e4m3", "mx_e5m2_bitcast", "mx_format_bf16", "mx_e5m2", "mx_fp8"):
+        e[n + "_exact"] = e[n]
     e["bf16_mmad_ragged"] = g.bf16_mmad(200, 136, 96)
     e["bf16_mmad_ragged128"] = g.bf16_mmad(200, 136, 192)
     # B [K, N] through the ring (16-bit transposing reads), bf16 and f16
@@ -1292,4 +1295,6 @@ def options(name):
         return dyn_options(name, DYN_ROWS[name][0])
     if name.endswith("_rmsq"):
         return "rmsq_kernel=1"
+    if name.endswith("_exact"):
+        return "mx_exact=1"
     return "rmsn_kernel=1" if name.endswith("_rmsn") else ""
