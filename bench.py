@@ -334,6 +334,14 @@ def summarize_counters(d, out, command):
             fh.write(f"{k}: " + " ".join(f"{c}={v:.0f}" for c, v in sorted(med.items())) + "\n")
             if "SQ_INSTS_VALU_MFMA_MOPS_I8" in med:
                 fh.write(f"  int8 matrix ops = {med['SQ_INSTS_VALU_MFMA_MOPS_I8'] * 512:.4e}\n")
+            if "SQ_INSTS_VALU_MFMA_MOPS_F8" in med:
+                fh.write(f"  fp8 matrix flops = {med['SQ_INSTS_VALU_MFMA_MOPS_F8'] * 512:.4e}\n")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in med and "GRBM_GUI_ACTIVE" in med:
+                fh.write(f"  MFMA busy / GPU active cycles (GRBM_GUI_ACTIVE / 8 XCDs) = "
+                         f"{med['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024 / (med['GRBM_GUI_ACTIVE'] / 8):.3f}\n")
+            if "SQ_WAIT_INST_LDS" in med and "SQ_WAVE_CYCLES" in med:
+                fh.write(f"  wave cycles waiting on LDS instructions / wave cycles = "
+                         f"{med['SQ_WAIT_INST_LDS'] / max(1.0, med['SQ_WAVE_CYCLES']):.3f}\n")
             if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
                 fh.write(f"  MFMA busy cycles per SIMD = {med['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024:.0f}\n")
             if "SQ_BUSY_CYCLES" in med:
