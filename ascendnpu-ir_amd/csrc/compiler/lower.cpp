@@ -2411,7 +2411,12 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
   // A B [K, N] with 128-byte K slices goes through the ring as it is
   // (mode 4): whole 256-byte k-rows are staged and the matrix-core operand is
   // formed by transposing LDS reads, so no re-layout pass is needed.
-  const int dma0 = (K * esz) % 128 == 0 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
+  // The 128-byte ring addresses each lane's source as a 32-bit offset from
+  // a per-step base: 256 rows of K bytes, or 128 bytes' worth of k-rows of a
+  // [K, N] / [K, M] operand, must stay below 2^32 bytes.
+  const bool offs32 = K * esz <= (int64_t(1) << 24) && M <= (int64_t(1) << 25) && N <= (int64_t(1) << 25);
+  if (mx && !offs32) unsupported(mm, "matmul_mx with K above 2^24 bytes or M, N above 2^25");
+  const int dma0 = (K * esz) % 128 == 0 && offs32 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
   // The same holds for a bf16 / f16 B [K, N] (512-byte k-rows, 16-bit
   // transposing reads).
   // An A [K, M] is staged and read the same way.

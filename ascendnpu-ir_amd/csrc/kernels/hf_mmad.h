@@ -215,32 +215,41 @@ __device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][JT], typename Ep
     __syncthreads(); // the stage is free
     if (one_pass || wm == h) {
       const int rbase = one_pass ? wm * 128 : 0; // this wave's first staged row
+      // FULL: every tile lies inside C (M and N multiples of the tile, known
+      // when the shapes are compile-time constants), so the operand indices
+      // need no clamping and the functor's per-row loads of 4 consecutive
+      // rows merge into one vector load
+      auto stage_tiles = [&](auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        typename Epi::row_t rv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-          rv[r] = Epi::row(m < M ? m : M - 1, P);
-        }
-#pragma unroll
-        for (int j = 0; j < JT; ++j) {
-          const int col = wn * (32 * JT) + j * 32 + lane % 32;
-          const int64_t n = n0 + col;
-          const typename Epi::col_t cv = Epi::col(n < N ? n : N - 1, P);
-          acc_t a = acc[i][j];
-          asm volatile("" : "+a"(a)::"memory"); // one tile in VGPRs at a time
+        for (int i = 0; i < 4; ++i) {
+          typename Epi::row_t rv[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int row = i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-            const int64_t m = m0 + wm * 128 + row;
-            // rows and columns past C are staged (from clamped operand
-            // indices) but never stored
-            *reinterpret_cast<O *>(stage + (rbase + row) * RS + col * (int)sizeof(O)) =
-                Epi::apply(a[r], m < M ? m : M - 1, n < N ? n : N - 1, rv[r], cv, P);
+            const int64_t m = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+            rv[r] = Epi::row(FULL || m < M ? m : M - 1, P);
+          }
+#pragma unroll
+          for (int j = 0; j < JT; ++j) {
+            const int col = wn * (32 * JT) + j * 32 + lane % 32;
+            const int64_t n = n0 + col;
+            const typename Epi::col_t cv = Epi::col(FULL || n < N ? n : N - 1, P);
+            acc_t a = acc[i][j];
+            asm volatile("" : "+a"(a)::"memory"); // one tile in VGPRs at a time
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int row = i * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+              const int64_t m = m0 + wm * 128 + row;
+              // rows and columns past C are staged (from clamped operand
+              // indices) but never stored
+              *reinterpret_cast<O *>(stage + (rbase + row) * RS + col * (int)sizeof(O)) =
+                  Epi::apply(a[r], FULL || m < M ? m : M - 1, FULL || n < N ? n : N - 1, rv[r], cv, P);
+            }
           }
         }
-      }
+      };
+      if (M % 256 == 0 && N % 256 == 0) stage_tiles(std::true_type{});
+      else stage_tiles(std::false_type{});
     }
     __syncthreads();
     const int64_t mrow0 = m0 + (one_pass ? 0 : h * 128);
@@ -348,6 +357,11 @@ __device__ __forceinline__ void mmd_dma16(const void *g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory");
 }
 
+// 16 bytes per lane from the wave-uniform base + the lane's 32-bit offset
+// into LDS at M0 + 16 * lane
+__device__ __forceinline__ void mmd_dma16_off(const char *base, uint32_t off, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr) : "memory");
+}
 // 4 bytes per lane into LDS at M0 + 4 * lane
 __device__ __forceinline__ void mmd_dma4(const void *g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr) : "memory");
@@ -556,40 +570,57 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   auto kn16_swz = [](int kr) { return (kr & 3) << 2; };
 
   // DMA d (0..7) of K slice s into ring slot `slot`: d < 4 this wave's A
-  // rows (32 * wave ..), else its B rows, 8 rows per instruction
-  auto issue_one = [&](int s, int slot, int d) {
-    const uint32_t st = lds0 + (uint32_t)(slot * 2 * MMD2_SLICE) + (d < 4 ? 0u : (uint32_t)MMD2_SLICE);
+  // rows (32 * wave ..), else its B rows, 8 rows per instruction.  Each lane's
+  // source is a 32-bit offset, fixed for the whole loop, from a wave-uniform
+  // base that advances by one K slice per step, so a step's DMAs cost no
+  // vector address arithmetic.
+  //   row-major operand: offset (row - row0) * Kb + 16 g from the tile's
+  //     first row (rows past the end re-read the last row);
+  //   K-major operand (int8): 4 k-rows of 256 columns per instruction, lane l
+  //     filling position l % 16 of k-row 4 blk + l / 16 with logical granule
+  //     (l % 16) ^ kn_swz(k-row); offset k-row * cols + column from the
+  //     slice's first k-row (columns past the end re-read valid bytes,
+  //     masked later);
+  //   K-major 16-bit: a 128-byte slice is 64 k-rows of 512 bytes, lane l
+  //     filling position l % 32 of k-row 2 blk + l / 32 with logical granule
+  //     (8 columns) (l % 32) ^ kn16_swz(k-row).
+  // The lowering keeps these offsets below 2^32 (256 rows of K bytes, or
+  // 128 bytes' worth of k-rows).
+  uint32_t dofs[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
     const int blk = wave * 4 + (d & 3);
-    const int r = 8 * blk + lane / 8;
-    const int g = (lane % 8) ^ ((r >> 1) & 7);
     const bool kmaj = d >= 4 ? BKN : AKM; // this operand is stored [K, columns]
     if (kmaj) {
-      const char *base = d >= 4 ? Bb : Ab;
       const int64_t cols = d >= 4 ? N : M, c0 = d >= 4 ? n0 : m0;
       if constexpr (ESZ == 1) {
-        // 4 k-rows of 256 columns: lane l fills position l % 16 of k-row
-        // 4 blk + l / 16 with logical granule (l % 16) ^ kn_swz(k-row)
         const int kr = 4 * blk + lane / 16;
         const int gg = (lane % 16) ^ kn_swz(kr);
         int64_t col = c0 + 16 * gg;
-        col = col + 16 <= cols ? col : cols - 16; // columns past the end: any valid bytes (masked later)
-        mmd_dma16(base + ((int64_t)s * 128 + kr) * cols + col, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+        col = col + 16 <= cols ? col : cols - 16;
+        dofs[d] = (uint32_t)(kr * cols + col);
       } else {
-        // 16-bit elements: a 128-byte slice is 64 k-rows of 512 bytes; lane l
-        // fills position l % 32 of k-row 2 blk + l / 32 with logical granule
-        // (8 columns) (l % 32) ^ kn16_swz(k-row)
         const int kr = 2 * blk + lane / 32;
         const int gg = (lane % 32) ^ kn16_swz(kr);
         int64_t col = c0 + 8 * gg;
         col = col + 8 <= cols ? col : cols - 8;
-        mmd_dma16(base + (((int64_t)s * 64 + kr) * cols + col) * 2, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+        dofs[d] = (uint32_t)((kr * cols + col) * 2);
       }
-      return;
+    } else {
+      const int r = 8 * blk + lane / 8;
+      const int g = (lane % 8) ^ ((r >> 1) & 7);
+      const int64_t rows = d < 4 ? M : N, row0 = d < 4 ? m0 : n0;
+      int64_t row = row0 + r;
+      row = row < rows ? row : rows - 1;
+      dofs[d] = (uint32_t)((row - row0) * Kb + g * 16);
     }
-    const int64_t rows = d < 4 ? M : N, row0 = d < 4 ? m0 : n0;
-    int64_t row = row0 + r;
-    row = row < rows ? row : rows - 1;
-    mmd_dma16((d < 4 ? Ab : Bb) + row * Kb + (int64_t)s * 128 + g * 16, __builtin_amdgcn_readfirstlane(st + blk * 1024));
+  }
+  const char *const dbase[2] = {AKM ? Ab : Ab + m0 * Kb, BKN ? Bb : Bb + n0 * Kb};
+  const int64_t dstride[2] = {AKM ? 128 * M : 128, BKN ? 128 * N : 128};
+  auto issue_one = [&](int s, int slot, int d) {
+    const uint32_t st = lds0 + (uint32_t)(slot * 2 * MMD2_SLICE) + (d < 4 ? 0u : (uint32_t)MMD2_SLICE) +
+                        (uint32_t)((wave * 4 + (d & 3)) * 1024);
+    mmd_dma16_off(dbase[d >= 4] + (int64_t)s * dstride[d >= 4], dofs[d], __builtin_amdgcn_readfirstlane(st));
   };
   // the scales of K slice s: wave w carries 64 rows (w < 4: A rows 64 w ..,
   // else B columns 64 (w - 4) ..), 4 bytes each

@@ -126,33 +126,60 @@ def input_sets(dargs):
     return sets
 
 
-def time_group(grp, sets, steps, warmup):
+def time_group(grp, sets, steps, warmup, min_warm_s=0.25):
     """Kernel time per launch (ms): K back-to-back launches between two HIP
-    events on the stream they are launched on, total / K.  A spin kernel is
-    queued first so the host enqueues all K launches before the first one
-    runs: the timed region holds no host launch gaps."""
+    events on the stream they are launched on, total / K.
+
+    Warmup: at least W launches and at least `min_warm_s` of back-to-back
+    work.  After the host has been idle the MI355X's clocks take tens of
+    milliseconds of load to come back up (measured: a 4096^3 W8A8 launch runs
+    ~10 % slower over its first ~100 launches after a 0.2 s pause than after
+    1000), so a fixed handful of warmup launches would time the ramp, not the
+    kernel.
+
+    Timed region: the host must never leave the GPU idle between the K
+    launches.  When one launch runs longer than the host takes to enqueue it,
+    a lead of untimed launches queued just before the start event keeps the
+    GPU busy (at full clock) while the host enqueues the K timed ones;
+    otherwise a spin kernel covers the enqueue."""
     import torch
     stream = torch.cuda.current_stream()
     n = len(sets)
+    torch.cuda.synchronize()
+    i = 0
     t0 = time.perf_counter()
-    for i in range(warmup):
-        grp(*sets[i % n])
-    enq = (time.perf_counter() - t0) / max(1, warmup)
-    torch.cuda.synchronize()
-    # spin long enough to cover the host-side enqueue of K launches
-    cal0, cal1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    cal0.record(stream)
-    torch.cuda._sleep(1 << 20)
-    cal1.record(stream)
-    torch.cuda.synchronize()
-    s_per_cycle = cal0.elapsed_time(cal1) * 1e-3 / (1 << 20)
-    spin = int(min(2.0, 2.0 * enq * steps + 0.005) / s_per_cycle)
+    block_enq, block_wall = [], []
+    while i < warmup or time.perf_counter() - t0 < min_warm_s:
+        b0 = time.perf_counter()
+        for _ in range(32):
+            grp(*sets[i % n])
+            i += 1
+        b1 = time.perf_counter()
+        torch.cuda.synchronize()
+        b2 = time.perf_counter()
+        block_enq.append((b1 - b0) / 32)
+        block_wall.append((b2 - b0) / 32)
+    enq = sorted(block_enq)[len(block_enq) // 2]      # host seconds per launch
+    per = sorted(block_wall)[len(block_wall) // 2]    # >= GPU seconds per launch
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(spin)
+    if per > 1.5 * enq:
+        lead = int(2.0 * enq * steps / per) + 16
+        for _ in range(lead):
+            grp(*sets[i % n])
+            i += 1
+    else:
+        cal0, cal1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cal0.record(stream)
+        torch.cuda._sleep(1 << 20)
+        cal1.record(stream)
+        torch.cuda.synchronize()
+        s_per_cycle = cal0.elapsed_time(cal1) * 1e-3 / (1 << 20)
+        torch.cuda._sleep(int(min(2.0, 2.0 * enq * steps + 0.005) / s_per_cycle))
     t0 = time.perf_counter()
     start.record(stream)
-    for i in range(steps):
+    for _ in range(steps):
         grp(*sets[i % n])
+        i += 1
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
