@@ -730,12 +730,8 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     mmd_wait_vm<DPS>();
     __syncthreads();
     fetch(s, 0, f0);
-    if constexpr (!MX) fetch(s, 1, f1);
+    fetch(s, 1, f1);
     if constexpr (MX) {
-      // the second half's fragments are read after the first half's MFMAs
-      // are issued: a scaled MFMA takes its operands as 8-register tuples,
-      // and a whole slice of them beside the scales does not fit the 128
-      // VGPRs left next to the accumulators
       read_scales(s);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -743,8 +739,6 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
         for (int j = 0; j < 2; ++j)
           acc[i][j] = Op::template run<0>(mx_cat(f0[0][i], f0[1][i]), mx_cat(f0[0][4 + j], f0[1][4 + j]), acc[i][j],
                                           (int)sa_w[i], (int)sb_w[j]);
-      __builtin_amdgcn_sched_barrier(0);
-      fetch(s, 1, f1);
     } else {
 #pragma unroll
       for (int q = 0; q < 2; ++q)
