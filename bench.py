@@ -516,6 +516,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None, help="measure one group (e.g. for rocprofv3)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--warm-seconds", type=float, default=0.25,
+                    help="minimum untimed back-to-back work before each group's timed steps (clock ramp)")
     ap.add_argument("--summarize-stats", nargs=2, metavar=("DIR", "OUT"),
                     help="write a text summary of a rocprofv3 --stats csv run")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
@@ -567,7 +569,7 @@ def main():
             dargs, host_ins = device_inputs(name, dev)
         log(f"[bench] {name}: timing {args.steps} steps")
         sets = input_sets(dargs)
-        total_ms, wall = time_group(grp, sets, args.steps, args.warmup)
+        total_ms, wall = time_group(grp, sets, args.steps, args.warmup, args.warm_seconds)
         ms = total_ms / args.steps
         kern_ms = ms
         meta = grp.meta
@@ -607,7 +609,7 @@ def main():
     line = {
         "metric": "HBM GB/s (% of peak) per fused HFusion group; W8A8 mmad TOPS (% MFMA)",
         "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "warm_seconds": args.warm_seconds, "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32", "argmax": "f32",
                   "w8a8_dequant": "int8", "w8a8_dequant_kn": "int8", "bf16_mmad": "bf16",
                   "transpose_cast": "bf16", "mx_fp8": "fp8 (e4m3, e8m0 scales)",
