@@ -2123,9 +2123,20 @@ struct EltwiseEmitter {
       << "  constexpr int VEC = " << VEC << ";\n";
     for (const Value *v : staged)
       k << "  __shared__ " << wordType(v->type.elem) << " " << ldsName(v) << "[" << TILE * PITCH << "];\n";
+    // Workgroup b runs on XCD b % 8.  Each run of 8 G consecutive tiles is
+    // dealt out so that XCD x takes G consecutive tiles of it (G = NTL / 8
+    // when a row of tiles splits evenly: each XCD then extends its own
+    // stretch of every output row).  Measured at [4096, 8192] bf16 -> f32:
+    // 37.7 us dealt one tile at a time, 36.1 us with G = 4 (2 and 8: 36.4,
+    // 36.5; 16 and 64: 37.2, 38.1).
+    const int64_t G = NTL % 8 == 0 && NTL / 8 <= 8 ? NTL / 8 : NTL >= 32 ? 4 : 1;
+    const int64_t NTF = NT / (8 * G) * (8 * G);
     k << "  for (int64_t tile = blockIdx.x; tile < " << NT << "ll; tile += gridDim.x) {\n"
-      << "    int64_t t_ = tile;\n"
-      << "    const int64_t tl_ = t_ % " << NTL << "ll; t_ /= " << NTL << "ll;\n"
+      << "    int64_t t_ = tile;\n";
+    if (G > 1)
+      k << "    if (tile < " << NTF << "ll) t_ = tile / " << 8 * G << "ll * " << 8 * G << "ll + tile % 8 * " << G
+        << "ll + tile % " << 8 * G << "ll / 8;\n";
+    k << "    const int64_t tl_ = t_ % " << NTL << "ll; t_ /= " << NTL << "ll;\n"
       << "    const int64_t tq_ = t_ % " << NTQ << "ll; t_ /= " << NTQ << "ll;\n";
     for (int d = r - 1; d >= 0; --d) {
       if (d == TQ || d == LD) continue;
