@@ -143,7 +143,7 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
   try {
     hfc::LowerOptions lo;
     if (opts.count("ordered_fp_sums")) lo.orderedFloatSums = opts["ordered_fp_sums"] == "1" ? 1 : 0;
-    lo.rmsqKernel = opts.count("rmsq_kernel") && opts["rmsq_kernel"] == "1";
+    lo.rmsqKernel = !(opts.count("rmsq_kernel") && opts["rmsq_kernel"] == "0");
     lo.rmsnKernel = opts.count("rmsn_kernel") && opts["rmsn_kernel"] == "1";
     lo.mxExact = opts.count("mx_exact") && opts["mx_exact"] == "1";
     plans = hfc::lowerModule(*mod, lo);

@@ -4076,10 +4076,10 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
           rows = A.D.size() <= 2 && reducesLastDimOnly(A);
         }
         RmsqMatch rq;
-        if (rows && opt.rmsqKernel && matchRmsQuant(A, rq)) {
-          p = lowerRmsQuant(A, rq, kname);
-        } else if (rows && opt.rmsnKernel && matchRmsQuant(A, rq)) {
+        if (rows && opt.rmsnKernel && matchRmsQuant(A, rq)) {
           p = lowerRmsNorm(A, rq, kname);
+        } else if (rows && opt.rmsqKernel && matchRmsQuant(A, rq)) {
+          p = lowerRmsQuant(A, rq, kname);
         } else if (rows) {
           RowEmitter e(A, opt);
           p = e.run(kname, "LAST_AXIS_PBR");

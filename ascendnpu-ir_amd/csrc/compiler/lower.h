@@ -54,7 +54,9 @@ struct LowerOptions {
   // the sum (tree order elsewhere); the default (-1) is the serial order for
   // rows of at most 4096 elements
   int orderedFloatSums = -1;
-  bool rmsqKernel = false;       // RMSNorm + dynamic quantisation through hf_rmsq.h
+  // RMSNorm + dynamic quantisation (matchRmsQuant) through hf_rmsq.h, the
+  // default for rows it takes (option rmsq_kernel=0: the generic row program)
+  bool rmsqKernel = true;
   bool mxExact = false;          // matmul_mx through scaled bf16 operands and the bf16 matrix core
   bool rmsnKernel = false;       // ... through hf_rmsn.h (chain wave + product maxima; opt-in)
 };

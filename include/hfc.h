@@ -38,6 +38,14 @@
  *                           LAST_AXIS_PBR, ANY_PBR, MIX_CV), as the
  *                           reference's --test-assign-fusion-kind does
  *   ordered_fp_sums=0|1     serial-order fp32 sums for every linalg.reduce addf
+ *   rmsq_kernel=0|1         RMSNorm + dynamic int8 quantisation groups: 1 (the
+ *                           default) through the one-wave-per-row exact
+ *                           parallel sum where the widths allow, 0 through the
+ *                           generic row program
+ *   rmsn_kernel=1           the same groups through the chain-wave kernel
+ *   mx_exact=1              hfusion.matmul_mx through scaled bf16 operands and
+ *                           the bf16 matrix core (exact products, f32 sums)
+ *   dyn=<func>:<arg>.<dim>=<size>,...  sizes of dynamic dims
  *
  * Returns 0 on success; a negative code with a message in `err` otherwise
  * (mirrors the reference's "[ERROR] ..." + EXIT_FAILURE convention).

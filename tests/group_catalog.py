@@ -1239,9 +1239,13 @@ def entries():
     e["softmax_dyn"] = g.with_dynamic_rows(g.safe_softmax(7919, 1000), 7919)
     e["vec_add_dyn"] = g.with_dynamic_rows(g.vec_add(7919), 7919)
     e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
-    # the same groups through the opt-in one-wave-per-row kernel (hf_rmsq.h)
+    # the same groups through the one-wave-per-row kernel (hf_rmsq.h, the
+    # default for the widths it takes), named for it ...
     for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3", "rmsnorm_quant_ragged"):
         e[n + "_rmsq"] = e[n]
+    # ... through the generic row program (option rmsq_kernel=0) ...
+    for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3"):
+        e[n + "_rowprog"] = e[n]
     # ... and through the opt-in chain-wave kernel (hf_rmsn.h)
     for n in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3"):
         e[n + "_rmsn"] = e[n]
@@ -1295,6 +1299,8 @@ def options(name):
         return dyn_options(name, DYN_ROWS[name][0])
     if name.endswith("_rmsq"):
         return "rmsq_kernel=1"
+    if name.endswith("_rowprog"):
+        return "rmsq_kernel=0"
     if name.endswith("_exact"):
         return "mx_exact=1"
     return "rmsn_kernel=1" if name.endswith("_rmsn") else ""

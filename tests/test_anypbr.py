@@ -152,7 +152,7 @@ def test_lowering_kinds(tmp_path):
     assert "serial-order" in kinds["sum_rank3_last"][1]
     assert kinds["max_bias_rank3"][0] == "ANY_PBR"        # [S,C] operand: no row layout
     rq = hf.compile(cat.get("rmsnorm_quant_rank3")).blocks[0]
-    assert rq["kind"] == "LAST_AXIS_PBR" and "serial-order" in rq.get("variant", "")
+    assert rq["kind"] == "LAST_AXIS_PBR" and "binade-run exact serial sum" in rq.get("variant", "")
 
 
 # ----------------------------------------------------------------- GPU parity

@@ -76,7 +76,7 @@ def test_classification_and_ties(tmp_path):
         assert b["kind"] == kind, name
     b = hf.parse_manifest(str(tmp_path / "rmsnorm_quant") + ".manifest")[0]
     assert [r["tied"] for r in b["results"]] == [2, 3]
-    assert "serial-order" in b["variant"]
+    assert "binade-run exact serial sum" in b["variant"]
     assert b["algo_bytes"] == 100704256
     b = hf.parse_manifest(str(tmp_path / "w8a8_dequant") + ".manifest")[0]
     assert b["algo_ops"] == 2 * 4096 ** 3

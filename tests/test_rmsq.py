@@ -1,5 +1,6 @@
-"""The opt-in RMSNorm + dynamic int8 quantisation kernel (hf_rmsq.h, compiler
-option rmsq_kernel=1; catalog names ending in _rmsq): its exact
+"""The RMSNorm + dynamic int8 quantisation kernel (hf_rmsq.h, the default for
+rows of 1024..4096 columns in multiples of 1024; option rmsq_kernel=0 selects
+the generic row program, catalog names ending in _rowprog): its exact
 serial fp32 sum of squares (binade runs composed across lanes, stitched from
 the init) on rows built to stress every path of the stitch, bit-exact against
 the CPU oracle's serial loop.
@@ -61,10 +62,10 @@ def stress_rows(rows=256, seed=0x524D53):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["rmsnorm_quant_256_rmsq", "rmsnorm_quant_256", "rmsnorm_quant_256_rmsn"])
+@pytest.mark.parametrize("name", ["rmsnorm_quant_256", "rmsnorm_quant_256_rowprog", "rmsnorm_quant_256_rmsn"])
 def test_rmsq_stress_rows_bit_exact(gpu, name):
-    """The stress rows through the three kernels of the pattern: the opt-in
-    parallel sum (hf_rmsq.h), the generic row program (the default) and the
+    """The stress rows through the three kernels of the pattern: the
+    parallel sum (hf_rmsq.h, the default), the generic row program and the
     opt-in chain-wave kernel (hf_rmsn.h, whose exact re-execution takes the
     NaN, infinite, overflowing and zero rows)."""
     print(f"[case] {name} stress rows", flush=True)
@@ -81,20 +82,22 @@ def test_rmsq_stress_rows_bit_exact(gpu, name):
     assert bad.size == 0, f"codes differ in rows {bad[:16]}"
 
 
-def test_rmsq_selected_only_when_asked():
+def test_rmsq_kernel_selection():
     for name in ("rmsnorm_quant", "rmsnorm_quant_256", "rmsnorm_quant_rank3"):
         v = hf.compile(cat.get(name)).blocks[0]["variant"]
+        assert "binade-run" in v, name
+        v = hf.compile(cat.get(name), options="rmsq_kernel=1").blocks[0]["variant"]
+        assert "binade-run" in v, name
+        v = hf.compile(cat.get(name), options="rmsq_kernel=0").blocks[0]["variant"]
         assert v.startswith("row-resident, serial-order"), name
         v = hf.compile(cat.get(name), options="rmsn_kernel=1").blocks[0]["variant"]
         assert "serial-order" in v and "chain wave" in v, name
-        v = hf.compile(cat.get(name), options="rmsq_kernel=1").blocks[0]["variant"]
-        assert "binade-run" in v, name
     # a width the kernel does not take keeps the generic row program
-    v = hf.compile(cat.get("rmsnorm_quant_ragged"), options="rmsq_kernel=1").blocks[0]["variant"]
+    v = hf.compile(cat.get("rmsnorm_quant_ragged")).blocks[0]["variant"]
     assert "serial-order" in v
 
 
-SHAPES = {"rmsnorm_quant_rmsq": (8192, 4096), "rmsnorm_quant_rank3_rmsq": (4, 64, 1024),
+SHAPES = {"rmsnorm_quant_rowprog": (8192, 4096), "rmsnorm_quant_rank3_rowprog": (4, 64, 1024),
           "rmsnorm_quant_ragged_rmsq": (13, 1000), "rmsnorm_quant_rmsn": (8192, 4096),
           "rmsnorm_quant_rank3_rmsn": (4, 64, 1024), "rmsnorm_quant_rank3": (4, 64, 1024)}
 
