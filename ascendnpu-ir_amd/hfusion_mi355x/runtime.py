@@ -206,6 +206,16 @@ class Group:
         """Launches the group on `stream` (torch's current stream by default).
         noalloc=True goes through hfr_group_launch_noalloc (the library's
         static scratch instead of a workspace)."""
+        return self._bind(args, results, stream, workspace, noalloc)()
+
+    def launcher(self, *args, results=None, stream=None, workspace=None, noalloc=False):
+        """The launch of __call__ with its arguments checked and packed once:
+        returns a callable that only enqueues the kernels (for loops that
+        launch the same buffers many times)."""
+        fn = self._bind(args, results, stream, workspace, noalloc)
+        return lambda: fn()
+
+    def _bind(self, args, results, stream, workspace, noalloc):
         import torch
         params = self.meta["params"]
         if len(args) != len(params):
@@ -239,14 +249,22 @@ class Group:
                 rptrs[j] = t.data_ptr()
         if stream is None:
             stream = torch.cuda.current_stream(device).cuda_stream
+        ret = outs[0] if len(outs) == 1 else tuple(outs)
+        lib, h, n, nr = native.hfr(), self._h, len(params), len(res_meta)
         if noalloc:
             if workspace is not None:
                 raise ValueError("noalloc launches take no workspace")
-            native.check(native.hfr().hfr_group_launch_noalloc(self._h, slots, len(params), rptrs, len(res_meta), stream))
+
+            def launch():
+                native.check(lib.hfr_group_launch_noalloc(h, slots, n, rptrs, nr, stream))
+                return ret
         else:
             ws = workspace.data_ptr() if workspace is not None else None
-            native.check(native.hfr().hfr_group_launch(self._h, slots, len(params), rptrs, len(res_meta), ws, stream))
-        return outs[0] if len(outs) == 1 else tuple(outs)
+
+            def launch():
+                native.check(lib.hfr_group_launch(h, slots, n, rptrs, nr, ws, stream))
+                return ret
+        return launch
 
 
 def _check_arg(i, a, p, name):

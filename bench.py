@@ -31,7 +31,10 @@ ORDER = ["rmsnorm_quant", "vec_add", "safe_softmax", "argmax", "w8a8_dequant"]
 # the block-scaled fp8 contraction (hfusion.matmul_mx)
 EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast", "mx_fp8", "mx_fp8_exact"]
 # bench names that are a product group compiled with options
-VARIANTS = {"mx_fp8_exact": ("mx_fp8", "mx_exact=1")}
+VARIANTS = {"mx_fp8_exact": ("mx_fp8", "mx_exact=1"),
+            # the other kernels of the RMSNorm pattern, for --only runs
+            "rmsnorm_quant_rowprog": ("rmsnorm_quant", "rmsq_kernel=0"),
+            "rmsnorm_quant_rmsn": ("rmsnorm_quant", "rmsn_kernel=1")}
 FP8_PEAK_TFLOPS = 5000.0  # dense fp8 MFMA (the block-scaled form runs at the same rate)
 
 
@@ -141,10 +144,18 @@ def time_group(grp, sets, steps, warmup, min_warm_s=0.25):
     launches.  When one launch runs longer than the host takes to enqueue it,
     a lead of untimed launches queued just before the start event keeps the
     GPU busy (at full clock) while the host enqueues the K timed ones;
-    otherwise a spin kernel covers the enqueue."""
+    otherwise a spin kernel covers the enqueue (the clocks sink while it
+    spins, so this is the fallback: a group's packed launch enqueues in a few
+    microseconds, well under any of the configs' kernels)."""
     import torch
     stream = torch.cuda.current_stream()
     n = len(sets)
+    # a group's launches are checked and packed once per input set, so that the
+    # host enqueues each step in a few microseconds
+    if hasattr(grp, "launcher"):
+        fns = [grp.launcher(*s) for s in sets]
+        grp = lambda *a, _f=fns: _f[a[0]]()
+        sets = [(k,) for k in range(n)]
     torch.cuda.synchronize()
     i = 0
     t0 = time.perf_counter()
@@ -566,7 +577,7 @@ def main():
         if name in EXTRA:
             dargs, host_ins = generic_inputs(grp.meta, dev), None
         else:
-            dargs, host_ins = device_inputs(name, dev)
+            dargs, host_ins = device_inputs(base, dev)
         log(f"[bench] {name}: timing {args.steps} steps")
         sets = input_sets(dargs)
         total_ms, wall = time_group(grp, sets, args.steps, args.warmup, args.warm_seconds)
@@ -598,14 +609,15 @@ def main():
             f"{ms * 1e3:.1f} us/step")
         if not args.no_cpu and host_ins is not None and (name == HEADLINE or args.only):
             log(f"[bench] {name}: CPU baseline (oracle restatement, 1 core)")
-            headline_cpu = cpu_baseline(name, host_ins)
-            headline_cpu_mt = cpu_baseline_mt(name, host_ins)
+            headline_cpu = cpu_baseline(base, host_ins)
+            headline_cpu_mt = cpu_baseline_mt(base, host_ins)
         entry["input_sets"] = len(sets)
         del dargs, sets
         torch.cuda.empty_cache()
     head = HEADLINE if HEADLINE in groups else names[0]
+    head_base = VARIANTS.get(head, (head, ""))[0]
     h = groups[head]
-    cfg = hf.groups.CONFIGS[head]["kw"] if head in hf.groups.CONFIGS else {}
+    cfg = hf.groups.CONFIGS[head_base]["kw"] if head_base in hf.groups.CONFIGS else {}
     line = {
         "metric": "HBM GB/s (% of peak) per fused HFusion group; W8A8 mmad TOPS (% MFMA)",
         "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -613,7 +625,7 @@ def main():
         "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32", "argmax": "f32",
                   "w8a8_dequant": "int8", "w8a8_dequant_kn": "int8", "bf16_mmad": "bf16",
                   "transpose_cast": "bf16", "mx_fp8": "fp8 (e4m3, e8m0 scales)",
-                  "mx_fp8_exact": "fp8 (e4m3, e8m0 scales) via bf16"}[head],
+                  "mx_fp8_exact": "fp8 (e4m3, e8m0 scales) via bf16"}[head_base if head_base != "mx_fp8" else head],
         "data": "synthetic (seeded splitmix64)",
         "config": {"workload": head, **{k: v for k, v in cfg.items()}},
         "roofline": h["roofline"],
