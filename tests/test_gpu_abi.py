@@ -217,3 +217,28 @@ def test_memref_strided_views(gpu, x_transposed):
     outside = np.ones(Q.shape, bool)
     outside.T[3:3 + rows, 6:6 + cols] = False
     assert bool((gQ[outside] == 0x5A).all()) and bool((gS[:4] == -1.0).all()) and bool((gS[4 + rows:] == -1.0).all())
+
+
+def test_group_launcher_repeats_the_launch(gpu):
+    """Group.launcher: the arguments checked and packed once, then launched
+    three times over new contents of the same buffers; each launch matches
+    the oracle on the contents it saw (safe softmax rows, bf16 out, within
+    the softmax bar of 1 bf16 ulp)."""
+    import torch
+    from helpers import bf16_ulp_diff
+    note("launcher safe_softmax_ragged x3")
+    art = hf.compile(cat.get("safe_softmax_ragged"), options=cat.options("safe_softmax_ragged"), require_cached=True)
+    grp = art.load()
+    p = grp.meta["params"]
+    rows, cols = p[0]["shape"]
+    x = to_dev(np.zeros((rows, cols), np.float32), p[0]["elem"], gpu)
+    o = to_dev(np.zeros((rows, cols), np.uint16), p[1]["elem"], gpu)
+    go = grp.launcher(x, o)
+    for k in range(3):
+        xs = I.normal_f32(I.SEED_BASE + 900 + k, (rows, cols), 2.0)
+        x.copy_(torch.from_numpy(xs).to(gpu))
+        go()
+        torch.cuda.synchronize()
+        ref, = run_oracle("safe_softmax_ragged", [xs, np.zeros((rows, cols), np.uint16)])
+        d = bf16_ulp_diff(to_host(o, p[1]["elem"]), ref)
+        assert d.max() <= 1, (k, int(d.max()))
