@@ -187,7 +187,44 @@ void specializeFunc(Func &f, const std::map<std::pair<int, int>, int64_t> &sizes
 
 } // namespace
 
+// spec "runtime": the row count stays a launch-time value
+void specializeRuntimeRows(Module &m) {
+  for (auto &f : m.funcs) {
+    std::vector<Value *> vals(f->args.begin(), f->args.end());
+    for (Op *op : f->ops)
+      for (Value *r : op->results) vals.push_back(r);
+    // the dims that are dynamic now: each must end up as the row count itself
+    std::vector<std::pair<Value *, size_t>> dyn;
+    for (Value *v : vals)
+      for (size_t d = 0; d < v->type.shape.size(); ++d) {
+        if (v->type.shape[d] == kRuntimeRows)
+          throw CompileError("@" + f->name + " has a static dim of " + std::to_string(kRuntimeRows) +
+                             ", the placeholder of runtime row counts");
+        if (v->type.shape[d] < 0) dyn.push_back({v, d});
+      }
+    if (dyn.empty()) continue;
+    std::map<std::pair<int, int>, int64_t> sizes;
+    for (Value *a : f->args)
+      for (size_t d = 0; d < a->type.shape.size(); ++d) {
+        if (a->type.shape[d] >= 0) continue;
+        if (d != 0)
+          throw CompileError("runtime row counts: dynamic dim " + std::to_string(d) + " of argument " +
+                             std::to_string(a->argIdx) + " of @" + f->name + " is not dim 0");
+        sizes[{a->argIdx, 0}] = kRuntimeRows;
+      }
+    specializeFunc(*f, sizes);
+    for (auto &vd : dyn)
+      if (vd.first->type.shape[vd.second] != kRuntimeRows)
+        throw CompileError("runtime row counts: dim " + std::to_string(vd.second) + " of " + vd.first->name + " in @" +
+                           f->name + " is derived from the row count, not the row count itself (compile per size)");
+  }
+}
+
 void specializeDynamic(Module &m, const std::string &spec) {
+  if (spec == "runtime") {
+    specializeRuntimeRows(m);
+    return;
+  }
   // spec: <func>:<arg>.<dim>=<size>, comma-separated
   std::map<std::string, std::map<std::pair<int, int>, int64_t>> sizes;
   std::stringstream ss(spec);

@@ -146,6 +146,7 @@ int compileText(const std::string &text, const char *outPrefix, const char *opti
     lo.rmsqKernel = !(opts.count("rmsq_kernel") && opts["rmsq_kernel"] == "0");
     lo.rmsnKernel = opts.count("rmsn_kernel") && opts["rmsn_kernel"] == "1";
     lo.mxExact = opts.count("mx_exact") && opts["mx_exact"] == "1";
+    lo.runtimeRows = opts.count("dyn") && opts["dyn"] == "runtime";
     plans = hfc::lowerModule(*mod, lo);
   } catch (const hfc::CompileError &e) {
     setErr(err, errlen, std::string("lowering error: ") + e.what());

@@ -121,7 +121,11 @@ std::unique_ptr<Module> parseModule(const std::string &text);
 // Dynamic dims (shape -1 after parsing): true when any value has one.
 bool hasDynamicDims(const Module &m);
 // Makes every type static from the sizes of the functions' dynamic argument
-// dims, spec "<func>:<arg>.<dim>=<size>,..." (dynamic.cpp).
+// dims, spec "<func>:<arg>.<dim>=<size>,..." (dynamic.cpp).  Spec "runtime":
+// every dynamic dim must be the row count (dim 0 of the arguments, and only
+// that size where it flows); it becomes kRuntimeRows, which the lowering
+// turns into a kernel argument (LowerOptions::runtimeRows).
 void specializeDynamic(Module &m, const std::string &spec);
+constexpr int64_t kRuntimeRows = int64_t(1) << 30;
 
 } // namespace hfc

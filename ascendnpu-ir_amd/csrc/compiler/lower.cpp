@@ -838,6 +838,9 @@ struct Analysis {
   std::vector<BufferDesc> params, results;
   std::vector<int> resultTied;                 // tied param per result (-1: own buffer)
   std::set<int> paramsRead, paramsWritten;
+  // dim 0 is the runtime row count (kRuntimeRows): kernels take it as their
+  // last argument, hf_rows
+  bool rowsDyn = false;
 };
 
 // The func argument a destination operand finally writes into (through
@@ -1139,8 +1142,14 @@ std::string kernelParamList(const Analysis &A, std::vector<std::string> &kargs, 
   }
   if (withWs) {
     if (!first) s << ", ";
+    first = false;
     s << "void* __restrict__ ws";
     kargs.push_back("ws");
+  }
+  if (A.rowsDyn) {
+    if (!first) s << ", ";
+    s << "int64_t hf_rows";
+    kargs.push_back("rows");
   }
   return s.str();
 }
@@ -1761,6 +1770,13 @@ struct RowEmitter {
     for (size_t i = 0; i < A.params.size(); ++i) argNames += (A.params[i].role == "scalar" ? "s" : "p") + std::to_string(i) + ", ";
     for (size_t i = 0; i < A.results.size(); ++i)
       if (A.resultTied[i] < 0) argNames += "r" + std::to_string(i) + ", ";
+    if (A.rowsDyn) {
+      if (R != kRuntimeRows) throw CompileError("runtime row counts: the row program's rows are not the row count");
+      argNames += "hf_rows, ";
+      p.rowsDyn = true;
+      p.rowsA = 1;
+      p.rowsB = rowsPerBlock;
+    }
     std::string ldsParams = "uint64_t* lds_red, float* lds_chain, float* lds_bcast";
     std::string ldsArgs = "lds_red_, lds_chain_, lds_bcast_";
     // the row program, instantiated for a fast (kFast) and an exact (kExact) mode
@@ -1769,7 +1785,8 @@ struct RowEmitter {
       << "  constexpr int TR = " << TR << ", RB = " << RB << ", RPW = " << RPW << ", VEC = " << VEC << ", EPL = " << EPL
       << ", WPR = " << std::max(1, TR / 64) << ";\n"
       << "  constexpr bool MASKED = " << (masked ? "true" : "false") << ";\n"
-      << "  constexpr int64_t R = " << R << "ll, C = " << C << "ll;\n"
+      << (A.rowsDyn ? std::string("  const int64_t R = hf_rows;\n  constexpr int64_t C = ") + std::to_string(C) + "ll;\n"
+                    : "  constexpr int64_t R = " + std::to_string(R) + "ll, C = " + std::to_string(C) + "ll;\n")
       << "  const int tid = threadIdx.x, rloc = tid / TR, lt = tid % TR;\n"
       << "  int64_t row[RPW];\n  bool row_ok[RPW];\n"
       << "#pragma unroll\n  for (int rr = 0; rr < RPW; ++rr) {\n"
@@ -2054,11 +2071,17 @@ struct EltwiseEmitter {
     while (VEC > 1 && L % VEC) VEC /= 2;
     chooseStaging();
     if (TQ >= 0) return runTiled(kname, kind);
+    // a runtime row count: dim 0 is the row count, the rest a static row
+    const bool dynRows = A.rowsDyn && r >= 2 && A.D[0] == kRuntimeRows;
     // coordinates of the chunk base
     std::ostringstream coords;
     if (r > 1) {
       coords << "    int64_t t_ = base;\n";
       for (int d = r - 1; d >= 0; --d) {
+        if (d == 0 && dynRows) {
+          coords << "    const int64_t c0 = t_;\n";
+          continue;
+        }
         coords << "    const int64_t c" << d << " = t_ % " << A.D[d] << "ll; t_ /= " << A.D[d] << "ll;\n";
       }
       coords << "    (void)t_;\n";
@@ -2074,11 +2097,20 @@ struct EltwiseEmitter {
     p.variant = "streaming";
     int block = 256;
     int64_t nch = N / VEC;
+    // chunks of VEC elements per row (a row's length is a multiple of VEC)
+    const int64_t nchRow = dynRows ? N / kRuntimeRows / VEC : 0;
+    if (dynRows) {
+      p.rowsDyn = true;
+      p.rowsA = nchRow;
+      p.rowsB = block;
+      p.rowsCap = 1 << 20;
+    }
     std::ostringstream k;
     k << "extern \"C\" __global__ __launch_bounds__(" << block << ") void " << kname << "("
       << kernelParamList(A, p.kargs, false) << ") {\n"
       << "  constexpr int VEC = " << VEC << ";\n"
-      << "  constexpr int64_t NCH = " << nch << "ll;\n"
+      << (dynRows ? "  const int64_t NCH = hf_rows * " + std::to_string(nchRow) + "ll;\n"
+                  : "  constexpr int64_t NCH = " + std::to_string(nch) + "ll;\n")
       << "  for (int64_t ch = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; ch < NCH; ch += (int64_t)gridDim.x * blockDim.x) {\n"
       << "    const int64_t base = ch * VEC;\n"
       << body.str() << "  }\n}\n";
@@ -3905,9 +3937,12 @@ KernelPlan lowerRmsQuant(Analysis &A, const RmsqMatch &m, const std::string &kna
     << "(" << kernelParamList(A, p.kargs, false) << ") {\n"
     << "  hf::rmsq_rows<" << C << ", " << m.lo << ", " << m.hi << ", " << WPB << ">((const uint16_t*)p" << m.x
     << ", (const uint16_t*)p" << m.gamma << ", (int8_t*)" << resultPtr(A, m.qRes) << ", (float*)" << resultPtr(A, m.sRes)
-    << ", " << R << "ll, " << floatLit((float)m.s0) << ", " << floatLit((float)m.K) << ", " << floatLit((float)m.eps) << ", "
+    << ", " << (A.rowsDyn ? std::string("hf_rows") : std::to_string(R) + "ll") << ", " << floatLit((float)m.s0) << ", "
+    << floatLit((float)m.K) << ", " << floatLit((float)m.eps) << ", "
     << floatLit((float)m.a0) << ", " << floatLit((float)m.qd) << ");\n}\n";
   p.source = k.str();
+  // a runtime row count keeps the full grid: waves past the last row exit
+  if (A.rowsDyn) p.rowsDyn = true;
   // three waves per SIMD (the occupancy the register budget allows), each
   // walking rows
   const int64_t waves = std::min<int64_t>(R, 3072);
@@ -4041,6 +4076,12 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
         if (v->type.uns) unsupported(op, "ui8 operand outside matmul_mx scales");
     }
     describeBuffers(A);
+    if (opt.runtimeRows) {
+      for (auto &b : A.params)
+        for (auto d : b.shape) A.rowsDyn |= d == kRuntimeRows;
+      for (auto &b : A.results)
+        for (auto d : b.shape) A.rowsDyn |= d == kRuntimeRows;
+    }
     std::string kname = "hf_" + f.name;
     KernelPlan p;
     const Op *single = findOp(f, [](const Op *o) { return isSingleOpKernel(o->name); });
@@ -4099,6 +4140,21 @@ std::vector<KernelPlan> lowerModule(Module &m, const LowerOptions &opt) {
     p.params = A.params;
     p.results = A.results;
     p.algoBytes = algoBytes(A);
+    if (A.rowsDyn) {
+      if (!p.rowsDyn)
+        throw CompileError("runtime row counts: @" + f.name + " lowers to a " + p.kind + " kernel (" + p.variant +
+                           "), which is compiled per size (dyn=<func>:<arg>.<dim>=<size>)");
+      // the row count must not be baked into the kernel anywhere else
+      if (p.source.find(std::to_string(kRuntimeRows)) != std::string::npos ||
+          p.source.find(std::to_string(kRuntimeRows - 1)) != std::string::npos)
+        throw CompileError("runtime row counts: the kernel of @" + f.name + " depends on the row count");
+      for (auto *bufs : {&p.params, &p.results})
+        for (auto &b : *bufs)
+          for (auto &d : b.shape)
+            if (d == kRuntimeRows) d = -1;
+      p.algoBytes /= (double)kRuntimeRows;
+      if (p.rowsA > 0) p.grid[0] = 1; // set at launch from the row count
+    }
     std::string declared = f.fusionKind();
     if (!declared.empty() && declared != p.kind && !(declared == "PURE_ELEMWISE" && p.kind == "ANY_PB") &&
         !(declared == "ANY_PB" && p.kind == "PURE_ELEMWISE") && !(declared == "ANY_PBR" && p.kind == "LAST_AXIS_PBR") &&
@@ -4133,6 +4189,7 @@ std::string emitManifest(const KernelPlan &p, const std::string &hsacoName) {
     << "workspace " << p.workspaceBytes << " " << (p.workspaceZeroInit ? 1 : 0) << "\n"
     << "algo_bytes " << (uint64_t)p.algoBytes << "\n"
     << "algo_ops " << (uint64_t)p.algoOps << "\n";
+  if (p.rowsDyn) s << "rows_dyn " << p.rowsA << " " << p.rowsB << " " << p.rowsCap << "\n";
   auto shp = [](const std::vector<int64_t> &v) {
     std::string r = std::to_string(v.size());
     for (auto d : v) r += " " + std::to_string(d);

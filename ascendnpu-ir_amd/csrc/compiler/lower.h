@@ -46,6 +46,13 @@ struct KernelPlan {
     std::vector<std::string> kargs;
   };
   std::vector<PreKernel> pre;
+  // runtime row count (compiler option dyn=runtime): the kernel takes the
+  // row count R as its last argument (karg "rows"); the launch grid is
+  // min(ceil(R * rowsA / rowsB), rowsCap) blocks (rowsCap 0: no cap), or the
+  // static grid when rowsA is 0.  Shapes hold -1 for the row dim, and
+  // algoBytes is per row.
+  bool rowsDyn = false;
+  int64_t rowsA = 0, rowsB = 1, rowsCap = 0;
 };
 
 struct LowerOptions {
@@ -59,6 +66,9 @@ struct LowerOptions {
   bool rmsqKernel = true;
   bool mxExact = false;          // matmul_mx through scaled bf16 operands and the bf16 matrix core
   bool rmsnKernel = false;       // ... through hf_rmsn.h (chain wave + product maxima; opt-in)
+  // dynamic dims specialised to kRuntimeRows (option dyn=runtime): the row
+  // count becomes a kernel argument where the group kind allows it
+  bool runtimeRows = false;
 };
 
 // Ops lowered as a kernel of their own (cumulative ops, histogram,

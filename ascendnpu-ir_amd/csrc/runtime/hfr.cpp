@@ -43,7 +43,7 @@ struct Buf {
 };
 
 struct Karg {
-  enum Kind { Param, Result, Workspace } kind;
+  enum Kind { Param, Result, Workspace, Rows } kind;
   int index;
 };
 
@@ -65,6 +65,10 @@ struct hfr_group {
   uint64_t wsBytes = 0;
   bool wsZero = false;
   uint64_t algoBytes = 0, algoOps = 0;
+  // runtime row count (manifest `rows_dyn a b cap`): grid.x = min(ceil(R * a
+  // / b), cap) (cap 0: none), or the static grid when a is 0
+  bool rowsDyn = false;
+  int64_t rowsA = 0, rowsB = 1, rowsCap = 0;
   std::vector<std::string> paramRoles;
   std::vector<Buf> paramBufs, resultBufs;
   std::vector<int> resultTied;
@@ -125,6 +129,7 @@ std::string dirOf(const std::string &p) {
 
 bool parseKarg(const std::string &k, Karg &a) {
   if (k == "ws") { a.kind = Karg::Workspace; a.index = 0; return true; }
+  if (k == "rows") { a.kind = Karg::Rows; a.index = 0; return true; }
   if (k.rfind("param:", 0) == 0) { a.kind = Karg::Param; a.index = std::atoi(k.c_str() + 6); return true; }
   if (k.rfind("result:", 0) == 0) { a.kind = Karg::Result; a.index = std::atoi(k.c_str() + 7); return true; }
   return false;
@@ -145,6 +150,11 @@ int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
     else if (key == "workspace") { int z = 0; is >> g.wsBytes >> z; g.wsZero = z != 0; }
     else if (key == "algo_bytes") is >> g.algoBytes;
     else if (key == "algo_ops") is >> g.algoOps;
+    else if (key == "rows_dyn") {
+      is >> g.rowsA >> g.rowsB >> g.rowsCap;
+      g.rowsDyn = true;
+      if (g.rowsA < 0 || g.rowsB <= 0 || g.rowsCap < 0) return fail(HFR_ERR_MANIFEST, "bad rows_dyn line: " + ln);
+    }
     else if (key == "param" || key == "result") {
       int i, tied = -1, rank = 0;
       std::string role;
@@ -191,6 +201,7 @@ int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
       if (a.kind == Karg::Result && (a.index < 0 || a.index >= (int)g.resultTied.size()))
         return fail(HFR_ERR_MANIFEST, "karg refers to a missing result");
       if (a.kind == Karg::Workspace && !g.wsBytes) return fail(HFR_ERR_MANIFEST, "karg ws without a workspace");
+      if (a.kind == Karg::Rows && !g.rowsDyn) return fail(HFR_ERR_MANIFEST, "karg rows without rows_dyn");
     }
     return (int)HFR_OK;
   };
@@ -266,8 +277,14 @@ int checkGroupArgs(const hfr_group *g, const uint64_t *params, size_t nparams, v
 // Assembles the kernel arguments (params, own result buffers, workspace) and
 // launches the group's kernels: its pre kernels in order, then the main one,
 // all on `stream`.
-int launchGroup(const hfr_group *g, const uint64_t *params, void *const *results, void *ws, void *stream) {
-  auto launch = [&](hipFunction_t fn, const hfr_launch_cfg &cfg, const std::vector<Karg> &kargs) {
+int launchGroup(const hfr_group *g, const uint64_t *params, void *const *results, void *ws, void *stream,
+                int64_t rows = -1) {
+  auto launch = [&](hipFunction_t fn, hfr_launch_cfg cfg, const std::vector<Karg> &kargs) {
+    if (g->rowsDyn && g->rowsA > 0) {
+      int64_t blocks = (rows * g->rowsA + g->rowsB - 1) / g->rowsB;
+      if (g->rowsCap > 0 && blocks > g->rowsCap) blocks = g->rowsCap;
+      cfg.grid[0] = (unsigned)(blocks > 0 ? blocks : 1);
+    }
     uint64_t args[HFR_MAX_KARGS];
     if (kargs.size() > HFR_MAX_KARGS) return fail(HFR_ERR_INVALID, "too many kernel arguments");
     size_t n = 0;
@@ -276,6 +293,7 @@ int launchGroup(const hfr_group *g, const uint64_t *params, void *const *results
       case Karg::Param: args[n++] = params[a.index]; break;
       case Karg::Result: args[n++] = (uint64_t)(uintptr_t)results[a.index]; break;
       case Karg::Workspace: args[n++] = (uint64_t)(uintptr_t)ws; break;
+      case Karg::Rows: args[n++] = (uint64_t)rows; break;
       }
     }
     return launchRaw(fn, cfg, args, n, stream);
@@ -425,8 +443,19 @@ int hfr_group_info_get(hfr_group_t g, hfr_group_info *info) {
 
 int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
                      void *workspace, void *stream) {
+  if (g && g->rowsDyn)
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " takes its row count at launch (hfr_group_launch_rows)");
+  return hfr_group_launch_rows(g, params, nparams, results, nresults, -1, workspace, stream);
+}
+
+int hfr_group_launch_rows(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
+                          int64_t rows, void *workspace, void *stream) {
+  if (g && !g->rowsDyn && rows != -1)
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " has a static row count");
+  if (g && g->rowsDyn && rows < 0) return fail(HFR_ERR_INVALID, "negative row count for group @" + g->func);
   int rc = checkGroupArgs(g, params, nparams, results, nresults);
   if (rc) return rc;
+  if (g->rowsDyn && rows == 0) return HFR_OK; // nothing to do
   void *ws = workspace;
   if (g->wsBytes && !ws) {
     int dev = 0;
@@ -434,7 +463,7 @@ int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void
     if (dev != g->ownWsDevice) return fail(HFR_ERR_INVALID, "group workspace belongs to another device");
     ws = g->ownWs;
   }
-  return launchGroup(g, params, results, ws, stream);
+  return launchGroup(g, params, results, ws, stream, rows);
 }
 
 } // extern "C"
@@ -650,7 +679,10 @@ struct View {
   int64_t numel = 1;
 };
 
-int readDesc(const Buf &b, const void *desc, const char *what, size_t idx, View &v) {
+// A dim the group gives as -1 (a runtime row count) takes the descriptor's
+// size, which must agree with every other such dim (`rows`, -1 until the
+// first).
+int readDesc(const Buf &b, const void *desc, const char *what, size_t idx, View &v, int64_t &rows) {
   if (!desc) return fail(HFR_ERR_INVALID, std::string("null descriptor for ") + what + " " + std::to_string(idx));
   const char *d = (const char *)desc;
   char *aligned = *(char *const *)(d + sizeof(void *));
@@ -662,7 +694,13 @@ int readDesc(const Buf &b, const void *desc, const char *what, size_t idx, View 
   v.rank = (int)b.shape.size();
   int64_t expect = 1;
   for (int k = v.rank; k-- > 0;) {
-    if (sizes[k] != b.shape[k])
+    if (b.shape[k] == -1) {
+      if (sizes[k] < 0) return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": negative size");
+      if (rows >= 0 && sizes[k] != rows)
+        return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": " + std::to_string(sizes[k]) +
+                                         " rows, another view has " + std::to_string(rows));
+      rows = sizes[k];
+    } else if (sizes[k] != b.shape[k])
       return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": size " + std::to_string(sizes[k]) +
                                        " in dim " + std::to_string(k) + ", the group expects " + std::to_string(b.shape[k]));
     v.sizes[k] = sizes[k];
@@ -765,6 +803,7 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
   std::vector<Staged> staged;
   std::vector<std::pair<int, size_t>> stagedParam, stagedResult; // index -> staged slot
   size_t total = 0;
+  int64_t rows = -1; // a runtime row count, read from the descriptors
   auto stage = [&](const View &v, const std::string &elem, bool read, bool written, const char *what, size_t idx) -> int {
     if (written && !nonOverlapping(v))
       return fail(HFR_ERR_INVALID, std::string(what) + " " + std::to_string(idx) + ": the written view overlaps itself");
@@ -782,7 +821,7 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
       continue;
     }
     View v;
-    int rc = readDesc(g->paramBufs[i], descs[i], "argument", i, v);
+    int rc = readDesc(g->paramBufs[i], descs[i], "argument", i, v, rows);
     if (rc) return rc;
     params[i] = (uint64_t)(uintptr_t)v.base;
     if (!v.dense) {
@@ -797,7 +836,7 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
     results[j] = nullptr;
     if (g->resultTied[j] >= 0) continue;
     View v;
-    int rc = readDesc(g->resultBufs[j], descs[k++], "result", j, v);
+    int rc = readDesc(g->resultBufs[j], descs[k++], "result", j, v, rows);
     if (rc) return rc;
     results[j] = v.base;
     if (!v.dense) {
@@ -806,8 +845,10 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
       stagedResult.push_back({(int)j, staged.size() - 1});
     }
   }
+  if (g->rowsDyn && rows < 0) return fail(HFR_ERR_INVALID, "group @" + g->func + ": no view carries the row count");
+  if (!g->rowsDyn) rows = -1;
   if (staged.empty())
-    return hfr_group_launch(g, params, g->paramRoles.size(), results, g->resultTied.size(), nullptr, stream);
+    return hfr_group_launch_rows(g, params, g->paramRoles.size(), results, g->resultTied.size(), rows, nullptr, stream);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hipFail(e, "hipGetDevice");
@@ -836,7 +877,7 @@ extern "C" int hfr_group_launch_memref(hfr_group_t g, void *const *descs, size_t
       int rc = stridedCopy(sv.v, sv.eb, base + sv.off, true, st);
       if (rc) return rc;
     }
-  int rc = hfr_group_launch(g, params, g->paramRoles.size(), results, g->resultTied.size(), nullptr, stream);
+  int rc = hfr_group_launch_rows(g, params, g->paramRoles.size(), results, g->resultTied.size(), rows, nullptr, stream);
   if (rc) return rc;
   for (auto &sv : staged)
     if (sv.written) {
@@ -885,6 +926,8 @@ extern "C" int hfr_group_launch_noalloc(hfr_group_t g, const uint64_t *params, s
                                         size_t nresults, void *stream) {
   int rc = checkGroupArgs(g, params, nparams, results, nresults);
   if (rc) return rc;
+  if (g->rowsDyn)
+    return fail(HFR_ERR_INVALID, "group @" + g->func + " takes its row count at launch (hfr_group_launch_rows)");
   if (g->wsBytes > HFR_SCRATCH_BYTES)
     return fail(HFR_ERR_INVALID, "group @" + g->func + " needs " + std::to_string(g->wsBytes) +
                                      " workspace bytes; the static scratch holds " + std::to_string(HFR_SCRATCH_BYTES));

@@ -76,6 +76,8 @@ def hfr():
         lib.hfr_program_info_get.argtypes = [vp, ctypes.POINTER(ProgramInfo)]
         lib.hfr_program_launch.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t,
                                            ctypes.POINTER(vp), ctypes.c_size_t, vp, vp]
+        lib.hfr_group_launch_rows.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t,
+                                              ctypes.POINTER(vp), ctypes.c_size_t, ctypes.c_int64, vp, vp]
         lib.hfr_group_launch_memref.argtypes = [vp, ctypes.POINTER(vp), ctypes.c_size_t, vp]
         lib.hfr_group_launch_noalloc.argtypes = [vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t,
                                                  ctypes.POINTER(vp), ctypes.c_size_t, vp]
@@ -83,7 +85,7 @@ def hfr():
         for fn in ("hfr_module_load", "hfr_module_unload", "hfr_kernel_get", "hfr_launch", "hfr_group_load",
                    "hfr_group_unload", "hfr_group_info_get", "hfr_group_launch", "hfr_program_load",
                    "hfr_program_unload", "hfr_program_info_get", "hfr_program_launch", "hfr_group_launch_memref",
-                   "hfr_group_launch_noalloc"):
+                   "hfr_group_launch_noalloc", "hfr_group_launch_rows"):
             getattr(lib, fn).restype = ctypes.c_int
         lib.hfr_last_error.restype = cp
         lib.hfr_version.restype = cp

@@ -153,6 +153,8 @@ def parse_manifest(path, with_programs=False):
                 b["results"].append(dict(tied=int(parts[1]), elem=parts[2], shape=_shape(parts, 3)))
             elif key == "karg":
                 b["kargs"].append(parts[0])
+            elif key == "rows_dyn":
+                b["rows_dyn"] = tuple(int(x) for x in parts)
             elif key == "pre":
                 b.setdefault("pre", []).append(dict(kernel=parts[0], grid=tuple(int(x) for x in parts[1:4]),
                                                     block=tuple(int(x) for x in parts[4:7]), kargs=parts[8:]))
@@ -220,6 +222,21 @@ class Group:
         params = self.meta["params"]
         if len(args) != len(params):
             raise TypeError(f"@{self.func} takes {len(params)} arguments ({len(args)} given)")
+        # a runtime row count (-1 row dims in the manifest): read from the
+        # arguments, which must agree
+        dyn = "rows_dyn" in self.meta
+        rows = None
+        for i, (a, p) in enumerate(zip(args, params)):
+            if dyn and p["role"] != "scalar" and -1 in p["shape"] and isinstance(a, torch.Tensor):
+                r = int(a.shape[p["shape"].index(-1)]) if a.dim() == len(p["shape"]) else -1
+                if rows is not None and r != rows:
+                    raise ValueError(f"argument {i} of @{self.func} has {r} rows, an earlier one {rows}")
+                rows = r
+        if dyn and rows is None:
+            raise ValueError(f"@{self.func} takes its row count from a tensor argument")
+
+        def want(shape):
+            return tuple(rows if d == -1 else d for d in shape)
         device = None
         slots = (ctypes.c_uint64 * len(params))()
         for i, (a, p) in enumerate(zip(args, params)):
@@ -228,9 +245,9 @@ class Group:
                 continue
             if not isinstance(a, torch.Tensor) or not a.is_cuda:
                 raise TypeError(f"argument {i} of @{self.func} must be a device tensor")
-            if a.dtype != torch_dtype(p["elem"]) or tuple(a.shape) != p["shape"] or not a.is_contiguous():
-                raise ValueError(f"argument {i} of @{self.func}: expected contiguous {p['elem']}{list(p['shape'])}, "
-                                 f"got {a.dtype}{list(a.shape)}")
+            if a.dtype != torch_dtype(p["elem"]) or tuple(a.shape) != want(p["shape"]) or not a.is_contiguous():
+                raise ValueError(f"argument {i} of @{self.func}: expected contiguous "
+                                 f"{p['elem']}{list(want(p['shape']))}, got {a.dtype}{list(a.shape)}")
             device = a.device if device is None else device
             slots[i] = a.data_ptr()
         res_meta = self.meta["results"]
@@ -241,10 +258,10 @@ class Group:
                 outs.append(args[r["tied"]])
                 rptrs[j] = None
             else:
-                t = results[j] if results is not None else torch.empty(r["shape"], dtype=torch_dtype(r["elem"]),
+                t = results[j] if results is not None else torch.empty(want(r["shape"]), dtype=torch_dtype(r["elem"]),
                                                                       device=device)
-                if tuple(t.shape) != r["shape"] or t.dtype != torch_dtype(r["elem"]) or not t.is_cuda:
-                    raise ValueError(f"result {j} of @{self.func}: expected {r['elem']}{list(r['shape'])}")
+                if tuple(t.shape) != want(r["shape"]) or t.dtype != torch_dtype(r["elem"]) or not t.is_cuda:
+                    raise ValueError(f"result {j} of @{self.func}: expected {r['elem']}{list(want(r['shape']))}")
                 outs.append(t)
                 rptrs[j] = t.data_ptr()
         if stream is None:
@@ -257,6 +274,12 @@ class Group:
 
             def launch():
                 native.check(lib.hfr_group_launch_noalloc(h, slots, n, rptrs, nr, stream))
+                return ret
+        elif dyn:
+            ws = workspace.data_ptr() if workspace is not None else None
+
+            def launch():
+                native.check(lib.hfr_group_launch_rows(h, slots, n, rptrs, nr, rows, ws, stream))
                 return ret
         else:
             ws = workspace.data_ptr() if workspace is not None else None
@@ -394,22 +417,32 @@ def dynamic_dims(ir_text, func=None):
 
 
 class DynamicGroup:
-    """A group whose IR has dynamic (`?`) dims, compiled per set of sizes.
+    """A group whose IR has dynamic (`?`) dims.
 
-    The sizes of the dynamic argument dims are read from the tensors of each
-    call; the group is specialised to them (compiler option
-    `dyn=<func>:<arg>.<dim>=<size>,...`: every type of the function becomes
-    static) and compiled once per size set, content-cached like any group.
-    A serving loop that buckets its sizes compiles each bucket once.  With
-    `require_cached`, a size set that was not prebuilt raises instead of
-    compiling."""
+    Per size set (the default): the sizes of the dynamic argument dims are
+    read from the tensors of each call; the group is specialised to them
+    (compiler option `dyn=<func>:<arg>.<dim>=<size>,...`: every type of the
+    function becomes static) and compiled once per size set, content-cached
+    like any group.  A serving loop that buckets its sizes compiles each
+    bucket once.  With `require_cached`, a size set that was not prebuilt
+    raises instead of compiling.
 
-    def __init__(self, ir_text, func=None, options="", require_cached=False):
+    runtime=True: one kernel for every row count (compiler option
+    `dyn=runtime`), for groups whose dynamic dims are all the row count
+    (dim 0 of the arguments) and whose kernel takes it at launch (row
+    programs, the RMSNorm + quant kernel, streaming elementwise groups of
+    rank 2 and more); the compiler refuses the others."""
+
+    def __init__(self, ir_text, func=None, options="", require_cached=False, runtime=False):
         self.ir_text, self.func, self.options, self.require_cached = ir_text, func, options, require_cached
         self.dims = dynamic_dims(ir_text, func)
         if not self.dims:
             raise ValueError("the group has no dynamic dims; use load()")
         self._groups = {}
+        self._rt = None
+        if runtime:
+            opts = (options + ";" if options else "") + "dyn=runtime"
+            self._rt = compile(ir_text, options=opts, require_cached=require_cached).load(func)
 
     def options_for(self, sizes):
         spec = ",".join(f"{f}:{a}.{d}={int(s)}" for (f, a, d), s in zip(self.dims, sizes))
@@ -419,6 +452,8 @@ class DynamicGroup:
         return tuple(int(args[a].shape[d]) for _, a, d in self.dims)
 
     def specialise(self, sizes):
+        if self._rt is not None:
+            return self._rt
         sizes = tuple(int(s) for s in sizes)
         if sizes not in self._groups:
             art = compile(self.ir_text, options=self.options_for(sizes), require_cached=self.require_cached)
@@ -426,4 +461,6 @@ class DynamicGroup:
         return self._groups[sizes]
 
     def __call__(self, *args, **kw):
+        if self._rt is not None:
+            return self._rt(*args, **kw)
         return self.specialise(self.sizes_of(args))(*args, **kw)

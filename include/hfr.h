@@ -78,6 +78,16 @@ int hfr_group_info_get(hfr_group_t g, hfr_group_info *info);
  * use when the group requires it). */
 int hfr_group_launch(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results, size_t nresults,
                      void *workspace, void *stream);
+/* A group compiled with runtime row counts (compiler option dyn=runtime; its
+ * manifest holds `rows_dyn`, and -1 for the row dim of each shape): the same
+ * launch over `rows` rows (0: no launch).  One compiled kernel serves every
+ * row count, where the reference schedules a dynamic-shape kernel once and
+ * reads the sizes at run time from its memref descriptors
+ * (bishengir/lib/Dialect/HFusion/Transforms/AutoSchedule/AnyPBRSchedule.cpp).
+ * hfr_group_launch refuses such a group; this entry refuses a static group
+ * unless rows is -1. */
+int hfr_group_launch_rows(hfr_group_t g, const uint64_t *params, size_t nparams, void *const *results,
+                          size_t nresults, int64_t rows, void *workspace, void *stream);
 
 /* ---- launch programs (an un-fused function split into fused groups)
  * Replaces the host function the reference's HFusion auto-fusion leaves
@@ -114,7 +124,8 @@ int hfr_program_launch(hfr_program_t p, const uint64_t *params, size_t nparams, 
  *              int64_t sizes[R]; int64_t strides[R]; }
  * (R = the tensor's rank; a scalar argument passes a pointer to its value).
  * The device buffer is aligned + offset elements.  Sizes must equal the
- * group's static shape (otherwise HFR_ERR_INVALID).  Dense row-major views are
+ * group's static shape (otherwise HFR_ERR_INVALID); a group with a runtime
+ * row count takes its rows from the descriptors' row dims, which must agree.  Dense row-major views are
  * used in place; any other strides (row pitches, transposed or broadcast
  * views) go through a dense staging copy on `stream`: gathered before the
  * group's kernels when the group reads the view, scattered back after them

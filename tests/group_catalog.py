@@ -1238,6 +1238,10 @@ def entries():
     e["rmsnorm_quant_dyn"] = g.with_dynamic_rows(g.rmsnorm_quant(7919, 4096), 7919)
     e["softmax_dyn"] = g.with_dynamic_rows(g.safe_softmax(7919, 1000), 7919)
     e["vec_add_dyn"] = g.with_dynamic_rows(g.vec_add(7919), 7919)
+    # one kernel for every row count (compiler option dyn=runtime)
+    e["rmsnorm_quant_dyn_rt"] = e["rmsnorm_quant_dyn"]
+    e["softmax_dyn_rt"] = e["softmax_dyn"]
+    e["eltwise_mix_dyn_rt"] = g.with_dynamic_rows(eltwise_mix(67, 1000), 67)
     e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
     # the same groups through the one-wave-per-row kernel (hf_rmsq.h, the
     # default for the widths it takes), named for it ...
@@ -1301,6 +1305,8 @@ def options(name):
         return "rmsq_kernel=1"
     if name.endswith("_rowprog"):
         return "rmsq_kernel=0"
+    if name.endswith("_rt"):
+        return "dyn=runtime"
     if name.endswith("_exact"):
         return "mx_exact=1"
     return "rmsn_kernel=1" if name.endswith("_rmsn") else ""

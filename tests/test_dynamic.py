@@ -6,7 +6,15 @@ DynamicGroup reads those sizes from each call's tensors and compiles one code
 object per size set.  CPU: the specialised group lowers to exactly the kernel
 of the same group written with static types; missing or disagreeing sizes
 are errors; the oracle runs the dynamic IR directly.  GPU: the dynamic groups
-at several row counts against the oracle (through prebuilt code objects)."""
+at several row counts against the oracle (through prebuilt code objects).
+
+Runtime row counts (option dyn=runtime, catalog names ending in _rt): one
+kernel for every row count, the count passed at launch
+(hfr_group_launch_rows, or read from memref descriptors).  CPU: the
+manifest marks the row dims and the launch rule, the kernel source holds no
+row count, and groups whose kernels cannot take one are refused.  GPU: each
+such group at several row counts, through the same code object, against the
+oracle."""
 import ctypes
 import os
 
@@ -86,7 +94,7 @@ def test_oracle_runs_dynamic_ir():
 
 def _call(name, args, gpu):
     import torch
-    dg = hf.DynamicGroup(cat.get(name), require_cached=True)
+    dg = hf.DynamicGroup(cat.get(name), require_cached=True, runtime=name.endswith("_rt"))
     g = dg.specialise(dg.sizes_of(args))
     devs = [to_dev(a, p["elem"], gpu) for a, p in zip(args, g.meta["params"])]
     out = dg(*devs)
@@ -169,3 +177,134 @@ def test_signed_division_folds_round_toward_minus_or_plus_infinity(div, size, tm
 def test_dyn_entries_that_name_nothing_are_refused(spec, msg, tmp_path):
     hip, err = emit_hip(_half_ir("floordivsi"), spec, tmp_path)
     assert hip is None and msg in err
+
+
+# ------------------------------------------------------------- runtime rows
+RT = ["rmsnorm_quant_dyn_rt", "softmax_dyn_rt", "eltwise_mix_dyn_rt"]
+
+
+@pytest.mark.parametrize("name", RT)
+def test_runtime_rows_manifest(name, tmp_path):
+    art = hf.compile(cat.get(name), options=cat.options(name))
+    b = art.blocks[0]
+    assert "rows_dyn" in b and b["kargs"][-1] == "rows", b
+    for p in b["params"] + b["results"]:
+        assert p["shape"].count(-1) <= 1 and (-1 not in p["shape"] or p["shape"][0] == -1), p
+    assert any(-1 in p["shape"] for p in b["params"])
+    src, err = emit_hip(cat.get(name), cat.options(name), tmp_path)
+    assert src is not None, err
+    from hfusion_mi355x import native  # noqa: F401
+    assert str(1 << 30) not in src and str((1 << 30) - 1) not in src
+    assert "hf_rows" in src
+    if b["rows_dyn"][0] > 0:
+        assert b["grid"][0] == 1  # set at launch from the row count
+
+
+def test_runtime_rows_refusals(tmp_path):
+    # a rank-1 streaming group: its vector chunks would straddle the end
+    _, err = emit_hip(cat.get("vec_add_dyn"), "dyn=runtime", tmp_path / "a")
+    assert "compiled per size" in err, err
+    # a dynamic dim other than dim 0
+    ir = """module {
+  func.func @f(%x: tensor<4x?xf32>, %y: tensor<4x?xf32>) -> tensor<4x?xf32>
+      attributes {hacc.entry, hfusion.fusion_kind = #hfusion.fusion_kind<PURE_ELEMWISE>} {
+    %r = linalg.elemwise_unary {fun = #linalg.unary_fn<exp>} ins(%x : tensor<4x?xf32>) outs(%y : tensor<4x?xf32>) -> tensor<4x?xf32>
+    return %r : tensor<4x?xf32>
+  }
+}
+"""
+    _, err = emit_hip(ir, "dyn=runtime", tmp_path / "b")
+    assert "is not dim 0" in err, err
+    # a size derived from the row count, not the count itself
+    ir2 = """module {
+  func.func @g(%x: tensor<?x8xf32>) -> tensor<?xf32>
+      attributes {hacc.entry, hfusion.fusion_kind = #hfusion.fusion_kind<PURE_ELEMWISE>} {
+    %c = tensor.collapse_shape %x [[0, 1]] : tensor<?x8xf32> into tensor<?xf32>
+    return %c : tensor<?xf32>
+  }
+}
+"""
+    _, err = emit_hip(ir2, "dyn=runtime", tmp_path / "c")
+    assert err and ("derived from the row count" in err or "compiled per size" in err), err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 37, 300, 4100])
+def test_gpu_runtime_rows_rmsnorm_quant(gpu, rows):
+    note(f"rmsnorm_quant_dyn_rt rows={rows}")
+    rng = np.random.default_rng(1000 + rows)
+    x = (rng.standard_normal((rows, 4096)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    g = (rng.uniform(0.5, 1.5, 4096).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    args = [x, g, np.zeros((rows, 4096), np.int8), np.zeros(rows, np.float32)]
+    q, s = _call("rmsnorm_quant_dyn_rt", args, gpu)
+    rq, rs = run_oracle("rmsnorm_quant_dyn", args)
+    assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 5, 129, 1000])
+def test_gpu_runtime_rows_softmax(gpu, rows):
+    note(f"softmax_dyn_rt rows={rows}")
+    x = np.random.default_rng(2000 + rows).normal(0, 2, (rows, 1000)).astype(np.float32)
+    out, = _call("softmax_dyn_rt", [x, np.zeros((rows, 1000), np.uint16)], gpu)
+    ref, = run_oracle("softmax_dyn", [x, np.zeros((rows, 1000), np.uint16)])
+    assert bf16_ulp_diff(out.view(np.uint16), ref).max() <= 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 67, 333])
+def test_gpu_runtime_rows_eltwise(gpu, rows):
+    """Row and column broadcasts through the streaming kernel with a runtime
+    row count (bf16 out within 1 ulp: exp; the i1 mask bit-exact)."""
+    note(f"eltwise_mix_dyn_rt rows={rows}")
+    I = hf.inputs
+    s = I.SEED_BASE + 3000 + rows
+    x, b, sc = I.normal_f32(s, (rows, 1000)), I.normal_f32(s + 1, (1000,)), I.uniform_f32(s + 2, (rows,), 0.5, 2.0)
+    args = [x, b, sc, np.zeros((rows, 1000), np.uint16), np.zeros((rows, 1000), np.bool_)]
+    y, mask = _call("eltwise_mix_dyn_rt", args, gpu)
+    ry, rmask = run_oracle("eltwise_mix_dyn_rt", args)
+    assert np.array_equal(mask.astype(bool), rmask.astype(bool))
+    assert bf16_ulp_diff(y.view(np.uint16), ry).max() <= 1
+
+
+@pytest.mark.gpu
+def test_gpu_runtime_rows_memref_and_errors(gpu):
+    """The memref entry reads the row count from the descriptors; a launch
+    whose arguments disagree on it, hfr_group_launch on a runtime-rows group
+    and a negative count are refused."""
+    import torch
+    from hfusion_mi355x import native
+    note("softmax_dyn_rt memref rows=77")
+    rows = 77
+    art = hf.compile(cat.get("softmax_dyn_rt"), options=cat.options("softmax_dyn_rt"), require_cached=True)
+    grp = art.load()
+    x = np.random.default_rng(7).normal(0, 2, (rows, 1000)).astype(np.float32)
+    xd = torch.from_numpy(x).to(gpu)
+    od = torch.zeros((rows, 1000), dtype=torch.int16, device=gpu)
+
+    class Desc(ctypes.Structure):
+        _fields_ = [("allocated", ctypes.c_void_p), ("aligned", ctypes.c_void_p), ("offset", ctypes.c_int64),
+                    ("sizes", ctypes.c_int64 * 2), ("strides", ctypes.c_int64 * 2)]
+    dx = Desc(xd.data_ptr(), xd.data_ptr(), 0, (rows, 1000), (1000, 1))
+    do = Desc(od.data_ptr(), od.data_ptr(), 0, (rows, 1000), (1000, 1))
+    descs = (ctypes.c_void_p * 2)(ctypes.addressof(dx), ctypes.addressof(do))
+    lib = native.hfr()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    native.check(lib.hfr_group_launch_memref(grp._h, descs, 2, stream))
+    torch.cuda.synchronize()
+    ref, = run_oracle("softmax_dyn", [x, np.zeros((rows, 1000), np.uint16)])
+    assert bf16_ulp_diff(od.cpu().numpy().view(np.uint16), ref).max() <= 1
+    # disagreeing row counts
+    do2 = Desc(od.data_ptr(), od.data_ptr(), 0, (rows - 1, 1000), (1000, 1))
+    descs2 = (ctypes.c_void_p * 2)(ctypes.addressof(dx), ctypes.addressof(do2))
+    assert lib.hfr_group_launch_memref(grp._h, descs2, 2, stream) == -1
+    assert b"rows" in lib.hfr_last_error()
+    slots = (ctypes.c_uint64 * 2)(xd.data_ptr(), od.data_ptr())
+    res = (ctypes.c_void_p * 1)(None)
+    assert lib.hfr_group_launch(grp._h, slots, 2, res, 1, None, stream) != 0
+    assert b"row count at launch" in lib.hfr_last_error()
+    assert lib.hfr_group_launch_rows(grp._h, slots, 2, res, 1, -5, None, stream) != 0
+    # the Python launch refuses arguments that disagree
+    with pytest.raises(ValueError):
+        grp(xd, torch.zeros((rows + 1, 1000), dtype=torch.bfloat16, device=gpu))
+    torch.cuda.synchronize()
