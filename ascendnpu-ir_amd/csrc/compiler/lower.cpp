@@ -2457,7 +2457,9 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
   // The 128-byte ring addresses each lane's source as a 32-bit offset from
   // a per-step base: 256 rows of K bytes, or 128 bytes' worth of k-rows of a
   // [K, N] / [K, M] operand, must stay below 2^32 bytes.
-  const bool offs32 = K * esz <= (int64_t(1) << 24) && M <= (int64_t(1) << 25) && N <= (int64_t(1) << 25);
+  // (a row-major operand's offsets count from its tile's first row, so only
+  // a K-major operand's column count is bounded)
+  const bool offs32 = K * esz <= (int64_t(1) << 24) && (!aT || M <= (int64_t(1) << 25)) && (bT || N <= (int64_t(1) << 25));
   if (mx && !offs32) unsupported(mm, "matmul_mx with K above 2^24 bytes or M, N above 2^25");
   const int dma0 = (K * esz) % 128 == 0 && offs32 ? 3 : (K * esz) % 64 == 0 ? 1 : 0;
   // The same holds for a bf16 / f16 B [K, N] (512-byte k-rows, 16-bit
@@ -2476,6 +2478,10 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
   // products are exact and whose sums are f32 (the fp8 matrix core's 64-k dot
   // product is not: about 2^-11 of the products' magnitude sum)
   const bool mxExact = mx && opt.mxExact;
+  // a runtime row count is M, the rows of a row-major A and of C
+  if (A.rowsDyn && (aT || M != kRuntimeRows || mxExact))
+    unsupported(mm, "a runtime row count other than the rows of A [M, K] (or with mx_exact=1)");
+  const std::string Mx = A.rowsDyn ? std::string("hf_rows") : std::to_string(M) + "ll";
   const uint64_t wsXA = mxExact ? align256((uint64_t)(M * K * 2)) : 0, wsXB = mxExact ? align256((uint64_t)(K * N * 2)) : 0;
   // matmul_mx accumulates onto its `outs`: a tensor.empty (taken as zero) or
   // a constant fill, added after the contraction
@@ -2604,14 +2610,14 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
   const std::string bPtr = preB ? "(const " + et + "*)ws" : "(const " + et + "*)p" + std::to_string(b->argIdx);
   if (mxExact)
     k << "  hf::mmad<" << MK_BF16_CODE << ", " << kname << "_epi, false, false, 4>((const uint16_t*)ws, (const uint16_t*)((char*)ws + "
-      << wsXA << "), (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
+      << wsXA << "), (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << Mx << ", " << N << "ll, " << K << "ll, P);\n}\n";
   else if (mx)
     k << "  hf::mmad_mx<" << mk << ", " << kname << "_epi>((const uint8_t*)p" << a->argIdx << ", (const uint8_t*)p" << b->argIdx
       << ", (const uint8_t*)p" << sa->argIdx << ", (const uint8_t*)p" << sb->argIdx << ", (" << mtype(oe) << "*)"
-      << resultPtr(A, 0) << ", " << M << "ll, " << N << "ll, " << K << "ll, P);\n}\n";
+      << resultPtr(A, 0) << ", " << Mx << ", " << N << "ll, " << K << "ll, P);\n}\n";
   else
     k << "  hf::mmad<" << mk << ", " << kname << "_epi, " << (mT ? "true" : "false") << ", " << (kT ? "true" : "false") << ", "
-      << dma << ">(" << aPtr << ", " << bPtr << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << M << "ll, " << N
+      << dma << ">(" << aPtr << ", " << bPtr << ", (" << mtype(oe) << "*)" << resultPtr(A, 0) << ", " << Mx << ", " << N
       << "ll, " << K << "ll, P);\n}\n";
   // the re-layout kernels: [K, X] -> [X, K], 128 x 128-byte tiles
   auto preKernel = [&](const char *suffix, const Value *src, int64_t X, uint64_t off) {
@@ -2650,6 +2656,13 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
   // 256x256 macro-tiles, one workgroup each (XCD-aware order inside the kernel)
   const int64_t TM = 256, TN = 256;
   p.grid[0] = (unsigned)(((M + TM - 1) / TM) * ((N + TN - 1) / TN));
+  if (A.rowsDyn) {
+    // ceil(M / 256) row tiles of ceil(N / 256) tiles each
+    p.rowsDyn = true;
+    p.rowsA = 1;
+    p.rowsB = TM;
+    p.rowsC = (N + TN - 1) / TN;
+  }
   p.block[0] = (unsigned)threads;
   static const char *mxName[4] = {"e4m3 x e4m3", "e4m3 x e5m2", "e5m2 x e4m3", "e5m2 x e5m2"};
   p.variant = std::string(mxExact ? std::string("exact matmul_mx: ") + mxName[mk - 3] +
@@ -4189,7 +4202,7 @@ std::string emitManifest(const KernelPlan &p, const std::string &hsacoName) {
     << "workspace " << p.workspaceBytes << " " << (p.workspaceZeroInit ? 1 : 0) << "\n"
     << "algo_bytes " << (uint64_t)p.algoBytes << "\n"
     << "algo_ops " << (uint64_t)p.algoOps << "\n";
-  if (p.rowsDyn) s << "rows_dyn " << p.rowsA << " " << p.rowsB << " " << p.rowsCap << "\n";
+  if (p.rowsDyn) s << "rows_dyn " << p.rowsA << " " << p.rowsB << " " << p.rowsC << " " << p.rowsCap << "\n";
   auto shp = [](const std::vector<int64_t> &v) {
     std::string r = std::to_string(v.size());
     for (auto d : v) r += " " + std::to_string(d);

@@ -48,11 +48,11 @@ struct KernelPlan {
   std::vector<PreKernel> pre;
   // runtime row count (compiler option dyn=runtime): the kernel takes the
   // row count R as its last argument (karg "rows"); the launch grid is
-  // min(ceil(R * rowsA / rowsB), rowsCap) blocks (rowsCap 0: no cap), or the
-  // static grid when rowsA is 0.  Shapes hold -1 for the row dim, and
+  // min(ceil(R * rowsA / rowsB) * rowsC, rowsCap) blocks (rowsCap 0: no cap),
+  // or the static grid when rowsA is 0.  Shapes hold -1 for the row dim, and
   // algoBytes is per row.
   bool rowsDyn = false;
-  int64_t rowsA = 0, rowsB = 1, rowsCap = 0;
+  int64_t rowsA = 0, rowsB = 1, rowsC = 1, rowsCap = 0;
 };
 
 struct LowerOptions {

@@ -215,8 +215,8 @@ __device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][JT], typename Ep
     __syncthreads(); // the stage is free
     if (one_pass || wm == h) {
       const int rbase = one_pass ? wm * 128 : 0; // this wave's first staged row
-      // FULL: every tile lies inside C (M and N multiples of the tile, known
-      // when the shapes are compile-time constants), so the operand indices
+      // FULL: every tile lies inside C (M and N multiples of the tile and
+      // compile-time constants), so the operand indices
       // need no clamping and the functor's per-row loads of 4 consecutive
       // rows merge into one vector load
       auto stage_tiles = [&](auto full_c) {
@@ -248,8 +248,11 @@ __device__ __forceinline__ void mm_epilogue_lds(acc_t (&acc)[4][JT], typename Ep
           }
         }
       };
-      if (M % 256 == 0 && N % 256 == 0) stage_tiles(std::true_type{});
-      else stage_tiles(std::false_type{});
+      // (a runtime M keeps one epilogue: both would not fit the registers)
+      if (__builtin_constant_p(M) && __builtin_constant_p(N) && M % 256 == 0 && N % 256 == 0)
+        stage_tiles(std::true_type{});
+      else
+        stage_tiles(std::false_type{});
     }
     __syncthreads();
     const int64_t mrow0 = m0 + (one_pass ? 0 : h * 128);

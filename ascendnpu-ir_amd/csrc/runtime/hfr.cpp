@@ -65,10 +65,10 @@ struct hfr_group {
   uint64_t wsBytes = 0;
   bool wsZero = false;
   uint64_t algoBytes = 0, algoOps = 0;
-  // runtime row count (manifest `rows_dyn a b cap`): grid.x = min(ceil(R * a
-  // / b), cap) (cap 0: none), or the static grid when a is 0
+  // runtime row count (manifest `rows_dyn a b c cap`): grid.x =
+  // min(ceil(R * a / b) * c, cap) (cap 0: none), or the static grid when a is 0
   bool rowsDyn = false;
-  int64_t rowsA = 0, rowsB = 1, rowsCap = 0;
+  int64_t rowsA = 0, rowsB = 1, rowsC = 1, rowsCap = 0;
   std::vector<std::string> paramRoles;
   std::vector<Buf> paramBufs, resultBufs;
   std::vector<int> resultTied;
@@ -151,9 +151,10 @@ int parseBlock(const std::vector<std::string> &lines, hfr_group &g) {
     else if (key == "algo_bytes") is >> g.algoBytes;
     else if (key == "algo_ops") is >> g.algoOps;
     else if (key == "rows_dyn") {
-      is >> g.rowsA >> g.rowsB >> g.rowsCap;
+      is >> g.rowsA >> g.rowsB >> g.rowsC >> g.rowsCap;
       g.rowsDyn = true;
-      if (g.rowsA < 0 || g.rowsB <= 0 || g.rowsCap < 0) return fail(HFR_ERR_MANIFEST, "bad rows_dyn line: " + ln);
+      if (g.rowsA < 0 || g.rowsB <= 0 || g.rowsC <= 0 || g.rowsCap < 0)
+        return fail(HFR_ERR_MANIFEST, "bad rows_dyn line: " + ln);
     }
     else if (key == "param" || key == "result") {
       int i, tied = -1, rank = 0;
@@ -281,7 +282,7 @@ int launchGroup(const hfr_group *g, const uint64_t *params, void *const *results
                 int64_t rows = -1) {
   auto launch = [&](hipFunction_t fn, hfr_launch_cfg cfg, const std::vector<Karg> &kargs) {
     if (g->rowsDyn && g->rowsA > 0) {
-      int64_t blocks = (rows * g->rowsA + g->rowsB - 1) / g->rowsB;
+      int64_t blocks = (rows * g->rowsA + g->rowsB - 1) / g->rowsB * g->rowsC;
       if (g->rowsCap > 0 && blocks > g->rowsCap) blocks = g->rowsCap;
       cfg.grid[0] = (unsigned)(blocks > 0 ? blocks : 1);
     }

@@ -180,7 +180,7 @@ def test_dyn_entries_that_name_nothing_are_refused(spec, msg, tmp_path):
 
 
 # ------------------------------------------------------------- runtime rows
-RT = ["rmsnorm_quant_dyn_rt", "softmax_dyn_rt", "eltwise_mix_dyn_rt"]
+RT = ["rmsnorm_quant_dyn_rt", "softmax_dyn_rt", "eltwise_mix_dyn_rt", "w8a8_dyn_rt"]
 
 
 @pytest.mark.parametrize("name", RT)
@@ -308,3 +308,20 @@ def test_gpu_runtime_rows_memref_and_errors(gpu):
     with pytest.raises(ValueError):
         grp(xd, torch.zeros((rows + 1, 1000), dtype=torch.bfloat16, device=gpu))
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 100, 333, 1000])
+def test_gpu_runtime_rows_w8a8(gpu, rows):
+    """W8A8 with the token count M at launch (B [N, K] weights, K = N = 512):
+    bit-exact bf16 against the oracle for ragged and multiple-of-tile M."""
+    note(f"w8a8_dyn_rt M={rows}")
+    rng = np.random.default_rng(4000 + rows)
+    a = rng.integers(-127, 128, (rows, 512), dtype=np.int8)
+    b = rng.integers(-127, 128, (512, 512), dtype=np.int8)
+    st = rng.uniform(0.001, 0.02, rows).astype(np.float32)
+    sc = rng.uniform(0.001, 0.02, 512).astype(np.float32)
+    args = [a, b, st, sc, np.zeros((rows, 512), np.uint16)]
+    out, = _call("w8a8_dyn_rt", args, gpu)
+    ref, = run_oracle("w8a8_dyn_rt", args)
+    assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
