@@ -46,6 +46,11 @@
  *   mx_exact=1              hfusion.matmul_mx through scaled bf16 operands and
  *                           the bf16 matrix core (exact products, f32 sums)
  *   dyn=<func>:<arg>.<dim>=<size>,...  sizes of dynamic dims
+ *   dyn=runtime             one kernel for every row count (every dynamic dim
+ *                           is dim 0 of the arguments; row programs, RMSNorm +
+ *                           quant, streaming elementwise of rank >= 2,
+ *                           contractions over M): launch with
+ *                           hfr_group_launch_rows
  *
  * Returns 0 on success; a negative code with a message in `err` otherwise
  * (mirrors the reference's "[ERROR] ..." + EXIT_FAILURE convention).
