@@ -2269,20 +2269,56 @@ KernelPlan lowerReduceWithIndex(Analysis &A, const std::string &kname) {
   }
   // schedule: with at least one row per CU, one workgroup per row (no
   // cross-workgroup step); otherwise about two workgroups per CU, each on a
-  // segment of a row (a multiple of 4 elements, so float4 loads stay aligned)
+  // segment of a row (a multiple of 4 elements, so float4 loads stay aligned).
+  // hf::arg_schedule (hf_argmax.h) is the same rule for a runtime row count.
   const int64_t CUS = 256;
-  int64_t segs = R >= CUS ? 1 : std::max<int64_t>(1, (2 * CUS + R - 1) / R);
-  int64_t segLen = ((C + segs - 1) / segs + 3) / 4 * 4;
-  segLen = std::max<int64_t>(segLen, std::min<int64_t>((C + 3) / 4 * 4, 4096)); // no tiny segments
-  segs = (C + segLen - 1) / segLen;
+  auto schedule = [&](int64_t rows, int64_t &segs, int64_t &segLen) {
+    segs = rows >= CUS ? 1 : std::max<int64_t>(1, (2 * CUS + rows - 1) / rows);
+    segLen = ((C + segs - 1) / segs + 3) / 4 * 4;
+    segLen = std::max<int64_t>(segLen, std::min<int64_t>((C + 3) / 4 * 4, 4096)); // no tiny segments
+    segs = (C + segLen - 1) / segLen;
+  };
+  int64_t segs, segLen;
+  schedule(A.rowsDyn ? CUS : R, segs, segLen);
   const int BLOCK = segLen >= 32768 ? 1024 : (segLen >= 8192 ? 512 : 256);
   bool aligned = (C % 4) == 0;
   KernelPlan p;
   p.kernelName = kname;
   p.kind = "REDUCE_WITH_INDEX";
-  p.variant = segs == 1 ? "one workgroup per row, streaming" : "split-row two-level, last-block combine";
   std::ostringstream k;
   std::string IT = ctype(idxE);
+  if (A.rowsDyn) {
+    if (R != kRuntimeRows) unsupported(rw, "a runtime row count that is not the rows of the input");
+    // the largest workspace any row count asks for (from CUS rows on, one
+    // segment per row and no records)
+    uint64_t ws = 256;
+    for (int64_t r = 1; r < CUS; ++r) {
+      int64_t sg, sl;
+      schedule(r, sg, sl);
+      ws = std::max<uint64_t>(ws, (uint64_t)(r * sg * 16 + r * 4 + 256));
+    }
+    p.variant = "runtime rows: split rows below one per CU, a workgroup per row above";
+    k << "extern \"C\" __global__ __launch_bounds__(" << BLOCK << ") void " << kname << "("
+      << kernelParamList(A, p.kargs, true) << ") {\n"
+      << "  constexpr int64_t C = " << C << "ll;\n"
+      << "  auto init = [&](int64_t row, float &v, " << IT << " &i) {\n"
+      << "    v = " << (ivArg.empty() ? iv : "((const float*)" + ivArg + ")[row]") << ";\n"
+      << "    i = " << (iiArg.empty() ? ii : "((const " + IT + "*)" + iiArg + ")[row]") << ";\n  };\n"
+      << "  hf::argreduce_rows_dyn<" << kind << ", " << BLOCK << ", " << (aligned ? "true" : "false") << ", " << IT
+      << ">((const float*)p" << x->argIdx << ", hf_rows, C, " << ws << "ull, init, (float*)" << outV << ", (" << IT << "*)"
+      << outI << ", ws);\n}\n";
+    p.source = k.str();
+    // R * SEG work items (at most ceil(C / min(C, 4096)) segments a row)
+    p.rowsDyn = true;
+    p.rowsA = (C + std::min<int64_t>(C, 4096) - 1) / std::min<int64_t>(C, 4096);
+    p.rowsB = 1;
+    p.rowsCap = 2048;
+    p.block[0] = BLOCK;
+    p.workspaceBytes = ws;
+    p.workspaceZeroInit = true;
+    return p;
+  }
+  p.variant = segs == 1 ? "one workgroup per row, streaming" : "split-row two-level, last-block combine";
   k << "extern \"C\" __global__ __launch_bounds__(" << BLOCK << ") void " << kname << "("
     << kernelParamList(A, p.kargs, true) << ") {\n"
     << "  constexpr int64_t R = " << R << "ll, C = " << C << "ll, SEG = " << segs << "ll, SEGLEN = " << segLen << "ll;\n"

@@ -211,9 +211,12 @@ __device__ __forceinline__ bool arg_segment_fast(const float *__restrict__ row, 
   return true;
 }
 
+// One work item: segment `item % SEG` of row `item / SEG` (SEG segments of
+// SEGLEN elements per row); with SEG > 1 the last of a row's segments to
+// arrive folds the row's records.
 template <int KIND, int BLOCK, bool ALIGNED, typename IdxT>
-__device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C, int64_t SEG, int64_t SEGLEN, float init_v,
-                               IdxT init_i, float *__restrict__ out_v, IdxT *__restrict__ out_i, void *ws) {
+__device__ void arg_item(const float *__restrict__ x, int64_t R, int64_t C, int64_t SEG, int64_t SEGLEN, int64_t item,
+                         float init_v, IdxT init_i, float *__restrict__ out_v, IdxT *__restrict__ out_i, void *ws) {
   __shared__ float sv[BLOCK / 64];
   __shared__ int64_t si[BLOCK / 64];
   __shared__ int64_t snan[BLOCK / 64];
@@ -222,7 +225,7 @@ __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C
   __shared__ int last;
   ArgRec *recs = reinterpret_cast<ArgRec *>(ws);
   unsigned *counters = reinterpret_cast<unsigned *>(recs + R * SEG);
-  const int64_t row = blockIdx.x / SEG, seg = blockIdx.x % SEG;
+  const int64_t row = item / SEG, seg = item % SEG;
   const float *rp = x + row * C;
   const int64_t s0 = seg * SEGLEN, s1 = (s0 + SEGLEN < C) ? s0 + SEGLEN : C;
   float v;
@@ -268,7 +271,7 @@ __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C
     r.m = v;
     r.has_nan = has_nan;
     r.j = i;
-    rec_store(&recs[blockIdx.x], r);
+    rec_store(&recs[item], r);
     // release: the record happens-before the count that the last arriver
     // reads; acquire: the last arriver's reads of the other records follow it
     unsigned prev = __hip_atomic_fetch_add(&counters[row], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
@@ -307,6 +310,47 @@ __device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C
   if (out_v) out_v[row] = V;
   if (out_i) out_i[row] = (IdxT)I;
   __hip_atomic_store(&counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int KIND, int BLOCK, bool ALIGNED, typename IdxT>
+__device__ void argreduce_rows(const float *__restrict__ x, int64_t R, int64_t C, int64_t SEG, int64_t SEGLEN, float init_v,
+                               IdxT init_i, float *__restrict__ out_v, IdxT *__restrict__ out_i, void *ws) {
+  arg_item<KIND, BLOCK, ALIGNED, IdxT>(x, R, C, SEG, SEGLEN, blockIdx.x, init_v, init_i, out_v, out_i, ws);
+}
+
+// The split of a row into segments for R rows of C elements: about two
+// workgroups per CU when there are fewer rows than CUs, segments a multiple
+// of 4 elements (aligned float4 loads) and at least min(C, 4096) long.  The
+// compiler uses the same rule for a static R (lower.cpp, REDUCE_WITH_INDEX).
+__device__ __forceinline__ void arg_schedule(int64_t R, int64_t C, int64_t &segs, int64_t &segLen) {
+  constexpr int64_t CUS = 256;
+  segs = R >= CUS ? 1 : ((2 * CUS + R - 1) / R > 1 ? (2 * CUS + R - 1) / R : 1);
+  segLen = ((C + segs - 1) / segs + 3) / 4 * 4;
+  const int64_t minLen = (C + 3) / 4 * 4 < 4096 ? (C + 3) / 4 * 4 : 4096;
+  segLen = segLen > minLen ? segLen : minLen;
+  segs = (C + segLen - 1) / segLen;
+}
+
+// A runtime row count R: the segments follow arg_schedule (one segment per
+// row when the workspace of WS bytes could not hold the records), and the
+// grid walks the R * SEG work items.  init(row) gives the row's init value
+// and index.
+template <int KIND, int BLOCK, bool ALIGNED, typename IdxT, typename Init>
+__device__ void argreduce_rows_dyn(const float *__restrict__ x, int64_t R, int64_t C, uint64_t WS, Init init,
+                                   float *__restrict__ out_v, IdxT *__restrict__ out_i, void *ws) {
+  int64_t SEG, SEGLEN;
+  arg_schedule(R, C, SEG, SEGLEN);
+  if ((uint64_t)(R * SEG * 16 + R * 4 + 256) > WS) {
+    SEG = 1;
+    SEGLEN = (C + 3) / 4 * 4;
+  }
+  for (int64_t item = blockIdx.x; item < R * SEG; item += gridDim.x) {
+    float init_v;
+    IdxT init_i;
+    init(item / SEG, init_v, init_i);
+    arg_item<KIND, BLOCK, ALIGNED, IdxT>(x, R, C, SEG, SEGLEN, item, init_v, init_i, out_v, out_i, ws);
+    __syncthreads(); // the item's shared scratch is free
+  }
 }
 
 } // namespace hf

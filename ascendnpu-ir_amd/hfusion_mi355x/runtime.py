@@ -431,8 +431,8 @@ class DynamicGroup:
     `dyn=runtime`), for groups whose dynamic dims are all the row count
     (dim 0 of the arguments) and whose kernel takes it at launch (row
     programs, the RMSNorm + quant kernel, streaming elementwise groups of
-    rank 2 and more, contractions whose M is the row count); the compiler
-    refuses the others."""
+    rank 2 and more, contractions whose M is the row count, reduce_with_index
+    over rows); the compiler refuses the others."""
 
     def __init__(self, ir_text, func=None, options="", require_cached=False, runtime=False):
         self.ir_text, self.func, self.options, self.require_cached = ir_text, func, options, require_cached

@@ -49,7 +49,8 @@
  *   dyn=runtime             one kernel for every row count (every dynamic dim
  *                           is dim 0 of the arguments; row programs, RMSNorm +
  *                           quant, streaming elementwise of rank >= 2,
- *                           contractions over M): launch with
+ *                           contractions over M, reduce_with_index over
+ *                           rows): launch with
  *                           hfr_group_launch_rows
  *
  * Returns 0 on success; a negative code with a message in `err` otherwise

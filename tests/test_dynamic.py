@@ -180,7 +180,7 @@ def test_dyn_entries_that_name_nothing_are_refused(spec, msg, tmp_path):
 
 
 # ------------------------------------------------------------- runtime rows
-RT = ["rmsnorm_quant_dyn_rt", "softmax_dyn_rt", "eltwise_mix_dyn_rt", "w8a8_dyn_rt"]
+RT = ["rmsnorm_quant_dyn_rt", "softmax_dyn_rt", "eltwise_mix_dyn_rt", "w8a8_dyn_rt", "argmax_dyn_rt"]
 
 
 @pytest.mark.parametrize("name", RT)
@@ -325,3 +325,22 @@ def test_gpu_runtime_rows_w8a8(gpu, rows):
     out, = _call("w8a8_dyn_rt", args, gpu)
     ref, = run_oracle("w8a8_dyn_rt", args)
     assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 7, 255, 256, 600])
+def test_gpu_runtime_rows_argmax(gpu, rows):
+    """argmax over [rows, 50000] logits with the row count at launch: split
+    rows below one row per CU, a workgroup per row from 256 rows on; values
+    and first-index ties bit-exact (a NaN row and an all -inf row included)."""
+    note(f"argmax_dyn_rt rows={rows}")
+    x = hf.inputs.argmax_logits(hf.inputs.SEED_BASE + 5000 + rows, rows, 50000, dup_every=3)
+    if rows >= 7:
+        x[5, 1234] = np.nan
+        x[6, :] = -np.inf
+    args = [x, np.zeros(rows, np.float32), np.zeros(rows, np.int32)]
+    v, i = _call("argmax_dyn_rt", args, gpu)
+    rv, ri = run_oracle("argmax_dyn_rt", args)
+    assert np.array_equal(v.view(np.uint32), rv.view(np.uint32)) or \
+        (np.array_equal(np.isnan(v), np.isnan(rv)) and np.array_equal(v[~np.isnan(v)], rv[~np.isnan(rv)]))
+    assert np.array_equal(i, ri)
