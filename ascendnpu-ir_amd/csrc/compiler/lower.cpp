@@ -3912,7 +3912,7 @@ bool matchRmsQuant(const Analysis &A, RmsqMatch &m) {
   const Func &f = *A.f;
   if (A.D.size() != 2 || f.returns.size() != 2) return false;
   const int64_t C = A.D[1];
-  if (C % 1024 != 0 || C > 4096) return false;
+  if (C != 1024 && C != 2048 && C != 4096) return false;
   for (size_t i = 0; i < 2; ++i) {
     if (f.returns[i]->type.elem == Elem::I8) m.qRes = i;
     else m.sRes = i;

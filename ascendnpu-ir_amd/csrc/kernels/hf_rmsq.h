@@ -51,10 +51,16 @@ typedef unsigned rq_u4 __attribute__((ext_vector_type(4)));
 struct BandFn {
   int32_t d0, d1;
 };
+__device__ __forceinline__ int32_t band_pick(int32_t d, int32_t odd, int32_t even) {
+  // odd if d is odd, else even: a bit-field insert under the mask -(d & 1)
+  int32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(__builtin_amdgcn_sbfe(d, 0, 1)), "v"(odd), "v"(even));
+  return r;
+}
 __device__ __forceinline__ BandFn band_compose(BandFn f, BandFn g) {
   BandFn h;
-  h.d0 = f.d0 + ((f.d0 & 1) ? g.d1 : g.d0);
-  h.d1 = f.d1 + ((f.d1 & 1) ? g.d0 : g.d1);
+  h.d0 = f.d0 + band_pick(f.d0, g.d1, g.d0);
+  h.d1 = f.d1 + band_pick(f.d1, g.d0, g.d1);
   return h;
 }
 
@@ -96,8 +102,11 @@ __device__ __forceinline__ BandFn wave_seg_compose(BandFn g, int start, int lane
   const int l16 = lane & 15, row0 = lane & ~15;
 #define HF_SEG_STEP(CTRL, MASK, COND)                                                                 \
   {                                                                                                   \
-    const BandFn pv = {dpp<CTRL, MASK>(0, g.d0), dpp<CTRL, MASK>(0, g.d1)};                           \
-    if (COND) g = band_compose(pv, g);                                                                \
+    const BandFn pv = {dpp<CTRL, MASK>(g.d0, g.d0), dpp<CTRL, MASK>(g.d1, g.d1)};                     \
+    const BandFn cg = band_compose(pv, g);                                                            \
+    const bool c_ = (COND);                                                                           \
+    g.d0 = c_ ? cg.d0 : g.d0;                                                                         \
+    g.d1 = c_ ? cg.d1 : g.d1;                                                                         \
   }
   HF_SEG_STEP(DPP_ROW_SHR1, 0xf, l16 >= 1 && lane - 1 >= start)
   HF_SEG_STEP(DPP_ROW_SHR2, 0xf, l16 >= 2 && lane - 2 >= start)
@@ -173,11 +182,10 @@ template <int C, int LO, int HI, int WPB>
 __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gamma,
                                           int8_t *__restrict__ q, float *__restrict__ scale, int64_t R, float s0,
                                           float K, float eps, float a0, float qd, float *dbg = nullptr) {
-  static_assert(C % 1024 == 0 && C <= 4096, "rows of 1024..4096 elements, multiple of 1024");
+  static_assert(C == 1024 || C == 2048 || C == 4096, "rows of 1024, 2048 or 4096 elements");
   constexpr int SEG = C / 64;      // elements per lane
   constexpr int NG = SEG / 8;      // 16-byte granules per lane
   constexpr int NS = SEG / 16;     // sub-segments per lane
-  constexpr int SWD = 16 / NG;     // lanes per swizzle group
   __shared__ rq_u4 lds_all[WPB][C / 8];
   const int lane0 = threadIdx.x & 63;
   rq_u4 *lds = lds_all[threadIdx.x / 64];
@@ -194,34 +202,42 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
                                          __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
   }
   __syncthreads();
-  // row DMA straight into this wave's LDS row buffer, in the swizzled order:
-  // instruction k, lane l fills slot 64k + l (lane j's granule g sits at slot
-  // NG*j + (g ^ sw(j))); eight consecutive lanes read one 128-byte line
-  const uint32_t ldsBase = (uint32_t)(uintptr_t)lds;
-  auto issueRow = [&](int64_t r, int lane) {
+  // row DMA straight into this wave's LDS row buffer.  Granule G (16 bytes,
+  // columns 8G .. 8G+7) of the row sits at slot G ^ ((G >> 4) & 7): a
+  // permutation inside every 128-byte line, so DMA instruction k, lane l
+  // fills slot 64k + l from one line per eight lanes (coalesced), and lane j's
+  // granule g (G = NG*j + g) is read with the 64 lanes spread over the banks.
+  // Slot 64k + l holds G = 64k + 8(l/8) + ((l % 8) ^ ((4k + l/16) & 7)); its
+  // byte offset is 1024k + off[k & 1] with off[1] = off[0] ^ 64.
+  const uint32_t ldsBase = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  const uint32_t dmaOff0 = 128u * (lane0 / 8) + 16u * ((lane0 % 8) ^ (lane0 / 16)), dmaOff1 = dmaOff0 ^ 64u;
+  const rq_u4 *rdPtr[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const uint32_t G = NG * lane0 + g;
+    rdPtr[g] = lds + (G ^ ((G >> 4) & 7u));
+  }
+  auto issueRow = [&](int64_t r) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); // this wave's reads of the buffer are done
+    const uint16_t *rowp = x + r * C;                   // wave-uniform
 #pragma unroll
     for (int k = 0; k < NG; ++k) {
-      const int slot = 64 * k + lane, j = slot / NG, g = (slot % NG) ^ ((j / SWD) & (NG - 1));
-      const uint16_t *src = x + r * C + 8 * (NG * j + g);
-      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
-                   "s"(__builtin_amdgcn_readfirstlane(ldsBase + 1024u * k))
+      asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"((k & 1) ? dmaOff1 : dmaOff0),
+                   "s"(rowp + 512 * k), "s"(ldsBase + 1024u * k)
                    : "memory");
     }
   };
-  if (row < R) issueRow(row, lane0);
+  row = (int64_t)__builtin_amdgcn_readfirstlane((int)row); // wave-uniform
+  if (row < R) issueRow(row);
   for (; row < R; row += W) {
-    // per-lane index arithmetic is recomputed each row rather than held in
-    // registers across the loop
-    int lane = lane0;
-    asm volatile("" : "+v"(lane));
+    const int lane = lane0;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the row's DMA has landed
     __builtin_amdgcn_wave_barrier();
     rq_u4 seg[NG];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) seg[g] = lds[NG * lane + (g ^ ((lane / SWD) & (NG - 1)))];
+    for (int g = 0; g < NG; ++g) seg[g] = *rdPtr[g];
     // prefetch the next row into the buffer once these reads are done
-    if (row + W < R) issueRow(row + W, lane);
+    if (row + W < R) issueRow(row + W);
 
     // ---- 2. approximate prefix: sub-segment sums and a wave scan
     float xf[SEG];
@@ -401,9 +417,11 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
     const float r = 1.0f / sc;
     Guard gd;
     gd.divisor(r);
-    rq_u4 *qrow = reinterpret_cast<rq_u4 *>(q + row * C) + NG / 2 * lane;
+    // codes as words: cw[c][d] = word d of lane's 16-byte chunk c
+    constexpr int NCH = SEG / 16;
+    uint32_t cw[NCH][4];
 #pragma unroll
-    for (int i = 0; i < SEG / 16; ++i) {
+    for (int c = 0; c < NCH; ++c) {
       // 16 codes: the bracketing pair of packed words, one test for the chunk
       constexpr float D = 0x1p-15f;
       uint32_t wl[4], wh[4];
@@ -413,7 +431,7 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
         wh[w] = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float a = xf[16 * i + 4 * w + e];
+          const float a = xf[16 * c + 4 * w + e];
           wl[w] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(a, r, 128.0f - D), e, wl[w]);
           wh[w] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(a, r, 128.0f + D), e, wh[w]);
         }
@@ -421,19 +439,67 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
       if (__builtin_expect(((wl[0] ^ wh[0]) | (wl[1] ^ wh[1]) | (wl[2] ^ wh[2]) | (wl[3] ^ wh[3])) != 0, 0)) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const float a4[4] = {xf[16 * i + 4 * w], xf[16 * i + 4 * w + 1], xf[16 * i + 4 * w + 2], xf[16 * i + 4 * w + 3]};
+          const float a4[4] = {xf[16 * c + 4 * w], xf[16 * c + 4 * w + 1], xf[16 * c + 4 * w + 2], xf[16 * c + 4 * w + 3]};
           wl[w] = quant8x4_inner(a4, sc, r, gd) ^ 0x80808080u;
         }
       }
-      qrow[i] = rq_u4{wl[0] ^ 0x80808080u, wl[1] ^ 0x80808080u, wl[2] ^ 0x80808080u, wl[3] ^ 0x80808080u};
-      __builtin_amdgcn_sched_barrier(0); // bound the live range to one 16-byte store
+#pragma unroll
+      for (int w = 0; w < 4; ++w) cw[c][w] = wl[w] ^ 0x80808080u;
     }
     if (__ballot(gd.bad()) != 0 || !(amax <= 0x1.fffffep+127f)) {
       // rare: an unsafe magnitude or a NaN quotient -- IEEE division
-      int8_t *qe = q + row * C + SEG * lane;
 #pragma unroll
-      for (int k = 0; k < SEG; ++k)
-        qe[k] = (int8_t)(int32_t)maximumf(minimumf(__builtin_roundevenf(xf[k] / sc), (float)HI), (float)LO);
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t v = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float qf = maximumf(minimumf(__builtin_roundevenf(xf[16 * c + 4 * w + e] / sc), (float)HI), (float)LO);
+            v |= ((uint32_t)(int32_t)qf & 0xFFu) << (8 * e);
+          }
+          cw[c][w] = v;
+        }
+    }
+    // The row's codes leave in NCH stores of 1024 contiguous bytes each (whole
+    // 128-byte lines per instruction), non-temporal, so that no dirty lines
+    // of them are left in the L2 for the end-of-kernel write-back to wait
+    // on.  Lane L's chunk c holds row bytes 16 (NCH L + c) .. +15; a transpose
+    // of the chunk index with the lane's 16-lane row (NCH = 4: permlane32 and
+    // permlane16 swaps) or 32-lane half (NCH = 2) gives store i, lane (h, m)
+    // the chunk h of lane (i, m).
+    int8_t *qr = q + row * C;
+    if constexpr (NCH == 4) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        auto r02 = __builtin_amdgcn_permlane32_swap(cw[0][d], cw[2][d], false, false);
+        auto r13 = __builtin_amdgcn_permlane32_swap(cw[1][d], cw[3][d], false, false);
+        auto r01 = __builtin_amdgcn_permlane16_swap(r02[0], r13[0], false, false);
+        auto r23 = __builtin_amdgcn_permlane16_swap(r02[1], r13[1], false, false);
+        cw[0][d] = r01[0];
+        cw[1][d] = r01[1];
+        cw[2][d] = r23[0];
+        cw[3][d] = r23[1];
+      }
+      // lane 16h + m, store i: bytes 1024 i + 64 m + 16 h (chunk h of lane 16 i + m)
+      rq_u4 *dst = reinterpret_cast<rq_u4 *>(qr + 64 * (lane & 15) + 16 * (lane >> 4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __builtin_nontemporal_store(rq_u4{cw[i][0], cw[i][1], cw[i][2], cw[i][3]}, dst + 64 * i);
+    } else if constexpr (NCH == 2) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        auto r01 = __builtin_amdgcn_permlane32_swap(cw[0][d], cw[1][d], false, false);
+        cw[0][d] = r01[0];
+        cw[1][d] = r01[1];
+      }
+      // lane 32h + m, store i: bytes 1024 i + 32 m + 16 h (chunk h of lane 32 i + m)
+      rq_u4 *dst = reinterpret_cast<rq_u4 *>(qr + 32 * (lane & 31) + 16 * (lane >> 5));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        __builtin_nontemporal_store(rq_u4{cw[i][0], cw[i][1], cw[i][2], cw[i][3]}, dst + 64 * i);
+    } else {
+      __builtin_nontemporal_store(rq_u4{cw[0][0], cw[0][1], cw[0][2], cw[0][3]}, reinterpret_cast<rq_u4 *>(qr) + lane);
     }
   }
 }

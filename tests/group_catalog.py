@@ -1158,6 +1158,8 @@ def entries():
     e["vec_add_ragged"] = g.vec_add(1001)
     e["vec_add_i16"] = g.vec_add(16, dtype="i16")
     e["rmsnorm_quant_ragged"] = g.rmsnorm_quant(13, 1000)
+    e["rmsnorm_quant_w2048"] = g.rmsnorm_quant(96, 2048)
+    e["rmsnorm_quant_w3072"] = g.rmsnorm_quant(64, 3072)
     e["safe_softmax_64"] = g.safe_softmax(64, 32768)
     e["safe_softmax_ragged"] = g.safe_softmax(33, 1000)
     e["argmax_16"] = g.argmax(16, 152064)

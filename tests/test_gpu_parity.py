@@ -53,7 +53,8 @@ def test_vec_add(gpu, name, n):
 
 
 # ------------------------------------------------------------------ rmsnorm + quant
-@pytest.mark.parametrize("name,rows,cols", [("rmsnorm_quant_256", 256, 4096), ("rmsnorm_quant_ragged", 13, 1000)])
+@pytest.mark.parametrize("name,rows,cols", [("rmsnorm_quant_256", 256, 4096), ("rmsnorm_quant_ragged", 13, 1000),
+                                            ("rmsnorm_quant_w2048", 96, 2048), ("rmsnorm_quant_w3072", 64, 3072)])
 def test_rmsnorm_quant(gpu, name, rows, cols):
     note(name)
     x, gamma = I.config_inputs("rmsnorm_quant", rows=rows, cols=cols)

@@ -1,5 +1,5 @@
 """The RMSNorm + dynamic int8 quantisation kernel (hf_rmsq.h, the default for
-rows of 1024..4096 columns in multiples of 1024; option rmsq_kernel=0 selects
+rows of 1024, 2048 or 4096 columns; option rmsq_kernel=0 selects
 the generic row program, catalog names ending in _rowprog): its exact
 serial fp32 sum of squares (binade runs composed across lanes, stitched from
 the init) on rows built to stress every path of the stitch, bit-exact against
@@ -92,9 +92,11 @@ def test_rmsq_kernel_selection():
         assert v.startswith("row-resident, serial-order"), name
         v = hf.compile(cat.get(name), options="rmsn_kernel=1").blocks[0]["variant"]
         assert "serial-order" in v and "chain wave" in v, name
-    # a width the kernel does not take keeps the generic row program
-    v = hf.compile(cat.get("rmsnorm_quant_ragged")).blocks[0]["variant"]
-    assert "serial-order" in v
+    # widths the kernel does not take keep the generic row program
+    for name in ("rmsnorm_quant_ragged", "rmsnorm_quant_w3072"):
+        v = hf.compile(cat.get(name)).blocks[0]["variant"]
+        assert "serial-order" in v, name
+    assert "binade-run" in hf.compile(cat.get("rmsnorm_quant_w2048")).blocks[0]["variant"]
 
 
 SHAPES = {"rmsnorm_quant_rowprog": (8192, 4096), "rmsnorm_quant_rank3_rowprog": (4, 64, 1024),
