@@ -3976,7 +3976,10 @@ bool matchRmsQuant(const Analysis &A, RmsqMatch &m) {
 
 KernelPlan lowerRmsQuant(Analysis &A, const RmsqMatch &m, const std::string &kname) {
   const int64_t R = A.D[0], C = A.D[1];
-  constexpr int WPB = 4;
+  // one workgroup per CU: 12 waves, three per SIMD (the occupancy the
+  // register budget allows); 12 row buffers and gamma fill 112 KB of LDS at
+  // 4096 columns
+  constexpr int WPB = 12;
   KernelPlan p;
   p.kernelName = kname;
   p.kind = "LAST_AXIS_PBR";
@@ -3992,10 +3995,7 @@ KernelPlan lowerRmsQuant(Analysis &A, const RmsqMatch &m, const std::string &kna
   p.source = k.str();
   // a runtime row count keeps the full grid: waves past the last row exit
   if (A.rowsDyn) p.rowsDyn = true;
-  // three waves per SIMD (the occupancy the register budget allows), each
-  // walking rows
-  const int64_t waves = std::min<int64_t>(R, 3072);
-  p.grid[0] = (unsigned)((waves + WPB - 1) / WPB);
+  p.grid[0] = (unsigned)(A.rowsDyn ? 256 : std::min<int64_t>(R, 256));
   p.block[0] = WPB * 64;
   return p;
 }

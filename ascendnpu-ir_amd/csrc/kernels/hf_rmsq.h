@@ -178,6 +178,12 @@ __device__ __forceinline__ uint32_t quant8x4_inner(const float (&a)[4], float b,
   return w;
 }
 
+// a wave-uniform value the compiler cannot prove uniform, moved to SGPRs
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 template <int C, int LO, int HI, int WPB>
 __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const uint16_t *__restrict__ gamma,
                                           int8_t *__restrict__ q, float *__restrict__ scale, int64_t R, float s0,
@@ -189,9 +195,20 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
   __shared__ rq_u4 lds_all[WPB][C / 8];
   const int lane0 = threadIdx.x & 63;
   rq_u4 *lds = lds_all[threadIdx.x / 64];
+  // rows in rounds of W = grid * WPB: in a full round, wave w of workgroup b
+  // takes row b WPB + w of it; the last, partial round of Rl rows is split
+  // as evenly: workgroup b takes PL = ceil(Rl / grid) of its rows, on its
+  // first PL waves (with one workgroup per CU, every SIMD gets the same
+  // number of rows to within one, and the rows in flight stay together)
   const int64_t W = (int64_t)gridDim.x * WPB;
-  int64_t row = (int64_t)blockIdx.x * WPB + threadIdx.x / 64;
-
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / 64)); // wave-uniform
+  const int64_t lastBase = (R / W) * W, PL = (R - lastBase + gridDim.x - 1) / gridDim.x;
+  auto rowOf = [&](int64_t base) -> int64_t {
+    if (base < lastBase) return base + (int64_t)blockIdx.x * WPB + wv;
+    return wv < PL ? base + (int64_t)blockIdx.x * PL + wv : R;
+  };
+  int64_t base = 0;
+  int64_t row = rowOf(0);
   // gamma as f32 in LDS for the workgroup (lane j's 4-float groups at
   // stride 64 so that the reads are free of bank conflicts), read where used
   __shared__ float4 lds_gamma[C / 4];
@@ -219,7 +236,7 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
   }
   auto issueRow = [&](int64_t r) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); // this wave's reads of the buffer are done
-    const uint16_t *rowp = x + r * C;                   // wave-uniform
+    const uint16_t *rowp = x + uniform_i64(r) * C;
 #pragma unroll
     for (int k = 0; k < NG; ++k) {
       asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"((k & 1) ? dmaOff1 : dmaOff0),
@@ -227,9 +244,12 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
                    : "memory");
     }
   };
-  row = (int64_t)__builtin_amdgcn_readfirstlane((int)row); // wave-uniform
+  // staggered start: the k-th wave on each SIMD (k = w / 4) issues its first
+  // row 2048 k cycles later, so that the first waves' rows arrive without
+  // the whole grid's first rows competing with them and work starts sooner
+  for (int t = 0; t < wv / 4; ++t) __builtin_amdgcn_s_sleep(32);
   if (row < R) issueRow(row);
-  for (; row < R; row += W) {
+  for (; row < R; base += W, row = rowOf(base)) {
     const int lane = lane0;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the row's DMA has landed
     __builtin_amdgcn_wave_barrier();
@@ -237,7 +257,8 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
 #pragma unroll
     for (int g = 0; g < NG; ++g) seg[g] = *rdPtr[g];
     // prefetch the next row into the buffer once these reads are done
-    if (row + W < R) issueRow(row + W);
+    const int64_t next = rowOf(base + W);
+    if (next < R) issueRow(next);
 
     // ---- 2. approximate prefix: sub-segment sums and a wave scan
     float xf[SEG];
