@@ -244,10 +244,15 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
                    : "memory");
     }
   };
-  // staggered start: the k-th wave on each SIMD (k = w / 4) issues its first
-  // row 2048 k cycles later, so that the first waves' rows arrive without
-  // the whole grid's first rows competing with them and work starts sooner
-  for (int t = 0; t < wv / 4; ++t) __builtin_amdgcn_s_sleep(32);
+  // staggered start: the second wave on each SIMD (w / 4 = 1) issues its
+  // first row C/2 cycles late and the third (which has one row fewer) 2C
+  // cycles late, so that the first waves' rows arrive without the whole
+  // grid's first rows competing with them and work starts sooner
+  if (wv / 4 == 1) __builtin_amdgcn_s_sleep(C / 128); // 64 cycles a unit
+  if (wv / 4 == 2) {
+    __builtin_amdgcn_s_sleep(C / 64);
+    __builtin_amdgcn_s_sleep(C / 64);
+  }
   if (row < R) issueRow(row);
   for (; row < R; base += W, row = rowOf(base)) {
     const int lane = lane0;
@@ -434,7 +439,7 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
       asm volatile("v_maximum3_f32 %0, %0, |%1|, |%2|" : "+v"(m) : "v"(xf[k]), "v"(xf[k + 1]));
     const float amax = maximumf(wave_max(m), a0);
     const float sc = amax / qd;
-    if (lane == 0) scale[row] = sc;
+    if (lane == 0) __builtin_nontemporal_store(sc, &scale[row]);
     const float r = 1.0f / sc;
     Guard gd;
     gd.divisor(r);
