@@ -17,7 +17,7 @@
 // values; runs compose (f then g: D[b] = Df[b] + Dg[b ^ (Df[b] & 1)]).  The
 // kernel:
 //   1. each lane owns C/64 consecutive elements of the row (the row lands in
-//      LDS by DMA, prefetched one row ahead, in an XOR-swizzled order that
+//      LDS by DMA, prefetched one row ahead, in a line-swizzled order that
 //      keeps the DMA reads coalesced and the segment reads free of bank
 //      conflicts), split into sub-segments of 16;
 //   2. an approximate prefix (fp32 partial sums and a wave scan) predicts the
@@ -27,19 +27,22 @@
 //      and 2^p + u (n = 1), give D[0] and D[1]: fmaf(x, x, c) = RN(x^2 + c)
 //      because x^2 is exact (for |x| < 2^-63 the square is below half an ulp
 //      of c >= 2^-60 either way);
-//   4. sub-segment maps compose inside the lane, then across lanes with a
-//      segmented scan over runs of lanes in one binade;
-//   5. a wave-uniform stitch walks the runs from s0: a run applies when the
+//   4. runs (maximal sequences of clean sub-segments of one binade, in row
+//      order) compose inside the lane, then across lanes with a segmented
+//      scan over runs of whole lanes; a lane keeps an event per run that
+//      ends in it and per dirty sub-segment;
+//   5. a wave-uniform stitch walks the events from s0: a run applies when the
 //      exact running sum lies in its binade and the result stays below
 //      2^(p+1) (the addends are >= 0, so every intermediate value is inside);
-//      otherwise the lane's own map, then each sub-segment's, and for a dirty
-//      sub-segment the 16 serial steps themselves.
+//      a dirty sub-segment takes its 16 serial steps; if a run does not
+//      apply (a mispredicted binade), the row is walked again sub-segment by
+//      sub-segment.
 //   The result is the bit pattern of the serial sum for every input,
 //   including NaN and infinity (which always take the serial steps).
 // Quantisation: y stays in registers; the row maximum is a wave reduction;
-// the int8 codes go through hf::quant8x4 (bracketed fast path, exact
-// recomputation of near-tie words) and a row whose Guard reports an unsafe
-// magnitude is recomputed with IEEE division.
+// the int8 codes go through a bracketed fast path (exact recomputation of
+// near-tie words), a row whose Guard reports an unsafe magnitude is
+// recomputed with IEEE division, and the codes leave as whole lines.
 #pragma once
 #include "hf_ops.h"
 
@@ -313,68 +316,57 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
       w0[t] = d0 | base | (clean ? 0x80000000u : 0u); // band_pack(p, d0, clean)
       w1[t] = d1;
     }
-    // ---- 4. lane structure: head items (the key of item 0), middle items,
-    //         tail items (the key of the last item); runs of one key joined
-    //         across lanes by a segmented scan
-    int h = 1, sft = NS - 1;
+    // ---- 4. runs: maximal sequences of clean items of one binade, in row
+    //         order.  Q[t] composes the run that ends at item t from its start
+    //         in this lane; a segmented scan over the lanes composes the runs
+    //         that pass through whole lanes.
+    BandFn Q[NS];
+    Q[0] = {(int32_t)(w0[0] & 0x7fffffu), (int32_t)w1[0]};
+#pragma unroll
+    for (int t = 1; t < NS; ++t) {
+      const BandFn f = {(int32_t)(w0[t] & 0x7fffffu), (int32_t)w1[t]};
+      const BandFn c = band_compose(Q[t - 1], f);
+      const bool join = kt[t] == kt[t - 1]; // dirty keys are unique: never joined
+      Q[t].d0 = join ? c.d0 : f.d0;
+      Q[t].d1 = join ? c.d1 : f.d1;
+    }
+    // h: the leading items that share item 0's key
+    int h = 1;
 #pragma unroll
     for (int t = 1; t < NS; ++t) h += (h == t && kt[t] == kt[0]) ? 1 : 0;
-#pragma unroll
-    for (int t = NS - 2; t >= 0; --t) sft -= (sft == t + 1 && kt[t] == kt[NS - 1]) ? 1 : 0;
     const bool whole = h == NS && kt[0] > -1000;
-    if (kt[0] <= -1000) h = 0;
-    if (kt[NS - 1] <= -1000) sft = NS;
-    // prefix and suffix compositions of the items, then the head / tail parts
-    BandFn P[NS], S[NS];
-    P[0] = {(int32_t)(w0[0] & 0x7fffffu), (int32_t)w1[0]};
-#pragma unroll
-    for (int t = 1; t < NS; ++t) P[t] = band_compose(P[t - 1], BandFn{(int32_t)(w0[t] & 0x7fffffu), (int32_t)w1[t]});
-    S[NS - 1] = {(int32_t)(w0[NS - 1] & 0x7fffffu), (int32_t)w1[NS - 1]};
-#pragma unroll
-    for (int t = NS - 2; t >= 0; --t) S[t] = band_compose(BandFn{(int32_t)(w0[t] & 0x7fffffu), (int32_t)w1[t]}, S[t + 1]);
-    BandFn pre = {0, 0}, suf = {0, 0};
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      if (h == t + 1) pre = P[t];
-      if (sft == t) suf = S[t];
-    }
     const int lastKeyPrev = dpp<DPP_WAVE_SHR1>(-2000, kt[NS - 1]);
-    const bool connIn = lane > 0 && kt[0] == lastKeyPrev;   // dirty keys are unique
+    const bool connIn = lane > 0 && kt[0] == lastKeyPrev; // item 0 continues a run
     const bool connOut = __builtin_amdgcn_update_dpp(0, (int)connIn, DPP_WAVE_SHL1, 0xf, 0xf, false) != 0 && lane < 63;
     const bool segHead = !(whole && connIn);
     const uint64_t heads = __ballot(segHead);
     const int start = 63 - __builtin_clzll(heads & (lane == 63 ? ~0ull : ((2ull << lane) - 1)));
-    const BandFn A = wave_seg_compose(whole ? pre : suf, start, lane);
-    // the run ending in this lane's head items, from its head in an earlier lane
+    // the run ending at the lane's last item, from its head in this or an earlier lane
+    const BandFn A = wave_seg_compose(Q[NS - 1], start, lane);
+    // the head run (items 0 .. h-1) from its head in an earlier lane
     const BandFn Aprev = {dpp<DPP_WAVE_SHR1>(0, A.d0), dpp<DPP_WAVE_SHR1>(0, A.d1)};
-    const BandFn H = connIn ? band_compose(Aprev, pre) : pre;
-    const uint32_t hw0 = band_pack(kt[0] > -1000 ? kt[0] : 0, H.d0 & 0x7fffff,
-                                   h > 0 && ((uint32_t)H.d0 | (uint32_t)H.d1) < (1u << 23)),
-                   hw1 = (uint32_t)H.d1;
-    const int akey = whole ? kt[0] : kt[NS - 1];
-    const uint32_t aw0 = band_pack(akey > -1000 ? akey : 0, A.d0 & 0x7fffff,
-                                   (whole || sft < NS) && ((uint32_t)A.d0 | (uint32_t)A.d1) < (1u << 23)),
-                   aw1 = (uint32_t)A.d1;
-    const uint64_t visit = __ballot(segHead || !connOut);
-    // the lane's stitch events in order, each a packed map (bit 31 set), the
-    // serial marker 0x40000000 (a dirty middle item), or 0 (none):
-    //   0: the run ending in the head items;  1..NS: middle items;
-    //   NS+1: the run ending at the lane's end
-    constexpr int NE = NS + 2;
-    uint32_t ev0[NE], ev1[NE];
-    ev0[0] = (!whole && h > 0) ? hw0 : 0u;
-    ev1[0] = hw1;
+    BandFn Qh = Q[0];
+#pragma unroll
+    for (int t = 1; t < NS; ++t) {
+      Qh.d0 = h == t + 1 ? Q[t].d0 : Qh.d0;
+      Qh.d1 = h == t + 1 ? Q[t].d1 : Qh.d1;
+    }
+    const BandFn H = band_compose(Aprev, Qh);
+    // the lane's stitch events, item by item: a packed map (bit 31 set) where
+    // a run ends, the serial marker 0x40000000 for a dirty item, 0 otherwise
+    uint32_t ev0[NS], ev1[NS], evmask = 0;
 #pragma unroll
     for (int t = 0; t < NS; ++t) {
-      const bool mid = !whole && t >= h && t < sft;
-      ev0[1 + t] = mid ? ((w0[t] >> 31) ? w0[t] : 0x40000000u) : 0u;
-      ev1[1 + t] = w1[t];
+      const bool end = t < NS - 1 ? kt[t] != kt[t + 1] : !connOut;
+      const bool useH = connIn && t == h - 1;
+      const int32_t m0 = useH ? H.d0 : Q[t].d0, m1 = useH ? H.d1 : Q[t].d1;
+      const bool ok = ((uint32_t)m0 | (uint32_t)m1) < (1u << 23);
+      const uint32_t pk = ((uint32_t)m0 & 0x7fffffu) | (w0[t] & 0x7f800000u) | (ok ? 0x80000000u : 0u);
+      ev0[t] = kt[t] <= -1000 ? 0x40000000u : end ? pk : 0u;
+      ev1[t] = (uint32_t)m1;
+      evmask |= ev0[t] ? (1u << t) : 0u;
     }
-    ev0[NS + 1] = (!connOut && (whole || sft < NS)) ? aw0 : 0u;
-    ev1[NS + 1] = aw1;
-    uint32_t evmask = 0;
-#pragma unroll
-    for (int e = 0; e < NE; ++e) evmask |= ev0[e] ? (1u << e) : 0u;
+    const uint64_t visit = __ballot(evmask != 0);
     // ---- 5. wave-uniform stitch from s0 (scalar code: a wave issues one
     //         instruction per four cycles, so the step is kept short)
     uint32_t s = __float_as_uint(s0);
@@ -384,24 +376,23 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
       const int j = __builtin_ctzll(vm);
       const uint32_t m = __builtin_amdgcn_readlane(evmask, j);
 #pragma unroll
-      for (int e = 0; e < NE; ++e) {
-        if (!(m & (1u << e))) continue;
-        const uint32_t a0 = __builtin_amdgcn_readlane(ev0[e], j), a1 = __builtin_amdgcn_readlane(ev1[e], j);
+      for (int t = 0; t < NS; ++t) {
+        if (!(m & (1u << t))) continue;
+        const uint32_t a0 = __builtin_amdgcn_readlane(ev0[t], j);
+        if (a0 == 0x40000000u) {
+          // a dirty item: its own serial steps (every lane runs its own
+          // elements from s; lane j's result is kept)
+          s = serial16(s, &xf[16 * t], j);
+          ++nslow;
+          continue;
+        }
+        const uint32_t a1 = __builtin_amdgcn_readlane(ev1[t], j);
         const uint32_t lo = a0 & 0x7f800000u;
         const uint32_t ns = s + ((s & 1u) ? a1 : (a0 & 0x7fffffu));
         // zero iff the map is valid and s and its image lie in the binade
         const uint32_t chk = ((s - lo) | (ns - lo) | (~a0 & 0x80000000u)) >> 23;
-        if (e == 0 || e == NE - 1) {
-          runBad |= chk;
-          s = chk ? s : ns;
-        } else if (chk == 0) {
-          s = ns;
-        } else {
-          // the item's own serial steps (every lane runs its own elements
-          // from s; lane j's result is kept)
-          s = serial16(s, &xf[16 * (e - 1)], j);
-          ++nslow;
-        }
+        runBad |= chk;
+        s = chk ? s : ns;
       }
     }
     const bool fail = runBad != 0; // a run did not hold (its binade was mispredicted)
