@@ -372,6 +372,9 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
     uint32_t s = __float_as_uint(s0);
     int nslow = 0;
     uint32_t runBad = 0;
+    // (raised issue priority: the stitch is the wave's latency-bound part,
+    // and the SIMD's other waves fill the VALU around it)
+    __builtin_amdgcn_s_setprio(1);
     for (uint64_t vm = visit; vm; vm &= vm - 1) {
       const int j = __builtin_ctzll(vm);
       const uint32_t m = __builtin_amdgcn_readlane(evmask, j);
@@ -395,6 +398,7 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
         s = chk ? s : ns;
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     const bool fail = runBad != 0; // a run did not hold (its binade was mispredicted)
     if (fail) {
       // a run did not hold (its binade was mispredicted): item by item
