@@ -2432,47 +2432,56 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
   if ((bT ? b->type.shape[1] : b->type.shape[0]) != K) unsupported(mm, "matmul shapes");
   Elem ae = a->type.elem, be = b->type.elem;
   int mk = -1;
+  bool fp4 = false;
+  int64_t Kl = K; // logical K (fp4 packs two values per byte)
   const Value *sa = nullptr, *sb = nullptr;
   if (mx) {
-    // the matrix core's format codes: 0 e4m3, 1 e5m2 (HFusionAttrs.td:131-137
-    // numbers them FP8E5M2_T = 1, FP8E4M3_T = 2, FP4E2M1_T = 3)
+    // the matrix core's format codes: 0 e4m3, 1 e5m2, 4 e2m1 (fp4).  The
+    // lhsFormat / rhsFormat attribute (HFusionAttrs.td:131-137: FP8E5M2_T = 1,
+    // FP8E4M3_T = 2, FP4E2M1_T = 3) decides over the element type when
+    // present, as HFusionToHIVM keeps it for the HIVM op when the type does
+    // not match it (Matmul.cpp:62-70); fp4 operands are bytes holding two
+    // values along K, the even k in the low nibble (LocalMmadMx.cpp:131-133,
+    // K factor 2)
     auto fmt = [&](const Value *orig, const char *attr) -> int {
+      auto it = mm->attrs.find(attr);
+      if (it != mm->attrs.end()) {
+        int code = -1;
+        size_t used = 0;
+        try { code = std::stoi(it->second, &used); } catch (...) { code = -1; }
+        if (used == 0) code = -1;
+        if (code == 1) return 1;
+        if (code == 2) return 0;
+        if (code == 3) return 4;
+        unsupported(mm, std::string("matmul_mx operand without a valid ") + attr);
+      }
       const Elem e = orig->type.elem;
       if (e == Elem::F8E4M3FN) return 0;
       if (e == Elem::F8E5M2) return 1;
-      if (e == Elem::I8) {
-        auto it = mm->attrs.find(attr);
-        int code = -1;
-        if (it != mm->attrs.end()) {
-          size_t used = 0;
-          try { code = std::stoi(it->second, &used); } catch (...) { code = -1; }
-          if (used == 0) code = -1;
-        }
-        if (code == 1) return 1;
-        if (code == 2) return 0;
-        if (code == 3) unsupported(mm, "matmul_mx fp4 (e2m1) operands");
-        unsupported(mm, std::string("matmul_mx byte operand without a valid ") + attr);
-      }
+      if (e == Elem::I8) unsupported(mm, std::string("matmul_mx byte operand without a valid ") + attr);
       unsupported(mm, "matmul_mx operand type (f8E4M3FN, f8E5M2 or bytes with a format)");
       return -1;
     };
     const int fa = fmt(mm->ins[0], "lhsFormat"), fb = fmt(mm->ins[1], "rhsFormat");
-    mk = 3 + 2 * fa + fb;
+    if ((fa == 4) != (fb == 4)) unsupported(mm, "matmul_mx mixing fp4 (e2m1) and fp8 operands");
+    fp4 = fa == 4;
+    mk = fp4 ? 7 : 3 + 2 * fa + fb;
+    Kl = fp4 ? 2 * K : K;
     if (mm->ins.size() != 4) unsupported(mm, "matmul_mx takes A, B and two scale operands");
     sa = mm->ins[2];
     sb = mm->ins[3];
     if (sa->argIdx < 0 || sb->argIdx < 0) unsupported(mm, "matmul_mx scales must be group arguments");
     if (sa->type.elem != Elem::I8 || sb->type.elem != Elem::I8) unsupported(mm, "matmul_mx scales are ui8 / i8 (e8m0)");
-    if (K % 32 != 0 || sa->type.shape != std::vector<int64_t>{M, K / 32} || sb->type.shape != std::vector<int64_t>{N, K / 32})
+    if (Kl % 32 != 0 || sa->type.shape != std::vector<int64_t>{M, Kl / 32} || sb->type.shape != std::vector<int64_t>{N, Kl / 32})
       unsupported(mm, "matmul_mx scales must be [M, K/32] and [N, K/32]");
-    if (K % 128 != 0) unsupported(mm, "matmul_mx K must be a multiple of 128");
+    if (K % 128 != 0) unsupported(mm, fp4 ? "matmul_mx fp4 K must be a multiple of 256" : "matmul_mx K must be a multiple of 128");
     if (N % 16 != 0) unsupported(mm, "matmul_mx N must be a multiple of 16");
     if (mm->results[0]->type.elem != Elem::F32) unsupported(mm, "matmul_mx accumulates in f32");
     ae = be = Elem::I8; // bytes from here on
   } else if (ae == Elem::I8 && be == Elem::I8) mk = 0;
   else if (ae == Elem::BF16 && be == Elem::BF16) mk = 1;
   else if (ae == Elem::F16 && be == Elem::F16) mk = 2;
-  if (mk < 0) unsupported(mm, "matmul element types (supported: i8 x i8, bf16 x bf16, f16 x f16, matmul_mx fp8)");
+  if (mk < 0) unsupported(mm, "matmul element types (supported: i8 x i8, bf16 x bf16, f16 x f16, matmul_mx fp8 / fp4)");
   const bool i8 = mk == 0;
   if (!hivm && !mx) {
     Elem ce = mm->results[0]->type.elem;
@@ -2514,6 +2523,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
   // products are exact and whose sums are f32 (the fp8 matrix core's 64-k dot
   // product is not: about 2^-11 of the products' magnitude sum)
   const bool mxExact = mx && opt.mxExact;
+  if (mxExact && fp4) unsupported(mm, "mx_exact=1 with fp4 operands (the option is for fp8)");
   // a runtime row count is M, the rows of a row-major A and of C
   if (A.rowsDyn && (aT || M != kRuntimeRows || mxExact))
     unsupported(mm, "a runtime row count other than the rows of A [M, K] (or with mx_exact=1)");
@@ -2700,7 +2710,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
     p.rowsC = (N + TN - 1) / TN;
   }
   p.block[0] = (unsigned)threads;
-  static const char *mxName[4] = {"e4m3 x e4m3", "e4m3 x e5m2", "e5m2 x e4m3", "e5m2 x e5m2"};
+  static const char *mxName[5] = {"e4m3 x e4m3", "e4m3 x e5m2", "e5m2 x e4m3", "e5m2 x e5m2", "e2m1 x e2m1, fp4 two per byte"};
   p.variant = std::string(mxExact ? std::string("exact matmul_mx: ") + mxName[mk - 3] +
                                          " with e8m0 scales per 32 k, scaled into bf16 by pre kernels, mfma_f32_32x32x16_bf16"
                           : mx ? std::string("mfma_scale_f32_32x32x64_f8f6f4 (") + mxName[mk - 3] + ", e8m0 scales per 32 k)"
@@ -2710,7 +2720,7 @@ KernelPlan lowerMatmul(Analysis &A, const std::string &kname, const LowerOptions
               (dma == 4 ? std::string(", LDS DMA ring (128-byte slices, 2 waves/SIMD; ") + (aT && bT ? "A" : aT ? "A and B" : "B") +
                               " k-rows staged whole, transposing LDS reads)" :
                dma == 3 ? ", LDS DMA ring (128-byte slices, 2 waves/SIMD)" : dma == 1 ? ", LDS DMA ring" : ", register staging");
-  p.algoOps = 2.0 * (double)M * (double)N * (double)K;
+  p.algoOps = 2.0 * (double)M * (double)N * (double)Kl;
   return p;
 }
 

@@ -36,9 +36,11 @@ constexpr int MM_LDS_STRIDE = MM_BK + 16;             // 80 B rows: conflict-fre
 // Matrix-core kinds: int8 -> int32, bf16 -> fp32, f16 -> fp32 (32x32 tiles;
 // each lane feeds 16 bytes of A and of B per instruction, 32 bytes of K).
 // MK_MX + 2 * fa + fb: block-scaled fp8 (fa, fb: 0 e4m3, 1 e5m2, the
-// matrix core's format codes), 32 k per e8m0 scale
-enum MmadKind : int { MK_I8 = 0, MK_BF16 = 1, MK_F16 = 2, MK_MX = 3 };
-constexpr bool mk_is_mx(int mk) { return mk >= MK_MX && mk < MK_MX + 4; }
+// matrix core's format codes), 32 k per e8m0 scale; MK_MX4: block-scaled
+// fp4 (e2m1, format code 4) on both sides, two values per byte along K
+enum MmadKind : int { MK_I8 = 0, MK_BF16 = 1, MK_F16 = 2, MK_MX = 3, MK_MX4 = 7 };
+constexpr bool mk_is_mx(int mk) { return mk >= MK_MX && mk <= MK_MX4; }
+constexpr bool mk_is_fp4(int mk) { return mk == MK_MX4; }
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 template <int MK> struct MfmaOp;
@@ -63,15 +65,20 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 // byte of lane l applies to row (col) l % 32 at k = 32 (l / 32) .. +31, i.e.
 // to bytes 0-15 of lanes 32 (l / 32) / 32 and bytes 16-31 alike.  SEL picks
 // the byte of the scale register.
+// For fp4 each lane's 16 bytes hold its 32 k (k = 32 (l / 32) + 0..31, the
+// even k in the low nibble): exactly the int8 fragment of one 32-byte k-block,
+// in the operand's low four registers.
 template <int MK> struct MfmaMx {
   static_assert(mk_is_mx(MK), "block-scaled kind");
   using acc_t = v16f;
+  static constexpr int FA = mk_is_fp4(MK) ? 4 : (MK - MK_MX) / 2, FB = mk_is_fp4(MK) ? 4 : (MK - MK_MX) % 2;
   template <int SEL>
   __device__ __forceinline__ static acc_t run(v8i a, v8i b, acc_t c, int sa, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, (MK - MK_MX) / 2, (MK - MK_MX) % 2, SEL, sa, SEL, sb);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, SEL, sa, SEL, sb);
   }
 };
 __device__ __forceinline__ v8i mx_cat(v4i lo, v4i hi) { return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}; }
+__device__ __forceinline__ v8i mx_lo(v4i lo) { return v8i{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0}; }
 template <> struct MfmaOp<MK_F16> {
   using acc_t = v16f;
   using scalar_t = float;
@@ -538,14 +545,18 @@ constexpr int MMD2_SLICE = 256 * 128;
 // slice's scales (bytes 4s .. 4s+3 of each row: 1 KB for the tile's 256 A
 // rows, 1 KB for its 256 B columns) ride the same ring, one 4-byte-per-lane
 // DMA per wave per stage, so every load of a stage is covered by the ring's
-// own wait.
+// own wait.  Block-scaled fp4 (MK_MX4): a 128-byte slice holds 256 k, four
+// scaled fp4 MFMAs of 64 k per tile, each taking the int8 path's fragment of
+// one k-block (16 bytes, 32 k per lane); the slice's scales are 8 bytes of
+// each row, two 4-byte DMAs per wave per stage into two planes.
 // AKM: A is [K, M] (hivm a_transpose), staged and read exactly as a [K, N] B
 // (its M columns in place of N).
 template <int MK, typename Epi, bool BKN, bool AKM = false, typename ElemT, typename Args>
 __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restrict__ B, typename Epi::out_t *__restrict__ out,
                              int64_t M, int64_t N, int64_t K, const Args &P, const uint8_t *__restrict__ SA = nullptr,
                              const uint8_t *__restrict__ SB = nullptr) {
-  constexpr bool MX = mk_is_mx(MK);
+  constexpr bool MX = mk_is_mx(MK), FP4 = mk_is_fp4(MK);
+  constexpr int NW = FP4 ? 2 : 1; // scale words per row per stage (32 k per byte)
   static_assert(!AKM || !MX, "block-scaled A is [M, K]");
   static_assert(!(BKN || AKM) || (((MK == MK_I8 || MX) && sizeof(ElemT) == 1) ||
                                   ((MK == MK_BF16 || MK == MK_F16) && sizeof(ElemT) == 2)),
@@ -555,7 +566,7 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   using acc_t = typename Op::acc_t;
   constexpr int ESZ = sizeof(ElemT);
   __shared__ __attribute__((aligned(1024))) char lds[2][2][MMD2_SLICE]; // [stage][A/B]
-  __shared__ __attribute__((aligned(1024))) uint32_t lds_sc[MX ? 2 : 1][2][MX ? 256 : 1]; // [stage][A/B][row]
+  __shared__ __attribute__((aligned(1024))) uint32_t lds_sc[MX ? 2 : 1][2 * NW][MX ? 256 : 1]; // [stage][A/B x word][row]
   const int tmt = (int)((M + MM_TM - 1) / MM_TM), tnt = (int)((N + MM_TN - 1) / MM_TN);
   int ti, tj;
   mm_tile_of(blockIdx.x, tmt, tnt, ti, tj);
@@ -563,7 +574,7 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   const int64_t Kb = K * ESZ;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int wm = wave / 4, wn = wave % 4; // waves w and w+4 share a SIMD
-  constexpr int DPS = MX ? 9 : 8;         // DMA instructions per wave per stage
+  constexpr int DPS = 8 + (MX ? NW : 0); // DMA instructions per wave per stage
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)&lds[0][0][0];
   const char *Ab = reinterpret_cast<const char *>(A), *Bb = reinterpret_cast<const char *>(B);
   const int nsteps = (int)(Kb / 128);
@@ -626,7 +637,8 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     mmd_dma16_off(dbase[d >= 4] + (int64_t)s * dstride[d >= 4], dofs[d], __builtin_amdgcn_readfirstlane(st));
   };
   // the scales of K slice s: wave w carries 64 rows (w < 4: A rows 64 w ..,
-  // else B columns 64 (w - 4) ..), 4 bytes each
+  // else B columns 64 (w - 4) ..), 4 bytes each (fp4: 8 bytes, as two words
+  // in two planes); a row of scales has K/32 bytes (fp4: K/16, K in bytes)
   const uint32_t lds_sc0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t *)&lds_sc[0][0][0];
   auto issue_scales = [&](int s, int slot) {
     if constexpr (MX) {
@@ -634,8 +646,10 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
       const int64_t rows = op ? N : M, row0 = op ? n0 : m0;
       int64_t row = row0 + r;
       row = row < rows ? row : rows - 1;
-      mmd_dma4((op ? SB : SA) + row * (K / 32) + 4 * (int64_t)s,
-               __builtin_amdgcn_readfirstlane(lds_sc0 + (uint32_t)((slot * 2 + op) * 1024 + 256 * (wave % 4))));
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+        mmd_dma4((op ? SB : SA) + row * (K / (32 / NW)) + 4 * NW * (int64_t)s + 4 * w,
+                 __builtin_amdgcn_readfirstlane(lds_sc0 + (uint32_t)(((slot * 2 + op) * NW + w) * 1024 + 256 * (wave % 4))));
     }
   };
   auto issue_stage = [&](int s) {
@@ -711,13 +725,17 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
   };
 
   // this lane's scale words for stage s, shifted so that byte 2h is the scale
-  // of its k-half in half h of the slice
+  // of its k-half in half h of the slice (fp4: word w, byte 2q, of its
+  // k-half in k-block 2w + q; word 1 is read for the second half, after the
+  // first half's fragments are dead)
   uint32_t sa_w[4], sb_w[2];
-  auto read_scales = [&](int s) {
+  auto read_scales = [&](int s, int w) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sa_w[i] = lds_sc[MX ? (s & 1) : 0][0][MX ? wm * 128 + i * 32 + lane % 32 : 0] >> (8 * (lane / 32));
+    for (int i = 0; i < 4; ++i)
+      sa_w[i] = lds_sc[MX ? (s & 1) : 0][w][MX ? wm * 128 + i * 32 + lane % 32 : 0] >> (8 * (lane / 32));
 #pragma unroll
-    for (int j = 0; j < 2; ++j) sb_w[j] = lds_sc[MX ? (s & 1) : 0][1][MX ? (wn * 2 + j) * 32 + lane % 32 : 0] >> (8 * (lane / 32));
+    for (int j = 0; j < 2; ++j)
+      sb_w[j] = lds_sc[MX ? (s & 1) : 0][NW + w][MX ? (wn * 2 + j) * 32 + lane % 32 : 0] >> (8 * (lane / 32));
   };
 
   // Step s: wait for stage s (stage s+1 may be in flight); multiply its first
@@ -734,8 +752,19 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     __syncthreads();
     fetch(s, 0, f0);
     fetch(s, 1, f1);
-    if constexpr (MX) {
-      read_scales(s);
+    if constexpr (FP4) {
+      // k-blocks 0 and 1 of the slice: one scaled fp4 MFMA each
+      read_scales(s, 0);
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = q == 0 ? Op::template run<0>(mx_lo(f0[0][i]), mx_lo(f0[0][4 + j]), acc[i][j], (int)sa_w[i], (int)sb_w[j])
+                               : Op::template run<2>(mx_lo(f0[1][i]), mx_lo(f0[1][4 + j]), acc[i][j], (int)sa_w[i], (int)sb_w[j]);
+    } else if constexpr (MX) {
+      read_scales(s, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -753,7 +782,20 @@ __device__ void mmad_core_pp(const ElemT *__restrict__ A, const ElemT *__restric
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads(); // every wave holds stage s in registers: its slot is free
     const int s2 = s + 2 < nsteps ? s + 2 : nsteps - 1;
-    if constexpr (MX) {
+    if constexpr (FP4) {
+      // k-blocks 2 and 3
+      read_scales(s, 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue_one(s2, s & 1, i * 2 + j);
+          acc[i][j] = Op::template run<0>(mx_lo(f1[0][i]), mx_lo(f1[0][4 + j]), acc[i][j], (int)sa_w[i], (int)sb_w[j]);
+          acc[i][j] = Op::template run<2>(mx_lo(f1[1][i]), mx_lo(f1[1][4 + j]), acc[i][j], (int)sa_w[i], (int)sb_w[j]);
+        }
+      issue_scales(s2, s & 1);
+    } else if constexpr (MX) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -925,8 +967,10 @@ __device__ __forceinline__ void mmad(const ElemT *A, const ElemT *B, typename Ep
   else mmad_core<MK, Epi, AT, BT>(A, B, out, M, N, K, P);
 }
 
-// Block-scaled fp8 contraction: A [M, K], B [K, N] (bytes of the formats
-// MK encodes), SA [M, K/32], SB [N, K/32] e8m0; K a multiple of 128, N of 16.
+// Block-scaled fp8 / fp4 contraction: A [M, K], B [K, N] (bytes of the
+// formats MK encodes; K counts bytes), SA [M, K/32], SB [N, K/32] e8m0 (fp4:
+// two values per byte, so [M, K/16] and [N, K/16]); K a multiple of 128, N
+// of 16.
 template <int MK, typename Epi, typename Args>
 __device__ __forceinline__ void mmad_mx(const uint8_t *A, const uint8_t *B, const uint8_t *SA, const uint8_t *SB,
                                         typename Epi::out_t *out, int64_t M, int64_t N, int64_t K, const Args &P) {

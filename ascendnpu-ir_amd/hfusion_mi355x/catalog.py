@@ -22,6 +22,8 @@ def entries():
     e["w8a8_dequant_kn"] = g.w8a8_dequant(4096, 4096, 4096, b_layout="kn").replace("@w8a8_dequant(", "@w8a8_dequant_kn(")
     # block-scaled fp8 (hfusion.matmul_mx), e4m3 x e4m3 with e8m0 scales
     e["mx_fp8"] = g.matmul_mx(4096, 4096, 4096, name="mx_fp8")
+    # block-scaled fp4 (e2m1, two values per byte), 4096^3 logical
+    e["mx_fp4"] = g.matmul_mx(4096, 4096, 4096, fa="e2m1", fb="e2m1", via="bitcast", name="mx_fp4")
     return e
 
 

@@ -415,18 +415,24 @@ def exp_cumsum_scale(rows=64, cols=1000):
 
 
 def matmul_mx(m=4096, n=4096, k=4096, fa="e4m3", fb="e4m3", via="fp8", init=None, out="f32", name="matmul_mx"):
-    """Block-scaled fp8 contraction (hfusion.matmul_mx, HFusionOps.td:1233-1291):
+    """Block-scaled fp8 / fp4 contraction (hfusion.matmul_mx, HFusionOps.td:1233-1291):
     C = init + (A * 2^(sa-127)) x (B * 2^(sb-127)), A [M, K], B [K, N],
-    e8m0 scales sa [M, K/32] and sb [N, K/32] (ui8).  `via` is how the fp8
+    e8m0 scales sa [M, K/32] and sb [N, K/32] (ui8); fp4 operands are
+    [M, K/2] and [K/2, N] bytes.  `via` is how the fp8
     operands arrive: typed ("fp8"), as bytes through hfusion.bitcast
     ("bitcast", the form of the reference's conversion tests), or as bytes
     with lhsFormat / rhsFormat ("format").  init None accumulates onto a
     tensor.empty (zero); a number fills the accumulator first.  out "bf16"
     adds a cast epilogue."""
-    ty = {"e4m3": "f8E4M3FN", "e5m2": "f8E5M2"}
-    code = {"e5m2": 1, "e4m3": 2}
-    FA, FB = _t([m, k], ty[fa]), _t([k, n], ty[fb])
-    IA, IB = _t([m, k], "i8"), _t([k, n], "i8")
+    # fp4 ("e2m1", format 3): two values per byte along K, carried as bytes
+    # bitcast to f8E5M2, as in matmul-mx-format.mlir's fp4 case
+    ty = {"e4m3": "f8E4M3FN", "e5m2": "f8E5M2", "e2m1": "f8E5M2"}
+    code = {"e5m2": 1, "e4m3": 2, "e2m1": 3}
+    if (fa == "e2m1") != (fb == "e2m1") or (fa == "e2m1" and via == "fp8"):
+        raise ValueError("fp4 operands come in pairs, as bytes with a format")
+    ka, kb = (k // 2, k // 2) if fa == "e2m1" else (k, k)
+    FA, FB = _t([m, ka], ty[fa]), _t([kb, n], ty[fb])
+    IA, IB = _t([m, ka], "i8"), _t([kb, n], "i8")
     SA, SB = _t([m, k // 32], "ui8"), _t([n, k // 32], "ui8")
     C, O = _t([m, n], "f32"), _t([m, n], out)
     pa, pb = (IA, IB) if via in ("bitcast", "format") else (FA, FB)

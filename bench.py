@@ -29,13 +29,14 @@ ORDER = ["rmsnorm_quant", "vec_add", "safe_softmax", "argmax", "w8a8_dequant"]
 # further groups on the hot path, measured the same way (not BASELINE configs):
 # the bf16 contraction, W8A8 with B as [K, N], a transpose fused with a cast,
 # the block-scaled fp8 contraction (hfusion.matmul_mx)
-EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast", "mx_fp8", "mx_fp8_exact"]
+EXTRA = ["bf16_mmad", "w8a8_dequant_kn", "transpose_cast", "mx_fp8", "mx_fp8_exact", "mx_fp4"]
 # bench names that are a product group compiled with options
 VARIANTS = {"mx_fp8_exact": ("mx_fp8", "mx_exact=1"),
             # the other kernels of the RMSNorm pattern, for --only runs
             "rmsnorm_quant_rowprog": ("rmsnorm_quant", "rmsq_kernel=0"),
             "rmsnorm_quant_rmsn": ("rmsnorm_quant", "rmsn_kernel=1")}
 FP8_PEAK_TFLOPS = 5000.0  # dense fp8 MFMA (the block-scaled form runs at the same rate)
+FP4_PEAK_TFLOPS = 10100.0  # dense fp4 (and fp6) MFMA
 
 
 def log(msg):
@@ -49,7 +50,7 @@ def generic_inputs(meta, dev, seed=7):
     rng = np.random.default_rng(seed)
     out = []
     scaled = "e8m0" in meta.get("variant", "")
-    for p in meta["params"]:
+    for idx, p in enumerate(meta["params"]):
         shape, elem = tuple(p["shape"]), p["elem"]
         if elem in ("f8E4M3FN", "f8E5M2") and p["role"] == "in":
             # every finite code (NaN / inf codes moved to finite neighbours)
@@ -57,6 +58,10 @@ def generic_inputs(meta, dev, seed=7):
             v[(v & 0x7F) == 0x7F if elem == "f8E4M3FN" else (v & 0x7C) == 0x7C] &= 0xF7 if elem == "f8E4M3FN" else 0xF3
             dt = torch.float8_e4m3fn if elem == "f8E4M3FN" else torch.float8_e5m2
             out.append(torch.from_numpy(v).view(dt).to(dev))
+            continue
+        if scaled and elem == "i8" and p["role"] == "in" and idx < 2:
+            # fp4 operand bytes: every code is a number
+            out.append(torch.from_numpy(rng.integers(0, 256, shape).astype(np.uint8)).view(torch.int8).to(dev))
             continue
         if scaled and elem == "i8" and p["role"] == "in":
             # e8m0 block scales around 2^0
@@ -589,8 +594,9 @@ def main():
             achieved = ops / (kern_ms * 1e-3) / 1e12
             bf16 = "bf16" in meta.get("variant", "")
             fp8 = "mfma_scale" in meta.get("variant", "")
-            peak, unit = ((BF16_PEAK_TFLOPS, "TFLOP/s") if bf16 else (FP8_PEAK_TFLOPS, "TFLOP/s") if fp8
-                          else (INT8_PEAK_TOPS, "TOPS"))
+            fp4 = fp8 and "e2m1" in meta.get("variant", "")
+            peak, unit = ((BF16_PEAK_TFLOPS, "TFLOP/s") if bf16 else (FP4_PEAK_TFLOPS, "TFLOP/s") if fp4
+                          else (FP8_PEAK_TFLOPS, "TFLOP/s") if fp8 else (INT8_PEAK_TOPS, "TOPS"))
             entry = {"value": ops * args.steps / (total_ms * 1e-3) / 1e12, "unit": unit, "ms_per_step": ms,
                      "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": unit,
                                   "frac": achieved / peak, "traffic": None}}
@@ -625,7 +631,7 @@ def main():
         "dtype": {"rmsnorm_quant": "f32", "vec_add": "f32", "safe_softmax": "f32", "argmax": "f32",
                   "w8a8_dequant": "int8", "w8a8_dequant_kn": "int8", "bf16_mmad": "bf16",
                   "transpose_cast": "bf16", "mx_fp8": "fp8 (e4m3, e8m0 scales)",
-                  "mx_fp8_exact": "fp8 (e4m3, e8m0 scales) via bf16"}[head_base if head_base != "mx_fp8" else head],
+                  "mx_fp8_exact": "fp8 (e4m3, e8m0 scales) via bf16", "mx_fp4": "fp4 (e2m1, e8m0 scales)"}[head_base if head_base != "mx_fp8" else head],
         "data": "synthetic (seeded splitmix64)",
         "config": {"workload": head, **{k: v for k, v in cfg.items()}},
         "roofline": h["roofline"],

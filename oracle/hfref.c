@@ -598,10 +598,22 @@ void hfref_matmul_f32(const float *A, const float *B, float *C, int64_t M,
     }
 }
 
+/* e2m1 (OCP MX fp4): sign, two exponent bits (bias 1), one mantissa bit;
+ * exponent 0 is the subnormal 0.5 m.  The 16 values are +-{0, 0.5, 1, 1.5,
+ * 2, 3, 4, 6}. */
+float hfref_fp4_to_f32(uint8_t v) {
+  const float sgn = (v & 8) ? -1.0f : 1.0f;
+  const int e = (v >> 1) & 3, m = v & 1;
+  return sgn * (e == 0 ? 0.5f * (float)m : ldexpf(1.0f + 0.5f * (float)m, e - 1));
+}
+
 /* hfusion.matmul_mx (HFusionOps.td:1233-1291): C = C + (A * 2^(sa-127)) x
- * (B * 2^(sb-127)), A [M, K] and B [K, N] fp8 bytes of formats fa / fb (0
- * e4m3, 1 e5m2), sa [M, ceil(K/32)] and sb [N, ceil(K/32)] e8m0 bytes, one
- * per 32 k.  Each scaled operand is rounded to f32, the product is an f32
+ * (B * 2^(sb-127)), A [M, K] and B [K, N] of formats fa / fb (0 e4m3, 1
+ * e5m2: one byte each; 4 e2m1: two values per byte, the even k in the low
+ * nibble, so A is [M, K/2] and B [K/2, N] bytes -- the packing of the
+ * reference's fp4x2_e2m1_t, LocalMmadMx.cpp:131-133, whose K factor is 2),
+ * sa [M, ceil(K/32)] and sb [N, ceil(K/32)] e8m0 bytes, one per 32 k of the
+ * K logical values.  Each scaled operand is rounded to f32, the product is an f32
  * multiply and the sum runs serially over k from C's value, as the linalg.matmul
  * region the reference's decomposition ends in (HFusionOps.cpp:3590-3790:
  * operand * broadcast scale, then linalg.matmul).  Where the
@@ -616,17 +628,25 @@ static float mx_scale(uint8_t e) {
   return e == 255 ? NAN : ldexpf(1.0f, (int)e - 127);
 }
 static float mx_scaled(uint8_t v, int fmt, uint8_t e) {
-  return (float)((double)hfref_fp8_to_f32(v, fmt) * (double)mx_scale(e));
+  const float x = fmt == 4 ? hfref_fp4_to_f32(v) : hfref_fp8_to_f32(v, fmt);
+  return (float)((double)x * (double)mx_scale(e));
+}
+/* element k of a row of packed values (fmt 4: nibbles, low one first) */
+static uint8_t mx_elem(const uint8_t *row, int64_t k, int64_t stride, int fmt) {
+  if (fmt != 4) return row[k * stride];
+  const uint8_t b = row[(k / 2) * stride];
+  return (k & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 15);
 }
 void hfref_matmul_mx(const uint8_t *A, const uint8_t *B, const uint8_t *sa, const uint8_t *sb, float *C, int64_t M,
                      int64_t N, int64_t K, int fa, int fb) {
   const int64_t kb = (K + 31) / 32;
+  const int64_t Ka = fa == 4 ? (K + 1) / 2 : K; /* bytes per row of A */
   for (int64_t m = 0; m < M; ++m)
     for (int64_t n = 0; n < N; ++n) {
       float acc = C[m * N + n];
       for (int64_t k = 0; k < K; ++k) {
-        const float x = mx_scaled(A[m * K + k], fa, sa[m * kb + k / 32]);
-        const float y = mx_scaled(B[k * N + n], fb, sb[n * kb + k / 32]);
+        const float x = mx_scaled(mx_elem(A + m * Ka, k, 1, fa), fa, sa[m * kb + k / 32]);
+        const float y = mx_scaled(mx_elem(B + n, k, N, fb), fb, sb[n * kb + k / 32]);
         const float p = x * y;
         acc = acc + p;
       }

@@ -120,7 +120,10 @@ void hfref_matmul_i8_i32(const int8_t *A, const int8_t *B, int32_t *C,
                          int64_t M, int64_t N, int64_t K, int b_transposed);
 void hfref_matmul_f32(const float *A, const float *B, float *C, int64_t M,
                       int64_t N, int64_t K, int b_transposed);
-/* hfusion.matmul_mx: fp8 operands with e8m0 scales per 32 k, f32 serial sum */
+/* hfusion.matmul_mx: fp8 (fa/fb 0 e4m3, 1 e5m2) or packed fp4 (4 e2m1, two
+ * per byte) operands with e8m0 scales per 32 k, f32 serial sum; K counts
+ * logical values */
+float hfref_fp4_to_f32(uint8_t v);
 void hfref_matmul_mx(const uint8_t *A, const uint8_t *B, const uint8_t *sa, const uint8_t *sb, float *C, int64_t M,
                      int64_t N, int64_t K, int fa, int fb);
 

@@ -93,6 +93,8 @@ def lib():
         L.hfref_f32_to_f16_mode.argtypes = [ctypes.c_float, INT]
         L.hfref_bf16_to_f32.argtypes = [ctypes.c_uint16]
         L.hfref_bf16_to_f32.restype = ctypes.c_float
+        L.hfref_fp4_to_f32.argtypes = [ctypes.c_uint8]
+        L.hfref_fp4_to_f32.restype = ctypes.c_float
         L.hfref_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.hfref_f16_to_f32.restype = ctypes.c_float
         L.hfref_f32_to_int_mode.argtypes = [ctypes.c_float, INT, INT, INT]
@@ -857,22 +859,31 @@ class Interp:
             self._reduce_with_index(res, rest, ins, outs, env)
             return
         if op == "hfusion.matmul_mx":
-            # fp8 A [M, K], B [K, N] (bytes take lhsFormat / rhsFormat: 1 e5m2,
-            # 2 e4m3, HFusionAttrs.td:131-137), e8m0 scales [M|N, K/32]
+            # fp8 A [M, K], B [K, N]; lhsFormat / rhsFormat (1 e5m2, 2 e4m3,
+            # 3 fp4 e2m1, HFusionAttrs.td:131-137) decide over the element
+            # type when present (HFusionToHIVM keeps the format when the type
+            # does not match it, Matmul.cpp:62-70); fp4 packs two values per
+            # byte along K (A [M, K/2], B [K/2, N] bytes); e8m0 scales
+            # [M|N, K/32]
             A, B, SA, SB, Cinit = get(ins[0]), get(ins[1]), get(ins[2]), get(ins[3]), get(outs[0])
 
             def fmt(v, attr):
+                code = re.search(attr + r"\s*=\s*(\d+)", rest)
+                if code:
+                    if code.group(1) not in ("1", "2", "3"):
+                        raise NotImplementedError("matmul_mx operand format")
+                    return {"1": 1, "2": 0, "3": 4}[code.group(1)]
                 if v.elem in FP8:
                     return FP8[v.elem]
-                code = re.search(attr + r"\s*=\s*(\d+)", rest)
-                if v.elem not in ("i8", "ui8") or not code or code.group(1) not in ("1", "2"):
-                    raise NotImplementedError("matmul_mx operand format")
-                return 1 if code.group(1) == "1" else 0
+                raise NotImplementedError("matmul_mx operand format")
+            fa_, fb_ = fmt(A, "lhsFormat"), fmt(B, "rhsFormat")
             M, K = A.a.shape
             N = B.a.shape[1]
+            if fa_ == 4:
+                K *= 2
             C = _contig(np.array(Cinit.a, np.float32, copy=True))
             byts = [_contig(v.a).view(np.uint8) for v in (A, B, SA, SB)]  # raw bytes, sign-free
-            lib().hfref_matmul_mx(*(ptr(x) for x in byts), ptr(C), M, N, K, fmt(A, "lhsFormat"), fmt(B, "rhsFormat"))
+            lib().hfref_matmul_mx(*(ptr(x) for x in byts), ptr(C), M, N, K, fa_, fb_)
             env[res] = T(C, "f32")
             return
         if op in ("linalg.matmul", "linalg.matmul_transpose_b"):

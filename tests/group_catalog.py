@@ -1182,6 +1182,11 @@ def entries():
     e["mx_e5m2_bitcast"] = g.matmul_mx(300, 208, 384, fa="e5m2", fb="e4m3", via="bitcast", init=0.5, name="mx_e5m2_bitcast")
     e["mx_format_bf16"] = g.matmul_mx(264, 784, 256, fa="e4m3", fb="e5m2", via="format", out="bf16", name="mx_format_bf16")
     e["mx_e5m2"] = g.matmul_mx(128, 128, 128, fa="e5m2", fb="e5m2", name="mx_e5m2")
+    # fp4 (e2m1, format 3): bytes holding two values along K, bitcast to
+    # f8E5M2 as in matmul-mx-format.mlir, or with the formats alone
+    e["mx_fp4_256"] = g.matmul_mx(256, 256, 512, fa="e2m1", fb="e2m1", via="bitcast", name="mx_fp4_256")
+    e["mx_fp4_ragged"] = g.matmul_mx(300, 208, 768, fa="e2m1", fb="e2m1", via="format", init=0.5, name="mx_fp4_ragged")
+    e["mx_fp4_bf16"] = g.matmul_mx(264, 784, 256, fa="e2m1", fb="e2m1", via="bitcast", out="bf16", name="mx_fp4_bf16")
     # the same through scaled bf16 operands and the bf16 matrix core (mx_exact=1)
     for n in ("mx_e4m3", "mx_e5m2_bitcast", "mx_format_bf16", "mx_e5m2", "mx_fp8"):
         e[n + "_exact"] = e[n]

@@ -157,9 +157,13 @@ def test_matmul_mx_lowering_limits():
         text = hf.groups.matmul_mx(m, n, k, via="format" if extra_attr else "fp8")
         return text.replace("lhsFormat = 2", extra_attr) if extra_attr else text
     for text, msg in ((ir(64, 64, 96), "multiple of 128"), (ir(64, 72, 128), "N must be a multiple of 16"),
-                      (ir(64, 64, 128, "lhsFormat = 3"), "fp4"), (ir(64, 64, 128, "lhsFormat = 12"), "valid lhsFormat")):
+                      (ir(64, 64, 128, "lhsFormat = 3"), "fp4"), (ir(64, 64, 128, "lhsFormat = 12"), "valid lhsFormat"),
+                      (hf.groups.matmul_mx(64, 64, 128, fa="e2m1", fb="e2m1", via="format"), "multiple of 256")):
         with pytest.raises(hf.CompileError, match=msg):
             hf.compile(text, options="emit=hip")
+    with pytest.raises(hf.CompileError, match="fp4"):
+        hf.compile(cat.get("mx_fp4_256"), options="emit=hip;mx_exact=1")
+    assert "mmad_mx<7," in open(hf.compile(cat.get("mx_fp4_256"), options="emit=hip").source).read()
     # ui8 only as matmul_mx scales
     bad = """module {
   func.func @f(%x: tensor<8x8xui8>) -> tensor<8x8xi32>
@@ -173,6 +177,71 @@ def test_matmul_mx_lowering_limits():
     with pytest.raises(hf.CompileError, match="ui8"):
         hf.compile(bad, options="emit=hip")
     assert "mmad_mx" in open(hf.compile(base, options="emit=hip").source).read()
+
+
+# ---- fp4 (e2m1, format 3): two values per byte along K, the even k in the
+# low nibble (the reference library's fp4x2_e2m1_t, LocalMmadMx.cpp:131-133)
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float64)  # OCP MX, magnitudes of codes 0-7
+
+
+def fp4_decode(nib):
+    nib = np.asarray(nib, np.uint8)
+    return np.where(nib & 8, -1.0, 1.0) * E2M1[nib & 7]
+
+
+def fp4_case(rng, m, n, k, spread=8):
+    """Random e2m1 codes (every code is a number) packed two per byte:
+    A [m, k/2], B [k/2, n] bytes, and the unpacked codes [m, k], [k, n]."""
+    ca = rng.integers(0, 16, (m, k)).astype(np.uint8)
+    cb = rng.integers(0, 16, (k, n)).astype(np.uint8)
+    a = (ca[:, 0::2] | (ca[:, 1::2] << 4)).astype(np.uint8)
+    b = (cb[0::2, :] | (cb[1::2, :] << 4)).astype(np.uint8)
+    sa = rng.integers(127 - spread, 128 + spread, (m, k // 32)).astype(np.uint8)
+    sb = rng.integers(127 - spread, 128 + spread, (n, k // 32)).astype(np.uint8)
+    return a, b, sa, sb, ca, cb
+
+
+def fp4_products(ca, cb, sa, sb):
+    k = ca.shape[1]
+    x = fp4_decode(ca) * np.exp2(np.repeat(sa.astype(np.float64) - 127, 32, axis=1)[:, :k])
+    y = fp4_decode(cb) * np.exp2(np.repeat(sb.astype(np.float64) - 127, 32, axis=1)[:, :k]).T
+    return np.abs(x) @ np.abs(y), x @ y
+
+
+def oracle_fp4(a, b, sa, sb, m, n, k):
+    text = hf.groups.matmul_mx(m, n, k, fa="e2m1", fb="e2m1", via="bitcast")
+    return interp.run(text, a, b, sa, sb)[0]
+
+
+def test_oracle_fp4_values():
+    # the 16 e2m1 codes: sign, 2 exponent bits (bias 1), 1 mantissa bit
+    got = np.array([lib().hfref_fp4_to_f32(v) for v in range(16)], np.float64)
+    assert np.array_equal(got, fp4_decode(np.arange(16)))
+    assert np.array_equal(np.signbit(got), np.arange(16) >= 8)
+
+
+def test_oracle_mx_fp4_exact_and_packing():
+    rng = np.random.default_rng(5)
+    m, n, k = 12, 20, 256
+    a, b, sa, sb, ca, cb = fp4_case(rng, m, n, k, spread=0)
+    # unit scales: every product a multiple of 1/4 below 36, every partial
+    # sum below 2^14: the f32 serial sum is the exact (float64) product
+    got = oracle_fp4(a, b, sa, sb, m, n, k)
+    _, exact = fp4_products(ca, cb, sa, sb)
+    assert np.array_equal(got.astype(np.float64), exact)
+    # the nibble order: one nonzero code at an odd k picks B's row k
+    a1 = np.zeros_like(a)
+    a1[3, 7] = 0x20                       # k = 15 (high nibble of byte 7): 1.0
+    got = oracle_fp4(a1, b, sa, sb, m, n, k)
+    assert np.array_equal(got[3].astype(np.float64), fp4_decode(cb[15]))
+    assert not got[np.arange(m) != 3].any()
+    # scales: raising A's block scales by d scales every product by 2^d
+    a, b, sa, sb, ca, cb = fp4_case(rng, m, n, k, spread=3)
+    base = oracle_fp4(a, b, sa, sb, m, n, k)
+    got = oracle_fp4(a, b, (sa.astype(int) + 4).astype(np.uint8), sb, m, n, k)
+    assert np.array_equal(got, np.ldexp(base, 4).astype(np.float32))
+    mag, exact = fp4_products(ca, cb, sa, sb)
+    assert np.all(np.abs(base - exact) <= k * 2.0 ** -24 * mag + 1e-30)
 
 
 # The matrix core's fp8 dot product over 64 k (scaled or not: the unscaled
@@ -217,6 +286,33 @@ def test_matmul_mx_gpu(gpu, name):
         assert np.all(np.abs(gf - wf) <= tol * mag + 2.0 ** -7 * np.abs(wf) + 1e-30)
 
 
+# fp4 on the scaled matrix core (format code 4): the bar is measured below
+# (printed as [err]) and set with margin
+TOL_FP4 = 2.0 ** -17
+FP4_CASES = {"mx_fp4_256": (256, 256, 512, None, "f32"), "mx_fp4_ragged": (300, 208, 768, 0.5, "f32"),
+             "mx_fp4_bf16": (264, 784, 256, None, "bf16")}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(FP4_CASES))
+def test_matmul_mx_fp4_gpu(gpu, name):
+    m, n, k, init, out = FP4_CASES[name]
+    note(f"{name} {m}x{n}x{k} fp4 init={init} out={out}")
+    rng = np.random.default_rng(sum(map(ord, name)))
+    a, b, sa, sb, ca, cb = fp4_case(rng, m, n, k)
+    got, = run_gpu(name, [a, b, sa, sb], gpu)
+    want, = run_oracle(name, [a, b, sa, sb])
+    mag, _ = fp4_products(ca, cb, sa, sb)
+    if out == "f32":
+        err = np.abs(got.astype(np.float64) - want) / np.maximum(mag, 1e-30)
+        print(f"[err] {name}: max |gpu - oracle| / sum|A'B'| = {err.max():.3e}", flush=True)
+        assert np.all(np.abs(got.astype(np.float64) - want) <= TOL_FP4 * mag + 1e-30)
+    else:
+        gf = (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        wf = (want.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        assert np.all(np.abs(gf - wf) <= TOL_FP4 * mag + 2.0 ** -7 * np.abs(wf) + 1e-30)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("exact", [False, True])
 def test_mx_fp8_full_sampled(gpu, exact):
@@ -239,6 +335,29 @@ def test_mx_fp8_full_sampled(gpu, exact):
     err = np.abs(got[rows].astype(np.float64) - want) / np.maximum(mag, 1e-30)
     print(f"[err] mx_fp8 exact={exact}: max |gpu - oracle| / sum|A'B'| = {err.max():.3e}", flush=True)
     assert np.all(np.abs(got[rows].astype(np.float64) - want) <= (TOL_EXACT if exact else TOL) * mag + 1e-30)
+
+
+@pytest.mark.gpu
+def test_mx_fp4_full_sampled(gpu):
+    """The 4096^3 (logical) fp4 group: 16 rows spread over every tile row
+    against the oracle run on those rows."""
+    note("mx_fp4 4096^3, 16 sampled rows")
+    rng = np.random.default_rng(98)
+    m = n = k = 4096
+    a, b, sa, sb, ca, cb = fp4_case(rng, m, n, k, spread=6)
+    import hfusion_mi355x as hfm
+    grp = hfm.compile(hfm.catalog.get("mx_fp4"), require_cached=True).load()
+    from helpers import to_dev, to_host
+    got = to_host(grp(*(to_dev(x, p["elem"], gpu) for x, p in zip((a, b, sa, sb), grp.meta["params"]))), "f32")
+    rows = np.arange(7, m, m // 16)
+    want = np.zeros((len(rows), n), np.float32)
+    ar, sar = np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows])
+    lib().hfref_matmul_mx(ptr(ar), ptr(np.ascontiguousarray(b)), ptr(sar), ptr(np.ascontiguousarray(sb)), ptr(want),
+                          len(rows), n, k, 4, 4)
+    mag, _ = fp4_products(ca[rows], cb, sar, sb)
+    err = np.abs(got[rows].astype(np.float64) - want) / np.maximum(mag, 1e-30)
+    print(f"[err] mx_fp4: max |gpu - oracle| / sum|A'B'| = {err.max():.3e}", flush=True)
+    assert np.all(np.abs(got[rows].astype(np.float64) - want) <= TOL_FP4 * mag + 1e-30)
 
 
 @pytest.mark.gpu
