@@ -43,8 +43,8 @@
  *                           parallel sum where the widths allow, 0 through the
  *                           generic row program
  *   rmsn_kernel=1           the same groups through the chain-wave kernel
- *   mx_exact=1              hfusion.matmul_mx through scaled bf16 operands and
- *                           the bf16 matrix core (exact products, f32 sums)
+ *   mx_exact=1              fp8 hfusion.matmul_mx through scaled bf16 operands
+ *                           and the bf16 matrix core (exact products, f32 sums)
  *   dyn=<func>:<arg>.<dim>=<size>,...  sizes of dynamic dims
  *   dyn=runtime             one kernel for every row count (every dynamic dim
  *                           is dim 0 of the arguments; row programs, RMSNorm +
