@@ -31,7 +31,8 @@
 //      order) compose inside the lane, then across lanes with a segmented
 //      scan over runs of whole lanes; a lane keeps an event per run that
 //      ends in it and per dirty sub-segment;
-//   5. a wave-uniform stitch walks the events from s0: a run applies when the
+//   5. lane 0's elements take their serial steps from s0 ahead of the rest;
+//      a wave-uniform stitch walks the other lanes' events: a run applies when the
 //      exact running sum lies in its binade and the result stays below
 //      2^(p+1) (the addends are >= 0, so every intermediate value is inside);
 //      a dirty sub-segment takes its 16 serial steps; if a run does not
@@ -316,6 +317,14 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
       w0[t] = d0 | base | (clean ? 0x80000000u : 0u); // band_pack(p, d0, clean)
       w1[t] = d1;
     }
+    // lane 0's elements serially from s0, the one start known before the
+    // stitch (the running sum crosses a binade every few elements there, so
+    // its sub-segments are mostly dirty; as a chain of its own the steps
+    // overlap the work below instead of lengthening the stitch): every lane
+    // runs the steps over its own elements, lane 0's result is kept
+    uint32_t p0 = __float_as_uint(s0);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) p0 = serial16(p0, &xf[16 * t], 0);
     // ---- 4. runs: maximal sequences of clean items of one binade, in row
     //         order.  Q[t] composes the run that ends at item t from its start
     //         in this lane; a segmented scan over the lanes composes the runs
@@ -336,7 +345,7 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
     for (int t = 1; t < NS; ++t) h += (h == t && kt[t] == kt[0]) ? 1 : 0;
     const bool whole = h == NS && kt[0] > -1000;
     const int lastKeyPrev = dpp<DPP_WAVE_SHR1>(-2000, kt[NS - 1]);
-    const bool connIn = lane > 0 && kt[0] == lastKeyPrev; // item 0 continues a run
+    const bool connIn = lane > 1 && kt[0] == lastKeyPrev; // item 0 continues a run (lane 0 is summed apart)
     const bool connOut = __builtin_amdgcn_update_dpp(0, (int)connIn, DPP_WAVE_SHL1, 0xf, 0xf, false) != 0 && lane < 63;
     const bool segHead = !(whole && connIn);
     const uint64_t heads = __ballot(segHead);
@@ -366,10 +375,10 @@ __device__ __forceinline__ void rmsq_rows(const uint16_t *__restrict__ x, const 
       ev1[t] = (uint32_t)m1;
       evmask |= ev0[t] ? (1u << t) : 0u;
     }
-    const uint64_t visit = __ballot(evmask != 0);
+    const uint64_t visit = __ballot(evmask != 0) & ~1ull;
     // ---- 5. wave-uniform stitch from s0 (scalar code: a wave issues one
     //         instruction per four cycles, so the step is kept short)
-    uint32_t s = __float_as_uint(s0);
+    uint32_t s = p0; // the stitch starts at lane 1
     int nslow = 0;
     uint32_t runBad = 0;
     // (raised issue priority: the stitch is the wave's latency-bound part,
