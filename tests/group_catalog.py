@@ -1159,6 +1159,11 @@ def entries():
     e["vec_add_i16"] = g.vec_add(16, dtype="i16")
     e["rmsnorm_quant_ragged"] = g.rmsnorm_quant(13, 1000)
     e["rmsnorm_quant_w2048"] = g.rmsnorm_quant(96, 2048)
+    # a nonzero init of the sum of squares (the kernel's first lane and its
+    # fallback walk start from it)
+    e["rmsnorm_quant_init"] = g.rmsnorm_quant(256, 4096).replace(
+        "%i2 = linalg.fill ins(%zero", "%i2 = linalg.fill ins(%sinit").replace(
+        "%zero = arith.constant", "%sinit = arith.constant 3.000000e-01 : f32\n    %zero = arith.constant", 1)
     e["rmsnorm_quant_w3072"] = g.rmsnorm_quant(64, 3072)
     e["safe_softmax_64"] = g.safe_softmax(64, 32768)
     e["safe_softmax_ragged"] = g.safe_softmax(33, 1000)

@@ -62,7 +62,8 @@ def stress_rows(rows=256, seed=0x524D53):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["rmsnorm_quant_256", "rmsnorm_quant_256_rowprog", "rmsnorm_quant_256_rmsn"])
+@pytest.mark.parametrize("name", ["rmsnorm_quant_256", "rmsnorm_quant_256_rowprog", "rmsnorm_quant_256_rmsn",
+                                  "rmsnorm_quant_init"])
 def test_rmsq_stress_rows_bit_exact(gpu, name):
     """The stress rows through the three kernels of the pattern: the
     parallel sum (hf_rmsq.h, the default), the generic row program and the
@@ -73,7 +74,7 @@ def test_rmsq_stress_rows_bit_exact(gpu, name):
     g = I.uniform_bf16(I.SEED_BASE + 77, (C,), 0.5, 1.5)
     args = [x, g, np.zeros((256, C), np.int8), np.zeros(256, np.float32)]
     q, s = run_gpu(name, args, gpu)
-    rq, rs = run_oracle("rmsnorm_quant_256", args)
+    rq, rs = run_oracle("rmsnorm_quant_init" if name == "rmsnorm_quant_init" else "rmsnorm_quant_256", args)
     nan = np.isnan(rs)
     assert np.array_equal(np.isnan(s), nan)
     assert np.array_equal(s[~nan].view(np.uint32), rs[~nan].view(np.uint32)), \
@@ -92,6 +93,8 @@ def test_rmsq_kernel_selection():
         assert v.startswith("row-resident, serial-order"), name
         v = hf.compile(cat.get(name), options="rmsn_kernel=1").blocks[0]["variant"]
         assert "serial-order" in v and "chain wave" in v, name
+    assert "binade-run" in hf.compile(cat.get("rmsnorm_quant_init")).blocks[0]["variant"]
+    assert "0x1.333334p-2f" in open(hf.compile(cat.get("rmsnorm_quant_init"), options="emit=hip").source).read()
     # widths the kernel does not take keep the generic row program
     for name in ("rmsnorm_quant_ragged", "rmsnorm_quant_w3072"):
         v = hf.compile(cat.get(name)).blocks[0]["variant"]
