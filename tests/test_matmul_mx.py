@@ -338,6 +338,28 @@ def test_mx_fp8_full_sampled(gpu, exact):
 
 
 @pytest.mark.gpu
+def test_matmul_mx_fp4_nan_scales(gpu):
+    """fp4 has no NaN or infinity codes; an e8m0 scale of 255 (NaN) on one A
+    row block and one B column block makes that row and column NaN, as in
+    the oracle; the rest within the bar."""
+    name = "mx_fp4_256"
+    m, n, k, _, _ = FP4_CASES[name]
+    note(name + " NaN scales")
+    rng = np.random.default_rng(23)
+    a, b, sa, sb, ca, cb = fp4_case(rng, m, n, k)
+    sa[5, 3] = 255
+    sb[9, 14] = 255
+    got, = run_gpu(name, [a, b, sa, sb], gpu)
+    want, = run_oracle(name, [a, b, sa, sb])
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.isnan(want[5]).all() and np.isnan(want[:, 9]).all()
+    ok = ~np.isnan(want)
+    with np.errstate(invalid="ignore"):
+        mag, _ = fp4_products(ca, cb, sa, sb)
+    assert np.all(np.abs(got[ok].astype(np.float64) - want[ok]) <= TOL_FP4 * mag[ok] + 1e-30)
+
+
+@pytest.mark.gpu
 def test_mx_fp4_full_sampled(gpu):
     """The 4096^3 (logical) fp4 group: 16 rows spread over every tile row
     against the oracle run on those rows."""
