@@ -1256,6 +1256,8 @@ def entries():
     e["eltwise_mix_dyn_rt"] = g.with_dynamic_rows(eltwise_mix(67, 1000), 67)
     e["w8a8_dyn_rt"] = g.with_dynamic_rows(g.w8a8_dequant(333, 512, 512), 333)
     e["argmax_dyn_rt"] = g.with_dynamic_rows(g.argmax(333, 50000), 333)
+    e["mx_fp4_dyn_rt"] = g.with_dynamic_rows(g.matmul_mx(333, 256, 512, fa="e2m1", fb="e2m1", via="bitcast",
+                                                         name="mx_fp4_dyn"), 333)
     e["rmsnorm_quant_rank3"] = g.rmsnorm_quant(256, 1024, batch=4)
     # the same groups through the one-wave-per-row kernel (hf_rmsq.h, the
     # default for the widths it takes), named for it ...

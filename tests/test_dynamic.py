@@ -180,7 +180,7 @@ def test_dyn_entries_that_name_nothing_are_refused(spec, msg, tmp_path):
 
 
 # ------------------------------------------------------------- runtime rows
-RT = ["rmsnorm_quant_dyn_rt", "softmax_dyn_rt", "eltwise_mix_dyn_rt", "w8a8_dyn_rt", "argmax_dyn_rt"]
+RT = ["rmsnorm_quant_dyn_rt", "softmax_dyn_rt", "eltwise_mix_dyn_rt", "w8a8_dyn_rt", "argmax_dyn_rt", "mx_fp4_dyn_rt"]
 
 
 @pytest.mark.parametrize("name", RT)
@@ -325,6 +325,21 @@ def test_gpu_runtime_rows_w8a8(gpu, rows):
     out, = _call("w8a8_dyn_rt", args, gpu)
     ref, = run_oracle("w8a8_dyn_rt", args)
     assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [1, 100, 333, 600])
+def test_gpu_runtime_rows_mx_fp4(gpu, rows):
+    """Block-scaled fp4 with the row count M at launch (A [M, K/2] bytes, its
+    scales [M, K/32], C [M, N]); against the oracle at the fp4 bar."""
+    note(f"mx_fp4_dyn_rt M={rows}")
+    from test_matmul_mx import fp4_case, fp4_products, TOL_FP4
+    rng = np.random.default_rng(6000 + rows)
+    a, b, sa, sb, ca, cb = fp4_case(rng, rows, 256, 512)
+    out, = _call("mx_fp4_dyn_rt", [a, b, sa, sb], gpu)
+    ref, = run_oracle("mx_fp4_dyn_rt", [a, b, sa, sb])
+    mag, _ = fp4_products(ca, cb, sa, sb)
+    assert np.all(np.abs(out.astype(np.float64) - ref) <= TOL_FP4 * mag + 1e-30)
 
 
 @pytest.mark.gpu
