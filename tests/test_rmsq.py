@@ -61,6 +61,45 @@ def stress_rows(rows=256, seed=0x524D53):
     return bf16(x)
 
 
+def fuzz_rows(rows=256, seed=0):
+    """Rows of mixed shape, seeded: a scale 10^U(-25, 25) per row (and per
+    segment of 64 in half of them), sparse rows, rows that start large or
+    tiny (the sum's early binade crossings move), heavy-tailed values."""
+    rng = np.random.default_rng(0xF022 + seed)
+    x = np.zeros((rows, C), np.float32)
+    for r in range(rows):
+        v = rng.standard_normal(C) * 10.0 ** rng.uniform(-25, 25)
+        if r % 2:
+            v *= np.repeat(10.0 ** rng.uniform(-3, 3, C // 64), 64)
+        if r % 5 == 0:
+            v *= rng.random(C) < rng.uniform(0.001, 0.3)
+        if r % 7 == 0:
+            v[:rng.integers(1, 300)] *= 10.0 ** rng.uniform(-8, 8)
+        if r % 11 == 0:
+            v = rng.standard_cauchy(C)
+        x[r] = v
+    with np.errstate(over="ignore"):
+        return bf16(x)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_rmsq_fuzz_rows_bit_exact(gpu, seed):
+    """The parallel-sum kernel on fuzzed rows against the CPU oracle."""
+    print(f"[case] rmsnorm_quant_256 fuzz seed={seed}", flush=True)
+    x = fuzz_rows(seed=seed)
+    g = I.uniform_bf16(I.SEED_BASE + 78 + seed, (C,), 0.25, 4.0)
+    args = [x, g, np.zeros((256, C), np.int8), np.zeros(256, np.float32)]
+    q, s = run_gpu("rmsnorm_quant_256", args, gpu)
+    rq, rs = run_oracle("rmsnorm_quant_256", args)
+    nan = np.isnan(rs)
+    assert np.array_equal(np.isnan(s), nan)
+    assert np.array_equal(s[~nan].view(np.uint32), rs[~nan].view(np.uint32)), \
+        f"scales differ in rows {np.nonzero(s.view(np.uint32) != rs.view(np.uint32))[0][:16]}"
+    bad = np.nonzero((q != rq).any(axis=1))[0]
+    assert bad.size == 0, f"codes differ in rows {bad[:16]}"
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["rmsnorm_quant_256", "rmsnorm_quant_256_rowprog", "rmsnorm_quant_256_rmsn",
                                   "rmsnorm_quant_init"])
